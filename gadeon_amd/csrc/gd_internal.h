@@ -1,0 +1,114 @@
+// Internal declarations shared by the HIP translation units of libgadeon_hip.
+// Host side: the context object, error plumbing and launch checks.
+// Device side: f16 helpers, wave reductions and the LCG jump-ahead.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string>
+#include <atomic>
+
+#include "../../include/gadeon_hip.h"
+
+struct gd_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    hipEvent_t ev_start = nullptr;
+    hipEvent_t ev_stop = nullptr;
+    int num_cus = 0;
+    void *ws = nullptr;          // grow-only workspace (chunked GDN prefill)
+    size_t ws_bytes = 0;
+    std::string err;
+};
+
+// Record `msg` as the context's last error and return `code`.
+int gd_fail(gd_ctx *ctx, int code, const char *fmt, ...);
+// Grow-only context workspace of at least `bytes`; valid until the next call.
+int gd_ctx_workspace(gd_ctx *ctx, size_t bytes, void **out);
+// Map a HIP error to a GD code with a message naming `what`.
+int gd_hip_fail(gd_ctx *ctx, hipError_t e, const char *what);
+
+#define GD_CHECK_CTX(ctx) \
+    do { if (!(ctx)) return GD_EINVAL; } while (0)
+
+#define GD_REQUIRE(ctx, cond, ...) \
+    do { if (!(cond)) return gd_fail((ctx), GD_EINVAL, __VA_ARGS__); } while (0)
+
+#define GD_HIP(ctx, call) \
+    do { hipError_t e_ = (call); \
+         if (e_ != hipSuccess) return gd_hip_fail((ctx), e_, #call); } while (0)
+
+// After a hipLaunchKernelGGL: report a launch failure with the kernel name.
+#define GD_LAUNCHED(ctx, name) \
+    do { hipError_t e_ = hipGetLastError(); \
+         if (e_ != hipSuccess) return gd_fail((ctx), GD_ELAUNCH, \
+             "%s launch: %s", (name), hipGetErrorString(e_)); } while (0)
+
+static inline unsigned gd_blocks(int64_t n, int per) {
+    return (unsigned)((n + per - 1) / per);
+}
+
+// ---------------------------------------------------------------- device side
+
+typedef _Float16 f16;
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float gd_h2f(uint16_t h) {
+    return (float)__builtin_bit_cast(f16, h);
+}
+__device__ __forceinline__ uint16_t gd_f2h(float x) {
+    return __builtin_bit_cast(uint16_t, (f16)x);   // RNE
+}
+
+__device__ __forceinline__ float gd_silu(float x) { return x / (1.0f + expf(-x)); }
+__device__ __forceinline__ float gd_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+// Stable softplus, relu(x) + log1p(exp(-|x|)) (Kernels.swift:7-10).
+__device__ __forceinline__ float gd_softplus(float x) {
+    return fmaxf(x, 0.0f) + log1pf(expf(-fabsf(x)));
+}
+
+// Sum over the 64 lanes of a wave; every lane gets the total.
+__device__ __forceinline__ float gd_wave_sum(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+    return v;
+}
+
+// Sum over a block of `nthreads` (multiple of 64, <= 1024); `red` is LDS of
+// at least nthreads/64 floats.  Every thread gets the total.
+__device__ __forceinline__ float gd_block_sum(float v, float *red) {
+    v = gd_wave_sum(v);
+    const int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    float t = 0.0f;
+    for (int i = 0; i < nw; i++) t += red[i];
+    return t;
+}
+
+// The reference test LCG (MetalSelfTest.swift:12-21) with O(log n) jump-ahead:
+// state after n steps from s is A^n s + C (A^n - 1)/(A - 1), composed by
+// squaring the affine map.
+#define GD_LCG_A 6364136223846793005ULL
+#define GD_LCG_C 1442695040888963407ULL
+#define GD_LCG_SEED_MIX 0x9E3779B97F4A7C15ULL
+
+__host__ __device__ __forceinline__ uint64_t gd_lcg_skip(uint64_t s, uint64_t n) {
+    uint64_t a = GD_LCG_A, c = GD_LCG_C;      // current map x -> a x + c
+    uint64_t ra = 1, rc = 0;                  // accumulated map
+    while (n) {
+        if (n & 1) { ra = ra * a; rc = rc * a + c; }
+        c = c * (a + 1);
+        a = a * a;
+        n >>= 1;
+    }
+    return ra * s + rc;
+}

@@ -1,0 +1,464 @@
+// Runtime half of the boundary: context, device memory, copies, timing, the
+// host Q2_0 codec, the GGUF <-> device-plane repack and the synthetic-data
+// generators.  Replaces MetalContext (LLM/src/Metal/MetalContext.swift).
+#include "gd_internal.h"
+
+#include <stdarg.h>
+#include <string.h>
+#include <mutex>
+
+static std::mutex g_err_mu;
+static std::string g_err;   // last gd_ctx_create failure (no context yet)
+
+int gd_fail(gd_ctx *ctx, int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    if (ctx) {
+        ctx->err = buf;
+    } else {
+        std::lock_guard<std::mutex> lk(g_err_mu);
+        g_err = buf;
+    }
+    return code;
+}
+
+int gd_hip_fail(gd_ctx *ctx, hipError_t e, const char *what) {
+    int code = GD_EHIP;
+    if (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) code = GD_ENOMEM;
+    if (e == hipErrorNoDevice || e == hipErrorInvalidDevice) code = GD_ENODEV;
+    return gd_fail(ctx, code, "%s: %s", what, hipGetErrorString(e));
+}
+
+extern "C" int gd_device_count(int *n) {
+    if (!n) return GD_EINVAL;
+    int c = 0;
+    if (hipGetDeviceCount(&c) != hipSuccess) c = 0;
+    *n = c;
+    return GD_OK;
+}
+
+extern "C" int gd_ctx_create(int device, gd_ctx **out) {
+    if (!out) return GD_EINVAL;
+    *out = nullptr;
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n == 0)
+        return gd_fail(nullptr, GD_ENODEV, "no HIP device (%s)",
+                       e == hipSuccess ? "count 0" : hipGetErrorString(e));
+    if (device < 0 || device >= n)
+        return gd_fail(nullptr, GD_ENODEV, "device %d out of range [0,%d)", device, n);
+    gd_ctx *c = new gd_ctx();
+    c->device = device;
+    if ((e = hipSetDevice(device)) != hipSuccess ||
+        (e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking)) != hipSuccess ||
+        (e = hipEventCreate(&c->ev_start)) != hipSuccess ||
+        (e = hipEventCreate(&c->ev_stop)) != hipSuccess) {
+        gd_fail(nullptr, GD_EHIP, "context setup: %s", hipGetErrorString(e));
+        gd_ctx_destroy(c);
+        return GD_EHIP;
+    }
+    hipDeviceProp_t p;
+    if (hipGetDeviceProperties(&p, device) == hipSuccess) c->num_cus = p.multiProcessorCount;
+    *out = c;
+    return GD_OK;
+}
+
+extern "C" void gd_ctx_destroy(gd_ctx *ctx) {
+    if (!ctx) return;
+    (void)hipSetDevice(ctx->device);
+    if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    if (ctx->ev_start) (void)hipEventDestroy(ctx->ev_start);
+    if (ctx->ev_stop) (void)hipEventDestroy(ctx->ev_stop);
+    if (ctx->ws) (void)hipFree(ctx->ws);
+    if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+}
+
+extern "C" const char *gd_last_error(const gd_ctx *ctx) {
+    if (ctx) return ctx->err.c_str();
+    std::lock_guard<std::mutex> lk(g_err_mu);
+    static thread_local std::string copy;
+    copy = g_err;
+    return copy.c_str();
+}
+
+int gd_ctx_workspace(gd_ctx *ctx, size_t bytes, void **out) {
+    if (ctx->ws_bytes < bytes) {
+        if (ctx->ws) {
+            GD_HIP(ctx, hipStreamSynchronize(ctx->stream));
+            GD_HIP(ctx, hipFree(ctx->ws));
+            ctx->ws = nullptr;
+            ctx->ws_bytes = 0;
+        }
+        hipError_t e = hipMalloc(&ctx->ws, bytes);
+        if (e != hipSuccess) {
+            ctx->ws = nullptr;
+            return gd_fail(ctx, GD_ENOMEM, "workspace (%zu bytes): %s", bytes, hipGetErrorString(e));
+        }
+        ctx->ws_bytes = bytes;
+    }
+    *out = ctx->ws;
+    return GD_OK;
+}
+
+extern "C" int gd_alloc(gd_ctx *ctx, size_t bytes, void **dptr) {
+    GD_CHECK_CTX(ctx);
+    GD_REQUIRE(ctx, dptr != nullptr, "gd_alloc: null out pointer");
+    *dptr = nullptr;
+    if (bytes == 0) bytes = 256;
+    GD_HIP(ctx, hipSetDevice(ctx->device));
+    hipError_t e = hipMalloc(dptr, bytes);
+    if (e != hipSuccess) {
+        *dptr = nullptr;
+        return gd_fail(ctx, GD_ENOMEM, "gd_alloc(%zu bytes): %s", bytes, hipGetErrorString(e));
+    }
+    return GD_OK;
+}
+
+extern "C" int gd_free(gd_ctx *ctx, void *dptr) {
+    GD_CHECK_CTX(ctx);
+    if (!dptr) return GD_OK;
+    // Work enqueued on the stream may still read the buffer.
+    GD_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    GD_HIP(ctx, hipFree(dptr));
+    return GD_OK;
+}
+
+extern "C" int gd_upload(gd_ctx *ctx, void *dst, const void *src, size_t bytes) {
+    GD_CHECK_CTX(ctx);
+    GD_REQUIRE(ctx, (dst && src) || bytes == 0, "gd_upload: null pointer");
+    if (!bytes) return GD_OK;
+    GD_HIP(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+    GD_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return GD_OK;
+}
+
+extern "C" int gd_download(gd_ctx *ctx, void *dst, const void *src, size_t bytes) {
+    GD_CHECK_CTX(ctx);
+    GD_REQUIRE(ctx, (dst && src) || bytes == 0, "gd_download: null pointer");
+    if (!bytes) return GD_OK;
+    GD_HIP(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
+    GD_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return GD_OK;
+}
+
+extern "C" int gd_copy(gd_ctx *ctx, void *dst, const void *src, size_t bytes) {
+    GD_CHECK_CTX(ctx);
+    GD_REQUIRE(ctx, (dst && src) || bytes == 0, "gd_copy: null pointer");
+    if (!bytes) return GD_OK;
+    GD_HIP(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx->stream));
+    return GD_OK;
+}
+
+__global__ void gd_fill_u32_kernel(uint32_t *dst, uint32_t v, size_t n) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (; i < n; i += stride) dst[i] = v;
+}
+
+extern "C" int gd_fill_u32(gd_ctx *ctx, void *dst, uint32_t value, size_t count) {
+    GD_CHECK_CTX(ctx);
+    GD_REQUIRE(ctx, dst || count == 0, "gd_fill_u32: null pointer");
+    if (!count) return GD_OK;
+    unsigned blocks = (unsigned)std::min<size_t>((count + 255) / 256, 65536);
+    hipLaunchKernelGGL(gd_fill_u32_kernel, dim3(blocks), dim3(256), 0, ctx->stream,
+                       (uint32_t *)dst, value, count);
+    GD_LAUNCHED(ctx, "gd_fill_u32");
+    return GD_OK;
+}
+
+extern "C" int gd_sync(gd_ctx *ctx) {
+    GD_CHECK_CTX(ctx);
+    GD_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return GD_OK;
+}
+
+extern "C" int gd_timer_start(gd_ctx *ctx) {
+    GD_CHECK_CTX(ctx);
+    GD_HIP(ctx, hipEventRecord(ctx->ev_start, ctx->stream));
+    return GD_OK;
+}
+
+extern "C" int gd_timer_stop(gd_ctx *ctx, float *ms) {
+    GD_CHECK_CTX(ctx);
+    GD_REQUIRE(ctx, ms != nullptr, "gd_timer_stop: null out pointer");
+    GD_HIP(ctx, hipEventRecord(ctx->ev_stop, ctx->stream));
+    GD_HIP(ctx, hipEventSynchronize(ctx->ev_stop));
+    GD_HIP(ctx, hipEventElapsedTime(ms, ctx->ev_start, ctx->ev_stop));
+    return GD_OK;
+}
+
+// ---------------------------------------------------------------- host codec
+
+extern "C" int gd_q2_0_pack(const uint8_t *codes, const uint16_t *scales, size_t n,
+                            uint8_t *blocks) {
+    if (!codes || !scales || !blocks || n % GD_Q2_0_QK) return GD_EINVAL;
+    const size_t nb = n / GD_Q2_0_QK;
+    for (size_t b = 0; b < nb; b++) {
+        uint8_t *p = blocks + b * GD_Q2_0_BLOCK_BYTES;
+        const uint16_t d = scales[b];
+        p[0] = (uint8_t)(d & 0xff);          // f16 scale first, little-endian
+        p[1] = (uint8_t)(d >> 8);
+        const uint8_t *c = codes + b * GD_Q2_0_QK;
+        for (int j = 0; j < 32; j++) {
+            if ((c[4 * j] | c[4 * j + 1] | c[4 * j + 2] | c[4 * j + 3]) > 3) return GD_EINVAL;
+            p[2 + j] = (uint8_t)(c[4 * j] | (c[4 * j + 1] << 2) |
+                                 (c[4 * j + 2] << 4) | (c[4 * j + 3] << 6));
+        }
+    }
+    return GD_OK;
+}
+
+extern "C" int gd_q2_0_unpack(const uint8_t *blocks, size_t n, uint8_t *codes,
+                              uint16_t *scales) {
+    if (!blocks || n % GD_Q2_0_QK || (!codes && !scales)) return GD_EINVAL;
+    const size_t nb = n / GD_Q2_0_QK;
+    for (size_t b = 0; b < nb; b++) {
+        const uint8_t *p = blocks + b * GD_Q2_0_BLOCK_BYTES;
+        if (scales) scales[b] = (uint16_t)(p[0] | (p[1] << 8));
+        if (codes) {
+            uint8_t *c = codes + b * GD_Q2_0_QK;
+            for (int j = 0; j < GD_Q2_0_QK; j++)
+                c[j] = (uint8_t)((p[2 + (j >> 2)] >> ((j & 3) << 1)) & 3);
+        }
+    }
+    return GD_OK;
+}
+
+// ------------------------------------------------------- device planes / repack
+
+extern "C" int gd_q2w_alloc(gd_ctx *ctx, int64_t K, int64_t R, gd_q2w *w) {
+    GD_CHECK_CTX(ctx);
+    GD_REQUIRE(ctx, w && K > 0 && R > 0 && K % GD_Q2_0_QK == 0,
+               "gd_q2w_alloc: K=%lld must be a positive multiple of 128, R=%lld > 0",
+               (long long)K, (long long)R);
+    w->codes = w->scales = nullptr;
+    w->K = K; w->R = R;
+    int rc = gd_alloc(ctx, (size_t)(R * (K / 4)), &w->codes);
+    if (rc) return rc;
+    rc = gd_alloc(ctx, (size_t)(R * (K / GD_Q2_0_QK) * 2), &w->scales);
+    if (rc) { gd_free(ctx, w->codes); w->codes = nullptr; return rc; }
+    return GD_OK;
+}
+
+extern "C" int gd_q2w_free(gd_ctx *ctx, gd_q2w *w) {
+    GD_CHECK_CTX(ctx);
+    if (!w) return GD_OK;
+    int rc = gd_free(ctx, w->codes);
+    int rc2 = gd_free(ctx, w->scales);
+    w->codes = w->scales = nullptr;
+    return rc ? rc : rc2;
+}
+
+// One thread per 34-byte block.  The GGUF side is only 2-byte aligned, so it
+// is read as 17 halfwords; the planes are written as 8 aligned dwords + 1 f16.
+__global__ void gd_repack_kernel(const uint16_t *src, uint32_t *codes, uint16_t *scales,
+                                 int64_t nblocks) {
+    int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= nblocks) return;
+    const uint16_t *p = src + b * (GD_Q2_0_BLOCK_BYTES / 2);
+    scales[b] = p[0];
+    uint32_t *c = codes + b * 8;
+#pragma unroll
+    for (int j = 0; j < 8; j++) c[j] = (uint32_t)p[1 + 2 * j] | ((uint32_t)p[2 + 2 * j] << 16);
+}
+
+__global__ void gd_export_kernel(const uint32_t *codes, const uint16_t *scales, uint16_t *dst,
+                                 int64_t nblocks) {
+    int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= nblocks) return;
+    uint16_t *p = dst + b * (GD_Q2_0_BLOCK_BYTES / 2);
+    p[0] = scales[b];
+    const uint32_t *c = codes + b * 8;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        p[1 + 2 * j] = (uint16_t)(c[j] & 0xffff);
+        p[2 + 2 * j] = (uint16_t)(c[j] >> 16);
+    }
+}
+
+static int check_q2w(gd_ctx *ctx, const gd_q2w *w, const char *who) {
+    GD_REQUIRE(ctx, w && w->codes && w->scales, "%s: null weight planes", who);
+    GD_REQUIRE(ctx, w->K > 0 && w->K % GD_Q2_0_QK == 0 && w->R > 0,
+               "%s: K=%lld must be a positive multiple of 128, R=%lld > 0", who,
+               (long long)w->K, (long long)w->R);
+    GD_REQUIRE(ctx, ((uintptr_t)w->codes & 15) == 0 && ((uintptr_t)w->scales & 3) == 0,
+               "%s: codes plane must be 16-byte aligned, scales 4-byte aligned", who);
+    return GD_OK;
+}
+int gd_check_q2w(gd_ctx *ctx, const gd_q2w *w, const char *who) { return check_q2w(ctx, w, who); }
+
+extern "C" int gd_q2_0_repack(gd_ctx *ctx, const void *gguf, uint64_t woff, gd_q2w *w) {
+    GD_CHECK_CTX(ctx);
+    int rc = check_q2w(ctx, w, "gd_q2_0_repack");
+    if (rc) return rc;
+    GD_REQUIRE(ctx, gguf && woff % 2 == 0, "gd_q2_0_repack: null source or odd offset");
+    const int64_t nb = w->R * (w->K / GD_Q2_0_QK);
+    hipLaunchKernelGGL(gd_repack_kernel, dim3(gd_blocks(nb, 256)), dim3(256), 0, ctx->stream,
+                       (const uint16_t *)((const uint8_t *)gguf + woff), (uint32_t *)w->codes,
+                       (uint16_t *)w->scales, nb);
+    GD_LAUNCHED(ctx, "gd_repack_kernel");
+    return GD_OK;
+}
+
+extern "C" int gd_q2_0_export(gd_ctx *ctx, const gd_q2w *w, void *gguf_out) {
+    GD_CHECK_CTX(ctx);
+    int rc = check_q2w(ctx, w, "gd_q2_0_export");
+    if (rc) return rc;
+    GD_REQUIRE(ctx, gguf_out && ((uintptr_t)gguf_out & 1) == 0, "gd_q2_0_export: bad output");
+    const int64_t nb = w->R * (w->K / GD_Q2_0_QK);
+    hipLaunchKernelGGL(gd_export_kernel, dim3(gd_blocks(nb, 256)), dim3(256), 0, ctx->stream,
+                       (const uint32_t *)w->codes, (const uint16_t *)w->scales,
+                       (uint16_t *)gguf_out, nb);
+    GD_LAUNCHED(ctx, "gd_export_kernel");
+    return GD_OK;
+}
+
+extern "C" int gd_q2_0_upload(gd_ctx *ctx, const void *host_blocks, int64_t K, int64_t R,
+                              gd_q2w *w) {
+    GD_CHECK_CTX(ctx);
+    GD_REQUIRE(ctx, host_blocks && w, "gd_q2_0_upload: null pointer");
+    int rc = gd_q2w_alloc(ctx, K, R, w);
+    if (rc) return rc;
+    const size_t bytes = (size_t)(R * (K / GD_Q2_0_QK) * GD_Q2_0_BLOCK_BYTES);
+    void *staging = nullptr;
+    if ((rc = gd_alloc(ctx, bytes, &staging)) ||
+        (rc = gd_upload(ctx, staging, host_blocks, bytes)) ||
+        (rc = gd_q2_0_repack(ctx, staging, 0, w)) ||
+        (rc = gd_free(ctx, staging))) {
+        gd_free(ctx, staging);
+        gd_q2w_free(ctx, w);
+        return rc;
+    }
+    return GD_OK;
+}
+
+// ------------------------------------------------------------ synthetic data
+
+#define GD_RAND_RUN 64   // consecutive stream elements per thread
+
+__device__ __forceinline__ uint32_t lcg_bits(uint64_t s) { return (uint32_t)(s >> 33); }
+
+// lo + span*u with two roundings (no FMA contraction), as the host stream.
+__device__ __forceinline__ float lerp_unfused(float lo, float span, float u) {
+#pragma clang fp contract(off)
+    return lo + span * u;
+}
+
+__global__ void gd_rand_uniform_kernel(float *out, size_t n, uint64_t s0, float lo, float span) {
+    const size_t i0 = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * GD_RAND_RUN;
+    if (i0 >= n) return;
+    uint64_t s = gd_lcg_skip(s0, i0);
+    const size_t end = i0 + GD_RAND_RUN < n ? i0 + GD_RAND_RUN : n;
+    for (size_t i = i0; i < end; i++) {
+        s = s * GD_LCG_A + GD_LCG_C;
+        const float u = (float)lcg_bits(s) * 0x1p-31f;
+        out[i] = lerp_unfused(lo, span, u);
+    }
+}
+
+__global__ void gd_rand_normal_kernel(void *out, int dtype, size_t n, uint64_t s0, float mean,
+                                      float sd) {
+    // Each thread owns GD_RAND_RUN/2 Box-Muller pairs: elements [i0, i0+RUN).
+    const size_t i0 = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * GD_RAND_RUN;
+    if (i0 >= n) return;
+    uint64_t s = gd_lcg_skip(s0, i0);
+    for (size_t i = i0; i < i0 + GD_RAND_RUN && i < n; i += 2) {
+        s = s * GD_LCG_A + GD_LCG_C;
+        const uint32_t b1 = lcg_bits(s);
+        s = s * GD_LCG_A + GD_LCG_C;
+        const uint32_t b2 = lcg_bits(s);
+        const float u1 = (float)((uint64_t)b1 + 1) * 0x1p-31f;   // (0, 1]
+        const float u2 = (float)b2 * 0x1p-31f;                   // [0, 1)
+        const float r = sqrtf(-2.0f * logf(u1));
+        const float a = 6.283185307179586f * u2;
+        const float z0 = mean + sd * (r * cosf(a));
+        const float z1 = mean + sd * (r * sinf(a));
+        if (dtype == GD_F32) {
+            ((float *)out)[i] = z0;
+            if (i + 1 < n) ((float *)out)[i + 1] = z1;
+        } else {
+            ((uint16_t *)out)[i] = gd_f2h(z0);
+            if (i + 1 < n) ((uint16_t *)out)[i + 1] = gd_f2h(z1);
+        }
+    }
+}
+
+// Codes: one thread per 64 weights (16 code bytes) of the flattened [R][K]
+// matrix; weight e uses element e of stream s0.
+__global__ void gd_rand_codes_kernel(uint32_t *codes, size_t nweights, uint64_t s0) {
+    const size_t e0 = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 64;
+    if (e0 >= nweights) return;
+    uint64_t s = gd_lcg_skip(s0, e0);
+    uint32_t *dst = codes + e0 / 16;
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            s = s * GD_LCG_A + GD_LCG_C;
+            const uint32_t c = (uint32_t)(((uint64_t)lcg_bits(s) * 3u) >> 31);
+            word |= c << (2 * j);
+        }
+        dst[w] = word;
+    }
+}
+
+__global__ void gd_rand_scales_kernel(uint16_t *scales, size_t n, uint64_t s0, float lo,
+                                      float span) {
+    const size_t i0 = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * GD_RAND_RUN;
+    if (i0 >= n) return;
+    uint64_t s = gd_lcg_skip(s0, i0);
+    for (size_t i = i0; i < i0 + GD_RAND_RUN && i < n; i++) {
+        s = s * GD_LCG_A + GD_LCG_C;
+        const float u = (float)lcg_bits(s) * 0x1p-31f;
+        scales[i] = gd_f2h(lerp_unfused(lo, span, u));
+    }
+}
+
+static inline uint64_t stream_start(uint64_t seed) { return seed + GD_LCG_SEED_MIX; }
+
+extern "C" int gd_rand_uniform(gd_ctx *ctx, float *out, size_t n, uint64_t seed, float lo,
+                               float hi) {
+    GD_CHECK_CTX(ctx);
+    GD_REQUIRE(ctx, out || n == 0, "gd_rand_uniform: null output");
+    if (!n) return GD_OK;
+    const size_t threads = (n + GD_RAND_RUN - 1) / GD_RAND_RUN;
+    hipLaunchKernelGGL(gd_rand_uniform_kernel, dim3(gd_blocks(threads, 256)), dim3(256), 0,
+                       ctx->stream, out, n, stream_start(seed), lo, hi - lo);
+    GD_LAUNCHED(ctx, "gd_rand_uniform");
+    return GD_OK;
+}
+
+extern "C" int gd_rand_normal(gd_ctx *ctx, void *out, int dtype, size_t n, uint64_t seed,
+                              float mean, float sd) {
+    GD_CHECK_CTX(ctx);
+    GD_REQUIRE(ctx, out || n == 0, "gd_rand_normal: null output");
+    GD_REQUIRE(ctx, dtype == GD_F32 || dtype == GD_F16, "gd_rand_normal: bad dtype %d", dtype);
+    if (!n) return GD_OK;
+    const size_t threads = (n + GD_RAND_RUN - 1) / GD_RAND_RUN;
+    hipLaunchKernelGGL(gd_rand_normal_kernel, dim3(gd_blocks(threads, 256)), dim3(256), 0,
+                       ctx->stream, out, dtype, n, stream_start(seed), mean, sd);
+    GD_LAUNCHED(ctx, "gd_rand_normal");
+    return GD_OK;
+}
+
+extern "C" int gd_rand_q2w(gd_ctx *ctx, gd_q2w *w, uint64_t seed, float lo, float hi) {
+    GD_CHECK_CTX(ctx);
+    int rc = check_q2w(ctx, w, "gd_rand_q2w");
+    if (rc) return rc;
+    const size_t nw = (size_t)(w->R * w->K);       // multiple of 128
+    hipLaunchKernelGGL(gd_rand_codes_kernel, dim3(gd_blocks(nw / 64, 256)), dim3(256), 0,
+                       ctx->stream, (uint32_t *)w->codes, nw, stream_start(seed));
+    GD_LAUNCHED(ctx, "gd_rand_codes");
+    const size_t ns = nw / GD_Q2_0_QK;
+    const size_t threads = (ns + GD_RAND_RUN - 1) / GD_RAND_RUN;
+    hipLaunchKernelGGL(gd_rand_scales_kernel, dim3(gd_blocks(threads, 256)), dim3(256), 0,
+                       ctx->stream, (uint16_t *)w->scales, ns, stream_start(seed + 1), lo,
+                       hi - lo);
+    GD_LAUNCHED(ctx, "gd_rand_scales");
+    return GD_OK;
+}

@@ -1,0 +1,269 @@
+/*
+ * gadeon_hip.h -- C ABI of the MI355X (gfx950) implementation of Gadeon's
+ * quantized hot path: Q2_0 ternary GEMV/GEMM and the Gated DeltaNet (GDN)
+ * recurrence, plus the glue a Bonsai-shaped hybrid stack needs around them.
+ *
+ * The surface mirrors the reference's typed dispatch layer `MetalEnc`
+ * (LLM/src/Metal/MetalEnc.swift): one entry per kernel, asynchronous on the
+ * context's single in-order HIP stream, with the same argument meaning.  The
+ * runtime half (`MetalContext`, LLM/src/Metal/MetalContext.swift) becomes
+ * gd_ctx_* / gd_alloc / gd_upload.
+ *
+ * Conventions
+ *   - Every entry returns int: GD_OK (0) or a negative GD_E* code.  Entries
+ *     never abort; gd_last_error(ctx) returns the message of the last failure
+ *     on that context.  (Reference: MetalErr, MetalContext.swift:331-349, and
+ *     the non-throwing dispatch methods of MetalEnc.swift:9-13.)
+ *   - Device pointers are plain `void*` from gd_alloc.  The caller owns every
+ *     device buffer; the context owns only its stream and events.
+ *   - Compute entries enqueue on the context stream and return immediately;
+ *     gd_sync / gd_download block.  One context must not be used from two
+ *     threads at once (MetalBackend.swift:3-4: the session serializes calls).
+ *   - Dimension names follow the reference's GEMV/GEMM convention, spelled
+ *     out: K = reduction length (GGUF ne0), R = output rows (reference "M",
+ *     GGUF ne1), T = tokens (reference "N").  out[T][R] = X[T][K] . W[R][K]^T.
+ *   - Activation dtype codes: GD_F32 (IEEE binary32) and GD_F16 (binary16,
+ *     passed as uint16_t bit patterns).
+ */
+#ifndef GADEON_HIP_H
+#define GADEON_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- error codes --------------------------------------------------------- */
+#define GD_OK        0
+#define GD_EINVAL   -1   /* bad argument: shape, alignment, null pointer   */
+#define GD_ENODEV   -2   /* no HIP device / device index out of range      */
+#define GD_ENOMEM   -3   /* device allocation failed                       */
+#define GD_ELAUNCH  -4   /* kernel launch failed                           */
+#define GD_EHIP     -5   /* any other HIP runtime error                    */
+#define GD_ESTOPPED -6   /* cooperative stop observed between chunks       */
+
+#define GD_F32 0
+#define GD_F16 1
+
+/* Q2_0 block geometry: 128 weights in 34 bytes {f16 d; u8 qs[32]}.
+ * Reference: Quant.swift:2-12, GGUF.swift:13 (type 42), Kernels.metal:2484-2490. */
+#define GD_Q2_0_QK          128
+#define GD_Q2_0_BLOCK_BYTES 34
+
+typedef struct gd_ctx gd_ctx;
+
+/* ---- runtime: MetalContext (MetalContext.swift:103-305) ------------------ */
+
+/* Number of visible HIP devices (0 when none).  Does not create a context. */
+int gd_device_count(int *n);
+
+/* Create a context on `device`: sets the device, creates one default-priority
+ * stream and the timing events.  Replaces MetalContext.init (MetalContext.swift:103-129). */
+int gd_ctx_create(int device, gd_ctx **out);
+void gd_ctx_destroy(gd_ctx *ctx);
+
+/* Message of the last failing call on ctx ("" if none).  ctx may be NULL:
+ * then the message of the last failing gd_ctx_create in this process. */
+const char *gd_last_error(const gd_ctx *ctx);
+
+/* Device memory, owned by the caller (MetalContext.makeF32, :291-305). */
+int gd_alloc(gd_ctx *ctx, size_t bytes, void **dptr);
+int gd_free(gd_ctx *ctx, void *dptr);
+/* Host->device / device->host copies.  Both are synchronous with respect to
+ * the context stream (download waits for all enqueued work first). */
+int gd_upload(gd_ctx *ctx, void *dst, const void *src, size_t bytes);
+int gd_download(gd_ctx *ctx, void *dst, const void *src, size_t bytes);
+/* Device->device copy and fill, enqueued on the stream (fill via a kernel, so
+ * the call is safe inside stream capture). */
+int gd_copy(gd_ctx *ctx, void *dst, const void *src, size_t bytes);
+int gd_fill_u32(gd_ctx *ctx, void *dst, uint32_t value, size_t count);
+/* Block until every call enqueued on ctx has finished. */
+int gd_sync(gd_ctx *ctx);
+
+/* Stream-ordered timing with HIP events recorded on the context stream, the
+ * same stream every compute entry launches on.  gd_timer_stop waits for the
+ * stop event and returns the elapsed milliseconds. */
+int gd_timer_start(gd_ctx *ctx);
+int gd_timer_stop(gd_ctx *ctx, float *ms);
+
+/* ---- Q2_0 codec (host; no GPU needed) -------------------------------------
+ * The reference only decodes Q2_0 (Quant.swift:15-30); these are its exact
+ * inverse.  Code c in {0,1,2,3} means weight (c-1)*d; code of weight j of a
+ * block sits in qs[j>>2] at bits 2*(j&3), LSB-first (Quant.swift:4-7). */
+
+/* Pack n weights (n % 128 == 0): codes[n] (each 0..3) and one f16 scale bit
+ * pattern per 128 weights -> n/128 blocks of 34 bytes. */
+int gd_q2_0_pack(const uint8_t *codes, const uint16_t *scales, size_t n,
+                 uint8_t *blocks);
+/* Unpack n/128 blocks -> codes[n], scales[n/128] (bit patterns as stored). */
+int gd_q2_0_unpack(const uint8_t *blocks, size_t n, uint8_t *codes,
+                   uint16_t *scales);
+
+/* ---- Q2_0 device weights ---------------------------------------------------
+ * On the device a Q2_0 matrix [R][K] is held as two planes, the layout the
+ * MI355X kernels stream: codes[R][K/4] (each block's qs[32] bytes, rows
+ * contiguous) and scales[R][K/128] (f16).  Same 2.125 bits per weight as the
+ * GGUF blocks.  Reference weights arrive as GGUF bytes (GGUF.swift:107-117)
+ * and are repacked once at upload, where MetalContext wraps the mmap without
+ * a copy (MetalContext.swift:193-212). */
+typedef struct gd_q2w {
+    void *codes;    /* device, R*K/4 bytes, 16-byte aligned rows            */
+    void *scales;   /* device, R*K/128 f16                                  */
+    int64_t K;      /* reduction length, multiple of 128                   */
+    int64_t R;      /* output rows                                          */
+} gd_q2w;
+
+/* Allocate the two planes of a K x R matrix (caller frees via gd_q2w_free). */
+int gd_q2w_alloc(gd_ctx *ctx, int64_t K, int64_t R, gd_q2w *w);
+int gd_q2w_free(gd_ctx *ctx, gd_q2w *w);
+/* Repack R rows of GGUF Q2_0 blocks already in device memory (at byte offset
+ * woff of `gguf`, the MetalEnc WeightRef.local) into the planes of w. */
+int gd_q2_0_repack(gd_ctx *ctx, const void *gguf, uint64_t woff, gd_q2w *w);
+/* Host GGUF blocks -> freshly allocated device planes (upload + repack). */
+int gd_q2_0_upload(gd_ctx *ctx, const void *host_blocks, int64_t K, int64_t R,
+                   gd_q2w *w);
+/* Device planes -> GGUF blocks in device memory (inverse of repack). */
+int gd_q2_0_export(gd_ctx *ctx, const gd_q2w *w, void *gguf_out);
+
+/* ---- Q2_0 GEMV (decode): MetalEnc.gemv, MetalEnc.swift:78-99 -----------------
+ * y[r] = sum_k W[r,k] * x[k] for r < R, f32 accumulate, f32 out.
+ * x dtype GD_F32 (the reference's buffer type; split exactly into two f16
+ * halves in-kernel) or GD_F16 (the BASELINE decode activations).
+ * Replaces the Metal kernel q2_0_gemv (Kernels.metal:30-119) and the CPU
+ * Q2_0.matvec (Quant.swift:36-77). */
+int gd_q2_0_gemv(gd_ctx *ctx, const gd_q2w *w, const void *x, int x_dtype,
+                 float *y);
+
+/* ---- Q2_0 GEMM (prefill): MetalEnc.gemm, MetalEnc.swift:145-189 --------------
+ * Y[t][r] = sum_k X[t][k] * W[r][k], token-major X[T][K] and Y[T][R].
+ * Weights are dequantized to f16 tiles in LDS and multiplied on fp16 MFMA
+ * with f32 accumulation (reference: q2_0_gemm_mm_h, Kernels.metal:372-466,
+ * which stages both operands as half).  X dtype GD_F32 is rounded to f16
+ * while staging, as the reference does (Kernels.metal:428); Y dtype GD_F32
+ * or GD_F16 (round-to-nearest-even of the f32 accumulator). */
+int gd_q2_0_gemm(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X,
+                 int x_dtype, void *Y, int y_dtype);
+
+/* ---- Q2_0 row dequant: MetalEnc.dequantRow / embedBatch ----------------------
+ * out[n][k] = (code-1)*d of row ids[n], exactly (f16 * small integer is exact
+ * in f32).  Reference: q2_0_dequant_row (Kernels.metal:472-485), embed_batch
+ * (Kernels.metal:1468-1485), Q2_0.dequant (Quant.swift:15-30). */
+int gd_q2_0_dequant_rows(gd_ctx *ctx, const gd_q2w *w, const int32_t *ids,
+                         int64_t n, float *out);
+
+/* ---- GDN glue (MetalEnc.swift:603-653, 720-733; Kernels.metal:1146-1243) ----- */
+
+/* beta = sigmoid(bPre); g = softplus(aPre + dt[h]) * aNeg[h], h = i % nV,
+ * for i < count.  MetalEnc.gdnGate (MetalEnc.swift:603-618), gdn_gate
+ * (Kernels.metal:1146-1168), GDN.swift:39-42. */
+int gd_gdn_gate(gd_ctx *ctx, const float *bPre, const float *aPre,
+                const float *dt, const float *aNeg, float *beta, float *g,
+                int nV, int64_t count);
+
+/* Causal depthwise conv + silu over N tokens with the (dConv-1)-deep ring
+ * state[(dConv-1)][convDim] (time-minor), weights cw[convDim][dConv].
+ * N == 1 is MetalEnc.gdnConv, N > 1 MetalEnc.gdnConvBatch.  Reference:
+ * gdn_conv / gdn_conv_batch (Kernels.metal:1174-1199, 1490-1520), GDN.swift:44-62. */
+int gd_gdn_conv(gd_ctx *ctx, const float *qkvMix, float *convState,
+                const float *cw, float *out, int convDim, int dConv,
+                int64_t N);
+
+/* x / sqrt(sum(x^2) + eps) over `rowsPerTok` rows of length d per token,
+ * token n based at n*tokStride (floats), for `tokens` tokens.
+ * MetalEnc.l2normRows(Batch) (MetalEnc.swift:249-272), Kernels.swift:41-52. */
+int gd_l2norm_rows(gd_ctx *ctx, float *x, int d, int rowsPerTok,
+                   int64_t tokStride, int64_t tokens, float eps);
+
+/* In-place x * w / sqrt(mean(x^2) + eps) per row of length d (w[d]).
+ * MetalEnc.rmsnormRows (MetalEnc.swift:238-247), Kernels.swift:26-37. */
+int gd_rmsnorm_rows(gd_ctx *ctx, float *x, int d, int64_t rows,
+                    const float *w, float eps);
+
+/* y[row] = x[row] * w / sqrt(mean(x^2) + eps), rows of length n, into f32
+ * or f16 y.  MetalEnc.rmsnorm / rmsnormBatch (MetalEnc.swift:213-236). */
+int gd_rmsnorm(gd_ctx *ctx, const float *x, const float *w, void *y,
+               int y_dtype, int64_t n, int64_t rows, float eps);
+
+/* Elementwise glue: a = silu(a)*b (silu_mul), a = a*silu(b) (mul_silu),
+ * x += y (add_inplace).  MetalEnc.swift:572-597, Kernels.metal:1118-1139. */
+int gd_silu_mul(gd_ctx *ctx, float *a, const float *b, int64_t n);
+int gd_mul_silu(gd_ctx *ctx, float *a, const float *b, int64_t n);
+int gd_add(gd_ctx *ctx, float *x, const float *y, int64_t n);
+
+/* ---- GDN recurrence -----------------------------------------------------------
+ * State S[nV][dS][dS] f32, key-major: S[h][i*dS + j], i = key, j = value
+ * (GDN.swift:9-16, Kernels.metal:1225).  Head map hk = hv % nK
+ * (GDN.swift:79).  Per token and value head:
+ *   gamma = exp(g); S *= gamma; sk = S^T k; delta = beta*(v - sk);
+ *   S += k (x) delta; o = qScale * S^T q            (GDN.swift:84-108) */
+
+/* One token, q/k already L2-normalized: MetalEnc.gdnScan (MetalEnc.swift:636-653),
+ * gdn_scan (Kernels.metal:1206-1243).  q,k [nK*dS], v [nV*dS], g,beta [nV]. */
+int gd_gdn_scan(gd_ctx *ctx, const float *q, const float *k, const float *v,
+                const float *g, const float *beta, float *S, float *o,
+                int nV, int nK, int dS, float qScale);
+
+/* N tokens out of the conv output rows convOutN[N][convDim] = [q|k|v]:
+ * MetalEnc.gdnScanBatch (MetalEnc.swift:741-778), gdn_scan_batch2
+ * (Kernels.metal:1570-1625).  Runs the chunked kernel below. */
+int gd_gdn_scan_batch(gd_ctx *ctx, const float *convOutN, int keyDim,
+                      int valueDim, int convDim, const float *gN,
+                      const float *betaN, float *S, float *oN, int nV, int nK,
+                      int dS, float qScale, int64_t N);
+
+/* Fused state-carry decode step for B independent sequences (no reference
+ * counterpart as one kernel: it fuses gdn_gate, l2norm_rows x2 and gdn_scan,
+ * MetalEngine.swift:730-754).  Per sequence b:
+ *   q,k raw [B][nK][dS], v [B][nV][dS] (dtype io_dtype), o [B][nV][dS]
+ *   (io_dtype), S [B][nV][dS][dS] f32 in place.
+ *   If dt != NULL: beta = sigmoid(beta_in), g = softplus(g_in + dt)*aNeg
+ *   (pre-activations [B][nV]); else beta_in/g_in are beta and g.
+ *   q and k are L2-normalized with eps before use. */
+int gd_gdn_decode(gd_ctx *ctx, int B, int nV, int nK, int dS,
+                  const void *q, const void *k, const void *v, int io_dtype,
+                  const float *g_in, const float *beta_in, const float *dt,
+                  const float *aNeg, float *S, void *o, float qScale,
+                  float eps);
+
+/* Chunked prefill of T tokens for one sequence (new: the reference scans
+ * token by token; the chunk identity is the closed form of
+ * LLM/src/CoreML/MtpRollback.swift:3-12, 20-42).
+ *   q,k [T][nK][dk], v [T][nV][dv] (io_dtype, row stride given in elements:
+ *   q_stride, k_stride, v_stride between tokens), g, beta [T][nV] f32,
+ *   S [nV][dk][dv] f32 in/out, o [T][nV][dv] (o_dtype, stride o_stride).
+ *   q/k are used as given (normalize first with gd_l2norm_rows).  C is the
+ *   chunk length (16, 32 or 64); T need not be a multiple of C.
+ *   Currently dk == dv == 128. */
+int gd_gdn_prefill(gd_ctx *ctx, int64_t T, int nV, int nK, int dk, int dv,
+                   const void *q, int64_t q_stride, const void *k,
+                   int64_t k_stride, const void *v, int64_t v_stride,
+                   int io_dtype, const float *g, const float *beta, float *S,
+                   void *o, int64_t o_stride, int o_dtype, float qScale,
+                   int C);
+
+/* ---- synthetic data on the device -----------------------------------------
+ * Counter-addressable copy of the reference's test LCG
+ * (MetalSelfTest.swift:12-21): element i of stream `seed` is the (i+1)-th
+ * state s = s*6364136223846793005 + 1442695040888963407 from
+ * s0 = seed + 0x9E3779B97F4A7C15, bits = s >> 33.  Each thread jumps ahead
+ * to its run, so the stream is identical to the sequential one. */
+
+/* out[i] = bits/2^32 * (hi-lo) + lo  (f32), i < n. */
+int gd_rand_uniform(gd_ctx *ctx, float *out, size_t n, uint64_t seed,
+                    float lo, float hi);
+/* Normal(mean, std) by Box-Muller on the pairs (2i, 2i+1) of the stream,
+ * into f32 or f16. */
+int gd_rand_normal(gd_ctx *ctx, void *out, int dtype, size_t n, uint64_t seed,
+                   float mean, float std);
+/* A random Q2_0 matrix straight into device planes: codes iid uniform over
+ * {0,1,2} (ternary -1,0,+1, p = 1/3 each: code = (bits*3)>>32 of stream
+ * `seed`), scales RNE-f16 of lo + (hi-lo)*u over stream seed+1. */
+int gd_rand_q2w(gd_ctx *ctx, gd_q2w *w, uint64_t seed, float lo, float hi);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GADEON_HIP_H */

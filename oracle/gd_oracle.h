@@ -1,0 +1,92 @@
+/*
+ * gd_oracle.h -- CPU restatement of the reference's Q2_0 and Gated DeltaNet
+ * math, used ONLY as the checker in tests/ and as the CPU baseline leg of
+ * bench.py.  It is test infrastructure, never part of the product path: the
+ * library (gadeon_amd/libgadeon_hip.so) neither links nor calls it.
+ *
+ * Every function names the reference file:line it restates.  f32 functions
+ * keep the reference's operation order; *_f64 functions are independent
+ * double-precision formulations used to pin the f32 ones.
+ */
+#ifndef GD_ORACLE_H
+#define GD_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- deterministic inputs (MetalSelfTest.swift:12-21) ---------------------- */
+void or_lcg_uniform(float *out, size_t n, uint64_t seed, float lo, float hi);
+void or_lcg_normal(float *out, size_t n, uint64_t seed, float mean, float sd);
+void or_lcg_normal_f16(uint16_t *out, size_t n, uint64_t seed, float mean, float sd);
+/* GGUF Q2_0 blocks [R][K/128]: codes uniform over {0,1,2} from stream seed,
+ * scales f16(lo + (hi-lo) u) from stream seed+1. */
+void or_lcg_q2_0(uint8_t *blocks, int64_t K, int64_t R, uint64_t seed, float lo, float hi);
+
+/* ---- f16 helpers (IEEE binary16, round to nearest even) -------------------- */
+float or_h2f(uint16_t h);
+uint16_t or_f2h(float f);
+
+/* ---- Q2_0 (Quant.swift) ------------------------------------------------------ */
+/* Quant.swift:15-30 */
+void or_q2_0_dequant(const uint8_t *blocks, size_t n, float *out);
+/* Quant.swift:36-77; rows split over `threads` pthreads (concurrentPerform, :52). */
+void or_q2_0_matvec(const uint8_t *w, int64_t K, int64_t M, const float *x, float *out,
+                    int threads);
+/* Independent f64 brute force: out[m] = sum_k (code-1)*d*x[k] in double. */
+void or_q2_0_matvec_f64(const uint8_t *w, int64_t K, int64_t M, const double *x, double *out);
+
+/* ---- primitives (Kernels.swift:5-84) ---------------------------------------- */
+float or_silu(float x);
+float or_sigmoid(float x);
+float or_softplus(float x);
+/* Kern.rmsnorm (Kernels.swift:15-23) */
+void or_rmsnorm(const float *x, const float *w, float *y, int64_t n, float eps);
+/* Kern.rmsnormRows (Kernels.swift:26-37) */
+void or_rmsnorm_rows(float *x, int d, int64_t rows, const float *w, float eps);
+/* Kern.l2normRows (Kernels.swift:41-52) */
+void or_l2norm_rows(float *x, int d, int64_t rows, float eps);
+/* Kern.softmaxInPlace (Kernels.swift:54-61) */
+void or_softmax(float *x, int n);
+/* Kern.ropeNeox (Kernels.swift:66-84) */
+void or_rope_neox(float *x, int headDim, int nHead, int nRot, float base, int pos);
+
+/* ---- GDN (GDN.swift) ---------------------------------------------------------- */
+/* Gates, GDN.swift:39-42: beta = sigmoid(bPre), g = softplus(aPre + dt[h]) * aNeg[h]. */
+void or_gdn_gate(const float *bPre, const float *aPre, const float *dt, const float *aNeg,
+                 float *beta, float *g, int nV, int64_t count);
+/* Causal conv + silu + ring shift for one token, GDN.swift:44-62. */
+void or_gdn_conv(const float *qkvMix, float *ring, const float *cw, float *out, int convDim,
+                 int dConv);
+/* The delta-rule scan for one token, GDN.swift:71-109, q/k already normalized. */
+void or_gdn_scan(const float *q, const float *k, const float *v, const float *g,
+                 const float *beta, float *S, float *o, int nV, int nK, int dS, float qScale);
+/* Same recurrence in double (independent check of the f32 order). */
+void or_gdn_scan_f64(const double *q, const double *k, const double *v, const double *g,
+                     const double *beta, double *S, double *o, int nV, int nK, int dS,
+                     double qScale);
+/* Chunked (WY/UT) form in double for one sequence of T tokens:
+ * q,k [T][nK][dk], v [T][nV][dv], g,beta [T][nV], S [nV][dk][dv], o [T][nV][dv]. */
+void or_gdn_chunked_f64(int64_t T, int nV, int nK, int dk, int dv, const double *q,
+                        const double *k, const double *v, const double *g, const double *beta,
+                        double *S, double *o, double qScale, int C);
+
+/* ---- closed form (MtpRollback.swift:20-60) ------------------------------------ */
+void or_mtp_state_after(int m, int H, int DK, int DV, int C, const float *s0, const float *delta,
+                        const float *k, const float *gcum, float *out);
+
+/* ---- threaded batch of independent decode scans (CPU baseline) ---------------- */
+/* B sequences, one token each: per sequence l2norm q,k (eps) then or_gdn_scan.
+ * q,k [B][nK*dS], v/o [B][nV*dS], g/beta [B][nV], S [B][nV*dS*dS]. */
+void or_gdn_decode_batch(int B, int nV, int nK, int dS, float *q, float *k, const float *v,
+                         const float *g, const float *beta, float *S, float *o, float qScale,
+                         float eps, int threads);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

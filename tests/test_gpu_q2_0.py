@@ -1,0 +1,196 @@
+"""GPU parity of the Q2_0 path against the CPU oracle (Quant.swift restated).
+
+Tolerances (norm-wise relative error max|a-b|/max|b|, MetalSelfTest.swift:437-448):
+  * codec, repack, dequant, synthetic codes/scales: bit-exact;
+  * GEMV: 1e-4 (the oracle sees the same f16 x values; only summation order
+    differs) -- inside the north-star bound of 1e-2;
+  * GEMM: 2e-3 for f32 out (the reference's own GEMM gate, MetalSelfTest.swift:487),
+    the oracle receiving X rounded to f16 exactly as both GEMMs stage it.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import gadeon_amd as ga
+import oracle as O
+from conftest import rel_diff
+
+pytestmark = pytest.mark.gpu
+
+
+def upload_w(ctx, blocks, K, R):
+    w = ga.Q2W()
+    ctx.gd_q2_0_upload(blocks.ctypes.data, K, R, C.byref(w))
+    return w
+
+
+def free_w(ctx, w):
+    ctx.gd_q2w_free(C.byref(w))
+
+
+def export_w(ctx, w):
+    n = w.R * (w.K // 128) * 34
+    d = ctx.alloc(n)
+    ctx.gd_q2_0_export(C.byref(w), d)
+    out = ctx.get(d, n, np.uint8)
+    ctx.free(d)
+    return out
+
+
+@pytest.mark.parametrize("K,R", [(128, 1), (1024, 3072), (384, 37), (5120, 64)])
+def test_repack_export_round_trip(ctx, K, R):
+    blocks = O.lcg_q2_0(K, R, 100 + K)
+    w = upload_w(ctx, blocks, K, R)
+    assert np.array_equal(export_w(ctx, w), blocks)
+    free_w(ctx, w)
+
+
+def test_device_generators_match_sequential_lcg(ctx):
+    K, R = 1024, 300
+    w = ga.Q2W()
+    ctx.gd_q2w_alloc(K, R, C.byref(w))
+    ctx.gd_rand_q2w(C.byref(w), 42, 0.01, 0.05)
+    assert np.array_equal(export_w(ctx, w), O.lcg_q2_0(K, R, 42))
+    free_w(ctx, w)
+    n = 100_003
+    d = ctx.alloc(n * 4)
+    ctx.gd_rand_uniform(d, n, 9, -2.0, 3.0)
+    assert np.array_equal(ctx.get(d, n, np.float32), O.lcg_uniform(n, 9, -2.0, 3.0))
+    ctx.gd_rand_normal(d, ga.F32, n, 10, 0.5, 2.0)
+    z = ctx.get(d, n, np.float32)
+    assert rel_diff(z, O.lcg_normal(n, 10, 0.5, 2.0)) < 1e-5
+    ctx.free(d)
+
+
+def test_dequant_rows_exact(ctx):
+    K, R = 5120, 50
+    blocks = O.lcg_q2_0(K, R, 7)
+    w = upload_w(ctx, blocks, K, R)
+    ids = np.array([3, 0, 49, 17, 3, 60, -1], np.int32)    # last two out of range -> 0
+    dids = ctx.put(ids)
+    dout = ctx.alloc(ids.size * K * 4)
+    ctx.gd_q2_0_dequant_rows(C.byref(w), dids, ids.size, dout)
+    got = ctx.get(dout, (ids.size, K), np.float32)
+    full = O.q2_0_dequant(blocks, K * R).reshape(R, K)
+    for n, i in enumerate(ids):
+        want = full[i] if 0 <= i < R else np.zeros(K, np.float32)
+        assert np.array_equal(got[n], want), (n, i)
+    free_w(ctx, w)
+
+
+GEMV_SHAPES = [(1024, 3072), (128, 5), (384, 37), (2048, 1000), (5120, 777), (17408, 130),
+               (6144, 64)]
+
+
+@pytest.mark.parametrize("K,R", GEMV_SHAPES)
+@pytest.mark.parametrize("xt", [ga.F16, ga.F32])
+def test_gemv_vs_oracle(ctx, K, R, xt):
+    blocks = O.lcg_q2_0(K, R, K + R)
+    w = upload_w(ctx, blocks, K, R)
+    if xt == ga.F16:
+        xh = O.lcg_normal_f16(K, 5)
+        x_ref = xh.astype(np.float32)
+        dx = ctx.put(xh.view(np.uint16))
+    else:
+        x_ref = O.lcg_normal(K, 5)
+        dx = ctx.put(x_ref)
+    dy = ctx.alloc(R * 4)
+    ctx.gd_q2_0_gemv(C.byref(w), dx, xt, dy)
+    y = ctx.get(dy, R, np.float32)
+    want = O.q2_0_matvec(blocks, K, R, x_ref, threads=8)
+    assert rel_diff(y, want) < 1e-4
+    # The reference's own absolute gate for the gemv self-test (MetalSelfTest.swift:504)
+    # holds at these magnitudes too.
+    assert np.max(np.abs(y - want)) < 1e-3 * max(1.0, np.max(np.abs(want)) / 10)
+    free_w(ctx, w)
+    ctx.free(dx)
+    ctx.free(dy)
+
+
+def test_gemv_zero_and_single_weight(ctx):
+    K, R = 1024, 8
+    codes = np.ones(K * R, np.uint8)
+    codes[3 * K + 999] = 3                     # +2d at row 3, k 999
+    scales = np.full(K * R // 128, 0.03, np.float16).view(np.uint16)
+    blocks = np.empty(K * R // 128 * 34, np.uint8)
+    ga.load().gd_q2_0_pack(codes.ctypes.data, scales.ctypes.data, K * R, blocks.ctypes.data)
+    w = upload_w(ctx, blocks, K, R)
+    x = O.lcg_normal(K, 3)
+    dx = ctx.put(x)
+    dy = ctx.alloc(R * 4)
+    ctx.gd_q2_0_gemv(C.byref(w), dx, ga.F32, dy)
+    y = ctx.get(dy, R, np.float32)
+    want = np.zeros(R, np.float32)
+    want[3] = 2 * np.float32(np.float16(0.03)) * x[999]
+    # sum(code*x) and sum(x) are formed in different orders, so the all-zero
+    # rows carry f32 roundoff of the size of d * sum|x| * 2^-24.
+    atol = 1e-6 * 0.03 * np.abs(x).sum()
+    assert np.allclose(y, want, rtol=1e-5, atol=atol)
+    free_w(ctx, w)
+
+
+def _gemm(ctx, w, X, xt, yt, T, R):
+    dX = ctx.put(X)
+    dY = ctx.alloc(T * R * (4 if yt == ga.F32 else 2))
+    ctx.gd_q2_0_gemm(C.byref(w), T, dX, xt, dY, yt)
+    Y = ctx.get(dY, (T, R), np.float32 if yt == ga.F32 else np.float16)
+    ctx.free(dX)
+    ctx.free(dY)
+    return Y.astype(np.float32)
+
+
+@pytest.mark.parametrize("T,K,R", [(5, 1024, 300), (33, 5120, 200), (128, 2048, 256),
+                                   (200, 17408, 96), (1, 128, 1)])
+@pytest.mark.parametrize("xt,yt", [(ga.F16, ga.F32), (ga.F32, ga.F32), (ga.F16, ga.F16)])
+def test_gemm_vs_oracle(ctx, T, K, R, xt, yt):
+    blocks = O.lcg_q2_0(K, R, 3 * K + R)
+    w = upload_w(ctx, blocks, K, R)
+    Xh = O.lcg_normal_f16(T * K, 77).reshape(T, K)
+    X = Xh.view(np.uint16) if xt == ga.F16 else Xh.astype(np.float32)
+    Y = _gemm(ctx, w, X, xt, yt, T, R)
+    Xr = Xh.astype(np.float32)                 # f16 staging, as both GEMMs stage X
+    want = np.stack([O.q2_0_matvec(blocks, K, R, Xr[t], threads=8) for t in range(T)])
+    assert rel_diff(Y, want) < (2e-3 if yt == ga.F16 else 1e-4)
+    free_w(ctx, w)
+
+
+def test_gemm_full_size_sampled_rows(ctx):
+    """BASELINE config 1 shapes at full size: every output row against the GPU
+    GEMV of the same weights (independent kernel), and 48 sampled rows x all
+    512 tokens against the oracle."""
+    T = 512
+    for K, R in ((5120, 17408), (17408, 5120)):
+        w = ga.Q2W()
+        ctx.gd_q2w_alloc(K, R, C.byref(w))
+        ctx.gd_rand_q2w(C.byref(w), K + 1, 0.01, 0.05)
+        dX = ctx.alloc(T * K * 2)
+        ctx.gd_rand_normal(dX, ga.F16, T * K, 55, 0.0, 1.0)
+        dY = ctx.alloc(T * R * 2)
+        ctx.gd_q2_0_gemm(C.byref(w), T, dX, ga.F16, dY, ga.F16)
+        Y = ctx.get(dY, (T, R), np.float16).astype(np.float32)
+        X = ctx.get(dX, (T, K), np.float16)
+        # GEMV on a few tokens (all rows)
+        dy = ctx.alloc(R * 4)
+        for t in (0, 1, 255, 511):
+            ctx.gd_q2_0_gemv(C.byref(w), dX + t * K * 2, ga.F16, dy)
+            assert rel_diff(Y[t], ctx.get(dy, R, np.float32)) < 2e-3, t
+        # Oracle on sampled rows
+        blocks = export_w(ctx, w).reshape(R, -1)
+        rows = np.random.default_rng(K).choice(R, 48, replace=False)
+        sub = np.ascontiguousarray(blocks[rows])
+        Xr = X.astype(np.float32)
+        want = np.stack([O.q2_0_matvec(sub, K, 48, Xr[t], threads=8) for t in range(T)])
+        assert rel_diff(Y[:, rows], want) < 2e-3
+        for p in (dX, dY, dy):
+            ctx.free(p)
+        free_w(ctx, w)
+
+
+def test_invalid_shapes_are_errors(ctx):
+    w = ga.Q2W()
+    lib = ga.load()
+    assert lib.gd_q2w_alloc(ctx.h, 100, 4, C.byref(w)) == ga.GD_EINVAL
+    assert b"multiple of 128" in lib.gd_last_error(ctx.h)
+    bad = ga.Q2W(None, None, 128, 1)
+    assert lib.gd_q2_0_gemv(ctx.h, C.byref(bad), None, ga.F16, None) == ga.GD_EINVAL
