@@ -49,6 +49,7 @@ _PROTOS = {
     "gd_download": (_i, [_vp, _vp, _vp, _sz]),
     "gd_copy": (_i, [_vp, _vp, _vp, _sz]),
     "gd_fill_u32": (_i, [_vp, _vp, C.c_uint32, _sz]),
+    "gd_cast": (_i, [_vp, _vp, _i, _vp, _i, _sz]),
     "gd_sync": (_i, [_vp]),
     "gd_timer_start": (_i, [_vp]),
     "gd_timer_stop": (_i, [_vp, _fp]),

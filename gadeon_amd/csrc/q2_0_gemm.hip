@@ -67,36 +67,28 @@ __global__ __launch_bounds__(THREADS) void q2_0_gemm_kernel(
     const int wrow = tid >> 1;       // weight row within the tile
     const int wpart = tid & 1;       // which 32 codes of the 64-code slice
 
+    // Tile rows past T (tokens) or R (weight rows) re-read the last valid row:
+    // their outputs are never stored and no valid output depends on them, so
+    // the loads need no branch and all of them issue together.
     auto load_slice = [&](int k0) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int seg = tid + THREADS * i;
             const int row = seg >> 3, col = (seg & 7) * 8;
-            const int t = t0 + row;
+            const int t = min(t0 + row, T - 1);
             if (XT == 0) {
-                if (t < T) xr[i] = *(const u32x4 *)((const f16 *)Xv + (size_t)t * K + k0 + col);
-                else xr[i] = u32x4{0u, 0u, 0u, 0u};
+                xr[i] = *(const u32x4 *)((const f16 *)Xv + (size_t)t * K + k0 + col);
             } else {
-                if (t < T) {
-                    const f32x4 *p = (const f32x4 *)((const float *)Xv + (size_t)t * K + k0 + col);
-                    xf[2 * i] = p[0];
-                    xf[2 * i + 1] = p[1];
-                } else {
-                    xf[2 * i] = f32x4{0.f, 0.f, 0.f, 0.f};
-                    xf[2 * i + 1] = xf[2 * i];
-                }
+                const f32x4 *p = (const f32x4 *)((const float *)Xv + (size_t)t * K + k0 + col);
+                xf[2 * i] = p[0];
+                xf[2 * i + 1] = p[1];
             }
         }
-        const int r = r0 + wrow;
-        if (r < R) {
-            const uint32_t *p = codes + ((size_t)r * cpr + (k0 >> 2) + 8 * wpart) / 4;
-            wc2[0] = p[0];
-            wc2[1] = p[1];
-            wd = scales[(size_t)r * nblk + (k0 >> 7)];
-        } else {
-            wc2[0] = wc2[1] = 0x55555555u;   // code 1 -> weight 0
-            wd = 0;
-        }
+        const int r = min(r0 + wrow, R - 1);
+        const uint32_t *p = codes + ((size_t)r * cpr + (k0 >> 2) + 8 * wpart) / 4;
+        wc2[0] = p[0];
+        wc2[1] = p[1];
+        wd = scales[(size_t)r * nblk + (k0 >> 7)];
     };
 
     auto store_slice = [&](int buf) {

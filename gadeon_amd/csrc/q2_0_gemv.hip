@@ -25,7 +25,6 @@
 
 namespace {
 
-constexpr int GEMV_G = 4;           // row groups (of 4 rows) per wave
 constexpr int GEMV_THREADS = 256;   // 4 waves
 
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
@@ -72,103 +71,86 @@ __device__ __forceinline__ float chunk_dot(const u32x4 &cw, const uint32_t (*xp)
     return fmaf(a, 4.0f, b) * 0x1p16f;    // 2^18 a + 2^16 b
 }
 
-// XT: 0 = f16 x, 1 = f32 x.  KW: waves sharing one row set (split of K).
-template <int XT>
-__global__ __launch_bounds__(GEMV_THREADS) void q2_0_gemv_kernel(
-        const u32x4 *__restrict__ codes, const uint16_t *__restrict__ scales,
-        const void *__restrict__ xv, float *__restrict__ y, int K, int R, int KW) {
-    constexpr int XS = XT == 0 ? 1 : 2;
-    __shared__ float red[GEMV_THREADS / 64][4 * GEMV_G];
-
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int cl = lane & 15;          // chunk lane within the row slot
-    const int slot = lane >> 4;        // row slot 0..3
-    const int sets_per_block = 4 / KW;
-    const int rowset = blockIdx.x * sets_per_block + wave / KW;
-    const int kpart = wave % KW;
-    const int row0 = rowset * (4 * GEMV_G);
-    const int cpr = K >> 6;            // 16-byte chunks per row
-    const int nblk = K >> 7;
-    const int steps = (cpr + 15) >> 4;
-
-    float acc[GEMV_G];
+// x for codes 64c .. 64c+63 of chunk c, as the pairs (16q+k, 16q+k+8), plus
+// their f32 sum.  XT 0: f16 x.  XT 1: f32 x split exactly into hi + lo f16.
+template <int XT, int XS>
+__device__ __forceinline__ float load_x_chunk(const void *__restrict__ xv, int c,
+                                              uint32_t (&xp)[XS][8][4]) {
+    float sx = 0.f;
+    if (XT == 0) {
+        const u32x4 *xs = (const u32x4 *)xv + 8 * c;
+        uint32_t xd[32];
 #pragma unroll
-    for (int g = 0; g < GEMV_G; g++) acc[g] = 0.f;
-
-    for (int s = kpart; s < steps; s += KW) {
-        const int c = cl + 16 * s;
-        if (c < cpr) {
-            // x for codes 64c .. 64c+63, as pairs (16q+k, 16q+k+8).
-            uint32_t xp[XS][8][4];
-            float sx = 0.f;
-            if (XT == 0) {
-                const u32x4 *xs = (const u32x4 *)xv + 8 * c;
-                uint32_t xd[32];
+        for (int i = 0; i < 8; i++) {
+            const u32x4 t = xs[i];
+            xd[4 * i] = t[0]; xd[4 * i + 1] = t[1];
+            xd[4 * i + 2] = t[2]; xd[4 * i + 3] = t[3];
+        }
 #pragma unroll
-                for (int i = 0; i < 8; i++) {
-                    const u32x4 t = xs[i];
-                    xd[4 * i] = t[0]; xd[4 * i + 1] = t[1];
-                    xd[4 * i + 2] = t[2]; xd[4 * i + 3] = t[3];
-                }
+        for (int i = 0; i < 32; i++) sx = dot2(xd[i], 0x3C003C00u, sx);
 #pragma unroll
-                for (int i = 0; i < 32; i++) sx = dot2(xd[i], 0x3C003C00u, sx);
+        for (int q = 0; q < 4; q++)
 #pragma unroll
-                for (int q = 0; q < 4; q++)
+            for (int k = 0; k < 8; k++) xp[0][k][q] = xpair(xd, q, k);
+    } else {
+        const f32x4 *xs = (const f32x4 *)xv + 16 * c;
+        uint32_t hi[32], lo[32];
 #pragma unroll
-                    for (int k = 0; k < 8; k++) xp[0][k][q] = xpair(xd, q, k);
-            } else {
-                const f32x4 *xs = (const f32x4 *)xv + 16 * c;
-                uint32_t hi[32], lo[32];
+        for (int i = 0; i < 16; i++) {
+            const f32x4 t = xs[i];
 #pragma unroll
-                for (int i = 0; i < 16; i++) {
-                    const f32x4 t = xs[i];
-#pragma unroll
-                    for (int e = 0; e < 4; e += 2) {
-                        const float x0 = t[e], x1 = t[e + 1];
-                        sx += x0;
-                        sx += x1;
-                        const f16 h0 = (f16)x0, h1 = (f16)x1;
-                        const f16 l0 = (f16)(x0 - (float)h0), l1 = (f16)(x1 - (float)h1);
-                        hi[2 * i + e / 2] = (uint32_t)__builtin_bit_cast(uint16_t, h0) |
-                                            ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
-                        lo[2 * i + e / 2] = (uint32_t)__builtin_bit_cast(uint16_t, l0) |
-                                            ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
-                    }
-                }
-#pragma unroll
-                for (int q = 0; q < 4; q++)
-#pragma unroll
-                    for (int k = 0; k < 8; k++) {
-                        xp[0][k][q] = xpair(hi, q, k);
-                        xp[XS - 1][k][q] = xpair(lo, q, k);
-                    }
-            }
-            // Issue every row's weight load before any decode.
-            u32x4 cw[GEMV_G];
-            float d[GEMV_G];
-#pragma unroll
-            for (int g = 0; g < GEMV_G; g++) {
-                const int r = row0 + 4 * g + slot;
-                if (r < R) {
-                    cw[g] = __builtin_nontemporal_load(codes + (size_t)r * cpr + c);
-                    d[g] = gd_h2f(scales[(size_t)r * nblk + (c >> 1)]);
-                } else {
-                    cw[g] = u32x4{0u, 0u, 0u, 0u};
-                    d[g] = 0.f;
-                }
-            }
-#pragma unroll
-            for (int g = 0; g < GEMV_G; g++) {
-                const float cx = chunk_dot<XS>(cw[g], xp);
-                acc[g] = fmaf(d[g], cx - sx, acc[g]);
+            for (int e = 0; e < 4; e += 2) {
+                const float x0 = t[e], x1 = t[e + 1];
+                sx += x0;
+                sx += x1;
+                const f16 h0 = (f16)x0, h1 = (f16)x1;
+                const f16 l0 = (f16)(x0 - (float)h0), l1 = (f16)(x1 - (float)h1);
+                hi[2 * i + e / 2] = (uint32_t)__builtin_bit_cast(uint16_t, h0) |
+                                    ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+                lo[2 * i + e / 2] = (uint32_t)__builtin_bit_cast(uint16_t, l0) |
+                                    ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
             }
         }
-    }
-
-    // Reduce over the 16 chunk lanes of each row slot.
 #pragma unroll
-    for (int g = 0; g < GEMV_G; g++) {
+        for (int q = 0; q < 4; q++)
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                xp[0][k][q] = xpair(hi, q, k);
+                xp[XS - 1][k][q] = xpair(lo, q, k);
+            }
+    }
+    return sx;
+}
+
+// One chunk step for G row groups: all G weight loads issue before any decode.
+template <int XS, int G>
+__device__ __forceinline__ void rows_step(const u32x4 *__restrict__ codes,
+                                          const uint16_t *__restrict__ scales, int row0,
+                                          int slot, int c, int cpr, int nblk, int R,
+                                          const uint32_t (&xp)[XS][8][4], float sx,
+                                          float (&acc)[G]) {
+    // Rows past R read row R-1 (in bounds) and are zeroed by their scale, so
+    // the loads carry no branch and all 2G of them are in flight together.
+    u32x4 cw[G];
+    uint16_t dh[G];
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        const int r = min(row0 + 4 * g + slot, R - 1);
+        cw[g] = __builtin_nontemporal_load(codes + (size_t)r * cpr + c);
+        dh[g] = scales[(size_t)r * nblk + (c >> 1)];
+    }
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        const float d = row0 + 4 * g + slot < R ? gd_h2f(dh[g]) : 0.f;
+        const float cx = chunk_dot<XS>(cw[g], xp);
+        acc[g] = fmaf(d, cx - sx, acc[g]);
+    }
+}
+
+template <int G>
+__device__ __forceinline__ void reduce16(float (&acc)[G]) {
+#pragma unroll
+    for (int g = 0; g < G; g++) {
         float v = acc[g];
         v += __shfl_xor(v, 1, 64);
         v += __shfl_xor(v, 2, 64);
@@ -176,24 +158,91 @@ __global__ __launch_bounds__(GEMV_THREADS) void q2_0_gemv_kernel(
         v += __shfl_xor(v, 8, 64);
         acc[g] = v;
     }
-    if (KW == 1) {
+}
+
+// Row-streaming GEMV: every wave owns whole rows (row sets of 4G rows, one
+// row per 16-lane slot) and walks the row sets grid-stride.  When K fits one
+// chunk step (K <= 1024) the lane's x chunk is loaded once and stays in
+// registers for every row the wave visits.
+template <int XT, int G>
+__global__ __launch_bounds__(GEMV_THREADS) void q2_0_gemv_rows_kernel(
+        const u32x4 *__restrict__ codes, const uint16_t *__restrict__ scales,
+        const void *__restrict__ xv, float *__restrict__ y, int K, int R) {
+    constexpr int XS = XT == 0 ? 1 : 2;
+    const int lane = threadIdx.x & 63;
+    const int cl = lane & 15, slot = lane >> 4;
+    const int cpr = K >> 6, nblk = K >> 7;
+    const int steps = (cpr + 15) >> 4;
+    const int nsets = (R + 4 * G - 1) / (4 * G);
+    const int wave_id = blockIdx.x * (GEMV_THREADS / 64) + (threadIdx.x >> 6);
+    const int nwaves = gridDim.x * (GEMV_THREADS / 64);
+
+    uint32_t xp[XS][8][4];
+    float sx = 0.f;
+    const bool one_step = steps == 1;
+    if (one_step && cl < cpr) sx = load_x_chunk<XT, XS>(xv, cl, xp);
+
+    for (int set = wave_id; set < nsets; set += nwaves) {
+        const int row0 = set * 4 * G;
+        float acc[G];
+#pragma unroll
+        for (int g = 0; g < G; g++) acc[g] = 0.f;
+        for (int s = 0; s < steps; s++) {
+            const int c = cl + 16 * s;
+            if (c < cpr) {
+                if (!one_step) sx = load_x_chunk<XT, XS>(xv, c, xp);
+                rows_step<XS, G>(codes, scales, row0, slot, c, cpr, nblk, R, xp, sx, acc);
+            }
+        }
+        reduce16<G>(acc);
         if (cl == 0) {
 #pragma unroll
-            for (int g = 0; g < GEMV_G; g++) {
+            for (int g = 0; g < G; g++) {
                 const int r = row0 + 4 * g + slot;
                 if (r < R) y[r] = acc[g];
             }
         }
-        return;
     }
+}
+
+// K-split GEMV for few rows and long K: the four waves of a workgroup share
+// one row set of 4G rows and take interleaved chunk steps; partial sums meet
+// once in LDS.
+template <int XT, int G>
+__global__ __launch_bounds__(GEMV_THREADS) void q2_0_gemv_ksplit_kernel(
+        const u32x4 *__restrict__ codes, const uint16_t *__restrict__ scales,
+        const void *__restrict__ xv, float *__restrict__ y, int K, int R) {
+    constexpr int XS = XT == 0 ? 1 : 2;
+    constexpr int KW = GEMV_THREADS / 64;
+    __shared__ float red[KW][4 * G];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int cl = lane & 15, slot = lane >> 4;
+    const int row0 = blockIdx.x * 4 * G;
+    const int cpr = K >> 6, nblk = K >> 7;
+    const int steps = (cpr + 15) >> 4;
+
+    float acc[G];
+#pragma unroll
+    for (int g = 0; g < G; g++) acc[g] = 0.f;
+    for (int s = wave; s < steps; s += KW) {
+        const int c = cl + 16 * s;
+        if (c < cpr) {
+            uint32_t xp[XS][8][4];
+            const float sx = load_x_chunk<XT, XS>(xv, c, xp);
+            rows_step<XS, G>(codes, scales, row0, slot, c, cpr, nblk, R, xp, sx, acc);
+        }
+    }
+    reduce16<G>(acc);
     if (cl == 0) {
 #pragma unroll
-        for (int g = 0; g < GEMV_G; g++) red[wave][4 * g + slot] = acc[g];
+        for (int g = 0; g < G; g++) red[wave][4 * g + slot] = acc[g];
     }
     __syncthreads();
-    if (kpart == 0 && lane < 4 * GEMV_G) {
+    if (wave == 0 && lane < 4 * G) {
         float v = 0.f;
-        for (int w = 0; w < KW; w++) v += red[wave + w][lane];
+#pragma unroll
+        for (int w = 0; w < KW; w++) v += red[w][lane];
         const int r = row0 + 4 * (lane >> 2) + (lane & 3);
         if (r < R) y[r] = v;
     }
@@ -262,15 +311,32 @@ extern "C" int gd_q2_0_gemv(gd_ctx *ctx, const gd_q2w *w, const void *x, int x_d
                "gd_q2_0_gemv: K=%lld or R=%lld too large", (long long)w->K, (long long)w->R);
     const int K = (int)w->K, R = (int)w->R;
     const int steps = ((K >> 6) + 15) >> 4;
-    const int KW = steps >= 4 ? 4 : (steps >= 2 ? 2 : 1);
-    const int rows_per_block = (4 / KW) * 4 * GEMV_G;
-    const unsigned grid = gd_blocks(R, rows_per_block);
-    if (x_dtype == GD_F16)
-        hipLaunchKernelGGL(q2_0_gemv_kernel<0>, dim3(grid), dim3(GEMV_THREADS), 0, ctx->stream,
-                           (const u32x4 *)w->codes, (const uint16_t *)w->scales, x, y, K, R, KW);
-    else
-        hipLaunchKernelGGL(q2_0_gemv_kernel<1>, dim3(grid), dim3(GEMV_THREADS), 0, ctx->stream,
-                           (const u32x4 *)w->codes, (const uint16_t *)w->scales, x, y, K, R, KW);
+    const auto *c = (const u32x4 *)w->codes;
+    const auto *s = (const uint16_t *)w->scales;
+    const int cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
+    // Enough row sets to give every CU several waves -> stream whole rows;
+    // otherwise split K across the waves of a workgroup.
+    const bool rows = steps == 1 || (R + 31) / 32 >= 8 * cus;
+    if (rows) {
+        const bool big = (R + 31) / 32 >= 8 * cus;
+        const int G = big ? 8 : 2;
+        const int nsets = (R + 4 * G - 1) / (4 * G);
+        const unsigned grid = (unsigned)std::min<int64_t>((nsets + 3) / 4, (int64_t)cus * 8);
+#define GD_ROWS(XT, G_) \
+    hipLaunchKernelGGL((q2_0_gemv_rows_kernel<XT, G_>), dim3(grid), dim3(GEMV_THREADS), 0, \
+                       ctx->stream, c, s, x, y, K, R)
+        if (x_dtype == GD_F16) { if (big) GD_ROWS(0, 8); else GD_ROWS(0, 2); }
+        else { if (big) GD_ROWS(1, 8); else GD_ROWS(1, 2); }
+#undef GD_ROWS
+    } else {
+        const unsigned grid = gd_blocks(R, 16);
+        if (x_dtype == GD_F16)
+            hipLaunchKernelGGL((q2_0_gemv_ksplit_kernel<0, 4>), dim3(grid), dim3(GEMV_THREADS), 0,
+                               ctx->stream, c, s, x, y, K, R);
+        else
+            hipLaunchKernelGGL((q2_0_gemv_ksplit_kernel<1, 4>), dim3(grid), dim3(GEMV_THREADS), 0,
+                               ctx->stream, c, s, x, y, K, R);
+    }
     GD_LAUNCHED(ctx, "q2_0_gemv");
     return GD_OK;
 }

@@ -170,6 +170,31 @@ extern "C" int gd_fill_u32(gd_ctx *ctx, void *dst, uint32_t value, size_t count)
     return GD_OK;
 }
 
+__global__ void gd_cast_kernel(const void *src, int st, void *dst, int dt, size_t n) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (; i < n; i += stride) {
+        const float v = st == GD_F32 ? ((const float *)src)[i] : gd_h2f(((const uint16_t *)src)[i]);
+        if (dt == GD_F32) ((float *)dst)[i] = v;
+        else ((uint16_t *)dst)[i] = gd_f2h(v);
+    }
+}
+
+extern "C" int gd_cast(gd_ctx *ctx, const void *src, int src_dtype, void *dst, int dst_dtype,
+                       size_t n) {
+    GD_CHECK_CTX(ctx);
+    GD_REQUIRE(ctx, (src && dst) || n == 0, "gd_cast: null pointer");
+    GD_REQUIRE(ctx, (src_dtype == GD_F32 || src_dtype == GD_F16) &&
+                        (dst_dtype == GD_F32 || dst_dtype == GD_F16),
+               "gd_cast: bad dtypes %d -> %d", src_dtype, dst_dtype);
+    if (!n) return GD_OK;
+    unsigned blocks = (unsigned)std::min<size_t>((n + 255) / 256, 65536);
+    hipLaunchKernelGGL(gd_cast_kernel, dim3(blocks), dim3(256), 0, ctx->stream, src, src_dtype,
+                       dst, dst_dtype, n);
+    GD_LAUNCHED(ctx, "gd_cast");
+    return GD_OK;
+}
+
 extern "C" int gd_sync(gd_ctx *ctx) {
     GD_CHECK_CTX(ctx);
     GD_HIP(ctx, hipStreamSynchronize(ctx->stream));

@@ -79,6 +79,9 @@ int gd_download(gd_ctx *ctx, void *dst, const void *src, size_t bytes);
  * the call is safe inside stream capture). */
 int gd_copy(gd_ctx *ctx, void *dst, const void *src, size_t bytes);
 int gd_fill_u32(gd_ctx *ctx, void *dst, uint32_t value, size_t count);
+/* dst[i] = src[i] converted between GD_F32 and GD_F16 (RNE), i < n. */
+int gd_cast(gd_ctx *ctx, const void *src, int src_dtype, void *dst, int dst_dtype,
+            size_t n);
 /* Block until every call enqueued on ctx has finished. */
 int gd_sync(gd_ctx *ctx);
 
