@@ -190,6 +190,150 @@ def cpu_baseline_gemv(seconds: float = 10.0) -> dict:
                       f"C restatement of Q2_0.matvec, {threads} threads"}
 
 
+STACK_CFG = dict(n_layer=64, n_embd=5120, n_ff=17408, n_head=40, n_head_kv=8, head_dim=128,
+                 n_rot=64, rope_base=1e7, eps=1e-6, n_vocab=151936, attn_interval=4,
+                 d_state=128, n_k_head=16, n_v_head=16, d_conv=4, kv_block=16, max_ctx=1024,
+                 max_batch=512)
+PP, TG = 512, 128
+
+
+def stack_weight_bytes(c: dict) -> dict:
+    """Q2_0 bytes streamed per decoded token (2.125 bits per weight)."""
+    E, FF, H, HKV, hd = c["n_embd"], c["n_ff"], c["n_head"], c["n_head_kv"], c["head_dim"]
+    kd, vd = c["d_state"] * c["n_k_head"], c["d_state"] * c["n_v_head"]
+    conv = 2 * kd + vd
+    q2 = lambda K, R: K * R * 17 // 64
+    n_att = c["n_layer"] // c["attn_interval"]
+    n_rec = c["n_layer"] - n_att
+    per_rec = q2(E, conv + vd + 2 * c["n_v_head"]) + q2(vd, E)
+    per_att = q2(E, 2 * H * hd + 2 * HKV * hd) + q2(H * hd, E)
+    ffn = q2(E, 2 * FF) + q2(FF, E)
+    trunk = n_rec * per_rec + n_att * per_att + c["n_layer"] * ffn
+    return {"trunk": trunk, "lm_head": q2(E, c["n_vocab"]), "total": trunk + q2(E, c["n_vocab"])}
+
+
+def stack_flops_pp(c: dict, T: int) -> float:
+    """Dense-equivalent FLOPs of the linears for T prefill tokens (2*T*K*R)."""
+    E, FF, H, HKV, hd = c["n_embd"], c["n_ff"], c["n_head"], c["n_head_kv"], c["head_dim"]
+    kd, vd = c["d_state"] * c["n_k_head"], c["d_state"] * c["n_v_head"]
+    conv = 2 * kd + vd
+    n_att = c["n_layer"] // c["attn_interval"]
+    n_rec = c["n_layer"] - n_att
+    lin = n_rec * (E * (conv + vd + 2 * c["n_v_head"]) + vd * E) + \
+        n_att * (E * (2 * H * hd + 2 * HKV * hd) + H * hd * E) + c["n_layer"] * 3 * E * FF
+    return 2.0 * T * lin
+
+
+def run_stack(ctx, ga, args) -> dict:
+    import numpy as np
+    c = dict(STACK_CFG)
+    sc = ga.StackConfig(**c)
+    h = C.c_void_p()
+    log("creating the 64-layer stack (random init on the device) ...")
+    ctx.check(ctx.lib.gd_stack_create(ctx.h, C.byref(sc), 2024, C.byref(h)))
+    lib = ctx.lib
+    ids = np.random.default_rng(512).integers(0, c["n_vocab"], PP).astype(np.int32)
+    gen = np.empty(TG, np.int32)
+    nxt = C.c_int32()
+    ms = C.c_float()
+    try:
+        for _ in range(args.warmup):                 # extend(512) + 8 decodes, then reset
+            ctx.check(lib.gd_stack_reset(h))
+            ctx.check(lib.gd_stack_prefill(h, ids.ctypes.data, PP, C.byref(nxt), None))
+            ctx.check(lib.gd_stack_generate(h, 8, gen.ctypes.data))
+        pp_ms, tg_ms = [], []
+        for i in range(args.steps):
+            ctx.check(lib.gd_stack_reset(h))
+            ctx.gd_timer_start()
+            ctx.check(lib.gd_stack_prefill(h, ids.ctypes.data, PP, C.byref(nxt), None))
+            ctx.gd_timer_stop(C.byref(ms))
+            pp_ms.append(ms.value)
+            ctx.gd_timer_start()
+            ctx.check(lib.gd_stack_generate(h, TG, gen.ctypes.data))
+            ctx.gd_timer_stop(C.byref(ms))
+            tg_ms.append(ms.value)
+            log(f"pass {i}: pp{PP} {pp_ms[-1]:.1f} ms, tg{TG} {tg_ms[-1]:.1f} ms, "
+                f"first tokens {nxt.value} {list(gen[:4])}")
+        cpu = None
+        if args.cpu_seconds > 0:
+            cpu = cpu_baseline_stack(ctx, ga, h, c, args.cpu_seconds)
+    finally:
+        lib.gd_stack_destroy(h)
+    pp = sum(pp_ms) / len(pp_ms)
+    tg = sum(tg_ms) / len(tg_ms)
+    wb = stack_weight_bytes(c)
+    return {"pp_ms": pp, "tg_ms": tg, "pp_tok_s": PP / (pp * 1e-3), "tg_tok_s": TG / (tg * 1e-3),
+            "pp_tflops": stack_flops_pp(c, PP) / (pp * 1e-3) / 1e12,
+            "tg_weight_gbs": wb["total"] / (tg / TG * 1e-3) / 1e9, "weight_bytes": wb,
+            "pp_ms_all": pp_ms, "tg_ms_all": tg_ms, "cpu": cpu}
+
+
+def cpu_baseline_stack(ctx, ga, h, c, seconds: float) -> dict:
+    """The oracle's token-by-token restatement of BonsaiEngine.forward over the
+    same 64-layer weights (downloaded from the device), timed on the host for
+    a bounded number of decoded tokens."""
+    import numpy as np
+    import oracle as O
+    threads = min(16, os.cpu_count() or 1)
+    lib = ctx.lib
+
+    def read(layer, name):
+        w = ga.Q2W()
+        f = C.POINTER(C.c_float)()
+        n = C.c_int64()
+        ctx.check(lib.gd_stack_tensor(h, layer, name.encode(), C.byref(w), C.byref(f), C.byref(n)))
+        if f:
+            return ctx.get(C.cast(f, C.c_void_p).value, n.value, np.float32)
+        nbytes = w.R * (w.K // 128) * 34
+        d = ctx.alloc(nbytes)
+        ctx.gd_q2_0_export(C.byref(w), d)
+        out = ctx.get(d, nbytes, np.uint8)
+        ctx.free(d)
+        return out
+
+    log("cpu baseline: downloading weights for the oracle ...")
+    ref = O.Stack(c, read, stage_f16=False, threads=threads)
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds or n == 0:
+        ref.token(n * 7 + 1)
+        n += 1
+    dt = (time.perf_counter() - t0) / n
+    return {"value": 1.0 / dt, "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"{n} tokens through the 64-layer stack (token-by-token C restatement of "
+                      f"BonsaiEngine.forward, f32, Q2_0.matvec on {threads} threads), "
+                      f"{dt:.2f} s/token; the CPU engine has no batched prefill, so pp and tg "
+                      f"run at this same rate"}
+
+
+def kernel_rooflines(ctx, ga, steps: int) -> dict:
+    """The stack's dominant kernels at their in-stack shapes, timed alone with
+    HIP events on the context stream: the FFN gate|up Q2_0 GEMV of decode
+    (K=5120, R=34816, f16 x) and the same GEMM at T=512 for prefill."""
+    K, R, T = 5120, 34816, 512
+    w = ga.Q2W()
+    ctx.gd_q2w_alloc(K, R, C.byref(w))
+    ctx.gd_rand_q2w(C.byref(w), 77, 0.01, 0.05)
+    dx = ctx.alloc(T * K * 2)
+    ctx.gd_rand_normal(dx, ga.F16, T * K, 78, 0.0, 1.0)
+    dy = ctx.alloc(T * R * 4)
+    t = Timer(ctx)
+    gemv = lambda: ctx.gd_q2_0_gemv(C.byref(w), dx, ga.F16, dy)
+    gemm = lambda: ctx.gd_q2_0_gemm(C.byref(w), T, dx, ga.F16, dy, ga.F32)
+    for _ in range(3):
+        gemv()
+        gemm()
+    gemv_ms = t.ms(gemv, max(steps, 50))
+    gemm_ms = t.ms(gemm, max(steps, 10))
+    ctx.gd_q2w_free(C.byref(w))
+    ctx.free(dx)
+    ctx.free(dy)
+    gemv_bytes = R * K * 17 // 64 + K * 2 + R * 4
+    return {"gemv": {"shape": f"K={K} R={R} x f16", "us": gemv_ms * 1e3, "bytes": gemv_bytes,
+                     "gbs": gemv_bytes / (gemv_ms * 1e-3) / 1e9},
+            "gemm": {"shape": f"T={T} K={K} R={R}", "us": gemm_ms * 1e3,
+                     "tflops": 2 * T * K * R / (gemm_ms * 1e-3) / 1e12}}
+
+
 def run_kernels(ctx, ga, args) -> dict:
     log("copy bandwidth ...")
     copy = copy_bandwidth(ctx)
@@ -211,10 +355,11 @@ def run_kernels(ctx, ga, args) -> dict:
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=("kernels",), default="kernels")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--steps", type=int, default=3,
+                    help="timed passes (stack: one pp512 + tg128 pass each)")
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--workload", choices=("stack", "kernels"), default="stack")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
@@ -223,9 +368,43 @@ def main() -> int:
     import gadeon_amd as ga
     ctx = ga.Context(0)
     try:
-        r = run_kernels(ctx, ga, args)
+        if args.workload == "stack":
+            r = run_stack(ctx, ga, args)
+            r["kernels"] = kernel_rooflines(ctx, ga, 20)
+        else:
+            r = run_kernels(ctx, ga, args)
     finally:
         ctx.close()
+    if args.workload == "stack":
+        g = r["kernels"]["gemv"]
+        out = {
+            "metric": BASELINE_METRIC,
+            "value": round(r["pp_tok_s"], 1),
+            "unit": "tok/s",
+            "n_gpus": 1,
+            "steps": args.steps,
+            "warmup": args.warmup,
+            "ms_per_step": round(r["pp_ms"] + r["tg_ms"], 3),
+            "higher_is_better": True,
+            "scaling": "weak",
+            "vs_baseline": None,
+            "dtype": "f16",
+            "data": "synthetic (random-init weights and a random 512-id prompt, generated on "
+                    "the device / seeded)",
+            "config": {"workload": "config 4: 64-layer Bonsai-27B-shape hybrid stack, Q2_0 "
+                                   "linears, pp512 then tg128 greedy", "pp": PP, "tg": TG},
+            "pp512_tok_s": round(r["pp_tok_s"], 1),
+            "tg128_tok_s": round(r["tg_tok_s"], 1),
+            "gemv_hbm_gbs": round(g["gbs"], 1),
+            "gemv_frac_hbm_peak": round(g["gbs"] / HBM_PEAK_GBS, 4),
+            "roofline": {"bound": "hbm", "achieved": round(g["gbs"], 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(g["gbs"] / HBM_PEAK_GBS, 4),
+                         "traffic": None, "kernel": "q2_0_gemv " + g["shape"]},
+            "cpu_baseline": r["cpu"],
+            "detail": r,
+        }
+        print(json.dumps(out))
+        return 0
     gemv = r["gemv"]
     out = {
         "metric": BASELINE_METRIC,

@@ -80,6 +80,15 @@ _PROTOS = {
     "gd_rand_uniform": (_i, [_vp, _vp, _sz, _u64, _f, _f]),
     "gd_rand_normal": (_i, [_vp, _vp, _i, _sz, _u64, _f, _f]),
     "gd_rand_q2w": (_i, [_vp, _Q2WP, _u64, _f, _f]),
+    "gd_stack_create": (_i, [_vp, C.POINTER(StackConfig), _u64, C.POINTER(_vp)]),
+    "gd_stack_destroy": (None, [_vp]),
+    "gd_stack_reset": (_i, [_vp]),
+    "gd_stack_prefill": (_i, [_vp, _vp, _i, C.POINTER(C.c_int32), _vp]),
+    "gd_stack_decode": (_i, [_vp, C.c_int32, C.POINTER(C.c_int32), _vp]),
+    "gd_stack_request_stop": (_i, [_vp]),
+    "gd_stack_tensor": (_i, [_vp, _i, C.c_char_p, _Q2WP, C.POINTER(_fp), C.POINTER(_i64)]),
+    "gd_stack_position": (_i, [_vp, C.POINTER(_i64)]),
+    "gd_stack_generate": (_i, [_vp, _i, _vp]),
 }
 
 _lib = None

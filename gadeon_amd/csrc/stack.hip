@@ -1,0 +1,714 @@
+// A random-init Bonsai-shape hybrid stack: Gated DeltaNet layers with a gated
+// full-attention layer every `attn_interval`-th, each followed by a SwiGLU FFN,
+// all linears Q2_0.  It is the HIP counterpart of the reference's GPU engine
+// (MetalEngine.extend / decode, LLM/src/Metal/MetalEngine.swift:183-296,
+// 367-451, 657-796) and follows the op order of the CPU oracle
+// BonsaiEngine.forward (LLM/src/SIMD/BonsaiEngine.swift:155-178), GDN.step
+// (GDN.swift:20-120) and Attn.step (Attention.swift:72-139).
+//
+// MI355X layout choices:
+//   * Projections that read the same input are stored as one Q2_0 matrix and
+//     run as one GEMM/GEMV: GDN [qkv | z | beta | alpha], attention
+//     [q|gate | k | v], FFN [gate | up].  Rows of a Q2_0 plane are
+//     contiguous, so each original tensor is a row range of the fused one.
+//   * Activations feeding a Q2_0 GEMM/GEMV are written as f16 by the kernel
+//     that produces them (the reference stages GEMM inputs as half,
+//     Kernels.metal:428); the residual stream and every recurrent state are f32.
+//   * The attention KV cache is f16 in pages of `kv_block` positions reached
+//     through a page table (MetalKVPool.swift); positions are read from device
+//     memory so a decode step can be replayed as a captured HIP graph.
+#include "gd_internal.h"
+
+#include <atomic>
+#include <cmath>
+#include <string>
+#include <vector>
+
+namespace {
+
+constexpr int HD = 128;   // head_dim / d_state handled by the fused kernels
+
+// ------------------------------------------------------------------ kernels
+
+// beta = sigmoid(bPre), g = softplus(aPre + dt) * aNeg, reading the pre-
+// activations out of the fused projection rows (GDN.swift:39-42).
+__global__ void k_gate(const float *proj, int64_t stride, int off_b, int off_a, const float *dt,
+                       const float *aNeg, float *beta, float *g, int nV, int N) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= N * nV) return;
+    const int n = i / nV, h = i % nV;
+    const float *row = proj + (int64_t)n * stride;
+    beta[i] = gd_sigmoid(row[off_b + h]);
+    g[i] = gd_softplus(row[off_a + h] + dt[h]) * aNeg[h];
+}
+
+// Causal depthwise conv (dConv = 4) + silu over N tokens of the strided qkv
+// rows, ring in registers (GDN.swift:44-62).
+__global__ void k_conv4(const float *proj, int64_t stride, float *ring, const float *cw,
+                        float *out, int convDim, int N) {
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= convDim) return;
+    const float w0 = cw[c * 4], w1 = cw[c * 4 + 1], w2 = cw[c * 4 + 2], w3 = cw[c * 4 + 3];
+    float r0 = ring[c], r1 = ring[convDim + c], r2 = ring[2 * convDim + c];
+    for (int n = 0; n < N; n++) {
+        const float cur = proj[(int64_t)n * stride + c];
+        float acc = 0.0f;
+        acc += r0 * w0;
+        acc += r1 * w1;
+        acc += r2 * w2;
+        acc += cur * w3;
+        out[(int64_t)n * convDim + c] = gd_silu(acc);
+        r0 = r1; r1 = r2; r2 = cur;
+    }
+    ring[c] = r0; ring[convDim + c] = r1; ring[2 * convDim + c] = r2;
+}
+
+// o <- rmsnorm_d(o) * w * silu(z), written as f16 for the out projection
+// (GDN.swift:113-115).  One wave per (token, value head).
+__global__ void k_onorm_silu(const float *o, const float *proj, int64_t stride, int off_z,
+                             const float *w, uint16_t *out, int nV, int N, float eps) {
+    const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (row >= N * nV) return;
+    const int lane = threadIdx.x & 63;
+    const int n = row / nV, h = row % nV;
+    const float *r = o + (int64_t)row * HD;
+    const float a = r[lane], b = r[lane + 64];
+    const float ss = gd_wave_sum(a * a + b * b);
+    const float s = 1.0f / sqrtf(ss / (float)HD + eps);
+    const float *z = proj + (int64_t)n * stride + off_z + h * HD;
+    uint16_t *dst = out + (int64_t)row * HD;
+    dst[lane] = gd_f2h(a * s * w[lane] * gd_silu(z[lane]));
+    dst[lane + 64] = gd_f2h(b * s * w[lane + 64] * gd_silu(z[lane + 64]));
+}
+
+// act = silu(gate) * up -> f16 (BonsaiEngine.swift:141-150).
+__global__ void k_swiglu(const float *gu, int FF, uint16_t *out, int N) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t)N * FF) return;
+    const int64_t n = i / FF, j = i % FF;
+    const float *row = gu + n * 2 * FF;
+    out[i] = gd_f2h(gd_silu(row[j]) * row[FF + j]);
+}
+
+// Attention prep, one block of HD threads per (token, head): q heads take
+// the q half of the fused [q | gate] pair, RMS-normalize it with q_norm and
+// rotate it; kv heads normalize + rotate k and append k, v to the f16 cache
+// at the token's position (Attention.swift:79-107).
+__global__ void k_attn_prep(const float *proj, int64_t stride, const float *q_norm,
+                            const float *k_norm, float *q_out, float *gate_out, uint16_t *kc,
+                            uint16_t *vc, const int32_t *page_table, const int32_t *pos_ptr,
+                            int H, int HKV, int n_rot, float base, int block, float eps) {
+    __shared__ float buf[HD];
+    __shared__ float red[2];
+    const int n = blockIdx.x, h = blockIdx.y, i = threadIdx.x;
+    const int pos = *pos_ptr + n;
+    const float *row = proj + (int64_t)n * stride;
+    const bool is_q = h < H;
+    const int kh = h - H;
+    const float x = is_q ? row[h * 2 * HD + i] : row[2 * H * HD + kh * HD + i];
+    // RMS norm over the head (Kern.rmsnormRows, Kernels.swift:26-37).
+    float ss = gd_wave_sum(x * x);
+    if ((i & 63) == 0) red[i >> 6] = ss;
+    __syncthreads();
+    ss = red[0] + red[1];
+    const float s = 1.0f / sqrtf(ss / (float)HD + eps);
+    float y = x * s * (is_q ? q_norm[i] : k_norm[i]);
+    buf[i] = y;
+    __syncthreads();
+    // Partial NEOX rope on the first n_rot dims (Kern.ropeNeox, Kernels.swift:66-84).
+    const int half = n_rot / 2;
+    if (i < n_rot) {
+        const int j = i < half ? i : i - half;
+        const float freq = powf(base, -2.0f * (float)j / (float)n_rot);
+        const float ang = (float)pos * freq;
+        const float c = cosf(ang), sn = sinf(ang);
+        y = i < half ? buf[i] * c - buf[i + half] * sn : buf[i - half] * sn + buf[i] * c;
+    }
+    if (is_q) {
+        q_out[((int64_t)n * H + h) * HD + i] = y;
+        gate_out[((int64_t)n * H + h) * HD + i] = row[h * 2 * HD + HD + i];
+    } else {
+        const int kvDim = HKV * HD;
+        const int64_t slot = (int64_t)page_table[pos / block] * block + pos % block;
+        kc[slot * kvDim + kh * HD + i] = gd_f2h(y);
+        vc[slot * kvDim + kh * HD + i] = gd_f2h(row[2 * H * HD + HKV * HD + kh * HD + i]);
+    }
+}
+
+__device__ __forceinline__ int64_t kv_slot(const int32_t *pt, int pos, int block) {
+    return (int64_t)pt[pos / block] * block + pos % block;
+}
+
+// Causal prefill attention with the sigmoid output gate, online softmax.
+// Block (head h, 32 queries): 8 threads per query, each owning 16 of the 128
+// dims; keys stream through LDS in tiles of 32 (Attention.swift:108-134).
+constexpr int AQ = 32, AK = 32;
+__global__ __launch_bounds__(256) void k_attn_prefill(
+        const float *q, const float *gate, const uint16_t *kc, const uint16_t *vc,
+        const int32_t *page_table, const int32_t *pos_ptr, uint16_t *out, int H, int HKV,
+        int N, int block, float scale) {
+    __shared__ float Ks[AK][HD + 4];
+    __shared__ float Vs[AK][HD + 4];
+    const int h = blockIdx.x, q0 = blockIdx.y * AQ;
+    const int t = threadIdx.x, qi = t >> 3, sub = t & 7;
+    const int kvh = h / (H / HKV);
+    const int kvDim = HKV * HD;
+    const int pos0 = *pos_ptr;
+    const int n = q0 + qi;
+    const bool valid = n < N;
+    const int my_pos = pos0 + (valid ? n : N - 1);
+    float qv[16], acc[16];
+    const float *qrow = q + ((int64_t)(valid ? n : N - 1) * H + h) * HD + sub * 16;
+#pragma unroll
+    for (int d = 0; d < 16; d++) { qv[d] = qrow[d] * scale; acc[d] = 0.f; }
+    float m = -INFINITY, l = 0.f;
+    const int last = pos0 + min(q0 + AQ, N) - 1;       // last key any query here needs
+    for (int k0 = 0; k0 <= last; k0 += AK) {
+        __syncthreads();
+        for (int e = t; e < AK * HD; e += 256) {
+            const int kk = e / HD, d = e % HD;
+            const int p = min(k0 + kk, last);
+            const int64_t base = kv_slot(page_table, p, block) * kvDim + kvh * HD + d;
+            Ks[kk][d] = gd_h2f(kc[base]);
+            Vs[kk][d] = gd_h2f(vc[base]);
+        }
+        __syncthreads();
+        const int kend = min(AK, my_pos - k0 + 1);     // causal: keys <= my position
+        for (int kk = 0; kk < kend; kk++) {
+            float s = 0.f;
+#pragma unroll
+            for (int d = 0; d < 16; d++) s = fmaf(qv[d], Ks[kk][sub * 16 + d], s);
+            s += __shfl_xor(s, 1, 64);
+            s += __shfl_xor(s, 2, 64);
+            s += __shfl_xor(s, 4, 64);
+            const float mn = fmaxf(m, s);
+            const float alpha = expf(m - mn), p = expf(s - mn);
+            l = l * alpha + p;
+#pragma unroll
+            for (int d = 0; d < 16; d++) acc[d] = fmaf(p, Vs[kk][sub * 16 + d], acc[d] * alpha);
+            m = mn;
+        }
+    }
+    if (valid) {
+        const float inv = 1.0f / l;
+        const float *grow = gate + ((int64_t)n * H + h) * HD + sub * 16;
+        uint16_t *orow = out + ((int64_t)n * H + h) * HD + sub * 16;
+#pragma unroll
+        for (int d = 0; d < 16; d++) orow[d] = gd_f2h(acc[d] * inv * gd_sigmoid(grow[d]));
+    }
+}
+
+// Decode attention, one block per head: the 256 threads split the keys for
+// the scores, then split (dims x key halves) for P.V.
+__global__ __launch_bounds__(256) void k_attn_decode(
+        const float *q, const float *gate, const uint16_t *kc, const uint16_t *vc,
+        const int32_t *page_table, const int32_t *pos_ptr, uint16_t *out, int H, int HKV,
+        int block, float scale, float *scores, int max_ctx) {
+    __shared__ float qs[HD];
+    __shared__ float red[8];
+    __shared__ float part[2][HD];
+    const int h = blockIdx.x, t = threadIdx.x;
+    const int kvh = h / (H / HKV), kvDim = HKV * HD;
+    const int T = *pos_ptr + 1;
+    float *sc = scores + (int64_t)h * max_ctx;
+    if (t < HD) qs[t] = q[(int64_t)h * HD + t] * scale;
+    __syncthreads();
+    float mx = -INFINITY;
+    for (int j = t; j < T; j += 256) {
+        const uint16_t *kr = kc + kv_slot(page_table, j, block) * kvDim + kvh * HD;
+        float s = 0.f;
+        for (int d = 0; d < HD; d += 8) {
+            const u32x4 w = *(const u32x4 *)(kr + d);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                s = fmaf(qs[d + 2 * e], gd_h2f((uint16_t)(w[e] & 0xffff)), s);
+                s = fmaf(qs[d + 2 * e + 1], gd_h2f((uint16_t)(w[e] >> 16)), s);
+            }
+        }
+        sc[j] = s;
+        mx = fmaxf(mx, s);
+    }
+    // block max
+    for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    if ((t & 63) == 0) red[t >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    float sum = 0.f;
+    for (int j = t; j < T; j += 256) {
+        const float p = expf(sc[j] - mx);
+        sc[j] = p;
+        sum += p;
+    }
+    sum = gd_block_sum(sum, red);
+    __threadfence_block();
+    __syncthreads();
+    // P.V: thread (d = t % 128, half = t / 128) sums keys of its parity.
+    const int d = t & (HD - 1), hf = t >> 7;
+    float acc = 0.f;
+    for (int j = hf; j < T; j += 2)
+        acc = fmaf(sc[j], gd_h2f(vc[kv_slot(page_table, j, block) * kvDim + kvh * HD + d]), acc);
+    part[hf][d] = acc;
+    __syncthreads();
+    if (t < HD) {
+        const float o = (part[0][t] + part[1][t]) / sum;
+        out[(int64_t)h * HD + t] = gd_f2h(o * gd_sigmoid(gate[(int64_t)h * HD + t]));
+    }
+}
+
+// Greedy pick: index of the first maximum (BonsaiEngine.argmax, :187-191).
+__global__ __launch_bounds__(1024) void k_argmax(const float *v, int n, int32_t *out) {
+    __shared__ float bv[16];
+    __shared__ int bi[16];
+    float best = -INFINITY;
+    int idx = 0x7fffffff;
+    for (int i = threadIdx.x; i < n; i += 1024) {
+        const float x = v[i];
+        if (x > best) { best = x; idx = i; }
+    }
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float ob = __shfl_xor(best, o, 64);
+        const int oi = __shfl_xor(idx, o, 64);
+        if (ob > best || (ob == best && oi < idx)) { best = ob; idx = oi; }
+    }
+    if ((threadIdx.x & 63) == 0) { bv[threadIdx.x >> 6] = best; bi[threadIdx.x >> 6] = idx; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 16; w++)
+            if (bv[w] > best || (bv[w] == best && bi[w] < idx)) { best = bv[w]; idx = bi[w]; }
+        *out = idx;
+    }
+}
+
+__global__ void k_add_pos(int32_t *pos, int n) { *pos += n; }
+
+__global__ void k_iota(int32_t *p, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = i;
+}
+
+}  // namespace
+
+// --------------------------------------------------------------- host side
+
+struct StackLayer {
+    bool rec = false;
+    float *attn_norm = nullptr, *post_norm = nullptr;
+    gd_q2w in_proj{}, out_proj{}, gate_up{}, down{};
+    // GDN
+    float *conv_w = nullptr, *dt = nullptr, *a_neg = nullptr, *ssm_norm = nullptr;
+    float *conv_state = nullptr, *rec_state = nullptr;
+    // attention
+    float *q_norm = nullptr, *k_norm = nullptr;
+    uint16_t *kc = nullptr, *vc = nullptr;
+};
+
+struct gd_stack {
+    gd_ctx *ctx = nullptr;
+    gd_stack_config c{};
+    int keyDim = 0, valDim = 0, convDim = 0, rp_rec = 0, rp_att = 0, max_pages = 0;
+    std::vector<StackLayer> L;
+    gd_q2w embd{};
+    float *out_norm = nullptr;
+    int32_t *page_table = nullptr;
+    // scratch
+    float *x = nullptr, *proj = nullptr, *conv_out = nullptr, *o32 = nullptr, *contrib = nullptr;
+    float *beta = nullptr, *g = nullptr, *q32 = nullptr, *gate32 = nullptr, *logits = nullptr;
+    float *scores = nullptr;
+    uint16_t *xn16 = nullptr, *a16 = nullptr;
+    int32_t *ids = nullptr, *dpos = nullptr, *dtok = nullptr;
+    int64_t pos = 0;
+    std::atomic<bool> stop{false};
+    std::vector<void *> allocs;
+    hipGraphExec_t decode_exec = nullptr;
+    hipGraph_t decode_graph = nullptr;
+};
+
+namespace {
+
+int salloc(gd_stack *st, size_t bytes, void **p) {
+    int rc = gd_alloc(st->ctx, bytes, p);
+    if (rc == GD_OK) st->allocs.push_back(*p);
+    return rc;
+}
+
+template <typename T>
+int salloc_t(gd_stack *st, size_t count, T **p) {
+    void *v = nullptr;
+    int rc = salloc(st, count * sizeof(T), &v);
+    *p = (T *)v;
+    return rc;
+}
+
+int q2w_make(gd_stack *st, int64_t K, int64_t R, uint64_t seed, gd_q2w *w) {
+    int rc = gd_q2w_alloc(st->ctx, K, R, w);
+    if (rc) return rc;
+    st->allocs.push_back(w->codes);
+    st->allocs.push_back(w->scales);
+    return gd_rand_q2w(st->ctx, w, seed, 0.01f, 0.05f);
+}
+
+int f32_make(gd_stack *st, int64_t n, uint64_t seed, float lo, float hi, float **p) {
+    int rc = salloc_t(st, (size_t)n, p);
+    if (rc) return rc;
+    return gd_rand_uniform(st->ctx, *p, (size_t)n, seed, lo, hi);
+}
+
+gd_q2w rows_of(const gd_q2w &w, int64_t r0, int64_t r1) {
+    gd_q2w s;
+    s.codes = (uint8_t *)w.codes + r0 * (w.K / 4);
+    s.scales = (uint16_t *)w.scales + r0 * (w.K / 128);
+    s.K = w.K;
+    s.R = r1 - r0;
+    return s;
+}
+
+// One chunk of N tokens whose embeddings are already in st->x (f32 [N][E]):
+// the layer stack, the final norm and the last token's logits + greedy pick.
+// Positions come from st->dpos.  `decode` selects the single-token kernels.
+int forward(gd_stack *st, int N, bool decode) {
+    gd_ctx *ctx = st->ctx;
+    const gd_stack_config &c = st->c;
+    const int E = c.n_embd, FF = c.n_ff, H = c.n_head, HKV = c.n_head_kv;
+    const int nV = c.n_v_head, nK = c.n_k_head;
+    const float eps = c.eps, qScale = 1.0f / sqrtf((float)c.d_state);
+    hipStream_t s = ctx->stream;
+    int rc;
+#define R_(call) do { if ((rc = (call)) != GD_OK) return rc; } while (0)
+    for (int il = 0; il < c.n_layer; il++) {
+        StackLayer &ly = st->L[il];
+        R_(gd_rmsnorm(ctx, st->x, ly.attn_norm, st->xn16, GD_F16, E, N, eps));
+        const int RP = ly.rec ? st->rp_rec : st->rp_att;
+        if (decode) R_(gd_q2_0_gemv(ctx, &ly.in_proj, st->xn16, GD_F16, st->proj));
+        else R_(gd_q2_0_gemm(ctx, &ly.in_proj, N, st->xn16, GD_F16, st->proj, GD_F32));
+        if (ly.rec) {
+            const int off_z = st->convDim, off_b = off_z + st->valDim, off_a = off_b + nV;
+            hipLaunchKernelGGL(k_conv4, dim3(gd_blocks(st->convDim, 256)), dim3(256), 0, s,
+                               st->proj, (int64_t)RP, ly.conv_state, ly.conv_w, st->conv_out,
+                               st->convDim, N);
+            GD_LAUNCHED(ctx, "k_conv4");
+            if (decode) {
+                // Fused gate + L2 norm + delta-rule step, state in place.
+                R_(gd_gdn_decode(ctx, 1, nV, nK, c.d_state, st->conv_out,
+                                 st->conv_out + st->keyDim, st->conv_out + 2 * st->keyDim,
+                                 GD_F32, st->proj + off_a, st->proj + off_b, ly.dt, ly.a_neg,
+                                 ly.rec_state, st->o32, qScale, eps));
+            } else {
+                hipLaunchKernelGGL(k_gate, dim3(gd_blocks((int64_t)N * nV, 256)), dim3(256), 0, s,
+                                   st->proj, (int64_t)RP, off_b, off_a, ly.dt, ly.a_neg, st->beta,
+                                   st->g, nV, N);
+                GD_LAUNCHED(ctx, "k_gate");
+                R_(gd_l2norm_rows(ctx, st->conv_out, c.d_state, 2 * nK, st->convDim, N, eps));
+                R_(gd_gdn_prefill(ctx, N, nV, nK, c.d_state, c.d_state, st->conv_out,
+                                  st->convDim, st->conv_out + st->keyDim, st->convDim,
+                                  st->conv_out + 2 * st->keyDim, st->convDim, GD_F32, st->g,
+                                  st->beta, ly.rec_state, st->o32, st->valDim, GD_F32, qScale,
+                                  64));
+            }
+            hipLaunchKernelGGL(k_onorm_silu, dim3(gd_blocks((int64_t)N * nV, 4)), dim3(256), 0, s,
+                               st->o32, st->proj, (int64_t)RP, off_z, ly.ssm_norm, st->a16, nV, N,
+                               eps);
+            GD_LAUNCHED(ctx, "k_onorm_silu");
+        } else {
+            hipLaunchKernelGGL(k_attn_prep, dim3(N, H + HKV), dim3(HD), 0, s, st->proj,
+                               (int64_t)RP, ly.q_norm, ly.k_norm, st->q32, st->gate32, ly.kc,
+                               ly.vc, st->page_table, st->dpos, H, HKV, c.n_rot, c.rope_base,
+                               c.kv_block, eps);
+            GD_LAUNCHED(ctx, "k_attn_prep");
+            const float scale = 1.0f / sqrtf((float)HD);
+            if (decode)
+                hipLaunchKernelGGL(k_attn_decode, dim3(H), dim3(256), 0, s, st->q32, st->gate32,
+                                   ly.kc, ly.vc, st->page_table, st->dpos, st->a16, H, HKV,
+                                   c.kv_block, scale, st->scores, c.max_ctx);
+            else
+                hipLaunchKernelGGL(k_attn_prefill, dim3(H, gd_blocks(N, AQ)), dim3(256), 0, s,
+                                   st->q32, st->gate32, ly.kc, ly.vc, st->page_table, st->dpos,
+                                   st->a16, H, HKV, N, c.kv_block, scale);
+            GD_LAUNCHED(ctx, "k_attn");
+        }
+        if (decode) R_(gd_q2_0_gemv(ctx, &ly.out_proj, st->a16, GD_F16, st->contrib));
+        else R_(gd_q2_0_gemm(ctx, &ly.out_proj, N, st->a16, GD_F16, st->contrib, GD_F32));
+        R_(gd_add(ctx, st->x, st->contrib, (int64_t)N * E));
+        R_(gd_rmsnorm(ctx, st->x, ly.post_norm, st->xn16, GD_F16, E, N, eps));
+        if (decode) R_(gd_q2_0_gemv(ctx, &ly.gate_up, st->xn16, GD_F16, st->proj));
+        else R_(gd_q2_0_gemm(ctx, &ly.gate_up, N, st->xn16, GD_F16, st->proj, GD_F32));
+        hipLaunchKernelGGL(k_swiglu, dim3(gd_blocks((int64_t)N * FF, 256)), dim3(256), 0, s,
+                           st->proj, FF, st->a16, N);
+        GD_LAUNCHED(ctx, "k_swiglu");
+        if (decode) R_(gd_q2_0_gemv(ctx, &ly.down, st->a16, GD_F16, st->contrib));
+        else R_(gd_q2_0_gemm(ctx, &ly.down, N, st->a16, GD_F16, st->contrib, GD_F32));
+        R_(gd_add(ctx, st->x, st->contrib, (int64_t)N * E));
+    }
+    // Final norm of the last token, tied lm_head, greedy pick.
+    R_(gd_rmsnorm(ctx, st->x + (int64_t)(N - 1) * E, st->out_norm, st->xn16, GD_F16, E, 1, eps));
+    R_(gd_q2_0_gemv(ctx, &st->embd, st->xn16, GD_F16, st->logits));
+    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, s, st->logits, c.n_vocab, st->dtok);
+    GD_LAUNCHED(ctx, "k_argmax");
+    hipLaunchKernelGGL(k_add_pos, dim3(1), dim3(1), 0, s, st->dpos, N);
+    GD_LAUNCHED(ctx, "k_add_pos");
+#undef R_
+    return GD_OK;
+}
+
+int finish(gd_stack *st, int32_t *next, float *logits) {
+    gd_ctx *ctx = st->ctx;
+    int rc;
+    if (logits && (rc = gd_download(ctx, logits, st->logits, (size_t)st->c.n_vocab * 4))) return rc;
+    if (next && (rc = gd_download(ctx, next, st->dtok, 4))) return rc;
+    return GD_OK;
+}
+
+}  // namespace
+
+extern "C" void gd_stack_destroy(gd_stack *st) {
+    if (!st) return;
+    if (st->decode_exec) (void)hipGraphExecDestroy(st->decode_exec);
+    if (st->decode_graph) (void)hipGraphDestroy(st->decode_graph);
+    for (void *p : st->allocs) gd_free(st->ctx, p);
+    delete st;
+}
+
+extern "C" int gd_stack_create(gd_ctx *ctx, const gd_stack_config *cfg, uint64_t seed,
+                               gd_stack **out) {
+    GD_CHECK_CTX(ctx);
+    GD_REQUIRE(ctx, cfg && out, "gd_stack_create: null argument");
+    const gd_stack_config &c = *cfg;
+    GD_REQUIRE(ctx, c.n_layer > 0 && c.attn_interval > 0, "gd_stack_create: bad layer count");
+    GD_REQUIRE(ctx, c.head_dim == HD && c.d_state == HD,
+               "gd_stack_create: head_dim and d_state must be 128");
+    GD_REQUIRE(ctx, c.d_conv == 4, "gd_stack_create: d_conv must be 4");
+    GD_REQUIRE(ctx, c.n_head > 0 && c.n_head_kv > 0 && c.n_head % c.n_head_kv == 0,
+               "gd_stack_create: n_head must be a multiple of n_head_kv");
+    GD_REQUIRE(ctx, c.n_k_head > 0 && c.n_v_head % c.n_k_head == 0,
+               "gd_stack_create: n_v_head must be a multiple of n_k_head");
+    GD_REQUIRE(ctx, c.n_rot > 0 && c.n_rot <= HD && c.n_rot % 2 == 0, "gd_stack_create: n_rot");
+    GD_REQUIRE(ctx, c.n_embd % 128 == 0 && c.n_ff % 128 == 0 && c.n_vocab > 0,
+               "gd_stack_create: n_embd and n_ff must be multiples of 128");
+    GD_REQUIRE(ctx, c.kv_block > 0 && c.max_ctx > 0 && c.max_batch > 0,
+               "gd_stack_create: kv_block, max_ctx, max_batch must be positive");
+    *out = nullptr;
+    gd_stack *st = new gd_stack();
+    st->ctx = ctx;
+    st->c = c;
+    st->keyDim = HD * c.n_k_head;
+    st->valDim = HD * c.n_v_head;
+    st->convDim = 2 * st->keyDim + st->valDim;
+    st->rp_rec = st->convDim + st->valDim + 2 * c.n_v_head;
+    st->rp_att = 2 * c.n_head * HD + 2 * c.n_head_kv * HD;
+    st->max_pages = (c.max_ctx + c.kv_block - 1) / c.kv_block;
+    const int E = c.n_embd, FF = c.n_ff, B = c.max_batch;
+    int rc = GD_OK;
+#define C_(call) do { if ((rc = (call)) != GD_OK) { gd_stack_destroy(st); return rc; } } while (0)
+    uint64_t sd = seed * 1000003ULL;
+    auto next_seed = [&]() { sd += 2; return sd; };   // streams use seed and seed+1
+    st->L.resize(c.n_layer);
+    for (int il = 0; il < c.n_layer; il++) {
+        StackLayer &ly = st->L[il];
+        ly.rec = (il + 1) % c.attn_interval != 0;     // Model.swift:37
+        C_(f32_make(st, E, next_seed(), 0.8f, 1.2f, &ly.attn_norm));
+        C_(f32_make(st, E, next_seed(), 0.8f, 1.2f, &ly.post_norm));
+        if (ly.rec) {
+            C_(q2w_make(st, E, st->rp_rec, next_seed(), &ly.in_proj));
+            C_(q2w_make(st, st->valDim, E, next_seed(), &ly.out_proj));
+            C_(f32_make(st, (int64_t)st->convDim * 4, next_seed(), -0.5f, 0.5f, &ly.conv_w));
+            C_(f32_make(st, c.n_v_head, next_seed(), -0.5f, 0.5f, &ly.dt));
+            C_(f32_make(st, c.n_v_head, next_seed(), -2.0f, -0.3f, &ly.a_neg));
+            C_(f32_make(st, HD, next_seed(), 0.8f, 1.2f, &ly.ssm_norm));
+            C_(salloc_t(st, (size_t)3 * st->convDim, &ly.conv_state));
+            C_(salloc_t(st, (size_t)c.n_v_head * HD * HD, &ly.rec_state));
+        } else {
+            C_(q2w_make(st, E, st->rp_att, next_seed(), &ly.in_proj));
+            C_(q2w_make(st, (int64_t)c.n_head * HD, E, next_seed(), &ly.out_proj));
+            C_(f32_make(st, HD, next_seed(), 0.8f, 1.2f, &ly.q_norm));
+            C_(f32_make(st, HD, next_seed(), 0.8f, 1.2f, &ly.k_norm));
+            const size_t kv = (size_t)st->max_pages * c.kv_block * c.n_head_kv * HD;
+            C_(salloc_t(st, kv, &ly.kc));
+            C_(salloc_t(st, kv, &ly.vc));
+        }
+        C_(q2w_make(st, E, 2 * (int64_t)FF, next_seed(), &ly.gate_up));
+        C_(q2w_make(st, FF, E, next_seed(), &ly.down));
+    }
+    C_(q2w_make(st, E, c.n_vocab, next_seed(), &st->embd));
+    C_(f32_make(st, E, next_seed(), 0.8f, 1.2f, &st->out_norm));
+    C_(salloc_t(st, (size_t)st->max_pages, &st->page_table));
+    hipLaunchKernelGGL(k_iota, dim3(gd_blocks(st->max_pages, 256)), dim3(256), 0, ctx->stream,
+                       st->page_table, st->max_pages);
+    const int maxproj = std::max(std::max(st->rp_rec, st->rp_att), 2 * FF);
+    C_(salloc_t(st, (size_t)B * E, &st->x));
+    C_(salloc_t(st, (size_t)B * maxproj, &st->proj));
+    C_(salloc_t(st, (size_t)B * st->convDim, &st->conv_out));
+    C_(salloc_t(st, (size_t)B * st->valDim, &st->o32));
+    C_(salloc_t(st, (size_t)B * E, &st->contrib));
+    C_(salloc_t(st, (size_t)B * c.n_v_head, &st->beta));
+    C_(salloc_t(st, (size_t)B * c.n_v_head, &st->g));
+    C_(salloc_t(st, (size_t)B * c.n_head * HD, &st->q32));
+    C_(salloc_t(st, (size_t)B * c.n_head * HD, &st->gate32));
+    C_(salloc_t(st, (size_t)c.n_vocab, &st->logits));
+    C_(salloc_t(st, (size_t)c.n_head * c.max_ctx, &st->scores));
+    C_(salloc_t(st, (size_t)B * E, &st->xn16));
+    const int a16n = std::max(std::max(st->valDim, c.n_head * HD), FF);
+    C_(salloc_t(st, (size_t)B * a16n, &st->a16));
+    C_(salloc_t(st, (size_t)B, &st->ids));
+    C_(salloc_t(st, 1, &st->dpos));
+    C_(salloc_t(st, 1, &st->dtok));
+    C_(gd_stack_reset(st));
+#undef C_
+    *out = st;
+    return GD_OK;
+}
+
+extern "C" int gd_stack_reset(gd_stack *st) {
+    if (!st) return GD_EINVAL;
+    gd_ctx *ctx = st->ctx;
+    int rc;
+    for (StackLayer &ly : st->L) {
+        if (ly.rec) {
+            if ((rc = gd_fill_u32(ctx, ly.conv_state, 0, (size_t)3 * st->convDim)) ||
+                (rc = gd_fill_u32(ctx, ly.rec_state, 0, (size_t)st->c.n_v_head * HD * HD)))
+                return rc;
+        }
+    }
+    if ((rc = gd_fill_u32(ctx, st->dpos, 0, 1)) || (rc = gd_fill_u32(ctx, st->dtok, 0, 1)))
+        return rc;
+    st->pos = 0;
+    st->stop.store(false);
+    return gd_sync(ctx);
+}
+
+extern "C" int gd_stack_request_stop(gd_stack *st) {
+    if (!st) return GD_EINVAL;
+    st->stop.store(true);
+    return GD_OK;
+}
+
+extern "C" int gd_stack_prefill(gd_stack *st, const int32_t *ids, int n, int32_t *next,
+                                float *logits) {
+    if (!st) return GD_EINVAL;
+    gd_ctx *ctx = st->ctx;
+    GD_REQUIRE(ctx, ids && n > 0, "gd_stack_prefill: no tokens");
+    GD_REQUIRE(ctx, st->pos + n <= st->c.max_ctx, "gd_stack_prefill: context %lld + %d > max_ctx %d",
+               (long long)st->pos, n, st->c.max_ctx);
+    for (int i = 0; i < n; i++)
+        GD_REQUIRE(ctx, ids[i] >= 0 && ids[i] < st->c.n_vocab, "gd_stack_prefill: id %d out of vocab",
+                   ids[i]);
+    int rc;
+    for (int i = 0; i < n; i += st->c.max_batch) {
+        if (st->stop.exchange(false)) return gd_fail(ctx, GD_ESTOPPED, "prefill stopped");
+        const int N = std::min(st->c.max_batch, n - i);
+        if ((rc = gd_upload(ctx, st->ids, ids + i, (size_t)N * 4)) ||
+            (rc = gd_q2_0_dequant_rows(ctx, &st->embd, st->ids, N, st->x)) ||
+            (rc = forward(st, N, false)))
+            return rc;
+        st->pos += N;
+    }
+    return finish(st, next, logits);
+}
+
+extern "C" int gd_stack_decode(gd_stack *st, int32_t token, int32_t *next, float *logits) {
+    if (!st) return GD_EINVAL;
+    gd_ctx *ctx = st->ctx;
+    GD_REQUIRE(ctx, token >= 0 && token < st->c.n_vocab, "gd_stack_decode: token %d out of vocab",
+               token);
+    GD_REQUIRE(ctx, st->pos + 1 <= st->c.max_ctx, "gd_stack_decode: context full");
+    int rc;
+    if ((rc = gd_upload(ctx, st->dtok, &token, 4))) return rc;
+    if ((rc = gd_q2_0_dequant_rows(ctx, &st->embd, st->dtok, 1, st->x)) ||
+        (rc = forward(st, 1, true)))
+        return rc;
+    st->pos += 1;
+    return finish(st, next, logits);
+}
+
+extern "C" int gd_stack_generate(gd_stack *st, int n, int32_t *tokens) {
+    if (!st) return GD_EINVAL;
+    gd_ctx *ctx = st->ctx;
+    GD_REQUIRE(ctx, n >= 0 && tokens, "gd_stack_generate: bad arguments");
+    GD_REQUIRE(ctx, st->pos + n <= st->c.max_ctx, "gd_stack_generate: context full");
+    if (n == 0) return GD_OK;
+    int rc;
+    // One decode step reads the previous pick from st->dtok, so the whole step
+    // (embed .. argmax, position bump) replays with no host involvement.
+    if (!st->decode_exec) {
+        GD_HIP(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+        rc = gd_q2_0_dequant_rows(ctx, &st->embd, st->dtok, 1, st->x);
+        if (rc == GD_OK) rc = forward(st, 1, true);
+        hipGraph_t graph = nullptr;
+        hipError_t e = hipStreamEndCapture(ctx->stream, &graph);
+        if (rc != GD_OK) {
+            if (graph) (void)hipGraphDestroy(graph);
+            return rc;
+        }
+        if (e != hipSuccess) return gd_hip_fail(ctx, e, "decode graph capture");
+        st->decode_graph = graph;
+        GD_HIP(ctx, hipGraphInstantiate(&st->decode_exec, graph, nullptr, nullptr, 0));
+    }
+    // Each step's pick is copied into a device ring so nothing syncs per token.
+    int32_t *ring = nullptr;
+    if ((rc = gd_alloc(ctx, (size_t)n * 4, (void **)&ring))) return rc;
+    for (int i = 0; i < n; i++) {
+        hipError_t e = hipGraphLaunch(st->decode_exec, ctx->stream);
+        if (e != hipSuccess) { gd_free(ctx, ring); return gd_hip_fail(ctx, e, "decode graph launch"); }
+        e = hipMemcpyAsync(ring + i, st->dtok, 4, hipMemcpyDeviceToDevice, ctx->stream);
+        if (e != hipSuccess) { gd_free(ctx, ring); return gd_hip_fail(ctx, e, "token copy"); }
+    }
+    rc = gd_download(ctx, tokens, ring, (size_t)n * 4);
+    gd_free(ctx, ring);
+    if (rc) return rc;
+    st->pos += n;
+    return GD_OK;
+}
+
+extern "C" int gd_stack_position(gd_stack *st, int64_t *pos) {
+    if (!st || !pos) return GD_EINVAL;
+    *pos = st->pos;
+    return GD_OK;
+}
+
+extern "C" int gd_stack_tensor(gd_stack *st, int layer, const char *name, gd_q2w *w, float **f32,
+                               int64_t *count) {
+    if (!st || !name) return GD_EINVAL;
+    gd_ctx *ctx = st->ctx;
+    const std::string n(name);
+    const gd_stack_config &c = st->c;
+    auto q = [&](const gd_q2w &m) { if (w) *w = m; return GD_OK; };
+    auto f = [&](float *p, int64_t cnt) {
+        if (f32) *f32 = p;
+        if (count) *count = cnt;
+        return GD_OK;
+    };
+    if (layer < 0) {
+        if (n == "token_embd") return q(st->embd);
+        if (n == "output_norm") return f(st->out_norm, c.n_embd);
+        return gd_fail(ctx, GD_EINVAL, "gd_stack_tensor: no global tensor '%s'", name);
+    }
+    GD_REQUIRE(ctx, layer < c.n_layer, "gd_stack_tensor: layer %d out of range", layer);
+    StackLayer &ly = st->L[layer];
+    if (n == "attn_norm") return f(ly.attn_norm, c.n_embd);
+    if (n == "post_attention_norm") return f(ly.post_norm, c.n_embd);
+    if (n == "ffn_gate") return q(rows_of(ly.gate_up, 0, c.n_ff));
+    if (n == "ffn_up") return q(rows_of(ly.gate_up, c.n_ff, 2 * (int64_t)c.n_ff));
+    if (n == "ffn_down") return q(ly.down);
+    if (ly.rec) {
+        const int cd = st->convDim, vd = st->valDim, nv = c.n_v_head;
+        if (n == "attn_qkv") return q(rows_of(ly.in_proj, 0, cd));
+        if (n == "attn_gate") return q(rows_of(ly.in_proj, cd, cd + vd));
+        if (n == "ssm_beta") return q(rows_of(ly.in_proj, cd + vd, cd + vd + nv));
+        if (n == "ssm_alpha") return q(rows_of(ly.in_proj, cd + vd + nv, cd + vd + 2 * nv));
+        if (n == "ssm_out") return q(ly.out_proj);
+        if (n == "ssm_conv1d") return f(ly.conv_w, (int64_t)cd * 4);
+        if (n == "ssm_dt") return f(ly.dt, nv);
+        if (n == "ssm_a") return f(ly.a_neg, nv);
+        if (n == "ssm_norm") return f(ly.ssm_norm, HD);
+        if (n == "ssm_conv_state") return f(ly.conv_state, (int64_t)3 * cd);
+        if (n == "ssm_state") return f(ly.rec_state, (int64_t)nv * HD * HD);
+    } else {
+        const int qf = 2 * c.n_head * HD, kv = c.n_head_kv * HD;
+        if (n == "attn_q") return q(rows_of(ly.in_proj, 0, qf));
+        if (n == "attn_k") return q(rows_of(ly.in_proj, qf, qf + kv));
+        if (n == "attn_v") return q(rows_of(ly.in_proj, qf + kv, qf + 2 * kv));
+        if (n == "attn_output") return q(ly.out_proj);
+        if (n == "attn_q_norm") return f(ly.q_norm, HD);
+        if (n == "attn_k_norm") return f(ly.k_norm, HD);
+    }
+    return gd_fail(ctx, GD_EINVAL, "gd_stack_tensor: layer %d has no tensor '%s'", layer, name);
+}

@@ -265,6 +265,67 @@ int gd_rand_normal(gd_ctx *ctx, void *out, int dtype, size_t n, uint64_t seed,
  * `seed`), scales RNE-f16 of lo + (hi-lo)*u over stream seed+1. */
 int gd_rand_q2w(gd_ctx *ctx, gd_q2w *w, uint64_t seed, float lo, float hi);
 
+/* ---- Bonsai-shape hybrid stack (config 4) --------------------------------------
+ * A random-init 64-layer GDN/attention hybrid driven exactly like
+ * MetalEngine.extend / decode (MetalEngine.swift:183-257, 657-728) and the
+ * CPU oracle BonsaiEngine.forward (BonsaiEngine.swift:155-178). */
+typedef struct gd_stack_config {
+    int n_layer;        /* 64 */
+    int n_embd;         /* 5120 */
+    int n_ff;           /* 17408 */
+    int n_head;         /* 40 (attention q heads) */
+    int n_head_kv;      /* 8 */
+    int head_dim;       /* 128 */
+    int n_rot;          /* 64 (partial NEOX rope) */
+    float rope_base;    /* 1e7 */
+    float eps;          /* 1e-6 */
+    int n_vocab;        /* 151936 */
+    int attn_interval;  /* 4: attention where (il+1) % 4 == 0 */
+    int d_state;        /* 128 */
+    int n_k_head;       /* 16 */
+    int n_v_head;       /* 16 */
+    int d_conv;         /* 4 */
+    int kv_block;       /* 16 positions per KV page */
+    int max_ctx;        /* KV capacity in positions */
+    int max_batch;      /* largest prefill chunk (tokens) */
+} gd_stack_config;
+
+typedef struct gd_stack gd_stack;
+
+int gd_stack_create(gd_ctx *ctx, const gd_stack_config *cfg, uint64_t seed,
+                    gd_stack **out);
+void gd_stack_destroy(gd_stack *st);
+/* Clear GDN conv/recurrent state, KV pages and position (BonsaiEngine.reset). */
+int gd_stack_reset(gd_stack *st);
+/* Prefill n ids onto the current state (chunks of cfg.max_batch) and return
+ * the greedy next token (MetalEngine.extend).  logits may be NULL, else it
+ * receives the last token's n_vocab f32 logits (host memory). */
+int gd_stack_prefill(gd_stack *st, const int32_t *ids, int n, int32_t *next,
+                     float *logits);
+/* One token (MetalEngine.decode). */
+int gd_stack_decode(gd_stack *st, int32_t token, int32_t *next,
+                    float *logits);
+/* n greedy decode steps continuing from the token the last prefill/decode
+ * picked, with no host round trip between steps (the step is captured once
+ * as a HIP graph; the picked id stays on the device).  tokens[n] receives the
+ * n ids generated.  Equivalent to n chained gd_stack_decode calls. */
+int gd_stack_generate(gd_stack *st, int n, int32_t *tokens);
+/* Cooperative stop, safe from another thread: the next chunk boundary of a
+ * running prefill returns GD_ESTOPPED (MetalEngine.swift:15-25, 79-81). */
+int gd_stack_request_stop(gd_stack *st);
+
+/* Weight and state introspection for parity tests: tensor `name` of layer
+ * `layer` (-1 for global tensors).  Q2_0 tensors fill *w; f32 tensors fill
+ * *f32 and *count.  Names follow the GGUF ones used in Model.swift:100-145
+ * ("attn_norm", "attn_qkv", "attn_gate", "ssm_beta", "ssm_alpha", "ssm_dt",
+ * "ssm_a", "ssm_conv1d", "ssm_norm", "ssm_out", "attn_q", "attn_k", "attn_v",
+ * "attn_output", "attn_q_norm", "attn_k_norm", "post_attention_norm",
+ * "ffn_gate", "ffn_up", "ffn_down", "token_embd", "output_norm",
+ * "ssm_conv_state", "ssm_state"). */
+int gd_stack_tensor(gd_stack *st, int layer, const char *name, gd_q2w *w,
+                    float **f32, int64_t *count);
+int gd_stack_position(gd_stack *st, int64_t *pos);
+
 #ifdef __cplusplus
 }
 #endif

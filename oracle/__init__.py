@@ -46,7 +46,7 @@ _PROTOS = {
                                    _i]),
 }
 
-_lib = None
+_lib = None  # noqa
 
 
 def build() -> Path:
@@ -164,7 +164,8 @@ def l2norm_rows(x: np.ndarray, d: int, eps: float) -> np.ndarray:
 
 def rmsnorm_rows(x: np.ndarray, d: int, w: np.ndarray, eps: float) -> np.ndarray:
     x = np.ascontiguousarray(x, np.float32).copy()
-    lib().or_rmsnorm_rows(P(x), d, x.size // d, P(np.ascontiguousarray(w, np.float32)), eps)
+    w = np.ascontiguousarray(w, np.float32)
+    lib().or_rmsnorm_rows(P(x), d, x.size // d, P(w), eps)
     return x
 
 
@@ -183,8 +184,9 @@ def gdn_gate(bPre, aPre, dt, aNeg, nV):
     aPre = np.ascontiguousarray(aPre, np.float32)
     beta = np.empty_like(bPre)
     g = np.empty_like(bPre)
-    lib().or_gdn_gate(P(bPre), P(aPre), P(np.ascontiguousarray(dt, np.float32)),
-                      P(np.ascontiguousarray(aNeg, np.float32)), P(beta), P(g), nV, bPre.size)
+    dt = np.ascontiguousarray(dt, np.float32)       # keep the converted arrays alive
+    aNeg = np.ascontiguousarray(aNeg, np.float32)
+    lib().or_gdn_gate(P(bPre), P(aPre), P(dt), P(aNeg), P(beta), P(g), nV, bPre.size)
     return beta, g
 
 
@@ -204,3 +206,92 @@ def mtp_state_after(m, H, DK, DV, C_, s0, delta, k, gcum):
     arrs = [np.ascontiguousarray(a, np.float32) for a in (s0, delta, k, gcum)]
     lib().or_mtp_state_after(m, H, DK, DV, C_, *[P(a) for a in arrs], P(out))
     return out
+
+
+# ---- hybrid stack -------------------------------------------------------------
+
+class OrStackLayer(C.Structure):
+    _fields_ = [("rec", _i)] + [(n, _vp) for n in (
+        "attn_norm", "post_norm", "wqkv", "wgate", "wbeta", "walpha", "ssm_out", "conv_w", "dt",
+        "a_neg", "ssm_norm", "wq", "wk", "wv", "wo", "q_norm", "k_norm", "ffn_gate", "ffn_up",
+        "ffn_down", "conv_state", "rec_state", "kcache", "vcache")]
+
+
+class OrStack(C.Structure):
+    _fields_ = [(n, _i) for n in ("n_layer", "n_embd", "n_ff", "n_head", "n_head_kv", "head_dim",
+                                  "n_rot")] + [("rope_base", _f), ("eps", _f)] + \
+               [(n, _i) for n in ("n_vocab", "d_state", "n_k_head", "n_v_head", "d_conv",
+                                  "max_ctx", "stage_f16", "threads")] + \
+               [("layers", C.POINTER(OrStackLayer)), ("embd", _vp), ("out_norm", _vp)]
+
+
+_PROTOS["or_stack_token"] = (None, [C.POINTER(OrStack), _i, _i, _vp, _vp])
+
+
+class Stack:
+    """CPU restatement of BonsaiEngine (token by token) over given weights.
+
+    `tensors(layer, name)` must return a GGUF-block uint8 array for Q2_0
+    tensors and an f32 array otherwise (layer -1: global tensors)."""
+
+    Q2 = {"rec": ("attn_qkv", "attn_gate", "ssm_beta", "ssm_alpha", "ssm_out"),
+          "att": ("attn_q", "attn_k", "attn_v", "attn_output")}
+
+    def __init__(self, cfg: dict, tensors, stage_f16: bool = True, threads: int = 8):
+        self.cfg = cfg
+        self.keep = []
+        n = cfg["n_layer"]
+        self.layers = (OrStackLayer * n)()
+        hd, nkv = cfg["head_dim"], cfg["n_head_kv"]
+        convDim = (2 * cfg["n_k_head"] + cfg["n_v_head"]) * cfg["d_state"]
+
+        def ptr(a):
+            a = np.ascontiguousarray(a)
+            self.keep.append(a)
+            return a.ctypes.data
+
+        for il in range(n):
+            L = self.layers[il]
+            L.rec = 1 if (il + 1) % cfg["attn_interval"] != 0 else 0
+            get = lambda name: ptr(tensors(il, name))
+            L.attn_norm, L.post_norm = get("attn_norm"), get("post_attention_norm")
+            L.ffn_gate, L.ffn_up, L.ffn_down = get("ffn_gate"), get("ffn_up"), get("ffn_down")
+            if L.rec:
+                L.wqkv, L.wgate, L.wbeta, L.walpha, L.ssm_out = (get(x) for x in self.Q2["rec"])
+                L.conv_w, L.dt, L.a_neg, L.ssm_norm = (get(x) for x in
+                                                      ("ssm_conv1d", "ssm_dt", "ssm_a", "ssm_norm"))
+                L.conv_state = ptr(np.zeros((cfg["d_conv"] - 1) * convDim, np.float32))
+                L.rec_state = ptr(np.zeros(cfg["n_v_head"] * cfg["d_state"] ** 2, np.float32))
+            else:
+                L.wq, L.wk, L.wv, L.wo = (get(x) for x in self.Q2["att"])
+                L.q_norm, L.k_norm = get("attn_q_norm"), get("attn_k_norm")
+                L.kcache = ptr(np.zeros(cfg["max_ctx"] * nkv * hd, np.float32))
+                L.vcache = ptr(np.zeros(cfg["max_ctx"] * nkv * hd, np.float32))
+        st = OrStack()
+        for k in ("n_layer", "n_embd", "n_ff", "n_head", "n_head_kv", "head_dim", "n_rot",
+                  "rope_base", "eps", "n_vocab", "d_state", "n_k_head", "n_v_head", "d_conv",
+                  "max_ctx"):
+            setattr(st, k, cfg[k])
+        st.stage_f16 = 1 if stage_f16 else 0
+        st.threads = threads
+        st.layers = self.layers
+        st.embd = ptr(tensors(-1, "token_embd"))
+        st.out_norm = ptr(tensors(-1, "output_norm"))
+        self.st = st
+        self.pos = 0
+
+    def token(self, tok: int):
+        """Advance one token; returns (hidden, logits)."""
+        h = np.empty(self.cfg["n_embd"], np.float32)
+        lg = np.empty(self.cfg["n_vocab"], np.float32)
+        lib().or_stack_token(C.byref(self.st), tok, self.pos, P(h), P(lg))
+        self.pos += 1
+        return h, lg
+
+    def layer_state(self, il: int, name: str) -> np.ndarray:
+        L = self.layers[il]
+        cfg = self.cfg
+        if name == "ssm_state":
+            n = cfg["n_v_head"] * cfg["d_state"] ** 2
+            return np.ctypeslib.as_array(C.cast(L.rec_state, C.POINTER(C.c_float)), (n,)).copy()
+        raise KeyError(name)

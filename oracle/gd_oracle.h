@@ -85,6 +85,35 @@ void or_gdn_decode_batch(int B, int nV, int nK, int dS, float *q, float *k, cons
                          const float *g, const float *beta, float *S, float *o, float qScale,
                          float eps, int threads);
 
+/* ---- hybrid stack (BonsaiEngine.swift:134-191, GDN.swift:20-120,
+ *      Attention.swift:72-139) ------------------------------------------------- */
+typedef struct or_stack_layer {
+    int rec;                                    /* 1 = GDN layer, 0 = attention */
+    const float *attn_norm, *post_norm;
+    const uint8_t *wqkv, *wgate, *wbeta, *walpha, *ssm_out;   /* GGUF Q2_0 blocks */
+    const float *conv_w, *dt, *a_neg, *ssm_norm;
+    const uint8_t *wq, *wk, *wv, *wo;
+    const float *q_norm, *k_norm;
+    const uint8_t *ffn_gate, *ffn_up, *ffn_down;
+    float *conv_state, *rec_state;              /* GDN state (caller-owned, zeroed) */
+    float *kcache, *vcache;                     /* [max_ctx][n_head_kv*head_dim] */
+} or_stack_layer;
+
+typedef struct or_stack {
+    int n_layer, n_embd, n_ff, n_head, n_head_kv, head_dim, n_rot;
+    float rope_base, eps;
+    int n_vocab, d_state, n_k_head, n_v_head, d_conv, max_ctx;
+    int stage_f16;     /* round matvec inputs and K/V to f16 as the reference GPU does */
+    int threads;
+    or_stack_layer *layers;
+    const uint8_t *embd;                        /* tied token_embd / lm_head */
+    const float *out_norm;
+} or_stack;
+
+/* BonsaiEngine.forward for one token at position pos: hidden_out[n_embd] is
+ * the post-final-norm hidden; logits_out[n_vocab] may be NULL. */
+void or_stack_token(or_stack *st, int token, int pos, float *hidden_out, float *logits_out);
+
 #ifdef __cplusplus
 }
 #endif
