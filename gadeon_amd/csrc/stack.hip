@@ -63,6 +63,42 @@ __global__ void k_conv4(const float *proj, int64_t stride, float *ring, const fl
     ring[c] = r0; ring[convDim + c] = r1; ring[2 * convDim + c] = r2;
 }
 
+// The same conv for a whole prefill chunk, parallel over (token, channel): a
+// causal FIR reads the ring only for the first dConv-1 tokens.  The ring is
+// advanced afterwards by k_conv4_ring (a separate launch, so no token reads a
+// ring entry that is being overwritten).
+__global__ void k_conv4_fir(const float *proj, int64_t stride, const float *ring,
+                            const float *cw, float *out, int convDim, int N) {
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= (int64_t)N * convDim) return;
+    const int n = (int)(e / convDim), c = (int)(e % convDim);
+    float in[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int m = n - 3 + j;                 // token index of window slot j
+        in[j] = m >= 0 ? proj[(int64_t)m * stride + c] : ring[(int64_t)(3 + m) * convDim + c];
+    }
+    float acc = 0.0f;
+    acc += in[0] * cw[c * 4];
+    acc += in[1] * cw[c * 4 + 1];
+    acc += in[2] * cw[c * 4 + 2];
+    acc += in[3] * cw[c * 4 + 3];
+    out[e] = gd_silu(acc);
+}
+
+__global__ void k_conv4_ring(const float *proj, int64_t stride, float *ring, int convDim, int N) {
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= convDim) return;
+    float r[3];
+#pragma unroll
+    for (int j = 0; j < 3; j++) {
+        const int m = N - 3 + j;
+        r[j] = m >= 0 ? proj[(int64_t)m * stride + c] : ring[(int64_t)(3 + m) * convDim + c];
+    }
+#pragma unroll
+    for (int j = 0; j < 3; j++) ring[(int64_t)j * convDim + c] = r[j];
+}
+
 // o <- rmsnorm_d(o) * w * silu(z), written as f16 for the out projection
 // (GDN.swift:113-115).  One wave per (token, value head).
 __global__ void k_onorm_silu(const float *o, const float *proj, int64_t stride, int off_z,
@@ -198,85 +234,139 @@ __global__ __launch_bounds__(256) void k_attn_prefill(
     }
 }
 
-// Decode attention, one block per head: the 256 threads split the keys for
-// the scores, then split (dims x key halves) for P.V.
+// Decode attention for one query token, split over keys (flash decoding):
+// block (head h, split sp) has 4 waves; each wave takes whole keys with a lane
+// holding 2 of the 128 dims, and keeps an online-softmax partial.  The block
+// merges its waves and writes (max, sum, acc[128]) for the split to a
+// workspace; k_attn_combine merges the splits (Attention.swift:108-134).
+constexpr int DSPLIT = 16;      // key splits per head
 __global__ __launch_bounds__(256) void k_attn_decode(
-        const float *q, const float *gate, const uint16_t *kc, const uint16_t *vc,
-        const int32_t *page_table, const int32_t *pos_ptr, uint16_t *out, int H, int HKV,
-        int block, float scale, float *scores, int max_ctx) {
-    __shared__ float qs[HD];
-    __shared__ float red[8];
-    __shared__ float part[2][HD];
-    const int h = blockIdx.x, t = threadIdx.x;
+        const float *q, const uint16_t *kc, const uint16_t *vc, const int32_t *page_table,
+        const int32_t *pos_ptr, float *part, int H, int HKV, int block, float scale) {
+    __shared__ float wm[4], wl[4];
+    __shared__ float wacc[4][HD];
+    const int h = blockIdx.x, sp = blockIdx.y, t = threadIdx.x;
+    const int lane = t & 63, w = t >> 6;
     const int kvh = h / (H / HKV), kvDim = HKV * HD;
     const int T = *pos_ptr + 1;
-    float *sc = scores + (int64_t)h * max_ctx;
-    if (t < HD) qs[t] = q[(int64_t)h * HD + t] * scale;
-    __syncthreads();
-    float mx = -INFINITY;
-    for (int j = t; j < T; j += 256) {
-        const uint16_t *kr = kc + kv_slot(page_table, j, block) * kvDim + kvh * HD;
-        float s = 0.f;
-        for (int d = 0; d < HD; d += 8) {
-            const u32x4 w = *(const u32x4 *)(kr + d);
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                s = fmaf(qs[d + 2 * e], gd_h2f((uint16_t)(w[e] & 0xffff)), s);
-                s = fmaf(qs[d + 2 * e + 1], gd_h2f((uint16_t)(w[e] >> 16)), s);
-            }
-        }
-        sc[j] = s;
-        mx = fmaxf(mx, s);
+    const float q0 = q[(int64_t)h * HD + 2 * lane] * scale;
+    const float q1 = q[(int64_t)h * HD + 2 * lane + 1] * scale;
+    float m = -INFINITY, l = 0.f, a0 = 0.f, a1 = 0.f;
+    // Wave w of split sp takes keys j = (sp * 4 + w) + 64 * i.
+    for (int j = sp * 4 + w; j < T; j += DSPLIT * 4) {
+        const int64_t base = kv_slot(page_table, j, block) * kvDim + kvh * HD + 2 * lane;
+        const uint32_t kk = *(const uint32_t *)(kc + base);
+        const uint32_t vv = *(const uint32_t *)(vc + base);
+        float s = q0 * gd_h2f((uint16_t)(kk & 0xffff)) + q1 * gd_h2f((uint16_t)(kk >> 16));
+        s = gd_wave_sum(s);
+        const float mn = fmaxf(m, s);
+        const float al = expf(m - mn), p = expf(s - mn);
+        l = l * al + p;
+        a0 = fmaf(p, gd_h2f((uint16_t)(vv & 0xffff)), a0 * al);
+        a1 = fmaf(p, gd_h2f((uint16_t)(vv >> 16)), a1 * al);
+        m = mn;
     }
-    // block max
-    for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-    if ((t & 63) == 0) red[t >> 6] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    __syncthreads();
-    float sum = 0.f;
-    for (int j = t; j < T; j += 256) {
-        const float p = expf(sc[j] - mx);
-        sc[j] = p;
-        sum += p;
-    }
-    sum = gd_block_sum(sum, red);
-    __threadfence_block();
-    __syncthreads();
-    // P.V: thread (d = t % 128, half = t / 128) sums keys of its parity.
-    const int d = t & (HD - 1), hf = t >> 7;
-    float acc = 0.f;
-    for (int j = hf; j < T; j += 2)
-        acc = fmaf(sc[j], gd_h2f(vc[kv_slot(page_table, j, block) * kvDim + kvh * HD + d]), acc);
-    part[hf][d] = acc;
+    if (lane == 0) { wm[w] = m; wl[w] = l; }
+    wacc[w][2 * lane] = a0;
+    wacc[w][2 * lane + 1] = a1;
     __syncthreads();
     if (t < HD) {
-        const float o = (part[0][t] + part[1][t]) / sum;
-        out[(int64_t)h * HD + t] = gd_f2h(o * gd_sigmoid(gate[(int64_t)h * HD + t]));
+        float M = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
+        float L = 0.f, A = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float f = wm[i] == -INFINITY ? 0.f : expf(wm[i] - M);
+            L += wl[i] * f;
+            A += wacc[i][t] * f;
+        }
+        float *p = part + ((int64_t)h * DSPLIT + sp) * (HD + 2);
+        p[t] = A;
+        if (t == 0) { p[HD] = M; p[HD + 1] = L; }
     }
 }
 
+__global__ void k_attn_combine(const float *part, const float *gate, uint16_t *out) {
+    const int h = blockIdx.x, t = threadIdx.x;      // HD threads
+    const float *p = part + (int64_t)h * DSPLIT * (HD + 2);
+    float M = -INFINITY;
+    for (int s = 0; s < DSPLIT; s++) M = fmaxf(M, p[s * (HD + 2) + HD]);
+    float L = 0.f, A = 0.f;
+    for (int s = 0; s < DSPLIT; s++) {
+        const float ms = p[s * (HD + 2) + HD];
+        const float f = ms == -INFINITY ? 0.f : expf(ms - M);
+        L += p[s * (HD + 2) + HD + 1] * f;
+        A += p[s * (HD + 2) + t] * f;
+    }
+    out[(int64_t)h * HD + t] = gd_f2h(A / L * gd_sigmoid(gate[(int64_t)h * HD + t]));
+}
+
 // Greedy pick: index of the first maximum (BonsaiEngine.argmax, :187-191).
-__global__ __launch_bounds__(1024) void k_argmax(const float *v, int n, int32_t *out) {
-    __shared__ float bv[16];
-    __shared__ int bi[16];
-    float best = -INFINITY;
-    int idx = 0x7fffffff;
-    for (int i = threadIdx.x; i < n; i += 1024) {
-        const float x = v[i];
-        if (x > best) { best = x; idx = i; }
-    }
-    for (int o = 32; o >= 1; o >>= 1) {
-        const float ob = __shfl_xor(best, o, 64);
-        const int oi = __shfl_xor(idx, o, 64);
-        if (ob > best || (ob == best && oi < idx)) { best = ob; idx = oi; }
-    }
+// Pass 1: per-block (max, first index) pairs; pass 2 (one block) reduces them.
+__device__ __forceinline__ void argmax_merge(float &best, int &idx, float ob, int oi) {
+    if (ob > best || (ob == best && oi < idx)) { best = ob; idx = oi; }
+}
+
+__device__ void argmax_block(float best, int idx, float *bv, int *bi, float *ob, int *oi) {
+    for (int o = 32; o >= 1; o >>= 1)
+        argmax_merge(best, idx, __shfl_xor(best, o, 64), __shfl_xor(idx, o, 64));
     if ((threadIdx.x & 63) == 0) { bv[threadIdx.x >> 6] = best; bi[threadIdx.x >> 6] = idx; }
     __syncthreads();
     if (threadIdx.x == 0) {
-        for (int w = 1; w < 16; w++)
-            if (bv[w] > best || (bv[w] == best && bi[w] < idx)) { best = bv[w]; idx = bi[w]; }
-        *out = idx;
+        for (int w = 1; w < (int)(blockDim.x >> 6); w++) argmax_merge(best, idx, bv[w], bi[w]);
+        *ob = best;
+        *oi = idx;
+    }
+}
+
+constexpr int AMAX_BLOCKS = 128;
+__global__ __launch_bounds__(256) void k_argmax_part(const float *v, int n, float *pv, int *pi) {
+    __shared__ float bv[4];
+    __shared__ int bi[4];
+    float best = -INFINITY;
+    int idx = 0x7fffffff;
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += AMAX_BLOCKS * 256)
+        argmax_merge(best, idx, v[i], i);
+    argmax_block(best, idx, bv, bi, pv + blockIdx.x, pi + blockIdx.x);
+}
+
+__global__ __launch_bounds__(128) void k_argmax_final(const float *pv, const int *pi,
+                                                      int32_t *out) {
+    __shared__ float bv[2];
+    __shared__ int bi[2];
+    __shared__ float fb;
+    __shared__ int fi;
+    argmax_block(pv[threadIdx.x], pi[threadIdx.x], bv, bi, &fb, &fi);
+    if (threadIdx.x == 0) *out = fi;
+}
+
+// x += y over rows of n, then y16 = rmsnorm(x) * w as f16 (the residual add
+// and the following norm, BonsaiEngine.swift:169-171).  One block per row.
+__global__ __launch_bounds__(1024) void k_add_rmsnorm(float *x, const float *y, const float *w,
+                                                      uint16_t *out, int n, float eps) {
+    __shared__ float red[16];
+    const int64_t row = blockIdx.x;
+    float *xr = x + row * n;
+    const float *yr = y + row * n;
+    float ss = 0.f;
+    for (int i = threadIdx.x * 4; i < n; i += blockDim.x * 4) {
+        f32x4 a = *(const f32x4 *)(xr + i);
+        if (yr) {
+            const f32x4 b = *(const f32x4 *)(yr + i);
+            a += b;
+            *(f32x4 *)(xr + i) = a;
+        }
+        ss += a[0] * a[0] + a[1] * a[1] + a[2] * a[2] + a[3] * a[3];
+    }
+    ss = gd_block_sum(ss, red);
+    const float s = 1.0f / sqrtf(ss / (float)n + eps);
+    for (int i = threadIdx.x * 4; i < n; i += blockDim.x * 4) {
+        const f32x4 a = *(const f32x4 *)(xr + i);
+        const f32x4 ww = *(const f32x4 *)(w + i);
+        uint16_t *o = out + row * n + i;
+        o[0] = gd_f2h(a[0] * s * ww[0]);
+        o[1] = gd_f2h(a[1] * s * ww[1]);
+        o[2] = gd_f2h(a[2] * s * ww[2]);
+        o[3] = gd_f2h(a[3] * s * ww[3]);
     }
 }
 
@@ -314,7 +404,8 @@ struct gd_stack {
     // scratch
     float *x = nullptr, *proj = nullptr, *conv_out = nullptr, *o32 = nullptr, *contrib = nullptr;
     float *beta = nullptr, *g = nullptr, *q32 = nullptr, *gate32 = nullptr, *logits = nullptr;
-    float *scores = nullptr;
+    float *attn_part = nullptr, *amax_v = nullptr;
+    int *amax_i = nullptr;
     uint16_t *xn16 = nullptr, *a16 = nullptr;
     int32_t *ids = nullptr, *dpos = nullptr, *dtok = nullptr;
     int64_t pos = 0;
@@ -375,29 +466,33 @@ int forward(gd_stack *st, int N, bool decode) {
     hipStream_t s = ctx->stream;
     int rc;
 #define R_(call) do { if ((rc = (call)) != GD_OK) return rc; } while (0)
+#define K_(name, ...) do { hipLaunchKernelGGL(name, __VA_ARGS__); GD_LAUNCHED(ctx, #name); } while (0)
+    // attn_norm of layer 0; every later norm is fused with the residual add
+    // that precedes it (k_add_rmsnorm).
+    K_(k_add_rmsnorm, dim3(N), dim3(1024), 0, s, st->x, (const float *)nullptr,
+       st->L[0].attn_norm, st->xn16, E, eps);
     for (int il = 0; il < c.n_layer; il++) {
         StackLayer &ly = st->L[il];
-        R_(gd_rmsnorm(ctx, st->x, ly.attn_norm, st->xn16, GD_F16, E, N, eps));
         const int RP = ly.rec ? st->rp_rec : st->rp_att;
         if (decode) R_(gd_q2_0_gemv(ctx, &ly.in_proj, st->xn16, GD_F16, st->proj));
         else R_(gd_q2_0_gemm(ctx, &ly.in_proj, N, st->xn16, GD_F16, st->proj, GD_F32));
         if (ly.rec) {
             const int off_z = st->convDim, off_b = off_z + st->valDim, off_a = off_b + nV;
-            hipLaunchKernelGGL(k_conv4, dim3(gd_blocks(st->convDim, 256)), dim3(256), 0, s,
-                               st->proj, (int64_t)RP, ly.conv_state, ly.conv_w, st->conv_out,
-                               st->convDim, N);
-            GD_LAUNCHED(ctx, "k_conv4");
             if (decode) {
+                K_(k_conv4, dim3(gd_blocks(st->convDim, 256)), dim3(256), 0, s, st->proj,
+                   (int64_t)RP, ly.conv_state, ly.conv_w, st->conv_out, st->convDim, 1);
                 // Fused gate + L2 norm + delta-rule step, state in place.
                 R_(gd_gdn_decode(ctx, 1, nV, nK, c.d_state, st->conv_out,
                                  st->conv_out + st->keyDim, st->conv_out + 2 * st->keyDim,
                                  GD_F32, st->proj + off_a, st->proj + off_b, ly.dt, ly.a_neg,
                                  ly.rec_state, st->o32, qScale, eps));
             } else {
-                hipLaunchKernelGGL(k_gate, dim3(gd_blocks((int64_t)N * nV, 256)), dim3(256), 0, s,
-                                   st->proj, (int64_t)RP, off_b, off_a, ly.dt, ly.a_neg, st->beta,
-                                   st->g, nV, N);
-                GD_LAUNCHED(ctx, "k_gate");
+                K_(k_conv4_fir, dim3(gd_blocks((int64_t)N * st->convDim, 256)), dim3(256), 0, s,
+                   st->proj, (int64_t)RP, ly.conv_state, ly.conv_w, st->conv_out, st->convDim, N);
+                K_(k_conv4_ring, dim3(gd_blocks(st->convDim, 256)), dim3(256), 0, s, st->proj,
+                   (int64_t)RP, ly.conv_state, st->convDim, N);
+                K_(k_gate, dim3(gd_blocks((int64_t)N * nV, 256)), dim3(256), 0, s, st->proj,
+                   (int64_t)RP, off_b, off_a, ly.dt, ly.a_neg, st->beta, st->g, nV, N);
                 R_(gd_l2norm_rows(ctx, st->conv_out, c.d_state, 2 * nK, st->convDim, N, eps));
                 R_(gd_gdn_prefill(ctx, N, nV, nK, c.d_state, c.d_state, st->conv_out,
                                   st->convDim, st->conv_out + st->keyDim, st->convDim,
@@ -405,47 +500,51 @@ int forward(gd_stack *st, int N, bool decode) {
                                   st->beta, ly.rec_state, st->o32, st->valDim, GD_F32, qScale,
                                   64));
             }
-            hipLaunchKernelGGL(k_onorm_silu, dim3(gd_blocks((int64_t)N * nV, 4)), dim3(256), 0, s,
-                               st->o32, st->proj, (int64_t)RP, off_z, ly.ssm_norm, st->a16, nV, N,
-                               eps);
-            GD_LAUNCHED(ctx, "k_onorm_silu");
+            K_(k_onorm_silu, dim3(gd_blocks((int64_t)N * nV, 4)), dim3(256), 0, s, st->o32,
+               st->proj, (int64_t)RP, off_z, ly.ssm_norm, st->a16, nV, N, eps);
         } else {
-            hipLaunchKernelGGL(k_attn_prep, dim3(N, H + HKV), dim3(HD), 0, s, st->proj,
-                               (int64_t)RP, ly.q_norm, ly.k_norm, st->q32, st->gate32, ly.kc,
-                               ly.vc, st->page_table, st->dpos, H, HKV, c.n_rot, c.rope_base,
-                               c.kv_block, eps);
-            GD_LAUNCHED(ctx, "k_attn_prep");
+            K_(k_attn_prep, dim3(N, H + HKV), dim3(HD), 0, s, st->proj, (int64_t)RP, ly.q_norm,
+               ly.k_norm, st->q32, st->gate32, ly.kc, ly.vc, st->page_table, st->dpos, H, HKV,
+               c.n_rot, c.rope_base, c.kv_block, eps);
             const float scale = 1.0f / sqrtf((float)HD);
-            if (decode)
-                hipLaunchKernelGGL(k_attn_decode, dim3(H), dim3(256), 0, s, st->q32, st->gate32,
-                                   ly.kc, ly.vc, st->page_table, st->dpos, st->a16, H, HKV,
-                                   c.kv_block, scale, st->scores, c.max_ctx);
-            else
-                hipLaunchKernelGGL(k_attn_prefill, dim3(H, gd_blocks(N, AQ)), dim3(256), 0, s,
-                                   st->q32, st->gate32, ly.kc, ly.vc, st->page_table, st->dpos,
-                                   st->a16, H, HKV, N, c.kv_block, scale);
-            GD_LAUNCHED(ctx, "k_attn");
+            if (decode) {
+                K_(k_attn_decode, dim3(H, DSPLIT), dim3(256), 0, s, st->q32, ly.kc, ly.vc,
+                   st->page_table, st->dpos, st->attn_part, H, HKV, c.kv_block, scale);
+                K_(k_attn_combine, dim3(H), dim3(HD), 0, s, st->attn_part, st->gate32, st->a16);
+            } else {
+                K_(k_attn_prefill, dim3(H, gd_blocks(N, AQ)), dim3(256), 0, s, st->q32,
+                   st->gate32, ly.kc, ly.vc, st->page_table, st->dpos, st->a16, H, HKV, N,
+                   c.kv_block, scale);
+            }
         }
         if (decode) R_(gd_q2_0_gemv(ctx, &ly.out_proj, st->a16, GD_F16, st->contrib));
         else R_(gd_q2_0_gemm(ctx, &ly.out_proj, N, st->a16, GD_F16, st->contrib, GD_F32));
-        R_(gd_add(ctx, st->x, st->contrib, (int64_t)N * E));
-        R_(gd_rmsnorm(ctx, st->x, ly.post_norm, st->xn16, GD_F16, E, N, eps));
+        K_(k_add_rmsnorm, dim3(N), dim3(1024), 0, s, st->x, st->contrib, ly.post_norm, st->xn16,
+           E, eps);
         if (decode) R_(gd_q2_0_gemv(ctx, &ly.gate_up, st->xn16, GD_F16, st->proj));
         else R_(gd_q2_0_gemm(ctx, &ly.gate_up, N, st->xn16, GD_F16, st->proj, GD_F32));
-        hipLaunchKernelGGL(k_swiglu, dim3(gd_blocks((int64_t)N * FF, 256)), dim3(256), 0, s,
-                           st->proj, FF, st->a16, N);
-        GD_LAUNCHED(ctx, "k_swiglu");
+        K_(k_swiglu, dim3(gd_blocks((int64_t)N * FF, 256)), dim3(256), 0, s, st->proj, FF,
+           st->a16, N);
         if (decode) R_(gd_q2_0_gemv(ctx, &ly.down, st->a16, GD_F16, st->contrib));
         else R_(gd_q2_0_gemm(ctx, &ly.down, N, st->a16, GD_F16, st->contrib, GD_F32));
-        R_(gd_add(ctx, st->x, st->contrib, (int64_t)N * E));
+        if (il + 1 < c.n_layer) {
+            K_(k_add_rmsnorm, dim3(N), dim3(1024), 0, s, st->x, st->contrib,
+               st->L[il + 1].attn_norm, st->xn16, E, eps);
+        } else {
+            // Only the last token's hidden feeds the logits: residual add and
+            // final norm on that row alone.
+            const int64_t last = (int64_t)(N - 1) * E;
+            K_(k_add_rmsnorm, dim3(1), dim3(1024), 0, s, st->x + last, st->contrib + last,
+               st->out_norm, st->xn16, E, eps);
+        }
     }
-    // Final norm of the last token, tied lm_head, greedy pick.
-    R_(gd_rmsnorm(ctx, st->x + (int64_t)(N - 1) * E, st->out_norm, st->xn16, GD_F16, E, 1, eps));
+    // Tied lm_head on the last token, greedy pick, position bump.
     R_(gd_q2_0_gemv(ctx, &st->embd, st->xn16, GD_F16, st->logits));
-    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, s, st->logits, c.n_vocab, st->dtok);
-    GD_LAUNCHED(ctx, "k_argmax");
-    hipLaunchKernelGGL(k_add_pos, dim3(1), dim3(1), 0, s, st->dpos, N);
-    GD_LAUNCHED(ctx, "k_add_pos");
+    K_(k_argmax_part, dim3(AMAX_BLOCKS), dim3(256), 0, s, st->logits, c.n_vocab, st->amax_v,
+       st->amax_i);
+    K_(k_argmax_final, dim3(1), dim3(AMAX_BLOCKS), 0, s, st->amax_v, st->amax_i, st->dtok);
+    K_(k_add_pos, dim3(1), dim3(1), 0, s, st->dpos, N);
+#undef K_
 #undef R_
     return GD_OK;
 }
@@ -544,7 +643,9 @@ extern "C" int gd_stack_create(gd_ctx *ctx, const gd_stack_config *cfg, uint64_t
     C_(salloc_t(st, (size_t)B * c.n_head * HD, &st->q32));
     C_(salloc_t(st, (size_t)B * c.n_head * HD, &st->gate32));
     C_(salloc_t(st, (size_t)c.n_vocab, &st->logits));
-    C_(salloc_t(st, (size_t)c.n_head * c.max_ctx, &st->scores));
+    C_(salloc_t(st, (size_t)c.n_head * DSPLIT * (HD + 2), &st->attn_part));
+    C_(salloc_t(st, (size_t)AMAX_BLOCKS, &st->amax_v));
+    C_(salloc_t(st, (size_t)AMAX_BLOCKS, &st->amax_i));
     C_(salloc_t(st, (size_t)B * E, &st->xn16));
     const int a16n = std::max(std::max(st->valDim, c.n_head * HD), FF);
     C_(salloc_t(st, (size_t)B * a16n, &st->a16));
