@@ -280,6 +280,7 @@ __global__ void q2_0_dequant_rows_kernel(const uint32_t *__restrict__ codes,
 }  // namespace
 
 int gd_check_q2w(gd_ctx *ctx, const gd_q2w *w, const char *who);
+int gd_gemv_mfma(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y);
 
 extern "C" int gd_q2_0_dequant_rows(gd_ctx *ctx, const gd_q2w *w, const int32_t *ids, int64_t n,
                                     float *out) {
@@ -310,6 +311,9 @@ extern "C" int gd_q2_0_gemv(gd_ctx *ctx, const gd_q2w *w, const void *x, int x_d
     GD_REQUIRE(ctx, w->K <= (1 << 24) && w->R < (1LL << 31),
                "gd_q2_0_gemv: K=%lld or R=%lld too large", (long long)w->K, (long long)w->R);
     const int K = (int)w->K, R = (int)w->R;
+    // f16 x runs on the matrix cores (q2_0_gemv_mfma.hip); f32 x keeps the
+    // exact hi+lo split on the VALU kernels below.
+    if (x_dtype == GD_F16 && gd_gemv_mfma(ctx, w, x, y) == GD_OK) return GD_OK;
     const int steps = ((K >> 6) + 15) >> 4;
     const auto *c = (const u32x4 *)w->codes;
     const auto *s = (const uint16_t *)w->scales;
