@@ -280,13 +280,15 @@ def cpu_baseline_stack(ctx, ga, h, c, seconds: float) -> dict:
     def read(layer, name):
         w = ga.Q2W()
         f = C.POINTER(C.c_float)()
+        r0 = C.c_int64()
         n = C.c_int64()
-        ctx.check(lib.gd_stack_tensor(h, layer, name.encode(), C.byref(w), C.byref(f), C.byref(n)))
+        ctx.check(lib.gd_stack_tensor(h, layer, name.encode(), C.byref(w), C.byref(r0), C.byref(f),
+                                      C.byref(n)))
         if f:
             return ctx.get(C.cast(f, C.c_void_p).value, n.value, np.float32)
-        nbytes = w.R * (w.K // 128) * 34
+        nbytes = n.value * (w.K // 128) * 34
         d = ctx.alloc(nbytes)
-        ctx.gd_q2_0_export(C.byref(w), d)
+        ctx.gd_q2_0_export_rows(C.byref(w), r0.value, n.value, d)
         out = ctx.get(d, nbytes, np.uint8)
         ctx.free(d)
         return out

@@ -60,6 +60,7 @@ _PROTOS = {
     "gd_q2_0_repack": (_i, [_vp, _vp, _u64, _Q2WP]),
     "gd_q2_0_upload": (_i, [_vp, _vp, _i64, _i64, _Q2WP]),
     "gd_q2_0_export": (_i, [_vp, _Q2WP, _vp]),
+    "gd_q2_0_export_rows": (_i, [_vp, _Q2WP, _i64, _i64, _vp]),
     "gd_q2_0_gemv": (_i, [_vp, _Q2WP, _vp, _i, _vp]),
     "gd_q2_0_gemm": (_i, [_vp, _Q2WP, _i64, _vp, _i, _vp, _i]),
     "gd_q2_0_dequant_rows": (_i, [_vp, _Q2WP, _vp, _i64, _vp]),
@@ -86,7 +87,8 @@ _PROTOS = {
     "gd_stack_prefill": (_i, [_vp, _vp, _i, C.POINTER(C.c_int32), _vp]),
     "gd_stack_decode": (_i, [_vp, C.c_int32, C.POINTER(C.c_int32), _vp]),
     "gd_stack_request_stop": (_i, [_vp]),
-    "gd_stack_tensor": (_i, [_vp, _i, C.c_char_p, _Q2WP, C.POINTER(_fp), C.POINTER(_i64)]),
+    "gd_stack_tensor": (_i, [_vp, _i, C.c_char_p, _Q2WP, C.POINTER(_i64), C.POINTER(_fp),
+                         C.POINTER(_i64)]),
     "gd_stack_position": (_i, [_vp, C.POINTER(_i64)]),
     "gd_stack_generate": (_i, [_vp, _i, _vp]),
 }

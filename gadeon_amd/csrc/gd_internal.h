@@ -50,6 +50,37 @@ static inline unsigned gd_blocks(int64_t n, int per) {
     return (unsigned)((n + per - 1) / per);
 }
 
+// ------------------------------------------------- device Q2_0 weight layout
+// Rows come in groups of 16 and K in steps of 512 (4 blocks of 128).
+//   codes:  one 2 KiB tile per (row group, step): [half h][block-in-step kb]
+//           [row-in-group r][16 bytes] holds code bytes 16h..16h+15 of block
+//           4*step+kb of row 16*group+r.  The 64 lanes of a wave reading
+//           lane*16 + h*1024 get exactly the matrix-core A operand layout
+//           (lane = 16*kb + r), one contiguous 1 KiB per load instruction.
+//   scales: [row group][block/16][block%16][r] f16, so the 16 rows of a block
+//           are 32 contiguous bytes.
+// Rows past R and blocks past K/128 are padding and hold zeros.
+__host__ __device__ inline int64_t gd_q2_steps(int64_t K) { return (K / 128 + 3) / 4; }
+__host__ __device__ inline int64_t gd_q2_bgroups(int64_t K) { return (K / 128 + 15) / 16; }
+__host__ __device__ inline int64_t gd_q2_rgroups(int64_t R) { return (R + 15) / 16; }
+__host__ __device__ inline size_t gd_q2_codes_bytes(int64_t K, int64_t R) {
+    return (size_t)gd_q2_rgroups(R) * gd_q2_steps(K) * 2048;
+}
+__host__ __device__ inline size_t gd_q2_scales_count(int64_t K, int64_t R) {
+    return (size_t)gd_q2_rgroups(R) * gd_q2_bgroups(K) * 256;
+}
+// Byte offset of code bytes 16h..16h+15 of block `blk` of row `row`.
+__host__ __device__ inline size_t gd_q2_code_off(int64_t row, int64_t blk, int h,
+                                                 int64_t steps) {
+    return (((size_t)(row >> 4) * steps + (size_t)(blk >> 2)) << 11) + ((size_t)h << 10) +
+           ((size_t)(((blk & 3) << 4) | (row & 15)) << 4);
+}
+// Index (in f16 units) of the scale of block `blk` of row `row`.
+__host__ __device__ inline size_t gd_q2_scale_idx(int64_t row, int64_t blk, int64_t bgroups) {
+    return (((((size_t)(row >> 4) * bgroups + (size_t)(blk >> 4)) << 4) | (size_t)(blk & 15))
+            << 4) | (size_t)(row & 15);
+}
+
 // ---------------------------------------------------------------- device side
 
 typedef _Float16 f16;
@@ -58,6 +89,7 @@ typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float gd_h2f(uint16_t h) {

@@ -43,7 +43,7 @@ __device__ __forceinline__ void dequant8(uint32_t u, f16x2 d2, uint32_t *out) {
 
 template <int XT, int YT>
 __global__ __launch_bounds__(THREADS) void q2_0_gemm_kernel(
-        const uint32_t *__restrict__ codes, const uint16_t *__restrict__ scales,
+        const uint8_t *__restrict__ codes, const uint16_t *__restrict__ scales,
         const void *__restrict__ Xv, void *__restrict__ Yv, int T, int K, int R) {
     __shared__ __attribute__((aligned(16))) f16 Xs[2][BT * LDSW];
     __shared__ __attribute__((aligned(16))) f16 Ws[2][BR * LDSW];
@@ -56,7 +56,8 @@ __global__ __launch_bounds__(THREADS) void q2_0_gemm_kernel(
     const int wr = wave & 1;         // token half of the tile
     const int wc = wave >> 1;        // weight-row half
     const int nblk = K >> 7;
-    const int cpr = K >> 2;          // code bytes per row
+    const int csteps = (nblk + 3) >> 2;
+    const int bgroups = (nblk + 15) >> 4;
 
     // Global -> register staging for one K-slice.
     u32x4 xr[4];                     // X: 4 x 8 halves per thread (f16 path)
@@ -84,11 +85,14 @@ __global__ __launch_bounds__(THREADS) void q2_0_gemm_kernel(
                 xf[2 * i + 1] = p[1];
             }
         }
+        // Codes k0 .. k0+63 of a row are one 16-byte slot of its tile
+        // (half (k0/64)%2 of block k0/128); this thread takes 8 bytes of it.
         const int r = min(r0 + wrow, R - 1);
-        const uint32_t *p = codes + ((size_t)r * cpr + (k0 >> 2) + 8 * wpart) / 4;
-        wc2[0] = p[0];
-        wc2[1] = p[1];
-        wd = scales[(size_t)r * nblk + (k0 >> 7)];
+        const u32x2 v = *(const u32x2 *)(codes + gd_q2_code_off(r, k0 >> 7, (k0 >> 6) & 1, csteps) +
+                                         8 * wpart);
+        wc2[0] = v[0];
+        wc2[1] = v[1];
+        wd = scales[gd_q2_scale_idx(r, k0 >> 7, bgroups)];
     };
 
     auto store_slice = [&](int buf) {
@@ -197,7 +201,7 @@ extern "C" int gd_q2_0_gemm(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void 
                "gd_q2_0_gemm: shape too large");
     const int K = (int)w->K, R = (int)w->R;
     dim3 grid(gd_blocks(R, BR), gd_blocks(T, BT));
-    auto *c = (const uint32_t *)w->codes;
+    auto *c = (const uint8_t *)w->codes;
     auto *s = (const uint16_t *)w->scales;
     if (x_dtype == GD_F16 && y_dtype == GD_F32)
         hipLaunchKernelGGL((q2_0_gemm_kernel<0, 0>), grid, dim3(THREADS), 0, ctx->stream, c, s, X,

@@ -262,10 +262,17 @@ extern "C" int gd_q2w_alloc(gd_ctx *ctx, int64_t K, int64_t R, gd_q2w *w) {
                (long long)K, (long long)R);
     w->codes = w->scales = nullptr;
     w->K = K; w->R = R;
-    int rc = gd_alloc(ctx, (size_t)(R * (K / 4)), &w->codes);
+    const size_t cb = gd_q2_codes_bytes(K, R), sb = gd_q2_scales_count(K, R) * 2;
+    int rc = gd_alloc(ctx, cb, &w->codes);
     if (rc) return rc;
-    rc = gd_alloc(ctx, (size_t)(R * (K / GD_Q2_0_QK) * 2), &w->scales);
+    rc = gd_alloc(ctx, sb, &w->scales);
     if (rc) { gd_free(ctx, w->codes); w->codes = nullptr; return rc; }
+    // Padding rows and blocks must read as zero weights.
+    if ((rc = gd_fill_u32(ctx, w->codes, 0u, cb / 4)) ||
+        (rc = gd_fill_u32(ctx, w->scales, 0u, sb / 4))) {
+        gd_q2w_free(ctx, w);
+        return rc;
+    }
     return GD_OK;
 }
 
@@ -278,30 +285,44 @@ extern "C" int gd_q2w_free(gd_ctx *ctx, gd_q2w *w) {
     return rc ? rc : rc2;
 }
 
-// One thread per 34-byte block.  The GGUF side is only 2-byte aligned, so it
-// is read as 17 halfwords; the planes are written as 8 aligned dwords + 1 f16.
-__global__ void gd_repack_kernel(const uint16_t *src, uint32_t *codes, uint16_t *scales,
-                                 int64_t nblocks) {
-    int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+// One thread per 34-byte GGUF block (row-major order).  The GGUF side is only
+// 2-byte aligned, so it is read as 17 halfwords; the code bytes go to their
+// two 16-byte slots of the row group's tile, the scale to its slot.
+__global__ void gd_repack_kernel(const uint16_t *src, uint8_t *codes, uint16_t *scales,
+                                 int64_t nblk, int64_t nblocks) {
+    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (b >= nblocks) return;
+    const int64_t row = b / nblk, blk = b % nblk;
+    const int64_t steps = (nblk + 3) / 4, bgroups = (nblk + 15) / 16;
     const uint16_t *p = src + b * (GD_Q2_0_BLOCK_BYTES / 2);
-    scales[b] = p[0];
-    uint32_t *c = codes + b * 8;
+    scales[gd_q2_scale_idx(row, blk, bgroups)] = p[0];
 #pragma unroll
-    for (int j = 0; j < 8; j++) c[j] = (uint32_t)p[1 + 2 * j] | ((uint32_t)p[2 + 2 * j] << 16);
+    for (int h = 0; h < 2; h++) {
+        u32x4 v;
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            v[j] = (uint32_t)p[1 + 8 * h + 2 * j] | ((uint32_t)p[2 + 8 * h + 2 * j] << 16);
+        *(u32x4 *)(codes + gd_q2_code_off(row, blk, h, steps)) = v;
+    }
 }
 
-__global__ void gd_export_kernel(const uint32_t *codes, const uint16_t *scales, uint16_t *dst,
-                                 int64_t nblocks) {
-    int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+// Inverse of gd_repack_kernel for rows [row0, row0 + nrows).
+__global__ void gd_export_kernel(const uint8_t *codes, const uint16_t *scales, uint16_t *dst,
+                                 int64_t nblk, int64_t row0, int64_t nblocks) {
+    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (b >= nblocks) return;
+    const int64_t row = row0 + b / nblk, blk = b % nblk;
+    const int64_t steps = (nblk + 3) / 4, bgroups = (nblk + 15) / 16;
     uint16_t *p = dst + b * (GD_Q2_0_BLOCK_BYTES / 2);
-    p[0] = scales[b];
-    const uint32_t *c = codes + b * 8;
+    p[0] = scales[gd_q2_scale_idx(row, blk, bgroups)];
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-        p[1 + 2 * j] = (uint16_t)(c[j] & 0xffff);
-        p[2 + 2 * j] = (uint16_t)(c[j] >> 16);
+    for (int h = 0; h < 2; h++) {
+        const u32x4 v = *(const u32x4 *)(codes + gd_q2_code_off(row, blk, h, steps));
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            p[1 + 8 * h + 2 * j] = (uint16_t)(v[j] & 0xffff);
+            p[2 + 8 * h + 2 * j] = (uint16_t)(v[j] >> 16);
+        }
     }
 }
 
@@ -310,8 +331,8 @@ static int check_q2w(gd_ctx *ctx, const gd_q2w *w, const char *who) {
     GD_REQUIRE(ctx, w->K > 0 && w->K % GD_Q2_0_QK == 0 && w->R > 0,
                "%s: K=%lld must be a positive multiple of 128, R=%lld > 0", who,
                (long long)w->K, (long long)w->R);
-    GD_REQUIRE(ctx, ((uintptr_t)w->codes & 15) == 0 && ((uintptr_t)w->scales & 3) == 0,
-               "%s: codes plane must be 16-byte aligned, scales 4-byte aligned", who);
+    GD_REQUIRE(ctx, ((uintptr_t)w->codes & 255) == 0 && ((uintptr_t)w->scales & 7) == 0,
+               "%s: codes plane must be 256-byte aligned, scales 8-byte aligned", who);
     return GD_OK;
 }
 int gd_check_q2w(gd_ctx *ctx, const gd_q2w *w, const char *who) { return check_q2w(ctx, w, who); }
@@ -321,11 +342,29 @@ extern "C" int gd_q2_0_repack(gd_ctx *ctx, const void *gguf, uint64_t woff, gd_q
     int rc = check_q2w(ctx, w, "gd_q2_0_repack");
     if (rc) return rc;
     GD_REQUIRE(ctx, gguf && woff % 2 == 0, "gd_q2_0_repack: null source or odd offset");
-    const int64_t nb = w->R * (w->K / GD_Q2_0_QK);
+    const int64_t nblk = w->K / GD_Q2_0_QK, nb = w->R * nblk;
     hipLaunchKernelGGL(gd_repack_kernel, dim3(gd_blocks(nb, 256)), dim3(256), 0, ctx->stream,
-                       (const uint16_t *)((const uint8_t *)gguf + woff), (uint32_t *)w->codes,
-                       (uint16_t *)w->scales, nb);
+                       (const uint16_t *)((const uint8_t *)gguf + woff), (uint8_t *)w->codes,
+                       (uint16_t *)w->scales, nblk, nb);
     GD_LAUNCHED(ctx, "gd_repack_kernel");
+    return GD_OK;
+}
+
+extern "C" int gd_q2_0_export_rows(gd_ctx *ctx, const gd_q2w *w, int64_t row0, int64_t nrows,
+                                   void *gguf_out) {
+    GD_CHECK_CTX(ctx);
+    int rc = check_q2w(ctx, w, "gd_q2_0_export_rows");
+    if (rc) return rc;
+    GD_REQUIRE(ctx, gguf_out && ((uintptr_t)gguf_out & 1) == 0, "gd_q2_0_export_rows: bad output");
+    GD_REQUIRE(ctx, row0 >= 0 && nrows >= 0 && row0 + nrows <= w->R,
+               "gd_q2_0_export_rows: rows [%lld, %lld) outside [0, %lld)", (long long)row0,
+               (long long)(row0 + nrows), (long long)w->R);
+    const int64_t nblk = w->K / GD_Q2_0_QK, nb = nrows * nblk;
+    if (!nb) return GD_OK;
+    hipLaunchKernelGGL(gd_export_kernel, dim3(gd_blocks(nb, 256)), dim3(256), 0, ctx->stream,
+                       (const uint8_t *)w->codes, (const uint16_t *)w->scales,
+                       (uint16_t *)gguf_out, nblk, row0, nb);
+    GD_LAUNCHED(ctx, "gd_export_kernel");
     return GD_OK;
 }
 
@@ -333,13 +372,7 @@ extern "C" int gd_q2_0_export(gd_ctx *ctx, const gd_q2w *w, void *gguf_out) {
     GD_CHECK_CTX(ctx);
     int rc = check_q2w(ctx, w, "gd_q2_0_export");
     if (rc) return rc;
-    GD_REQUIRE(ctx, gguf_out && ((uintptr_t)gguf_out & 1) == 0, "gd_q2_0_export: bad output");
-    const int64_t nb = w->R * (w->K / GD_Q2_0_QK);
-    hipLaunchKernelGGL(gd_export_kernel, dim3(gd_blocks(nb, 256)), dim3(256), 0, ctx->stream,
-                       (const uint32_t *)w->codes, (const uint16_t *)w->scales,
-                       (uint16_t *)gguf_out, nb);
-    GD_LAUNCHED(ctx, "gd_export_kernel");
-    return GD_OK;
+    return gd_q2_0_export_rows(ctx, w, 0, w->R, gguf_out);
 }
 
 extern "C" int gd_q2_0_upload(gd_ctx *ctx, const void *host_blocks, int64_t K, int64_t R,
@@ -412,13 +445,14 @@ __global__ void gd_rand_normal_kernel(void *out, int dtype, size_t n, uint64_t s
     }
 }
 
-// Codes: one thread per 64 weights (16 code bytes) of the flattened [R][K]
-// matrix; weight e uses element e of stream s0.
-__global__ void gd_rand_codes_kernel(uint32_t *codes, size_t nweights, uint64_t s0) {
+// Codes: one thread per 64 weights (16 code bytes, half a block) of the
+// flattened [R][K] matrix; weight e uses element e of stream s0.
+__global__ void gd_rand_codes_kernel(uint8_t *codes, int64_t K, size_t nweights, uint64_t s0) {
     const size_t e0 = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 64;
     if (e0 >= nweights) return;
     uint64_t s = gd_lcg_skip(s0, e0);
-    uint32_t *dst = codes + e0 / 16;
+    const int64_t row = (int64_t)(e0 / (size_t)K), k0 = (int64_t)(e0 % (size_t)K);
+    u32x4 v;
 #pragma unroll
     for (int w = 0; w < 4; w++) {
         uint32_t word = 0;
@@ -428,19 +462,23 @@ __global__ void gd_rand_codes_kernel(uint32_t *codes, size_t nweights, uint64_t 
             const uint32_t c = (uint32_t)(((uint64_t)lcg_bits(s) * 3u) >> 31);
             word |= c << (2 * j);
         }
-        dst[w] = word;
+        v[w] = word;
     }
+    *(u32x4 *)(codes + gd_q2_code_off(row, k0 >> 7, (int)((k0 >> 6) & 1), gd_q2_steps(K))) = v;
 }
 
-__global__ void gd_rand_scales_kernel(uint16_t *scales, size_t n, uint64_t s0, float lo,
-                                      float span) {
+// Scales: element i of the stream is block i of the flattened [R][K/128] grid.
+__global__ void gd_rand_scales_kernel(uint16_t *scales, int64_t nblk, size_t n, uint64_t s0,
+                                      float lo, float span) {
     const size_t i0 = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * GD_RAND_RUN;
     if (i0 >= n) return;
     uint64_t s = gd_lcg_skip(s0, i0);
+    const int64_t bgroups = (nblk + 15) / 16;
     for (size_t i = i0; i < i0 + GD_RAND_RUN && i < n; i++) {
         s = s * GD_LCG_A + GD_LCG_C;
         const float u = (float)lcg_bits(s) * 0x1p-31f;
-        scales[i] = gd_f2h(lerp_unfused(lo, span, u));
+        const int64_t row = (int64_t)(i / (size_t)nblk), blk = (int64_t)(i % (size_t)nblk);
+        scales[gd_q2_scale_idx(row, blk, bgroups)] = gd_f2h(lerp_unfused(lo, span, u));
     }
 }
 
@@ -477,13 +515,13 @@ extern "C" int gd_rand_q2w(gd_ctx *ctx, gd_q2w *w, uint64_t seed, float lo, floa
     if (rc) return rc;
     const size_t nw = (size_t)(w->R * w->K);       // multiple of 128
     hipLaunchKernelGGL(gd_rand_codes_kernel, dim3(gd_blocks(nw / 64, 256)), dim3(256), 0,
-                       ctx->stream, (uint32_t *)w->codes, nw, stream_start(seed));
+                       ctx->stream, (uint8_t *)w->codes, w->K, nw, stream_start(seed));
     GD_LAUNCHED(ctx, "gd_rand_codes");
     const size_t ns = nw / GD_Q2_0_QK;
     const size_t threads = (ns + GD_RAND_RUN - 1) / GD_RAND_RUN;
     hipLaunchKernelGGL(gd_rand_scales_kernel, dim3(gd_blocks(threads, 256)), dim3(256), 0,
-                       ctx->stream, (uint16_t *)w->scales, ns, stream_start(seed + 1), lo,
-                       hi - lo);
+                       ctx->stream, (uint16_t *)w->scales, w->K / GD_Q2_0_QK, ns,
+                       stream_start(seed + 1), lo, hi - lo);
     GD_LAUNCHED(ctx, "gd_rand_scales");
     return GD_OK;
 }

@@ -445,15 +445,6 @@ int f32_make(gd_stack *st, int64_t n, uint64_t seed, float lo, float hi, float *
     return gd_rand_uniform(st->ctx, *p, (size_t)n, seed, lo, hi);
 }
 
-gd_q2w rows_of(const gd_q2w &w, int64_t r0, int64_t r1) {
-    gd_q2w s;
-    s.codes = (uint8_t *)w.codes + r0 * (w.K / 4);
-    s.scales = (uint16_t *)w.scales + r0 * (w.K / 128);
-    s.K = w.K;
-    s.R = r1 - r0;
-    return s;
-}
-
 // One chunk of N tokens whose embeddings are already in st->x (f32 [N][E]):
 // the layer stack, the final norm and the last token's logits + greedy pick.
 // Positions come from st->dpos.  `decode` selects the single-token kernels.
@@ -765,13 +756,19 @@ extern "C" int gd_stack_position(gd_stack *st, int64_t *pos) {
     return GD_OK;
 }
 
-extern "C" int gd_stack_tensor(gd_stack *st, int layer, const char *name, gd_q2w *w, float **f32,
-                               int64_t *count) {
+extern "C" int gd_stack_tensor(gd_stack *st, int layer, const char *name, gd_q2w *w,
+                               int64_t *row0, float **f32, int64_t *count) {
     if (!st || !name) return GD_EINVAL;
     gd_ctx *ctx = st->ctx;
     const std::string n(name);
     const gd_stack_config &c = st->c;
-    auto q = [&](const gd_q2w &m) { if (w) *w = m; return GD_OK; };
+    // Rows [r0, r1) of matrix m.
+    auto q = [&](const gd_q2w &m, int64_t r0 = 0, int64_t r1 = -1) {
+        if (w) *w = m;
+        if (row0) *row0 = r0;
+        if (count) *count = (r1 < 0 ? m.R : r1) - r0;
+        return GD_OK;
+    };
     auto f = [&](float *p, int64_t cnt) {
         if (f32) *f32 = p;
         if (count) *count = cnt;
@@ -786,15 +783,15 @@ extern "C" int gd_stack_tensor(gd_stack *st, int layer, const char *name, gd_q2w
     StackLayer &ly = st->L[layer];
     if (n == "attn_norm") return f(ly.attn_norm, c.n_embd);
     if (n == "post_attention_norm") return f(ly.post_norm, c.n_embd);
-    if (n == "ffn_gate") return q(rows_of(ly.gate_up, 0, c.n_ff));
-    if (n == "ffn_up") return q(rows_of(ly.gate_up, c.n_ff, 2 * (int64_t)c.n_ff));
+    if (n == "ffn_gate") return q(ly.gate_up, 0, c.n_ff);
+    if (n == "ffn_up") return q(ly.gate_up, c.n_ff, 2 * (int64_t)c.n_ff);
     if (n == "ffn_down") return q(ly.down);
     if (ly.rec) {
         const int cd = st->convDim, vd = st->valDim, nv = c.n_v_head;
-        if (n == "attn_qkv") return q(rows_of(ly.in_proj, 0, cd));
-        if (n == "attn_gate") return q(rows_of(ly.in_proj, cd, cd + vd));
-        if (n == "ssm_beta") return q(rows_of(ly.in_proj, cd + vd, cd + vd + nv));
-        if (n == "ssm_alpha") return q(rows_of(ly.in_proj, cd + vd + nv, cd + vd + 2 * nv));
+        if (n == "attn_qkv") return q(ly.in_proj, 0, cd);
+        if (n == "attn_gate") return q(ly.in_proj, cd, cd + vd);
+        if (n == "ssm_beta") return q(ly.in_proj, cd + vd, cd + vd + nv);
+        if (n == "ssm_alpha") return q(ly.in_proj, cd + vd + nv, cd + vd + 2 * nv);
         if (n == "ssm_out") return q(ly.out_proj);
         if (n == "ssm_conv1d") return f(ly.conv_w, (int64_t)cd * 4);
         if (n == "ssm_dt") return f(ly.dt, nv);
@@ -804,9 +801,9 @@ extern "C" int gd_stack_tensor(gd_stack *st, int layer, const char *name, gd_q2w
         if (n == "ssm_state") return f(ly.rec_state, (int64_t)nv * HD * HD);
     } else {
         const int qf = 2 * c.n_head * HD, kv = c.n_head_kv * HD;
-        if (n == "attn_q") return q(rows_of(ly.in_proj, 0, qf));
-        if (n == "attn_k") return q(rows_of(ly.in_proj, qf, qf + kv));
-        if (n == "attn_v") return q(rows_of(ly.in_proj, qf + kv, qf + 2 * kv));
+        if (n == "attn_q") return q(ly.in_proj, 0, qf);
+        if (n == "attn_k") return q(ly.in_proj, qf, qf + kv);
+        if (n == "attn_v") return q(ly.in_proj, qf + kv, qf + 2 * kv);
         if (n == "attn_output") return q(ly.out_proj);
         if (n == "attn_q_norm") return f(ly.q_norm, HD);
         if (n == "attn_k_norm") return f(ly.k_norm, HD);

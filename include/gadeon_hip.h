@@ -105,20 +105,25 @@ int gd_q2_0_unpack(const uint8_t *blocks, size_t n, uint8_t *codes,
                    uint16_t *scales);
 
 /* ---- Q2_0 device weights ---------------------------------------------------
- * On the device a Q2_0 matrix [R][K] is held as two planes, the layout the
- * MI355X kernels stream: codes[R][K/4] (each block's qs[32] bytes, rows
- * contiguous) and scales[R][K/128] (f16).  Same 2.125 bits per weight as the
- * GGUF blocks.  Reference weights arrive as GGUF bytes (GGUF.swift:107-117)
- * and are repacked once at upload, where MetalContext wraps the mmap without
- * a copy (MetalContext.swift:193-212). */
+ * On the device a Q2_0 matrix [R][K] is held as two planes in the layout the
+ * MI355X kernels stream, with the same 2.125 bits per weight as the GGUF
+ * blocks (plus zero padding of R to a multiple of 16 and K/128 blocks to a
+ * multiple of 4):
+ *   codes:  2 KiB tiles of 16 rows x 512 K, each the exact matrix-core
+ *           operand order of one wave (one contiguous 1 KiB per load);
+ *   scales: f16, the 16 rows of a block contiguous.
+ * The layout is internal: weights enter through gd_q2_0_repack/upload and
+ * leave through gd_q2_0_export(_rows).  Reference weights arrive as GGUF
+ * bytes (GGUF.swift:107-117) and are repacked once at upload, where
+ * MetalContext wraps the mmap without a copy (MetalContext.swift:193-212). */
 typedef struct gd_q2w {
-    void *codes;    /* device, R*K/4 bytes, 16-byte aligned rows            */
-    void *scales;   /* device, R*K/128 f16                                  */
+    void *codes;    /* device, ceil(R/16)*ceil(K/512)*2048 bytes, 256-aligned */
+    void *scales;   /* device, ceil(R/16)*ceil(K/2048)*256 f16, 8-aligned     */
     int64_t K;      /* reduction length, multiple of 128                   */
     int64_t R;      /* output rows                                          */
 } gd_q2w;
 
-/* Allocate the two planes of a K x R matrix (caller frees via gd_q2w_free). */
+/* Allocate the two zeroed planes of a K x R matrix (free with gd_q2w_free). */
 int gd_q2w_alloc(gd_ctx *ctx, int64_t K, int64_t R, gd_q2w *w);
 int gd_q2w_free(gd_ctx *ctx, gd_q2w *w);
 /* Repack R rows of GGUF Q2_0 blocks already in device memory (at byte offset
@@ -129,6 +134,10 @@ int gd_q2_0_upload(gd_ctx *ctx, const void *host_blocks, int64_t K, int64_t R,
                    gd_q2w *w);
 /* Device planes -> GGUF blocks in device memory (inverse of repack). */
 int gd_q2_0_export(gd_ctx *ctx, const gd_q2w *w, void *gguf_out);
+/* Rows [row0, row0+nrows) of w -> nrows*K/128 GGUF blocks in device memory
+ * (one tensor of a fused projection, as GGUF stores it). */
+int gd_q2_0_export_rows(gd_ctx *ctx, const gd_q2w *w, int64_t row0, int64_t nrows,
+                        void *gguf_out);
 
 /* ---- Q2_0 GEMV (decode): MetalEnc.gemv, MetalEnc.swift:78-99 -----------------
  * y[r] = sum_k W[r,k] * x[k] for r < R, f32 accumulate, f32 out.
@@ -315,15 +324,17 @@ int gd_stack_generate(gd_stack *st, int n, int32_t *tokens);
 int gd_stack_request_stop(gd_stack *st);
 
 /* Weight and state introspection for parity tests: tensor `name` of layer
- * `layer` (-1 for global tensors).  Q2_0 tensors fill *w; f32 tensors fill
- * *f32 and *count.  Names follow the GGUF ones used in Model.swift:100-145
+ * `layer` (-1 for global tensors).  A Q2_0 tensor fills *w with the matrix
+ * that holds it (projections that read the same input are fused into one
+ * matrix), *row0 with its first row there and *count with its row count
+ * (read it with gd_q2_0_export_rows); f32 tensors fill *f32 and *count.  Names follow the GGUF ones used in Model.swift:100-145
  * ("attn_norm", "attn_qkv", "attn_gate", "ssm_beta", "ssm_alpha", "ssm_dt",
  * "ssm_a", "ssm_conv1d", "ssm_norm", "ssm_out", "attn_q", "attn_k", "attn_v",
  * "attn_output", "attn_q_norm", "attn_k_norm", "post_attention_norm",
  * "ffn_gate", "ffn_up", "ffn_down", "token_embd", "output_norm",
  * "ssm_conv_state", "ssm_state"). */
 int gd_stack_tensor(gd_stack *st, int layer, const char *name, gd_q2w *w,
-                    float **f32, int64_t *count);
+                    int64_t *row0, float **f32, int64_t *count);
 int gd_stack_position(gd_stack *st, int64_t *pos);
 
 #ifdef __cplusplus
