@@ -3,72 +3,75 @@
 // Same result as q2_0_gemv (Kernels.metal:30-119) and Q2_0.matvec
 // (Quant.swift:36-77): per block d * (sum(code*x) - sum(x)), f32 throughout.
 //
-// MI355X design.  v_mfma_f32_16x16x32_f16 multiplies 16 weight rows by 32
-// K-values per instruction; the VALU only unpacks codes:
+// MI355X design.  v_mfma_f32_4x4x4f16 (16 independent 4x4x4 products per
+// instruction) does the multiply-adds; the VALU only unpacks codes.
 //   * A operand: the weights are stored in 2 KiB tiles (16 rows x 512 K) in
-//     the order the 64 lanes need them: lane (row l%16, K-group l/16) reads
-//     one Q2_0 block (32 code bytes) of its row as two 16-byte loads, at
-//     lane*16 and 1024 + lane*16, so every load instruction of a wave is one
-//     contiguous 1 KiB.  Codes k and k+8 of a code dword are shifted onto bits
-//     8-9 of the two f16 halves and masked: the halves are exactly c * 2^-16
-//     (f16 subnormals, which the matrix cores take at full precision), 15
-//     VALU ops per 16 weights.
-//   * B operand: the single x column is placed in output column (block % 16):
-//     lane (column j, K-group) holds x only when j is its block's slot, else
-//     zeros.  Sixteen consecutive blocks therefore accumulate in sixteen
-//     different output columns, and each column is scaled by its own block
-//     scale d once per 16 blocks ("drain"), where sum(x) of the block is
-//     subtracted as well.  x is staged once per workgroup in LDS, already
-//     permuted into the (k, k+8) pair order of the unpack, with a zero block
-//     for the non-matching lanes.  f32 x is split exactly enough into
-//     hi = f16(x) and lo = f16((x - hi) * 2^11), two B operands accumulated
-//     apart and recombined in f32 at the drain.
+//     the order the 64 lanes need them: lane l holds one Q2_0 block (32 code
+//     bytes) of row l%16, block l/16 of the step, read as two 16-byte loads
+//     at lane*16 and 1024 + lane*16, so every load instruction of a wave is
+//     one contiguous 1 KiB.  As a 4x4x4 lane, l is row l%4 of MFMA block
+//     l/4: MFMA block m covers rows 4*(m%4) .. 4*(m%4)+3 of Q2 block m/4.
+//     Codes k and k+8 of a code dword land in the two f16 halves of an
+//     operand dword by a mask alone (codes 2, 3, 4 sit at bits 4, 6, 8), or
+//     by a mask after one of two shared shifts (w << 4 for codes 0, 1; w >> 6
+//     for 5, 6, 7): ten VALU ops per 16 weights.  A half is then exactly
+//     c * 2^(p-24) for bit position p (an f16 subnormal), and the x it meets
+//     is staged pre-scaled by 2^(8-p), so every product is c * x * 2^-16.
+//     Positions below 4 are not used: the matrix cores lose precision on
+//     those subnormals (measured), while 4, 6 and 8 stay within about 1e-6
+//     of the exact sum.  A block whose x would overflow f16 after the x16
+//     pre-scale is staged scaled down by a power of two 2^-e, undone later.
+//   * B operand: each MFMA block has four output columns; at chunk step s the
+//     x of its Q2 block goes into column s % 4 and the other columns get
+//     zeros, so four consecutive steps accumulate in four columns and each
+//     is scaled by its own block scale d once per four steps ("drain"),
+//     where sum(x) of the block is subtracted as well.  x is staged once per
+//     workgroup in LDS, already permuted into the (k, k+8) pair order of the
+//     unpack and pre-scaled, with zero blocks for the other columns.  f32 x
+//     is split into hi = f16(x) and lo = f16((x - hi) * 2^11), two B operands
+//     accumulated apart and recombined in f32 at the drain.
 //   * Work split.  A "set" is one 16-row group; an "item" is one tile (one
 //     chunk step of 512 K of one set).  Every workgroup gets the same number
-//     of consecutive sets, and its four waves split the workgroup's items
-//     into four equal contiguous ranges, so no wave waits on a longer one.
-//     A set that one wave covers whole is written by that wave; a set cut by
-//     a range boundary is summed in LDS after one barrier, in wave order (the
-//     result does not depend on timing).
+//     of consecutive sets, and its NW waves split the workgroup's items into
+//     NW equal contiguous ranges.  A set that one wave covers whole goes to
+//     the workgroup's LDS results directly; a set cut by a range boundary is
+//     summed after one barrier, in wave order (the result does not depend on
+//     timing); the rows go out as one coalesced store at the end.
 //   * Latency.  Each wave keeps the next P tiles in flight (a register ring),
-//     and the four scales of a drain (one 8-byte load) are fetched with the
-//     first tile of its group, so no load waits in the loop.
+//     each with the four scales its drain needs (one 8-byte load).  Tiles,
+//     scales and x are read with bounds-checked buffer loads: a load past
+//     the end returns zeros without a memory access, so every load in the
+//     main loop is unconditional and the compiler waits only for the tile an
+//     item needs.  x is requested before the tiles (loads return in order).
 #include "gd_internal.h"
 
 namespace {
 
-constexpr int MT = 256;
-constexpr int P = 2;
+constexpr int XB = 68;    // LDS dwords per staged x block
+// Dynamic LDS available beside the static reduction array (16 waves).
+constexpr size_t LDS_BYTES = 160 * 1024 - 2048;
 
+// Operand dword m holds codes (m, m+8) of w at bit position POS[m] of its
+// two f16 halves; the x pair it meets is pre-scaled by XSCALE[m] = 2^(8-POS[m]).
 __device__ __forceinline__ void unpack_dword(uint32_t w, uint32_t (&t)[8]) {
-    constexpr uint32_t M = 0x03000300u;
-    t[0] = (w << 8) & M;
-    t[1] = (w << 6) & M;
-    t[2] = (w << 4) & M;
-    t[3] = (w << 2) & M;
-    t[4] = w & M;
-    t[5] = (w >> 2) & M;
-    t[6] = (w >> 4) & M;
-    t[7] = (w >> 6) & M;
+    constexpr uint32_t M4 = 0x00300030u, M6 = 0x00C000C0u, M8 = 0x03000300u;
+    const uint32_t u = w << 4, v = w >> 6;
+    t[0] = u & M4;     // code 0 at bit 4
+    t[1] = u & M6;     // code 1 at bit 6
+    t[2] = w & M4;     // code 2 at bit 4
+    t[3] = w & M6;     // code 3 at bit 6
+    t[4] = w & M8;     // code 4 at bit 8
+    t[5] = v & M4;     // code 5 at bit 4
+    t[6] = v & M6;     // code 6 at bit 6
+    t[7] = v & M8;     // code 7 at bit 8
 }
+__device__ constexpr float XSCALE[8] = {16.f, 4.f, 16.f, 4.f, 1.f, 16.f, 4.f, 1.f};
 
 __device__ __forceinline__ f16x8 as_f16x8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
     return __builtin_bit_cast(f16x8, u32x4{a, b, c, d});
 }
 
-// Pairs (x[16i+k], x[16i+k+8]), k = 0..7, of 16 consecutive f16 values held
-// as lo = x[16i..16i+7], hi = x[16i+8..16i+15].
-__device__ __forceinline__ void make_pairs(const u32x4 &lo, const u32x4 &hi, u32x4 &p0,
-                                           u32x4 &p1) {
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const uint32_t l0 = lo[k >> 1], h0 = hi[k >> 1];
-        const uint32_t l1 = lo[2 + (k >> 1)], h1 = hi[2 + (k >> 1)];
-        p0[k] = (k & 1) ? ((l0 >> 16) | (h0 & 0xffff0000u)) : ((l0 & 0xffffu) | (h0 << 16));
-        p1[k] = (k & 1) ? ((l1 >> 16) | (h1 & 0xffff0000u)) : ((l1 & 0xffffu) | (h1 << 16));
-    }
-}
-
+// Two f32 -> two f16 (RNE) in one dword.
 __device__ __forceinline__ uint32_t pack_h2(float a, float b) {
     return (uint32_t)gd_f2h(a) | ((uint32_t)gd_f2h(b) << 16);
 }
@@ -81,267 +84,373 @@ struct Cursor {
     }
 };
 
-// XT: 0 = f16 x, 1 = f32 x (hi + lo split).
-template <int XT>
-__global__ __launch_bounds__(MT) void q2_0_gemv_mfma_kernel(
+// Buffer resource over `bytes` bytes at p (raw: no stride).  Loads at an
+// offset past the end return zeros without touching memory, which keeps
+// every load of the main loop unconditional.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes,
+                                             0x00020000);
+}
+constexpr int CP_NT = 2;   // cache policy: non-temporal (streamed once)
+
+// x values of one staging entry (16 consecutive elements of one block).
+template <int XT> struct XChunk;
+template <> struct XChunk<0> { u32x4 lo, hi; };
+template <> struct XChunk<1> { f32x4 f[4]; };
+
+// XT: 0 = f16 x, 1 = f32 x (hi + lo split).  NW waves per workgroup.
+template <int XT, int NW, int P>
+__global__ __launch_bounds__(64 * NW) void q2_0_gemv_mfma_kernel(
         const uint8_t *__restrict__ codes, const uint16_t *__restrict__ scales,
         const void *__restrict__ xv, float *__restrict__ y, int K, int R, int nsets,
         int sets_per_wg) {
+    constexpr int MT = 64 * NW;
     extern __shared__ uint32_t lds[];
     const int nblk = K >> 7;
-    const int xstride = (nblk + 1) * 64;                   // dwords per x plane
-    uint32_t *xp = lds;                                    // [(nblk + 1)][64] x pairs (hi)
+    // LDS: x planes, block b at dword XB*b (64 pair dwords + 4 of padding, so
+    // the blocks one load instruction reads start on different banks), then
+    // two zero blocks four blocks apart (see zero_blk below); per-block sum
+    // and exponent of x; the workgroup's row results.
+    const int xstride = (nblk + 5) * XB;                   // dwords per x plane
+    uint32_t *xp = lds;                                    // hi (or f16) pairs
     uint32_t *xq = lds + xstride;                          // lo plane (f32 x only)
     float *sx = (float *)(lds + (XT ? 2 : 1) * xstride);   // [nblk] block sums of x
-    __shared__ float red[4][2][16];                        // partial sums of cut sets
+    float *ex = sx + nblk;                                 // [nblk] 2^(16+e_b)
+    float *ysum = ex + nblk;                               // [sets_per_wg * 16]
+    __shared__ float red[NW][2][16];                       // partial sums of cut sets
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int col = lane & 15, kg = lane >> 4;
+    // Lane l holds row l%16 of Q2 block l/16 of a step (the tile order); as
+    // a 4x4x4 MFMA lane it is row / column j = l%4 of MFMA block l/4, which
+    // covers rows 4*rq .. 4*rq+3 (rq = l/4 % 4) of Q2 block kb = l/16.
+    const int j = lane & 3, rq = (lane >> 2) & 3, kb = lane >> 4;
     const int steps = (nblk + 3) >> 2;
     const int bgroups = (nblk + 15) >> 4;
 
     const int set_lo = blockIdx.x * sets_per_wg;
     const int nset_wg = min(sets_per_wg, nsets - set_lo);
     const int total = nset_wg * steps;
-    const int a = total * wave / 4, b = total * (wave + 1) / 4;
+    const int a = total * wave / NW, b = total * (wave + 1) / NW;
     const int nitems = b - a;
 
-    // Loads of item `ld`: its tile, and at a group start (the first step of
-    // 4, or the wave's first item) the scales its drain will use: rows
-    // 4*kg .. 4*kg+3 of block 16*(s/4) + col.
-    auto load = [&](const Cursor &ld, bool first, u32x4 (&cw)[2], u32x2 &sc) {
-        const size_t set = (size_t)(set_lo + ld.set);
-        const u32x4 *t = (const u32x4 *)(codes + ((set * steps + ld.s) << 11)) + lane;
-        cw[0] = __builtin_nontemporal_load(t);
-        cw[1] = __builtin_nontemporal_load(t + 64);
-        if ((ld.s & 3) == 0 || first)
-            sc = *(const u32x2 *)(scales + (((set * bgroups + (ld.s >> 2)) * 16 + col) * 16 + 4 * kg));
+    // Staging entry e = (block e/8, chunk e%8): its x loads are issued before
+    // the tile prefetch, so waiting for them leaves the tiles in flight.
+    const int nstage = (nblk + 5) * 8;
+    // Entries past the last x block (the zero blocks, and threads with no
+    // entry) read past the end of x: zeros, without a memory access.
+    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(xv, (uint32_t)K * (XT ? 4u : 2u));
+    auto load_x = [&](int e) {
+        const int off = e < nblk * 8 ? (e >> 3) * 128 + 16 * (e & 7) : K;   // element offset
+        XChunk<XT> c;
+        if constexpr (XT == 0) {
+            c.lo = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, off * 2, 0, 0));
+            c.hi = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, off * 2 + 16, 0, 0));
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                c.f[q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, off * 4 + 16 * q, 0, 0));
+        }
+        return c;
+    };
+    XChunk<XT> xc = load_x(threadIdx.x);
+    // Keep the x loads ahead of the tile prefetch in the instruction stream:
+    // loads complete in issue order, so x issued after the tiles would only
+    // arrive behind them.
+    __builtin_amdgcn_sched_barrier(0);
+
+    // The wave's items are consecutive tiles (tiles of consecutive sets are
+    // contiguous): item i is tile (set_lo * steps + a + i).  Loads past the
+    // wave's range, or scales past the workgroup's sets, return zeros.
+    const __amdgpu_buffer_rsrc_t trs =
+            make_rsrc(codes + ((size_t)set_lo * steps + a) * 2048, (uint32_t)nitems * 2048u);
+    const __amdgpu_buffer_rsrc_t srs =
+            make_rsrc(scales + (size_t)set_lo * bgroups * 256, (uint32_t)nset_wg * bgroups * 512u);
+    // Loads of item `it` (at cursor `ld`): its tile and the scales of its
+    // drain group that this lane's column needs: rows 4*rq .. 4*rq+3 of
+    // block 16*(s/4) + 4*j + kb.
+    auto load = [&](int it, const Cursor &ld, u32x4 (&cw)[2], u32x2 &sc) {
+        const int off = it * 2048 + lane * 16;
+        cw[0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(trs, off, 0, CP_NT));
+        cw[1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(trs, off + 1024, 0, CP_NT));
+        const int si = ((ld.set * bgroups + (ld.s >> 2)) * 16 + 4 * j + kb) * 16 + 4 * rq;
+        sc = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(srs, si * 2, 0, 0));
     };
 
+    // One tile goes out before the staging; the rest of the ring after it,
+    // so x (needed first) does not queue behind the whole grid's prefetch.
     u32x4 ring[P][2];
     u32x2 rsc[P];
     Cursor ld{a / steps, a % steps};
-#pragma unroll
-    for (int p = 0; p < P; p++) {
-        if (p < nitems) load(ld, p == 0, ring[p], rsc[p]);
-        ld.next(steps);
-    }
+    load(0, ld, ring[0], rsc[0]);
+    ld.next(steps);
 
-    // Stage x (all threads, while the first tiles are in flight): pair
-    // p = 8i + k of block b holds (x[b,16i+k], x[b,16i+k+8]).  Thread (b, i)
-    // loads x[16i .. 16i+15] of block b, forms its 8 pairs in registers and
-    // writes them as 32 bytes; block sums come from an 8-lane shuffle sum.
-    for (int e = threadIdx.x; e < (nblk + 1) * 8; e += MT) {
+    // Stage x: pair p = 8i + k of block b holds (x[b,16i+k], x[b,16i+k+8]) *
+    // XSCALE[k] * 2^-e_b.  Thread (b, i) forms the 8 pairs of x[16i ..
+    // 16i+15] in registers and writes them as 32 bytes; the block's sum and
+    // max|x| come from 8-lane shuffles.  e_b = 0 unless max|x| >= 2048.
+    auto stage = [&](const int e, const XChunk<XT> &xc) {
         const int bb = e >> 3, i = e & 7;
-        float sum = 0.f;
-        u32x4 p0, p1;
-        if (XT == 0) {
-            u32x4 lo = u32x4{0u, 0u, 0u, 0u}, hi = lo;
-            if (bb < nblk) {
-                const u32x4 *src = (const u32x4 *)((const uint16_t *)xv + (size_t)bb * 128 + 16 * i);
-                lo = src[0];
-                hi = src[1];
-            }
-            make_pairs(lo, hi, p0, p1);
+        float sum = 0.f, amax = 0.f;
+        f32x4 f[4];
+        if constexpr (XT == 0) {
 #pragma unroll
-            for (int k = 0; k < 4; k++) {
-                sum += gd_h2f((uint16_t)(lo[k] & 0xffff)) + gd_h2f((uint16_t)(lo[k] >> 16));
-                sum += gd_h2f((uint16_t)(hi[k] & 0xffff)) + gd_h2f((uint16_t)(hi[k] >> 16));
+            for (int q = 0; q < 8; q++) {
+                const uint32_t d = q < 4 ? xc.lo[q] : xc.hi[q - 4];
+                f[q >> 1][2 * (q & 1)] = gd_h2f((uint16_t)(d & 0xffff));
+                f[q >> 1][2 * (q & 1) + 1] = gd_h2f((uint16_t)(d >> 16));
             }
         } else {
-            f32x4 f[4] = {};
-            if (bb < nblk) {
-                const f32x4 *src = (const f32x4 *)((const float *)xv + (size_t)bb * 128 + 16 * i);
 #pragma unroll
-                for (int q = 0; q < 4; q++) f[q] = src[q];
-            }
-            u32x4 hl, hh, ll, lh;                 // hi/lo halves of x[0..7], x[8..15]
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const float x0 = f[q >> 1][2 * (q & 1)], x1 = f[q >> 1][2 * (q & 1) + 1];
-                const float y0 = f[2 + (q >> 1)][2 * (q & 1)], y1 = f[2 + (q >> 1)][2 * (q & 1) + 1];
-                const float hx0 = (float)(f16)x0, hx1 = (float)(f16)x1;
-                const float hy0 = (float)(f16)y0, hy1 = (float)(f16)y1;
-                hl[q] = pack_h2(x0, x1);
-                hh[q] = pack_h2(y0, y1);
-                ll[q] = pack_h2((x0 - hx0) * 0x1p11f, (x1 - hx1) * 0x1p11f);
-                lh[q] = pack_h2((y0 - hy0) * 0x1p11f, (y1 - hy1) * 0x1p11f);
-                sum += (x0 + x1) + (y0 + y1);
-            }
-            u32x4 q0, q1;
-            make_pairs(hl, hh, p0, p1);
-            make_pairs(ll, lh, q0, q1);
-            u32x4 *dq = (u32x4 *)(xq + bb * 64 + 8 * i);
-            dq[0] = q0;
-            dq[1] = q1;
+            for (int q = 0; q < 4; q++) f[q] = xc.f[q];
         }
-        u32x4 *dst = (u32x4 *)(xp + bb * 64 + 8 * i);
-        dst[0] = p0;
-        dst[1] = p1;
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                sum += f[q][j];
+                amax = fmaxf(amax, fabsf(f[q][j]));
+            }
         sum += __shfl_xor(sum, 1, 64);
         sum += __shfl_xor(sum, 2, 64);
         sum += __shfl_xor(sum, 4, 64);
-        if (i == 0 && bb < nblk) sx[bb] = sum;
+        amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+        amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+        amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+        // amax < 2^(E-126) for f32 exponent field E; amax * 16 * 2^-eb < 2^15.
+        const int eb = min(111, max(0, (int)((__float_as_uint(amax) >> 23) & 0xff) - 137));
+        const float down = __uint_as_float((uint32_t)(127 - eb) << 23);    // 2^-eb
+        u32x4 p0, p1, q0, q1;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            // pair k = (x[16i+k], x[16i+k+8]) = (f[k/4][k%4], f[2+k/4][k%4])
+            const float xa = f[k >> 2][k & 3] * down, xb = f[2 + (k >> 2)][k & 3] * down;
+            const float ha = (float)(f16)xa, hb = (float)(f16)xb;
+            const uint32_t hp = pack_h2(ha * XSCALE[k], hb * XSCALE[k]);
+            if (k < 4) p0[k] = hp; else p1[k - 4] = hp;
+            if (XT) {
+                const uint32_t lp = pack_h2((xa - ha) * (0x1p11f * XSCALE[k]),
+                                            (xb - hb) * (0x1p11f * XSCALE[k]));
+                if (k < 4) q0[k] = lp; else q1[k - 4] = lp;
+            }
+        }
+        if (e < nstage) {
+            u32x4 *dst = (u32x4 *)(xp + bb * XB + 8 * i);
+            dst[0] = p0;
+            dst[1] = p1;
+            if (XT) {
+                u32x4 *dq = (u32x4 *)(xq + bb * XB + 8 * i);
+                dq[0] = q0;
+                dq[1] = q1;
+            }
+            if (i == 0 && bb < nblk) {
+                sx[bb] = sum;
+                ex[bb] = __uint_as_float((uint32_t)(127 + 16 + eb) << 23);   // 2^(16+eb)
+            }
+        }
+    };
+    // The first entry is straight-line code after the tile prefetch, so its
+    // wait for x leaves the tiles in flight; further entries (K long enough
+    // that (K/128 + 5) * 8 > threads) follow in a loop.
+    stage(threadIdx.x, xc);
+    for (int e = threadIdx.x + MT; e < nstage; e += MT) stage(e, load_x(e));
+#pragma unroll
+    for (int p = 1; p < P; p++) {
+        load(p, ld, ring[p], rsc[p]);
+        ld.next(steps);
     }
     __syncthreads();
 
-    f32x4 C = f32x4{0.f, 0.f, 0.f, 0.f}, D = C, C2 = C, D2 = C;
-    float yp[4] = {0.f, 0.f, 0.f, 0.f}, dsc[4] = {0.f, 0.f, 0.f, 0.f};
+    // Accumulator chains: f16 x uses four, f32 x two for hi and two for lo.
+    f32x4 acc[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float yp[4] = {0.f, 0.f, 0.f, 0.f};
     Cursor cur{a / steps, a % steps};
     int dlo = cur.s;                                      // first step of the open group
-    for (int base = 0; base < nitems; base += P) {
+    // One item: ring slot p holds its tile and scales.
+    auto step = [&](const int item, u32x4 (&tile)[2], u32x2 &sc) {
+        const int s = cur.s;
+        if ((s & 3) == 0 || item == 0) dlo = s;
+        // MFMA block mb = lane/4 multiplies rows 4*rq .. 4*rq+3 of Q2 block
+        // 4s + kb by four K values; column j of its B is x when j == s % 4.
+        const int blk = 4 * s + kb;
+        const bool match = j == (s & 3) && blk < nblk;
+        // Zero block for the other lanes: of the two, the one whose LDS
+        // banks the four blocks of this step do not use.
+        const int zero_blk = ((s ^ (nblk >> 2)) & 1) ? nblk : nblk + 4;
+        const int xoff = (match ? blk : zero_blk) * XB;
+        const u32x4 *src = (const u32x4 *)(xp + xoff);
+        const u32x4 *srq = (const u32x4 *)(xq + xoff);
 #pragma unroll
-        for (int p = 0; p < P; p++) {
-            const int item = base + p;
-            if (item >= nitems) break;
-            const u32x4 cw0 = ring[p][0], cw1 = ring[p][1];
-            const u32x2 sc = rsc[p];
-            if (item + P < nitems) load(ld, false, ring[p], rsc[p]);
-            ld.next(steps);
-            const int s = cur.s;
-            if ((s & 3) == 0 || item == 0) {
-                dlo = s;
-                dsc[0] = gd_h2f((uint16_t)(sc[0] & 0xffff));
-                dsc[1] = gd_h2f((uint16_t)(sc[0] >> 16));
-                dsc[2] = gd_h2f((uint16_t)(sc[1] & 0xffff));
-                dsc[3] = gd_h2f((uint16_t)(sc[1] >> 16));
-            }
-            const int blk = 4 * s + kg;
-            const bool match = col == (blk & 15) && blk < nblk;
-            const int xoff = (match ? blk : nblk) * 64;
-            const u32x4 *src = (const u32x4 *)(xp + xoff);
-            const u32x4 *srq = (const u32x4 *)(xq + xoff);
-            // Independent accumulator chains, interleaved, so consecutive
-            // MFMAs do not wait on each other's results.
+        for (int d = 0; d < 8; d++) {
+            uint32_t t[8];
+            unpack_dword(tile[d >> 2][d & 3], t);
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                uint32_t t[8];
-                unpack_dword(i < 4 ? cw0[i] : cw1[i - 4], t);
-                const f16x8 a0 = as_f16x8(t[0], t[1], t[2], t[3]);
-                const f16x8 a1 = as_f16x8(t[4], t[5], t[6], t[7]);
-                C = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                        a0, __builtin_bit_cast(f16x8, src[2 * i]), C, 0, 0, 0);
-                D = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                        a1, __builtin_bit_cast(f16x8, src[2 * i + 1]), D, 0, 0, 0);
+            for (int q = 0; q < 2; q++) {
+                // Pairs 4q .. 4q+3 of chunk d: two MFMAs of four K values.
+                const u32x4 bx = src[2 * d + q];
+                const f16x4 a0 = __builtin_bit_cast(f16x4, u32x2{t[4 * q], t[4 * q + 1]});
+                const f16x4 a1 = __builtin_bit_cast(f16x4, u32x2{t[4 * q + 2], t[4 * q + 3]});
+                const int c0 = XT ? q : (2 * q) & 3, c1 = XT ? q : (2 * q + 1) & 3;
+                acc[c0] = __builtin_amdgcn_mfma_f32_4x4x4f16(
+                        a0, __builtin_bit_cast(f16x4, u32x2{bx[0], bx[1]}), acc[c0], 0, 0, 0);
+                acc[c1] = __builtin_amdgcn_mfma_f32_4x4x4f16(
+                        a1, __builtin_bit_cast(f16x4, u32x2{bx[2], bx[3]}), acc[c1], 0, 0, 0);
                 if (XT) {
-                    C2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                            a0, __builtin_bit_cast(f16x8, srq[2 * i]), C2, 0, 0, 0);
-                    D2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                            a1, __builtin_bit_cast(f16x8, srq[2 * i + 1]), D2, 0, 0, 0);
+                    const u32x4 bq = srq[2 * d + q];
+                    acc[2 + q] = __builtin_amdgcn_mfma_f32_4x4x4f16(
+                            a0, __builtin_bit_cast(f16x4, u32x2{bq[0], bq[1]}), acc[2 + q], 0, 0, 0);
+                    acc[2 + q] = __builtin_amdgcn_mfma_f32_4x4x4f16(
+                            a1, __builtin_bit_cast(f16x4, u32x2{bq[2], bq[3]}), acc[2 + q], 0, 0, 0);
                 }
             }
-            const bool set_end = s + 1 == steps;
-            const bool range_end = item + 1 == nitems;
-            if (((s + 1) & 3) == 0 || set_end || range_end) {
-                // Drain: column `col` holds block 16*(dlo/4) + col of the
-                // steps [dlo, s]; rows 4*kg + v.
-                const int bj = 16 * (dlo >> 2) + col;
-                const bool valid = bj >= 4 * dlo && bj < 4 * (s + 1) && bj < nblk;
-                const float sxj = sx[min(bj, nblk - 1)];
-#pragma unroll
-                for (int v = 0; v < 4; v++) {
-                    // The codes entered the MFMA as c * 2^-16 (and lo as x * 2^11).
-                    float cx = (C[v] + D[v]) * 0x1p16f;
-                    if (XT) cx += (C2[v] + D2[v]) * 0x1p5f;
-                    yp[v] += valid ? dsc[v] * (cx - sxj) : 0.f;
-                }
-                C = f32x4{0.f, 0.f, 0.f, 0.f};
-                D = C;
-                C2 = C;
-                D2 = C;
-            }
-            if (set_end || range_end) {
-                // Sum the 16 block columns of every row.  A set this wave
-                // covers whole goes straight to y; a cut one to LDS (slot 0
-                // if it began before this wave's range, else slot 1).
-                const int set_first = cur.set * steps;          // item index of s = 0
-                const bool whole = set_first >= a && set_first + steps <= b;
-                const int slot = set_first < a ? 0 : 1;
-                const int row_base = (set_lo + cur.set) * 16;
-#pragma unroll
-                for (int v = 0; v < 4; v++) {
-                    float acc = yp[v];
-                    acc += __shfl_xor(acc, 1, 64);
-                    acc += __shfl_xor(acc, 2, 64);
-                    acc += __shfl_xor(acc, 4, 64);
-                    acc += __shfl_xor(acc, 8, 64);
-                    const int r = 4 * kg + v;
-                    if (col == 0) {
-                        if (!whole) red[wave][slot][r] = acc;
-                        else if (row_base + r < R) y[row_base + r] = acc;
-                    }
-                    yp[v] = 0.f;
-                }
-            }
-            cur.next(steps);
         }
+        const bool set_end = s + 1 == steps;
+        const bool range_end = item + 1 == nitems;
+        if (((s + 1) & 3) == 0 || set_end || range_end) {
+            // Drain: column j holds step sj = 4*(dlo/4) + j of the group, i.e.
+            // block 4*sj + kb, for rows 4*rq + v.
+            const int sj = 4 * (dlo >> 2) + j, bj = 4 * sj + kb;
+            const bool valid = sj >= dlo && sj <= s && bj < nblk;
+            const float sxj = sx[min(bj, nblk - 1)], exj = ex[min(bj, nblk - 1)];
+            const float dsc[4] = {gd_h2f((uint16_t)(sc[0] & 0xffff)),
+                                  gd_h2f((uint16_t)(sc[0] >> 16)),
+                                  gd_h2f((uint16_t)(sc[1] & 0xffff)),
+                                  gd_h2f((uint16_t)(sc[1] >> 16))};
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                // Every product entered as c * x * 2^(-16-e_b) (lo with x 2^11).
+                const float cx = XT ? (acc[0][v] + acc[1][v]) + (acc[2][v] + acc[3][v]) * 0x1p-11f
+                                    : (acc[0][v] + acc[1][v]) + (acc[2][v] + acc[3][v]);
+                yp[v] += valid ? dsc[v] * (cx * exj - sxj) : 0.f;
+            }
+#pragma unroll
+            for (int c = 0; c < 4; c++) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+        if (set_end || range_end) {
+            // Sum each row over its 16 lanes (4 columns x 4 K-blocks).  A set
+            // this wave covers whole goes to the workgroup's results; a cut
+            // one to `red` (slot 0 if it began before this wave's range).
+            const int set_first = cur.set * steps;          // item index of s = 0
+            const bool whole = set_first >= a && set_first + steps <= b;
+            const int slot = set_first < a ? 0 : 1;
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                float r = yp[v];
+                r += __shfl_xor(r, 1, 64);
+                r += __shfl_xor(r, 2, 64);
+                r += __shfl_xor(r, 16, 64);
+                r += __shfl_xor(r, 32, 64);
+                const int row = 4 * rq + v;
+                if ((lane & 0x33) == 0) {
+                    if (whole) ysum[cur.set * 16 + row] = r;
+                    else red[wave][slot][row] = r;
+                }
+                yp[v] = 0.f;
+            }
+        }
+        // The ring slot is consumed: refill it with the tile P items
+        // ahead (zeros, without a memory access, past the range).
+        load(item + P, ld, tile, sc);
+        ld.next(steps);
+        cur.next(steps);
+    };
+    // Whole blocks of P items: straight-line code, so the compiler waits
+    // only for the tile each item needs.  The last nitems % P items follow.
+    int base = 0;
+    for (; base + P <= nitems; base += P) {
+#pragma unroll
+        for (int p = 0; p < P; p++) step(base + p, ring[p], rsc[p]);
     }
+#pragma unroll
+    for (int p = 0; p < P - 1; p++)
+        if (base + p < nitems) step(base + p, ring[p], rsc[p]);
     __syncthreads();
     // Cut sets: one per range boundary strictly inside a set (the same set
-    // may hold several boundaries; the first of them sums it).
-    if (threadIdx.x < 3 * 16) {
+    // may hold several boundaries; the first of them sums it, in wave order).
+    if (threadIdx.x < (NW - 1) * 16) {
         const int bi = threadIdx.x / 16 + 1, r = threadIdx.x % 16;
-        const int bnd = total * bi / 4;
+        const int bnd = total * bi / NW;
         const int j = bnd / steps;
-        const int prev = total * (bi - 1) / 4;
+        const int prev = total * (bi - 1) / NW;
         const bool first_in_set = bi == 1 || prev <= j * steps;
         if (bnd % steps != 0 && first_in_set) {
             float acc = 0.f;
-            for (int w = 0; w < 4; w++) {
-                const int wa = total * w / 4, wb = total * (w + 1) / 4;
+            for (int w = 0; w < NW; w++) {
+                const int wa = total * w / NW, wb = total * (w + 1) / NW;
                 const bool overlap = wa < wb && wa < (j + 1) * steps && wb > j * steps;
                 const bool whole = wa <= j * steps && wb >= (j + 1) * steps;
                 if (overlap && !whole) acc += red[w][j * steps < wa ? 0 : 1][r];
             }
-            const int row = (set_lo + j) * 16 + r;
-            if (row < R) y[row] = acc;
+            ysum[j * 16 + r] = acc;
         }
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < nset_wg * 16; i += MT) {
+        const int row = set_lo * 16 + i;
+        if (row < R) y[row] = ysum[i];
     }
 }
 
-template <int XT>
+template <int XT, int NW, int P>
 int occupancy_wgs(size_t lds) {
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, q2_0_gemv_mfma_kernel<XT>, MT, lds) !=
-                hipSuccess ||
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, q2_0_gemv_mfma_kernel<XT, NW, P>, 64 * NW,
+                                                     lds) != hipSuccess ||
         n < 1)
         n = 1;
     return n;
+}
+
+template <int XT, int NW, int P>
+int launch(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, size_t xlds) {
+    const int64_t K = w->K, R = w->R;
+    const int nblk = (int)(K >> 7), steps = (nblk + 3) / 4;
+    const int cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
+    const int64_t nsets = (R + 15) / 16;
+    // Row results of up to `cap` sets fit beside x in LDS.
+    const int64_t cap = std::min<int64_t>(256, (int64_t)(LDS_BYTES - xlds) / 64);
+    // Every resident workgroup gets the same number of sets; the occupancy
+    // depends on the LDS footprint, so it is looked up per K.
+    static int occ_memo[513];                             // by nblk; 0 = unknown
+    int &occ = occ_memo[nblk];
+    if (occ == 0) occ = occupancy_wgs<XT, NW, P>(xlds + (size_t)cap * 64);
+    const int64_t max_wgs = (int64_t)cus * occ;
+    const int64_t per = std::min(cap, (nsets + max_wgs - 1) / max_wgs);
+    GD_REQUIRE(ctx, per * steps * NW < (1LL << 31) && per * steps / NW + 1 < (1LL << 20),
+               "gd_q2_0_gemv: R=%lld too large", (long long)R);
+    const unsigned grid = (unsigned)((nsets + per - 1) / per);
+    const size_t lds = xlds + (size_t)per * 64;
+    hipLaunchKernelGGL((q2_0_gemv_mfma_kernel<XT, NW, P>), dim3(grid), dim3(64 * NW), lds,
+                       ctx->stream, (const uint8_t *)w->codes, (const uint16_t *)w->scales, x, y,
+                       (int)K, (int)R, (int)nsets, (int)per);
+    GD_LAUNCHED(ctx, "q2_0_gemv_mfma");
+    return GD_OK;
+}
+
+template <int XT>
+int launch_nw(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, size_t xlds) {
+    // Waves per workgroup (all share one staged copy of x) and tiles in
+    // flight per wave; GADEON_GEMV_NW / GADEON_GEMV_P override for tuning.
+    static const char *env_nw = getenv("GADEON_GEMV_NW");
+    static const char *env_p = getenv("GADEON_GEMV_P");
+    const int nw = env_nw ? atoi(env_nw) : 16, pp = env_p ? atoi(env_p) : 2;
+    if (nw == 4) return pp == 2 ? launch<XT, 4, 2>(ctx, w, x, y, xlds) : pp == 4 ? launch<XT, 4, 4>(ctx, w, x, y, xlds) : launch<XT, 4, 3>(ctx, w, x, y, xlds);
+    if (nw == 8) return pp == 2 ? launch<XT, 8, 2>(ctx, w, x, y, xlds) : pp == 4 ? launch<XT, 8, 4>(ctx, w, x, y, xlds) : launch<XT, 8, 3>(ctx, w, x, y, xlds);
+    return pp == 2 ? launch<XT, 16, 2>(ctx, w, x, y, xlds) : pp == 4 ? launch<XT, 16, 4>(ctx, w, x, y, xlds) : launch<XT, 16, 3>(ctx, w, x, y, xlds);
 }
 
 }  // namespace
 
 // GEMV on the matrix cores for f16 or f32 x (the caller has checked w, x, y).
 int gd_gemv_mfma(gd_ctx *ctx, const gd_q2w *w, const void *x, int x_dtype, float *y) {
-    const int64_t K = w->K, R = w->R;
+    const int64_t K = w->K;
     const int XT = x_dtype == GD_F32 ? 1 : 0;
     const int nblk = (int)(K >> 7);
-    const size_t lds = (size_t)(nblk + 1) * 64 * 4 * (XT ? 2 : 1) + (size_t)nblk * 4;
-    GD_REQUIRE(ctx, lds <= 160 * 1024 - 512,
+    const size_t xlds = (size_t)(nblk + 5) * XB * 4 * (XT ? 2 : 1) + (size_t)nblk * 8;
+    GD_REQUIRE(ctx, xlds + 16 * 64 <= LDS_BYTES,
                "gd_q2_0_gemv: K=%lld too long for LDS staging of %s x", (long long)K,
                XT ? "f32" : "f16");
-    const int cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
-    const int steps = (nblk + 3) / 4;
-    const int64_t nsets = (R + 15) / 16;
-    // Every resident workgroup gets the same number of sets.  The LDS
-    // footprint depends on K, so the occupancy is looked up per shape.
-    static int occ_memo[2][513];                          // by x type and nblk; 0 = unknown
-    int &occ = occ_memo[XT][nblk];
-    if (occ == 0) occ = XT ? occupancy_wgs<1>(lds) : occupancy_wgs<0>(lds);
-    const int64_t max_wgs = (int64_t)cus * occ;
-    const int64_t per = (nsets + max_wgs - 1) / max_wgs;
-    GD_REQUIRE(ctx, per * steps * 4 < (1LL << 31), "gd_q2_0_gemv: R=%lld too large",
-               (long long)R);
-    const unsigned grid = (unsigned)((nsets + per - 1) / per);
-    auto *c = (const uint8_t *)w->codes;
-    auto *s = (const uint16_t *)w->scales;
-    if (XT)
-        hipLaunchKernelGGL(q2_0_gemv_mfma_kernel<1>, dim3(grid), dim3(MT), lds, ctx->stream, c, s,
-                           x, y, (int)K, (int)R, (int)nsets, (int)per);
-    else
-        hipLaunchKernelGGL(q2_0_gemv_mfma_kernel<0>, dim3(grid), dim3(MT), lds, ctx->stream, c, s,
-                           x, y, (int)K, (int)R, (int)nsets, (int)per);
-    GD_LAUNCHED(ctx, "q2_0_gemv_mfma");
-    return GD_OK;
+    return XT ? launch_nw<1>(ctx, w, x, y, xlds) : launch_nw<0>(ctx, w, x, y, xlds);
 }
