@@ -307,33 +307,74 @@ def cpu_baseline_stack(ctx, ga, h, c, seconds: float) -> dict:
                       f"run at this same rate"}
 
 
-def kernel_rooflines(ctx, ga, steps: int) -> dict:
+TRAFFIC_FILE = ROOT / "profiles" / "q2_0_gemv_K5120_R34816_traffic.txt"
+
+
+def gemv_traffic():
+    """HBM bytes per launch of the roofline GEMV as rocprofv3 --pmc measured
+    them (FETCH_SIZE + WRITE_SIZE, each scaled by the same counter on a copy
+    kernel of known size), read from the committed summary; None if absent."""
+    try:
+        for line in TRAFFIC_FILE.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1])
+    except (OSError, ValueError):
+        pass
+    return None
+
+
+def kernel_rooflines(ctx, ga, steps: int, pool: int = 8) -> dict:
     """The stack's dominant kernels at their in-stack shapes, timed alone with
     HIP events on the context stream: the FFN gate|up Q2_0 GEMV of decode
-    (K=5120, R=34816, f16 x) and the same GEMM at T=512 for prefill."""
+    (K=5120, R=34816, f16 x) and the same GEMM at T=512 for prefill.  The
+    GEMV rotates over `pool` distinct weight matrices (8 x 47.5 MB, beyond
+    the 256 MB Infinity Cache) so every call streams its weights from HBM,
+    as it does in decode."""
     K, R, T = 5120, 34816, 512
-    w = ga.Q2W()
-    ctx.gd_q2w_alloc(K, R, C.byref(w))
-    ctx.gd_rand_q2w(C.byref(w), 77, 0.01, 0.05)
+    ws = []
+    for i in range(pool):
+        w = ga.Q2W()
+        ctx.gd_q2w_alloc(K, R, C.byref(w))
+        ctx.gd_rand_q2w(C.byref(w), 77 + i, 0.01, 0.05)
+        ws.append(w)
     dx = ctx.alloc(T * K * 2)
     ctx.gd_rand_normal(dx, ga.F16, T * K, 78, 0.0, 1.0)
     dy = ctx.alloc(T * R * 4)
     t = Timer(ctx)
-    gemv = lambda: ctx.gd_q2_0_gemv(C.byref(w), dx, ga.F16, dy)
-    gemm = lambda: ctx.gd_q2_0_gemm(C.byref(w), T, dx, ga.F16, dy, ga.F32)
-    for _ in range(3):
+    it = [0]
+
+    def gemv():
+        ctx.gd_q2_0_gemv(C.byref(ws[it[0] % pool]), dx, ga.F16, dy)
+        it[0] += 1
+
+    gemm = lambda: ctx.gd_q2_0_gemm(C.byref(ws[0]), T, dx, ga.F16, dy, ga.F32)
+    for _ in range(pool):
         gemv()
-        gemm()
-    gemv_ms = t.ms(gemv, max(steps, 50))
+    gemm()
+    gemv_ms = t.ms(gemv, max(steps, 5 * pool))
     gemm_ms = t.ms(gemm, max(steps, 10))
-    ctx.gd_q2w_free(C.byref(w))
+    for w in ws:
+        ctx.gd_q2w_free(C.byref(w))
     ctx.free(dx)
     ctx.free(dy)
     gemv_bytes = R * K * 17 // 64 + K * 2 + R * 4
     return {"gemv": {"shape": f"K={K} R={R} x f16", "us": gemv_ms * 1e3, "bytes": gemv_bytes,
-                     "gbs": gemv_bytes / (gemv_ms * 1e-3) / 1e9},
+                     "gbs": gemv_bytes / (gemv_ms * 1e-3) / 1e9, "pool": pool},
             "gemm": {"shape": f"T={T} K={K} R={R}", "us": gemm_ms * 1e3,
                      "tflops": 2 * T * K * R / (gemm_ms * 1e-3) / 1e12}}
+
+
+def calibration_copy(ctx, ga, n: int = 1 << 24) -> dict:
+    """A plain copy kernel of known traffic for scaling rocprofv3 byte
+    counters: gd_cast of n f16 -> n f32 reads 2n bytes and writes 4n."""
+    a, b = ctx.alloc(n * 2), ctx.alloc(n * 4)
+    ctx.gd_fill_u32(a, 0x3C003C00, n // 2)
+    for _ in range(3):
+        ctx.gd_cast(a, ga.F16, b, ga.F32, n)
+    ctx.gd_sync()
+    ctx.free(a)
+    ctx.free(b)
+    return {"kernel": "gd_cast_kernel", "read_bytes": 2 * n, "write_bytes": 4 * n}
 
 
 def run_kernels(ctx, ga, args) -> dict:
@@ -360,7 +401,9 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=3,
                     help="timed passes (stack: one pp512 + tg128 pass each)")
     ap.add_argument("--warmup", type=int, default=1)
-    ap.add_argument("--workload", choices=("stack", "kernels"), default="stack")
+    ap.add_argument("--workload", choices=("stack", "kernels", "roofline"), default="stack",
+                    help="stack: config 4 (the metric); kernels: configs 0-3; roofline: only "
+                         "the roofline GEMV/GEMM and a calibration copy (for rocprofv3 runs)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -373,6 +416,11 @@ def main() -> int:
         if args.workload == "stack":
             r = run_stack(ctx, ga, args)
             r["kernels"] = kernel_rooflines(ctx, ga, 20)
+        elif args.workload == "roofline":
+            r = kernel_rooflines(ctx, ga, 40)
+            r["calibration"] = calibration_copy(ctx, ga)
+            print(json.dumps(r))
+            return 0
         else:
             r = run_kernels(ctx, ga, args)
     finally:
@@ -401,7 +449,9 @@ def main() -> int:
             "gemv_frac_hbm_peak": round(g["gbs"] / HBM_PEAK_GBS, 4),
             "roofline": {"bound": "hbm", "achieved": round(g["gbs"], 1), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(g["gbs"] / HBM_PEAK_GBS, 4),
-                         "traffic": None, "kernel": "q2_0_gemv " + g["shape"]},
+                         "traffic": gemv_traffic(),
+                         "kernel": "q2_0_gemv_mfma " + g["shape"] + " (weights rotated over "
+                                   f"{g['pool']} copies, streamed from HBM)"},
             "cpu_baseline": r["cpu"],
             "detail": r,
         }

@@ -29,6 +29,8 @@ int gd_fail(gd_ctx *ctx, int code, const char *fmt, ...);
 int gd_ctx_workspace(gd_ctx *ctx, size_t bytes, void **out);
 // Map a HIP error to a GD code with a message naming `what`.
 int gd_hip_fail(gd_ctx *ctx, hipError_t e, const char *what);
+// Host-side set-up of the GEMV for reduction length K (before graph capture).
+int gd_gemv_mfma_prepare(gd_ctx *ctx, int64_t K, int x_dtype);
 
 #define GD_CHECK_CTX(ctx) \
     do { if (!(ctx)) return GD_EINVAL; } while (0)

@@ -403,6 +403,14 @@ int occupancy_wgs(size_t lds) {
     return n;
 }
 
+// Workgroups per CU for a K (the LDS footprint depends on it), looked up once.
+template <int XT, int NW, int P>
+int occupancy_memo(int nblk, size_t lds) {
+    static int memo[513];                                 // by nblk; 0 = unknown
+    if (memo[nblk] == 0) memo[nblk] = occupancy_wgs<XT, NW, P>(lds);
+    return memo[nblk];
+}
+
 template <int XT, int NW, int P>
 int launch(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, size_t xlds) {
     const int64_t K = w->K, R = w->R;
@@ -413,9 +421,7 @@ int launch(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, size_t xlds) {
     const int64_t cap = std::min<int64_t>(256, (int64_t)(LDS_BYTES - xlds) / 64);
     // Every resident workgroup gets the same number of sets; the occupancy
     // depends on the LDS footprint, so it is looked up per K.
-    static int occ_memo[513];                             // by nblk; 0 = unknown
-    int &occ = occ_memo[nblk];
-    if (occ == 0) occ = occupancy_wgs<XT, NW, P>(xlds + (size_t)cap * 64);
+    const int occ = occupancy_memo<XT, NW, P>(nblk, xlds + (size_t)cap * 64);
     const int64_t max_wgs = (int64_t)cus * occ;
     const int64_t per = std::min(cap, (nsets + max_wgs - 1) / max_wgs);
     GD_REQUIRE(ctx, per * steps * NW < (1LL << 31) && per * steps / NW + 1 < (1LL << 20),
@@ -429,6 +435,16 @@ int launch(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, size_t xlds) {
     return GD_OK;
 }
 
+template <int XT, int NW, int P>
+int launch_or_prepare(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, size_t xlds) {
+    if (w) return launch<XT, NW, P>(ctx, w, x, y, xlds);
+    // Preparation only (x carries nblk): fill the occupancy memo.
+    const int nblk = (int)(intptr_t)x;
+    const size_t cap = std::min<size_t>(256, (LDS_BYTES - xlds) / 64);
+    (void)occupancy_memo<XT, NW, P>(nblk, xlds + cap * 64);
+    return GD_OK;
+}
+
 template <int XT>
 int launch_nw(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, size_t xlds) {
     // Waves per workgroup (all share one staged copy of x) and tiles in
@@ -436,9 +452,11 @@ int launch_nw(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, size_t xlds
     static const char *env_nw = getenv("GADEON_GEMV_NW");
     static const char *env_p = getenv("GADEON_GEMV_P");
     const int nw = env_nw ? atoi(env_nw) : 16, pp = env_p ? atoi(env_p) : 2;
-    if (nw == 4) return pp == 2 ? launch<XT, 4, 2>(ctx, w, x, y, xlds) : pp == 4 ? launch<XT, 4, 4>(ctx, w, x, y, xlds) : launch<XT, 4, 3>(ctx, w, x, y, xlds);
-    if (nw == 8) return pp == 2 ? launch<XT, 8, 2>(ctx, w, x, y, xlds) : pp == 4 ? launch<XT, 8, 4>(ctx, w, x, y, xlds) : launch<XT, 8, 3>(ctx, w, x, y, xlds);
-    return pp == 2 ? launch<XT, 16, 2>(ctx, w, x, y, xlds) : pp == 4 ? launch<XT, 16, 4>(ctx, w, x, y, xlds) : launch<XT, 16, 3>(ctx, w, x, y, xlds);
+#define GD_L(NW_, P_) launch_or_prepare<XT, NW_, P_>(ctx, w, x, y, xlds)
+    if (nw == 4) return pp == 2 ? GD_L(4, 2) : pp == 4 ? GD_L(4, 4) : GD_L(4, 3);
+    if (nw == 8) return pp == 2 ? GD_L(8, 2) : pp == 4 ? GD_L(8, 4) : GD_L(8, 3);
+    return pp == 2 ? GD_L(16, 2) : pp == 4 ? GD_L(16, 4) : GD_L(16, 3);
+#undef GD_L
 }
 
 }  // namespace
@@ -453,4 +471,16 @@ int gd_gemv_mfma(gd_ctx *ctx, const gd_q2w *w, const void *x, int x_dtype, float
                "gd_q2_0_gemv: K=%lld too long for LDS staging of %s x", (long long)K,
                XT ? "f32" : "f16");
     return XT ? launch_nw<1>(ctx, w, x, y, xlds) : launch_nw<0>(ctx, w, x, y, xlds);
+}
+
+// Host-side set-up for GEMVs of reduction length K (the occupancy lookup),
+// so that a later call can be captured into a graph without runtime queries.
+int gd_gemv_mfma_prepare(gd_ctx *ctx, int64_t K, int x_dtype) {
+    const int XT = x_dtype == GD_F32 ? 1 : 0;
+    const int nblk = (int)(K >> 7);
+    const size_t xlds = (size_t)(nblk + 5) * XB * 4 * (XT ? 2 : 1) + (size_t)nblk * 8;
+    if (K % 128 || K > 65536 || xlds + 16 * 64 > LDS_BYTES) return GD_EINVAL;
+    const void *tag = (const void *)(intptr_t)nblk;
+    return XT ? launch_nw<1>(ctx, nullptr, tag, nullptr, xlds)
+              : launch_nw<0>(ctx, nullptr, tag, nullptr, xlds);
 }

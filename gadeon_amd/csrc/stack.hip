@@ -718,9 +718,17 @@ extern "C" int gd_stack_generate(gd_stack *st, int n, int32_t *tokens) {
     GD_REQUIRE(ctx, st->pos + n <= st->c.max_ctx, "gd_stack_generate: context full");
     if (n == 0) return GD_OK;
     int rc;
+    // GADEON_STACK_EAGER=1 launches every step's kernels directly instead of
+    // replaying the captured graph (same kernels and results; for profilers
+    // that do not follow graph launches).
+    static const bool eager = getenv("GADEON_STACK_EAGER") != nullptr;
     // One decode step reads the previous pick from st->dtok, so the whole step
     // (embed .. argmax, position bump) replays with no host involvement.
-    if (!st->decode_exec) {
+    if (!st->decode_exec && !eager) {
+        // Host-side lookups the GEMVs make on first use happen before capture.
+        for (int64_t K : {(int64_t)st->c.n_embd, (int64_t)st->c.n_ff, (int64_t)st->valDim,
+                          (int64_t)st->c.n_head * HD})
+            if ((rc = gd_gemv_mfma_prepare(ctx, K, GD_F16))) return rc;
         GD_HIP(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
         rc = gd_q2_0_dequant_rows(ctx, &st->embd, st->dtok, 1, st->x);
         if (rc == GD_OK) rc = forward(st, 1, true);
@@ -738,8 +746,17 @@ extern "C" int gd_stack_generate(gd_stack *st, int n, int32_t *tokens) {
     int32_t *ring = nullptr;
     if ((rc = gd_alloc(ctx, (size_t)n * 4, (void **)&ring))) return rc;
     for (int i = 0; i < n; i++) {
-        hipError_t e = hipGraphLaunch(st->decode_exec, ctx->stream);
-        if (e != hipSuccess) { gd_free(ctx, ring); return gd_hip_fail(ctx, e, "decode graph launch"); }
+        if (eager) {
+            if ((rc = gd_q2_0_dequant_rows(ctx, &st->embd, st->dtok, 1, st->x)) ||
+                (rc = forward(st, 1, true))) {
+                gd_free(ctx, ring);
+                return rc;
+            }
+        } else {
+            hipError_t e = hipGraphLaunch(st->decode_exec, ctx->stream);
+            if (e != hipSuccess) { gd_free(ctx, ring); return gd_hip_fail(ctx, e, "decode graph launch"); }
+        }
+        hipError_t e;
         e = hipMemcpyAsync(ring + i, st->dtok, 4, hipMemcpyDeviceToDevice, ctx->stream);
         if (e != hipSuccess) { gd_free(ctx, ring); return gd_hip_fail(ctx, e, "token copy"); }
     }
