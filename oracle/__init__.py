@@ -179,6 +179,19 @@ def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
     return y
 
 
+def softmax(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32).copy()
+    lib().or_softmax(P(x), x.size)
+    return x
+
+
+def rope_neox(x: np.ndarray, head_dim: int, n_rot: int, base: float, pos: int) -> np.ndarray:
+    """x [nHead * head_dim] (heads contiguous), rotated in a copy."""
+    x = np.ascontiguousarray(x, np.float32).copy()
+    lib().or_rope_neox(P(x), head_dim, x.size // head_dim, n_rot, base, pos)
+    return x
+
+
 def gdn_gate(bPre, aPre, dt, aNeg, nV):
     bPre = np.ascontiguousarray(bPre, np.float32)
     aPre = np.ascontiguousarray(aPre, np.float32)
