@@ -1,4 +1,4 @@
-// Chunked (WY / UT) Gated DeltaNet prefill.
+// Chunked (WY / UT) Gated DeltaNet prefill on the matrix cores.
 //
 // The reference runs prefill as a token-serial scan (gdn_scan_batch2,
 // LLM/metal/Kernels.metal:1570-1625; GDN.step, LLM/src/SIMD/GDN.swift:71-109).
@@ -14,142 +14,282 @@
 // Every exponent is a difference G_t - G_s <= 0 (or G <= 0), so no factor
 // exceeds 1 and nothing overflows however long the decay runs.
 //
-// Kernels:
-//   gdn_chunk_prep  (value head, chunk)   -> W, U, P, G into a workspace; the
-//                                            chunks are independent.
-//   gdn_chunk_scan  (value head, columns) -> walks the chunks in order with a
-//                                            slice of S resident in LDS:
-//                                            delta, O, S update.
-// Value columns of S are independent (column j needs only S[:, j]), which
-// is what splits the serial part across workgroups.
+// MI355X design.  Every product above runs on v_mfma_f32_16x16x32_f16 with
+// f32 accumulation.  q, k, v enter as f16 (f32 inputs are rounded once, at
+// load, so every use of a token sees the same values).  Operands that are f32
+// by nature -- S, delta, T, beta e^G k, beta v, P -- are split into
+// hi = f16(x) and lo = f16(x - hi) and multiplied as hi*hi + hi*lo + lo*hi
+// (about 22 significant bits), so the result tracks the f32 recurrence.
+//   gdn_prep  (value head, chunk): K K^T and Q K^T on the matrix cores give A
+//             and P; one wave inverts I + A by forward substitution with its
+//             column of T in registers while the others stage the transposed
+//             operands; then W = T X and U = T Y (the UT transform) on the
+//             matrix cores.  The chunks are independent.
+//   gdn_scan  (value head, 32 columns of S): walks the chunks in order with
+//             its slice of S resident in LDS: delta = U - W S, O = qScale
+//             e^G (Q S) + P delta, S <- e^{G_L} S + K^T (e^{G_L-G} delta).
+//             Value columns of S are independent, which is what splits the
+//             serial part across workgroups.
+// Workspace per (head, chunk) unit, CP = max(32, C) rows (rows past the
+// chunk's tokens are zero): W hi/lo [CP][128] f16, U [CP][128] f32, P hi/lo
+// [CP][CP] f16, K^T [128][CP] f16, G [CP] f32.
 #include "gd_internal.h"
-
 
 namespace {
 
-constexpr int CMAX = 64;         // largest chunk
 constexpr int DK = 128;          // key size handled
 constexpr int DV = 128;          // value size handled
-constexpr int SCAN_COLS = 8;     // value columns per scan workgroup
+constexpr int NCOL = 32;         // value columns of S per scan workgroup
+constexpr int PADK = DK + 8;     // LDS row of 128 f16 plus 16 bytes (bank spread)
 
-template <typename T> __device__ __forceinline__ float ldx(const void *p, int64_t i);
-template <> __device__ __forceinline__ float ldx<float>(const void *p, int64_t i) {
-    return ((const float *)p)[i];
+__device__ __forceinline__ f32x4 mfma(const f16x8 &a, const f16x8 &b, const f32x4 &c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
-template <> __device__ __forceinline__ float ldx<uint16_t>(const void *p, int64_t i) {
-    return gd_h2f(((const uint16_t *)p)[i]);
+
+// x = hi + lo, hi = f16(x), lo = f16(x - hi).
+__device__ __forceinline__ void split8(const float (&x)[8], f16x8 &hi, f16x8 &lo) {
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        hi[e] = (f16)x[e];
+        lo[e] = (f16)(x[e] - (float)hi[e]);
+    }
 }
+
+// hi*hi + hi*lo + lo*hi, accumulated into c.
+__device__ __forceinline__ f32x4 mfma3(const f16x8 &ah, const f16x8 &al, const f16x8 &bh,
+                                       const f16x8 &bl, f32x4 c) {
+    c = mfma(ah, bh, c);
+    c = mfma(ah, bl, c);
+    return mfma(al, bh, c);
+}
+
+// Eight consecutive activations (f16 or f32) as f16, zero when !ok.
+template <typename IO>
+__device__ __forceinline__ f16x8 load8(const void *base, int64_t idx, bool ok) {
+    f16x8 r;
+    if constexpr (sizeof(IO) == 2) {
+        const u32x4 v = ok ? *(const u32x4 *)((const uint16_t *)base + idx) : u32x4{0, 0, 0, 0};
+        r = __builtin_bit_cast(f16x8, v);
+    } else {
+        f32x4 a = f32x4{0.f, 0.f, 0.f, 0.f}, b = a;
+        if (ok) {
+            const f32x4 *p = (const f32x4 *)((const float *)base + idx);
+            a = p[0];
+            b = p[1];
+        }
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            r[e] = (f16)a[e];
+            r[4 + e] = (f16)b[e];
+        }
+    }
+    return r;
+}
+
+struct Work {
+    f16 *Wh, *Wl;     // [u][CP][DK]
+    float *U;         // [u][CP][DV]
+    f16 *Ph, *Pl;     // [u][CP][CP]
+    f16 *KT;          // [u][DK][CP]
+    float *G;         // [u][CP]
+};
 
 struct PrepArgs {
     const void *q, *k, *v;
     int64_t q_stride, k_stride, v_stride;
     const float *g, *beta;
-    float *W, *U, *P, *G;        // workspace
+    Work w;
     int64_t T;
     int nV, nK, C, nchunks;
     float qScale;
 };
 
-// Workspace layout per (head, chunk) unit u = hv * nchunks + c:
-//   W[u][C][DK], U[u][C][DV], P[u][C][C], G[u][C]
-
-template <typename IO>
-__global__ __launch_bounds__(256) void gdn_chunk_prep(PrepArgs a) {
-    __shared__ float Ks[CMAX][DK + 1];
-    __shared__ float QVs[CMAX][DK + 1];      // Q, later V
-    __shared__ float As[CMAX][CMAX + 1];
-    __shared__ float Ts[CMAX][CMAX + 1];
-    __shared__ float Gs[CMAX], Bs[CMAX];
+template <int CP, typename IO>
+__global__ __launch_bounds__(256) void gdn_prep(PrepArgs a) {
+    __shared__ __attribute__((aligned(16))) f16 Ks[CP][PADK];
+    __shared__ __attribute__((aligned(16))) f16 QVs[CP][PADK];     // Q, later V
+    __shared__ __attribute__((aligned(16))) f16 Xh[DK][CP + 8], Xl[DK][CP + 8];
+    __shared__ __attribute__((aligned(16))) f16 Yh[DV][CP + 8], Yl[DV][CP + 8];
+    __shared__ __attribute__((aligned(16))) float Af[CP][CP + 4];
+    __shared__ __attribute__((aligned(16))) float Tf[CP][CP + 4];
+    __shared__ float Gs[CP], Bs[CP];
 
     const int hv = blockIdx.x / a.nchunks, c = blockIdx.x % a.nchunks;
     const int hk = hv % a.nK;
-    const int tid = threadIdx.x;
-    const int C = a.C;
-    const int64_t t0 = (int64_t)c * C;
-    const int L = (int)((a.T - t0) < C ? (a.T - t0) : C);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t t0 = (int64_t)c * a.C;
+    const int L = (int)min((int64_t)a.C, a.T - t0);
     const int64_t u = (int64_t)hv * a.nchunks + c;
+    const int lr = lane & 15, kg = lane >> 4;
 
-    for (int e = tid; e < C * DK; e += 256) {
-        const int t = e / DK, i = e % DK;
-        float kv = 0.f, qv = 0.f;
-        if (t < L) {
-            kv = ldx<IO>(a.k, (t0 + t) * a.k_stride + (int64_t)hk * DK + i);
-            qv = ldx<IO>(a.q, (t0 + t) * a.q_stride + (int64_t)hk * DK + i);
-        }
-        Ks[t][i] = kv;
-        QVs[t][i] = qv;
+    // Rows of K and Q (and V, kept in registers until Q is done): thread e
+    // handles 8 consecutive elements of row e / 16.
+    constexpr int NE = CP * DK / 8 / 256;                   // entries per thread
+    f16x8 vreg[NE];
+#pragma unroll
+    for (int n = 0; n < NE; n++) {
+        const int e = tid + 256 * n, t = e >> 4, i8 = (e & 15) * 8;
+        const bool ok = t < L;
+        const int64_t tok = t0 + (ok ? t : 0);
+        *(f16x8 *)&Ks[t][i8] = load8<IO>(a.k, tok * a.k_stride + (int64_t)hk * DK + i8, ok);
+        *(f16x8 *)&QVs[t][i8] = load8<IO>(a.q, tok * a.q_stride + (int64_t)hk * DK + i8, ok);
+        vreg[n] = load8<IO>(a.v, tok * a.v_stride + (int64_t)hv * DV + i8, ok);
     }
-    if (tid < 64) {
-        // Inclusive cumulative gate inside the chunk (one wave, serial adds in
-        // token order, as the token-serial recurrence multiplies them).
-        if (tid == 0) {
-            float acc = 0.f;
-            for (int t = 0; t < C; t++) {
-                if (t < L) acc += a.g[(t0 + t) * a.nV + hv];
-                Gs[t] = acc;
-                Bs[t] = t < L ? a.beta[(t0 + t) * a.nV + hv] : 0.f;
-            }
+    if (wave == 0) {
+        // Inclusive cumulative gate inside the chunk (wave prefix sum); rows
+        // past L keep G[L-1] and get beta = 0.
+        float gv = lane < L ? a.g[(t0 + lane) * a.nV + hv] : 0.f;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const float o = __shfl_up(gv, off, 64);
+            if (lane >= off) gv += o;
+        }
+        if (lane < CP) {
+            Gs[lane] = gv;
+            Bs[lane] = lane < L ? a.beta[(t0 + lane) * a.nV + hv] : 0.f;
         }
     }
     __syncthreads();
-    if (tid < C) a.G[u * C + tid] = Gs[tid];
 
-    // A (strictly lower) and P (lower incl. diagonal).
-    for (int e = tid; e < C * C; e += 256) {
-        const int t = e / C, s = e % C;
-        float av = 0.f, pv = 0.f;
-        if (s <= t && t < L) {
-            float kk = 0.f, qk = 0.f;
-            for (int i = 0; i < DK; i++) {
-                kk = fmaf(Ks[t][i], Ks[s][i], kk);
-                qk = fmaf(QVs[t][i], Ks[s][i], qk);
+    // K K^T -> A (s < t) and Q K^T -> P (s <= t), lower tiles on the matrix
+    // cores; P's upper tiles are written as zeros.
+    constexpr int NB = CP / 16;
+    for (int tile = wave; tile < 2 * NB * NB; tile += 4) {
+        const bool isP = tile >= NB * NB;
+        const int tt = isP ? tile - NB * NB : tile;
+        const int ti = tt / NB, si = tt % NB;
+        f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (si <= ti) {
+#pragma unroll
+            for (int k0 = 0; k0 < DK; k0 += 32) {
+                const f16x8 av = isP ? *(const f16x8 *)&QVs[ti * 16 + lr][k0 + kg * 8]
+                                     : *(const f16x8 *)&Ks[ti * 16 + lr][k0 + kg * 8];
+                const f16x8 bv = *(const f16x8 *)&Ks[si * 16 + lr][k0 + kg * 8];
+                acc = mfma(av, bv, acc);
             }
+        }
+        const int s = si * 16 + lr;
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const int t = ti * 16 + kg * 4 + v;
             const float dec = expf(Gs[t] - Gs[s]);
-            if (s < t) av = Bs[t] * dec * kk;
-            pv = a.qScale * dec * qk;
+            if (!isP) {
+                Af[t][s] = (s < t && t < L) ? Bs[t] * dec * acc[v] : 0.f;
+            } else {
+                const float p = (s <= t && t < L) ? a.qScale * dec * acc[v] : 0.f;
+                const f16 ph = (f16)p;
+                const size_t pi = ((size_t)u * CP + t) * CP + s;
+                a.w.Ph[pi] = ph;
+                a.w.Pl[pi] = (f16)(p - (float)ph);
+            }
         }
-        As[t][s] = av;
-        a.P[u * C * C + e] = pv;
     }
     __syncthreads();
-
-    // T = (I + A)^-1, one column per thread: column s depends only on its own
-    // earlier entries, T[t][s] = -sum_{m=s}^{t-1} A[t][m] T[m][s].
-    if (tid < C) {
-        const int s = tid;
-        for (int t = 0; t < C; t++) Ts[t][s] = (t == s) ? 1.f : 0.f;
-        for (int t = s + 1; t < C; t++) {
-            float acc = 0.f;
-            for (int m = s; m < t; m++) acc = fmaf(As[t][m], Ts[m][s], acc);
-            Ts[t][s] = -acc;
-        }
-    }
     // V replaces Q.
-    __syncthreads();
-    for (int e = tid; e < C * DV; e += 256) {
-        const int t = e / DV, j = e % DV;
-        QVs[t][j] = t < L ? ldx<IO>(a.v, (t0 + t) * a.v_stride + (int64_t)hv * DV + j) : 0.f;
+#pragma unroll
+    for (int n = 0; n < NE; n++) {
+        const int e = tid + 256 * n, t = e >> 4, i8 = (e & 15) * 8;
+        *(f16x8 *)&QVs[t][i8] = vreg[n];
     }
     __syncthreads();
 
-    // W = T diag(beta e^G) K and U = T diag(beta) V.
-    const int col = tid & 127;
-    for (int t = tid >> 7; t < C; t += 2) {
-        float w = 0.f, uu = 0.f;
-        for (int s = 0; s <= t; s++) {
-            const float ts = Ts[t][s] * Bs[s];
-            w = fmaf(ts * expf(Gs[s]), Ks[s][col], w);
-            uu = fmaf(ts, QVs[s][col], uu);
+    if (wave == 0) {
+        // T = (I + A)^-1 by forward substitution, lane s holding column s of
+        // T in registers: T[t][s] = -sum_{m<t} A[t][m] T[m][s] (T[m][s] = 0
+        // for m < s, T[s][s] = 1).  A[t][m] is a broadcast read.
+        const int s = lane;
+        float Tc[CP];
+#pragma unroll
+        for (int m = 0; m < CP; m++) Tc[m] = m == s ? 1.f : 0.f;
+#pragma unroll
+        for (int t = 1; t < CP; t++) {
+            float acc0 = 0.f, acc1 = 0.f;
+#pragma unroll
+            for (int m = 0; m < t; m += 2) {
+                acc0 = fmaf(Af[t][m], Tc[m], acc0);
+                if (m + 1 < t) acc1 = fmaf(Af[t][m + 1], Tc[m + 1], acc1);
+            }
+            Tc[t] = t == s ? 1.f : -(acc0 + acc1);
         }
-        a.W[(u * C + t) * DK + col] = w;
-        a.U[(u * C + t) * DV + col] = uu;
+        if (s < CP) {
+#pragma unroll
+            for (int m = 0; m < CP; m++) Tf[m][s] = Tc[m];
+        }
+    } else {
+        // X^T = (diag(beta e^G) K)^T and Y^T = (diag(beta) V)^T, split, as
+        // the B operands of T X and T Y: entry (i, 8 tokens s .. s+7).
+        for (int e = tid - 64; e < DK * (CP / 8); e += 192) {
+            const int i = e / (CP / 8), s8 = (e % (CP / 8)) * 8;
+            float xv[8], yv[8];
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                const int s = s8 + q;
+                const float bt = Bs[s];
+                xv[q] = bt * expf(Gs[s]) * (float)Ks[s][i];
+                yv[q] = bt * (float)QVs[s][i];
+            }
+            f16x8 h, l;
+            split8(xv, h, l);
+            *(f16x8 *)&Xh[i][s8] = h;
+            *(f16x8 *)&Xl[i][s8] = l;
+            split8(yv, h, l);
+            *(f16x8 *)&Yh[i][s8] = h;
+            *(f16x8 *)&Yl[i][s8] = l;
+        }
+    }
+    // K^T to the workspace for the scan's state update (its A operand).
+    for (int e = tid; e < DK * (CP / 8); e += 256) {
+        const int i = e / (CP / 8), s8 = (e % (CP / 8)) * 8;
+        f16x8 kv;
+#pragma unroll
+        for (int q = 0; q < 8; q++) kv[q] = Ks[s8 + q][i];
+        *(f16x8 *)&a.w.KT[((size_t)u * DK + i) * CP + s8] = kv;
+    }
+    if (tid < CP) a.w.G[(size_t)u * CP + tid] = Gs[tid];
+    __syncthreads();
+
+    // W = T X, U = T Y: wave w takes row block rb (of CP/16) for all 16
+    // column tiles of W and U; T's rows are split once and reused.
+    for (int rb = wave; rb < NB; rb += 4) {
+        f16x8 th[CP / 32], tl[CP / 32];
+#pragma unroll
+        for (int ks = 0; ks < CP / 32; ks++) {
+            float tv[8];
+#pragma unroll
+            for (int q = 0; q < 8; q++) tv[q] = Tf[rb * 16 + lr][ks * 32 + kg * 8 + q];
+            split8(tv, th[ks], tl[ks]);
+        }
+        for (int ct = 0; ct < 16; ct++) {
+            const bool isU = ct >= 8;
+            const int ci = (ct & 7) * 16 + lr;          // column (key or value index)
+            f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < CP / 32; ks++) {
+                const int s0 = ks * 32 + kg * 8;
+                const f16x8 bh = isU ? *(const f16x8 *)&Yh[ci][s0] : *(const f16x8 *)&Xh[ci][s0];
+                const f16x8 bl = isU ? *(const f16x8 *)&Yl[ci][s0] : *(const f16x8 *)&Xl[ci][s0];
+                acc = mfma3(th[ks], tl[ks], bh, bl, acc);
+            }
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int t = rb * 16 + kg * 4 + v;
+                const size_t idx = ((size_t)u * CP + t) * DK + ci;
+                if (isU) {
+                    a.w.U[idx] = acc[v];
+                } else {
+                    const f16 h = (f16)acc[v];
+                    a.w.Wh[idx] = h;
+                    a.w.Wl[idx] = (f16)(acc[v] - (float)h);
+                }
+            }
+        }
     }
 }
 
 struct ScanArgs {
-    const void *q, *k;
-    int64_t q_stride, k_stride;
-    const float *W, *U, *P, *G;
+    const void *q;
+    int64_t q_stride;
+    Work w;
     float *S;
     void *o;
     int64_t o_stride;
@@ -158,84 +298,185 @@ struct ScanArgs {
     float qScale;
 };
 
-template <typename IO, typename OT>
-__global__ __launch_bounds__(256) void gdn_chunk_scan(ScanArgs a) {
-    __shared__ float Ws[CMAX][DK + 1];
-    __shared__ float Qs[CMAX][DK + 1];
-    __shared__ float Ks[CMAX][DK + 1];
-    __shared__ float Ps[CMAX][CMAX + 1];
-    __shared__ float Ss[DK][SCAN_COLS];
-    __shared__ float Ds[CMAX][SCAN_COLS];
-    __shared__ float Gs[CMAX];
+template <int CP, typename IO, typename OT>
+__global__ __launch_bounds__(256) void gdn_scan(ScanArgs a) {
+    __shared__ __attribute__((aligned(16))) float Sf[DK][NCOL + 4];          // S[i][j] slice
+    __shared__ __attribute__((aligned(16))) f16 Sh[NCOL][PADK], Sl[NCOL][PADK];  // S^T split
+    __shared__ __attribute__((aligned(16))) f16 Dh[NCOL][CP + 8], Dl[NCOL][CP + 8];  // delta^T
+    __shared__ __attribute__((aligned(16))) f16 Eh[NCOL][CP + 8], El[NCOL][CP + 8];  // decayed
+    __shared__ float Gs[CP];
 
-    const int ncb = DV / SCAN_COLS;
-    const int hv = blockIdx.x / ncb, cb = blockIdx.x % ncb;
+    constexpr int NCB = DV / NCOL;
+    const int hv = blockIdx.x / NCB, j0 = (blockIdx.x % NCB) * NCOL;
     const int hk = hv % a.nK;
-    const int tid = threadIdx.x;
-    const int C = a.C;
-    float *Sh = a.S + (int64_t)hv * DK * DV;
-    const int j0 = cb * SCAN_COLS;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lr = lane & 15, kg = lane >> 4;
+    float *Sg = a.S + (size_t)hv * DK * DV;
 
-    for (int e = tid; e < DK * SCAN_COLS; e += 256) {
-        const int i = e / SCAN_COLS, jj = e % SCAN_COLS;
-        Ss[i][jj] = Sh[(int64_t)i * DV + j0 + jj];
+    for (int e = tid; e < DK * NCOL; e += 256) {
+        const int i = e / NCOL, j = e % NCOL;
+        Sf[i][j] = Sg[(size_t)i * DV + j0 + j];
     }
 
     for (int c = 0; c < a.nchunks; c++) {
-        const int64_t t0 = (int64_t)c * C;
-        const int L = (int)((a.T - t0) < C ? (a.T - t0) : C);
-        const int64_t u = (int64_t)hv * a.nchunks + c;
+        const int64_t t0 = (int64_t)c * a.C;
+        const int L = (int)min((int64_t)a.C, a.T - t0);
+        const size_t u = (size_t)hv * a.nchunks + c;
         __syncthreads();
-        for (int e = tid; e < C * DK; e += 256) {
-            const int t = e / DK, i = e % DK;
-            Ws[t][i] = a.W[(u * C + t) * DK + i];
-            float qv = 0.f, kv = 0.f;
-            if (t < L) {
-                qv = ldx<IO>(a.q, (t0 + t) * a.q_stride + (int64_t)hk * DK + i);
-                kv = ldx<IO>(a.k, (t0 + t) * a.k_stride + (int64_t)hk * DK + i);
-            }
-            Qs[t][i] = qv;
-            Ks[t][i] = kv;
+        // S^T split (B operand of W S and Q S): entry (j, 8 rows i .. i+7).
+        for (int e = tid; e < NCOL * (DK / 8); e += 256) {
+            const int j = e / (DK / 8), i8 = (e % (DK / 8)) * 8;
+            float sv[8];
+#pragma unroll
+            for (int q = 0; q < 8; q++) sv[q] = Sf[i8 + q][j];
+            f16x8 h, l;
+            split8(sv, h, l);
+            *(f16x8 *)&Sh[j][i8] = h;
+            *(f16x8 *)&Sl[j][i8] = l;
         }
-        for (int e = tid; e < C * C; e += 256) Ps[e / C][e % C] = a.P[u * C * C + e];
-        if (tid < C) Gs[tid] = a.G[u * C + tid];
+        if (tid < CP) Gs[tid] = a.w.G[u * CP + tid];
+        __syncthreads();
+        const float gl = Gs[CP - 1];                    // G of the chunk's last token
+
+        // delta = U - W S (rows 16*wave ..), then delta^T and its decayed
+        // copy e^{G_L - G_t} delta^T, split, to LDS.
+        if (wave < CP / 16) {
+            const int tb = wave * 16;
+            f16x8 wh[DK / 32], wl[DK / 32];
+#pragma unroll
+            for (int ks = 0; ks < DK / 32; ks++) {
+                const size_t wi = (u * CP + tb + lr) * DK + ks * 32 + kg * 8;
+                wh[ks] = *(const f16x8 *)&a.w.Wh[wi];
+                wl[ks] = *(const f16x8 *)&a.w.Wl[wi];
+            }
+#pragma unroll
+            for (int ct = 0; ct < NCOL / 16; ct++) {
+                const int j = ct * 16 + lr;
+                f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ks = 0; ks < DK / 32; ks++) {
+                    const int i0 = ks * 32 + kg * 8;
+                    acc = mfma3(wh[ks], wl[ks], *(const f16x8 *)&Sh[j][i0],
+                                *(const f16x8 *)&Sl[j][i0], acc);
+                }
+                f16 dh[4], dl[4], eh[4], el[4];
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const int t = tb + kg * 4 + v;
+                    const float d = a.w.U[(u * CP + t) * DV + j0 + j] - acc[v];
+                    const float ed = expf(gl - Gs[t]) * d;
+                    dh[v] = (f16)d;
+                    dl[v] = (f16)(d - (float)dh[v]);
+                    eh[v] = (f16)ed;
+                    el[v] = (f16)(ed - (float)eh[v]);
+                }
+                const int tq = tb + kg * 4;
+                *(f16x4 *)&Dh[j][tq] = f16x4{dh[0], dh[1], dh[2], dh[3]};
+                *(f16x4 *)&Dl[j][tq] = f16x4{dl[0], dl[1], dl[2], dl[3]};
+                *(f16x4 *)&Eh[j][tq] = f16x4{eh[0], eh[1], eh[2], eh[3]};
+                *(f16x4 *)&El[j][tq] = f16x4{el[0], el[1], el[2], el[3]};
+            }
+        }
         __syncthreads();
 
-        // delta = U - W S
-        for (int e = tid; e < C * SCAN_COLS; e += 256) {
-            const int t = e / SCAN_COLS, jj = e % SCAN_COLS;
-            float acc = 0.f;
-            for (int i = 0; i < DK; i++) acc = fmaf(Ws[t][i], Ss[i][jj], acc);
-            Ds[t][jj] = t < L ? a.U[(u * C + t) * DV + j0 + jj] - acc : 0.f;
+        // O = qScale e^{G_t} (Q S) + P delta for the chunk's tokens.
+        if (wave < CP / 16) {
+            const int tb = wave * 16;
+            const int tr = tb + lr;                     // this lane's A row
+            const bool rok = tr < L;
+            f16x8 qa[DK / 32];
+#pragma unroll
+            for (int ks = 0; ks < DK / 32; ks++)
+                qa[ks] = load8<IO>(a.q, (t0 + (rok ? tr : 0)) * a.q_stride + (int64_t)hk * DK +
+                                            ks * 32 + kg * 8, rok);
+            f16x8 ph[CP / 32], pl[CP / 32];
+#pragma unroll
+            for (int ks = 0; ks < CP / 32; ks++) {
+                const size_t pi = (u * CP + tr) * CP + ks * 32 + kg * 8;
+                ph[ks] = *(const f16x8 *)&a.w.Ph[pi];
+                pl[ks] = *(const f16x8 *)&a.w.Pl[pi];
+            }
+#pragma unroll
+            for (int ct = 0; ct < NCOL / 16; ct++) {
+                const int j = ct * 16 + lr;
+                f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ks = 0; ks < DK / 32; ks++) {
+                    const int i0 = ks * 32 + kg * 8;
+                    acc = mfma(qa[ks], *(const f16x8 *)&Sh[j][i0], acc);
+                    acc = mfma(qa[ks], *(const f16x8 *)&Sl[j][i0], acc);
+                }
+#pragma unroll
+                for (int v = 0; v < 4; v++) acc[v] *= a.qScale * expf(Gs[tb + kg * 4 + v]);
+#pragma unroll
+                for (int ks = 0; ks < CP / 32; ks++) {
+                    const int s0 = ks * 32 + kg * 8;
+                    acc = mfma3(ph[ks], pl[ks], *(const f16x8 *)&Dh[j][s0],
+                                *(const f16x8 *)&Dl[j][s0], acc);
+                }
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const int t = tb + kg * 4 + v;
+                    if (t < L) {
+                        const int64_t oi = (t0 + t) * a.o_stride + (int64_t)hv * DV + j0 + j;
+                        if constexpr (sizeof(OT) == 4) ((float *)a.o)[oi] = acc[v];
+                        else ((uint16_t *)a.o)[oi] = gd_f2h(acc[v]);
+                    }
+                }
+            }
         }
-        __syncthreads();
-        // O = qScale e^G (Q S) + P delta
-        for (int e = tid; e < C * SCAN_COLS; e += 256) {
-            const int t = e / SCAN_COLS, jj = e % SCAN_COLS;
-            if (t >= L) continue;
-            float qs = 0.f, pd = 0.f;
-            for (int i = 0; i < DK; i++) qs = fmaf(Qs[t][i], Ss[i][jj], qs);
-            for (int s = 0; s <= t; s++) pd = fmaf(Ps[t][s], Ds[s][jj], pd);
-            const float ov = a.qScale * expf(Gs[t]) * qs + pd;
-            const int64_t oi = (t0 + t) * a.o_stride + (int64_t)hv * DV + j0 + jj;
-            if (sizeof(OT) == 4) ((float *)a.o)[oi] = ov;
-            else ((uint16_t *)a.o)[oi] = gd_f2h(ov);
-        }
-        __syncthreads();
-        // S = e^{G_L} S + K^T diag(e^{G_L - G}) delta
-        const float gl = Gs[L - 1];
-        for (int e = tid; e < DK * SCAN_COLS; e += 256) {
-            const int i = e / SCAN_COLS, jj = e % SCAN_COLS;
-            float acc = 0.f;
-            for (int s = 0; s < L; s++) acc = fmaf(Ks[s][i] * expf(gl - Gs[s]), Ds[s][jj], acc);
-            Ss[i][jj] = expf(gl) * Ss[i][jj] + acc;
+
+        // S <- e^{G_L} S + K^T (e^{G_L - G} delta): rows 32*wave .. +31.
+        {
+            const float decay = expf(gl);
+#pragma unroll
+            for (int rt = 0; rt < 2; rt++) {
+                const int ib = wave * 32 + rt * 16;
+                f16x8 ka[CP / 32];
+#pragma unroll
+                for (int ks = 0; ks < CP / 32; ks++)
+                    ka[ks] = *(const f16x8 *)&a.w.KT[(u * DK + ib + lr) * CP + ks * 32 + kg * 8];
+#pragma unroll
+                for (int ct = 0; ct < NCOL / 16; ct++) {
+                    const int j = ct * 16 + lr;
+                    f32x4 acc;
+#pragma unroll
+                    for (int v = 0; v < 4; v++) acc[v] = decay * Sf[ib + kg * 4 + v][j];
+#pragma unroll
+                    for (int ks = 0; ks < CP / 32; ks++) {
+                        const int s0 = ks * 32 + kg * 8;
+                        acc = mfma(ka[ks], *(const f16x8 *)&Eh[j][s0], acc);
+                        acc = mfma(ka[ks], *(const f16x8 *)&El[j][s0], acc);
+                    }
+#pragma unroll
+                    for (int v = 0; v < 4; v++) Sf[ib + kg * 4 + v][j] = acc[v];
+                }
+            }
         }
     }
     __syncthreads();
-    for (int e = tid; e < DK * SCAN_COLS; e += 256) {
-        const int i = e / SCAN_COLS, jj = e % SCAN_COLS;
-        Sh[(int64_t)i * DV + j0 + jj] = Ss[i][jj];
+    for (int e = tid; e < DK * NCOL; e += 256) {
+        const int i = e / NCOL, j = e % NCOL;
+        Sg[(size_t)i * DV + j0 + j] = Sf[i][j];
     }
+}
+
+template <int CP>
+int launch(gd_ctx *ctx, const PrepArgs &pa, const ScanArgs &sa, int io_dtype, int o_dtype) {
+    const unsigned units = (unsigned)(pa.nV * pa.nchunks);
+    if (io_dtype == GD_F32)
+        hipLaunchKernelGGL((gdn_prep<CP, float>), dim3(units), dim3(256), 0, ctx->stream, pa);
+    else
+        hipLaunchKernelGGL((gdn_prep<CP, uint16_t>), dim3(units), dim3(256), 0, ctx->stream, pa);
+    GD_LAUNCHED(ctx, "gdn_prep");
+    const dim3 grid((unsigned)(sa.nV * (DV / NCOL)));
+#define GD_SCAN(IO, OT) \
+    hipLaunchKernelGGL((gdn_scan<CP, IO, OT>), grid, dim3(256), 0, ctx->stream, sa)
+    if (io_dtype == GD_F32) { if (o_dtype == GD_F32) GD_SCAN(float, float); else GD_SCAN(float, uint16_t); }
+    else { if (o_dtype == GD_F32) GD_SCAN(uint16_t, float); else GD_SCAN(uint16_t, uint16_t); }
+#undef GD_SCAN
+    GD_LAUNCHED(ctx, "gdn_scan");
+    return GD_OK;
 }
 
 }  // namespace
@@ -258,38 +499,40 @@ extern "C" int gd_gdn_prefill(gd_ctx *ctx, int64_t T, int nV, int nK, int dk, in
     GD_REQUIRE(ctx, q_stride >= (int64_t)nK * dk && k_stride >= (int64_t)nK * dk &&
                         v_stride >= (int64_t)nV * dv && o_stride >= (int64_t)nV * dv,
                "gd_gdn_prefill: strides smaller than a token row");
+    // Rows are read 8 elements at a time.
+    const int vec = io_dtype == GD_F16 ? 8 : 4;
+    const int esz = io_dtype == GD_F16 ? 2 : 4;
+    GD_REQUIRE(ctx, q_stride % 8 == 0 && k_stride % 8 == 0 && v_stride % 8 == 0 &&
+                        ((uintptr_t)q % (vec * esz)) == 0 && ((uintptr_t)k % (vec * esz)) == 0 &&
+                        ((uintptr_t)v % (vec * esz)) == 0,
+               "gd_gdn_prefill: q/k/v rows must be 8-element strided and %d-byte aligned",
+               vec * esz);
     if (T == 0) return GD_OK;
     const int nchunks = (int)((T + C - 1) / C);
+    const int CP = C < 32 ? 32 : C;
     const size_t units = (size_t)nV * nchunks;
-    const size_t floats = units * ((size_t)C * DK + (size_t)C * DV + (size_t)C * C + C);
+    const size_t wbytes = units * CP * DK * 2;          // each of Wh, Wl
+    const size_t ubytes = units * CP * DV * 4;
+    const size_t pbytes = units * CP * CP * 2;          // each of Ph, Pl
+    const size_t kbytes = units * DK * CP * 2;
+    const size_t gbytes = units * CP * 4;
     void *ws = nullptr;
-    int rc = gd_ctx_workspace(ctx, floats * 4, &ws);
+    int rc = gd_ctx_workspace(ctx, 2 * wbytes + ubytes + 2 * pbytes + kbytes + gbytes, &ws);
     if (rc) return rc;
-    float *W = (float *)ws;
-    float *U = W + units * C * DK;
-    float *P = U + units * C * DV;
-    float *G = P + units * C * C;
+    uint8_t *p = (uint8_t *)ws;
+    Work w;
+    w.Wh = (f16 *)p;            p += wbytes;
+    w.Wl = (f16 *)p;            p += wbytes;
+    w.U = (float *)p;           p += ubytes;
+    w.Ph = (f16 *)p;            p += pbytes;
+    w.Pl = (f16 *)p;            p += pbytes;
+    w.KT = (f16 *)p;            p += kbytes;
+    w.G = (float *)p;
 
-    PrepArgs pa{q, k, v, q_stride, k_stride, v_stride, g, beta, W, U, P, G, T, nV, nK, C,
-                nchunks, qScale};
-    if (io_dtype == GD_F32)
-        hipLaunchKernelGGL(gdn_chunk_prep<float>, dim3((unsigned)units), dim3(256), 0,
-                           ctx->stream, pa);
-    else
-        hipLaunchKernelGGL(gdn_chunk_prep<uint16_t>, dim3((unsigned)units), dim3(256), 0,
-                           ctx->stream, pa);
-    GD_LAUNCHED(ctx, "gdn_chunk_prep");
-
-    ScanArgs sa{q, k, q_stride, k_stride, W, U, P, G, S, o, o_stride, T, nV, nK, C, nchunks,
-                qScale};
-    dim3 grid((unsigned)(nV * (DV / SCAN_COLS)));
-#define GD_SCAN(IO, OT) \
-    hipLaunchKernelGGL((gdn_chunk_scan<IO, OT>), grid, dim3(256), 0, ctx->stream, sa)
-    if (io_dtype == GD_F32) { if (o_dtype == GD_F32) GD_SCAN(float, float); else GD_SCAN(float, uint16_t); }
-    else { if (o_dtype == GD_F32) GD_SCAN(uint16_t, float); else GD_SCAN(uint16_t, uint16_t); }
-#undef GD_SCAN
-    GD_LAUNCHED(ctx, "gdn_chunk_scan");
-    return GD_OK;
+    PrepArgs pa{q, k, v, q_stride, k_stride, v_stride, g, beta, w, T, nV, nK, C, nchunks, qScale};
+    ScanArgs sa{q, q_stride, w, S, o, o_stride, T, nV, nK, C, nchunks, qScale};
+    return CP == 64 ? launch<64>(ctx, pa, sa, io_dtype, o_dtype)
+                    : launch<32>(ctx, pa, sa, io_dtype, o_dtype);
 }
 
 extern "C" int gd_gdn_scan_batch(gd_ctx *ctx, const float *convOutN, int keyDim, int valueDim,
@@ -303,4 +546,3 @@ extern "C" int gd_gdn_scan_batch(gd_ctx *ctx, const float *convOutN, int keyDim,
                           convOutN + 2 * keyDim, convDim, GD_F32, gN, betaN, S, oN, valueDim,
                           GD_F32, qScale, 64);
 }
-
