@@ -31,6 +31,13 @@ int gd_ctx_workspace(gd_ctx *ctx, size_t bytes, void **out);
 int gd_hip_fail(gd_ctx *ctx, hipError_t e, const char *what);
 // Host-side set-up of the GEMV for reduction length K (before graph capture).
 int gd_gemv_mfma_prepare(gd_ctx *ctx, int64_t K, int x_dtype);
+// Prefill GEMM plan: MT x 32 tokens by 4 x NT x 32 weight rows per
+// workgroup, K split `split` ways into f32 partials.
+struct gd_gemm_plan { int mt, nt, split; };
+gd_gemm_plan gd_gemm_choose(gd_ctx *ctx, int64_t T, int64_t K, int64_t R, int x_dtype);
+// split > 1: y_dtype f32 and Y holds split * T * R partials, summed by the caller.
+int gd_gemm_launch(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, int x_dtype, void *Y,
+                   int y_dtype, const gd_gemm_plan &p);
 
 #define GD_CHECK_CTX(ctx) \
     do { if (!(ctx)) return GD_EINVAL; } while (0)
@@ -78,6 +85,13 @@ __host__ __device__ inline size_t gd_q2_code_off(int64_t row, int64_t blk, int h
            ((size_t)(((blk & 3) << 4) | (row & 15)) << 4);
 }
 // Index (in f16 units) of the scale of block `blk` of row `row`.
+// Raw buffer resource over `bytes` bytes at p.  A load whose VGPR offset lies
+// past the end returns zeros without touching memory.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t gd_rsrc(const void *p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes,
+                                             0x00020000);
+}
+
 __host__ __device__ inline size_t gd_q2_scale_idx(int64_t row, int64_t blk, int64_t bgroups) {
     return (((((size_t)(row >> 4) * bgroups + (size_t)(blk >> 4)) << 4) | (size_t)(blk & 15))
             << 4) | (size_t)(row & 15);

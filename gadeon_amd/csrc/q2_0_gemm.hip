@@ -6,188 +6,403 @@
 // f32.  The CPU oracle is T calls of Q2_0.matvec (Quant.swift:36-77).
 //
 // MI355X design:
-//   * Workgroup tile 128 tokens x 128 weight rows, 4 waves of 64x64, each a
-//     2x2 grid of v_mfma_f32_32x32x16_f16 (fp16 operands, f32 accumulate).
-//   * Per K-slice of 64: X is staged to LDS as f16 (rounded if it arrives as
-//     f32, exactly where the reference rounds), and the weight codes are
-//     dequantized to (code-1)*d in f16 -- exact, as in dq_q2_0_h -- straight
-//     into LDS.  Both tiles are double-buffered so the next slice's global
-//     loads overlap this slice's MFMAs.
-//   * LDS rows are padded by 16 bytes so the ds_read_b128 operand fetches of
-//     8-lane groups hit distinct banks.
+//   * v_mfma_f32_32x32x16_f16 (fp16 operands, f32 accumulate): the fastest
+//     f16 MFMA shape on gfx950.  A = X (tokens), B = W (weight rows).
+//   * X is the heavy operand (16 bits per element against 2 for W), so it is
+//     the one staged through LDS and shared by the workgroup's 4 waves; each
+//     wave owns NT*32 weight rows and all MT*32 tokens of the tile.
+//   * W never touches LDS: each lane loads the 2-bit codes of its own B
+//     operand (8 bytes per 64-K slice) straight from the tiled device layout
+//     and expands them in registers to (code-1)*d in f16 -- exact, as in
+//     dq_q2_0_h.  To make a lane's codes one 8-byte word, the K order inside
+//     each 64-K slice is permuted: lane half h, step s, element e carries
+//     K = 32h + 8s + e, for X and W alike (a sum over K does not care).
+//   * X slices are double-buffered in LDS (rows padded by 16 bytes); the
+//     next slice's X and codes are loaded while the current one multiplies.
+//   * Short-R shapes split K across gridDim.z into f32 partials that the
+//     caller sums, so that every CU gets work.
 #include "gd_internal.h"
+
+#include <cstdlib>
+#include <cstdio>
 
 namespace {
 
-constexpr int BT = 128;          // tokens per workgroup tile
-constexpr int BR = 128;          // weight rows per workgroup tile
-constexpr int BK = 64;           // K per LDS stage
-constexpr int LDSW = BK + 8;     // padded row length in halves
+constexpr int BK = 64;           // K per LDS stage (half a Q2_0 block)
 constexpr int THREADS = 256;
 
-// Eight codes (bits 0..15 of `u`) -> four f16x2 of (code-1)*d, in K order.
-// 0x6400 | c is the f16 value 1024 + c; subtracting 1025 leaves c - 1 exactly,
-// and the product with d is exact (a small integer times an f16).
-__device__ __forceinline__ void dequant8(uint32_t u, f16x2 d2, uint32_t *out) {
+// Eight codes (bits 0..15 of `u`, code i at bits 2i) -> eight f16 of
+// (code-1)*d, in K order.  s = u | u << 14 puts code 2m+1 (bits 4m+2..3) at
+// bits 4m+16..17, so (s >> 4m) & 0x00030003 holds codes 2m and 2m+1 at the
+// bottom of each half; 0x6400 | c is the f16 value 1024 + c, subtracting 1025
+// leaves c - 1 exactly, and the product with d is exact.
+__device__ __forceinline__ f16x8 dequant8(uint32_t u, f16x2 d2) {
     const f16x2 off = {(f16)-1025.0f, (f16)-1025.0f};
+    const uint32_t sp = u | (u << 14);
+    u32x4 r;
 #pragma unroll
     for (int m = 0; m < 4; m++) {
-        const uint32_t lo = (u >> (4 * m)) & 3u;
-        const uint32_t hi = (u >> (4 * m + 2)) & 3u;
-        const uint32_t bits = lo | (hi << 16) | 0x64006400u;
-        f16x2 v = __builtin_bit_cast(f16x2, bits) + off;
-        v = v * d2;
-        out[m] = __builtin_bit_cast(uint32_t, v);
+        uint32_t bits;
+        asm("v_and_or_b32 %0, %1, %2, %3"
+            : "=v"(bits) : "v"(sp >> (4 * m)), "v"(0x00030003u), "s"(0x64006400u));
+        const f16x2 v = __builtin_bit_cast(f16x2, bits) + off;
+        r[m] = __builtin_bit_cast(uint32_t, v * d2);
     }
+    return __builtin_bit_cast(f16x8, r);
 }
 
-template <int XT, int YT>
-__global__ __launch_bounds__(THREADS) void q2_0_gemm_kernel(
-        const uint8_t *__restrict__ codes, const uint16_t *__restrict__ scales,
-        const void *__restrict__ Xv, void *__restrict__ Yv, int T, int K, int R) {
-    __shared__ __attribute__((aligned(16))) f16 Xs[2][BT * LDSW];
-    __shared__ __attribute__((aligned(16))) f16 Ws[2][BR * LDSW];
+// LDS position of 16-byte chunk c (0..7) of X tile row r: rows are 128
+// bytes, unpadded, with the chunk index XOR-swizzled by the row so that the
+// 16 (or 8) lanes served together by a ds_read_b128 of an A fragment (rows
+// r..r+15, one chunk index) land on distinct banks.
+__device__ __forceinline__ uint32_t xswz(int r) {
+    return (uint32_t)(((r >> 1) & 7) ^ ((r & 1) << 2));
+}
 
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int t0 = blockIdx.y * BT;
-    const int r0 = blockIdx.x * BR;
-    const int wr = wave & 1;         // token half of the tile
-    const int wc = wave >> 1;        // weight-row half
+// MT x 32 tokens by 4 * NT * 32 weight rows per workgroup; slices
+// [z * sps, min((z+1) * sps, K/64)) of K for split z.  YT: 0 = f32, 1 = f16.
+// With nz > 1 the output is f32 partials at Y + z * T * R.
+template <int MT, int NT, int XT, int YT>
+__global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2))) void q2_0_gemm_kernel(
+        const uint8_t *__restrict__ codes, const uint16_t *__restrict__ scales,
+        const void *__restrict__ Xv, void *__restrict__ Yv, int T, int K, int R, int sps,
+        int nrt, int nz, int per) {
+    constexpr int BT = MT * 32;
+    constexpr int XTILE = BT * BK * 2;                       // bytes of one X slice
+    __shared__ __attribute__((aligned(16))) uint8_t Xs[2][XTILE];
+    // Per lane and weight fragment: {codes lo, codes hi, scale, 0} of one slice.
+    __shared__ __attribute__((aligned(16))) u32x4 Cs[2][4 * NT * 64];
+
+    // Workgroup b runs on XCD b % 8.  Units (token tile, K split, row tile)
+    // are numbered token-tile-major and dealt to XCDs in contiguous runs of
+    // `per`, so each XCD's L2 holds one or two token tiles of X rather than
+    // all of it.
+    const int u = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+    if (u >= (int)((T + BT - 1) / BT) * nz * nrt) return;
+    const int rt = u % nrt, z = (u / nrt) % nz, tt = u / (nrt * nz);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 31, lh = lane >> 5;
+    const int t0 = tt * BT;
+    const int rw = rt * (4 * NT * 32) + wave * (NT * 32);   // this wave's first row
     const int nblk = K >> 7;
     const int csteps = (nblk + 3) >> 2;
     const int bgroups = (nblk + 15) >> 4;
+    const int s_begin = z * sps;
+    const int s_end = min(s_begin + sps, 2 * nblk);
 
-    // Global -> register staging for one K-slice.
-    u32x4 xr[4];                     // X: 4 x 8 halves per thread (f16 path)
-    f32x4 xf[8];                     // X: 4 x 8 floats per thread (f32 path)
-    uint32_t wc2[2];                 // 32 codes per thread
-    uint16_t wd;                     // their block scale
-
-    const int wrow = tid >> 1;       // weight row within the tile
-    const int wpart = tid & 1;       // which 32 codes of the 64-code slice
-
-    // Tile rows past T (tokens) or R (weight rows) re-read the last valid row:
-    // their outputs are never stored and no valid output depends on them, so
-    // the loads need no branch and all of them issue together.
-    auto load_slice = [&](int k0) {
+    // Buffer resources: X from token t0, codes and scales from this wave's
+    // first 16-row group.  Tokens past T and row groups past R lie beyond
+    // the resource and load as zeros; their outputs are never stored.
+    constexpr uint32_t ESZ = XT ? 4 : 2;
+    const __amdgpu_buffer_rsrc_t xrs =
+            gd_rsrc((const char *)Xv + (size_t)t0 * K * ESZ, (uint32_t)min(BT, T - t0) * K * ESZ);
+    const int g0 = rw >> 4, rgroups = (R + 15) >> 4;
+    const uint32_t gvalid = (uint32_t)max(0, min(2 * NT, rgroups - g0));
+    const __amdgpu_buffer_rsrc_t crs =
+            gd_rsrc(codes + ((size_t)g0 * csteps << 11), gvalid * (uint32_t)csteps * 2048u);
+    const __amdgpu_buffer_rsrc_t srs =
+            gd_rsrc(scales + (size_t)g0 * bgroups * 256, gvalid * (uint32_t)bgroups * 512u);
+    // This thread stages chunk (tid & 7) of X rows (tid >> 3) + 32 i.
+    const int xr0 = tid >> 3, xc = tid & 7;
+    const uint32_t xoff = (uint32_t)(xr0 * K + xc * 8) * ESZ;
+    const uint32_t xrowstep = 32u * (uint32_t)K * ESZ;
+    const uint32_t xlds = (uint32_t)xr0 * 128 + ((xc ^ xswz(xr0)) << 4);
+    // A-fragment reads: row m*32 + li, chunk 4*lh + ks.
+    uint32_t alds[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int seg = tid + THREADS * i;
-            const int row = seg >> 3, col = (seg & 7) * 8;
-            const int t = min(t0 + row, T - 1);
+    for (int ks = 0; ks < 4; ks++) alds[ks] = (uint32_t)li * 128 + (((4 * lh + ks) ^ xswz(li)) << 4);
+    uint32_t coff[NT], soff[NT];
+#pragma unroll
+    for (int n = 0; n < NT; n++) {
+        const int g = 2 * n + (li >> 4);                // row group relative to g0
+        coff[n] = ((uint32_t)(g * csteps) << 11) + ((li & 15) << 4) + 8 * lh;
+        soff[n] = ((uint32_t)g * bgroups * 256 + (li & 15)) * 2;
+    }
+
+    // X of slice s+1 is loaded into registers while slice s multiplies and
+    // is stored to LDS after it; codes and scales run one slice further
+    // ahead (they come from HBM), passing through LDS beside X.  The loop is
+    // unrolled by two over static buffers and register sets, so no register
+    // is ever copied (a copy would wait for its load).  Loads past the last
+    // slice re-read the last slice: they stay unconditional, which keeps the
+    // compiler's waits exact.
+    u32x4 xr[MT];                    // f16 X: MT chunks of 8 halves
+    f32x4 xf[XT ? 2 * MT : 1];       // f32 X
+    struct Codes { u32x2 c[NT]; uint32_t d[NT]; };
+    auto load_x = [&](int s) {
+        s = min(s, s_end - 1);
+        const uint32_t k0 = (uint32_t)s * BK * ESZ;
+#pragma unroll
+        for (int i = 0; i < MT; i++) {
             if (XT == 0) {
-                xr[i] = *(const u32x4 *)((const f16 *)Xv + (size_t)t * K + k0 + col);
+                xr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, xoff, k0 + i * xrowstep, 0));
             } else {
-                const f32x4 *p = (const f32x4 *)((const float *)Xv + (size_t)t * K + k0 + col);
-                xf[2 * i] = p[0];
-                xf[2 * i + 1] = p[1];
+                xf[2 * i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, xoff, k0 + i * xrowstep, 0));
+                xf[2 * i + 1] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, xoff + 16, k0 + i * xrowstep, 0));
             }
         }
-        // Codes k0 .. k0+63 of a row are one 16-byte slot of its tile
-        // (half (k0/64)%2 of block k0/128); this thread takes 8 bytes of it.
-        const int r = min(r0 + wrow, R - 1);
-        const u32x2 v = *(const u32x2 *)(codes + gd_q2_code_off(r, k0 >> 7, (k0 >> 6) & 1, csteps) +
-                                         8 * wpart);
-        wc2[0] = v[0];
-        wc2[1] = v[1];
-        wd = scales[gd_q2_scale_idx(r, k0 >> 7, bgroups)];
     };
-
-    auto store_slice = [&](int buf) {
+    auto load_c = [&](int s, Codes &st) {
+        s = min(s, s_end - 1);
+        const int blk = s >> 1, h = s & 1;
+        const uint32_t cs = ((uint32_t)(blk >> 2) << 11) + ((uint32_t)h << 10) + ((uint32_t)(blk & 3) << 8);
+        const uint32_t ss = ((uint32_t)(blk >> 4) * 256 + (blk & 15) * 16) * 2;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int seg = tid + THREADS * i;
-            const int row = seg >> 3, col = (seg & 7) * 8;
+        for (int n = 0; n < NT; n++) {
+            st.c[n] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(crs, coff[n], cs, 0));
+            st.d[n] = __builtin_amdgcn_raw_buffer_load_b16(srs, soff[n], ss, 0);
+        }
+    };
+    auto store_x = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < MT; i++) {
             u32x4 v;
             if (XT == 0) {
                 v = xr[i];
             } else {
-                f16x8 h;
+                f16x8 hv;
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
-                    h[e] = (f16)xf[2 * i][e];
-                    h[4 + e] = (f16)xf[2 * i + 1][e];
+                    hv[e] = (f16)xf[2 * i][e];
+                    hv[4 + e] = (f16)xf[2 * i + 1][e];
                 }
-                v = __builtin_bit_cast(u32x4, h);
+                v = __builtin_bit_cast(u32x4, hv);
             }
-            *(u32x4 *)&Xs[buf][row * LDSW + col] = v;
+            *(u32x4 *)&Xs[buf][xlds + i * 4096] = v;
         }
-        const f16 d = __builtin_bit_cast(f16, wd);
-        const f16x2 d2 = {d, d};
-        uint32_t out[16];
-        dequant8(wc2[0] & 0xffffu, d2, out);
-        dequant8(wc2[0] >> 16, d2, out + 4);
-        dequant8(wc2[1] & 0xffffu, d2, out + 8);
-        dequant8(wc2[1] >> 16, d2, out + 12);
-        u32x4 *dst = (u32x4 *)&Ws[buf][wrow * LDSW + 32 * wpart];
+    };
+    auto store_c = [&](int buf, const Codes &st) {
 #pragma unroll
-        for (int i = 0; i < 4; i++)
-            dst[i] = u32x4{out[4 * i], out[4 * i + 1], out[4 * i + 2], out[4 * i + 3]};
+        for (int n = 0; n < NT; n++)
+            Cs[buf][(wave * NT + n) * 64 + lane] = u32x4{st.c[n][0], st.c[n][1], st.d[n], 0u};
     };
 
-    f32x16 acc[2][2];
+    f32x16 acc[MT][NT];
 #pragma unroll
-    for (int a = 0; a < 2; a++)
+    for (int m = 0; m < MT; m++)
 #pragma unroll
-        for (int b = 0; b < 2; b++)
+        for (int n = 0; n < NT; n++)
 #pragma unroll
-            for (int v = 0; v < 16; v++) acc[a][b][v] = 0.f;
+            for (int v = 0; v < 16; v++) acc[m][n][v] = 0.f;
 
-    const int nslices = K / BK;
-    load_slice(0);
-    store_slice(0);
-    __syncthreads();
-
-    const int li = lane & 31, lh = lane >> 5;
-    for (int s = 0; s < nslices; s++) {
-        const int buf = s & 1;
-        if (s + 1 < nslices) load_slice((s + 1) * BK);
+    // One slice: 4 K-steps of 16.  The A fragments and the dequantized B
+    // fragments of step ks+1 are fetched and built while step ks's MFMAs
+    // run, so no MFMA waits on an LDS read it has just issued.
+    auto compute = [&](int buf) {
+        u32x2 cw[NT];
+        f16x2 d2[NT];
 #pragma unroll
-        for (int ks = 0; ks < BK / 16; ks++) {
-            f16x8 a[2], b[2];
-#pragma unroll
-            for (int m = 0; m < 2; m++)
-                a[m] = *(const f16x8 *)&Xs[buf][(wr * 64 + m * 32 + li) * LDSW + ks * 16 + 8 * lh];
-#pragma unroll
-            for (int n = 0; n < 2; n++)
-                b[n] = *(const f16x8 *)&Ws[buf][(wc * 64 + n * 32 + li) * LDSW + ks * 16 + 8 * lh];
-#pragma unroll
-            for (int m = 0; m < 2; m++)
-#pragma unroll
-                for (int n = 0; n < 2; n++)
-                    acc[m][n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[m], b[n], acc[m][n], 0, 0, 0);
+        for (int n = 0; n < NT; n++) {
+            const u32x4 rec = Cs[buf][(wave * NT + n) * 64 + lane];
+            cw[n] = u32x2{rec[0], rec[1]};
+            const f16 d = __builtin_bit_cast(f16, (uint16_t)rec[2]);
+            d2[n] = f16x2{d, d};
         }
-        if (s + 1 < nslices) store_slice(buf ^ 1);
+        f16x8 a[2][MT], b[2][NT];
+#pragma unroll
+        for (int m = 0; m < MT; m++) a[0][m] = *(const f16x8 *)&Xs[buf][alds[0] + m * 4096];
+#pragma unroll
+        for (int n = 0; n < NT; n++) b[0][n] = dequant8(cw[n][0] & 0xffffu, d2[n]);
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            const int cur = ks & 1, nxt = cur ^ 1;
+            if (ks < 3) {
+#pragma unroll
+                for (int m = 0; m < MT; m++)
+                    a[nxt][m] = *(const f16x8 *)&Xs[buf][alds[ks + 1] + m * 4096];
+#pragma unroll
+                for (int n = 0; n < NT; n++)
+                    b[nxt][n] = dequant8((cw[n][(ks + 1) >> 1] >> (16 * ((ks + 1) & 1))) & 0xffffu, d2[n]);
+            }
+#pragma unroll
+            for (int m = 0; m < MT; m++)
+#pragma unroll
+                for (int n = 0; n < NT; n++)
+                    acc[m][n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[cur][m], b[cur][n], acc[m][n], 0, 0, 0);
+            if (ks < 3) {
+                // Interleave: each MFMA followed by a share of the next
+                // step's VALU (dequant) and LDS reads.
+#pragma unroll
+                for (int i = 0; i < MT * NT; i++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, (17 * NT + MT * NT - 1) / (MT * NT), 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                }
+            }
+        }
+    };
+
+    Codes CA, CB;
+    load_x(s_begin);
+    load_c(s_begin, CA);
+    store_x(0);
+    store_c(0, CA);
+    load_c(s_begin + 1, CB);
+    __syncthreads();
+    // Even step: LDS buffer 0 holds slice s, CB holds codes of s+1.  Odd
+    // step: buffer 1 holds s+1, CA holds codes of s+2.  Every split holds an
+    // even number of slices (the host guarantees it), so the loop runs whole
+    // pairs and the accumulators never change registers.
+    for (int s = s_begin; s < s_end; s += 2) {
+        load_x(s + 1);
+        load_c(s + 2, CA);
+        compute(0);
+        store_x(1);
+        store_c(1, CB);
+        __syncthreads();
+        load_x(s + 2);
+        load_c(s + 3, CB);
+        compute(1);
+        store_x(0);
+        store_c(0, CA);
         __syncthreads();
     }
 
     // D layout of the 32x32 MFMA: lane holds column li (weight row) and rows
     // 8*(v/4) + 4*lh + (v%4) (tokens) for v < 16.
+    const size_t zoff = (size_t)z * T * R;
 #pragma unroll
-    for (int m = 0; m < 2; m++)
+    for (int n = 0; n < NT; n++) {
+        const int r = rw + n * 32 + li;
+        if (r >= R) continue;
 #pragma unroll
-        for (int n = 0; n < 2; n++) {
-            const int r = r0 + wc * 64 + n * 32 + li;
-            if (r >= R) continue;
+        for (int m = 0; m < MT; m++)
 #pragma unroll
             for (int v = 0; v < 16; v++) {
-                const int t = t0 + wr * 64 + m * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
+                const int t = t0 + m * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
                 if (t < T) {
-                    if (YT == 0) ((float *)Yv)[(size_t)t * R + r] = acc[m][n][v];
-                    else ((uint16_t *)Yv)[(size_t)t * R + r] = gd_f2h(acc[m][n][v]);
+                    const size_t i = zoff + (size_t)t * R + r;
+                    if (YT == 0) ((float *)Yv)[i] = acc[m][n][v];
+                    else ((uint16_t *)Yv)[i] = gd_f2h(acc[m][n][v]);
                 }
+                // Store fragment by fragment: without the fence the compiler
+                // converts every accumulator up front and the extra VGPRs
+                // halve the occupancy of the whole kernel.
+                if (v == 15) __builtin_amdgcn_sched_barrier(0);
             }
-        }
+    }
+}
+
+// Y[i] = sum_z P[z][i] (n elements, 4 per thread).
+template <int YT>
+__global__ __launch_bounds__(256) void q2_0_gemm_reduce(const float *__restrict__ P,
+                                                        void *__restrict__ Y, size_t n, int nz) {
+    const size_t i = ((size_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (i >= n) return;
+    f32x4 a = *(const f32x4 *)(P + i);
+    for (int z = 1; z < nz; z++) a += *(const f32x4 *)(P + (size_t)z * n + i);
+    if (YT == 0) {
+        *(f32x4 *)((float *)Y + i) = a;
+    } else {
+        uint16_t *o = (uint16_t *)Y + i;
+        o[0] = gd_f2h(a[0]);
+        o[1] = gd_f2h(a[1]);
+        o[2] = gd_f2h(a[2]);
+        o[3] = gd_f2h(a[3]);
+    }
+}
+
+typedef void (*gemm_fn)(const uint8_t *, const uint16_t *, const void *, void *, int, int, int,
+                        int, int, int, int);
+
+template <int MT, int NT>
+gemm_fn pick(int x_dtype, int yt) {
+    if (x_dtype == GD_F16) return yt ? q2_0_gemm_kernel<MT, NT, 0, 1> : q2_0_gemm_kernel<MT, NT, 0, 0>;
+    // f32 X stages twice the bytes: only the smaller tiles fit two waves
+    // per SIMD without spilling.
+    if constexpr (MT * NT <= 4)
+        return yt ? q2_0_gemm_kernel<MT, NT, 1, 1> : q2_0_gemm_kernel<MT, NT, 1, 0>;
+    return nullptr;
+}
+
+gemm_fn kernel_for(int mt, int nt, int x_dtype, int yt) {
+    if (mt == 8 && nt == 1) return pick<8, 1>(x_dtype, yt);
+    if (mt == 4 && nt == 2) return pick<4, 2>(x_dtype, yt);
+    if (mt == 4 && nt == 1) return pick<4, 1>(x_dtype, yt);
+    if (mt == 2 && nt == 2) return pick<2, 2>(x_dtype, yt);
+    return nullptr;
 }
 
 }  // namespace
 
 int gd_check_q2w(gd_ctx *ctx, const gd_q2w *w, const char *who);
 
-extern "C" int gd_q2_0_gemm(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X,
-                            int x_dtype, void *Y, int y_dtype) {
+// Tile shape and K split for a T x K x R product, from a cost model fitted
+// to MI355X timings of every plan on the stack's six prefill shapes (its
+// picks land within 1% of the best measured plan there):
+//   * a CU completes about 3.5 TFLOP/s of this kernel once it holds two or
+//     more workgroups, whatever the tile; a lone workgroup of the smaller
+//     tiles runs slower (LONE);
+//   * workgroups are dealt evenly, so the busiest CU runs ceil(units / CUs)
+//     of them, each for its slices plus about two slices of prologue and
+//     store;
+//   * split partials cost (2s+1) f32 passes over T x R at about 7 TB/s.
+// GADEON_GEMM_CFG="MT,NT,S" forces a plan.
+gd_gemm_plan gd_gemm_choose(gd_ctx *ctx, int64_t T, int64_t K, int64_t R, int x_dtype) {
+    static const char *force = getenv("GADEON_GEMM_CFG");
+    const int nslices = (int)(K / BK);
+    auto nz_of = [&](int s) {
+        const int sps = 2 * ((nslices / 2 + s - 1) / s);
+        return (nslices + sps - 1) / sps;
+    };
+    if (force) {
+        int mt = 4, nt = 2, s = 1;
+        if (sscanf(force, "%d,%d,%d", &mt, &nt, &s) == 3 && kernel_for(mt, nt, x_dtype, 0) &&
+            s >= 1 && s <= 16)
+            return gd_gemm_plan{mt, nt, nz_of(s)};
+    }
+    const int cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
+    struct Shape { int mt, nt; double us_per_slice, lone; };
+    // us_per_slice: one slice (64 K) of one workgroup tile at CU saturation.
+    const Shape shapes[4] = {{4, 1, 0.6, 1.33}, {2, 2, 0.7, 1.4}, {4, 2, 1.2, 1.05},
+                             {8, 1, 1.25, 1.05}};
+    gd_gemm_plan best{4, 1, 1};
+    double best_cost = 1e30;
+    for (const Shape &sh : shapes) {
+        if (!kernel_for(sh.mt, sh.nt, x_dtype, 0)) continue;
+        const int64_t tiles = ((T + sh.mt * 32 - 1) / (sh.mt * 32)) *
+                              ((R + 4 * sh.nt * 32 - 1) / (4 * sh.nt * 32));
+        for (int s = 1; s <= 8; s++) {
+            const int sps = 2 * ((nslices / 2 + s - 1) / s);
+            if (s > 1 && (int64_t)(s - 1) * sps >= nslices) break;
+            const int64_t per = (tiles * s + cus - 1) / cus;
+            double cost = (double)per * (sps + 2) * sh.us_per_slice * (per == 1 ? sh.lone : 1.0);
+            if (s > 1) cost += (2.0 * s + 1) * (double)T * R * 4 / 7e6;
+            if (cost < best_cost) {
+                best_cost = cost;
+                best = gd_gemm_plan{sh.mt, sh.nt, s};
+            }
+        }
+    }
+    return best;
+}
+
+// Launch one plan.  plan.split > 1 requires y_dtype f32 and Y sized
+// split * T * R (partials, summed by the caller).
+int gd_gemm_launch(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, int x_dtype, void *Y,
+                   int y_dtype, const gd_gemm_plan &p) {
+    const int K = (int)w->K, R = (int)w->R;
+    const int nslices = K / BK;                         // even: K is whole blocks
+    const int sps = 2 * ((nslices / 2 + p.split - 1) / p.split);
+    const int nz = (nslices + sps - 1) / sps;
+    gemm_fn f = kernel_for(p.mt, p.nt, x_dtype, p.split > 1 ? 0 : (y_dtype == GD_F16));
+    GD_REQUIRE(ctx, f && (p.split == 1 || y_dtype == GD_F32) && nz == p.split,
+               "gd_q2_0_gemm: bad plan %d,%d,%d", p.mt, p.nt, p.split);
+    const int nrt = gd_blocks(R, 4 * p.nt * 32);
+    const int64_t units = (int64_t)gd_blocks(T, p.mt * 32) * nz * nrt;
+    const int per = (int)((units + 7) / 8);
+    hipLaunchKernelGGL(f, dim3(8 * per), dim3(THREADS), 0, ctx->stream, (const uint8_t *)w->codes,
+                       (const uint16_t *)w->scales, X, Y, (int)T, K, R, sps, nrt, nz, per);
+    GD_LAUNCHED(ctx, "q2_0_gemm");
+    return GD_OK;
+}
+
+namespace {
+
+// Checks shared by both entry points, then the plan (split partials summed
+// into Y through the context workspace).
+int gemm_run(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, int x_dtype, void *Y,
+             int y_dtype, const gd_gemm_plan *forced) {
     GD_CHECK_CTX(ctx);
     int rc = gd_check_q2w(ctx, w, "gd_q2_0_gemm");
     if (rc) return rc;
@@ -197,24 +412,52 @@ extern "C" int gd_q2_0_gemm(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void 
                         (y_dtype == GD_F32 || y_dtype == GD_F16),
                "gd_q2_0_gemm: bad dtypes x=%d y=%d", x_dtype, y_dtype);
     GD_REQUIRE(ctx, ((uintptr_t)X & 15) == 0, "gd_q2_0_gemm: X must be 16-byte aligned");
-    GD_REQUIRE(ctx, w->K <= (1 << 24) && w->R < (1LL << 31) && (size_t)T * w->R < (1ULL << 62),
+    // Buffer offsets are 32-bit: a 256-token X tile and a wave's code rows
+    // must stay below 4 GiB.
+    GD_REQUIRE(ctx, w->K <= (1 << 22) && w->R < (1LL << 31) && (size_t)T * w->R < (1ULL << 62),
                "gd_q2_0_gemm: shape too large");
-    const int K = (int)w->K, R = (int)w->R;
-    dim3 grid(gd_blocks(R, BR), gd_blocks(T, BT));
-    auto *c = (const uint8_t *)w->codes;
-    auto *s = (const uint16_t *)w->scales;
-    if (x_dtype == GD_F16 && y_dtype == GD_F32)
-        hipLaunchKernelGGL((q2_0_gemm_kernel<0, 0>), grid, dim3(THREADS), 0, ctx->stream, c, s, X,
-                           Y, (int)T, K, R);
-    else if (x_dtype == GD_F16)
-        hipLaunchKernelGGL((q2_0_gemm_kernel<0, 1>), grid, dim3(THREADS), 0, ctx->stream, c, s, X,
-                           Y, (int)T, K, R);
-    else if (y_dtype == GD_F32)
-        hipLaunchKernelGGL((q2_0_gemm_kernel<1, 0>), grid, dim3(THREADS), 0, ctx->stream, c, s, X,
-                           Y, (int)T, K, R);
+    gd_gemm_plan p;
+    if (forced) {
+        GD_REQUIRE(ctx, kernel_for(forced->mt, forced->nt, x_dtype, 0) && forced->split >= 1 &&
+                            forced->split <= 16,
+                   "gd_q2_0_gemm_plan: no kernel for mt=%d nt=%d split=%d with this X dtype",
+                   forced->mt, forced->nt, forced->split);
+        p = *forced;
+        const int nslices = (int)(w->K / BK);
+        const int sps = 2 * ((nslices / 2 + p.split - 1) / p.split);
+        p.split = (nslices + sps - 1) / sps;           // splits that hold slices
+    } else {
+        p = gd_gemm_choose(ctx, T, w->K, w->R, x_dtype);
+    }
+    const size_t n = (size_t)T * w->R;
+    // Partials are summed 4 at a time: odd-sized outputs run unsplit.
+    if (n % 4) p.split = 1;
+    if (p.split == 1) return gd_gemm_launch(ctx, w, T, X, x_dtype, Y, y_dtype, p);
+    void *part = nullptr;
+    rc = gd_ctx_workspace(ctx, n * p.split * 4, &part);
+    if (rc) return rc;
+    rc = gd_gemm_launch(ctx, w, T, X, x_dtype, part, GD_F32, p);
+    if (rc) return rc;
+    const unsigned blocks = (unsigned)gd_blocks((int64_t)(n / 4), 256);
+    if (y_dtype == GD_F32)
+        hipLaunchKernelGGL(q2_0_gemm_reduce<0>, dim3(blocks), dim3(256), 0, ctx->stream,
+                           (const float *)part, Y, n, p.split);
     else
-        hipLaunchKernelGGL((q2_0_gemm_kernel<1, 1>), grid, dim3(THREADS), 0, ctx->stream, c, s, X,
-                           Y, (int)T, K, R);
-    GD_LAUNCHED(ctx, "q2_0_gemm");
+        hipLaunchKernelGGL(q2_0_gemm_reduce<1>, dim3(blocks), dim3(256), 0, ctx->stream,
+                           (const float *)part, Y, n, p.split);
+    GD_LAUNCHED(ctx, "q2_0_gemm_reduce");
     return GD_OK;
+}
+
+}  // namespace
+
+extern "C" int gd_q2_0_gemm(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X,
+                            int x_dtype, void *Y, int y_dtype) {
+    return gemm_run(ctx, w, T, X, x_dtype, Y, y_dtype, nullptr);
+}
+
+extern "C" int gd_q2_0_gemm_plan(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X,
+                                 int x_dtype, void *Y, int y_dtype, int mt, int nt, int split) {
+    const gd_gemm_plan p{mt, nt, split};
+    return gemm_run(ctx, w, T, X, x_dtype, Y, y_dtype, &p);
 }

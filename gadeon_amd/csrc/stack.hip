@@ -341,18 +341,20 @@ __global__ __launch_bounds__(128) void k_argmax_final(const float *pv, const int
 
 // x += y over rows of n, then y16 = rmsnorm(x) * w as f16 (the residual add
 // and the following norm, BonsaiEngine.swift:169-171).  One block per row.
+// x += sum of the nsplit partials y + z * ystride (split-K GEMM output),
+// then out = f16(rmsnorm(x) * w).  y may be null (norm only).
 __global__ __launch_bounds__(1024) void k_add_rmsnorm(float *x, const float *y, const float *w,
-                                                      uint16_t *out, int n, float eps) {
+                                                      uint16_t *out, int n, float eps,
+                                                      int nsplit, int64_t ystride) {
     __shared__ float red[16];
     const int64_t row = blockIdx.x;
     float *xr = x + row * n;
-    const float *yr = y + row * n;
+    const float *yr = y ? y + row * n : nullptr;
     float ss = 0.f;
     for (int i = threadIdx.x * 4; i < n; i += blockDim.x * 4) {
         f32x4 a = *(const f32x4 *)(xr + i);
         if (yr) {
-            const f32x4 b = *(const f32x4 *)(yr + i);
-            a += b;
+            for (int z = 0; z < nsplit; z++) a += *(const f32x4 *)(yr + z * ystride + i);
             *(f32x4 *)(xr + i) = a;
         }
         ss += a[0] * a[0] + a[1] * a[1] + a[2] * a[2] + a[3] * a[3];
@@ -461,7 +463,7 @@ int forward(gd_stack *st, int N, bool decode) {
     // attn_norm of layer 0; every later norm is fused with the residual add
     // that precedes it (k_add_rmsnorm).
     K_(k_add_rmsnorm, dim3(N), dim3(1024), 0, s, st->x, (const float *)nullptr,
-       st->L[0].attn_norm, st->xn16, E, eps);
+       st->L[0].attn_norm, st->xn16, E, eps, 0, (int64_t)0);
     for (int il = 0; il < c.n_layer; il++) {
         StackLayer &ly = st->L[il];
         const int RP = ly.rec ? st->rp_rec : st->rp_att;
@@ -508,25 +510,39 @@ int forward(gd_stack *st, int N, bool decode) {
                    c.kv_block, scale);
             }
         }
-        if (decode) R_(gd_q2_0_gemv(ctx, &ly.out_proj, st->a16, GD_F16, st->contrib));
-        else R_(gd_q2_0_gemm(ctx, &ly.out_proj, N, st->a16, GD_F16, st->contrib, GD_F32));
+        // Output projections feed only the residual add: a split-K plan
+        // leaves its partials in contrib and k_add_rmsnorm sums them.
+        int nsplit = 1;
+        if (decode) {
+            R_(gd_q2_0_gemv(ctx, &ly.out_proj, st->a16, GD_F16, st->contrib));
+        } else {
+            const gd_gemm_plan p = gd_gemm_choose(ctx, N, ly.out_proj.K, ly.out_proj.R, GD_F16);
+            nsplit = p.split;
+            R_(gd_gemm_launch(ctx, &ly.out_proj, N, st->a16, GD_F16, st->contrib, GD_F32, p));
+        }
         K_(k_add_rmsnorm, dim3(N), dim3(1024), 0, s, st->x, st->contrib, ly.post_norm, st->xn16,
-           E, eps);
+           E, eps, nsplit, (int64_t)N * E);
         if (decode) R_(gd_q2_0_gemv(ctx, &ly.gate_up, st->xn16, GD_F16, st->proj));
         else R_(gd_q2_0_gemm(ctx, &ly.gate_up, N, st->xn16, GD_F16, st->proj, GD_F32));
         K_(k_swiglu, dim3(gd_blocks((int64_t)N * FF, 256)), dim3(256), 0, s, st->proj, FF,
            st->a16, N);
-        if (decode) R_(gd_q2_0_gemv(ctx, &ly.down, st->a16, GD_F16, st->contrib));
-        else R_(gd_q2_0_gemm(ctx, &ly.down, N, st->a16, GD_F16, st->contrib, GD_F32));
+        nsplit = 1;
+        if (decode) {
+            R_(gd_q2_0_gemv(ctx, &ly.down, st->a16, GD_F16, st->contrib));
+        } else {
+            const gd_gemm_plan p = gd_gemm_choose(ctx, N, ly.down.K, ly.down.R, GD_F16);
+            nsplit = p.split;
+            R_(gd_gemm_launch(ctx, &ly.down, N, st->a16, GD_F16, st->contrib, GD_F32, p));
+        }
         if (il + 1 < c.n_layer) {
             K_(k_add_rmsnorm, dim3(N), dim3(1024), 0, s, st->x, st->contrib,
-               st->L[il + 1].attn_norm, st->xn16, E, eps);
+               st->L[il + 1].attn_norm, st->xn16, E, eps, nsplit, (int64_t)N * E);
         } else {
             // Only the last token's hidden feeds the logits: residual add and
             // final norm on that row alone.
             const int64_t last = (int64_t)(N - 1) * E;
             K_(k_add_rmsnorm, dim3(1), dim3(1024), 0, s, st->x + last, st->contrib + last,
-               st->out_norm, st->xn16, E, eps);
+               st->out_norm, st->xn16, E, eps, nsplit, (int64_t)N * E);
         }
     }
     // Tied lm_head on the last token, greedy pick, position bump.
@@ -628,7 +644,8 @@ extern "C" int gd_stack_create(gd_ctx *ctx, const gd_stack_config *cfg, uint64_t
     C_(salloc_t(st, (size_t)B * maxproj, &st->proj));
     C_(salloc_t(st, (size_t)B * st->convDim, &st->conv_out));
     C_(salloc_t(st, (size_t)B * st->valDim, &st->o32));
-    C_(salloc_t(st, (size_t)B * E, &st->contrib));
+    // Room for the split-K partials of the output projections (at most 8).
+    C_(salloc_t(st, (size_t)8 * B * E, &st->contrib));
     C_(salloc_t(st, (size_t)B * c.n_v_head, &st->beta));
     C_(salloc_t(st, (size_t)B * c.n_v_head, &st->g));
     C_(salloc_t(st, (size_t)B * c.n_head * HD, &st->q32));

@@ -150,13 +150,22 @@ int gd_q2_0_gemv(gd_ctx *ctx, const gd_q2w *w, const void *x, int x_dtype,
 
 /* ---- Q2_0 GEMM (prefill): MetalEnc.gemm, MetalEnc.swift:145-189 --------------
  * Y[t][r] = sum_k X[t][k] * W[r][k], token-major X[T][K] and Y[T][R].
- * Weights are dequantized to f16 tiles in LDS and multiplied on fp16 MFMA
- * with f32 accumulation (reference: q2_0_gemm_mm_h, Kernels.metal:372-466,
- * which stages both operands as half).  X dtype GD_F32 is rounded to f16
- * while staging, as the reference does (Kernels.metal:428); Y dtype GD_F32
- * or GD_F16 (round-to-nearest-even of the f32 accumulator). */
+ * Weights are dequantized exactly to f16 in registers and multiplied on fp16
+ * MFMA with f32 accumulation (reference: q2_0_gemm_mm_h,
+ * Kernels.metal:372-466, which stages both operands as half).  X dtype GD_F32
+ * is rounded to f16 while staging, as the reference does (Kernels.metal:428);
+ * Y dtype GD_F32 or GD_F16 (round-to-nearest-even of the f32 accumulator).
+ * The tile shape and K split are chosen by a cost model of the MI355X. */
 int gd_q2_0_gemm(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X,
                  int x_dtype, void *Y, int y_dtype);
+
+/* gd_q2_0_gemm with an explicit plan: workgroup tiles of mt*32 tokens by
+ * 4*nt*32 weight rows, (mt, nt) in {(4,1), (2,2), (4,2), (8,1)} ((4,2) and
+ * (8,1) need f16 X), and K split `split` ways (1..16; partials summed in the
+ * context workspace).  For tuning and for tests that cover every kernel
+ * variant; no counterpart in the reference. */
+int gd_q2_0_gemm_plan(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X,
+                      int x_dtype, void *Y, int y_dtype, int mt, int nt, int split);
 
 /* ---- Q2_0 row dequant: MetalEnc.dequantRow / embedBatch ----------------------
  * out[n][k] = (code-1)*d of row ids[n], exactly (f16 * small integer is exact

@@ -157,6 +157,49 @@ def test_gemm_vs_oracle(ctx, T, K, R, xt, yt):
     free_w(ctx, w)
 
 
+PLANS_F16 = [(4, 1), (2, 2), (4, 2), (8, 1)]
+PLANS_F32 = [(4, 1), (2, 2)]
+
+
+@pytest.mark.parametrize("xt,yt,mt,nt", [(ga.F16, yt, mt, nt) for mt, nt in PLANS_F16
+                                         for yt in (ga.F32, ga.F16)] +
+                         [(ga.F32, ga.F32, mt, nt) for mt, nt in PLANS_F32])
+@pytest.mark.parametrize("split", [1, 3])
+def test_gemm_every_plan(ctx, xt, yt, mt, nt, split):
+    """Every tile shape and a K split against the oracle, on a ragged shape:
+    T and R are not multiples of any tile and K/64 = 42 slices do not divide
+    evenly into 3 splits of an even slice count."""
+    T, K, R = 200, 2688, 700
+    blocks = O.lcg_q2_0(K, R, 11 * mt + nt)
+    w = upload_w(ctx, blocks, K, R)
+    Xh = O.lcg_normal_f16(T * K, 78).reshape(T, K)
+    X = Xh.view(np.uint16) if xt == ga.F16 else Xh.astype(np.float32)
+    dX = ctx.put(X)
+    dY = ctx.alloc(T * R * (4 if yt == ga.F32 else 2))
+    ctx.gd_q2_0_gemm_plan(C.byref(w), T, dX, xt, dY, yt, mt, nt, split)
+    Y = ctx.get(dY, (T, R), np.float32 if yt == ga.F32 else np.float16).astype(np.float32)
+    want = np.stack([O.q2_0_matvec(blocks, K, R, Xh[t].astype(np.float32), threads=8)
+                     for t in range(T)])
+    assert rel_diff(Y, want) < (2e-3 if yt == ga.F16 else 1e-4)
+    ctx.free(dX)
+    ctx.free(dY)
+    free_w(ctx, w)
+
+
+def test_gemm_plan_rejects_unknown_tile(ctx):
+    w = ga.Q2W()
+    ctx.gd_q2w_alloc(256, 64, C.byref(w))
+    dX = ctx.alloc(4 * 256 * 4)
+    dY = ctx.alloc(4 * 64 * 4)
+    with pytest.raises(RuntimeError, match="no kernel"):
+        ctx.gd_q2_0_gemm_plan(C.byref(w), 4, dX, ga.F32, dY, ga.F32, 4, 2, 1)
+    with pytest.raises(RuntimeError, match="no kernel"):
+        ctx.gd_q2_0_gemm_plan(C.byref(w), 4, dX, ga.F16, dY, ga.F32, 3, 1, 1)
+    ctx.free(dX)
+    ctx.free(dY)
+    ctx.gd_q2w_free(C.byref(w))
+
+
 def test_gemm_full_size_sampled_rows(ctx):
     """BASELINE config 1 shapes at full size: every output row against the GPU
     GEMV of the same weights (independent kernel), and 48 sampled rows x all
