@@ -31,6 +31,9 @@ int gd_ctx_workspace(gd_ctx *ctx, size_t bytes, void **out);
 int gd_hip_fail(gd_ctx *ctx, hipError_t e, const char *what);
 // Host-side set-up of the GEMV for reduction length K (before graph capture).
 int gd_gemv_mfma_prepare(gd_ctx *ctx, int64_t K, int x_dtype);
+// GEMV of x = f16(rmsnorm(h + delta) * normw); hout <- h + delta if not null.
+int gd_gemv_mfma_norm(gd_ctx *ctx, const gd_q2w *w, const float *h, const float *delta,
+                      const float *normw, float eps, float *hout, float *y);
 // Prefill GEMM plan: MT x 32 tokens by 4 x NT x 32 weight rows per
 // workgroup, K split `split` ways into f32 partials.
 struct gd_gemm_plan { int mt, nt, split; };

@@ -77,3 +77,20 @@ extern "C" int gd_q2_0_gemv(gd_ctx *ctx, const gd_q2w *w, const void *x, int x_d
                (long long)w->R);
     return gd_gemv_mfma(ctx, w, x, x_dtype, y);
 }
+
+extern "C" int gd_q2_0_gemv_norm(gd_ctx *ctx, const gd_q2w *w, const float *h,
+                                 const float *delta, const float *w_norm, float eps,
+                                 float *hout, float *y) {
+    GD_CHECK_CTX(ctx);
+    int rc = gd_check_q2w(ctx, w, "gd_q2_0_gemv_norm");
+    if (rc) return rc;
+    GD_REQUIRE(ctx, h && w_norm && y, "gd_q2_0_gemv_norm: null h, w_norm or y");
+    GD_REQUIRE(ctx, hout != h, "gd_q2_0_gemv_norm: hout must not alias h");
+    GD_REQUIRE(ctx, ((uintptr_t)h & 15) == 0 && ((uintptr_t)delta & 15) == 0 &&
+                        ((uintptr_t)w_norm & 15) == 0 && ((uintptr_t)hout & 15) == 0,
+               "gd_q2_0_gemv_norm: h, delta, w_norm, hout must be 16-byte aligned");
+    GD_REQUIRE(ctx, w->K <= 15744 && w->R < (1LL << 30),
+               "gd_q2_0_gemv_norm: K=%lld (at most 15744) or R=%lld too large",
+               (long long)w->K, (long long)w->R);
+    return gd_gemv_mfma_norm(ctx, w, h, delta, w_norm, eps, hout, y);
+}

@@ -94,17 +94,30 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint3
 constexpr int CP_NT = 2;   // cache policy: non-temporal (streamed once)
 
 // x values of one staging entry (16 consecutive elements of one block).
+// XT = 0: f16 x; 1: f32 x; 2: f32 residual h (+ delta) normalized in the
+// staging (x = f16(rmsnorm(h + delta) * w)), then used as f16 x.
 template <int XT> struct XChunk;
 template <> struct XChunk<0> { u32x4 lo, hi; };
 template <> struct XChunk<1> { f32x4 f[4]; };
+template <> struct XChunk<2> { f32x4 f[4], d[4], w[4]; };
 
-// XT: 0 = f16 x, 1 = f32 x (hi + lo split).  NW waves per workgroup.
+// Fused input of the XT = 2 variant.
+struct NormIn {
+    const float *delta;      // added to h first (null: none)
+    const float *w;          // norm weight [K]
+    float *hout;             // h + delta, written by workgroup 0 (null: not kept)
+    float eps;
+};
+
+// XT: 0 = f16 x, 1 = f32 x (hi + lo split), 2 = normalized residual (see
+// XChunk).  NW waves per workgroup.
 template <int XT, int NW, int P>
 __global__ __launch_bounds__(64 * NW) void q2_0_gemv_mfma_kernel(
         const uint8_t *__restrict__ codes, const uint16_t *__restrict__ scales,
         const void *__restrict__ xv, float *__restrict__ y, int K, int R, int nsets,
-        int sets_per_wg) {
+        int sets_per_wg, NormIn nin) {
     constexpr int MT = 64 * NW;
+    constexpr bool HL = XT == 1;                          // x carried as f16 hi + lo
     extern __shared__ uint32_t lds[];
     const int nblk = K >> 7;
     // LDS: x planes, block b at dword XB*b (64 pair dwords + 4 of padding, so
@@ -114,7 +127,7 @@ __global__ __launch_bounds__(64 * NW) void q2_0_gemv_mfma_kernel(
     const int xstride = (nblk + 5) * XB;                   // dwords per x plane
     uint32_t *xp = lds;                                    // hi (or f16) pairs
     uint32_t *xq = lds + xstride;                          // lo plane (f32 x only)
-    float *sx = (float *)(lds + (XT ? 2 : 1) * xstride);   // [nblk] block sums of x
+    float *sx = (float *)(lds + (HL ? 2 : 1) * xstride);   // [nblk] block sums of x
     float *ex = sx + nblk;                                 // [nblk] 2^(16+e_b)
     float *ysum = ex + nblk;                               // [sets_per_wg * 16]
     __shared__ float red[NW][2][16];                       // partial sums of cut sets
@@ -140,6 +153,8 @@ __global__ __launch_bounds__(64 * NW) void q2_0_gemv_mfma_kernel(
     // Entries past the last x block (the zero blocks, and threads with no
     // entry) read past the end of x: zeros, without a memory access.
     const __amdgpu_buffer_rsrc_t xrs = make_rsrc(xv, (uint32_t)K * (XT ? 4u : 2u));
+    const __amdgpu_buffer_rsrc_t drs = make_rsrc(nin.delta, nin.delta ? (uint32_t)K * 4u : 0u);
+    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(nin.w, XT == 2 ? (uint32_t)K * 4u : 0u);
     auto load_x = [&](int e) {
         const int off = e < nblk * 8 ? (e >> 3) * 128 + 16 * (e & 7) : K;   // element offset
         XChunk<XT> c;
@@ -150,6 +165,13 @@ __global__ __launch_bounds__(64 * NW) void q2_0_gemv_mfma_kernel(
 #pragma unroll
             for (int q = 0; q < 4; q++)
                 c.f[q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, off * 4 + 16 * q, 0, 0));
+            if constexpr (XT == 2) {
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    c.d[q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(drs, off * 4 + 16 * q, 0, 0));
+                    c.w[q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs, off * 4 + 16 * q, 0, 0));
+                }
+            }
         }
         return c;
     };
@@ -228,7 +250,7 @@ __global__ __launch_bounds__(64 * NW) void q2_0_gemv_mfma_kernel(
             const float ha = (float)(f16)xa, hb = (float)(f16)xb;
             const uint32_t hp = pack_h2(ha * XSCALE[k], hb * XSCALE[k]);
             if (k < 4) p0[k] = hp; else p1[k - 4] = hp;
-            if (XT) {
+            if (HL) {
                 const uint32_t lp = pack_h2((xa - ha) * (0x1p11f * XSCALE[k]),
                                             (xb - hb) * (0x1p11f * XSCALE[k]));
                 if (k < 4) q0[k] = lp; else q1[k - 4] = lp;
@@ -238,7 +260,7 @@ __global__ __launch_bounds__(64 * NW) void q2_0_gemv_mfma_kernel(
             u32x4 *dst = (u32x4 *)(xp + bb * XB + 8 * i);
             dst[0] = p0;
             dst[1] = p1;
-            if (XT) {
+            if (HL) {
                 u32x4 *dq = (u32x4 *)(xq + bb * XB + 8 * i);
                 dq[0] = q0;
                 dq[1] = q1;
@@ -252,8 +274,40 @@ __global__ __launch_bounds__(64 * NW) void q2_0_gemv_mfma_kernel(
     // The first entry is straight-line code after the tile prefetch, so its
     // wait for x leaves the tiles in flight; further entries (K long enough
     // that (K/128 + 5) * 8 > threads) follow in a loop.
+    if constexpr (XT == 2) {
+        // x = f16(rmsnorm(h + delta) * w), as a separate add + norm kernel
+        // followed by an f16 GEMV would form it; one entry per thread (the
+        // host checks), entries past K load zeros.  Workgroup 0 keeps h +
+        // delta for the next residual add.
+        __shared__ float ssr[NW];
+        float ss = 0.f;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            xc.f[q] += xc.d[q];
+            ss += xc.f[q][0] * xc.f[q][0] + xc.f[q][1] * xc.f[q][1] +
+                  xc.f[q][2] * xc.f[q][2] + xc.f[q][3] * xc.f[q][3];
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        if (lane == 0) ssr[wave] = ss;
+        if (blockIdx.x == 0 && nin.hout && threadIdx.x < nblk * 8) {
+            float *ho = nin.hout + (threadIdx.x >> 3) * 128 + 16 * (threadIdx.x & 7);
+#pragma unroll
+            for (int q = 0; q < 4; q++) *(f32x4 *)(ho + 4 * q) = xc.f[q];
+        }
+        __syncthreads();
+        float tot = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) tot += ssr[w];
+        const float rs = 1.0f / sqrtf(tot / (float)K + nin.eps);
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+#pragma unroll
+            for (int c = 0; c < 4; c++) xc.f[q][c] = (float)(f16)(xc.f[q][c] * rs * xc.w[q][c]);
+    }
     stage(threadIdx.x, xc);
-    for (int e = threadIdx.x + MT; e < nstage; e += MT) stage(e, load_x(e));
+    if constexpr (XT != 2)
+        for (int e = threadIdx.x + MT; e < nstage; e += MT) stage(e, load_x(e));
 #pragma unroll
     for (int p = 1; p < P; p++) {
         load(p, ld, ring[p], rsc[p]);
@@ -292,12 +346,12 @@ __global__ __launch_bounds__(64 * NW) void q2_0_gemv_mfma_kernel(
                 const u32x4 bx = src[2 * d + q];
                 const f16x4 a0 = __builtin_bit_cast(f16x4, u32x2{t[4 * q], t[4 * q + 1]});
                 const f16x4 a1 = __builtin_bit_cast(f16x4, u32x2{t[4 * q + 2], t[4 * q + 3]});
-                const int c0 = XT ? q : (2 * q) & 3, c1 = XT ? q : (2 * q + 1) & 3;
+                const int c0 = HL ? q : (2 * q) & 3, c1 = HL ? q : (2 * q + 1) & 3;
                 acc[c0] = __builtin_amdgcn_mfma_f32_4x4x4f16(
                         a0, __builtin_bit_cast(f16x4, u32x2{bx[0], bx[1]}), acc[c0], 0, 0, 0);
                 acc[c1] = __builtin_amdgcn_mfma_f32_4x4x4f16(
                         a1, __builtin_bit_cast(f16x4, u32x2{bx[2], bx[3]}), acc[c1], 0, 0, 0);
-                if (XT) {
+                if (HL) {
                     const u32x4 bq = srq[2 * d + q];
                     acc[2 + q] = __builtin_amdgcn_mfma_f32_4x4x4f16(
                             a0, __builtin_bit_cast(f16x4, u32x2{bq[0], bq[1]}), acc[2 + q], 0, 0, 0);
@@ -321,7 +375,7 @@ __global__ __launch_bounds__(64 * NW) void q2_0_gemv_mfma_kernel(
 #pragma unroll
             for (int v = 0; v < 4; v++) {
                 // Every product entered as c * x * 2^(-16-e_b) (lo with x 2^11).
-                const float cx = XT ? (acc[0][v] + acc[1][v]) + (acc[2][v] + acc[3][v]) * 0x1p-11f
+                const float cx = HL ? (acc[0][v] + acc[1][v]) + (acc[2][v] + acc[3][v]) * 0x1p-11f
                                     : (acc[0][v] + acc[1][v]) + (acc[2][v] + acc[3][v]);
                 yp[v] += valid ? dsc[v] * (cx * exj - sxj) : 0.f;
             }
@@ -412,7 +466,7 @@ int occupancy_memo(int nblk, size_t lds) {
 }
 
 template <int XT, int NW, int P>
-int launch(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, size_t xlds) {
+int launch(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, size_t xlds, const NormIn &nin) {
     const int64_t K = w->K, R = w->R;
     const int nblk = (int)(K >> 7), steps = (nblk + 3) / 4;
     const int cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
@@ -430,14 +484,15 @@ int launch(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, size_t xlds) {
     const size_t lds = xlds + (size_t)per * 64;
     hipLaunchKernelGGL((q2_0_gemv_mfma_kernel<XT, NW, P>), dim3(grid), dim3(64 * NW), lds,
                        ctx->stream, (const uint8_t *)w->codes, (const uint16_t *)w->scales, x, y,
-                       (int)K, (int)R, (int)nsets, (int)per);
+                       (int)K, (int)R, (int)nsets, (int)per, nin);
     GD_LAUNCHED(ctx, "q2_0_gemv_mfma");
     return GD_OK;
 }
 
 template <int XT, int NW, int P>
-int launch_or_prepare(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, size_t xlds) {
-    if (w) return launch<XT, NW, P>(ctx, w, x, y, xlds);
+int launch_or_prepare(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, size_t xlds,
+                      const NormIn &nin) {
+    if (w) return launch<XT, NW, P>(ctx, w, x, y, xlds, nin);
     // Preparation only (x carries nblk): fill the occupancy memo.
     const int nblk = (int)(intptr_t)x;
     const size_t cap = std::min<size_t>(256, (LDS_BYTES - xlds) / 64);
@@ -446,16 +501,22 @@ int launch_or_prepare(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, siz
 }
 
 template <int XT>
-int launch_nw(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, size_t xlds) {
+int launch_nw(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, size_t xlds,
+              const NormIn &nin = NormIn{nullptr, nullptr, nullptr, 0.f}) {
     // Waves per workgroup (all share one staged copy of x) and tiles in
     // flight per wave; GADEON_GEMV_NW / GADEON_GEMV_P override for tuning.
     static const char *env_nw = getenv("GADEON_GEMV_NW");
     static const char *env_p = getenv("GADEON_GEMV_P");
     const int nw = env_nw ? atoi(env_nw) : 16, pp = env_p ? atoi(env_p) : 2;
-#define GD_L(NW_, P_) launch_or_prepare<XT, NW_, P_>(ctx, w, x, y, xlds)
-    if (nw == 4) return pp == 2 ? GD_L(4, 2) : pp == 4 ? GD_L(4, 4) : GD_L(4, 3);
-    if (nw == 8) return pp == 2 ? GD_L(8, 2) : pp == 4 ? GD_L(8, 4) : GD_L(8, 3);
-    return pp == 2 ? GD_L(16, 2) : pp == 4 ? GD_L(16, 4) : GD_L(16, 3);
+#define GD_L(NW_, P_) launch_or_prepare<XT, NW_, P_>(ctx, w, x, y, xlds, nin)
+    // The fused-norm variant stages one x entry per thread: 16 waves only.
+    if constexpr (XT == 2) {
+        return GD_L(16, 2);
+    } else {
+        if (nw == 4) return pp == 2 ? GD_L(4, 2) : pp == 4 ? GD_L(4, 4) : GD_L(4, 3);
+        if (nw == 8) return pp == 2 ? GD_L(8, 2) : pp == 4 ? GD_L(8, 4) : GD_L(8, 3);
+        return pp == 2 ? GD_L(16, 2) : pp == 4 ? GD_L(16, 4) : GD_L(16, 3);
+    }
 #undef GD_L
 }
 
@@ -473,14 +534,29 @@ int gd_gemv_mfma(gd_ctx *ctx, const gd_q2w *w, const void *x, int x_dtype, float
     return XT ? launch_nw<1>(ctx, w, x, y, xlds) : launch_nw<0>(ctx, w, x, y, xlds);
 }
 
+// GEMV of x = f16(rmsnorm(h + delta) * normw): the residual add and norm
+// that precede a decode projection, fused into its x staging (the caller has
+// checked w and the pointers; K <= 15744 so that one thread stages one
+// entry).  hout (if not null) receives h + delta; it must not alias h.
+int gd_gemv_mfma_norm(gd_ctx *ctx, const gd_q2w *w, const float *h, const float *delta,
+                      const float *normw, float eps, float *hout, float *y) {
+    const int nblk = (int)(w->K >> 7);
+    const size_t xlds = (size_t)(nblk + 5) * XB * 4 + (size_t)nblk * 8;
+    GD_REQUIRE(ctx, (nblk + 5) * 8 <= 1024, "gd_gemv_norm: K=%lld too long (at most 15744)",
+               (long long)w->K);
+    return launch_nw<2>(ctx, w, h, y, xlds, NormIn{delta, normw, hout, eps});
+}
+
 // Host-side set-up for GEMVs of reduction length K (the occupancy lookup),
 // so that a later call can be captured into a graph without runtime queries.
+// x_dtype GD_F16, GD_F32, or -1 for the fused-norm variant.
 int gd_gemv_mfma_prepare(gd_ctx *ctx, int64_t K, int x_dtype) {
-    const int XT = x_dtype == GD_F32 ? 1 : 0;
+    const int XT = x_dtype == GD_F32 ? 1 : x_dtype == -1 ? 2 : 0;
     const int nblk = (int)(K >> 7);
-    const size_t xlds = (size_t)(nblk + 5) * XB * 4 * (XT ? 2 : 1) + (size_t)nblk * 8;
+    const size_t xlds = (size_t)(nblk + 5) * XB * 4 * (XT == 1 ? 2 : 1) + (size_t)nblk * 8;
     if (K % 128 || K > 65536 || xlds + 16 * 64 > LDS_BYTES) return GD_EINVAL;
     const void *tag = (const void *)(intptr_t)nblk;
-    return XT ? launch_nw<1>(ctx, nullptr, tag, nullptr, xlds)
-              : launch_nw<0>(ctx, nullptr, tag, nullptr, xlds);
+    return XT == 1 ? launch_nw<1>(ctx, nullptr, tag, nullptr, xlds)
+         : XT == 2 ? launch_nw<2>(ctx, nullptr, tag, nullptr, xlds)
+                   : launch_nw<0>(ctx, nullptr, tag, nullptr, xlds);
 }

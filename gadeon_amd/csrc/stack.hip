@@ -19,6 +19,8 @@
 //     memory so a decode step can be replayed as a captured HIP graph.
 #include "gd_internal.h"
 
+#include <utility>
+
 #include <atomic>
 #include <cmath>
 #include <string>
@@ -405,6 +407,7 @@ struct gd_stack {
     int32_t *page_table = nullptr;
     // scratch
     float *x = nullptr, *proj = nullptr, *conv_out = nullptr, *o32 = nullptr, *contrib = nullptr;
+    float *x2 = nullptr;         // decode: second residual buffer (ping-pong with x)
     float *beta = nullptr, *g = nullptr, *q32 = nullptr, *gate32 = nullptr, *logits = nullptr;
     float *attn_part = nullptr, *amax_v = nullptr;
     int *amax_i = nullptr;
@@ -460,15 +463,29 @@ int forward(gd_stack *st, int N, bool decode) {
     int rc;
 #define R_(call) do { if ((rc = (call)) != GD_OK) return rc; } while (0)
 #define K_(name, ...) do { hipLaunchKernelGGL(name, __VA_ARGS__); GD_LAUNCHED(ctx, #name); } while (0)
-    // attn_norm of layer 0; every later norm is fused with the residual add
-    // that precedes it (k_add_rmsnorm).
-    K_(k_add_rmsnorm, dim3(N), dim3(1024), 0, s, st->x, (const float *)nullptr,
-       st->L[0].attn_norm, st->xn16, E, eps, 0, (int64_t)0);
+    // Prefill: attn_norm of layer 0 here; every later norm is fused with the
+    // residual add that precedes it (k_add_rmsnorm).  Decode: each add +
+    // norm is fused into the x staging of the GEMV that consumes it, with the
+    // residual alternating between x and x2 (hcur holds the live one).
+    float *hcur = st->x, *hnext = st->x2;
+    if (!decode)
+        K_(k_add_rmsnorm, dim3(N), dim3(1024), 0, s, st->x, (const float *)nullptr,
+           st->L[0].attn_norm, st->xn16, E, eps, 0, (int64_t)0);
     for (int il = 0; il < c.n_layer; il++) {
         StackLayer &ly = st->L[il];
         const int RP = ly.rec ? st->rp_rec : st->rp_att;
-        if (decode) R_(gd_q2_0_gemv(ctx, &ly.in_proj, st->xn16, GD_F16, st->proj));
-        else R_(gd_q2_0_gemm(ctx, &ly.in_proj, N, st->xn16, GD_F16, st->proj, GD_F32));
+        if (decode) {
+            if (il == 0) {
+                R_(gd_gemv_mfma_norm(ctx, &ly.in_proj, hcur, nullptr, ly.attn_norm, eps, nullptr,
+                                     st->proj));
+            } else {
+                R_(gd_gemv_mfma_norm(ctx, &ly.in_proj, hcur, st->contrib, ly.attn_norm, eps, hnext,
+                                     st->proj));
+                std::swap(hcur, hnext);
+            }
+        } else {
+            R_(gd_q2_0_gemm(ctx, &ly.in_proj, N, st->xn16, GD_F16, st->proj, GD_F32));
+        }
         if (ly.rec) {
             const int off_z = st->convDim, off_b = off_z + st->valDim, off_a = off_b + nV;
             if (decode) {
@@ -520,10 +537,15 @@ int forward(gd_stack *st, int N, bool decode) {
             nsplit = p.split;
             R_(gd_gemm_launch(ctx, &ly.out_proj, N, st->a16, GD_F16, st->contrib, GD_F32, p));
         }
-        K_(k_add_rmsnorm, dim3(N), dim3(1024), 0, s, st->x, st->contrib, ly.post_norm, st->xn16,
-           E, eps, nsplit, (int64_t)N * E);
-        if (decode) R_(gd_q2_0_gemv(ctx, &ly.gate_up, st->xn16, GD_F16, st->proj));
-        else R_(gd_q2_0_gemm(ctx, &ly.gate_up, N, st->xn16, GD_F16, st->proj, GD_F32));
+        if (decode) {
+            R_(gd_gemv_mfma_norm(ctx, &ly.gate_up, hcur, st->contrib, ly.post_norm, eps, hnext,
+                                 st->proj));
+            std::swap(hcur, hnext);
+        } else {
+            K_(k_add_rmsnorm, dim3(N), dim3(1024), 0, s, st->x, st->contrib, ly.post_norm,
+               st->xn16, E, eps, nsplit, (int64_t)N * E);
+            R_(gd_q2_0_gemm(ctx, &ly.gate_up, N, st->xn16, GD_F16, st->proj, GD_F32));
+        }
         K_(k_swiglu, dim3(gd_blocks((int64_t)N * FF, 256)), dim3(256), 0, s, st->proj, FF,
            st->a16, N);
         nsplit = 1;
@@ -534,7 +556,9 @@ int forward(gd_stack *st, int N, bool decode) {
             nsplit = p.split;
             R_(gd_gemm_launch(ctx, &ly.down, N, st->a16, GD_F16, st->contrib, GD_F32, p));
         }
-        if (il + 1 < c.n_layer) {
+        if (decode) {
+            // The next in_proj (or the lm_head) adds and normalizes.
+        } else if (il + 1 < c.n_layer) {
             K_(k_add_rmsnorm, dim3(N), dim3(1024), 0, s, st->x, st->contrib,
                st->L[il + 1].attn_norm, st->xn16, E, eps, nsplit, (int64_t)N * E);
         } else {
@@ -546,7 +570,11 @@ int forward(gd_stack *st, int N, bool decode) {
         }
     }
     // Tied lm_head on the last token, greedy pick, position bump.
-    R_(gd_q2_0_gemv(ctx, &st->embd, st->xn16, GD_F16, st->logits));
+    if (decode)
+        R_(gd_gemv_mfma_norm(ctx, &st->embd, hcur, st->contrib, st->out_norm, eps, nullptr,
+                             st->logits));
+    else
+        R_(gd_q2_0_gemv(ctx, &st->embd, st->xn16, GD_F16, st->logits));
     K_(k_argmax_part, dim3(AMAX_BLOCKS), dim3(256), 0, s, st->logits, c.n_vocab, st->amax_v,
        st->amax_i);
     K_(k_argmax_final, dim3(1), dim3(AMAX_BLOCKS), 0, s, st->amax_v, st->amax_i, st->dtok);
@@ -590,6 +618,9 @@ extern "C" int gd_stack_create(gd_ctx *ctx, const gd_stack_config *cfg, uint64_t
     GD_REQUIRE(ctx, c.n_rot > 0 && c.n_rot <= HD && c.n_rot % 2 == 0, "gd_stack_create: n_rot");
     GD_REQUIRE(ctx, c.n_embd % 128 == 0 && c.n_ff % 128 == 0 && c.n_vocab > 0,
                "gd_stack_create: n_embd and n_ff must be multiples of 128");
+    GD_REQUIRE(ctx, c.n_embd <= 15744,
+               "gd_stack_create: n_embd %d above 15744 (decode stages x one entry per thread)",
+               c.n_embd);
     GD_REQUIRE(ctx, c.kv_block > 0 && c.max_ctx > 0 && c.max_batch > 0,
                "gd_stack_create: kv_block, max_ctx, max_batch must be positive");
     *out = nullptr;
@@ -641,6 +672,7 @@ extern "C" int gd_stack_create(gd_ctx *ctx, const gd_stack_config *cfg, uint64_t
                        st->page_table, st->max_pages);
     const int maxproj = std::max(std::max(st->rp_rec, st->rp_att), 2 * FF);
     C_(salloc_t(st, (size_t)B * E, &st->x));
+    C_(salloc_t(st, (size_t)E, &st->x2));
     C_(salloc_t(st, (size_t)B * maxproj, &st->proj));
     C_(salloc_t(st, (size_t)B * st->convDim, &st->conv_out));
     C_(salloc_t(st, (size_t)B * st->valDim, &st->o32));
@@ -746,6 +778,7 @@ extern "C" int gd_stack_generate(gd_stack *st, int n, int32_t *tokens) {
         for (int64_t K : {(int64_t)st->c.n_embd, (int64_t)st->c.n_ff, (int64_t)st->valDim,
                           (int64_t)st->c.n_head * HD})
             if ((rc = gd_gemv_mfma_prepare(ctx, K, GD_F16))) return rc;
+        if ((rc = gd_gemv_mfma_prepare(ctx, st->c.n_embd, -1))) return rc;
         GD_HIP(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
         rc = gd_q2_0_dequant_rows(ctx, &st->embd, st->dtok, 1, st->x);
         if (rc == GD_OK) rc = forward(st, 1, true);

@@ -110,6 +110,53 @@ def test_gemv_vs_oracle(ctx, K, R, xt):
     ctx.free(dy)
 
 
+@pytest.mark.parametrize("K,R,with_delta", [(5120, 777, True), (5120, 34816, True),
+                                            (1024, 300, False), (15744, 64, True)])
+def test_gemv_norm_vs_oracle_and_unfused(ctx, K, R, with_delta):
+    """gd_q2_0_gemv_norm == add + rmsnorm (f16 out) + f16 GEMV: against the
+    oracle, against the three device calls it replaces, and h' exactly."""
+    eps = 1e-6
+    blocks = O.lcg_q2_0(K, R, K + 7 * R)
+    w = upload_w(ctx, blocks, K, R)
+    h = O.lcg_normal(K, 91, 0.0, 3.0)
+    d = O.lcg_normal(K, 92, 0.0, 1.0) if with_delta else np.zeros(K, np.float32)
+    wn = O.lcg_normal(K, 93, 1.0, 0.2)
+    dh, dd, dwn = ctx.put(h), ctx.put(d), ctx.put(wn)
+    dho, dy = ctx.alloc(K * 4), ctx.alloc(R * 4)
+    ctx.gd_q2_0_gemv_norm(C.byref(w), dh, dd if with_delta else None, dwn, eps, dho, dy)
+    y = ctx.get(dy, R, np.float32)
+    hp = (h + d).astype(np.float32)
+    assert np.array_equal(ctx.get(dho, K, np.float32), hp)
+    x16 = O.rmsnorm(hp[None], wn, eps)[0].astype(np.float16)
+    want = O.q2_0_matvec(blocks, K, R, x16.astype(np.float32), threads=8)
+    assert rel_diff(y, want) < 1e-3
+    # the unfused device chain
+    dh2, dx16, dy2 = ctx.put(h), ctx.alloc(K * 2), ctx.alloc(R * 4)
+    if with_delta:
+        ctx.gd_add(dh2, dd, K)
+    ctx.gd_rmsnorm(dh2, dwn, dx16, ga.F16, K, 1, eps)
+    ctx.gd_q2_0_gemv(C.byref(w), dx16, ga.F16, dy2)
+    assert rel_diff(y, ctx.get(dy2, R, np.float32)) < 1e-3
+    for p in (dh, dd, dwn, dho, dy, dh2, dx16, dy2):
+        ctx.free(p)
+    free_w(ctx, w)
+
+
+def test_gemv_norm_rejects_alias_and_long_k(ctx):
+    w = ga.Q2W()
+    ctx.gd_q2w_alloc(256, 16, C.byref(w))
+    dh, dy = ctx.alloc(256 * 4), ctx.alloc(16 * 4)
+    with pytest.raises(RuntimeError, match="alias"):
+        ctx.gd_q2_0_gemv_norm(C.byref(w), dh, None, dh, 1e-6, dh, dy)
+    ctx.gd_q2w_free(C.byref(w))
+    ctx.gd_q2w_alloc(15872, 16, C.byref(w))
+    with pytest.raises(RuntimeError, match="15744"):
+        ctx.gd_q2_0_gemv_norm(C.byref(w), dh, None, dh, 1e-6, None, dy)
+    ctx.gd_q2w_free(C.byref(w))
+    ctx.free(dh)
+    ctx.free(dy)
+
+
 def test_gemv_zero_and_single_weight(ctx):
     K, R = 1024, 8
     codes = np.ones(K * R, np.uint8)
