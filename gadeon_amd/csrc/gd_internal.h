@@ -29,11 +29,17 @@ int gd_fail(gd_ctx *ctx, int code, const char *fmt, ...);
 int gd_ctx_workspace(gd_ctx *ctx, size_t bytes, void **out);
 // Map a HIP error to a GD code with a message naming `what`.
 int gd_hip_fail(gd_ctx *ctx, hipError_t e, const char *what);
+// Matrix-core GEMV (checked by the caller); ksplit > 1 writes K-split partial
+// rows to y + z * R.
+int gd_gemv_mfma(gd_ctx *ctx, const gd_q2w *w, const void *x, int x_dtype, float *y, int ksplit);
 // Host-side set-up of the GEMV for reduction length K (before graph capture).
 int gd_gemv_mfma_prepare(gd_ctx *ctx, int64_t K, int x_dtype);
-// GEMV of x = f16(rmsnorm(h + delta) * normw); hout <- h + delta if not null.
-int gd_gemv_mfma_norm(gd_ctx *ctx, const gd_q2w *w, const float *h, const float *delta,
-                      const float *normw, float eps, float *hout, float *y);
+// GEMV of x = f16(rmsnorm(h + sum of nd delta partials) * normw); hout <- the
+// sum if not null.
+int gd_gemv_mfma_norm(gd_ctx *ctx, const gd_q2w *w, const float *h, const float *delta, int nd,
+                      int dstride, const float *normw, float eps, float *hout, float *y);
+// K splits an f16-x GEMV of this shape should use (partials summed by the consumer).
+int gd_gemv_ksplit(gd_ctx *ctx, int64_t K, int64_t R);
 // Prefill GEMM plan: MT x 32 tokens by 4 x NT x 32 weight rows per
 // workgroup, K split `split` ways into f32 partials.
 struct gd_gemm_plan { int mt, nt, split; };

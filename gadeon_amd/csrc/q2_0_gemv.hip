@@ -44,7 +44,6 @@ __global__ void q2_0_dequant_rows_kernel(const uint8_t *__restrict__ codes,
 }  // namespace
 
 int gd_check_q2w(gd_ctx *ctx, const gd_q2w *w, const char *who);
-int gd_gemv_mfma(gd_ctx *ctx, const gd_q2w *w, const void *x, int x_dtype, float *y);
 
 extern "C" int gd_q2_0_dequant_rows(gd_ctx *ctx, const gd_q2w *w, const int32_t *ids, int64_t n,
                                     float *out) {
@@ -75,22 +74,47 @@ extern "C" int gd_q2_0_gemv(gd_ctx *ctx, const gd_q2w *w, const void *x, int x_d
     GD_REQUIRE(ctx, w->K <= 65536 && w->R < (1LL << 30),
                "gd_q2_0_gemv: K=%lld (at most 65536) or R=%lld too large", (long long)w->K,
                (long long)w->R);
-    return gd_gemv_mfma(ctx, w, x, x_dtype, y);
+    return gd_gemv_mfma(ctx, w, x, x_dtype, y, 1);
+}
+
+extern "C" int gd_q2_0_gemv_split(gd_ctx *ctx, const gd_q2w *w, const void *x, int x_dtype,
+                                  float *y, int ksplit, int *nsplit) {
+    GD_CHECK_CTX(ctx);
+    GD_REQUIRE(ctx, ksplit >= 1 && ksplit <= 4 && nsplit, "gd_q2_0_gemv_split: ksplit %d not 1..4",
+               ksplit);
+    int rc = gd_check_q2w(ctx, w, "gd_q2_0_gemv_split");
+    if (rc) return rc;
+    GD_REQUIRE(ctx, x && y, "gd_q2_0_gemv_split: null x or y");
+    GD_REQUIRE(ctx, x_dtype == GD_F32 || x_dtype == GD_F16, "gd_q2_0_gemv_split: bad x dtype %d",
+               x_dtype);
+    GD_REQUIRE(ctx, ((uintptr_t)x & 15) == 0, "gd_q2_0_gemv_split: x must be 16-byte aligned");
+    GD_REQUIRE(ctx, w->K <= 65536 && w->R < (1LL << 30),
+               "gd_q2_0_gemv_split: K=%lld (at most 65536) or R=%lld too large", (long long)w->K,
+               (long long)w->R);
+    const int steps = (int)((w->K / 128 + 3) / 4);
+    const int ks = (steps + ksplit - 1) / ksplit;
+    *nsplit = (steps + ks - 1) / ks;
+    return gd_gemv_mfma(ctx, w, x, x_dtype, y, ksplit);
 }
 
 extern "C" int gd_q2_0_gemv_norm(gd_ctx *ctx, const gd_q2w *w, const float *h,
-                                 const float *delta, const float *w_norm, float eps,
-                                 float *hout, float *y) {
+                                 const float *delta, int nd, int64_t delta_stride,
+                                 const float *w_norm, float eps, float *hout, float *y) {
     GD_CHECK_CTX(ctx);
     int rc = gd_check_q2w(ctx, w, "gd_q2_0_gemv_norm");
     if (rc) return rc;
     GD_REQUIRE(ctx, h && w_norm && y, "gd_q2_0_gemv_norm: null h, w_norm or y");
     GD_REQUIRE(ctx, hout != h, "gd_q2_0_gemv_norm: hout must not alias h");
+    if (!delta) nd = 0;
+    GD_REQUIRE(ctx, nd >= 0 && nd <= 8 && (nd <= 1 || (delta_stride >= w->K &&
+                                                      delta_stride % 4 == 0 &&
+                                                      delta_stride * nd < (1LL << 28))),
+               "gd_q2_0_gemv_norm: nd=%d partials with stride %lld", nd, (long long)delta_stride);
     GD_REQUIRE(ctx, ((uintptr_t)h & 15) == 0 && ((uintptr_t)delta & 15) == 0 &&
                         ((uintptr_t)w_norm & 15) == 0 && ((uintptr_t)hout & 15) == 0,
                "gd_q2_0_gemv_norm: h, delta, w_norm, hout must be 16-byte aligned");
     GD_REQUIRE(ctx, w->K <= 15744 && w->R < (1LL << 30),
                "gd_q2_0_gemv_norm: K=%lld (at most 15744) or R=%lld too large",
                (long long)w->K, (long long)w->R);
-    return gd_gemv_mfma_norm(ctx, w, h, delta, w_norm, eps, hout, y);
+    return gd_gemv_mfma_norm(ctx, w, h, delta, nd, (int)delta_stride, w_norm, eps, hout, y);
 }

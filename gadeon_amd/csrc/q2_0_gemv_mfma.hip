@@ -77,10 +77,11 @@ __device__ __forceinline__ uint32_t pack_h2(float a, float b) {
 }
 
 // Position of an item inside the workgroup's item space (set-major).
+// Steps run s0 .. s1-1 within each set (the workgroup's K split).
 struct Cursor {
     int set, s;
-    __device__ void next(int steps) {
-        if (++s == steps) { s = 0; ++set; }
+    __device__ void next(int s0, int s1) {
+        if (++s == s1) { s = s0; ++set; }
     }
 };
 
@@ -103,10 +104,12 @@ template <> struct XChunk<2> { f32x4 f[4], d[4], w[4]; };
 
 // Fused input of the XT = 2 variant.
 struct NormIn {
-    const float *delta;      // added to h first (null: none)
+    const float *delta;      // nd partials delta + z * dstride added to h first
     const float *w;          // norm weight [K]
     float *hout;             // h + delta, written by workgroup 0 (null: not kept)
     float eps;
+    int nd;                  // partials in delta (0: none)
+    int dstride;             // floats between partials
 };
 
 // XT: 0 = f16 x, 1 = f32 x (hi + lo split), 2 = normalized residual (see
@@ -115,7 +118,7 @@ template <int XT, int NW, int P>
 __global__ __launch_bounds__(64 * NW) void q2_0_gemv_mfma_kernel(
         const uint8_t *__restrict__ codes, const uint16_t *__restrict__ scales,
         const void *__restrict__ xv, float *__restrict__ y, int K, int R, int nsets,
-        int sets_per_wg, NormIn nin) {
+        int sets_per_wg, int ksteps, NormIn nin) {
     constexpr int MT = 64 * NW;
     constexpr bool HL = XT == 1;                          // x carried as f16 hi + lo
     extern __shared__ uint32_t lds[];
@@ -141,9 +144,13 @@ __global__ __launch_bounds__(64 * NW) void q2_0_gemv_mfma_kernel(
     const int steps = (nblk + 3) >> 2;
     const int bgroups = (nblk + 15) >> 4;
 
+    // K split z = blockIdx.y: steps [s0, s1) of every set; its rows go to
+    // y + z * R.  Items are numbered set-major over the split's steps.
+    const int s0 = blockIdx.y * ksteps, s1 = min(steps, s0 + ksteps), L = s1 - s0;
+    y += (size_t)blockIdx.y * R;
     const int set_lo = blockIdx.x * sets_per_wg;
     const int nset_wg = min(sets_per_wg, nsets - set_lo);
-    const int total = nset_wg * steps;
+    const int total = nset_wg * L;
     const int a = total * wave / NW, b = total * (wave + 1) / NW;
     const int nitems = b - a;
 
@@ -153,7 +160,8 @@ __global__ __launch_bounds__(64 * NW) void q2_0_gemv_mfma_kernel(
     // Entries past the last x block (the zero blocks, and threads with no
     // entry) read past the end of x: zeros, without a memory access.
     const __amdgpu_buffer_rsrc_t xrs = make_rsrc(xv, (uint32_t)K * (XT ? 4u : 2u));
-    const __amdgpu_buffer_rsrc_t drs = make_rsrc(nin.delta, nin.delta ? (uint32_t)K * 4u : 0u);
+    const __amdgpu_buffer_rsrc_t drs =
+            make_rsrc(nin.delta, nin.nd ? (uint32_t)((nin.nd - 1) * nin.dstride + K) * 4u : 0u);
     const __amdgpu_buffer_rsrc_t wrs = make_rsrc(nin.w, XT == 2 ? (uint32_t)K * 4u : 0u);
     auto load_x = [&](int e) {
         const int off = e < nblk * 8 ? (e >> 3) * 128 + 16 * (e & 7) : K;   // element offset
@@ -168,7 +176,13 @@ __global__ __launch_bounds__(64 * NW) void q2_0_gemv_mfma_kernel(
             if constexpr (XT == 2) {
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
-                    c.d[q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(drs, off * 4 + 16 * q, 0, 0));
+                    c.d[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    // Entries past K (off == K) must read zeros: at z * dstride
+                    // + K lies the next partial.
+                    for (int z = 0; z < nin.nd; z++)
+                        c.d[q] += __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                drs, off < K ? (uint32_t)((z * nin.dstride + off) * 4 + 16 * q)
+                                             : 0xfffff000u, 0, 0));
                     c.w[q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs, off * 4 + 16 * q, 0, 0));
                 }
             }
@@ -181,18 +195,19 @@ __global__ __launch_bounds__(64 * NW) void q2_0_gemv_mfma_kernel(
     // arrive behind them.
     __builtin_amdgcn_sched_barrier(0);
 
-    // The wave's items are consecutive tiles (tiles of consecutive sets are
-    // contiguous): item i is tile (set_lo * steps + a + i).  Loads past the
-    // wave's range, or scales past the workgroup's sets, return zeros.
+    // Tiles of the workgroup's sets: (set, s) is tile set * steps + s.  Loads
+    // past the wave's range, or scales past the workgroup's sets, return
+    // zeros (a past-the-range item gets an offset beyond the resource).
     const __amdgpu_buffer_rsrc_t trs =
-            make_rsrc(codes + ((size_t)set_lo * steps + a) * 2048, (uint32_t)nitems * 2048u);
+            make_rsrc(codes + (size_t)set_lo * steps * 2048, (uint32_t)nset_wg * steps * 2048u);
     const __amdgpu_buffer_rsrc_t srs =
             make_rsrc(scales + (size_t)set_lo * bgroups * 256, (uint32_t)nset_wg * bgroups * 512u);
     // Loads of item `it` (at cursor `ld`): its tile and the scales of its
     // drain group that this lane's column needs: rows 4*rq .. 4*rq+3 of
     // block 16*(s/4) + 4*j + kb.
     auto load = [&](int it, const Cursor &ld, u32x4 (&cw)[2], u32x2 &sc) {
-        const int off = it * 2048 + lane * 16;
+        const uint32_t off = it < nitems ? (uint32_t)(ld.set * steps + ld.s) * 2048u + lane * 16
+                                         : 0xfffff000u;
         cw[0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(trs, off, 0, CP_NT));
         cw[1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(trs, off + 1024, 0, CP_NT));
         const int si = ((ld.set * bgroups + (ld.s >> 2)) * 16 + 4 * j + kb) * 16 + 4 * rq;
@@ -203,9 +218,9 @@ __global__ __launch_bounds__(64 * NW) void q2_0_gemv_mfma_kernel(
     // so x (needed first) does not queue behind the whole grid's prefetch.
     u32x4 ring[P][2];
     u32x2 rsc[P];
-    Cursor ld{a / steps, a % steps};
+    Cursor ld{a / L, s0 + a % L};
     load(0, ld, ring[0], rsc[0]);
-    ld.next(steps);
+    ld.next(s0, s1);
 
     // Stage x: pair p = 8i + k of block b holds (x[b,16i+k], x[b,16i+k+8]) *
     // XSCALE[k] * 2^-e_b.  Thread (b, i) forms the 8 pairs of x[16i ..
@@ -311,7 +326,7 @@ __global__ __launch_bounds__(64 * NW) void q2_0_gemv_mfma_kernel(
 #pragma unroll
     for (int p = 1; p < P; p++) {
         load(p, ld, ring[p], rsc[p]);
-        ld.next(steps);
+        ld.next(s0, s1);
     }
     __syncthreads();
 
@@ -320,12 +335,12 @@ __global__ __launch_bounds__(64 * NW) void q2_0_gemv_mfma_kernel(
 #pragma unroll
     for (int c = 0; c < 4; c++) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
     float yp[4] = {0.f, 0.f, 0.f, 0.f};
-    Cursor cur{a / steps, a % steps};
+    Cursor cur{a / L, s0 + a % L};
     int dlo = cur.s;                                      // first step of the open group
     // One item: ring slot p holds its tile and scales.
     auto step = [&](const int item, u32x4 (&tile)[2], u32x2 &sc) {
         const int s = cur.s;
-        if ((s & 3) == 0 || item == 0) dlo = s;
+        if ((s & 3) == 0 || s == s0 || item == 0) dlo = s;   // a drain group starts
         // MFMA block mb = lane/4 multiplies rows 4*rq .. 4*rq+3 of Q2 block
         // 4s + kb by four K values; column j of its B is x when j == s % 4.
         const int blk = 4 * s + kb;
@@ -360,7 +375,7 @@ __global__ __launch_bounds__(64 * NW) void q2_0_gemv_mfma_kernel(
                 }
             }
         }
-        const bool set_end = s + 1 == steps;
+        const bool set_end = s + 1 == s1;
         const bool range_end = item + 1 == nitems;
         if (((s + 1) & 3) == 0 || set_end || range_end) {
             // Drain: column j holds step sj = 4*(dlo/4) + j of the group, i.e.
@@ -386,8 +401,8 @@ __global__ __launch_bounds__(64 * NW) void q2_0_gemv_mfma_kernel(
             // Sum each row over its 16 lanes (4 columns x 4 K-blocks).  A set
             // this wave covers whole goes to the workgroup's results; a cut
             // one to `red` (slot 0 if it began before this wave's range).
-            const int set_first = cur.set * steps;          // item index of s = 0
-            const bool whole = set_first >= a && set_first + steps <= b;
+            const int set_first = cur.set * L;              // item index of s = s0
+            const bool whole = set_first >= a && set_first + L <= b;
             const int slot = set_first < a ? 0 : 1;
 #pragma unroll
             for (int v = 0; v < 4; v++) {
@@ -407,8 +422,8 @@ __global__ __launch_bounds__(64 * NW) void q2_0_gemv_mfma_kernel(
         // The ring slot is consumed: refill it with the tile P items
         // ahead (zeros, without a memory access, past the range).
         load(item + P, ld, tile, sc);
-        ld.next(steps);
-        cur.next(steps);
+        ld.next(s0, s1);
+        cur.next(s0, s1);
     };
     // Whole blocks of P items: straight-line code, so the compiler waits
     // only for the tile each item needs.  The last nitems % P items follow.
@@ -426,16 +441,16 @@ __global__ __launch_bounds__(64 * NW) void q2_0_gemv_mfma_kernel(
     if (threadIdx.x < (NW - 1) * 16) {
         const int bi = threadIdx.x / 16 + 1, r = threadIdx.x % 16;
         const int bnd = total * bi / NW;
-        const int j = bnd / steps;
+        const int j = bnd / L;
         const int prev = total * (bi - 1) / NW;
-        const bool first_in_set = bi == 1 || prev <= j * steps;
-        if (bnd % steps != 0 && first_in_set) {
+        const bool first_in_set = bi == 1 || prev <= j * L;
+        if (bnd % L != 0 && first_in_set) {
             float acc = 0.f;
             for (int w = 0; w < NW; w++) {
                 const int wa = total * w / NW, wb = total * (w + 1) / NW;
-                const bool overlap = wa < wb && wa < (j + 1) * steps && wb > j * steps;
-                const bool whole = wa <= j * steps && wb >= (j + 1) * steps;
-                if (overlap && !whole) acc += red[w][j * steps < wa ? 0 : 1][r];
+                const bool overlap = wa < wb && wa < (j + 1) * L && wb > j * L;
+                const bool whole = wa <= j * L && wb >= (j + 1) * L;
+                if (overlap && !whole) acc += red[w][j * L < wa ? 0 : 1][r];
             }
             ysum[j * 16 + r] = acc;
         }
@@ -465,34 +480,47 @@ int occupancy_memo(int nblk, size_t lds) {
     return memo[nblk];
 }
 
+// Work split of a GEMV: `per` consecutive sets per workgroup, K cut into nz
+// splits of ksteps steps (split z writes y + z * R).
+struct Split { int64_t per, grid; int ksteps, nz; };
+
+Split plan(int64_t nsets, int steps, int ksplit, int64_t slots, int64_t cap) {
+    Split sp;
+    sp.ksteps = (steps + ksplit - 1) / ksplit;
+    sp.nz = (steps + sp.ksteps - 1) / sp.ksteps;
+    // Every resident workgroup gets the same number of sets.
+    sp.per = std::min(cap, (nsets * sp.nz + slots - 1) / slots);
+    sp.grid = (nsets + sp.per - 1) / sp.per;
+    return sp;
+}
+
 template <int XT, int NW, int P>
-int launch(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, size_t xlds, const NormIn &nin) {
+int launch(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, size_t xlds, const NormIn &nin,
+           int ksplit) {
     const int64_t K = w->K, R = w->R;
     const int nblk = (int)(K >> 7), steps = (nblk + 3) / 4;
     const int cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
     const int64_t nsets = (R + 15) / 16;
-    // Row results of up to `cap` sets fit beside x in LDS.
-    const int64_t cap = std::min<int64_t>(256, (int64_t)(LDS_BYTES - xlds) / 64);
-    // Every resident workgroup gets the same number of sets; the occupancy
+    // Row results of up to `cap` sets fit beside x in LDS.  The occupancy
     // depends on the LDS footprint, so it is looked up per K.
+    const int64_t cap = std::min<int64_t>(256, (int64_t)(LDS_BYTES - xlds) / 64);
     const int occ = occupancy_memo<XT, NW, P>(nblk, xlds + (size_t)cap * 64);
-    const int64_t max_wgs = (int64_t)cus * occ;
-    const int64_t per = std::min(cap, (nsets + max_wgs - 1) / max_wgs);
-    GD_REQUIRE(ctx, per * steps * NW < (1LL << 31) && per * steps / NW + 1 < (1LL << 20),
+    const Split sp = plan(nsets, steps, ksplit, (int64_t)cus * occ, cap);
+    GD_REQUIRE(ctx, sp.per * steps * NW < (1LL << 31) && sp.per * steps / NW + 1 < (1LL << 20),
                "gd_q2_0_gemv: R=%lld too large", (long long)R);
-    const unsigned grid = (unsigned)((nsets + per - 1) / per);
-    const size_t lds = xlds + (size_t)per * 64;
-    hipLaunchKernelGGL((q2_0_gemv_mfma_kernel<XT, NW, P>), dim3(grid), dim3(64 * NW), lds,
-                       ctx->stream, (const uint8_t *)w->codes, (const uint16_t *)w->scales, x, y,
-                       (int)K, (int)R, (int)nsets, (int)per, nin);
+    const size_t lds = xlds + (size_t)sp.per * 64;
+    hipLaunchKernelGGL((q2_0_gemv_mfma_kernel<XT, NW, P>), dim3((unsigned)sp.grid, sp.nz),
+                       dim3(64 * NW), lds, ctx->stream, (const uint8_t *)w->codes,
+                       (const uint16_t *)w->scales, x, y, (int)K, (int)R, (int)nsets, (int)sp.per,
+                       sp.ksteps, nin);
     GD_LAUNCHED(ctx, "q2_0_gemv_mfma");
     return GD_OK;
 }
 
 template <int XT, int NW, int P>
 int launch_or_prepare(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, size_t xlds,
-                      const NormIn &nin) {
-    if (w) return launch<XT, NW, P>(ctx, w, x, y, xlds, nin);
+                      const NormIn &nin, int ksplit) {
+    if (w) return launch<XT, NW, P>(ctx, w, x, y, xlds, nin, ksplit);
     // Preparation only (x carries nblk): fill the occupancy memo.
     const int nblk = (int)(intptr_t)x;
     const size_t cap = std::min<size_t>(256, (LDS_BYTES - xlds) / 64);
@@ -502,13 +530,13 @@ int launch_or_prepare(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, siz
 
 template <int XT>
 int launch_nw(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, size_t xlds,
-              const NormIn &nin = NormIn{nullptr, nullptr, nullptr, 0.f}) {
+              const NormIn &nin = NormIn{nullptr, nullptr, nullptr, 0.f, 0, 0}, int ksplit = 1) {
     // Waves per workgroup (all share one staged copy of x) and tiles in
     // flight per wave; GADEON_GEMV_NW / GADEON_GEMV_P override for tuning.
     static const char *env_nw = getenv("GADEON_GEMV_NW");
     static const char *env_p = getenv("GADEON_GEMV_P");
     const int nw = env_nw ? atoi(env_nw) : 16, pp = env_p ? atoi(env_p) : 2;
-#define GD_L(NW_, P_) launch_or_prepare<XT, NW_, P_>(ctx, w, x, y, xlds, nin)
+#define GD_L(NW_, P_) launch_or_prepare<XT, NW_, P_>(ctx, w, x, y, xlds, nin, ksplit)
     // The fused-norm variant stages one x entry per thread: 16 waves only.
     if constexpr (XT == 2) {
         return GD_L(16, 2);
@@ -523,7 +551,10 @@ int launch_nw(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, size_t xlds
 }  // namespace
 
 // GEMV on the matrix cores for f16 or f32 x (the caller has checked w, x, y).
-int gd_gemv_mfma(gd_ctx *ctx, const gd_q2w *w, const void *x, int x_dtype, float *y) {
+// ksplit > 1 cuts K into that many splits whose partial rows go to y + z * R
+// (the caller sums them; gd_gemv_ksplit says how many there are).
+int gd_gemv_mfma(gd_ctx *ctx, const gd_q2w *w, const void *x, int x_dtype, float *y,
+                 int ksplit) {
     const int64_t K = w->K;
     const int XT = x_dtype == GD_F32 ? 1 : 0;
     const int nblk = (int)(K >> 7);
@@ -531,20 +562,50 @@ int gd_gemv_mfma(gd_ctx *ctx, const gd_q2w *w, const void *x, int x_dtype, float
     GD_REQUIRE(ctx, xlds + 16 * 64 <= LDS_BYTES,
                "gd_q2_0_gemv: K=%lld too long for LDS staging of %s x", (long long)K,
                XT ? "f32" : "f16");
-    return XT ? launch_nw<1>(ctx, w, x, y, xlds) : launch_nw<0>(ctx, w, x, y, xlds);
+    const NormIn none{nullptr, nullptr, nullptr, 0.f, 0, 0};
+    return XT ? launch_nw<1>(ctx, w, x, y, xlds, none, ksplit)
+              : launch_nw<0>(ctx, w, x, y, xlds, none, ksplit);
+}
+
+// K splits (1..4) for an f16-x GEMV whose partial rows the consumer can sum:
+// the count that minimizes the tiles streamed by the busiest CU (the
+// workgroups hold whole sets, so a short R leaves CUs idle unless K is
+// split), plus a small charge per extra partial.  Returns the number of
+// splits the launch will actually make.
+int gd_gemv_ksplit(gd_ctx *ctx, int64_t K, int64_t R) {
+    const int nblk = (int)(K >> 7), steps = (nblk + 3) / 4;
+    const size_t xlds = (size_t)(nblk + 5) * XB * 4 + (size_t)nblk * 8;
+    if (K % 128 || xlds + 16 * 64 > LDS_BYTES) return 1;
+    const int cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
+    const int64_t nsets = (R + 15) / 16;
+    const int64_t cap = std::min<int64_t>(256, (int64_t)(LDS_BYTES - xlds) / 64);
+    const int occ = occupancy_memo<0, 16, 2>(nblk, xlds + (size_t)cap * 64);
+    int best = 1;
+    double best_cost = 1e30;
+    for (int z = 1; z <= 4; z++) {
+        const Split sp = plan(nsets, steps, z, (int64_t)cus * occ, cap);
+        const double cost = (double)((sp.grid * sp.nz + cus - 1) / cus) * sp.per * sp.ksteps +
+                            2.0 * (sp.nz - 1);
+        if (cost < best_cost - 1e-9) {
+            best_cost = cost;
+            best = sp.nz;
+        }
+    }
+    return best;
 }
 
 // GEMV of x = f16(rmsnorm(h + delta) * normw): the residual add and norm
 // that precede a decode projection, fused into its x staging (the caller has
 // checked w and the pointers; K <= 15744 so that one thread stages one
-// entry).  hout (if not null) receives h + delta; it must not alias h.
-int gd_gemv_mfma_norm(gd_ctx *ctx, const gd_q2w *w, const float *h, const float *delta,
-                      const float *normw, float eps, float *hout, float *y) {
+// entry).  delta holds nd partials dstride floats apart (nd = 0: none);
+// hout (if not null) receives h + delta; it must not alias h.
+int gd_gemv_mfma_norm(gd_ctx *ctx, const gd_q2w *w, const float *h, const float *delta, int nd,
+                      int dstride, const float *normw, float eps, float *hout, float *y) {
     const int nblk = (int)(w->K >> 7);
     const size_t xlds = (size_t)(nblk + 5) * XB * 4 + (size_t)nblk * 8;
     GD_REQUIRE(ctx, (nblk + 5) * 8 <= 1024, "gd_gemv_norm: K=%lld too long (at most 15744)",
                (long long)w->K);
-    return launch_nw<2>(ctx, w, h, y, xlds, NormIn{delta, normw, hout, eps});
+    return launch_nw<2>(ctx, w, h, y, xlds, NormIn{delta, normw, hout, eps, delta ? nd : 0, dstride});
 }
 
 // Host-side set-up for GEMVs of reduction length K (the occupancy lookup),

@@ -468,6 +468,9 @@ int forward(gd_stack *st, int N, bool decode) {
     // norm is fused into the x staging of the GEMV that consumes it, with the
     // residual alternating between x and x2 (hcur holds the live one).
     float *hcur = st->x, *hnext = st->x2;
+    // Decode projections into the residual (out_proj, down) may split K;
+    // their consumer, the next fused-norm GEMV, sums the nd partials.
+    int nd = 0;
     if (!decode)
         K_(k_add_rmsnorm, dim3(N), dim3(1024), 0, s, st->x, (const float *)nullptr,
            st->L[0].attn_norm, st->xn16, E, eps, 0, (int64_t)0);
@@ -476,11 +479,11 @@ int forward(gd_stack *st, int N, bool decode) {
         const int RP = ly.rec ? st->rp_rec : st->rp_att;
         if (decode) {
             if (il == 0) {
-                R_(gd_gemv_mfma_norm(ctx, &ly.in_proj, hcur, nullptr, ly.attn_norm, eps, nullptr,
-                                     st->proj));
+                R_(gd_gemv_mfma_norm(ctx, &ly.in_proj, hcur, nullptr, 0, 0, ly.attn_norm, eps,
+                                     nullptr, st->proj));
             } else {
-                R_(gd_gemv_mfma_norm(ctx, &ly.in_proj, hcur, st->contrib, ly.attn_norm, eps, hnext,
-                                     st->proj));
+                R_(gd_gemv_mfma_norm(ctx, &ly.in_proj, hcur, st->contrib, nd, E, ly.attn_norm, eps,
+                                     hnext, st->proj));
                 std::swap(hcur, hnext);
             }
         } else {
@@ -531,15 +534,16 @@ int forward(gd_stack *st, int N, bool decode) {
         // leaves its partials in contrib and k_add_rmsnorm sums them.
         int nsplit = 1;
         if (decode) {
-            R_(gd_q2_0_gemv(ctx, &ly.out_proj, st->a16, GD_F16, st->contrib));
+            nd = gd_gemv_ksplit(ctx, ly.out_proj.K, ly.out_proj.R);
+            R_(gd_gemv_mfma(ctx, &ly.out_proj, st->a16, GD_F16, st->contrib, nd));
         } else {
             const gd_gemm_plan p = gd_gemm_choose(ctx, N, ly.out_proj.K, ly.out_proj.R, GD_F16);
             nsplit = p.split;
             R_(gd_gemm_launch(ctx, &ly.out_proj, N, st->a16, GD_F16, st->contrib, GD_F32, p));
         }
         if (decode) {
-            R_(gd_gemv_mfma_norm(ctx, &ly.gate_up, hcur, st->contrib, ly.post_norm, eps, hnext,
-                                 st->proj));
+            R_(gd_gemv_mfma_norm(ctx, &ly.gate_up, hcur, st->contrib, nd, E, ly.post_norm, eps,
+                                 hnext, st->proj));
             std::swap(hcur, hnext);
         } else {
             K_(k_add_rmsnorm, dim3(N), dim3(1024), 0, s, st->x, st->contrib, ly.post_norm,
@@ -550,7 +554,8 @@ int forward(gd_stack *st, int N, bool decode) {
            st->a16, N);
         nsplit = 1;
         if (decode) {
-            R_(gd_q2_0_gemv(ctx, &ly.down, st->a16, GD_F16, st->contrib));
+            nd = gd_gemv_ksplit(ctx, ly.down.K, ly.down.R);
+            R_(gd_gemv_mfma(ctx, &ly.down, st->a16, GD_F16, st->contrib, nd));
         } else {
             const gd_gemm_plan p = gd_gemm_choose(ctx, N, ly.down.K, ly.down.R, GD_F16);
             nsplit = p.split;
@@ -571,8 +576,8 @@ int forward(gd_stack *st, int N, bool decode) {
     }
     // Tied lm_head on the last token, greedy pick, position bump.
     if (decode)
-        R_(gd_gemv_mfma_norm(ctx, &st->embd, hcur, st->contrib, st->out_norm, eps, nullptr,
-                             st->logits));
+        R_(gd_gemv_mfma_norm(ctx, &st->embd, hcur, st->contrib, nd, E, st->out_norm, eps,
+                             nullptr, st->logits));
     else
         R_(gd_q2_0_gemv(ctx, &st->embd, st->xn16, GD_F16, st->logits));
     K_(k_argmax_part, dim3(AMAX_BLOCKS), dim3(256), 0, s, st->logits, c.n_vocab, st->amax_v,

@@ -148,15 +148,26 @@ int gd_q2_0_export_rows(gd_ctx *ctx, const gd_q2w *w, int64_t row0, int64_t nrow
 int gd_q2_0_gemv(gd_ctx *ctx, const gd_q2w *w, const void *x, int x_dtype,
                  float *y);
 
+/* gd_q2_0_gemv with K cut into `ksplit` (1..4) ranges whose partial rows go
+ * to y + z * R (y holds ksplit * R floats); *nsplit receives the number of
+ * partials written (it can be lower than ksplit for short K).  Summing them
+ * gives gd_q2_0_gemv's y.  A short R leaves CUs idle unless K is split; the
+ * partials are meant for a consumer that adds them anyway (the residual
+ * delta of gd_q2_0_gemv_norm).  No counterpart in the reference. */
+int gd_q2_0_gemv_split(gd_ctx *ctx, const gd_q2w *w, const void *x, int x_dtype,
+                       float *y, int ksplit, int *nsplit);
+
 /* Decode GEMV with the residual add and RMSNorm that precede it fused into
- * the x staging: h' = h + delta (delta may be null), x = f16(h' * w_norm /
- * sqrt(mean(h'^2) + eps)), y = W x.  hout (may be null, must not alias h)
- * receives h'.  Same result as gd_add + gd_rmsnorm(.., GD_F16, ..) +
- * gd_q2_0_gemv (MetalEnc.addInplace + rmsnorm + gemv, MetalEnc.swift:
- * 213-236, 572-597, 78-99) in one launch instead of three.  h, delta, w_norm
- * and hout are f32 [K], 16-byte aligned; K <= 15744. */
+ * the x staging: h' = h + sum of nd partials delta + z * delta_stride (nd = 0
+ * or delta null: none), x = f16(h' * w_norm / sqrt(mean(h'^2) + eps)),
+ * y = W x.  hout (may be null, must not alias h) receives h'.  Same result
+ * as gd_add + gd_rmsnorm(.., GD_F16, ..) + gd_q2_0_gemv (MetalEnc.addInplace
+ * + rmsnorm + gemv, MetalEnc.swift:213-236, 572-597, 78-99) in one launch
+ * instead of three.  h, delta, w_norm and hout are f32 [K], 16-byte aligned
+ * (delta_stride a multiple of 4); K <= 15744. */
 int gd_q2_0_gemv_norm(gd_ctx *ctx, const gd_q2w *w, const float *h, const float *delta,
-                      const float *w_norm, float eps, float *hout, float *y);
+                      int nd, int64_t delta_stride, const float *w_norm, float eps,
+                      float *hout, float *y);
 
 /* ---- Q2_0 GEMM (prefill): MetalEnc.gemm, MetalEnc.swift:145-189 --------------
  * Y[t][r] = sum_k X[t][k] * W[r][k], token-major X[T][K] and Y[T][R].

@@ -123,7 +123,7 @@ def test_gemv_norm_vs_oracle_and_unfused(ctx, K, R, with_delta):
     wn = O.lcg_normal(K, 93, 1.0, 0.2)
     dh, dd, dwn = ctx.put(h), ctx.put(d), ctx.put(wn)
     dho, dy = ctx.alloc(K * 4), ctx.alloc(R * 4)
-    ctx.gd_q2_0_gemv_norm(C.byref(w), dh, dd if with_delta else None, dwn, eps, dho, dy)
+    ctx.gd_q2_0_gemv_norm(C.byref(w), dh, dd if with_delta else None, 1, 0, dwn, eps, dho, dy)
     y = ctx.get(dy, R, np.float32)
     hp = (h + d).astype(np.float32)
     assert np.array_equal(ctx.get(dho, K, np.float32), hp)
@@ -142,16 +142,55 @@ def test_gemv_norm_vs_oracle_and_unfused(ctx, K, R, with_delta):
     free_w(ctx, w)
 
 
+@pytest.mark.parametrize("K,R,ksplit", [(17408, 5120, 4), (2048, 5120, 2), (5120, 777, 3),
+                                        (512, 100, 4), (17408, 130, 2)])
+def test_gemv_split_partials_sum_to_gemv(ctx, K, R, ksplit):
+    """The K-split partials add up to the oracle's y, and feed the fused
+    norm GEMV as nd deltas exactly as their sum would."""
+    blocks = O.lcg_q2_0(K, R, 5 * K + R)
+    w = upload_w(ctx, blocks, K, R)
+    x = O.lcg_normal_f16(K, 95)
+    dx, dy = ctx.put(x.view(np.uint16)), ctx.alloc(4 * R * 4)
+    ns = C.c_int()
+    ctx.gd_q2_0_gemv_split(C.byref(w), dx, ga.F16, dy, ksplit, C.byref(ns))
+    steps = (K // 128 + 3) // 4
+    ks = -(-steps // ksplit)
+    assert ns.value == -(-steps // ks)
+    parts = ctx.get(dy, ns.value * R, np.float32).reshape(ns.value, R)
+    want = O.q2_0_matvec(blocks, K, R, x.astype(np.float32), threads=8)
+    assert rel_diff(parts.sum(0), want) < 1e-4
+    if 128 <= R <= 15744 and R % 4 == 0:      # partial stride R must be 16-byte aligned
+        # the partials as the residual delta of a fused-norm GEMV (K' = R)
+        K2, R2 = R - R % 128, 64
+        b2 = O.lcg_q2_0(K2, R2, 17)
+        w2 = upload_w(ctx, b2, K2, R2)
+        h = O.lcg_normal(K2, 96, 0.0, 2.0)
+        wn = O.lcg_normal(K2, 97, 1.0, 0.1)
+        dh, dwn, dho, dy2 = ctx.put(h), ctx.put(wn), ctx.alloc(K2 * 4), ctx.alloc(R2 * 4)
+        ctx.gd_q2_0_gemv_norm(C.byref(w2), dh, dy, ns.value, R, dwn, 1e-6, dho, dy2)
+        hp = h + parts[:, :K2].sum(0, dtype=np.float32)
+        assert np.allclose(ctx.get(dho, K2, np.float32), hp, rtol=1e-6, atol=1e-5)
+        x16 = O.rmsnorm(hp[None], wn, 1e-6)[0].astype(np.float16)
+        want2 = O.q2_0_matvec(b2, K2, R2, x16.astype(np.float32), threads=8)
+        assert rel_diff(ctx.get(dy2, R2, np.float32), want2) < 1e-3
+        for p in (dh, dwn, dho, dy2):
+            ctx.free(p)
+        free_w(ctx, w2)
+    ctx.free(dx)
+    ctx.free(dy)
+    free_w(ctx, w)
+
+
 def test_gemv_norm_rejects_alias_and_long_k(ctx):
     w = ga.Q2W()
     ctx.gd_q2w_alloc(256, 16, C.byref(w))
     dh, dy = ctx.alloc(256 * 4), ctx.alloc(16 * 4)
     with pytest.raises(RuntimeError, match="alias"):
-        ctx.gd_q2_0_gemv_norm(C.byref(w), dh, None, dh, 1e-6, dh, dy)
+        ctx.gd_q2_0_gemv_norm(C.byref(w), dh, None, 0, 0, dh, 1e-6, dh, dy)
     ctx.gd_q2w_free(C.byref(w))
     ctx.gd_q2w_alloc(15872, 16, C.byref(w))
     with pytest.raises(RuntimeError, match="15744"):
-        ctx.gd_q2_0_gemv_norm(C.byref(w), dh, None, dh, 1e-6, None, dy)
+        ctx.gd_q2_0_gemv_norm(C.byref(w), dh, None, 0, 0, dh, 1e-6, None, dy)
     ctx.gd_q2w_free(C.byref(w))
     ctx.free(dh)
     ctx.free(dy)
