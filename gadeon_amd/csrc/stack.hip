@@ -177,62 +177,142 @@ __device__ __forceinline__ int64_t kv_slot(const int32_t *pt, int pos, int block
     return (int64_t)pt[pos / block] * block + pos % block;
 }
 
-// Causal prefill attention with the sigmoid output gate, online softmax.
-// Block (head h, 32 queries): 8 threads per query, each owning 16 of the 128
-// dims; keys stream through LDS in tiles of 32 (Attention.swift:108-134).
-constexpr int AQ = 32, AK = 32;
+// Causal prefill attention with the sigmoid output gate (Attention.swift:
+// 108-134), flash style on the matrix cores.  Block (head h, 64 queries):
+// wave w owns queries 16w .. 16w+15; keys stream through LDS in blocks of
+// 32 (K as [key][d], V transposed as [d][key]).  Per block a wave forms
+// S^T = K Q^T (v_mfma_f32_16x16x32_f16, lane = one query column and four
+// keys of each 16-key tile), updates its online softmax per query, and adds
+// V^T P^T into O^T.  The C layout of S^T is already the B operand of V^T P^T
+// once the MFMA's K index 8g + e (g = lane / 16) stands for key 4g + e
+// (e < 4) or 16 + 4g + e - 4: the A operand (V^T) reads the same keys, so P
+// never goes through LDS.  q and P enter as f16 hi + lo pairs (about 22
+// bits), K and V are the f16 cache itself, accumulation is f32.
+constexpr int AQ = 64, AK = 32;
 __global__ __launch_bounds__(256) void k_attn_prefill(
         const float *q, const float *gate, const uint16_t *kc, const uint16_t *vc,
         const int32_t *page_table, const int32_t *pos_ptr, uint16_t *out, int H, int HKV,
         int N, int block, float scale) {
-    __shared__ float Ks[AK][HD + 4];
-    __shared__ float Vs[AK][HD + 4];
+    __shared__ __attribute__((aligned(16))) f16 Ks[AK][HD + 8];
+    __shared__ __attribute__((aligned(16))) f16 Vt[HD][AK + 8];
     const int h = blockIdx.x, q0 = blockIdx.y * AQ;
-    const int t = threadIdx.x, qi = t >> 3, sub = t & 7;
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int lq = lane & 15, g = lane >> 4;
     const int kvh = h / (H / HKV);
     const int kvDim = HKV * HD;
     const int pos0 = *pos_ptr;
-    const int n = q0 + qi;
+    const int n = q0 + 16 * w + lq;                       // this lane's query
     const bool valid = n < N;
     const int my_pos = pos0 + (valid ? n : N - 1);
-    float qv[16], acc[16];
-    const float *qrow = q + ((int64_t)(valid ? n : N - 1) * H + h) * HD + sub * 16;
+    // B operand of S^T: q[n][32 ks + 8 g + e] * scale, split hi + lo.
+    f16x8 qh[HD / 32], ql[HD / 32];
+    {
+        const float *qrow = q + ((int64_t)(valid ? n : N - 1) * H + h) * HD;
 #pragma unroll
-    for (int d = 0; d < 16; d++) { qv[d] = qrow[d] * scale; acc[d] = 0.f; }
-    float m = -INFINITY, l = 0.f;
-    const int last = pos0 + min(q0 + AQ, N) - 1;       // last key any query here needs
-    for (int k0 = 0; k0 <= last; k0 += AK) {
-        __syncthreads();
-        for (int e = t; e < AK * HD; e += 256) {
-            const int kk = e / HD, d = e % HD;
-            const int p = min(k0 + kk, last);
-            const int64_t base = kv_slot(page_table, p, block) * kvDim + kvh * HD + d;
-            Ks[kk][d] = gd_h2f(kc[base]);
-            Vs[kk][d] = gd_h2f(vc[base]);
-        }
-        __syncthreads();
-        const int kend = min(AK, my_pos - k0 + 1);     // causal: keys <= my position
-        for (int kk = 0; kk < kend; kk++) {
-            float s = 0.f;
+        for (int ks = 0; ks < HD / 32; ks++) {
+            const f32x4 a = *(const f32x4 *)(qrow + 32 * ks + 8 * g);
+            const f32x4 b = *(const f32x4 *)(qrow + 32 * ks + 8 * g + 4);
 #pragma unroll
-            for (int d = 0; d < 16; d++) s = fmaf(qv[d], Ks[kk][sub * 16 + d], s);
-            s += __shfl_xor(s, 1, 64);
-            s += __shfl_xor(s, 2, 64);
-            s += __shfl_xor(s, 4, 64);
-            const float mn = fmaxf(m, s);
-            const float alpha = expf(m - mn), p = expf(s - mn);
-            l = l * alpha + p;
-#pragma unroll
-            for (int d = 0; d < 16; d++) acc[d] = fmaf(p, Vs[kk][sub * 16 + d], acc[d] * alpha);
-            m = mn;
+            for (int e = 0; e < 8; e++) {
+                const float v = (e < 4 ? a[e] : b[e - 4]) * scale;
+                qh[ks][e] = (f16)v;
+                ql[ks][e] = (f16)(v - (float)qh[ks][e]);
+            }
         }
     }
+    f32x4 acc[HD / 16];                                   // O^T rows 16 dt + 4 g + v
+#pragma unroll
+    for (int dt = 0; dt < HD / 16; dt++) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m = -INFINITY, l = 0.f;                         // this lane's keys only
+    const int last = pos0 + min(q0 + AQ, N) - 1;          // last key any query here needs
+    // Staging: thread t loads 16 dims (d0 .. d0+15) of key t / 8 of the block.
+    const int sk = t >> 3, d0 = (t & 7) * 16;
+    for (int k0 = 0; k0 <= last; k0 += AK) {
+        __syncthreads();
+        {
+            const int p = min(k0 + sk, last);
+            const int64_t base = kv_slot(page_table, p, block) * kvDim + kvh * HD + d0;
+            const u32x4 k_lo = *(const u32x4 *)(kc + base), k_hi = *(const u32x4 *)(kc + base + 8);
+            const u32x4 v_lo = *(const u32x4 *)(vc + base), v_hi = *(const u32x4 *)(vc + base + 8);
+            *(u32x4 *)&Ks[sk][d0] = k_lo;
+            *(u32x4 *)&Ks[sk][d0 + 8] = k_hi;
+            const f16x8 va = __builtin_bit_cast(f16x8, v_lo), vb = __builtin_bit_cast(f16x8, v_hi);
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                Vt[d0 + e][sk] = va[e];
+                Vt[d0 + 8 + e][sk] = vb[e];
+            }
+        }
+        __syncthreads();
+        // S^T tiles kt = 0, 1: keys 16 kt + 4 g + v for query lq.
+        f32x4 sc[2];
+#pragma unroll
+        for (int kt = 0; kt < 2; kt++) {
+            sc[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < HD / 32; ks++) {
+                const f16x8 ka = *(const f16x8 *)&Ks[16 * kt + lq][32 * ks + 8 * g];
+                sc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qh[ks], sc[kt], 0, 0, 0);
+                sc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, ql[ks], sc[kt], 0, 0, 0);
+            }
+        }
+        // Causal mask (and the clamped duplicates past `last`), then the
+        // online softmax of query lq over its lane group's keys.
+        float bmax = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int kp = k0 + 16 * kt + 4 * g + v;
+                if (kp > my_pos) sc[kt][v] = -INFINITY;
+                bmax = fmaxf(bmax, sc[kt][v]);
+            }
+        bmax = fmaxf(bmax, __shfl_xor(bmax, 16, 64));
+        bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
+        const float mn = fmaxf(m, bmax);                  // finite: key k0 <= my_pos
+        const float alpha = expf(m - mn);
+        m = mn;
+        l *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < HD / 16; dt++) acc[dt] *= alpha;
+        f16x8 ph, pl;
+#pragma unroll
+        for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const float pv = expf(sc[kt][v] - mn);
+                l += pv;
+                const f16 hi = (f16)pv;
+                ph[4 * kt + v] = hi;
+                pl[4 * kt + v] = (f16)(pv - (float)hi);
+            }
+        // O^T += V^T P^T: A lane row d = 16 dt + lq, the same 8 keys.
+#pragma unroll
+        for (int dt = 0; dt < HD / 16; dt++) {
+            const f16 *vr = &Vt[16 * dt + lq][0];
+            const f16x4 v0 = *(const f16x4 *)(vr + 4 * g), v1 = *(const f16x4 *)(vr + 16 + 4 * g);
+            const f16x8 va = f16x8{v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+            acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, ph, acc[dt], 0, 0, 0);
+            acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl, acc[dt], 0, 0, 0);
+        }
+    }
+    // Total weight of query lq: the four lane groups' partial sums.
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
     if (valid) {
         const float inv = 1.0f / l;
-        const float *grow = gate + ((int64_t)n * H + h) * HD + sub * 16;
-        uint16_t *orow = out + ((int64_t)n * H + h) * HD + sub * 16;
+        const float *grow = gate + ((int64_t)n * H + h) * HD;
+        uint16_t *orow = out + ((int64_t)n * H + h) * HD;
 #pragma unroll
-        for (int d = 0; d < 16; d++) orow[d] = gd_f2h(acc[d] * inv * gd_sigmoid(grow[d]));
+        for (int dt = 0; dt < HD / 16; dt++) {
+            const int d = 16 * dt + 4 * g;
+            const f32x4 gv = *(const f32x4 *)(grow + d);
+            uint16_t o[4];
+#pragma unroll
+            for (int v = 0; v < 4; v++) o[v] = gd_f2h(acc[dt][v] * inv * gd_sigmoid(gv[v]));
+            *(uint64_t *)(orow + d) = (uint64_t)o[0] | ((uint64_t)o[1] << 16) |
+                                      ((uint64_t)o[2] << 32) | ((uint64_t)o[3] << 48);
+        }
     }
 }
 
