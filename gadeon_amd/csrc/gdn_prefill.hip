@@ -25,7 +25,7 @@
 //             column of T in registers while the others stage the transposed
 //             operands; then W = T X and U = T Y (the UT transform) on the
 //             matrix cores.  The chunks are independent.
-//   gdn_scan  (value head, 32 columns of S): walks the chunks in order with
+//   gdn_scan  (value head, 16 columns of S): walks the chunks in order with
 //             its slice of S resident in LDS: delta = U - W S, O = qScale
 //             e^G (Q S) + P delta, S <- e^{G_L} S + K^T (e^{G_L-G} delta).
 //             Value columns of S are independent, which is what splits the
@@ -39,7 +39,7 @@ namespace {
 
 constexpr int DK = 128;          // key size handled
 constexpr int DV = 128;          // value size handled
-constexpr int NCOL = 32;         // value columns of S per scan workgroup
+constexpr int NCOL = 16;         // value columns of S per scan workgroup
 constexpr int PADK = DK + 8;     // LDS row of 128 f16 plus 16 bytes (bank spread)
 
 __device__ __forceinline__ f32x4 mfma(const f16x8 &a, const f16x8 &b, const f32x4 &c) {
@@ -298,6 +298,19 @@ struct ScanArgs {
     float qScale;
 };
 
+// One chunk's operands of this thread, all independent of S: loaded one
+// chunk ahead so that the serial walk over chunks waits on no memory but
+// its own LDS.
+template <int CP>
+struct ScanChunk {
+    float g;                              // G[tid] (tid < CP)
+    f16x8 wh[DK / 32], wl[DK / 32];       // W rows 16*wave + lr
+    float uv[NCOL / 16][4];               // U rows 16*wave + 4*kg + v, this lane's column
+    f16x8 qa[DK / 32];                    // Q row 16*wave + lr
+    f16x8 ph[CP / 32], pl[CP / 32];       // P row 16*wave + lr
+    f16x8 ka[2][CP / 32];                 // K^T rows 32*wave + 16*rt + lr
+};
+
 template <int CP, typename IO, typename OT>
 __global__ __launch_bounds__(256) void gdn_scan(ScanArgs a) {
     __shared__ __attribute__((aligned(16))) float Sf[DK][NCOL + 4];          // S[i][j] slice
@@ -311,6 +324,8 @@ __global__ __launch_bounds__(256) void gdn_scan(ScanArgs a) {
     const int hk = hv % a.nK;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int lr = lane & 15, kg = lane >> 4;
+    const bool rows = wave < CP / 16;                   // this wave owns 16 chunk rows
+    const int tb = wave * 16;
     float *Sg = a.S + (size_t)hv * DK * DV;
 
     for (int e = tid; e < DK * NCOL; e += 256) {
@@ -318,10 +333,48 @@ __global__ __launch_bounds__(256) void gdn_scan(ScanArgs a) {
         Sf[i][j] = Sg[(size_t)i * DV + j0 + j];
     }
 
-    for (int c = 0; c < a.nchunks; c++) {
+    auto load = [&](int c, ScanChunk<CP> &k) {
+        c = min(c, a.nchunks - 1);
         const int64_t t0 = (int64_t)c * a.C;
         const int L = (int)min((int64_t)a.C, a.T - t0);
         const size_t u = (size_t)hv * a.nchunks + c;
+        if (tid < CP) k.g = a.w.G[u * CP + tid];
+        if (rows) {
+#pragma unroll
+            for (int ks = 0; ks < DK / 32; ks++) {
+                const size_t wi = (u * CP + tb + lr) * DK + ks * 32 + kg * 8;
+                k.wh[ks] = *(const f16x8 *)&a.w.Wh[wi];
+                k.wl[ks] = *(const f16x8 *)&a.w.Wl[wi];
+            }
+#pragma unroll
+            for (int ct = 0; ct < NCOL / 16; ct++)
+#pragma unroll
+                for (int v = 0; v < 4; v++)
+                    k.uv[ct][v] = a.w.U[(u * CP + tb + kg * 4 + v) * DV + j0 + ct * 16 + lr];
+            const int tr = tb + lr;
+            const bool rok = tr < L;
+#pragma unroll
+            for (int ks = 0; ks < DK / 32; ks++)
+                k.qa[ks] = load8<IO>(a.q, (t0 + (rok ? tr : 0)) * a.q_stride + (int64_t)hk * DK +
+                                              ks * 32 + kg * 8, rok);
+#pragma unroll
+            for (int ks = 0; ks < CP / 32; ks++) {
+                const size_t pi = (u * CP + tr) * CP + ks * 32 + kg * 8;
+                k.ph[ks] = *(const f16x8 *)&a.w.Ph[pi];
+                k.pl[ks] = *(const f16x8 *)&a.w.Pl[pi];
+            }
+        }
+#pragma unroll
+        for (int rt = 0; rt < 2; rt++)
+#pragma unroll
+            for (int ks = 0; ks < CP / 32; ks++)
+                k.ka[rt][ks] = *(const f16x8 *)&a.w.KT[(u * DK + wave * 32 + rt * 16 + lr) * CP +
+                                                        ks * 32 + kg * 8];
+    };
+
+    auto process = [&](int c, const ScanChunk<CP> &k) {
+        const int64_t t0 = (int64_t)c * a.C;
+        const int L = (int)min((int64_t)a.C, a.T - t0);
         __syncthreads();
         // S^T split (B operand of W S and Q S): entry (j, 8 rows i .. i+7).
         for (int e = tid; e < NCOL * (DK / 8); e += 256) {
@@ -334,21 +387,13 @@ __global__ __launch_bounds__(256) void gdn_scan(ScanArgs a) {
             *(f16x8 *)&Sh[j][i8] = h;
             *(f16x8 *)&Sl[j][i8] = l;
         }
-        if (tid < CP) Gs[tid] = a.w.G[u * CP + tid];
+        if (tid < CP) Gs[tid] = k.g;
         __syncthreads();
         const float gl = Gs[CP - 1];                    // G of the chunk's last token
 
         // delta = U - W S (rows 16*wave ..), then delta^T and its decayed
         // copy e^{G_L - G_t} delta^T, split, to LDS.
-        if (wave < CP / 16) {
-            const int tb = wave * 16;
-            f16x8 wh[DK / 32], wl[DK / 32];
-#pragma unroll
-            for (int ks = 0; ks < DK / 32; ks++) {
-                const size_t wi = (u * CP + tb + lr) * DK + ks * 32 + kg * 8;
-                wh[ks] = *(const f16x8 *)&a.w.Wh[wi];
-                wl[ks] = *(const f16x8 *)&a.w.Wl[wi];
-            }
+        if (rows) {
 #pragma unroll
             for (int ct = 0; ct < NCOL / 16; ct++) {
                 const int j = ct * 16 + lr;
@@ -356,14 +401,14 @@ __global__ __launch_bounds__(256) void gdn_scan(ScanArgs a) {
 #pragma unroll
                 for (int ks = 0; ks < DK / 32; ks++) {
                     const int i0 = ks * 32 + kg * 8;
-                    acc = mfma3(wh[ks], wl[ks], *(const f16x8 *)&Sh[j][i0],
+                    acc = mfma3(k.wh[ks], k.wl[ks], *(const f16x8 *)&Sh[j][i0],
                                 *(const f16x8 *)&Sl[j][i0], acc);
                 }
                 f16 dh[4], dl[4], eh[4], el[4];
 #pragma unroll
                 for (int v = 0; v < 4; v++) {
                     const int t = tb + kg * 4 + v;
-                    const float d = a.w.U[(u * CP + t) * DV + j0 + j] - acc[v];
+                    const float d = k.uv[ct][v] - acc[v];
                     const float ed = expf(gl - Gs[t]) * d;
                     dh[v] = (f16)d;
                     dl[v] = (f16)(d - (float)dh[v]);
@@ -380,22 +425,7 @@ __global__ __launch_bounds__(256) void gdn_scan(ScanArgs a) {
         __syncthreads();
 
         // O = qScale e^{G_t} (Q S) + P delta for the chunk's tokens.
-        if (wave < CP / 16) {
-            const int tb = wave * 16;
-            const int tr = tb + lr;                     // this lane's A row
-            const bool rok = tr < L;
-            f16x8 qa[DK / 32];
-#pragma unroll
-            for (int ks = 0; ks < DK / 32; ks++)
-                qa[ks] = load8<IO>(a.q, (t0 + (rok ? tr : 0)) * a.q_stride + (int64_t)hk * DK +
-                                            ks * 32 + kg * 8, rok);
-            f16x8 ph[CP / 32], pl[CP / 32];
-#pragma unroll
-            for (int ks = 0; ks < CP / 32; ks++) {
-                const size_t pi = (u * CP + tr) * CP + ks * 32 + kg * 8;
-                ph[ks] = *(const f16x8 *)&a.w.Ph[pi];
-                pl[ks] = *(const f16x8 *)&a.w.Pl[pi];
-            }
+        if (rows) {
 #pragma unroll
             for (int ct = 0; ct < NCOL / 16; ct++) {
                 const int j = ct * 16 + lr;
@@ -403,15 +433,15 @@ __global__ __launch_bounds__(256) void gdn_scan(ScanArgs a) {
 #pragma unroll
                 for (int ks = 0; ks < DK / 32; ks++) {
                     const int i0 = ks * 32 + kg * 8;
-                    acc = mfma(qa[ks], *(const f16x8 *)&Sh[j][i0], acc);
-                    acc = mfma(qa[ks], *(const f16x8 *)&Sl[j][i0], acc);
+                    acc = mfma(k.qa[ks], *(const f16x8 *)&Sh[j][i0], acc);
+                    acc = mfma(k.qa[ks], *(const f16x8 *)&Sl[j][i0], acc);
                 }
 #pragma unroll
                 for (int v = 0; v < 4; v++) acc[v] *= a.qScale * expf(Gs[tb + kg * 4 + v]);
 #pragma unroll
                 for (int ks = 0; ks < CP / 32; ks++) {
                     const int s0 = ks * 32 + kg * 8;
-                    acc = mfma3(ph[ks], pl[ks], *(const f16x8 *)&Dh[j][s0],
+                    acc = mfma3(k.ph[ks], k.pl[ks], *(const f16x8 *)&Dh[j][s0],
                                 *(const f16x8 *)&Dl[j][s0], acc);
                 }
 #pragma unroll
@@ -427,32 +457,37 @@ __global__ __launch_bounds__(256) void gdn_scan(ScanArgs a) {
         }
 
         // S <- e^{G_L} S + K^T (e^{G_L - G} delta): rows 32*wave .. +31.
-        {
-            const float decay = expf(gl);
+        const float decay = expf(gl);
 #pragma unroll
-            for (int rt = 0; rt < 2; rt++) {
-                const int ib = wave * 32 + rt * 16;
-                f16x8 ka[CP / 32];
+        for (int rt = 0; rt < 2; rt++) {
+            const int ib = wave * 32 + rt * 16;
 #pragma unroll
-                for (int ks = 0; ks < CP / 32; ks++)
-                    ka[ks] = *(const f16x8 *)&a.w.KT[(u * DK + ib + lr) * CP + ks * 32 + kg * 8];
+            for (int ct = 0; ct < NCOL / 16; ct++) {
+                const int j = ct * 16 + lr;
+                f32x4 acc;
 #pragma unroll
-                for (int ct = 0; ct < NCOL / 16; ct++) {
-                    const int j = ct * 16 + lr;
-                    f32x4 acc;
+                for (int v = 0; v < 4; v++) acc[v] = decay * Sf[ib + kg * 4 + v][j];
 #pragma unroll
-                    for (int v = 0; v < 4; v++) acc[v] = decay * Sf[ib + kg * 4 + v][j];
-#pragma unroll
-                    for (int ks = 0; ks < CP / 32; ks++) {
-                        const int s0 = ks * 32 + kg * 8;
-                        acc = mfma(ka[ks], *(const f16x8 *)&Eh[j][s0], acc);
-                        acc = mfma(ka[ks], *(const f16x8 *)&El[j][s0], acc);
-                    }
-#pragma unroll
-                    for (int v = 0; v < 4; v++) Sf[ib + kg * 4 + v][j] = acc[v];
+                for (int ks = 0; ks < CP / 32; ks++) {
+                    const int s0 = ks * 32 + kg * 8;
+                    acc = mfma(k.ka[rt][ks], *(const f16x8 *)&Eh[j][s0], acc);
+                    acc = mfma(k.ka[rt][ks], *(const f16x8 *)&El[j][s0], acc);
                 }
+#pragma unroll
+                for (int v = 0; v < 4; v++) Sf[ib + kg * 4 + v][j] = acc[v];
             }
         }
+    };
+
+    // Two operand sets alternate (a copy would wait for its loads).
+    ScanChunk<CP> A, B;
+    load(0, A);
+    for (int c = 0; c < a.nchunks; c += 2) {
+        load(c + 1, B);
+        process(c, A);
+        if (c + 1 >= a.nchunks) break;
+        load(c + 2, A);
+        process(c + 1, B);
     }
     __syncthreads();
     for (int e = tid; e < DK * NCOL; e += 256) {
