@@ -36,8 +36,11 @@ int gd_gemv_mfma(gd_ctx *ctx, const gd_q2w *w, const void *x, int x_dtype, float
 int gd_gemv_mfma_prepare(gd_ctx *ctx, int64_t K, int x_dtype);
 // GEMV of x = f16(rmsnorm(h + sum of nd delta partials) * normw); hout <- the
 // sum if not null.
+// glu_out (if not null): w = [gate; up] and glu_out = f16(silu(gate x) * up x)
+// replaces y.
 int gd_gemv_mfma_norm(gd_ctx *ctx, const gd_q2w *w, const float *h, const float *delta, int nd,
-                      int dstride, const float *normw, float eps, float *hout, float *y);
+                      int dstride, const float *normw, float eps, float *hout, float *y,
+                      uint16_t *glu_out = nullptr);
 // K splits an f16-x GEMV of this shape should use (partials summed by the consumer).
 int gd_gemv_ksplit(gd_ctx *ctx, int64_t K, int64_t R);
 // Prefill GEMM plan: MT x 32 tokens by 4 x NT x 32 weight rows per
@@ -47,6 +50,8 @@ gd_gemm_plan gd_gemm_choose(gd_ctx *ctx, int64_t T, int64_t K, int64_t R, int x_
 // split > 1: y_dtype f32 and Y holds split * T * R partials, summed by the caller.
 int gd_gemm_launch(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, int x_dtype, void *Y,
                    int y_dtype, const gd_gemm_plan &p);
+// SwiGLU GEMM: w = [gate; up] (2 * ff rows), f16 X [T][K] -> f16 out [T][ff].
+int gd_gemm_glu(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, uint16_t *out);
 
 #define GD_CHECK_CTX(ctx) \
     do { if (!(ctx)) return GD_EINVAL; } while (0)

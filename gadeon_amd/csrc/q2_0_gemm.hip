@@ -62,11 +62,15 @@ __device__ __forceinline__ uint32_t xswz(int r) {
 // MT x 32 tokens by 4 * NT * 32 weight rows per workgroup; slices
 // [z * sps, min((z+1) * sps, K/64)) of K for split z.  YT: 0 = f32, 1 = f16.
 // With nz > 1 the output is f32 partials at Y + z * T * R.
+// glu_ff > 0 (NT = 1, one split): W is [gate; up] with glu_ff rows each and
+// the output is SwiGLU, Yv[t][r] = f16(silu(gate_r . x_t) * (up_r . x_t)),
+// r < glu_ff: lanes 0..15 of a wave's fragment take gate rows g .. g+15 and
+// lanes 16..31 up rows glu_ff + g .., so one shuffle pairs them.
 template <int MT, int NT, int XT, int YT>
 __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2))) void q2_0_gemm_kernel(
         const uint8_t *__restrict__ codes, const uint16_t *__restrict__ scales,
         const void *__restrict__ Xv, void *__restrict__ Yv, int T, int K, int R, int sps,
-        int nrt, int nz, int per) {
+        int nrt, int nz, int per, int glu_ff) {
     constexpr int BT = MT * 32;
     constexpr int XTILE = BT * BK * 2;                       // bytes of one X slice
     __shared__ __attribute__((aligned(16))) uint8_t Xs[2][XTILE];
@@ -83,7 +87,8 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2))) vo
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 31, lh = lane >> 5;
     const int t0 = tt * BT;
-    const int rw = rt * (4 * NT * 32) + wave * (NT * 32);   // this wave's first row
+    // This wave's first row (SwiGLU: first gate row, 16 per wave).
+    const int rw = glu_ff ? rt * 64 + wave * 16 : rt * (4 * NT * 32) + wave * (NT * 32);
     const int nblk = K >> 7;
     const int csteps = (nblk + 3) >> 2;
     const int bgroups = (nblk + 15) >> 4;
@@ -97,7 +102,7 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2))) vo
     const __amdgpu_buffer_rsrc_t xrs =
             gd_rsrc((const char *)Xv + (size_t)t0 * K * ESZ, (uint32_t)min(BT, T - t0) * K * ESZ);
     const int g0 = rw >> 4, rgroups = (R + 15) >> 4;
-    const uint32_t gvalid = (uint32_t)max(0, min(2 * NT, rgroups - g0));
+    const uint32_t gvalid = (uint32_t)max(0, min(glu_ff ? (glu_ff >> 4) + 1 : 2 * NT, rgroups - g0));
     const __amdgpu_buffer_rsrc_t crs =
             gd_rsrc(codes + ((size_t)g0 * csteps << 11), gvalid * (uint32_t)csteps * 2048u);
     const __amdgpu_buffer_rsrc_t srs =
@@ -114,7 +119,8 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2))) vo
     uint32_t coff[NT], soff[NT];
 #pragma unroll
     for (int n = 0; n < NT; n++) {
-        const int g = 2 * n + (li >> 4);                // row group relative to g0
+        // Row group relative to g0 (SwiGLU: lanes 16..31 read the up rows).
+        const int g = glu_ff ? ((li >> 4) ? (glu_ff >> 4) : 0) : 2 * n + (li >> 4);
         coff[n] = ((uint32_t)(g * csteps) << 11) + ((li & 15) << 4) + 8 * lh;
         soff[n] = ((uint32_t)g * bgroups * 256 + (li & 15)) * 2;
     }
@@ -260,6 +266,20 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2))) vo
 
     // D layout of the 32x32 MFMA: lane holds column li (weight row) and rows
     // 8*(v/4) + 4*lh + (v%4) (tokens) for v < 16.
+    if (glu_ff) {
+        // Lane li < 16 holds gate row rw + li, lane li + 16 the matching up row.
+#pragma unroll
+        for (int m = 0; m < MT; m++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const float up = __shfl_xor(acc[m][0][v], 16, 64);
+                const int t = t0 + m * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
+                if (li < 16 && t < T && rw + li < glu_ff)
+                    ((uint16_t *)Yv)[(size_t)t * glu_ff + rw + li] =
+                            gd_f2h(gd_silu(acc[m][0][v]) * up);
+            }
+        return;
+    }
     const size_t zoff = (size_t)z * T * R;
 #pragma unroll
     for (int n = 0; n < NT; n++) {
@@ -303,7 +323,7 @@ __global__ __launch_bounds__(256) void q2_0_gemm_reduce(const float *__restrict_
 }
 
 typedef void (*gemm_fn)(const uint8_t *, const uint16_t *, const void *, void *, int, int, int,
-                        int, int, int, int);
+                        int, int, int, int, int);
 
 template <int MT, int NT>
 gemm_fn pick(int x_dtype, int yt) {
@@ -392,8 +412,27 @@ int gd_gemm_launch(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, int x
     const int64_t units = (int64_t)gd_blocks(T, p.mt * 32) * nz * nrt;
     const int per = (int)((units + 7) / 8);
     hipLaunchKernelGGL(f, dim3(8 * per), dim3(THREADS), 0, ctx->stream, (const uint8_t *)w->codes,
-                       (const uint16_t *)w->scales, X, Y, (int)T, K, R, sps, nrt, nz, per);
+                       (const uint16_t *)w->scales, X, Y, (int)T, K, R, sps, nrt, nz, per, 0);
     GD_LAUNCHED(ctx, "q2_0_gemm");
+    return GD_OK;
+}
+
+// SwiGLU GEMM: w holds [gate; up] (R = 2 * ff rows), X f16 [T][K], out f16
+// [T][ff] = silu(gate . x) * (up . x).  Tiles of 128 tokens by 64 gate rows
+// (and their 64 up rows), K unsplit.
+int gd_gemm_glu(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, uint16_t *out) {
+    const int K = (int)w->K, R = (int)w->R, ff = R / 2;
+    GD_REQUIRE(ctx, R % 32 == 0 && T > 0 && K % 128 == 0, "gd_gemm_glu: R=%d must hold two "
+               "halves of 16-row groups", R);
+    const int nslices = K / BK;
+    gemm_fn f = kernel_for(4, 1, GD_F16, 0);
+    const int nrt = gd_blocks(ff, 64);
+    const int64_t units = (int64_t)gd_blocks(T, 128) * nrt;
+    const int per = (int)((units + 7) / 8);
+    hipLaunchKernelGGL(f, dim3(8 * per), dim3(THREADS), 0, ctx->stream, (const uint8_t *)w->codes,
+                       (const uint16_t *)w->scales, X, (void *)out, (int)T, K, R, nslices, nrt, 1,
+                       per, ff);
+    GD_LAUNCHED(ctx, "q2_0_gemm_glu");
     return GD_OK;
 }
 
@@ -460,4 +499,20 @@ extern "C" int gd_q2_0_gemm_plan(gd_ctx *ctx, const gd_q2w *w, int64_t T, const 
                                  int x_dtype, void *Y, int y_dtype, int mt, int nt, int split) {
     const gd_gemm_plan p{mt, nt, split};
     return gemm_run(ctx, w, T, X, x_dtype, Y, y_dtype, &p);
+}
+
+extern "C" int gd_q2_0_gemm_swiglu(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X,
+                                   uint16_t *out) {
+    GD_CHECK_CTX(ctx);
+    int rc = gd_check_q2w(ctx, w, "gd_q2_0_gemm_swiglu");
+    if (rc) return rc;
+    GD_REQUIRE(ctx, X && out, "gd_q2_0_gemm_swiglu: null X or out");
+    GD_REQUIRE(ctx, T > 0 && T < (1 << 30), "gd_q2_0_gemm_swiglu: T=%lld out of range",
+               (long long)T);
+    GD_REQUIRE(ctx, ((uintptr_t)X & 15) == 0, "gd_q2_0_gemm_swiglu: X must be 16-byte aligned");
+    GD_REQUIRE(ctx, w->R % 32 == 0, "gd_q2_0_gemm_swiglu: R=%lld is not 2 ff with ff a multiple "
+               "of 16", (long long)w->R);
+    GD_REQUIRE(ctx, w->K <= (1 << 22) && w->R < (1LL << 31) && (size_t)T * w->R < (1ULL << 62),
+               "gd_q2_0_gemm_swiglu: shape too large");
+    return gd_gemm_glu(ctx, w, T, X, out);
 }

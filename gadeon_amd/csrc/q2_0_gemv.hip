@@ -99,11 +99,14 @@ extern "C" int gd_q2_0_gemv_split(gd_ctx *ctx, const gd_q2w *w, const void *x, i
 
 extern "C" int gd_q2_0_gemv_norm(gd_ctx *ctx, const gd_q2w *w, const float *h,
                                  const float *delta, int nd, int64_t delta_stride,
-                                 const float *w_norm, float eps, float *hout, float *y) {
+                                 const float *w_norm, float eps, float *hout, float *y,
+                                 uint16_t *glu_out) {
     GD_CHECK_CTX(ctx);
     int rc = gd_check_q2w(ctx, w, "gd_q2_0_gemv_norm");
     if (rc) return rc;
-    GD_REQUIRE(ctx, h && w_norm && y, "gd_q2_0_gemv_norm: null h, w_norm or y");
+    GD_REQUIRE(ctx, h && w_norm && (y || glu_out), "gd_q2_0_gemv_norm: null h, w_norm or y");
+    GD_REQUIRE(ctx, !glu_out || w->R % 32 == 0,
+               "gd_q2_0_gemv_norm: SwiGLU needs R = 2 ff rows with ff a multiple of 16");
     GD_REQUIRE(ctx, hout != h, "gd_q2_0_gemv_norm: hout must not alias h");
     if (!delta) nd = 0;
     GD_REQUIRE(ctx, nd >= 0 && nd <= 8 && (nd <= 1 || (delta_stride >= w->K &&
@@ -116,5 +119,6 @@ extern "C" int gd_q2_0_gemv_norm(gd_ctx *ctx, const gd_q2w *w, const float *h,
     GD_REQUIRE(ctx, w->K <= 15744 && w->R < (1LL << 30),
                "gd_q2_0_gemv_norm: K=%lld (at most 15744) or R=%lld too large",
                (long long)w->K, (long long)w->R);
-    return gd_gemv_mfma_norm(ctx, w, h, delta, nd, (int)delta_stride, w_norm, eps, hout, y);
+    return gd_gemv_mfma_norm(ctx, w, h, delta, nd, (int)delta_stride, w_norm, eps, hout, y,
+                             glu_out);
 }

@@ -102,6 +102,15 @@ template <> struct XChunk<0> { u32x4 lo, hi; };
 template <> struct XChunk<1> { f32x4 f[4]; };
 template <> struct XChunk<2> { f32x4 f[4], d[4], w[4]; };
 
+// SwiGLU output: with pair_sets > 0, W is [gate; up] with pair_sets sets
+// (16 rows) in each half, a workgroup takes gate sets k .. and the matching
+// up sets pair_sets + k .., and out[r] = f16(silu(gate_r . x) * (up_r . x))
+// replaces y.
+struct GluOut {
+    uint16_t *out;
+    int pair_sets;
+};
+
 // Fused input of the XT = 2 variant.
 struct NormIn {
     const float *delta;      // nd partials delta + z * dstride added to h first
@@ -118,7 +127,7 @@ template <int XT, int NW, int P>
 __global__ __launch_bounds__(64 * NW) void q2_0_gemv_mfma_kernel(
         const uint8_t *__restrict__ codes, const uint16_t *__restrict__ scales,
         const void *__restrict__ xv, float *__restrict__ y, int K, int R, int nsets,
-        int sets_per_wg, int ksteps, NormIn nin) {
+        int sets_per_wg, int ksteps, NormIn nin, GluOut glu) {
     constexpr int MT = 64 * NW;
     constexpr bool HL = XT == 1;                          // x carried as f16 hi + lo
     extern __shared__ uint32_t lds[];
@@ -148,8 +157,15 @@ __global__ __launch_bounds__(64 * NW) void q2_0_gemv_mfma_kernel(
     // y + z * R.  Items are numbered set-major over the split's steps.
     const int s0 = blockIdx.y * ksteps, s1 = min(steps, s0 + ksteps), L = s1 - s0;
     y += (size_t)blockIdx.y * R;
+    // Sets of this workgroup, numbered c = 0 .. nset_wg-1 in LDS and in the
+    // item space; phys(c) = their set index relative to set_lo in W.  With
+    // SwiGLU, nsets counts gate sets and c < npair are gate sets, the rest
+    // their up sets.
     const int set_lo = blockIdx.x * sets_per_wg;
-    const int nset_wg = min(sets_per_wg, nsets - set_lo);
+    const int npair = min(sets_per_wg, nsets - set_lo);
+    const int nset_wg = glu.pair_sets ? 2 * npair : npair;
+    auto phys = [&](int c) { return glu.pair_sets && c >= npair ? glu.pair_sets + c - npair : c; };
+    const int wsets = glu.pair_sets ? glu.pair_sets + npair : npair;   // sets spanned in W
     const int total = nset_wg * L;
     const int a = total * wave / NW, b = total * (wave + 1) / NW;
     const int nitems = b - a;
@@ -199,18 +215,19 @@ __global__ __launch_bounds__(64 * NW) void q2_0_gemv_mfma_kernel(
     // past the wave's range, or scales past the workgroup's sets, return
     // zeros (a past-the-range item gets an offset beyond the resource).
     const __amdgpu_buffer_rsrc_t trs =
-            make_rsrc(codes + (size_t)set_lo * steps * 2048, (uint32_t)nset_wg * steps * 2048u);
+            make_rsrc(codes + (size_t)set_lo * steps * 2048, (uint32_t)wsets * steps * 2048u);
     const __amdgpu_buffer_rsrc_t srs =
-            make_rsrc(scales + (size_t)set_lo * bgroups * 256, (uint32_t)nset_wg * bgroups * 512u);
+            make_rsrc(scales + (size_t)set_lo * bgroups * 256, (uint32_t)wsets * bgroups * 512u);
     // Loads of item `it` (at cursor `ld`): its tile and the scales of its
     // drain group that this lane's column needs: rows 4*rq .. 4*rq+3 of
     // block 16*(s/4) + 4*j + kb.
     auto load = [&](int it, const Cursor &ld, u32x4 (&cw)[2], u32x2 &sc) {
-        const uint32_t off = it < nitems ? (uint32_t)(ld.set * steps + ld.s) * 2048u + lane * 16
+        const int ps = phys(ld.set);
+        const uint32_t off = it < nitems ? (uint32_t)(ps * steps + ld.s) * 2048u + lane * 16
                                          : 0xfffff000u;
         cw[0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(trs, off, 0, CP_NT));
         cw[1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(trs, off + 1024, 0, CP_NT));
-        const int si = ((ld.set * bgroups + (ld.s >> 2)) * 16 + 4 * j + kb) * 16 + 4 * rq;
+        const int si = ((ps * bgroups + (ld.s >> 2)) * 16 + 4 * j + kb) * 16 + 4 * rq;
         sc = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(srs, si * 2, 0, 0));
     };
 
@@ -456,6 +473,11 @@ __global__ __launch_bounds__(64 * NW) void q2_0_gemv_mfma_kernel(
         }
     }
     __syncthreads();
+    if (glu.pair_sets) {
+        for (int i = threadIdx.x; i < npair * 16; i += MT)
+            glu.out[set_lo * 16 + i] = gd_f2h(gd_silu(ysum[i]) * ysum[npair * 16 + i]);
+        return;
+    }
     for (int i = threadIdx.x; i < nset_wg * 16; i += MT) {
         const int row = set_lo * 16 + i;
         if (row < R) y[row] = ysum[i];
@@ -496,31 +518,34 @@ Split plan(int64_t nsets, int steps, int ksplit, int64_t slots, int64_t cap) {
 
 template <int XT, int NW, int P>
 int launch(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, size_t xlds, const NormIn &nin,
-           int ksplit) {
+           int ksplit, const GluOut &glu) {
     const int64_t K = w->K, R = w->R;
     const int nblk = (int)(K >> 7), steps = (nblk + 3) / 4;
     const int cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
-    const int64_t nsets = (R + 15) / 16;
+    // SwiGLU: split over gate sets, each bringing its up set along.
+    const int64_t nsets = glu.pair_sets ? glu.pair_sets : (R + 15) / 16;
+    const int rows_per_set = glu.pair_sets ? 2 : 1;
     // Row results of up to `cap` sets fit beside x in LDS.  The occupancy
     // depends on the LDS footprint, so it is looked up per K.
     const int64_t cap = std::min<int64_t>(256, (int64_t)(LDS_BYTES - xlds) / 64);
     const int occ = occupancy_memo<XT, NW, P>(nblk, xlds + (size_t)cap * 64);
-    const Split sp = plan(nsets, steps, ksplit, (int64_t)cus * occ, cap);
+    const Split sp = plan(nsets, steps, glu.pair_sets ? 1 : ksplit, (int64_t)cus * occ,
+                          cap / rows_per_set);
     GD_REQUIRE(ctx, sp.per * steps * NW < (1LL << 31) && sp.per * steps / NW + 1 < (1LL << 20),
                "gd_q2_0_gemv: R=%lld too large", (long long)R);
-    const size_t lds = xlds + (size_t)sp.per * 64;
+    const size_t lds = xlds + (size_t)sp.per * rows_per_set * 64;
     hipLaunchKernelGGL((q2_0_gemv_mfma_kernel<XT, NW, P>), dim3((unsigned)sp.grid, sp.nz),
                        dim3(64 * NW), lds, ctx->stream, (const uint8_t *)w->codes,
                        (const uint16_t *)w->scales, x, y, (int)K, (int)R, (int)nsets, (int)sp.per,
-                       sp.ksteps, nin);
+                       sp.ksteps, nin, glu);
     GD_LAUNCHED(ctx, "q2_0_gemv_mfma");
     return GD_OK;
 }
 
 template <int XT, int NW, int P>
 int launch_or_prepare(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, size_t xlds,
-                      const NormIn &nin, int ksplit) {
-    if (w) return launch<XT, NW, P>(ctx, w, x, y, xlds, nin, ksplit);
+                      const NormIn &nin, int ksplit, const GluOut &glu) {
+    if (w) return launch<XT, NW, P>(ctx, w, x, y, xlds, nin, ksplit, glu);
     // Preparation only (x carries nblk): fill the occupancy memo.
     const int nblk = (int)(intptr_t)x;
     const size_t cap = std::min<size_t>(256, (LDS_BYTES - xlds) / 64);
@@ -530,13 +555,14 @@ int launch_or_prepare(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, siz
 
 template <int XT>
 int launch_nw(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, size_t xlds,
-              const NormIn &nin = NormIn{nullptr, nullptr, nullptr, 0.f, 0, 0}, int ksplit = 1) {
+              const NormIn &nin = NormIn{nullptr, nullptr, nullptr, 0.f, 0, 0}, int ksplit = 1,
+              const GluOut &glu = GluOut{nullptr, 0}) {
     // Waves per workgroup (all share one staged copy of x) and tiles in
     // flight per wave; GADEON_GEMV_NW / GADEON_GEMV_P override for tuning.
     static const char *env_nw = getenv("GADEON_GEMV_NW");
     static const char *env_p = getenv("GADEON_GEMV_P");
     const int nw = env_nw ? atoi(env_nw) : 16, pp = env_p ? atoi(env_p) : 2;
-#define GD_L(NW_, P_) launch_or_prepare<XT, NW_, P_>(ctx, w, x, y, xlds, nin, ksplit)
+#define GD_L(NW_, P_) launch_or_prepare<XT, NW_, P_>(ctx, w, x, y, xlds, nin, ksplit, glu)
     // The fused-norm variant stages one x entry per thread: 16 waves only.
     if constexpr (XT == 2) {
         return GD_L(16, 2);
@@ -600,12 +626,16 @@ int gd_gemv_ksplit(gd_ctx *ctx, int64_t K, int64_t R) {
 // entry).  delta holds nd partials dstride floats apart (nd = 0: none);
 // hout (if not null) receives h + delta; it must not alias h.
 int gd_gemv_mfma_norm(gd_ctx *ctx, const gd_q2w *w, const float *h, const float *delta, int nd,
-                      int dstride, const float *normw, float eps, float *hout, float *y) {
+                      int dstride, const float *normw, float eps, float *hout, float *y,
+                      uint16_t *glu_out) {
     const int nblk = (int)(w->K >> 7);
     const size_t xlds = (size_t)(nblk + 5) * XB * 4 + (size_t)nblk * 8;
     GD_REQUIRE(ctx, (nblk + 5) * 8 <= 1024, "gd_gemv_norm: K=%lld too long (at most 15744)",
                (long long)w->K);
-    return launch_nw<2>(ctx, w, h, y, xlds, NormIn{delta, normw, hout, eps, delta ? nd : 0, dstride});
+    GD_REQUIRE(ctx, !glu_out || w->R % 32 == 0, "gd_gemv_norm: SwiGLU needs R = 2 x 16k rows");
+    const GluOut glu{glu_out, glu_out ? (int)(w->R / 32) : 0};
+    return launch_nw<2>(ctx, w, h, y, xlds, NormIn{delta, normw, hout, eps, delta ? nd : 0, dstride},
+                        1, glu);
 }
 
 // Host-side set-up for GEMVs of reduction length K (the occupancy lookup),

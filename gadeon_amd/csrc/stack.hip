@@ -120,14 +120,6 @@ __global__ void k_onorm_silu(const float *o, const float *proj, int64_t stride, 
 }
 
 // act = silu(gate) * up -> f16 (BonsaiEngine.swift:141-150).
-__global__ void k_swiglu(const float *gu, int FF, uint16_t *out, int N) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (int64_t)N * FF) return;
-    const int64_t n = i / FF, j = i % FF;
-    const float *row = gu + n * 2 * FF;
-    out[i] = gd_f2h(gd_silu(row[j]) * row[FF + j]);
-}
-
 // Attention prep, one block of HD threads per (token, head): q heads take
 // the q half of the fused [q | gate] pair, RMS-normalize it with q_norm and
 // rotate it; kv heads normalize + rotate k and append k, v to the f16 cache
@@ -621,17 +613,16 @@ int forward(gd_stack *st, int N, bool decode) {
             nsplit = p.split;
             R_(gd_gemm_launch(ctx, &ly.out_proj, N, st->a16, GD_F16, st->contrib, GD_F32, p));
         }
+        // gate_up with SwiGLU in its epilogue: a16 = silu(gate x) * (up x).
         if (decode) {
             R_(gd_gemv_mfma_norm(ctx, &ly.gate_up, hcur, st->contrib, nd, E, ly.post_norm, eps,
-                                 hnext, st->proj));
+                                 hnext, st->proj, st->a16));
             std::swap(hcur, hnext);
         } else {
             K_(k_add_rmsnorm, dim3(N), dim3(1024), 0, s, st->x, st->contrib, ly.post_norm,
                st->xn16, E, eps, nsplit, (int64_t)N * E);
-            R_(gd_q2_0_gemm(ctx, &ly.gate_up, N, st->xn16, GD_F16, st->proj, GD_F32));
+            R_(gd_gemm_glu(ctx, &ly.gate_up, N, st->xn16, st->a16));
         }
-        K_(k_swiglu, dim3(gd_blocks((int64_t)N * FF, 256)), dim3(256), 0, s, st->proj, FF,
-           st->a16, N);
         nsplit = 1;
         if (decode) {
             nd = gd_gemv_ksplit(ctx, ly.down.K, ly.down.R);

@@ -164,10 +164,13 @@ int gd_q2_0_gemv_split(gd_ctx *ctx, const gd_q2w *w, const void *x, int x_dtype,
  * as gd_add + gd_rmsnorm(.., GD_F16, ..) + gd_q2_0_gemv (MetalEnc.addInplace
  * + rmsnorm + gemv, MetalEnc.swift:213-236, 572-597, 78-99) in one launch
  * instead of three.  h, delta, w_norm and hout are f32 [K], 16-byte aligned
- * (delta_stride a multiple of 4); K <= 15744. */
+ * (delta_stride a multiple of 4); K <= 15744.  With glu_out not null, W is
+ * [gate; up] (R = 2 ff rows, ff a multiple of 16) and glu_out[r] =
+ * f16(silu(gate_r . x) * (up_r . x)), r < ff, replaces y (y unused): the
+ * feed-forward's SwiGLU (Kernels.metal:1118-1139 silu_mul) fused in. */
 int gd_q2_0_gemv_norm(gd_ctx *ctx, const gd_q2w *w, const float *h, const float *delta,
                       int nd, int64_t delta_stride, const float *w_norm, float eps,
-                      float *hout, float *y);
+                      float *hout, float *y, uint16_t *glu_out);
 
 /* ---- Q2_0 GEMM (prefill): MetalEnc.gemm, MetalEnc.swift:145-189 --------------
  * Y[t][r] = sum_k X[t][k] * W[r][k], token-major X[T][K] and Y[T][R].
@@ -187,6 +190,14 @@ int gd_q2_0_gemm(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X,
  * variant; no counterpart in the reference. */
 int gd_q2_0_gemm_plan(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X,
                       int x_dtype, void *Y, int y_dtype, int mt, int nt, int split);
+
+/* Feed-forward GEMM with SwiGLU fused into the epilogue: W is [gate; up]
+ * (R = 2 ff rows, ff a multiple of 16), X f16 [T][K], out f16 [T][ff] =
+ * silu(X gate^T) * (X up^T), as gd_q2_0_gemm (f32 Y) followed by the
+ * reference's silu_mul (Kernels.metal:1118-1139) and an f16 rounding, without
+ * the f32 intermediate.  No counterpart in the reference as one call. */
+int gd_q2_0_gemm_swiglu(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X,
+                        uint16_t *out);
 
 /* ---- Q2_0 row dequant: MetalEnc.dequantRow / embedBatch ----------------------
  * out[n][k] = (code-1)*d of row ids[n], exactly (f16 * small integer is exact

@@ -123,7 +123,8 @@ def test_gemv_norm_vs_oracle_and_unfused(ctx, K, R, with_delta):
     wn = O.lcg_normal(K, 93, 1.0, 0.2)
     dh, dd, dwn = ctx.put(h), ctx.put(d), ctx.put(wn)
     dho, dy = ctx.alloc(K * 4), ctx.alloc(R * 4)
-    ctx.gd_q2_0_gemv_norm(C.byref(w), dh, dd if with_delta else None, 1, 0, dwn, eps, dho, dy)
+    ctx.gd_q2_0_gemv_norm(C.byref(w), dh, dd if with_delta else None, 1, 0, dwn, eps, dho, dy,
+                          None)
     y = ctx.get(dy, R, np.float32)
     hp = (h + d).astype(np.float32)
     assert np.array_equal(ctx.get(dho, K, np.float32), hp)
@@ -167,7 +168,7 @@ def test_gemv_split_partials_sum_to_gemv(ctx, K, R, ksplit):
         h = O.lcg_normal(K2, 96, 0.0, 2.0)
         wn = O.lcg_normal(K2, 97, 1.0, 0.1)
         dh, dwn, dho, dy2 = ctx.put(h), ctx.put(wn), ctx.alloc(K2 * 4), ctx.alloc(R2 * 4)
-        ctx.gd_q2_0_gemv_norm(C.byref(w2), dh, dy, ns.value, R, dwn, 1e-6, dho, dy2)
+        ctx.gd_q2_0_gemv_norm(C.byref(w2), dh, dy, ns.value, R, dwn, 1e-6, dho, dy2, None)
         hp = h + parts[:, :K2].sum(0, dtype=np.float32)
         assert np.allclose(ctx.get(dho, K2, np.float32), hp, rtol=1e-6, atol=1e-5)
         x16 = O.rmsnorm(hp[None], wn, 1e-6)[0].astype(np.float16)
@@ -186,11 +187,11 @@ def test_gemv_norm_rejects_alias_and_long_k(ctx):
     ctx.gd_q2w_alloc(256, 16, C.byref(w))
     dh, dy = ctx.alloc(256 * 4), ctx.alloc(16 * 4)
     with pytest.raises(RuntimeError, match="alias"):
-        ctx.gd_q2_0_gemv_norm(C.byref(w), dh, None, 0, 0, dh, 1e-6, dh, dy)
+        ctx.gd_q2_0_gemv_norm(C.byref(w), dh, None, 0, 0, dh, 1e-6, dh, dy, None)
     ctx.gd_q2w_free(C.byref(w))
     ctx.gd_q2w_alloc(15872, 16, C.byref(w))
     with pytest.raises(RuntimeError, match="15744"):
-        ctx.gd_q2_0_gemv_norm(C.byref(w), dh, None, 0, 0, dh, 1e-6, None, dy)
+        ctx.gd_q2_0_gemv_norm(C.byref(w), dh, None, 0, 0, dh, 1e-6, None, dy, None)
     ctx.gd_q2w_free(C.byref(w))
     ctx.free(dh)
     ctx.free(dy)
@@ -269,6 +270,59 @@ def test_gemm_every_plan(ctx, xt, yt, mt, nt, split):
     assert rel_diff(Y, want) < (2e-3 if yt == ga.F16 else 1e-4)
     ctx.free(dX)
     ctx.free(dY)
+    free_w(ctx, w)
+
+
+def silu(v):
+    return v / (1.0 + np.exp(-v))
+
+
+@pytest.mark.parametrize("T,K,ff", [(512, 5120, 17408), (37, 1024, 208), (1, 256, 16)])
+def test_gemm_swiglu_vs_oracle(ctx, T, K, ff):
+    """SwiGLU epilogue: f16(silu(X gate^T) * (X up^T)) against the oracle
+    GEMV rows (ragged T and ff = 208, 13 groups of 16, exercise partial
+    tiles); the full-size case samples 64 gate rows."""
+    R = 2 * ff
+    blocks = O.lcg_q2_0(K, R, K + ff)
+    w = upload_w(ctx, blocks, K, R)
+    Xh = O.lcg_normal_f16(T * K, 79).reshape(T, K)
+    dX, dO = ctx.put(Xh.view(np.uint16)), ctx.alloc(T * ff * 2)
+    ctx.gd_q2_0_gemm_swiglu(C.byref(w), T, dX, dO)
+    out = ctx.get(dO, (T, ff), np.float16).astype(np.float32)
+    rows = np.arange(ff) if ff <= 1024 else np.random.default_rng(3).choice(ff, 64, replace=False)
+    blk = blocks.reshape(R, -1)
+    g = np.ascontiguousarray(blk[rows]); u = np.ascontiguousarray(blk[rows + ff])
+    toks = range(T) if T <= 64 else (0, 1, 200, T - 1)
+    for t in toks:
+        x = Xh[t].astype(np.float32)
+        gv = O.q2_0_matvec(g, K, len(rows), x, threads=8)
+        uv = O.q2_0_matvec(u, K, len(rows), x, threads=8)
+        want = (silu(gv) * uv).astype(np.float16).astype(np.float32)
+        assert rel_diff(out[t, rows], want) < 2e-3, t
+    ctx.free(dX)
+    ctx.free(dO)
+    free_w(ctx, w)
+
+
+@pytest.mark.parametrize("K,ff", [(5120, 17408), (1024, 208)])
+def test_gemv_norm_swiglu_vs_oracle(ctx, K, ff):
+    """The decode feed-forward input: fused add + norm, [gate; up] GEMV and
+    SwiGLU in one launch, against the oracle."""
+    R, eps = 2 * ff, 1e-6
+    blocks = O.lcg_q2_0(K, R, 3 * K + ff)
+    w = upload_w(ctx, blocks, K, R)
+    h = O.lcg_normal(K, 98, 0.0, 2.0)
+    d = O.lcg_normal(K, 99, 0.0, 1.0)
+    wn = O.lcg_normal(K, 100, 1.0, 0.1)
+    dh, dd, dwn, dho, dO = ctx.put(h), ctx.put(d), ctx.put(wn), ctx.alloc(K * 4), ctx.alloc(ff * 2)
+    ctx.gd_q2_0_gemv_norm(C.byref(w), dh, dd, 1, 0, dwn, eps, dho, None, dO)
+    out = ctx.get(dO, ff, np.float16).astype(np.float32)
+    x = O.rmsnorm((h + d)[None], wn, eps)[0].astype(np.float16).astype(np.float32)
+    y = O.q2_0_matvec(blocks, K, R, x, threads=8)
+    want = (silu(y[:ff]) * y[ff:]).astype(np.float16).astype(np.float32)
+    assert rel_diff(out, want) < 2e-3
+    for p in (dh, dd, dwn, dho, dO):
+        ctx.free(p)
     free_w(ctx, w)
 
 
