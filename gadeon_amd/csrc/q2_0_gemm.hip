@@ -225,16 +225,6 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2))) vo
 #pragma unroll
                 for (int n = 0; n < NT; n++)
                     acc[m][n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[cur][m], b[cur][n], acc[m][n], 0, 0, 0);
-            if (ks < 3) {
-                // Interleave: each MFMA followed by a share of the next
-                // step's VALU (dequant) and LDS reads.
-#pragma unroll
-                for (int i = 0; i < MT * NT; i++) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x002, (17 * NT + MT * NT - 1) / (MT * NT), 0);
-                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-                }
-            }
         }
     };
 
