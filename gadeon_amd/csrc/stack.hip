@@ -103,6 +103,113 @@ __global__ void k_conv4_ring(const float *proj, int64_t stride, float *ring, int
 
 // o <- rmsnorm_d(o) * w * silu(z), written as f16 for the out projection
 // (GDN.swift:113-115).  One wave per (token, value head).
+// Decode step of one recurrent layer for one value head, when every value
+// head has its own q/k head (nK == nV, so no two workgroups touch the same
+// conv channel): causal conv + SiLU of the head's q, k and v channels
+// (advancing their conv ring), gate, L2 norms of q and k, the delta-rule
+// state update, and the gated RMS norm of the output into f16.  The same
+// arithmetic, in the same order, as k_conv4 + gd_gdn_decode (GATE, NORM) +
+// k_onorm_silu, in one launch (GDN.swift:71-109, BonsaiEngine.swift:
+// 98-139).  Lane l of wave w owns value columns l and l + 64 and key rows
+// 32w .. 32w+31.
+__global__ __launch_bounds__(256) void k_gdn_step(
+        const float *proj, float *ring, const float *cw, const float *dt, const float *aNeg,
+        float *S, const float *onw, uint16_t *out, int convDim, int keyDim, int off_z, int off_b,
+        int off_a, float qScale, float eps) {
+    __shared__ float kq[2][HD];                  // k, q after conv + SiLU
+    __shared__ float vs[HD];
+    __shared__ float red[4][2][64];
+    __shared__ float scal[2];
+    __shared__ float gate[2];                    // beta, gamma
+    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    float *Sh = S + (int64_t)h * HD * HD;
+    // State loads first: they are the bandwidth.
+    float s0[32], s1[32];
+#pragma unroll
+    for (int r = 0; r < 32; r++) {
+        s0[r] = Sh[(int64_t)(wave * 32 + r) * HD + lane];
+        s1[r] = Sh[(int64_t)(wave * 32 + r) * HD + lane + 64];
+    }
+    auto conv = [&](int c) {
+        const float w0 = cw[c * 4], w1 = cw[c * 4 + 1], w2 = cw[c * 4 + 2], w3 = cw[c * 4 + 3];
+        const float r0 = ring[c], r1 = ring[convDim + c], r2 = ring[2 * convDim + c];
+        const float cur = proj[c];
+        float acc = 0.0f;
+        acc += r0 * w0;
+        acc += r1 * w1;
+        acc += r2 * w2;
+        acc += cur * w3;
+        ring[c] = r1;
+        ring[convDim + c] = r2;
+        ring[2 * convDim + c] = cur;
+        return gd_silu(acc);
+    };
+    // Threads 0..127: q channel tid; 128..255: k channel tid - 128; threads
+    // 0..127 also take v channel tid.
+    {
+        const int i = tid & (HD - 1);
+        const float y = conv(tid < HD ? h * HD + i : keyDim + h * HD + i);
+        kq[tid < HD ? 1 : 0][i] = y;
+        if (tid < HD) vs[i] = conv(2 * keyDim + h * HD + i);
+    }
+    if (tid == 0) {
+        gate[0] = gd_sigmoid(proj[off_b + h]);
+        gate[1] = expf(gd_softplus(proj[off_a + h] + dt[h]) * aNeg[h]);
+    }
+    __syncthreads();
+    // Waves 0/1 reduce |k|^2 and |q|^2.
+    if (wave < 2) {
+        const float a = kq[wave][lane], c = kq[wave][lane + 64];
+        const float ss = gd_wave_sum(a * a + c * c);
+        if (lane == 0) scal[wave] = 1.0f / sqrtf(ss + eps);
+    }
+    __syncthreads();
+    const float rk = scal[0], rq = scal[1], beta = gate[0], gam = gate[1];
+    float sk0 = 0.0f, sk1 = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 32; r++) {
+        const float kv = kq[0][wave * 32 + r];
+        s0[r] *= gam;
+        s1[r] *= gam;
+        sk0 = fmaf(s0[r], kv, sk0);
+        sk1 = fmaf(s1[r], kv, sk1);
+    }
+    red[wave][0][lane] = sk0;
+    red[wave][1][lane] = sk1;
+    __syncthreads();
+    sk0 = (red[0][0][lane] + red[1][0][lane] + red[2][0][lane] + red[3][0][lane]) * rk;
+    sk1 = (red[0][1][lane] + red[1][1][lane] + red[2][1][lane] + red[3][1][lane]) * rk;
+    const float d0 = beta * (vs[lane] - sk0) * rk, d1 = beta * (vs[lane + 64] - sk1) * rk;
+    __syncthreads();                             // red[] is reused below
+    float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 32; r++) {
+        const int i = wave * 32 + r;
+        const float kv = kq[0][i], qv = kq[1][i];
+        s0[r] = fmaf(kv, d0, s0[r]);
+        s1[r] = fmaf(kv, d1, s1[r]);
+        a0 = fmaf(s0[r], qv, a0);
+        a1 = fmaf(s1[r], qv, a1);
+        Sh[(int64_t)i * HD + lane] = s0[r];
+        Sh[(int64_t)i * HD + lane + 64] = s1[r];
+    }
+    red[wave][0][lane] = a0;
+    red[wave][1][lane] = a1;
+    __syncthreads();
+    if (wave == 0) {
+        const float o0 = (red[0][0][lane] + red[1][0][lane] + red[2][0][lane] + red[3][0][lane]) *
+                         rq * qScale;
+        const float o1 = (red[0][1][lane] + red[1][1][lane] + red[2][1][lane] + red[3][1][lane]) *
+                         rq * qScale;
+        const float ss = gd_wave_sum(o0 * o0 + o1 * o1);
+        const float sc = 1.0f / sqrtf(ss / (float)HD + eps);
+        const float *z = proj + off_z + h * HD;
+        out[h * HD + lane] = gd_f2h(o0 * sc * onw[lane] * gd_silu(z[lane]));
+        out[h * HD + lane + 64] = gd_f2h(o1 * sc * onw[lane + 64] * gd_silu(z[lane + 64]));
+    }
+}
+
 __global__ void k_onorm_silu(const float *o, const float *proj, int64_t stride, int off_z,
                              const float *w, uint16_t *out, int nV, int N, float eps) {
     const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
@@ -119,7 +226,6 @@ __global__ void k_onorm_silu(const float *o, const float *proj, int64_t stride, 
     dst[lane + 64] = gd_f2h(b * s * w[lane + 64] * gd_silu(z[lane + 64]));
 }
 
-// act = silu(gate) * up -> f16 (BonsaiEngine.swift:141-150).
 // Attention prep, one block of HD threads per (token, head): q heads take
 // the q half of the fused [q | gate] pair, RMS-normalize it with q_norm and
 // rotate it; kv heads normalize + rotate k and append k, v to the f16 cache
@@ -563,7 +669,11 @@ int forward(gd_stack *st, int N, bool decode) {
         }
         if (ly.rec) {
             const int off_z = st->convDim, off_b = off_z + st->valDim, off_a = off_b + nV;
-            if (decode) {
+            if (decode && nK == nV && c.d_state == HD) {
+                K_(k_gdn_step, dim3(nV), dim3(256), 0, s, st->proj, ly.conv_state, ly.conv_w,
+                   ly.dt, ly.a_neg, ly.rec_state, ly.ssm_norm, st->a16, st->convDim, st->keyDim,
+                   off_z, off_b, off_a, qScale, eps);
+            } else if (decode) {
                 K_(k_conv4, dim3(gd_blocks(st->convDim, 256)), dim3(256), 0, s, st->proj,
                    (int64_t)RP, ly.conv_state, ly.conv_w, st->conv_out, st->convDim, 1);
                 // Fused gate + L2 norm + delta-rule step, state in place.
@@ -585,8 +695,9 @@ int forward(gd_stack *st, int N, bool decode) {
                                   st->beta, ly.rec_state, st->o32, st->valDim, GD_F32, qScale,
                                   64));
             }
-            K_(k_onorm_silu, dim3(gd_blocks((int64_t)N * nV, 4)), dim3(256), 0, s, st->o32,
-               st->proj, (int64_t)RP, off_z, ly.ssm_norm, st->a16, nV, N, eps);
+            if (!(decode && nK == nV && c.d_state == HD))
+                K_(k_onorm_silu, dim3(gd_blocks((int64_t)N * nV, 4)), dim3(256), 0, s, st->o32,
+                   st->proj, (int64_t)RP, off_z, ly.ssm_norm, st->a16, nV, N, eps);
         } else {
             K_(k_attn_prep, dim3(N, H + HKV), dim3(HD), 0, s, st->proj, (int64_t)RP, ly.q_norm,
                ly.k_norm, st->q32, st->gate32, ly.kc, ly.vc, st->page_table, st->dpos, H, HKV,

@@ -60,8 +60,11 @@ def margin_ok(logits):
     return top[1] - top[0] > 1e-2 * max(1.0, np.abs(logits).max())
 
 
-def test_stack_prefill_decode_generate(ctx):
-    cfg, st = make_stack(ctx)
+@pytest.mark.parametrize("nk", [2, 4])   # 4: every value head has its own key head
+def test_stack_prefill_decode_generate(ctx, nk):
+    """nk = 2 shares key heads between value heads (separate conv, step and
+    gated-norm kernels in decode); nk = 4 takes the fused one-launch step."""
+    cfg, st = make_stack(ctx, n_k_head=nk)
     lib = ctx.lib
     try:
         read = tensor_reader(ctx, st)
