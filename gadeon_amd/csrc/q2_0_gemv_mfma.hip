@@ -23,22 +23,23 @@
 //     pre-scale is staged scaled down by a power of two 2^-e, undone later.
 //   * B operand: each MFMA block has four output columns; at chunk step s the
 //     x of its Q2 block goes into column s % 4 and the other columns get
-//     zeros, so four consecutive steps accumulate in four columns and each
-//     is scaled by its own block scale d once per four steps ("drain"),
-//     where sum(x) of the block is subtracted as well.  x is staged once per
-//     workgroup in LDS, already permuted into the (k, k+8) pair order of the
-//     unpack and pre-scaled, with zero blocks for the other columns.  f32 x
-//     is split into hi = f16(x) and lo = f16((x - hi) * 2^11), two B operands
-//     accumulated apart and recombined in f32 at the drain.
+//     zeros.  x is staged once per workgroup in LDS, already permuted into
+//     the (k, k+8) pair order of the unpack and pre-scaled, with zero blocks
+//     for the other columns.  f32 x is split into hi = f16(x) and
+//     lo = f16((x - hi) * 2^11), two B operands accumulated apart and
+//     recombined in f32.
 //   * Work split.  A "set" is one 16-row group; an "item" is one tile (one
 //     chunk step of 512 K of one set).  Every workgroup gets the same number
-//     of consecutive sets, and its NW waves split the workgroup's items into
-//     NW equal contiguous ranges.  A set that one wave covers whole goes to
-//     the workgroup's LDS results directly; a set cut by a range boundary is
-//     summed after one barrier, in wave order (the result does not depend on
-//     timing); the rows go out as one coalesced store at the end.
+//     of consecutive sets (and, with a K split, one range of steps).  Its
+//     waves take the workgroup's items one at a time from an LDS counter, so
+//     a wave whose loads come back late simply takes fewer items (with a
+//     fixed share per wave, the workgroup waited about 3 us for its slowest
+//     wave).  An item's products are scaled by their block scales d, sum(x)
+//     of each block is subtracted, and the item's 16 row partials go to LDS;
+//     after one barrier each row is summed over its steps in step order, so
+//     the result does not depend on which wave took which item.
 //   * Latency.  Each wave keeps the next P tiles in flight (a register ring),
-//     each with the four scales its drain needs (one 8-byte load).  Tiles,
+//     each with the four scales its item needs (one 8-byte load).  Tiles,
 //     scales and x are read with bounds-checked buffer loads: a load past
 //     the end returns zeros without a memory access, so every load in the
 //     main loop is unconditional and the compiler waits only for the tile an
@@ -48,8 +49,14 @@
 namespace {
 
 constexpr int XB = 68;    // LDS dwords per staged x block
-// Dynamic LDS available beside the static reduction array (16 waves).
+// Dynamic LDS available beside the kernel's few static words.
 constexpr size_t LDS_BYTES = 160 * 1024 - 2048;
+
+// LDS bytes of the x staging: the x planes (two for f32 x), then the block
+// sums and exponents of x.
+size_t xlds_bytes(int nblk, bool hl) {
+    return (size_t)(nblk + 5) * XB * 4 * (hl ? 2 : 1) + (size_t)((nblk + 1) & ~1) * 8;
+}
 
 // Operand dword m holds codes (m, m+8) of w at bit position POS[m] of its
 // two f16 halves; the x pair it meets is pre-scaled by XSCALE[m] = 2^(8-POS[m]).
@@ -75,15 +82,6 @@ __device__ __forceinline__ f16x8 as_f16x8(uint32_t a, uint32_t b, uint32_t c, ui
 __device__ __forceinline__ uint32_t pack_h2(float a, float b) {
     return (uint32_t)gd_f2h(a) | ((uint32_t)gd_f2h(b) << 16);
 }
-
-// Position of an item inside the workgroup's item space (set-major).
-// Steps run s0 .. s1-1 within each set (the workgroup's K split).
-struct Cursor {
-    int set, s;
-    __device__ void next(int s0, int s1) {
-        if (++s == s1) { s = s0; ++set; }
-    }
-};
 
 // Buffer resource over `bytes` bytes at p (raw: no stride).  Loads at an
 // offset past the end return zeros without touching memory, which keeps
@@ -130,19 +128,23 @@ __global__ __launch_bounds__(64 * NW) void q2_0_gemv_mfma_kernel(
         int sets_per_wg, int ksteps, NormIn nin, GluOut glu) {
     constexpr int MT = 64 * NW;
     constexpr bool HL = XT == 1;                          // x carried as f16 hi + lo
-    extern __shared__ uint32_t lds[];
+    // The dynamic LDS holds 16-byte operands, so it must start 16-byte
+    // aligned after the static words (a 4-byte offset made every b128 LDS
+    // access of the kernel misaligned and the GEMV several times slower).
+    extern __shared__ __align__(16) uint32_t lds[];
     const int nblk = K >> 7;
     // LDS: x planes, block b at dword XB*b (64 pair dwords + 4 of padding, so
     // the blocks one load instruction reads start on different banks), then
     // two zero blocks four blocks apart (see zero_blk below); per-block sum
-    // and exponent of x; the workgroup's row results.
+    // and exponent of x (nblk rounded up to even, so that what follows is
+    // 16-byte aligned); the row partials of every item.
     const int xstride = (nblk + 5) * XB;                   // dwords per x plane
     uint32_t *xp = lds;                                    // hi (or f16) pairs
     uint32_t *xq = lds + xstride;                          // lo plane (f32 x only)
     float *sx = (float *)(lds + (HL ? 2 : 1) * xstride);   // [nblk] block sums of x
-    float *ex = sx + nblk;                                 // [nblk] 2^(16+e_b)
-    float *ysum = ex + nblk;                               // [sets_per_wg * 16]
-    __shared__ float red[NW][2][16];                       // partial sums of cut sets
+    float *ex = sx + ((nblk + 1) & ~1);                    // [nblk] 2^(16+e_b)
+    float *part = ex + ((nblk + 1) & ~1);                  // [items][16] row partials
+    __shared__ __align__(16) int next_item;                // next item to take
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -154,21 +156,18 @@ __global__ __launch_bounds__(64 * NW) void q2_0_gemv_mfma_kernel(
     const int bgroups = (nblk + 15) >> 4;
 
     // K split z = blockIdx.y: steps [s0, s1) of every set; its rows go to
-    // y + z * R.  Items are numbered set-major over the split's steps.
+    // y + z * R.  Item i is step s0 + i % L of set i / L (set-major).
     const int s0 = blockIdx.y * ksteps, s1 = min(steps, s0 + ksteps), L = s1 - s0;
     y += (size_t)blockIdx.y * R;
     // Sets of this workgroup, numbered c = 0 .. nset_wg-1 in LDS and in the
-    // item space; phys(c) = their set index relative to set_lo in W.  With
-    // SwiGLU, nsets counts gate sets and c < npair are gate sets, the rest
-    // their up sets.
+    // item space; set c is set set_lo + c of W.  With SwiGLU, nsets counts
+    // gate sets, c < npair are gate sets and the rest their up sets, set
+    // set_lo + pair_sets + c - npair of W.
     const int set_lo = blockIdx.x * sets_per_wg;
     const int npair = min(sets_per_wg, nsets - set_lo);
     const int nset_wg = glu.pair_sets ? 2 * npair : npair;
-    auto phys = [&](int c) { return glu.pair_sets && c >= npair ? glu.pair_sets + c - npair : c; };
     const int wsets = glu.pair_sets ? glu.pair_sets + npair : npair;   // sets spanned in W
-    const int total = nset_wg * L;
-    const int a = total * wave / NW, b = total * (wave + 1) / NW;
-    const int nitems = b - a;
+    const int total = nset_wg * L;                         // items of the workgroup
 
     // Staging entry e = (block e/8, chunk e%8): its x loads are issued before
     // the tile prefetch, so waiting for them leaves the tiles in flight.
@@ -212,32 +211,43 @@ __global__ __launch_bounds__(64 * NW) void q2_0_gemv_mfma_kernel(
     __builtin_amdgcn_sched_barrier(0);
 
     // Tiles of the workgroup's sets: (set, s) is tile set * steps + s.  Loads
-    // past the wave's range, or scales past the workgroup's sets, return
-    // zeros (a past-the-range item gets an offset beyond the resource).
+    // for items past the workgroup's last return zeros (they get an offset
+    // beyond the resource).
     const __amdgpu_buffer_rsrc_t trs =
             make_rsrc(codes + (size_t)set_lo * steps * 2048, (uint32_t)wsets * steps * 2048u);
     const __amdgpu_buffer_rsrc_t srs =
             make_rsrc(scales + (size_t)set_lo * bgroups * 256, (uint32_t)wsets * bgroups * 512u);
-    // Loads of item `it` (at cursor `ld`): its tile and the scales of its
-    // drain group that this lane's column needs: rows 4*rq .. 4*rq+3 of
-    // block 16*(s/4) + 4*j + kb.
-    auto load = [&](int it, const Cursor &ld, u32x4 (&cw)[2], u32x2 &sc) {
-        const int ps = phys(ld.set);
-        const uint32_t off = it < nitems ? (uint32_t)(ps * steps + ld.s) * 2048u + lane * 16
-                                         : 0xfffff000u;
+    // Loads of item `it`: its tile, and for the lanes of column s % 4 the
+    // scales of rows 4*rq .. 4*rq+3 of their block 4*s + kb (the other
+    // lanes load nothing).
+    // The address arithmetic has no branch (the compiler's wait counting is
+    // exact only over straight-line loads): an item past the last gets the
+    // offset 0xfffff000, beyond every resource.
+    const int up_shift = glu.pair_sets ? glu.pair_sets - npair : 0;
+    auto pick = [](uint32_t off, uint32_t dead) { return (off & ~dead) | (dead & 0xfffff000u); };
+    auto load = [&](int it, u32x4 (&cw)[2], u32x2 &sc) {
+        const int c = it / L, s = s0 + (it - c * L);
+        const int ps = c + (c >= npair ? up_shift : 0);
+        const uint32_t dead = (uint32_t)((total - 1 - it) >> 31);      // all ones past the end
+        const uint32_t off = pick((uint32_t)(ps * steps + s) * 2048u + lane * 16, dead);
         cw[0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(trs, off, 0, CP_NT));
         cw[1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(trs, off + 1024, 0, CP_NT));
-        const int si = ((ps * bgroups + (ld.s >> 2)) * 16 + 4 * j + kb) * 16 + 4 * rq;
-        sc = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(srs, si * 2, 0, 0));
+        const uint32_t si = (uint32_t)((ps * bgroups + (s >> 2)) * 16 + 4 * (s & 3) + kb) * 32 + 8 * rq;
+        const uint32_t other = (uint32_t)-(int)(j != (s & 3));
+        sc = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(srs, pick(si, dead | other), 0, 0));
     };
 
-    // One tile goes out before the staging; the rest of the ring after it,
-    // so x (needed first) does not queue behind the whole grid's prefetch.
+    // Ring slot p starts with item p * NW + wave; each later item is taken
+    // from the workgroup counter when a slot frees up.  One tile goes out
+    // before the staging, the rest of the ring after it, so x (needed first)
+    // does not queue behind the whole grid's prefetch.
     u32x4 ring[P][2];
     u32x2 rsc[P];
-    Cursor ld{a / L, s0 + a % L};
-    load(0, ld, ring[0], rsc[0]);
-    ld.next(s0, s1);
+    int rit[P];
+#pragma unroll
+    for (int p = 0; p < P; p++) rit[p] = p * NW + wave;
+    if (threadIdx.x == 0) next_item = NW * P;
+    load(rit[0], ring[0], rsc[0]);
 
     // Stage x: pair p = 8i + k of block b holds (x[b,16i+k], x[b,16i+k+8]) *
     // XSCALE[k] * 2^-e_b.  Thread (b, i) forms the 8 pairs of x[16i ..
@@ -341,23 +351,13 @@ __global__ __launch_bounds__(64 * NW) void q2_0_gemv_mfma_kernel(
     if constexpr (XT != 2)
         for (int e = threadIdx.x + MT; e < nstage; e += MT) stage(e, load_x(e));
 #pragma unroll
-    for (int p = 1; p < P; p++) {
-        load(p, ld, ring[p], rsc[p]);
-        ld.next(s0, s1);
-    }
+    for (int p = 1; p < P; p++) load(rit[p], ring[p], rsc[p]);
     __syncthreads();
 
+    // One item (set c, step s): the four Q2 blocks 4s .. 4s+3 of 16 rows.
     // Accumulator chains: f16 x uses four, f32 x two for hi and two for lo.
-    f32x4 acc[4];
-#pragma unroll
-    for (int c = 0; c < 4; c++) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float yp[4] = {0.f, 0.f, 0.f, 0.f};
-    Cursor cur{a / L, s0 + a % L};
-    int dlo = cur.s;                                      // first step of the open group
-    // One item: ring slot p holds its tile and scales.
-    auto step = [&](const int item, u32x4 (&tile)[2], u32x2 &sc) {
-        const int s = cur.s;
-        if ((s & 3) == 0 || s == s0 || item == 0) dlo = s;   // a drain group starts
+    auto step = [&](const int it, u32x4 (&tile)[2], u32x2 &sc) {
+        const int c = it / L, s = s0 + (it - c * L);
         // MFMA block mb = lane/4 multiplies rows 4*rq .. 4*rq+3 of Q2 block
         // 4s + kb by four K values; column j of its B is x when j == s % 4.
         const int blk = 4 * s + kb;
@@ -368,6 +368,7 @@ __global__ __launch_bounds__(64 * NW) void q2_0_gemv_mfma_kernel(
         const int xoff = (match ? blk : zero_blk) * XB;
         const u32x4 *src = (const u32x4 *)(xp + xoff);
         const u32x4 *srq = (const u32x4 *)(xq + xoff);
+        f32x4 acc[4];
 #pragma unroll
         for (int d = 0; d < 8; d++) {
             uint32_t t[8];
@@ -379,108 +380,76 @@ __global__ __launch_bounds__(64 * NW) void q2_0_gemv_mfma_kernel(
                 const f16x4 a0 = __builtin_bit_cast(f16x4, u32x2{t[4 * q], t[4 * q + 1]});
                 const f16x4 a1 = __builtin_bit_cast(f16x4, u32x2{t[4 * q + 2], t[4 * q + 3]});
                 const int c0 = HL ? q : (2 * q) & 3, c1 = HL ? q : (2 * q + 1) & 3;
+                const f32x4 z{0.f, 0.f, 0.f, 0.f};
+                // The first product of a chain starts it from zero.
+                const bool first0 = d == 0, first1 = !HL && d == 0;
                 acc[c0] = __builtin_amdgcn_mfma_f32_4x4x4f16(
-                        a0, __builtin_bit_cast(f16x4, u32x2{bx[0], bx[1]}), acc[c0], 0, 0, 0);
+                        a0, __builtin_bit_cast(f16x4, u32x2{bx[0], bx[1]}), first0 ? z : acc[c0],
+                        0, 0, 0);
                 acc[c1] = __builtin_amdgcn_mfma_f32_4x4x4f16(
-                        a1, __builtin_bit_cast(f16x4, u32x2{bx[2], bx[3]}), acc[c1], 0, 0, 0);
+                        a1, __builtin_bit_cast(f16x4, u32x2{bx[2], bx[3]}), first1 ? z : acc[c1],
+                        0, 0, 0);
                 if (HL) {
                     const u32x4 bq = srq[2 * d + q];
                     acc[2 + q] = __builtin_amdgcn_mfma_f32_4x4x4f16(
-                            a0, __builtin_bit_cast(f16x4, u32x2{bq[0], bq[1]}), acc[2 + q], 0, 0, 0);
+                            a0, __builtin_bit_cast(f16x4, u32x2{bq[0], bq[1]}),
+                            d == 0 ? z : acc[2 + q], 0, 0, 0);
                     acc[2 + q] = __builtin_amdgcn_mfma_f32_4x4x4f16(
                             a1, __builtin_bit_cast(f16x4, u32x2{bq[2], bq[3]}), acc[2 + q], 0, 0, 0);
                 }
             }
         }
-        const bool set_end = s + 1 == s1;
-        const bool range_end = item + 1 == nitems;
-        if (((s + 1) & 3) == 0 || set_end || range_end) {
-            // Drain: column j holds step sj = 4*(dlo/4) + j of the group, i.e.
-            // block 4*sj + kb, for rows 4*rq + v.
-            const int sj = 4 * (dlo >> 2) + j, bj = 4 * sj + kb;
-            const bool valid = sj >= dlo && sj <= s && bj < nblk;
-            const float sxj = sx[min(bj, nblk - 1)], exj = ex[min(bj, nblk - 1)];
-            const float dsc[4] = {gd_h2f((uint16_t)(sc[0] & 0xffff)),
-                                  gd_h2f((uint16_t)(sc[0] >> 16)),
-                                  gd_h2f((uint16_t)(sc[1] & 0xffff)),
-                                  gd_h2f((uint16_t)(sc[1] >> 16))};
+        // Column s % 4 holds the item: lane (s % 4, rq, kb) has rows
+        // 4*rq + v of block 4s + kb; every product entered as
+        // c * x * 2^(-16-e_b) (lo with x 2^11).
+        const int bj = min(blk, nblk - 1);
+        const float sxj = sx[bj], exj = ex[bj];
+        const float dsc[4] = {gd_h2f((uint16_t)(sc[0] & 0xffff)), gd_h2f((uint16_t)(sc[0] >> 16)),
+                              gd_h2f((uint16_t)(sc[1] & 0xffff)), gd_h2f((uint16_t)(sc[1] >> 16))};
+        f32x4 r;
 #pragma unroll
-            for (int v = 0; v < 4; v++) {
-                // Every product entered as c * x * 2^(-16-e_b) (lo with x 2^11).
-                const float cx = HL ? (acc[0][v] + acc[1][v]) + (acc[2][v] + acc[3][v]) * 0x1p-11f
-                                    : (acc[0][v] + acc[1][v]) + (acc[2][v] + acc[3][v]);
-                yp[v] += valid ? dsc[v] * (cx * exj - sxj) : 0.f;
-            }
-#pragma unroll
-            for (int c = 0; c < 4; c++) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int v = 0; v < 4; v++) {
+            const float cx = HL ? (acc[0][v] + acc[1][v]) + (acc[2][v] + acc[3][v]) * 0x1p-11f
+                                : (acc[0][v] + acc[1][v]) + (acc[2][v] + acc[3][v]);
+            float t = match ? dsc[v] * (cx * exj - sxj) : 0.f;
+            // Sum the item's four blocks (lanes kb = 0 .. 3).
+            t += __shfl_xor(t, 16, 64);
+            t += __shfl_xor(t, 32, 64);
+            r[v] = t;
         }
-        if (set_end || range_end) {
-            // Sum each row over its 16 lanes (4 columns x 4 K-blocks).  A set
-            // this wave covers whole goes to the workgroup's results; a cut
-            // one to `red` (slot 0 if it began before this wave's range).
-            const int set_first = cur.set * L;              // item index of s = s0
-            const bool whole = set_first >= a && set_first + L <= b;
-            const int slot = set_first < a ? 0 : 1;
-#pragma unroll
-            for (int v = 0; v < 4; v++) {
-                float r = yp[v];
-                r += __shfl_xor(r, 1, 64);
-                r += __shfl_xor(r, 2, 64);
-                r += __shfl_xor(r, 16, 64);
-                r += __shfl_xor(r, 32, 64);
-                const int row = 4 * rq + v;
-                if ((lane & 0x33) == 0) {
-                    if (whole) ysum[cur.set * 16 + row] = r;
-                    else red[wave][slot][row] = r;
-                }
-                yp[v] = 0.f;
-            }
-        }
-        // The ring slot is consumed: refill it with the tile P items
-        // ahead (zeros, without a memory access, past the range).
-        load(item + P, ld, tile, sc);
-        ld.next(s0, s1);
-        cur.next(s0, s1);
+        if (j == (s & 3) && kb == 0) *(f32x4 *)(part + it * 16 + 4 * rq) = r;
     };
-    // Whole blocks of P items: straight-line code, so the compiler waits
-    // only for the tile each item needs.  The last nitems % P items follow.
-    int base = 0;
-    for (; base + P <= nitems; base += P) {
+    // Items are consumed in the order they were taken and a wave's items
+    // only grow, so once slot 0 is past the last item the wave is done.  The
+    // loop has no other exit and every refill is issued (past the end: no
+    // memory access), so each item waits only for its own loads.
+    while (rit[0] < total) {
 #pragma unroll
-        for (int p = 0; p < P; p++) step(base + p, ring[p], rsc[p]);
-    }
-#pragma unroll
-    for (int p = 0; p < P - 1; p++)
-        if (base + p < nitems) step(base + p, ring[p], rsc[p]);
-    __syncthreads();
-    // Cut sets: one per range boundary strictly inside a set (the same set
-    // may hold several boundaries; the first of them sums it, in wave order).
-    if (threadIdx.x < (NW - 1) * 16) {
-        const int bi = threadIdx.x / 16 + 1, r = threadIdx.x % 16;
-        const int bnd = total * bi / NW;
-        const int j = bnd / L;
-        const int prev = total * (bi - 1) / NW;
-        const bool first_in_set = bi == 1 || prev <= j * L;
-        if (bnd % L != 0 && first_in_set) {
-            float acc = 0.f;
-            for (int w = 0; w < NW; w++) {
-                const int wa = total * w / NW, wb = total * (w + 1) / NW;
-                const bool overlap = wa < wb && wa < (j + 1) * L && wb > j * L;
-                const bool whole = wa <= j * L && wb >= (j + 1) * L;
-                if (overlap && !whole) acc += red[w][j * L < wa ? 0 : 1][r];
-            }
-            ysum[j * 16 + r] = acc;
+        for (int p = 0; p < P; p++) {
+            int g = 0;
+            if (lane == 0) g = atomicAdd(&next_item, 1);
+            if (rit[p] < total) step(rit[p], ring[p], rsc[p]);
+            rit[p] = __builtin_amdgcn_readfirstlane(g);
+            load(rit[p], ring[p], rsc[p]);
         }
     }
     __syncthreads();
+    // Rows: each summed over its steps in step order.
+    auto row_sum = [&](int c, int r) {
+        const float *pp = part + c * L * 16 + r;
+        float acc = 0.f;
+        for (int i = 0; i < L; i++) acc += pp[i * 16];
+        return acc;
+    };
     if (glu.pair_sets) {
         for (int i = threadIdx.x; i < npair * 16; i += MT)
-            glu.out[set_lo * 16 + i] = gd_f2h(gd_silu(ysum[i]) * ysum[npair * 16 + i]);
+            glu.out[set_lo * 16 + i] =
+                    gd_f2h(gd_silu(row_sum(i >> 4, i & 15)) * row_sum(npair + (i >> 4), i & 15));
         return;
     }
     for (int i = threadIdx.x; i < nset_wg * 16; i += MT) {
         const int row = set_lo * 16 + i;
-        if (row < R) y[row] = ysum[i];
+        if (row < R) y[row] = row_sum(i >> 4, i & 15);
     }
 }
 
@@ -494,9 +463,14 @@ int occupancy_wgs(size_t lds) {
     return n;
 }
 
-// Workgroups per CU for a K (the LDS footprint depends on it), looked up once.
+// Workgroups per CU the plan counts on.  The default 16-wave workgroup runs
+// one per CU: two fit (62 VGPRs), but on MI355X two per CU, each with half
+// the sets, measured 5-20% slower on every decode shape.  The smaller
+// workgroups of the tuning knobs use what fits, looked up once per K (the
+// LDS footprint depends on it).
 template <int XT, int NW, int P>
 int occupancy_memo(int nblk, size_t lds) {
+    if (NW == 16) return 1;
     static int memo[513];                                 // by nblk; 0 = unknown
     if (memo[nblk] == 0) memo[nblk] = occupancy_wgs<XT, NW, P>(lds);
     return memo[nblk];
@@ -506,15 +480,24 @@ int occupancy_memo(int nblk, size_t lds) {
 // splits of ksteps steps (split z writes y + z * R).
 struct Split { int64_t per, grid; int ksteps, nz; };
 
-Split plan(int64_t nsets, int steps, int ksplit, int64_t slots, int64_t cap) {
+// lds_free: LDS beside the x staging, which holds 16 row partials of every
+// item of the workgroup's sets (rows_per_set sets of W per set counted).
+Split plan(int64_t nsets, int steps, int ksplit, int64_t slots, size_t lds_free,
+           int rows_per_set) {
     Split sp;
     sp.ksteps = (steps + ksplit - 1) / ksplit;
     sp.nz = (steps + sp.ksteps - 1) / sp.ksteps;
+    const int64_t cap = std::max<int64_t>(
+            1, std::min<int64_t>(256, (int64_t)(lds_free / (64 * (size_t)sp.ksteps * rows_per_set))));
     // Every resident workgroup gets the same number of sets.
     sp.per = std::min(cap, (nsets * sp.nz + slots - 1) / slots);
     sp.grid = (nsets + sp.per - 1) / sp.per;
     return sp;
 }
+
+// LDS footprint used for the occupancy lookup: the x staging and one set's
+// partials (the kernel's registers, not LDS, bound the workgroups per CU).
+size_t occ_lds(size_t xlds, int steps) { return xlds + (size_t)128 * steps; }
 
 template <int XT, int NW, int P>
 int launch(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, size_t xlds, const NormIn &nin,
@@ -525,15 +508,12 @@ int launch(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, size_t xlds, c
     // SwiGLU: split over gate sets, each bringing its up set along.
     const int64_t nsets = glu.pair_sets ? glu.pair_sets : (R + 15) / 16;
     const int rows_per_set = glu.pair_sets ? 2 : 1;
-    // Row results of up to `cap` sets fit beside x in LDS.  The occupancy
-    // depends on the LDS footprint, so it is looked up per K.
-    const int64_t cap = std::min<int64_t>(256, (int64_t)(LDS_BYTES - xlds) / 64);
-    const int occ = occupancy_memo<XT, NW, P>(nblk, xlds + (size_t)cap * 64);
+    const int occ = occupancy_memo<XT, NW, P>(nblk, occ_lds(xlds, steps));
     const Split sp = plan(nsets, steps, glu.pair_sets ? 1 : ksplit, (int64_t)cus * occ,
-                          cap / rows_per_set);
-    GD_REQUIRE(ctx, sp.per * steps * NW < (1LL << 31) && sp.per * steps / NW + 1 < (1LL << 20),
-               "gd_q2_0_gemv: R=%lld too large", (long long)R);
-    const size_t lds = xlds + (size_t)sp.per * rows_per_set * 64;
+                          LDS_BYTES - xlds, rows_per_set);
+    const size_t lds = xlds + (size_t)sp.per * rows_per_set * sp.ksteps * 64;
+    GD_REQUIRE(ctx, lds <= LDS_BYTES && sp.grid < (1LL << 31),
+               "gd_q2_0_gemv: K=%lld R=%lld does not fit", (long long)K, (long long)R);
     hipLaunchKernelGGL((q2_0_gemv_mfma_kernel<XT, NW, P>), dim3((unsigned)sp.grid, sp.nz),
                        dim3(64 * NW), lds, ctx->stream, (const uint8_t *)w->codes,
                        (const uint16_t *)w->scales, x, y, (int)K, (int)R, (int)nsets, (int)sp.per,
@@ -548,8 +528,7 @@ int launch_or_prepare(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, siz
     if (w) return launch<XT, NW, P>(ctx, w, x, y, xlds, nin, ksplit, glu);
     // Preparation only (x carries nblk): fill the occupancy memo.
     const int nblk = (int)(intptr_t)x;
-    const size_t cap = std::min<size_t>(256, (LDS_BYTES - xlds) / 64);
-    (void)occupancy_memo<XT, NW, P>(nblk, xlds + cap * 64);
+    (void)occupancy_memo<XT, NW, P>(nblk, occ_lds(xlds, (nblk + 3) / 4));
     return GD_OK;
 }
 
@@ -584,8 +563,8 @@ int gd_gemv_mfma(gd_ctx *ctx, const gd_q2w *w, const void *x, int x_dtype, float
     const int64_t K = w->K;
     const int XT = x_dtype == GD_F32 ? 1 : 0;
     const int nblk = (int)(K >> 7);
-    const size_t xlds = (size_t)(nblk + 5) * XB * 4 * (XT ? 2 : 1) + (size_t)nblk * 8;
-    GD_REQUIRE(ctx, xlds + 16 * 64 <= LDS_BYTES,
+    const size_t xlds = xlds_bytes(nblk, XT);
+    GD_REQUIRE(ctx, xlds + (size_t)64 * ((nblk + 3) / 4) <= LDS_BYTES,
                "gd_q2_0_gemv: K=%lld too long for LDS staging of %s x", (long long)K,
                XT ? "f32" : "f16");
     const NormIn none{nullptr, nullptr, nullptr, 0.f, 0, 0};
@@ -600,16 +579,15 @@ int gd_gemv_mfma(gd_ctx *ctx, const gd_q2w *w, const void *x, int x_dtype, float
 // splits the launch will actually make.
 int gd_gemv_ksplit(gd_ctx *ctx, int64_t K, int64_t R) {
     const int nblk = (int)(K >> 7), steps = (nblk + 3) / 4;
-    const size_t xlds = (size_t)(nblk + 5) * XB * 4 + (size_t)nblk * 8;
-    if (K % 128 || xlds + 16 * 64 > LDS_BYTES) return 1;
+    const size_t xlds = xlds_bytes(nblk, false);
+    if (K % 128 || xlds + (size_t)64 * steps > LDS_BYTES) return 1;
     const int cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
     const int64_t nsets = (R + 15) / 16;
-    const int64_t cap = std::min<int64_t>(256, (int64_t)(LDS_BYTES - xlds) / 64);
-    const int occ = occupancy_memo<0, 16, 2>(nblk, xlds + (size_t)cap * 64);
+    const int occ = occupancy_memo<0, 16, 2>(nblk, occ_lds(xlds, steps));
     int best = 1;
     double best_cost = 1e30;
     for (int z = 1; z <= 4; z++) {
-        const Split sp = plan(nsets, steps, z, (int64_t)cus * occ, cap);
+        const Split sp = plan(nsets, steps, z, (int64_t)cus * occ, LDS_BYTES - xlds, 1);
         const double cost = (double)((sp.grid * sp.nz + cus - 1) / cus) * sp.per * sp.ksteps +
                             2.0 * (sp.nz - 1);
         if (cost < best_cost - 1e-9) {
@@ -629,7 +607,7 @@ int gd_gemv_mfma_norm(gd_ctx *ctx, const gd_q2w *w, const float *h, const float 
                       int dstride, const float *normw, float eps, float *hout, float *y,
                       uint16_t *glu_out) {
     const int nblk = (int)(w->K >> 7);
-    const size_t xlds = (size_t)(nblk + 5) * XB * 4 + (size_t)nblk * 8;
+    const size_t xlds = xlds_bytes(nblk, false);
     GD_REQUIRE(ctx, (nblk + 5) * 8 <= 1024, "gd_gemv_norm: K=%lld too long (at most 15744)",
                (long long)w->K);
     GD_REQUIRE(ctx, !glu_out || w->R % 32 == 0, "gd_gemv_norm: SwiGLU needs R = 2 x 16k rows");
@@ -644,8 +622,8 @@ int gd_gemv_mfma_norm(gd_ctx *ctx, const gd_q2w *w, const float *h, const float 
 int gd_gemv_mfma_prepare(gd_ctx *ctx, int64_t K, int x_dtype) {
     const int XT = x_dtype == GD_F32 ? 1 : x_dtype == -1 ? 2 : 0;
     const int nblk = (int)(K >> 7);
-    const size_t xlds = (size_t)(nblk + 5) * XB * 4 * (XT == 1 ? 2 : 1) + (size_t)nblk * 8;
-    if (K % 128 || K > 65536 || xlds + 16 * 64 > LDS_BYTES) return GD_EINVAL;
+    const size_t xlds = xlds_bytes(nblk, XT == 1);
+    if (K % 128 || K > 65536 || xlds + (size_t)64 * ((nblk + 3) / 4) > LDS_BYTES) return GD_EINVAL;
     const void *tag = (const void *)(intptr_t)nblk;
     return XT == 1 ? launch_nw<1>(ctx, nullptr, tag, nullptr, xlds)
          : XT == 2 ? launch_nw<2>(ctx, nullptr, tag, nullptr, xlds)
