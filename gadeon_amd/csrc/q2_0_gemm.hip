@@ -59,23 +59,48 @@ __device__ __forceinline__ uint32_t xswz(int r) {
     return (uint32_t)(((r >> 1) & 7) ^ ((r & 1) << 2));
 }
 
-// MT x 32 tokens by 4 * NT * 32 weight rows per workgroup; slices
-// [z * sps, min((z+1) * sps, K/64)) of K for split z.  YT: 0 = f32, 1 = f16.
-// With nz > 1 the output is f32 partials at Y + z * T * R.
+// Direct loads from a buffer into LDS (lds_base is the same for the wave;
+// the data is in LDS once the wave's vmcnt has drained).  16 bytes: lane
+// l's bytes land at lds_base + 16 l.  2 bytes: lane l writes a dword, the
+// value zero-extended, at lds_base + 4 l (measured on gfx950).
+__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, const void *lds_base,
+                                           uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            r, (__attribute__((address_space(3))) void *)lds_base, 16, voff, soff, 0, 0);
+}
+__device__ __forceinline__ void lds_load2(__amdgpu_buffer_rsrc_t r, const void *lds_base,
+                                          uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            r, (__attribute__((address_space(3))) void *)lds_base, 2, voff, soff, 0, 0);
+}
+
+// LDS of one pipeline stage (one 128-K block): X as two 64-K planes of BT
+// rows x 128 bytes, then per wave and weight fragment the codes of 32 rows
+// (lanes 0..31: first half of the block, 32..63: second half, 16 bytes a
+// row) and the 32 row scales (one dword each, the f16 in its low half; the
+// upper 32 dwords repeat them).
+template <int MT, int NT> struct Stage {
+    static constexpr int BT = MT * 32;
+    static constexpr int XPLANE = BT * 128;
+    static constexpr int X = 0, C = 2 * XPLANE, S = C + 4 * NT * 1024;
+    static constexpr int BYTES = S + 4 * NT * 256;
+};
+
+// MT x 32 tokens by 4 * NT * 32 weight rows per workgroup; blocks (128 K)
+// [z * bps, min((z+1) * bps, K/128)) of K for split z.  X is f16.  YT: 0 =
+// f32, 1 = f16.  With nz > 1 the output is f32 partials at Y + z * T * R.
 // glu_ff > 0 (NT = 1, one split): W is [gate; up] with glu_ff rows each and
 // the output is SwiGLU, Yv[t][r] = f16(silu(gate_r . x_t) * (up_r . x_t)),
 // r < glu_ff: lanes 0..15 of a wave's fragment take gate rows g .. g+15 and
 // lanes 16..31 up rows glu_ff + g .., so one shuffle pairs them.
-template <int MT, int NT, int XT, int YT>
+template <int MT, int NT, int YT>
 __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2))) void q2_0_gemm_kernel(
         const uint8_t *__restrict__ codes, const uint16_t *__restrict__ scales,
-        const void *__restrict__ Xv, void *__restrict__ Yv, int T, int K, int R, int sps,
+        const void *__restrict__ Xv, void *__restrict__ Yv, int T, int K, int R, int bps,
         int nrt, int nz, int per, int glu_ff) {
-    constexpr int BT = MT * 32;
-    constexpr int XTILE = BT * BK * 2;                       // bytes of one X slice
-    __shared__ __attribute__((aligned(16))) uint8_t Xs[2][XTILE];
-    // Per lane and weight fragment: {codes lo, codes hi, scale, 0} of one slice.
-    __shared__ __attribute__((aligned(16))) u32x4 Cs[2][4 * NT * 64];
+    using St = Stage<MT, NT>;
+    constexpr int BT = St::BT;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * St::BYTES];
 
     // Workgroup b runs on XCD b % 8.  Units (token tile, K split, row tile)
     // are numbered token-tile-major and dealt to XCDs in contiguous runs of
@@ -84,7 +109,8 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2))) vo
     const int u = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
     if (u >= (int)((T + BT - 1) / BT) * nz * nrt) return;
     const int rt = u % nrt, z = (u / nrt) % nz, tt = u / (nrt * nz);
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int li = lane & 31, lh = lane >> 5;
     const int t0 = tt * BT;
     // This wave's first row (SwiGLU: first gate row, 16 per wave).
@@ -92,96 +118,62 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2))) vo
     const int nblk = K >> 7;
     const int csteps = (nblk + 3) >> 2;
     const int bgroups = (nblk + 15) >> 4;
-    const int s_begin = z * sps;
-    const int s_end = min(s_begin + sps, 2 * nblk);
+    const int b_begin = z * bps;
+    const int b_end = min(b_begin + bps, nblk);
 
     // Buffer resources: X from token t0, codes and scales from this wave's
     // first 16-row group.  Tokens past T and row groups past R lie beyond
     // the resource and load as zeros; their outputs are never stored.
-    constexpr uint32_t ESZ = XT ? 4 : 2;
     const __amdgpu_buffer_rsrc_t xrs =
-            gd_rsrc((const char *)Xv + (size_t)t0 * K * ESZ, (uint32_t)min(BT, T - t0) * K * ESZ);
+            gd_rsrc((const char *)Xv + (size_t)t0 * K * 2, (uint32_t)min(BT, T - t0) * K * 2);
     const int g0 = rw >> 4, rgroups = (R + 15) >> 4;
     const uint32_t gvalid = (uint32_t)max(0, min(glu_ff ? (glu_ff >> 4) + 1 : 2 * NT, rgroups - g0));
     const __amdgpu_buffer_rsrc_t crs =
             gd_rsrc(codes + ((size_t)g0 * csteps << 11), gvalid * (uint32_t)csteps * 2048u);
     const __amdgpu_buffer_rsrc_t srs =
             gd_rsrc(scales + (size_t)g0 * bgroups * 256, gvalid * (uint32_t)bgroups * 512u);
-    // This thread stages chunk (tid & 7) of X rows (tid >> 3) + 32 i.
-    const int xr0 = tid >> 3, xc = tid & 7;
-    const uint32_t xoff = (uint32_t)(xr0 * K + xc * 8) * ESZ;
-    const uint32_t xrowstep = 32u * (uint32_t)K * ESZ;
-    const uint32_t xlds = (uint32_t)xr0 * 128 + ((xc ^ xswz(xr0)) << 4);
+
+    // X loads: 1 KB chunks q = wave + 4 i of a stage (plane q / (BT/8), rows
+    // 8 (q % (BT/8)) ..); lane l fills physical chunk l%8 of row l/8, which
+    // holds logical chunk (l%8) ^ xswz(row): the swizzle is applied by
+    // choosing each lane's source.
+    constexpr int XCH = BT / 16;                          // chunks per wave
+    uint32_t xvo[XCH];
+#pragma unroll
+    for (int i = 0; i < XCH; i++) {
+        const int q = wave + 4 * i, p = q / (BT / 8), r = 8 * (q % (BT / 8)) + (lane >> 3);
+        const int c = (lane & 7) ^ (int)xswz(r);
+        xvo[i] = (uint32_t)(r * K + 64 * p + 8 * c) * 2;
+    }
+    // Code and scale loads of fragment n: row group relative to g0 (SwiGLU:
+    // lanes 16..31 of each half read the up rows), block half lh.
+    uint32_t cvo[NT], svo[NT];
+#pragma unroll
+    for (int n = 0; n < NT; n++) {
+        const int g = glu_ff ? ((li >> 4) ? (glu_ff >> 4) : 0) : 2 * n + (li >> 4);
+        cvo[n] = ((uint32_t)(g * csteps) << 11) + ((uint32_t)lh << 10) + ((li & 15) << 4);
+        svo[n] = ((uint32_t)g * bgroups * 256 + (li & 15)) * 2;
+    }
+    // Issue every load of block blk into stage st.
+    auto issue = [&](int blk, int st) {
+        uint8_t *base = lds + st * St::BYTES;
+        const uint32_t xk = (uint32_t)blk * 256;          // bytes of K before the block
+#pragma unroll
+        for (int i = 0; i < XCH; i++)
+            lds_load16(xrs, base + St::X + (wave + 4 * i) * 1024, xvo[i], xk);
+        const uint32_t cs = ((uint32_t)(blk >> 2) << 11) + ((uint32_t)(blk & 3) << 8);
+        const uint32_t ss = ((uint32_t)(blk >> 4) * 256 + (blk & 15) * 16) * 2;
+#pragma unroll
+        for (int n = 0; n < NT; n++) {
+            lds_load16(crs, base + St::C + (wave * NT + n) * 1024, cvo[n], cs);
+            lds_load2(srs, base + St::S + (wave * NT + n) * 256, svo[n], ss);
+        }
+    };
+
     // A-fragment reads: row m*32 + li, chunk 4*lh + ks.
     uint32_t alds[4];
 #pragma unroll
     for (int ks = 0; ks < 4; ks++) alds[ks] = (uint32_t)li * 128 + (((4 * lh + ks) ^ xswz(li)) << 4);
-    uint32_t coff[NT], soff[NT];
-#pragma unroll
-    for (int n = 0; n < NT; n++) {
-        // Row group relative to g0 (SwiGLU: lanes 16..31 read the up rows).
-        const int g = glu_ff ? ((li >> 4) ? (glu_ff >> 4) : 0) : 2 * n + (li >> 4);
-        coff[n] = ((uint32_t)(g * csteps) << 11) + ((li & 15) << 4) + 8 * lh;
-        soff[n] = ((uint32_t)g * bgroups * 256 + (li & 15)) * 2;
-    }
-
-    // X of slice s+1 is loaded into registers while slice s multiplies and
-    // is stored to LDS after it; codes and scales run one slice further
-    // ahead (they come from HBM), passing through LDS beside X.  The loop is
-    // unrolled by two over static buffers and register sets, so no register
-    // is ever copied (a copy would wait for its load).  Loads past the last
-    // slice re-read the last slice: they stay unconditional, which keeps the
-    // compiler's waits exact.
-    u32x4 xr[MT];                    // f16 X: MT chunks of 8 halves
-    f32x4 xf[XT ? 2 * MT : 1];       // f32 X
-    struct Codes { u32x2 c[NT]; uint32_t d[NT]; };
-    auto load_x = [&](int s) {
-        s = min(s, s_end - 1);
-        const uint32_t k0 = (uint32_t)s * BK * ESZ;
-#pragma unroll
-        for (int i = 0; i < MT; i++) {
-            if (XT == 0) {
-                xr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, xoff, k0 + i * xrowstep, 0));
-            } else {
-                xf[2 * i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, xoff, k0 + i * xrowstep, 0));
-                xf[2 * i + 1] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, xoff + 16, k0 + i * xrowstep, 0));
-            }
-        }
-    };
-    auto load_c = [&](int s, Codes &st) {
-        s = min(s, s_end - 1);
-        const int blk = s >> 1, h = s & 1;
-        const uint32_t cs = ((uint32_t)(blk >> 2) << 11) + ((uint32_t)h << 10) + ((uint32_t)(blk & 3) << 8);
-        const uint32_t ss = ((uint32_t)(blk >> 4) * 256 + (blk & 15) * 16) * 2;
-#pragma unroll
-        for (int n = 0; n < NT; n++) {
-            st.c[n] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(crs, coff[n], cs, 0));
-            st.d[n] = __builtin_amdgcn_raw_buffer_load_b16(srs, soff[n], ss, 0);
-        }
-    };
-    auto store_x = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < MT; i++) {
-            u32x4 v;
-            if (XT == 0) {
-                v = xr[i];
-            } else {
-                f16x8 hv;
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    hv[e] = (f16)xf[2 * i][e];
-                    hv[4 + e] = (f16)xf[2 * i + 1][e];
-                }
-                v = __builtin_bit_cast(u32x4, hv);
-            }
-            *(u32x4 *)&Xs[buf][xlds + i * 4096] = v;
-        }
-    };
-    auto store_c = [&](int buf, const Codes &st) {
-#pragma unroll
-        for (int n = 0; n < NT; n++)
-            Cs[buf][(wave * NT + n) * 64 + lane] = u32x4{st.c[n][0], st.c[n][1], st.d[n], 0u};
-    };
 
     f32x16 acc[MT][NT];
 #pragma unroll
@@ -191,67 +183,63 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2))) vo
 #pragma unroll
             for (int v = 0; v < 16; v++) acc[m][n][v] = 0.f;
 
-    // One slice: 4 K-steps of 16.  The A fragments and the dequantized B
-    // fragments of step ks+1 are fetched and built while step ks's MFMAs
-    // run, so no MFMA waits on an LDS read it has just issued.
-    auto compute = [&](int buf) {
-        u32x2 cw[NT];
+    // One block from stage st: two 64-K halves of 4 K-steps of 16.  The A
+    // fragments and the dequantized B fragments of step ks+1 are fetched and
+    // built while step ks's MFMAs run, so no MFMA waits on an LDS read it has
+    // just issued.
+    auto compute = [&](int st) {
+        const uint8_t *base = lds + st * St::BYTES;
         f16x2 d2[NT];
 #pragma unroll
         for (int n = 0; n < NT; n++) {
-            const u32x4 rec = Cs[buf][(wave * NT + n) * 64 + lane];
-            cw[n] = u32x2{rec[0], rec[1]};
-            const f16 d = __builtin_bit_cast(f16, (uint16_t)rec[2]);
+            const f16 d = *(const f16 *)(base + St::S + (wave * NT + n) * 256 + 4 * li);
             d2[n] = f16x2{d, d};
         }
-        f16x8 a[2][MT], b[2][NT];
 #pragma unroll
-        for (int m = 0; m < MT; m++) a[0][m] = *(const f16x8 *)&Xs[buf][alds[0] + m * 4096];
+        for (int h = 0; h < 2; h++) {
+            const uint8_t *xb = base + St::X + h * St::XPLANE;
+            u32x2 cw[NT];
 #pragma unroll
-        for (int n = 0; n < NT; n++) b[0][n] = dequant8(cw[n][0] & 0xffffu, d2[n]);
+            for (int n = 0; n < NT; n++)
+                cw[n] = *(const u32x2 *)(base + St::C + (wave * NT + n) * 1024 + (h * 32 + li) * 16 + 8 * lh);
+            f16x8 a[2][MT], b[2][NT];
 #pragma unroll
-        for (int ks = 0; ks < 4; ks++) {
-            const int cur = ks & 1, nxt = cur ^ 1;
-            if (ks < 3) {
+            for (int m = 0; m < MT; m++) a[0][m] = *(const f16x8 *)(xb + alds[0] + m * 4096);
+#pragma unroll
+            for (int n = 0; n < NT; n++) b[0][n] = dequant8(cw[n][0] & 0xffffu, d2[n]);
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++) {
+                const int cur = ks & 1, nxt = cur ^ 1;
+                if (ks < 3) {
+#pragma unroll
+                    for (int m = 0; m < MT; m++)
+                        a[nxt][m] = *(const f16x8 *)(xb + alds[ks + 1] + m * 4096);
+#pragma unroll
+                    for (int n = 0; n < NT; n++)
+                        b[nxt][n] = dequant8((cw[n][(ks + 1) >> 1] >> (16 * ((ks + 1) & 1))) & 0xffffu, d2[n]);
+                }
 #pragma unroll
                 for (int m = 0; m < MT; m++)
-                    a[nxt][m] = *(const f16x8 *)&Xs[buf][alds[ks + 1] + m * 4096];
 #pragma unroll
-                for (int n = 0; n < NT; n++)
-                    b[nxt][n] = dequant8((cw[n][(ks + 1) >> 1] >> (16 * ((ks + 1) & 1))) & 0xffffu, d2[n]);
+                    for (int n = 0; n < NT; n++)
+                        acc[m][n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[cur][m], b[cur][n], acc[m][n], 0, 0, 0);
             }
-#pragma unroll
-            for (int m = 0; m < MT; m++)
-#pragma unroll
-                for (int n = 0; n < NT; n++)
-                    acc[m][n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[cur][m], b[cur][n], acc[m][n], 0, 0, 0);
         }
     };
 
-    Codes CA, CB;
-    load_x(s_begin);
-    load_c(s_begin, CA);
-    store_x(0);
-    store_c(0, CA);
-    load_c(s_begin + 1, CB);
-    __syncthreads();
-    // Even step: LDS buffer 0 holds slice s, CB holds codes of s+1.  Odd
-    // step: buffer 1 holds s+1, CA holds codes of s+2.  Every split holds an
-    // even number of slices (the host guarantees it), so the loop runs whole
-    // pairs and the accumulators never change registers.
-    for (int s = s_begin; s < s_end; s += 2) {
-        load_x(s + 1);
-        load_c(s + 2, CA);
-        compute(0);
-        store_x(1);
-        store_c(1, CB);
+    // Two stages: the loads of block b+1 go out right after the barrier that
+    // opens block b (every wave is then done with block b-1, whose stage
+    // they overwrite), so they have a whole block of MFMAs to land.  The
+    // wait before the barrier covers only this thread's own direct loads;
+    // the barrier makes every thread's visible.
+    issue(b_begin, 0);
+    int st = 0;
+    for (int blk = b_begin; blk < b_end; blk++) {
+        __builtin_amdgcn_s_waitcnt(0x0F70);               // vmcnt(0); lgkm and exp not waited
         __syncthreads();
-        load_x(s + 2);
-        load_c(s + 3, CB);
-        compute(1);
-        store_x(0);
-        store_c(0, CA);
-        __syncthreads();
+        if (blk + 1 < b_end) issue(blk + 1, st ^ 1);
+        compute(st);
+        st ^= 1;
     }
 
     // D layout of the 32x32 MFMA: lane holds column li (weight row) and rows
@@ -316,21 +304,28 @@ typedef void (*gemm_fn)(const uint8_t *, const uint16_t *, const void *, void *,
                         int, int, int, int, int);
 
 template <int MT, int NT>
-gemm_fn pick(int x_dtype, int yt) {
-    if (x_dtype == GD_F16) return yt ? q2_0_gemm_kernel<MT, NT, 0, 1> : q2_0_gemm_kernel<MT, NT, 0, 0>;
-    // f32 X stages twice the bytes: only the smaller tiles fit two waves
-    // per SIMD without spilling.
-    if constexpr (MT * NT <= 4)
-        return yt ? q2_0_gemm_kernel<MT, NT, 1, 1> : q2_0_gemm_kernel<MT, NT, 1, 0>;
+gemm_fn pick(int yt) {
+    return yt ? q2_0_gemm_kernel<MT, NT, 1> : q2_0_gemm_kernel<MT, NT, 0>;
+}
+
+// The kernel for a tile (f32 X is converted to f16 first, see gemm_run).
+gemm_fn kernel_for(int mt, int nt, int yt) {
+    if (mt == 8 && nt == 1) return pick<8, 1>(yt);
+    if (mt == 4 && nt == 2) return pick<4, 2>(yt);
+    if (mt == 4 && nt == 1) return pick<4, 1>(yt);
+    if (mt == 2 && nt == 2) return pick<2, 2>(yt);
     return nullptr;
 }
 
-gemm_fn kernel_for(int mt, int nt, int x_dtype, int yt) {
-    if (mt == 8 && nt == 1) return pick<8, 1>(x_dtype, yt);
-    if (mt == 4 && nt == 2) return pick<4, 2>(x_dtype, yt);
-    if (mt == 4 && nt == 1) return pick<4, 1>(x_dtype, yt);
-    if (mt == 2 && nt == 2) return pick<2, 2>(x_dtype, yt);
-    return nullptr;
+// X16[i] = f16(X[i]) (round to nearest even), 4 per thread.
+__global__ __launch_bounds__(256) void gemm_x_to_f16(const float *__restrict__ X,
+                                                     uint16_t *__restrict__ X16, size_t n) {
+    const size_t i = ((size_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (i >= n) return;
+    const f32x4 v = *(const f32x4 *)(X + i);
+    const uint32_t lo = (uint32_t)gd_f2h(v[0]) | ((uint32_t)gd_f2h(v[1]) << 16);
+    const uint32_t hi = (uint32_t)gd_f2h(v[2]) | ((uint32_t)gd_f2h(v[3]) << 16);
+    *(u32x2 *)(X16 + i) = u32x2{lo, hi};
 }
 
 }  // namespace
@@ -350,15 +345,16 @@ int gd_check_q2w(gd_ctx *ctx, const gd_q2w *w, const char *who);
 // GADEON_GEMM_CFG="MT,NT,S" forces a plan.
 gd_gemm_plan gd_gemm_choose(gd_ctx *ctx, int64_t T, int64_t K, int64_t R, int x_dtype) {
     static const char *force = getenv("GADEON_GEMM_CFG");
-    const int nslices = (int)(K / BK);
+    (void)x_dtype;
+    const int nblk = (int)(K / 128);
     auto nz_of = [&](int s) {
-        const int sps = 2 * ((nslices / 2 + s - 1) / s);
-        return (nslices + sps - 1) / sps;
+        const int bps = (nblk + s - 1) / s;
+        return (nblk + bps - 1) / bps;
     };
     if (force) {
         int mt = 4, nt = 2, s = 1;
-        if (sscanf(force, "%d,%d,%d", &mt, &nt, &s) == 3 && kernel_for(mt, nt, x_dtype, 0) &&
-            s >= 1 && s <= 16)
+        if (sscanf(force, "%d,%d,%d", &mt, &nt, &s) == 3 && kernel_for(mt, nt, 0) && s >= 1 &&
+            s <= 16)
             return gd_gemm_plan{mt, nt, nz_of(s)};
     }
     const int cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
@@ -369,12 +365,12 @@ gd_gemm_plan gd_gemm_choose(gd_ctx *ctx, int64_t T, int64_t K, int64_t R, int x_
     gd_gemm_plan best{4, 1, 1};
     double best_cost = 1e30;
     for (const Shape &sh : shapes) {
-        if (!kernel_for(sh.mt, sh.nt, x_dtype, 0)) continue;
+        if (!kernel_for(sh.mt, sh.nt, 0)) continue;
         const int64_t tiles = ((T + sh.mt * 32 - 1) / (sh.mt * 32)) *
                               ((R + 4 * sh.nt * 32 - 1) / (4 * sh.nt * 32));
         for (int s = 1; s <= 8; s++) {
-            const int sps = 2 * ((nslices / 2 + s - 1) / s);
-            if (s > 1 && (int64_t)(s - 1) * sps >= nslices) break;
+            const int sps = 2 * ((nblk + s - 1) / s);     // slices (64 K) per split
+            if (s > 1 && (int64_t)(s - 1) * sps >= 2 * nblk) break;
             const int64_t per = (tiles * s + cus - 1) / cus;
             double cost = (double)per * (sps + 2) * sh.us_per_slice * (per == 1 ? sh.lone : 1.0);
             if (s > 1) cost += (2.0 * s + 1) * (double)T * R * 4 / 7e6;
@@ -387,22 +383,22 @@ gd_gemm_plan gd_gemm_choose(gd_ctx *ctx, int64_t T, int64_t K, int64_t R, int x_
     return best;
 }
 
-// Launch one plan.  plan.split > 1 requires y_dtype f32 and Y sized
+// Launch one plan on f16 X.  plan.split > 1 requires y_dtype f32 and Y sized
 // split * T * R (partials, summed by the caller).
 int gd_gemm_launch(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, int x_dtype, void *Y,
                    int y_dtype, const gd_gemm_plan &p) {
     const int K = (int)w->K, R = (int)w->R;
-    const int nslices = K / BK;                         // even: K is whole blocks
-    const int sps = 2 * ((nslices / 2 + p.split - 1) / p.split);
-    const int nz = (nslices + sps - 1) / sps;
-    gemm_fn f = kernel_for(p.mt, p.nt, x_dtype, p.split > 1 ? 0 : (y_dtype == GD_F16));
-    GD_REQUIRE(ctx, f && (p.split == 1 || y_dtype == GD_F32) && nz == p.split,
+    const int nblk = K / 128;
+    const int bps = (nblk + p.split - 1) / p.split;     // blocks (128 K) per split
+    const int nz = (nblk + bps - 1) / bps;
+    gemm_fn f = kernel_for(p.mt, p.nt, p.split > 1 ? 0 : (y_dtype == GD_F16));
+    GD_REQUIRE(ctx, f && x_dtype == GD_F16 && (p.split == 1 || y_dtype == GD_F32) && nz == p.split,
                "gd_q2_0_gemm: bad plan %d,%d,%d", p.mt, p.nt, p.split);
     const int nrt = gd_blocks(R, 4 * p.nt * 32);
     const int64_t units = (int64_t)gd_blocks(T, p.mt * 32) * nz * nrt;
     const int per = (int)((units + 7) / 8);
     hipLaunchKernelGGL(f, dim3(8 * per), dim3(THREADS), 0, ctx->stream, (const uint8_t *)w->codes,
-                       (const uint16_t *)w->scales, X, Y, (int)T, K, R, sps, nrt, nz, per, 0);
+                       (const uint16_t *)w->scales, X, Y, (int)T, K, R, bps, nrt, nz, per, 0);
     GD_LAUNCHED(ctx, "q2_0_gemm");
     return GD_OK;
 }
@@ -414,13 +410,12 @@ int gd_gemm_glu(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, uint16_t
     const int K = (int)w->K, R = (int)w->R, ff = R / 2;
     GD_REQUIRE(ctx, R % 32 == 0 && T > 0 && K % 128 == 0, "gd_gemm_glu: R=%d must hold two "
                "halves of 16-row groups", R);
-    const int nslices = K / BK;
-    gemm_fn f = kernel_for(4, 1, GD_F16, 0);
+    gemm_fn f = kernel_for(4, 1, 0);
     const int nrt = gd_blocks(ff, 64);
     const int64_t units = (int64_t)gd_blocks(T, 128) * nrt;
     const int per = (int)((units + 7) / 8);
     hipLaunchKernelGGL(f, dim3(8 * per), dim3(THREADS), 0, ctx->stream, (const uint8_t *)w->codes,
-                       (const uint16_t *)w->scales, X, (void *)out, (int)T, K, R, nslices, nrt, 1,
+                       (const uint16_t *)w->scales, X, (void *)out, (int)T, K, R, K / 128, nrt, 1,
                        per, ff);
     GD_LAUNCHED(ctx, "q2_0_gemm_glu");
     return GD_OK;
@@ -447,25 +442,39 @@ int gemm_run(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, int x_dtype
                "gd_q2_0_gemm: shape too large");
     gd_gemm_plan p;
     if (forced) {
-        GD_REQUIRE(ctx, kernel_for(forced->mt, forced->nt, x_dtype, 0) && forced->split >= 1 &&
+        GD_REQUIRE(ctx, kernel_for(forced->mt, forced->nt, 0) && forced->split >= 1 &&
                             forced->split <= 16,
                    "gd_q2_0_gemm_plan: no kernel for mt=%d nt=%d split=%d with this X dtype",
                    forced->mt, forced->nt, forced->split);
         p = *forced;
-        const int nslices = (int)(w->K / BK);
-        const int sps = 2 * ((nslices / 2 + p.split - 1) / p.split);
-        p.split = (nslices + sps - 1) / sps;           // splits that hold slices
+        const int nblk = (int)(w->K / 128);
+        const int bps = (nblk + p.split - 1) / p.split;
+        p.split = (nblk + bps - 1) / bps;               // splits that hold blocks
     } else {
         p = gd_gemm_choose(ctx, T, w->K, w->R, x_dtype);
     }
     const size_t n = (size_t)T * w->R;
     // Partials are summed 4 at a time: odd-sized outputs run unsplit.
     if (n % 4) p.split = 1;
-    if (p.split == 1) return gd_gemm_launch(ctx, w, T, X, x_dtype, Y, y_dtype, p);
-    void *part = nullptr;
-    rc = gd_ctx_workspace(ctx, n * p.split * 4, &part);
-    if (rc) return rc;
-    rc = gd_gemm_launch(ctx, w, T, X, x_dtype, part, GD_F32, p);
+    // Workspace: f16 X (f32 X is rounded to f16 once, as the reference
+    // stages it, Kernels.metal:428), then the split partials.
+    const size_t nx = (size_t)T * w->K;
+    const size_t xbytes = x_dtype == GD_F32 ? (nx * 2 + 255) / 256 * 256 : 0;
+    const size_t pbytes = p.split > 1 ? n * p.split * 4 : 0;
+    uint8_t *ws = nullptr;
+    if (xbytes + pbytes) {
+        rc = gd_ctx_workspace(ctx, xbytes + pbytes, (void **)&ws);
+        if (rc) return rc;
+    }
+    if (xbytes) {
+        hipLaunchKernelGGL(gemm_x_to_f16, dim3((unsigned)gd_blocks((int64_t)(nx / 4), 256)), dim3(256),
+                           0, ctx->stream, (const float *)X, (uint16_t *)ws, nx);
+        GD_LAUNCHED(ctx, "gemm_x_to_f16");
+        X = ws;
+    }
+    if (p.split == 1) return gd_gemm_launch(ctx, w, T, X, GD_F16, Y, y_dtype, p);
+    void *part = ws + xbytes;
+    rc = gd_gemm_launch(ctx, w, T, X, GD_F16, part, GD_F32, p);
     if (rc) return rc;
     const unsigned blocks = (unsigned)gd_blocks((int64_t)(n / 4), 256);
     if (y_dtype == GD_F32)
