@@ -243,36 +243,57 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2))) vo
     }
 
     // D layout of the 32x32 MFMA: lane holds column li (weight row) and rows
-    // 8*(v/4) + 4*lh + (v%4) (tokens) for v < 16.
+    // 8*(v/4) + 4*lh + (v%4) (tokens) for v < 16.  Stores go through a
+    // buffer resource over this token tile's output rows: a lane's base
+    // offset is computed once, each value adds a constant multiple of the
+    // row pitch, and tokens past T fall outside the resource (the store is
+    // dropped; the whole offset is in the vector operand, which the bounds
+    // check covers).
+    const int rows_t = min(BT, T - t0);
     if (glu_ff) {
-        // Lane li < 16 holds gate row rw + li, lane li + 16 the matching up row.
+        // Lane li < 16 holds gate row g = rw + li, lane li + 16 the matching
+        // up row: each half finishes eight of a fragment's sixteen tokens
+        // (the first half v < 8, the second v >= 8), trading one shuffle
+        // per pair of values.
+        const bool gl = li < 16;
+        const int g = rw + (li & 15);
+        const __amdgpu_buffer_rsrc_t ors =
+                gd_rsrc((uint16_t *)Yv + (size_t)t0 * glu_ff, (uint32_t)rows_t * glu_ff * 2u);
+        const uint32_t obase = ((uint32_t)(4 * lh + (gl ? 0 : 16)) * glu_ff + g) * 2u;
+        if (g < glu_ff) {
 #pragma unroll
-        for (int m = 0; m < MT; m++)
+            for (int m = 0; m < MT; m++)
 #pragma unroll
-            for (int v = 0; v < 16; v++) {
-                const float up = __shfl_xor(acc[m][0][v], 16, 64);
-                const int t = t0 + m * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
-                if (li < 16 && t < T && rw + li < glu_ff)
-                    ((uint16_t *)Yv)[(size_t)t * glu_ff + rw + li] =
-                            gd_f2h(gd_silu(acc[m][0][v]) * up);
-            }
+                for (int q = 0; q < 8; q++) {
+                    const float other = __shfl_xor(gl ? acc[m][0][8 + q] : acc[m][0][q], 16, 64);
+                    const float mine = gl ? acc[m][0][q] : acc[m][0][8 + q];
+                    const float gate = gl ? mine : other, up = gl ? other : mine;
+                    const float sg = gate * __builtin_amdgcn_rcpf(1.0f + __expf(-gate));
+                    const uint32_t so = (uint32_t)(m * 32 + 8 * (q >> 2) + (q & 3)) * glu_ff * 2u;
+                    __builtin_amdgcn_raw_buffer_store_b16(gd_f2h(sg * up), ors, obase + so, 0, 0);
+                }
+        }
         return;
     }
-    const size_t zoff = (size_t)z * T * R;
+    constexpr uint32_t ESZ = YT ? 2 : 4;
+    const __amdgpu_buffer_rsrc_t yrs =
+            gd_rsrc((uint8_t *)Yv + ((size_t)z * T * R + (size_t)t0 * R) * ESZ, (uint32_t)rows_t * R * ESZ);
 #pragma unroll
     for (int n = 0; n < NT; n++) {
         const int r = rw + n * 32 + li;
         if (r >= R) continue;
+        const uint32_t ybase = ((uint32_t)(4 * lh) * R + r) * ESZ;
 #pragma unroll
         for (int m = 0; m < MT; m++)
 #pragma unroll
             for (int v = 0; v < 16; v++) {
-                const int t = t0 + m * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
-                if (t < T) {
-                    const size_t i = zoff + (size_t)t * R + r;
-                    if (YT == 0) ((float *)Yv)[i] = acc[m][n][v];
-                    else ((uint16_t *)Yv)[i] = gd_f2h(acc[m][n][v]);
-                }
+                const uint32_t so = (uint32_t)(m * 32 + 8 * (v >> 2) + (v & 3)) * R * ESZ;
+                if (YT == 0)
+                    // __float_as_uint: hipcc turns a __builtin_bit_cast of a
+                    // vector element into element 0 of the vector.
+                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[m][n][v]), yrs, ybase + so, 0, 0);
+                else
+                    __builtin_amdgcn_raw_buffer_store_b16(gd_f2h(acc[m][n][v]), yrs, ybase + so, 0, 0);
                 // Store fragment by fragment: without the fence the compiler
                 // converts every accumulator up front and the extra VGPRs
                 // halve the occupancy of the whole kernel.
@@ -314,6 +335,7 @@ gemm_fn kernel_for(int mt, int nt, int yt) {
     if (mt == 4 && nt == 2) return pick<4, 2>(yt);
     if (mt == 4 && nt == 1) return pick<4, 1>(yt);
     if (mt == 2 && nt == 2) return pick<2, 2>(yt);
+    if (mt == 2 && nt == 1) return pick<2, 1>(yt);
     return nullptr;
 }
 
@@ -334,14 +356,13 @@ int gd_check_q2w(gd_ctx *ctx, const gd_q2w *w, const char *who);
 
 // Tile shape and K split for a T x K x R product, from a cost model fitted
 // to MI355X timings of every plan on the stack's six prefill shapes (its
-// picks land within 1% of the best measured plan there):
-//   * a CU completes about 3.5 TFLOP/s of this kernel once it holds two or
-//     more workgroups, whatever the tile; a lone workgroup of the smaller
-//     tiles runs slower (LONE);
-//   * workgroups are dealt evenly, so the busiest CU runs ceil(units / CUs)
-//     of them, each for its slices plus about two slices of prologue and
-//     store;
-//   * split partials cost (2s+1) f32 passes over T x R at about 7 TB/s.
+// picks land within 1.2% of the best measured plans there, in total):
+//   * a tile runs `occ` workgroups per CU (its LDS: two stages of one
+//     128-K block);
+//   * workgroups run in rounds of CUs x occ; a full round costs T_FULL per
+//     block of its split, a last round of at most one workgroup per CU
+//     T_LONE (a lone workgroup has its CU to itself);
+//   * split partials cost (2s+1) f32 passes over T x R (CS us per MB).
 // GADEON_GEMM_CFG="MT,NT,S" forces a plan.
 gd_gemm_plan gd_gemm_choose(gd_ctx *ctx, int64_t T, int64_t K, int64_t R, int x_dtype) {
     static const char *force = getenv("GADEON_GEMM_CFG");
@@ -358,25 +379,25 @@ gd_gemm_plan gd_gemm_choose(gd_ctx *ctx, int64_t T, int64_t K, int64_t R, int x_
             return gd_gemm_plan{mt, nt, nz_of(s)};
     }
     const int cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
-    struct Shape { int mt, nt; double us_per_slice, lone; };
-    // us_per_slice: one slice (64 K) of one workgroup tile at CU saturation.
-    const Shape shapes[4] = {{4, 1, 0.6, 1.33}, {2, 2, 0.7, 1.4}, {4, 2, 1.2, 1.05},
-                             {8, 1, 1.25, 1.05}};
+    struct Shape { int mt, nt, occ; double t_full, t_lone; };
+    const Shape shapes[4] = {{2, 1, 3, 1.383, 0.497}, {4, 1, 2, 1.705, 1.134},
+                             {2, 2, 3, 2.060, 1.166}, {4, 2, 1, 1.838, 1.769}};
+    constexpr double CS = 0.188;                        // us per MB of split partials
     gd_gemm_plan best{4, 1, 1};
     double best_cost = 1e30;
     for (const Shape &sh : shapes) {
-        if (!kernel_for(sh.mt, sh.nt, 0)) continue;
         const int64_t tiles = ((T + sh.mt * 32 - 1) / (sh.mt * 32)) *
                               ((R + 4 * sh.nt * 32 - 1) / (4 * sh.nt * 32));
         for (int s = 1; s <= 8; s++) {
-            const int sps = 2 * ((nblk + s - 1) / s);     // slices (64 K) per split
-            if (s > 1 && (int64_t)(s - 1) * sps >= 2 * nblk) break;
-            const int64_t per = (tiles * s + cus - 1) / cus;
-            double cost = (double)per * (sps + 2) * sh.us_per_slice * (per == 1 ? sh.lone : 1.0);
-            if (s > 1) cost += (2.0 * s + 1) * (double)T * R * 4 / 7e6;
+            const int bps = (nblk + s - 1) / s, nz = (nblk + bps - 1) / bps;
+            if (nz < s) break;                            // no more distinct splits
+            const int64_t units = tiles * nz, slots = (int64_t)cus * sh.occ;
+            const int64_t full = units / slots, rem = units % slots;
+            double cost = bps * (full * sh.t_full + (rem ? (rem <= cus ? sh.t_lone : sh.t_full) : 0.0));
+            if (nz > 1) cost += CS * (2.0 * nz + 1) * (double)T * R * 4 / 1e6;
             if (cost < best_cost) {
                 best_cost = cost;
-                best = gd_gemm_plan{sh.mt, sh.nt, s};
+                best = gd_gemm_plan{sh.mt, sh.nt, nz};
             }
         }
     }
@@ -392,7 +413,8 @@ int gd_gemm_launch(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, int x
     const int bps = (nblk + p.split - 1) / p.split;     // blocks (128 K) per split
     const int nz = (nblk + bps - 1) / bps;
     gemm_fn f = kernel_for(p.mt, p.nt, p.split > 1 ? 0 : (y_dtype == GD_F16));
-    GD_REQUIRE(ctx, f && x_dtype == GD_F16 && (p.split == 1 || y_dtype == GD_F32) && nz == p.split,
+    GD_REQUIRE(ctx, f && x_dtype == GD_F16 && (p.split == 1 || y_dtype == GD_F32) && nz == p.split &&
+                        R < (1 << 22),
                "gd_q2_0_gemm: bad plan %d,%d,%d", p.mt, p.nt, p.split);
     const int nrt = gd_blocks(R, 4 * p.nt * 32);
     const int64_t units = (int64_t)gd_blocks(T, p.mt * 32) * nz * nrt;
@@ -408,8 +430,8 @@ int gd_gemm_launch(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, int x
 // (and their 64 up rows), K unsplit.
 int gd_gemm_glu(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, uint16_t *out) {
     const int K = (int)w->K, R = (int)w->R, ff = R / 2;
-    GD_REQUIRE(ctx, R % 32 == 0 && T > 0 && K % 128 == 0, "gd_gemm_glu: R=%d must hold two "
-               "halves of 16-row groups", R);
+    GD_REQUIRE(ctx, R % 32 == 0 && T > 0 && K % 128 == 0 && R < (1 << 22), "gd_gemm_glu: R=%d "
+               "must hold two halves of 16-row groups (and be below 4194304)", R);
     gemm_fn f = kernel_for(4, 1, 0);
     const int nrt = gd_blocks(ff, 64);
     const int64_t units = (int64_t)gd_blocks(T, 128) * nrt;
@@ -436,10 +458,10 @@ int gemm_run(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, int x_dtype
                         (y_dtype == GD_F32 || y_dtype == GD_F16),
                "gd_q2_0_gemm: bad dtypes x=%d y=%d", x_dtype, y_dtype);
     GD_REQUIRE(ctx, ((uintptr_t)X & 15) == 0, "gd_q2_0_gemm: X must be 16-byte aligned");
-    // Buffer offsets are 32-bit: a 256-token X tile and a wave's code rows
-    // must stay below 4 GiB.
-    GD_REQUIRE(ctx, w->K <= (1 << 22) && w->R < (1LL << 31) && (size_t)T * w->R < (1ULL << 62),
-               "gd_q2_0_gemm: shape too large");
+    // Buffer offsets are 32-bit: a 256-token tile of X or of the output and
+    // a wave's code rows must stay below 4 GiB.
+    GD_REQUIRE(ctx, w->K <= (1 << 22) && w->R < (1LL << 22) && (size_t)T * w->R < (1ULL << 62),
+               "gd_q2_0_gemm: shape too large (K and R at most 4194304)");
     gd_gemm_plan p;
     if (forced) {
         GD_REQUIRE(ctx, kernel_for(forced->mt, forced->nt, 0) && forced->split >= 1 &&
@@ -511,7 +533,7 @@ extern "C" int gd_q2_0_gemm_swiglu(gd_ctx *ctx, const gd_q2w *w, int64_t T, cons
     GD_REQUIRE(ctx, ((uintptr_t)X & 15) == 0, "gd_q2_0_gemm_swiglu: X must be 16-byte aligned");
     GD_REQUIRE(ctx, w->R % 32 == 0, "gd_q2_0_gemm_swiglu: R=%lld is not 2 ff with ff a multiple "
                "of 16", (long long)w->R);
-    GD_REQUIRE(ctx, w->K <= (1 << 22) && w->R < (1LL << 31) && (size_t)T * w->R < (1ULL << 62),
-               "gd_q2_0_gemm_swiglu: shape too large");
+    GD_REQUIRE(ctx, w->K <= (1 << 22) && w->R < (1LL << 22) && (size_t)T * w->R < (1ULL << 62),
+               "gd_q2_0_gemm_swiglu: shape too large (K and R at most 4194304)");
     return gd_gemm_glu(ctx, w, T, X, out);
 }
