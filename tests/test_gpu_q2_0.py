@@ -244,15 +244,17 @@ def test_gemm_vs_oracle(ctx, T, K, R, xt, yt):
     free_w(ctx, w)
 
 
-PLANS_F16 = [(4, 1), (2, 2), (4, 2), (8, 1)]
+# (mt, nt, waves per workgroup): every kernel the planner can pick.
+PLANS_F16 = [(2, 1, 4), (4, 1, 4), (2, 2, 4), (4, 2, 4), (8, 1, 4),
+             (2, 1, 8), (4, 1, 8), (2, 2, 8), (4, 2, 8)]
 PLANS_F32 = PLANS_F16                   # f32 X is rounded to f16 once, then any tile
 
 
-@pytest.mark.parametrize("xt,yt,mt,nt", [(ga.F16, yt, mt, nt) for mt, nt in PLANS_F16
-                                         for yt in (ga.F32, ga.F16)] +
-                         [(ga.F32, ga.F32, mt, nt) for mt, nt in PLANS_F32])
+@pytest.mark.parametrize("xt,yt,mt,nt,nw", [(ga.F16, yt, mt, nt, nw) for mt, nt, nw in PLANS_F16
+                                            for yt in (ga.F32, ga.F16)] +
+                         [(ga.F32, ga.F32, mt, nt, nw) for mt, nt, nw in PLANS_F32])
 @pytest.mark.parametrize("split", [1, 3])
-def test_gemm_every_plan(ctx, xt, yt, mt, nt, split):
+def test_gemm_every_plan(ctx, xt, yt, mt, nt, nw, split):
     """Every tile shape and a K split against the oracle, on a ragged shape:
     T and R are not multiples of any tile and K/64 = 42 slices do not divide
     evenly into 3 splits of an even slice count."""
@@ -263,7 +265,7 @@ def test_gemm_every_plan(ctx, xt, yt, mt, nt, split):
     X = Xh.view(np.uint16) if xt == ga.F16 else Xh.astype(np.float32)
     dX = ctx.put(X)
     dY = ctx.alloc(T * R * (4 if yt == ga.F32 else 2))
-    ctx.gd_q2_0_gemm_plan(C.byref(w), T, dX, xt, dY, yt, mt, nt, split)
+    ctx.gd_q2_0_gemm_plan(C.byref(w), T, dX, xt, dY, yt, mt, nt, split, nw)
     Y = ctx.get(dY, (T, R), np.float32 if yt == ga.F32 else np.float16).astype(np.float32)
     want = np.stack([O.q2_0_matvec(blocks, K, R, Xh[t].astype(np.float32), threads=8)
                      for t in range(T)])
@@ -333,9 +335,10 @@ def test_gemm_plan_rejects_unknown_tile(ctx):
     dY = ctx.alloc(4 * 64 * 4)
     for xt in (ga.F16, ga.F32):
         with pytest.raises(RuntimeError, match="no kernel"):
-            ctx.gd_q2_0_gemm_plan(C.byref(w), 4, dX, xt, dY, ga.F32, 3, 1, 1)
-    with pytest.raises(RuntimeError, match="no kernel"):
-        ctx.gd_q2_0_gemm_plan(C.byref(w), 4, dX, ga.F16, dY, ga.F32, 4, 2, 0)
+            ctx.gd_q2_0_gemm_plan(C.byref(w), 4, dX, xt, dY, ga.F32, 3, 1, 1, 4)
+    for mt, nt, split, nw in ((4, 2, 0, 4), (8, 1, 1, 8), (4, 1, 1, 6)):
+        with pytest.raises(RuntimeError, match="no kernel"):
+            ctx.gd_q2_0_gemm_plan(C.byref(w), 4, dX, ga.F16, dY, ga.F32, mt, nt, split, nw)
     ctx.free(dX)
     ctx.free(dY)
     ctx.gd_q2w_free(C.byref(w))
