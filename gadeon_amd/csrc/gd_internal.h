@@ -32,8 +32,6 @@ int gd_hip_fail(gd_ctx *ctx, hipError_t e, const char *what);
 // Matrix-core GEMV (checked by the caller); ksplit > 1 writes K-split partial
 // rows to y + z * R.
 int gd_gemv_mfma(gd_ctx *ctx, const gd_q2w *w, const void *x, int x_dtype, float *y, int ksplit);
-// Host-side set-up of the GEMV for reduction length K (before graph capture).
-int gd_gemv_mfma_prepare(gd_ctx *ctx, int64_t K, int x_dtype);
 // GEMV of x = f16(rmsnorm(h + sum of nd delta partials) * normw); hout <- the
 // sum if not null.
 // glu_out (if not null): w = [gate; up] and glu_out = f16(silu(gate x) * up x)

@@ -119,9 +119,16 @@ struct NormIn {
     int dstride;             // floats between partials
 };
 
+// Waves per workgroup (all share one staged copy of x) and tiles in flight
+// per wave.  Measured on the decode shapes: 16 waves and 2 tiles beat 4 or 8
+// waves and 3 or 4 tiles everywhere.
+constexpr int NW = 16, P = 2;
+
 // XT: 0 = f16 x, 1 = f32 x (hi + lo split), 2 = normalized residual (see
-// XChunk).  NW waves per workgroup.
-template <int XT, int NW, int P>
+// XChunk).  KBP: item partials kept per Q2 block (4 per row) in LDS, summed
+// with the rest of the row at the end; otherwise summed across the block
+// lanes first (needs 4x less LDS, for very long K).
+template <int XT, bool KBP>
 __global__ __launch_bounds__(64 * NW) void q2_0_gemv_mfma_kernel(
         const uint8_t *__restrict__ codes, const uint16_t *__restrict__ scales,
         const void *__restrict__ xv, float *__restrict__ y, int K, int R, int nsets,
@@ -135,7 +142,7 @@ __global__ __launch_bounds__(64 * NW) void q2_0_gemv_mfma_kernel(
     const int nblk = K >> 7;
     // LDS: x planes, block b at dword XB*b (64 pair dwords + 4 of padding, so
     // the blocks one load instruction reads start on different banks), then
-    // two zero blocks four blocks apart (see zero_blk below); per-block sum
+    // zero blocks for the blocks of a short last step past K; per-block sum
     // and exponent of x (nblk rounded up to even, so that what follows is
     // 16-byte aligned); the row partials of every item.
     const int xstride = (nblk + 5) * XB;                   // dwords per x plane
@@ -143,7 +150,7 @@ __global__ __launch_bounds__(64 * NW) void q2_0_gemv_mfma_kernel(
     uint32_t *xq = lds + xstride;                          // lo plane (f32 x only)
     float *sx = (float *)(lds + (HL ? 2 : 1) * xstride);   // [nblk] block sums of x
     float *ex = sx + ((nblk + 1) & ~1);                    // [nblk] 2^(16+e_b)
-    float *part = ex + ((nblk + 1) & ~1);                  // [items][16] row partials
+    float *part = ex + ((nblk + 1) & ~1);                  // [items][4 blocks if KBP][16 rows]
     __shared__ __align__(16) int next_item;                // next item to take
 
     const int lane = threadIdx.x & 63;
@@ -168,6 +175,10 @@ __global__ __launch_bounds__(64 * NW) void q2_0_gemv_mfma_kernel(
     const int nset_wg = glu.pair_sets ? 2 * npair : npair;
     const int wsets = glu.pair_sets ? glu.pair_sets + npair : npair;   // sets spanned in W
     const int total = nset_wg * L;                         // items of the workgroup
+    // Item i is set i / L, step s0 + i % L: the quotient by multiply-high
+    // (exact for i < 2^16 and L <= 128, which the host guarantees).
+    const uint32_t Lmag = L == 1 ? 0u : (uint32_t)((0x100000000ull + L - 1) / L);
+    auto set_of = [&](int it) { return L == 1 ? it : (int)__umulhi((uint32_t)it, Lmag); };
 
     // Staging entry e = (block e/8, chunk e%8): its x loads are issued before
     // the tile prefetch, so waiting for them leaves the tiles in flight.
@@ -217,23 +228,23 @@ __global__ __launch_bounds__(64 * NW) void q2_0_gemv_mfma_kernel(
             make_rsrc(codes + (size_t)set_lo * steps * 2048, (uint32_t)wsets * steps * 2048u);
     const __amdgpu_buffer_rsrc_t srs =
             make_rsrc(scales + (size_t)set_lo * bgroups * 256, (uint32_t)wsets * bgroups * 512u);
-    // Loads of item `it`: its tile, and for the lanes of column s % 4 the
-    // scales of rows 4*rq .. 4*rq+3 of their block 4*s + kb (the other
-    // lanes load nothing).
+    // Loads of item `it`: its tile, and for the lanes of column 0 the scales
+    // of rows 4*rq .. 4*rq+3 of their block 4*s + kb (the other lanes load
+    // nothing).
     // The address arithmetic has no branch (the compiler's wait counting is
     // exact only over straight-line loads): an item past the last gets the
     // offset 0xfffff000, beyond every resource.
     const int up_shift = glu.pair_sets ? glu.pair_sets - npair : 0;
     auto pick = [](uint32_t off, uint32_t dead) { return (off & ~dead) | (dead & 0xfffff000u); };
     auto load = [&](int it, u32x4 (&cw)[2], u32x2 &sc) {
-        const int c = it / L, s = s0 + (it - c * L);
+        const int c = set_of(it), s = s0 + (it - c * L);
         const int ps = c + (c >= npair ? up_shift : 0);
         const uint32_t dead = (uint32_t)((total - 1 - it) >> 31);      // all ones past the end
         const uint32_t off = pick((uint32_t)(ps * steps + s) * 2048u + lane * 16, dead);
         cw[0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(trs, off, 0, CP_NT));
         cw[1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(trs, off + 1024, 0, CP_NT));
         const uint32_t si = (uint32_t)((ps * bgroups + (s >> 2)) * 16 + 4 * (s & 3) + kb) * 32 + 8 * rq;
-        const uint32_t other = (uint32_t)-(int)(j != (s & 3));
+        const uint32_t other = (uint32_t)-(int)(j != 0);
         sc = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(srs, pick(si, dead | other), 0, 0));
     };
 
@@ -355,19 +366,18 @@ __global__ __launch_bounds__(64 * NW) void q2_0_gemv_mfma_kernel(
     __syncthreads();
 
     // One item (set c, step s): the four Q2 blocks 4s .. 4s+3 of 16 rows.
-    // Accumulator chains: f16 x uses four, f32 x two for hi and two for lo.
+    // Every lane reads x of its own block kb, so the four columns of an
+    // MFMA block hold the same products (only column 0 is used; a lane
+    // group of one kb reads one address, which the LDS broadcasts).
+    // Accumulator chains: f16 x uses two, f32 x two for hi and two for lo.
     auto step = [&](const int it, u32x4 (&tile)[2], u32x2 &sc) {
-        const int c = it / L, s = s0 + (it - c * L);
+        const int c = set_of(it), s = s0 + (it - c * L);
         // MFMA block mb = lane/4 multiplies rows 4*rq .. 4*rq+3 of Q2 block
-        // 4s + kb by four K values; column j of its B is x when j == s % 4.
+        // 4s + kb by four K values.  Blocks past the last (a short final
+        // step) read zero-staged x and give zero products.
         const int blk = 4 * s + kb;
-        const bool match = j == (s & 3) && blk < nblk;
-        // Zero block for the other lanes: of the two, the one whose LDS
-        // banks the four blocks of this step do not use.
-        const int zero_blk = ((s ^ (nblk >> 2)) & 1) ? nblk : nblk + 4;
-        const int xoff = (match ? blk : zero_blk) * XB;
-        const u32x4 *src = (const u32x4 *)(xp + xoff);
-        const u32x4 *srq = (const u32x4 *)(xq + xoff);
+        const u32x4 *src = (const u32x4 *)(xp + blk * XB);
+        const u32x4 *srq = (const u32x4 *)(xq + blk * XB);
         f32x4 acc[4];
 #pragma unroll
         for (int d = 0; d < 8; d++) {
@@ -379,29 +389,25 @@ __global__ __launch_bounds__(64 * NW) void q2_0_gemv_mfma_kernel(
                 const u32x4 bx = src[2 * d + q];
                 const f16x4 a0 = __builtin_bit_cast(f16x4, u32x2{t[4 * q], t[4 * q + 1]});
                 const f16x4 a1 = __builtin_bit_cast(f16x4, u32x2{t[4 * q + 2], t[4 * q + 3]});
-                const int c0 = HL ? q : (2 * q) & 3, c1 = HL ? q : (2 * q + 1) & 3;
                 const f32x4 z{0.f, 0.f, 0.f, 0.f};
                 // The first product of a chain starts it from zero.
-                const bool first0 = d == 0, first1 = !HL && d == 0;
-                acc[c0] = __builtin_amdgcn_mfma_f32_4x4x4f16(
-                        a0, __builtin_bit_cast(f16x4, u32x2{bx[0], bx[1]}), first0 ? z : acc[c0],
-                        0, 0, 0);
-                acc[c1] = __builtin_amdgcn_mfma_f32_4x4x4f16(
-                        a1, __builtin_bit_cast(f16x4, u32x2{bx[2], bx[3]}), first1 ? z : acc[c1],
-                        0, 0, 0);
+                const bool first = d == 0 && q == 0;
+                acc[0] = __builtin_amdgcn_mfma_f32_4x4x4f16(
+                        a0, __builtin_bit_cast(f16x4, u32x2{bx[0], bx[1]}), first ? z : acc[0], 0, 0, 0);
+                acc[1] = __builtin_amdgcn_mfma_f32_4x4x4f16(
+                        a1, __builtin_bit_cast(f16x4, u32x2{bx[2], bx[3]}), first ? z : acc[1], 0, 0, 0);
                 if (HL) {
                     const u32x4 bq = srq[2 * d + q];
-                    acc[2 + q] = __builtin_amdgcn_mfma_f32_4x4x4f16(
-                            a0, __builtin_bit_cast(f16x4, u32x2{bq[0], bq[1]}),
-                            d == 0 ? z : acc[2 + q], 0, 0, 0);
-                    acc[2 + q] = __builtin_amdgcn_mfma_f32_4x4x4f16(
-                            a1, __builtin_bit_cast(f16x4, u32x2{bq[2], bq[3]}), acc[2 + q], 0, 0, 0);
+                    acc[2] = __builtin_amdgcn_mfma_f32_4x4x4f16(
+                            a0, __builtin_bit_cast(f16x4, u32x2{bq[0], bq[1]}), first ? z : acc[2], 0, 0, 0);
+                    acc[3] = __builtin_amdgcn_mfma_f32_4x4x4f16(
+                            a1, __builtin_bit_cast(f16x4, u32x2{bq[2], bq[3]}), first ? z : acc[3], 0, 0, 0);
                 }
             }
         }
-        // Column s % 4 holds the item: lane (s % 4, rq, kb) has rows
-        // 4*rq + v of block 4s + kb; every product entered as
-        // c * x * 2^(-16-e_b) (lo with x 2^11).
+        // Lane (j, rq, kb) has rows 4*rq + v of block 4s + kb; every product
+        // entered as c * x * 2^(-16-e_b) (lo with x 2^11).
+        const bool live = blk < nblk;
         const int bj = min(blk, nblk - 1);
         const float sxj = sx[bj], exj = ex[bj];
         const float dsc[4] = {gd_h2f((uint16_t)(sc[0] & 0xffff)), gd_h2f((uint16_t)(sc[0] >> 16)),
@@ -410,14 +416,20 @@ __global__ __launch_bounds__(64 * NW) void q2_0_gemv_mfma_kernel(
 #pragma unroll
         for (int v = 0; v < 4; v++) {
             const float cx = HL ? (acc[0][v] + acc[1][v]) + (acc[2][v] + acc[3][v]) * 0x1p-11f
-                                : (acc[0][v] + acc[1][v]) + (acc[2][v] + acc[3][v]);
-            float t = match ? dsc[v] * (cx * exj - sxj) : 0.f;
-            // Sum the item's four blocks (lanes kb = 0 .. 3).
-            t += __shfl_xor(t, 16, 64);
-            t += __shfl_xor(t, 32, 64);
-            r[v] = t;
+                                : acc[0][v] + acc[1][v];
+            r[v] = live ? dsc[v] * (cx * exj - sxj) : 0.f;
         }
-        if (j == (s & 3) && kb == 0) *(f32x4 *)(part + it * 16 + 4 * rq) = r;
+        if constexpr (KBP) {
+            if (j == 0) *(f32x4 *)(part + (it * 4 + kb) * 16 + 4 * rq) = r;
+        } else {
+            // Sum the item's four blocks (lanes kb = 0 .. 3).
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                r[v] += __shfl_xor(r[v], 16, 64);
+                r[v] += __shfl_xor(r[v], 32, 64);
+            }
+            if (j == 0 && kb == 0) *(f32x4 *)(part + it * 16 + 4 * rq) = r;
+        }
     };
     // Items are consumed in the order they were taken and a wave's items
     // only grow, so once slot 0 is past the last item the wave is done.  The
@@ -434,123 +446,91 @@ __global__ __launch_bounds__(64 * NW) void q2_0_gemv_mfma_kernel(
         }
     }
     __syncthreads();
-    // Rows: each summed over its steps in step order.
-    auto row_sum = [&](int c, int r) {
-        const float *pp = part + c * L * 16 + r;
+    // Rows: four adjacent threads per row, thread q summing its share of
+    // the row's partials (KBP: block q of every step; else steps q, q+4,
+    // ...), then the four added in lane order: the same order every time.
+    constexpr int PI = KBP ? 4 : 1;                      // partials per item and row
+    auto quarter = [&](int c, int r, int q) {
+        const float *pp = part + c * L * PI * 16 + r;
         float acc = 0.f;
-        for (int i = 0; i < L; i++) acc += pp[i * 16];
+        if constexpr (KBP)
+            for (int i = 0; i < L; i++) acc += pp[(i * 4 + q) * 16];
+        else
+            for (int i = q; i < L; i += 4) acc += pp[i * 16];
         return acc;
     };
-    if (glu.pair_sets) {
-        for (int i = threadIdx.x; i < npair * 16; i += MT)
-            glu.out[set_lo * 16 + i] =
-                    gd_f2h(gd_silu(row_sum(i >> 4, i & 15)) * row_sum(npair + (i >> 4), i & 15));
-        return;
+    // Quad lanes by DPP quad_perm (1,0,3,2) then (2,3,0,1): each lane adds
+    // its neighbour's value, so the four hold the same sum.
+    auto combine = [](float a) {
+        a += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(a), 0xB1, 0xF, 0xF, false));
+        return a + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(a), 0x4E, 0xF, 0xF, false));
+    };
+    const int nrow = (glu.pair_sets ? npair : nset_wg) * 16;
+    for (int base = 0; base < nrow * 4; base += MT) {   // uniform trip count: shuffles stay whole
+        const int i = (base + threadIdx.x) >> 2, q = threadIdx.x & 3;
+        const bool ok = i < nrow;
+        const int c = ok ? i >> 4 : 0, r = i & 15;
+        if (glu.pair_sets) {
+            const float g = combine(ok ? quarter(c, r, q) : 0.f);
+            const float u = combine(ok ? quarter(npair + c, r, q) : 0.f);
+            if (ok && q == 0) glu.out[set_lo * 16 + i] = gd_f2h(gd_silu(g) * u);
+        } else {
+            const float v = combine(ok ? quarter(c, r, q) : 0.f);
+            if (ok && q == 0 && set_lo * 16 + i < R) y[set_lo * 16 + i] = v;
+        }
     }
-    for (int i = threadIdx.x; i < nset_wg * 16; i += MT) {
-        const int row = set_lo * 16 + i;
-        if (row < R) y[row] = row_sum(i >> 4, i & 15);
-    }
-}
-
-template <int XT, int NW, int P>
-int occupancy_wgs(size_t lds) {
-    int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, q2_0_gemv_mfma_kernel<XT, NW, P>, 64 * NW,
-                                                     lds) != hipSuccess ||
-        n < 1)
-        n = 1;
-    return n;
-}
-
-// Workgroups per CU the plan counts on.  The default 16-wave workgroup runs
-// one per CU: two fit (62 VGPRs), but on MI355X two per CU, each with half
-// the sets, measured 5-20% slower on every decode shape.  The smaller
-// workgroups of the tuning knobs use what fits, looked up once per K (the
-// LDS footprint depends on it).
-template <int XT, int NW, int P>
-int occupancy_memo(int nblk, size_t lds) {
-    if (NW == 16) return 1;
-    static int memo[513];                                 // by nblk; 0 = unknown
-    if (memo[nblk] == 0) memo[nblk] = occupancy_wgs<XT, NW, P>(lds);
-    return memo[nblk];
 }
 
 // Work split of a GEMV: `per` consecutive sets per workgroup, K cut into nz
-// splits of ksteps steps (split z writes y + z * R).
-struct Split { int64_t per, grid; int ksteps, nz; };
+// splits of ksteps steps (split z writes y + z * R).  One 16-wave workgroup
+// per CU: two fit, but two per CU, each with half the sets, measured 5-20%
+// slower on every decode shape.
+struct Split { int64_t per, grid; int ksteps, nz; bool kbp; };
 
-// lds_free: LDS beside the x staging, which holds 16 row partials of every
+// Item partial bytes: per Q2 block (KBP) or per row.
+constexpr size_t PART_KBP = 256, PART_ROW = 64;
+
+// lds_free: LDS beside the x staging, which holds the partials of every
 // item of the workgroup's sets (rows_per_set sets of W per set counted).
-Split plan(int64_t nsets, int steps, int ksplit, int64_t slots, size_t lds_free,
-           int rows_per_set) {
+// Per-block partials unless not even one set's fit.
+Split plan(int64_t nsets, int steps, int ksplit, int64_t cus, size_t lds_free, int rows_per_set) {
     Split sp;
     sp.ksteps = (steps + ksplit - 1) / ksplit;
     sp.nz = (steps + sp.ksteps - 1) / sp.ksteps;
+    const size_t per_set = (size_t)sp.ksteps * rows_per_set;
+    sp.kbp = PART_KBP * per_set <= lds_free;
     const int64_t cap = std::max<int64_t>(
-            1, std::min<int64_t>(256, (int64_t)(lds_free / (64 * (size_t)sp.ksteps * rows_per_set))));
+            1, std::min<int64_t>(256, (int64_t)(lds_free / ((sp.kbp ? PART_KBP : PART_ROW) * per_set))));
     // Every resident workgroup gets the same number of sets.
-    sp.per = std::min(cap, (nsets * sp.nz + slots - 1) / slots);
+    sp.per = std::min(cap, (nsets * sp.nz + cus - 1) / cus);
     sp.grid = (nsets + sp.per - 1) / sp.per;
     return sp;
 }
 
-// LDS footprint used for the occupancy lookup: the x staging and one set's
-// partials (the kernel's registers, not LDS, bound the workgroups per CU).
-size_t occ_lds(size_t xlds, int steps) { return xlds + (size_t)128 * steps; }
-
-template <int XT, int NW, int P>
-int launch(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, size_t xlds, const NormIn &nin,
-           int ksplit, const GluOut &glu) {
+template <int XT>
+int launch(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, size_t xlds,
+           const NormIn &nin = NormIn{nullptr, nullptr, nullptr, 0.f, 0, 0}, int ksplit = 1,
+           const GluOut &glu = GluOut{nullptr, 0}) {
     const int64_t K = w->K, R = w->R;
     const int nblk = (int)(K >> 7), steps = (nblk + 3) / 4;
     const int cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
     // SwiGLU: split over gate sets, each bringing its up set along.
     const int64_t nsets = glu.pair_sets ? glu.pair_sets : (R + 15) / 16;
     const int rows_per_set = glu.pair_sets ? 2 : 1;
-    const int occ = occupancy_memo<XT, NW, P>(nblk, occ_lds(xlds, steps));
-    const Split sp = plan(nsets, steps, glu.pair_sets ? 1 : ksplit, (int64_t)cus * occ,
-                          LDS_BYTES - xlds, rows_per_set);
-    const size_t lds = xlds + (size_t)sp.per * rows_per_set * sp.ksteps * 64;
-    GD_REQUIRE(ctx, lds <= LDS_BYTES && sp.grid < (1LL << 31),
+    const Split sp = plan(nsets, steps, glu.pair_sets ? 1 : ksplit, cus, LDS_BYTES - xlds,
+                          rows_per_set);
+    const size_t lds = xlds + (size_t)sp.per * rows_per_set * sp.ksteps * (sp.kbp ? PART_KBP : PART_ROW);
+    // Items of a workgroup stay below 2^16 and a split below 128 steps (the
+    // kernel's quotient by multiply-high).
+    GD_REQUIRE(ctx, lds <= LDS_BYTES && sp.grid < (1LL << 31) && sp.ksteps <= 128 &&
+                        sp.per * rows_per_set * sp.ksteps < (1 << 16),
                "gd_q2_0_gemv: K=%lld R=%lld does not fit", (long long)K, (long long)R);
-    hipLaunchKernelGGL((q2_0_gemv_mfma_kernel<XT, NW, P>), dim3((unsigned)sp.grid, sp.nz),
-                       dim3(64 * NW), lds, ctx->stream, (const uint8_t *)w->codes,
-                       (const uint16_t *)w->scales, x, y, (int)K, (int)R, (int)nsets, (int)sp.per,
-                       sp.ksteps, nin, glu);
+    auto kern = sp.kbp ? q2_0_gemv_mfma_kernel<XT, true> : q2_0_gemv_mfma_kernel<XT, false>;
+    hipLaunchKernelGGL(kern, dim3((unsigned)sp.grid, sp.nz), dim3(64 * NW), lds, ctx->stream,
+                       (const uint8_t *)w->codes, (const uint16_t *)w->scales, x, y, (int)K, (int)R,
+                       (int)nsets, (int)sp.per, sp.ksteps, nin, glu);
     GD_LAUNCHED(ctx, "q2_0_gemv_mfma");
     return GD_OK;
-}
-
-template <int XT, int NW, int P>
-int launch_or_prepare(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, size_t xlds,
-                      const NormIn &nin, int ksplit, const GluOut &glu) {
-    if (w) return launch<XT, NW, P>(ctx, w, x, y, xlds, nin, ksplit, glu);
-    // Preparation only (x carries nblk): fill the occupancy memo.
-    const int nblk = (int)(intptr_t)x;
-    (void)occupancy_memo<XT, NW, P>(nblk, occ_lds(xlds, (nblk + 3) / 4));
-    return GD_OK;
-}
-
-template <int XT>
-int launch_nw(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, size_t xlds,
-              const NormIn &nin = NormIn{nullptr, nullptr, nullptr, 0.f, 0, 0}, int ksplit = 1,
-              const GluOut &glu = GluOut{nullptr, 0}) {
-    // Waves per workgroup (all share one staged copy of x) and tiles in
-    // flight per wave; GADEON_GEMV_NW / GADEON_GEMV_P override for tuning.
-    static const char *env_nw = getenv("GADEON_GEMV_NW");
-    static const char *env_p = getenv("GADEON_GEMV_P");
-    const int nw = env_nw ? atoi(env_nw) : 16, pp = env_p ? atoi(env_p) : 2;
-#define GD_L(NW_, P_) launch_or_prepare<XT, NW_, P_>(ctx, w, x, y, xlds, nin, ksplit, glu)
-    // The fused-norm variant stages one x entry per thread: 16 waves only.
-    if constexpr (XT == 2) {
-        return GD_L(16, 2);
-    } else {
-        if (nw == 4) return pp == 2 ? GD_L(4, 2) : pp == 4 ? GD_L(4, 4) : GD_L(4, 3);
-        if (nw == 8) return pp == 2 ? GD_L(8, 2) : pp == 4 ? GD_L(8, 4) : GD_L(8, 3);
-        return pp == 2 ? GD_L(16, 2) : pp == 4 ? GD_L(16, 4) : GD_L(16, 3);
-    }
-#undef GD_L
 }
 
 }  // namespace
@@ -568,8 +548,7 @@ int gd_gemv_mfma(gd_ctx *ctx, const gd_q2w *w, const void *x, int x_dtype, float
                "gd_q2_0_gemv: K=%lld too long for LDS staging of %s x", (long long)K,
                XT ? "f32" : "f16");
     const NormIn none{nullptr, nullptr, nullptr, 0.f, 0, 0};
-    return XT ? launch_nw<1>(ctx, w, x, y, xlds, none, ksplit)
-              : launch_nw<0>(ctx, w, x, y, xlds, none, ksplit);
+    return XT ? launch<1>(ctx, w, x, y, xlds, none, ksplit) : launch<0>(ctx, w, x, y, xlds, none, ksplit);
 }
 
 // K splits (1..4) for an f16-x GEMV whose partial rows the consumer can sum:
@@ -583,11 +562,10 @@ int gd_gemv_ksplit(gd_ctx *ctx, int64_t K, int64_t R) {
     if (K % 128 || xlds + (size_t)64 * steps > LDS_BYTES) return 1;
     const int cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
     const int64_t nsets = (R + 15) / 16;
-    const int occ = occupancy_memo<0, 16, 2>(nblk, occ_lds(xlds, steps));
     int best = 1;
     double best_cost = 1e30;
     for (int z = 1; z <= 4; z++) {
-        const Split sp = plan(nsets, steps, z, (int64_t)cus * occ, LDS_BYTES - xlds, 1);
+        const Split sp = plan(nsets, steps, z, cus, LDS_BYTES - xlds, 1);
         const double cost = (double)((sp.grid * sp.nz + cus - 1) / cus) * sp.per * sp.ksteps +
                             2.0 * (sp.nz - 1);
         if (cost < best_cost - 1e-9) {
@@ -612,20 +590,6 @@ int gd_gemv_mfma_norm(gd_ctx *ctx, const gd_q2w *w, const float *h, const float 
                (long long)w->K);
     GD_REQUIRE(ctx, !glu_out || w->R % 32 == 0, "gd_gemv_norm: SwiGLU needs R = 2 x 16k rows");
     const GluOut glu{glu_out, glu_out ? (int)(w->R / 32) : 0};
-    return launch_nw<2>(ctx, w, h, y, xlds, NormIn{delta, normw, hout, eps, delta ? nd : 0, dstride},
-                        1, glu);
-}
-
-// Host-side set-up for GEMVs of reduction length K (the occupancy lookup),
-// so that a later call can be captured into a graph without runtime queries.
-// x_dtype GD_F16, GD_F32, or -1 for the fused-norm variant.
-int gd_gemv_mfma_prepare(gd_ctx *ctx, int64_t K, int x_dtype) {
-    const int XT = x_dtype == GD_F32 ? 1 : x_dtype == -1 ? 2 : 0;
-    const int nblk = (int)(K >> 7);
-    const size_t xlds = xlds_bytes(nblk, XT == 1);
-    if (K % 128 || K > 65536 || xlds + (size_t)64 * ((nblk + 3) / 4) > LDS_BYTES) return GD_EINVAL;
-    const void *tag = (const void *)(intptr_t)nblk;
-    return XT == 1 ? launch_nw<1>(ctx, nullptr, tag, nullptr, xlds)
-         : XT == 2 ? launch_nw<2>(ctx, nullptr, tag, nullptr, xlds)
-                   : launch_nw<0>(ctx, nullptr, tag, nullptr, xlds);
+    return launch<2>(ctx, w, h, y, xlds, NormIn{delta, normw, hout, eps, delta ? nd : 0, dstride}, 1,
+                     glu);
 }

@@ -961,11 +961,6 @@ extern "C" int gd_stack_generate(gd_stack *st, int n, int32_t *tokens) {
     // One decode step reads the previous pick from st->dtok, so the whole step
     // (embed .. argmax, position bump) replays with no host involvement.
     if (!st->decode_exec && !eager) {
-        // Host-side lookups the GEMVs make on first use happen before capture.
-        for (int64_t K : {(int64_t)st->c.n_embd, (int64_t)st->c.n_ff, (int64_t)st->valDim,
-                          (int64_t)st->c.n_head * HD})
-            if ((rc = gd_gemv_mfma_prepare(ctx, K, GD_F16))) return rc;
-        if ((rc = gd_gemv_mfma_prepare(ctx, st->c.n_embd, -1))) return rc;
         GD_HIP(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
         rc = gd_q2_0_dequant_rows(ctx, &st->embd, st->dtok, 1, st->x);
         if (rc == GD_OK) rc = forward(st, 1, true);
