@@ -21,10 +21,11 @@
 // hi = f16(x) and lo = f16(x - hi) and multiplied as hi*hi + hi*lo + lo*hi
 // (about 22 significant bits), so the result tracks the f32 recurrence.
 //   gdn_prep  (value head, chunk): K K^T and Q K^T on the matrix cores give A
-//             and P; one wave inverts I + A by forward substitution with its
-//             column of T in registers while the others stage the transposed
-//             operands; then W = T X and U = T Y (the UT transform) on the
-//             matrix cores.  The chunks are independent.
+//             and P; I + A is inverted in 16 x 16 blocks (diagonal blocks by
+//             forward substitution, one wave each, then the blocks below in
+//             levels of block products, all 256 threads); then W = T X and
+//             U = T Y (the UT transform) on the matrix cores.  The chunks are
+//             independent.
 //   gdn_scan  (value head, 16 columns of S): walks the chunks in order with
 //             its slice of S resident in LDS: delta = U - W S, O = qScale
 //             e^G (Q S) + P delta, S <- e^{G_L} S + K^T (e^{G_L-G} delta).
@@ -112,7 +113,8 @@ __global__ __launch_bounds__(256) void gdn_prep(PrepArgs a) {
     __shared__ __attribute__((aligned(16))) f16 Yh[DV][CP + 8], Yl[DV][CP + 8];
     __shared__ __attribute__((aligned(16))) float Af[CP][CP + 4];
     __shared__ __attribute__((aligned(16))) float Tf[CP][CP + 4];
-    __shared__ float Gs[CP], Bs[CP];
+    __shared__ __attribute__((aligned(16))) float Ms[(CP / 16 - 1) * 256];   // block products
+    __shared__ float Gs[CP], Bs[CP], BEs[CP];               // G, beta, beta e^G
 
     const int hv = blockIdx.x / a.nchunks, c = blockIdx.x % a.nchunks;
     const int hk = hv % a.nK;
@@ -145,8 +147,10 @@ __global__ __launch_bounds__(256) void gdn_prep(PrepArgs a) {
             if (lane >= off) gv += o;
         }
         if (lane < CP) {
+            const float bt = lane < L ? a.beta[(t0 + lane) * a.nV + hv] : 0.f;
             Gs[lane] = gv;
-            Bs[lane] = lane < L ? a.beta[(t0 + lane) * a.nV + hv] : 0.f;
+            Bs[lane] = bt;
+            BEs[lane] = bt * __expf(gv);
         }
     }
     __syncthreads();
@@ -172,7 +176,7 @@ __global__ __launch_bounds__(256) void gdn_prep(PrepArgs a) {
 #pragma unroll
         for (int v = 0; v < 4; v++) {
             const int t = ti * 16 + kg * 4 + v;
-            const float dec = expf(Gs[t] - Gs[s]);
+            const float dec = __expf(Gs[t] - Gs[s]);          // factor in (0, 1]
             if (!isP) {
                 Af[t][s] = (s < t && t < L) ? Bs[t] * dec * acc[v] : 0.f;
             } else {
@@ -193,56 +197,77 @@ __global__ __launch_bounds__(256) void gdn_prep(PrepArgs a) {
     }
     __syncthreads();
 
-    if (wave == 0) {
-        // T = (I + A)^-1 by forward substitution, lane s holding column s of
-        // T in registers: T[t][s] = -sum_{m<t} A[t][m] T[m][s] (T[m][s] = 0
-        // for m < s, T[s][s] = 1).  A[t][m] is a broadcast read.
-        const int s = lane;
-        float Tc[CP];
+    // T = (I + A)^-1 in 16 x 16 blocks (A is strictly lower triangular).
+    // Diagonal blocks first, wave w inverting block w by forward
+    // substitution with lane s < 16 holding its column s: T[t][s] =
+    // -sum_{m<t} A[t][m] T[m][s] (T[m][s] = 0 for m < s, T[s][s] = 1);
+    // blocks above the diagonal are zero.
+    if (wave < NB && lane < 16) {
+        const int b0 = wave * 16, s = lane;
+        float Tc[16];
 #pragma unroll
-        for (int m = 0; m < CP; m++) Tc[m] = m == s ? 1.f : 0.f;
+        for (int m = 0; m < 16; m++) Tc[m] = m == s ? 1.f : 0.f;
 #pragma unroll
-        for (int t = 1; t < CP; t++) {
-            float acc0 = 0.f, acc1 = 0.f;
+        for (int t = 1; t < 16; t++) {
+            float acc = 0.f;
 #pragma unroll
-            for (int m = 0; m < t; m += 2) {
-                acc0 = fmaf(Af[t][m], Tc[m], acc0);
-                if (m + 1 < t) acc1 = fmaf(Af[t][m + 1], Tc[m + 1], acc1);
-            }
-            Tc[t] = t == s ? 1.f : -(acc0 + acc1);
+            for (int m = 0; m < t; m++) acc = fmaf(Af[b0 + t][b0 + m], Tc[m], acc);
+            Tc[t] = t == s ? 1.f : -acc;
         }
-        if (s < CP) {
 #pragma unroll
-            for (int m = 0; m < CP; m++) Tf[m][s] = Tc[m];
-        }
-    } else {
-        // X^T = (diag(beta e^G) K)^T and Y^T = (diag(beta) V)^T, split, as
-        // the B operands of T X and T Y: entry (i, 8 tokens s .. s+7).
-        for (int e = tid - 64; e < DK * (CP / 8); e += 192) {
-            const int i = e / (CP / 8), s8 = (e % (CP / 8)) * 8;
-            float xv[8], yv[8];
-#pragma unroll
-            for (int q = 0; q < 8; q++) {
-                const int s = s8 + q;
-                const float bt = Bs[s];
-                xv[q] = bt * expf(Gs[s]) * (float)Ks[s][i];
-                yv[q] = bt * (float)QVs[s][i];
-            }
-            f16x8 h, l;
-            split8(xv, h, l);
-            *(f16x8 *)&Xh[i][s8] = h;
-            *(f16x8 *)&Xl[i][s8] = l;
-            split8(yv, h, l);
-            *(f16x8 *)&Yh[i][s8] = h;
-            *(f16x8 *)&Yl[i][s8] = l;
-        }
+        for (int m = 0; m < 16; m++) Tf[b0 + m][b0 + s] = Tc[m];
     }
-    // K^T to the workspace for the scan's state update (its A operand).
+    for (int e = tid; e < CP * CP; e += 256) {
+        const int r = e / CP, cc = e % CP;
+        if ((cc >> 4) > (r >> 4)) Tf[r][cc] = 0.f;
+    }
+    __syncthreads();
+    // Blocks below the diagonal by distance d = i - j, each level from the
+    // ones before it: T_ij = -T_ii (sum_{k=j}^{i-1} A_ik T_kj).  Thread e
+    // takes element (r, cc) of block i = d + e / 256.
+    for (int d = 1; d < NB; d++) {
+        for (int e = tid; e < (NB - d) * 256; e += 256) {
+            const int i = d + (e >> 8), j = i - d, r = (e >> 4) & 15, cc = e & 15;
+            float m = 0.f;
+            for (int k = j; k < i; k++)
+#pragma unroll
+                for (int q = 0; q < 16; q++)
+                    m = fmaf(Af[i * 16 + r][k * 16 + q], Tf[k * 16 + q][j * 16 + cc], m);
+            Ms[e] = m;
+        }
+        __syncthreads();
+        for (int e = tid; e < (NB - d) * 256; e += 256) {
+            const int i = d + (e >> 8), j = i - d, r = (e >> 4) & 15, cc = e & 15;
+            const float *mb = Ms + (e & ~255);
+            float t = 0.f;
+#pragma unroll
+            for (int q = 0; q < 16; q++) t = fmaf(Tf[i * 16 + r][i * 16 + q], mb[q * 16 + cc], t);
+            Tf[i * 16 + r][j * 16 + cc] = -t;
+        }
+        __syncthreads();
+    }
+    // X^T = (diag(beta e^G) K)^T and Y^T = (diag(beta) V)^T, split, as the
+    // B operands of T X and T Y, and K^T to the workspace for the scan's
+    // state update (its A operand): entry (8 tokens s .. s+7, i), lanes
+    // along i so that the row reads of K and V hit distinct banks.
     for (int e = tid; e < DK * (CP / 8); e += 256) {
-        const int i = e / (CP / 8), s8 = (e % (CP / 8)) * 8;
+        const int s8 = (e / DK) * 8, i = e % DK;
+        float xv[8], yv[8];
         f16x8 kv;
 #pragma unroll
-        for (int q = 0; q < 8; q++) kv[q] = Ks[s8 + q][i];
+        for (int q = 0; q < 8; q++) {
+            const int s = s8 + q;
+            kv[q] = Ks[s][i];
+            xv[q] = BEs[s] * (float)kv[q];
+            yv[q] = Bs[s] * (float)QVs[s][i];
+        }
+        f16x8 h, l;
+        split8(xv, h, l);
+        *(f16x8 *)&Xh[i][s8] = h;
+        *(f16x8 *)&Xl[i][s8] = l;
+        split8(yv, h, l);
+        *(f16x8 *)&Yh[i][s8] = h;
+        *(f16x8 *)&Yl[i][s8] = l;
         *(f16x8 *)&a.w.KT[((size_t)u * DK + i) * CP + s8] = kv;
     }
     if (tid < CP) a.w.G[(size_t)u * CP + tid] = Gs[tid];
