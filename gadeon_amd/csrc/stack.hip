@@ -108,28 +108,29 @@ __global__ void k_conv4_ring(const float *proj, int64_t stride, float *ring, int
 // conv channel): causal conv + SiLU of the head's q, k and v channels
 // (advancing their conv ring), gate, L2 norms of q and k, the delta-rule
 // state update, and the gated RMS norm of the output into f16.  The same
-// arithmetic, in the same order, as k_conv4 + gd_gdn_decode (GATE, NORM) +
-// k_onorm_silu, in one launch (GDN.swift:71-109, BonsaiEngine.swift:
-// 98-139).  Lane l of wave w owns value columns l and l + 64 and key rows
-// 32w .. 32w+31.
-__global__ __launch_bounds__(256) void k_gdn_step(
+// arithmetic as k_conv4 + gd_gdn_decode (GATE, NORM) + k_onorm_silu, in one
+// launch (GDN.swift:71-109, BonsaiEngine.swift:98-139).  16 waves: lane l of
+// wave w owns value columns l and l + 64 and key rows 8w .. 8w+7, so each
+// thread streams 16 state values and four waves per SIMD hide the latency.
+constexpr int GS_W = 16, GS_R = HD / GS_W;       // waves, key rows per wave
+__global__ __launch_bounds__(64 * GS_W) void k_gdn_step(
         const float *proj, float *ring, const float *cw, const float *dt, const float *aNeg,
         float *S, const float *onw, uint16_t *out, int convDim, int keyDim, int off_z, int off_b,
         int off_a, float qScale, float eps) {
     __shared__ float kq[2][HD];                  // k, q after conv + SiLU
     __shared__ float vs[HD];
-    __shared__ float red[4][2][64];
+    __shared__ float red[GS_W][2][64];
     __shared__ float scal[2];
     __shared__ float gate[2];                    // beta, gamma
     const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     float *Sh = S + (int64_t)h * HD * HD;
     // State loads first: they are the bandwidth.
-    float s0[32], s1[32];
+    float s0[GS_R], s1[GS_R];
 #pragma unroll
-    for (int r = 0; r < 32; r++) {
-        s0[r] = Sh[(int64_t)(wave * 32 + r) * HD + lane];
-        s1[r] = Sh[(int64_t)(wave * 32 + r) * HD + lane + 64];
+    for (int r = 0; r < GS_R; r++) {
+        s0[r] = Sh[(int64_t)(wave * GS_R + r) * HD + lane];
+        s1[r] = Sh[(int64_t)(wave * GS_R + r) * HD + lane + 64];
     }
     auto conv = [&](int c) {
         const float w0 = cw[c * 4], w1 = cw[c * 4 + 1], w2 = cw[c * 4 + 2], w3 = cw[c * 4 + 3];
@@ -145,15 +146,14 @@ __global__ __launch_bounds__(256) void k_gdn_step(
         ring[2 * convDim + c] = cur;
         return gd_silu(acc);
     };
-    // Threads 0..127: q channel tid; 128..255: k channel tid - 128; threads
-    // 0..127 also take v channel tid.
-    {
-        const int i = tid & (HD - 1);
-        const float y = conv(tid < HD ? h * HD + i : keyDim + h * HD + i);
-        kq[tid < HD ? 1 : 0][i] = y;
-        if (tid < HD) vs[i] = conv(2 * keyDim + h * HD + i);
-    }
-    if (tid == 0) {
+    // Threads 0..127: q channel tid; 128..255: k channel tid - 128;
+    // 256..383: v channel tid - 256.
+    if (tid < 3 * HD) {
+        const int part = tid / HD, i = tid % HD;
+        const float y = conv(part * keyDim + h * HD + i);
+        if (part < 2) kq[1 - part][i] = y;
+        else vs[i] = y;
+    } else if (tid == 3 * HD) {
         gate[0] = gd_sigmoid(proj[off_b + h]);
         gate[1] = expf(gd_softplus(proj[off_a + h] + dt[h]) * aNeg[h]);
     }
@@ -168,8 +168,8 @@ __global__ __launch_bounds__(256) void k_gdn_step(
     const float rk = scal[0], rq = scal[1], beta = gate[0], gam = gate[1];
     float sk0 = 0.0f, sk1 = 0.0f;
 #pragma unroll
-    for (int r = 0; r < 32; r++) {
-        const float kv = kq[0][wave * 32 + r];
+    for (int r = 0; r < GS_R; r++) {
+        const float kv = kq[0][wave * GS_R + r];
         s0[r] *= gam;
         s1[r] *= gam;
         sk0 = fmaf(s0[r], kv, sk0);
@@ -178,14 +178,21 @@ __global__ __launch_bounds__(256) void k_gdn_step(
     red[wave][0][lane] = sk0;
     red[wave][1][lane] = sk1;
     __syncthreads();
-    sk0 = (red[0][0][lane] + red[1][0][lane] + red[2][0][lane] + red[3][0][lane]) * rk;
-    sk1 = (red[0][1][lane] + red[1][1][lane] + red[2][1][lane] + red[3][1][lane]) * rk;
+    sk0 = 0.0f;
+    sk1 = 0.0f;
+#pragma unroll
+    for (int w = 0; w < GS_W; w++) {
+        sk0 += red[w][0][lane];
+        sk1 += red[w][1][lane];
+    }
+    sk0 *= rk;
+    sk1 *= rk;
     const float d0 = beta * (vs[lane] - sk0) * rk, d1 = beta * (vs[lane + 64] - sk1) * rk;
     __syncthreads();                             // red[] is reused below
     float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
-    for (int r = 0; r < 32; r++) {
-        const int i = wave * 32 + r;
+    for (int r = 0; r < GS_R; r++) {
+        const int i = wave * GS_R + r;
         const float kv = kq[0][i], qv = kq[1][i];
         s0[r] = fmaf(kv, d0, s0[r]);
         s1[r] = fmaf(kv, d1, s1[r]);
@@ -198,10 +205,14 @@ __global__ __launch_bounds__(256) void k_gdn_step(
     red[wave][1][lane] = a1;
     __syncthreads();
     if (wave == 0) {
-        const float o0 = (red[0][0][lane] + red[1][0][lane] + red[2][0][lane] + red[3][0][lane]) *
-                         rq * qScale;
-        const float o1 = (red[0][1][lane] + red[1][1][lane] + red[2][1][lane] + red[3][1][lane]) *
-                         rq * qScale;
+        float o0 = 0.0f, o1 = 0.0f;
+#pragma unroll
+        for (int w = 0; w < GS_W; w++) {
+            o0 += red[w][0][lane];
+            o1 += red[w][1][lane];
+        }
+        o0 *= rq * qScale;
+        o1 *= rq * qScale;
         const float ss = gd_wave_sum(o0 * o0 + o1 * o1);
         const float sc = 1.0f / sqrtf(ss / (float)HD + eps);
         const float *z = proj + off_z + h * HD;
@@ -670,7 +681,7 @@ int forward(gd_stack *st, int N, bool decode) {
         if (ly.rec) {
             const int off_z = st->convDim, off_b = off_z + st->valDim, off_a = off_b + nV;
             if (decode && nK == nV && c.d_state == HD) {
-                K_(k_gdn_step, dim3(nV), dim3(256), 0, s, st->proj, ly.conv_state, ly.conv_w,
+                K_(k_gdn_step, dim3(nV), dim3(64 * GS_W), 0, s, st->proj, ly.conv_state, ly.conv_w,
                    ly.dt, ly.a_neg, ly.rec_state, ly.ssm_norm, st->a16, st->convDim, st->keyDim,
                    off_z, off_b, off_a, qScale, eps);
             } else if (decode) {
