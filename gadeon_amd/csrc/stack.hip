@@ -443,11 +443,25 @@ __global__ __launch_bounds__(256) void k_attn_decode(
     const float q0 = q[(int64_t)h * HD + 2 * lane] * scale;
     const float q1 = q[(int64_t)h * HD + 2 * lane + 1] * scale;
     float m = -INFINITY, l = 0.f, a0 = 0.f, a1 = 0.f;
-    // Wave w of split sp takes keys j = (sp * 4 + w) + 64 * i.
-    for (int j = sp * 4 + w; j < T; j += DSPLIT * 4) {
-        const int64_t base = kv_slot(page_table, j, block) * kvDim + kvh * HD + 2 * lane;
-        const uint32_t kk = *(const uint32_t *)(kc + base);
-        const uint32_t vv = *(const uint32_t *)(vc + base);
+    // Wave w of split sp takes keys j = (sp * 4 + w) + 64 * i.  The next
+    // key's page-table entry and K/V values are requested before this key's
+    // arithmetic, so each key waits only for loads issued a key earlier.
+    constexpr int STEP = DSPLIT * 4;
+    auto kv_base = [&](int j) { return kv_slot(page_table, j, block) * kvDim + kvh * HD + 2 * lane; };
+    int j = sp * 4 + w;
+    uint32_t kn = 0, vn = 0;
+    if (j < T) {
+        const int64_t b0 = kv_base(j);
+        kn = *(const uint32_t *)(kc + b0);
+        vn = *(const uint32_t *)(vc + b0);
+    }
+    for (; j < T; j += STEP) {
+        const uint32_t kk = kn, vv = vn;
+        if (j + STEP < T) {
+            const int64_t bn = kv_base(j + STEP);
+            kn = *(const uint32_t *)(kc + bn);
+            vn = *(const uint32_t *)(vc + bn);
+        }
         float s = q0 * gd_h2f((uint16_t)(kk & 0xffff)) + q1 * gd_h2f((uint16_t)(kk >> 16));
         s = gd_wave_sum(s);
         const float mn = fmaxf(m, s);
