@@ -8,19 +8,19 @@
 // MI355X design:
 //   * v_mfma_f32_32x32x16_f16 (fp16 operands, f32 accumulate): the fastest
 //     f16 MFMA shape on gfx950.  A = X (tokens), B = W (weight rows).
-//   * X is the heavy operand (16 bits per element against 2 for W), so it is
-//     the one staged through LDS and shared by the workgroup's 4 waves; each
-//     wave owns NT*32 weight rows and all MT*32 tokens of the tile.
-//   * W never touches LDS: each lane loads the 2-bit codes of its own B
-//     operand (8 bytes per 64-K slice) straight from the tiled device layout
-//     and expands them in registers to (code-1)*d in f16 -- exact, as in
-//     dq_q2_0_h.  To make a lane's codes one 8-byte word, the K order inside
-//     each 64-K slice is permuted: lane half h, step s, element e carries
-//     K = 32h + 8s + e, for X and W alike (a sum over K does not care).
-//   * X slices are double-buffered in LDS (rows padded by 16 bytes); the
-//     next slice's X and codes are loaded while the current one multiplies.
-//   * Short-R shapes split K across gridDim.z into f32 partials that the
-//     caller sums, so that every CU gets work.
+//   * X is the heavy operand (16 bits per element against 2 for W): one X
+//     tile of MT*32 tokens is shared by the workgroup's NW waves, each of
+//     which owns NT*32 weight rows.
+//   * Every operand reaches LDS by direct buffer->LDS loads into a two-stage
+//     ring of 128-K blocks (X, each wave's codes and row scales); the next
+//     block's loads go out right after the barrier that opens this one.
+//   * Each lane expands the 2-bit codes of its own B operand in registers to
+//     (code-1)*d in f16 -- exact, as in dq_q2_0_h.  To make a lane's codes
+//     one 16-bit word, the K order inside each 64-K slice is permuted: lane
+//     half h, step s, element e carries K = 32h + 8s + e, for X and W alike
+//     (a sum over K does not care).
+//   * Short-R shapes split K into f32 partials that the caller sums, so that
+//     every CU gets work; a cost model picks the tile and the split.
 #include "gd_internal.h"
 
 #include <cstdlib>
