@@ -64,6 +64,39 @@ __device__ __forceinline__ f32x4 mfma3(const f16x8 &ah, const f16x8 &al, const f
     return mfma(al, bh, c);
 }
 
+// Eight consecutive activations as loaded (f16 or f32), converted by cvt8:
+// keeping them raw lets a prefetch stay in flight until the values are used.
+template <typename IO> struct Raw8;
+template <> struct Raw8<uint16_t> { u32x4 v; };
+template <> struct Raw8<float> { f32x4 a, b; };
+template <typename IO>
+__device__ __forceinline__ Raw8<IO> load_raw8(const void *base, int64_t idx) {
+    Raw8<IO> r;
+    if constexpr (sizeof(IO) == 2) {
+        r.v = *(const u32x4 *)((const uint16_t *)base + idx);
+    } else {
+        const f32x4 *p = (const f32x4 *)((const float *)base + idx);
+        r.a = p[0];
+        r.b = p[1];
+    }
+    return r;
+}
+// As f16, zero when !ok.
+template <typename IO>
+__device__ __forceinline__ f16x8 cvt8(const Raw8<IO> &r, bool ok) {
+    f16x8 h;
+    if constexpr (sizeof(IO) == 2) {
+        h = __builtin_bit_cast(f16x8, ok ? r.v : u32x4{0, 0, 0, 0});
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            h[e] = ok ? (f16)r.a[e] : (f16)0.0f;
+            h[4 + e] = ok ? (f16)r.b[e] : (f16)0.0f;
+        }
+    }
+    return h;
+}
+
 // Eight consecutive activations (f16 or f32) as f16, zero when !ok.
 template <typename IO>
 __device__ __forceinline__ f16x8 load8(const void *base, int64_t idx, bool ok) {
@@ -323,15 +356,15 @@ struct ScanArgs {
     float qScale;
 };
 
-// One chunk's operands of this thread, all independent of S: loaded one
-// chunk ahead so that the serial walk over chunks waits on no memory but
-// its own LDS.
-template <int CP>
+// One chunk's operands of this thread, all independent of S: each group is
+// loaded while the previous chunk's later phases run, so the serial walk over
+// chunks waits on little but its own LDS.
+template <int CP, typename IO>
 struct ScanChunk {
     float g;                              // G[tid] (tid < CP)
     f16x8 wh[DK / 32], wl[DK / 32];       // W rows 16*wave + lr
     float uv[NCOL / 16][4];               // U rows 16*wave + 4*kg + v, this lane's column
-    f16x8 qa[DK / 32];                    // Q row 16*wave + lr
+    Raw8<IO> qr[DK / 32];                 // Q row 16*wave + lr (row 0 past the chunk), raw
     f16x8 ph[CP / 32], pl[CP / 32];       // P row 16*wave + lr
     f16x8 ka[2][CP / 32];                 // K^T rows 32*wave + 16*rt + lr
 };
@@ -345,11 +378,20 @@ __global__ __launch_bounds__(256) void gdn_scan(ScanArgs a) {
     __shared__ float Gs[CP];
 
     constexpr int NCB = DV / NCOL;
-    const int hv = blockIdx.x / NCB, j0 = (blockIdx.x % NCB) * NCOL;
+    static_assert(NCB % 8 == 0, "the grid must split evenly over the 8 XCDs");
+    // Workgroup b runs on XCD b % 8.  The NCB column slices of one head read
+    // the same chunk operands (W, P, K^T, Q), so they are dealt to one XCD:
+    // unit u = (b % 8) * (grid / 8) + b / 8, head u / NCB, so each chunk is
+    // fetched into one L2 once instead of into every L2.
+    const int u = (int)((blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3));
+    const int hv = u / NCB, j0 = (u % NCB) * NCOL;
     const int hk = hv % a.nK;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int lr = lane & 15, kg = lane >> 4;
-    const bool rows = wave < CP / 16;                   // this wave owns 16 chunk rows
+    // This wave owns 16 chunk rows (with CP = 64 every wave does: a constant,
+    // so no load below sits in a branch, which keeps the compiler's wait
+    // counts exact).
+    const bool rows = CP / 16 >= 4 || wave < CP / 16;
     const int tb = wave * 16;
     float *Sg = a.S + (size_t)hv * DK * DV;
 
@@ -358,12 +400,16 @@ __global__ __launch_bounds__(256) void gdn_scan(ScanArgs a) {
         Sf[i][j] = Sg[(size_t)i * DV + j0 + j];
     }
 
-    auto load = [&](int c, ScanChunk<CP> &k) {
-        c = min(c, a.nchunks - 1);
-        const int64_t t0 = (int64_t)c * a.C;
-        const int L = (int)min((int64_t)a.C, a.T - t0);
-        const size_t u = (size_t)hv * a.nchunks + c;
-        if (tid < CP) k.g = a.w.G[u * CP + tid];
+    // The operands of chunk c, loaded in three groups, each refilled for the
+    // next chunk as soon as its phase of this chunk has used it: W, U and G
+    // after delta, Q and P after O, K^T after the state update.  One set of
+    // registers (two full sets made the compiler reuse registers that loads
+    // in flight were still to write, and wait for every load).
+    ScanChunk<CP, IO> k;
+    auto unit = [&](int c) { return (size_t)hv * a.nchunks + min(c, a.nchunks - 1); };
+    auto loadW = [&](int c) {
+        const size_t u = unit(c);
+        k.g = a.w.G[u * CP + min(tid, CP - 1)];         // used by tid < CP
         if (rows) {
 #pragma unroll
             for (int ks = 0; ks < DK / 32; ks++) {
@@ -376,12 +422,20 @@ __global__ __launch_bounds__(256) void gdn_scan(ScanArgs a) {
 #pragma unroll
                 for (int v = 0; v < 4; v++)
                     k.uv[ct][v] = a.w.U[(u * CP + tb + kg * 4 + v) * DV + j0 + ct * 16 + lr];
+        }
+    };
+    auto loadQP = [&](int c) {
+        c = min(c, a.nchunks - 1);
+        const size_t u = unit(c);
+        const int64_t t0 = (int64_t)c * a.C;
+        const int L = (int)min((int64_t)a.C, a.T - t0);
+        if (rows) {
             const int tr = tb + lr;
             const bool rok = tr < L;
 #pragma unroll
             for (int ks = 0; ks < DK / 32; ks++)
-                k.qa[ks] = load8<IO>(a.q, (t0 + (rok ? tr : 0)) * a.q_stride + (int64_t)hk * DK +
-                                              ks * 32 + kg * 8, rok);
+                k.qr[ks] = load_raw8<IO>(a.q, (t0 + (rok ? tr : 0)) * a.q_stride + (int64_t)hk * DK +
+                                                  ks * 32 + kg * 8);
 #pragma unroll
             for (int ks = 0; ks < CP / 32; ks++) {
                 const size_t pi = (u * CP + tr) * CP + ks * 32 + kg * 8;
@@ -389,6 +443,9 @@ __global__ __launch_bounds__(256) void gdn_scan(ScanArgs a) {
                 k.pl[ks] = *(const f16x8 *)&a.w.Pl[pi];
             }
         }
+    };
+    auto loadK = [&](int c) {
+        const size_t u = unit(c);
 #pragma unroll
         for (int rt = 0; rt < 2; rt++)
 #pragma unroll
@@ -397,7 +454,7 @@ __global__ __launch_bounds__(256) void gdn_scan(ScanArgs a) {
                                                         ks * 32 + kg * 8];
     };
 
-    auto process = [&](int c, const ScanChunk<CP> &k) {
+    auto process = [&](int c) {
         const int64_t t0 = (int64_t)c * a.C;
         const int L = (int)min((int64_t)a.C, a.T - t0);
         __syncthreads();
@@ -447,9 +504,14 @@ __global__ __launch_bounds__(256) void gdn_scan(ScanArgs a) {
                 *(f16x4 *)&El[j][tq] = f16x4{el[0], el[1], el[2], el[3]};
             }
         }
+        loadW(c + 1);
         __syncthreads();
 
         // O = qScale e^{G_t} (Q S) + P delta for the chunk's tokens.
+        // Output rows t0 .. t0+L-1 through a bounds-checked buffer resource.
+        const __amdgpu_buffer_rsrc_t ors = gd_rsrc((OT *)a.o + t0 * a.o_stride,
+                                                   (uint32_t)L * (uint32_t)a.o_stride * sizeof(OT));
+        const uint32_t obase = (uint32_t)hv * DV + j0;
         if (rows) {
 #pragma unroll
             for (int ct = 0; ct < NCOL / 16; ct++) {
@@ -458,8 +520,9 @@ __global__ __launch_bounds__(256) void gdn_scan(ScanArgs a) {
 #pragma unroll
                 for (int ks = 0; ks < DK / 32; ks++) {
                     const int i0 = ks * 32 + kg * 8;
-                    acc = mfma(k.qa[ks], *(const f16x8 *)&Sh[j][i0], acc);
-                    acc = mfma(k.qa[ks], *(const f16x8 *)&Sl[j][i0], acc);
+                    const f16x8 qa = cvt8<IO>(k.qr[ks], tb + lr < L);
+                    acc = mfma(qa, *(const f16x8 *)&Sh[j][i0], acc);
+                    acc = mfma(qa, *(const f16x8 *)&Sl[j][i0], acc);
                 }
 #pragma unroll
                 for (int v = 0; v < 4; v++) acc[v] *= a.qScale * expf(Gs[tb + kg * 4 + v]);
@@ -469,17 +532,19 @@ __global__ __launch_bounds__(256) void gdn_scan(ScanArgs a) {
                     acc = mfma3(k.ph[ks], k.pl[ks], *(const f16x8 *)&Dh[j][s0],
                                 *(const f16x8 *)&Dl[j][s0], acc);
                 }
+                // Rows t >= L lie past the resource: the store is dropped.
 #pragma unroll
                 for (int v = 0; v < 4; v++) {
-                    const int t = tb + kg * 4 + v;
-                    if (t < L) {
-                        const int64_t oi = (t0 + t) * a.o_stride + (int64_t)hv * DV + j0 + j;
-                        if constexpr (sizeof(OT) == 4) ((float *)a.o)[oi] = acc[v];
-                        else ((uint16_t *)a.o)[oi] = gd_f2h(acc[v]);
-                    }
+                    const uint32_t oo =
+                            ((uint32_t)(tb + kg * 4 + v) * (uint32_t)a.o_stride + obase + j) * sizeof(OT);
+                    if constexpr (sizeof(OT) == 4)
+                        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[v]), ors, oo, 0, 0);
+                    else
+                        __builtin_amdgcn_raw_buffer_store_b16(gd_f2h(acc[v]), ors, oo, 0, 0);
                 }
             }
         }
+        loadQP(c + 1);
 
         // S <- e^{G_L} S + K^T (e^{G_L - G} delta): rows 32*wave .. +31.
         const float decay = expf(gl);
@@ -502,18 +567,13 @@ __global__ __launch_bounds__(256) void gdn_scan(ScanArgs a) {
                 for (int v = 0; v < 4; v++) Sf[ib + kg * 4 + v][j] = acc[v];
             }
         }
+        loadK(c + 1);
     };
 
-    // Two operand sets alternate (a copy would wait for its loads).
-    ScanChunk<CP> A, B;
-    load(0, A);
-    for (int c = 0; c < a.nchunks; c += 2) {
-        load(c + 1, B);
-        process(c, A);
-        if (c + 1 >= a.nchunks) break;
-        load(c + 2, A);
-        process(c + 1, B);
-    }
+    loadW(0);
+    loadQP(0);
+    loadK(0);
+    for (int c = 0; c < a.nchunks; c++) process(c);
     __syncthreads();
     for (int e = tid; e < DK * NCOL; e += 256) {
         const int i = e / NCOL, j = e % NCOL;
@@ -559,6 +619,9 @@ extern "C" int gd_gdn_prefill(gd_ctx *ctx, int64_t T, int nV, int nK, int dk, in
     GD_REQUIRE(ctx, q_stride >= (int64_t)nK * dk && k_stride >= (int64_t)nK * dk &&
                         v_stride >= (int64_t)nV * dv && o_stride >= (int64_t)nV * dv,
                "gd_gdn_prefill: strides smaller than a token row");
+    // A chunk's output rows are stored through one 32-bit buffer range.
+    GD_REQUIRE(ctx, o_stride <= (1 << 24), "gd_gdn_prefill: o_stride %lld above 2^24",
+               (long long)o_stride);
     // Rows are read 8 elements at a time.
     const int vec = io_dtype == GD_F16 ? 8 : 4;
     const int esz = io_dtype == GD_F16 ? 2 : 4;

@@ -569,11 +569,9 @@ __global__ __launch_bounds__(1024) void k_add_rmsnorm(float *x, const float *y, 
     for (int i = threadIdx.x * 4; i < n; i += blockDim.x * 4) {
         const f32x4 a = *(const f32x4 *)(xr + i);
         const f32x4 ww = *(const f32x4 *)(w + i);
-        uint16_t *o = out + row * n + i;
-        o[0] = gd_f2h(a[0] * s * ww[0]);
-        o[1] = gd_f2h(a[1] * s * ww[1]);
-        o[2] = gd_f2h(a[2] * s * ww[2]);
-        o[3] = gd_f2h(a[3] * s * ww[3]);
+        const uint32_t lo = (uint32_t)gd_f2h(a[0] * s * ww[0]) | ((uint32_t)gd_f2h(a[1] * s * ww[1]) << 16);
+        const uint32_t hi = (uint32_t)gd_f2h(a[2] * s * ww[2]) | ((uint32_t)gd_f2h(a[3] * s * ww[3]) << 16);
+        *(u32x2 *)(out + row * n + i) = u32x2{lo, hi};   // n % 4 == 0: 8-byte aligned
     }
 }
 
