@@ -21,13 +21,14 @@
 //     those subnormals (measured), while 4, 6 and 8 stay within about 1e-6
 //     of the exact sum.  A block whose x would overflow f16 after the x16
 //     pre-scale is staged scaled down by a power of two 2^-e, undone later.
-//   * B operand: each MFMA block has four output columns; at chunk step s the
-//     x of its Q2 block goes into column s % 4 and the other columns get
-//     zeros.  x is staged once per workgroup in LDS, already permuted into
-//     the (k, k+8) pair order of the unpack and pre-scaled, with zero blocks
-//     for the other columns.  f32 x is split into hi = f16(x) and
-//     lo = f16((x - hi) * 2^11), two B operands accumulated apart and
-//     recombined in f32.
+//   * B operand: every lane reads the staged x of its own Q2 block, so the
+//     four output columns of an MFMA block hold the same products and
+//     column 0 is used (the lanes of one block read one LDS address, which
+//     the LDS broadcasts).  x is staged once per workgroup in LDS, already
+//     permuted into the (k, k+8) pair order of the unpack and pre-scaled,
+//     with zero blocks past the last one for a short final step.  f32 x is
+//     split into hi = f16(x) and lo = f16((x - hi) * 2^11), two B operands
+//     accumulated apart and recombined in f32.
 //   * Work split.  A "set" is one 16-row group; an "item" is one tile (one
 //     chunk step of 512 K of one set).  Every workgroup gets the same number
 //     of consecutive sets (and, with a K split, one range of steps).  Its
