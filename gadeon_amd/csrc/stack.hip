@@ -335,17 +335,29 @@ __global__ __launch_bounds__(256) void k_attn_prefill(
     float m = -INFINITY, l = 0.f;                         // this lane's keys only
     const int last = pos0 + min(q0 + AQ, N) - 1;          // last key any query here needs
     // Staging: thread t loads 16 dims (d0 .. d0+15) of key t / 8 of the block.
+    // The loads run ahead of the arithmetic: block k0 + AK's K and V rows are
+    // requested before block k0's MFMAs, and the page-table entry they need
+    // one block earlier still, so no block waits for a memory round trip
+    // (blocks past `last` clamp to it: loaded, never used).
     const int sk = t >> 3, d0 = (t & 7) * 16;
+    auto page_of = [&](int k0) { return page_table[min(k0 + sk, last) / block]; };
+    u32x4 kv[4];                                          // K lo, K hi, V lo, V hi
+    auto fetch = [&](int k0, int page) {
+        const int p = min(k0 + sk, last);
+        const int64_t base = ((int64_t)page * block + p % block) * kvDim + kvh * HD + d0;
+        kv[0] = *(const u32x4 *)(kc + base);
+        kv[1] = *(const u32x4 *)(kc + base + 8);
+        kv[2] = *(const u32x4 *)(vc + base);
+        kv[3] = *(const u32x4 *)(vc + base + 8);
+    };
+    fetch(0, page_of(0));
+    int page_next = page_of(AK);
     for (int k0 = 0; k0 <= last; k0 += AK) {
         __syncthreads();
         {
-            const int p = min(k0 + sk, last);
-            const int64_t base = kv_slot(page_table, p, block) * kvDim + kvh * HD + d0;
-            const u32x4 k_lo = *(const u32x4 *)(kc + base), k_hi = *(const u32x4 *)(kc + base + 8);
-            const u32x4 v_lo = *(const u32x4 *)(vc + base), v_hi = *(const u32x4 *)(vc + base + 8);
-            *(u32x4 *)&Ks[sk][d0] = k_lo;
-            *(u32x4 *)&Ks[sk][d0 + 8] = k_hi;
-            const f16x8 va = __builtin_bit_cast(f16x8, v_lo), vb = __builtin_bit_cast(f16x8, v_hi);
+            *(u32x4 *)&Ks[sk][d0] = kv[0];
+            *(u32x4 *)&Ks[sk][d0 + 8] = kv[1];
+            const f16x8 va = __builtin_bit_cast(f16x8, kv[2]), vb = __builtin_bit_cast(f16x8, kv[3]);
 #pragma unroll
             for (int e = 0; e < 8; e++) {
                 Vt[d0 + e][sk] = va[e];
@@ -353,6 +365,11 @@ __global__ __launch_bounds__(256) void k_attn_prefill(
             }
         }
         __syncthreads();
+        fetch(k0 + AK, page_next);
+        page_next = page_of(k0 + 2 * AK);
+        // Keep the loads here: the compiler would sink them below the MFMAs,
+        // next to the LDS writes that wait for them.
+        __builtin_amdgcn_sched_barrier(0);
         // S^T tiles kt = 0, 1: keys 16 kt + 4 g + v for query lq.
         f32x4 sc[2];
 #pragma unroll
