@@ -34,15 +34,6 @@ constexpr int HD = 128;   // head_dim / d_state handled by the fused kernels
 
 // beta = sigmoid(bPre), g = softplus(aPre + dt) * aNeg, reading the pre-
 // activations out of the fused projection rows (GDN.swift:39-42).
-__global__ void k_gate(const float *proj, int64_t stride, int off_b, int off_a, const float *dt,
-                       const float *aNeg, float *beta, float *g, int nV, int N) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= N * nV) return;
-    const int n = i / nV, h = i % nV;
-    const float *row = proj + (int64_t)n * stride;
-    beta[i] = gd_sigmoid(row[off_b + h]);
-    g[i] = gd_softplus(row[off_a + h] + dt[h]) * aNeg[h];
-}
 
 // Causal depthwise conv (dConv = 4) + silu over N tokens of the strided qkv
 // rows, ring in registers (GDN.swift:44-62).
@@ -65,40 +56,91 @@ __global__ void k_conv4(const float *proj, int64_t stride, float *ring, const fl
     ring[c] = r0; ring[convDim + c] = r1; ring[2 * convDim + c] = r2;
 }
 
-// The same conv for a whole prefill chunk, parallel over (token, channel): a
-// causal FIR reads the ring only for the first dConv-1 tokens.  The ring is
-// advanced afterwards by k_conv4_ring (a separate launch, so no token reads a
-// ring entry that is being overwritten).
-__global__ void k_conv4_fir(const float *proj, int64_t stride, const float *ring,
-                            const float *cw, float *out, int convDim, int N) {
-    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (e >= (int64_t)N * convDim) return;
-    const int n = (int)(e / convDim), c = (int)(e % convDim);
-    float in[4];
+// The GDN layer's prefill front end in one launch: causal conv + silu of
+// every conv channel (Kernels.metal:1490-1520), the L2 norm of each q and k
+// head row (Kernels.swift:41-52), the gates beta = sigmoid(b) and
+// g = softplus(a + dt) * aNeg (GDN.swift:39-42), and the advance of the conv
+// ring.  Wave task (row r of 128 channels, CT tokens n0 ..): lane l holds
+// channels 128r + l and 128r + 64 + l and slides a window over the token
+// rows n0-3 .. n0+CT-1.  Only the wave of the first tokens of a row reads the ring
+// (earlier tokens than 0), so it alone writes the new ring, after its reads.
+// The row-0 waves also compute the gates of their tokens.
+constexpr int CT = 4;                        // tokens per wave task
+static_assert(CT >= 3, "only the first task of a row may reach back into the ring");
+__global__ __launch_bounds__(256) void k_gdn_conv_prefill(
+        const float *proj, int64_t stride, float *ring, const float *cw, float *out,
+        int convDim, int nqk_rows, int N, float eps, int off_b, int off_a, const float *dt,
+        const float *aNeg, float *beta, float *g, int nV) {
+    const int nrows = convDim / HD;
+    const int64_t task = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int ngroups = (N + CT - 1) / CT;
+    if (task >= (int64_t)nrows * ngroups) return;
+    const int r = (int)(task % nrows), n0 = (int)(task / nrows) * CT;
+    const int lane = threadIdx.x & 63;
+    const int c[2] = {r * HD + lane, r * HD + 64 + lane};
+    float w[2][4], win[2][CT + 3];
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int m = n - 3 + j;                 // token index of window slot j
-        in[j] = m >= 0 ? proj[(int64_t)m * stride + c] : ring[(int64_t)(3 + m) * convDim + c];
+    for (int h = 0; h < 2; h++) {
+        const f32x4 wv = *(const f32x4 *)(cw + (int64_t)c[h] * 4);
+        w[h][0] = wv[0]; w[h][1] = wv[1]; w[h][2] = wv[2]; w[h][3] = wv[3];
+#pragma unroll
+        for (int j = 0; j < CT + 3; j++) {
+            const int m = n0 - 3 + j;            // token of window slot j
+            win[h][j] = m < 0 ? ring[(int64_t)(3 + m) * convDim + c[h]]
+                      : m < N ? proj[(int64_t)m * stride + c[h]] : 0.f;
+        }
     }
-    float acc = 0.0f;
-    acc += in[0] * cw[c * 4];
-    acc += in[1] * cw[c * 4 + 1];
-    acc += in[2] * cw[c * 4 + 2];
-    acc += in[3] * cw[c * 4 + 3];
-    out[e] = gd_silu(acc);
-}
-
-__global__ void k_conv4_ring(const float *proj, int64_t stride, float *ring, int convDim, int N) {
-    const int c = blockIdx.x * blockDim.x + threadIdx.x;
-    if (c >= convDim) return;
-    float r[3];
+    const bool norm = r < nqk_rows;
 #pragma unroll
-    for (int j = 0; j < 3; j++) {
-        const int m = N - 3 + j;
-        r[j] = m >= 0 ? proj[(int64_t)m * stride + c] : ring[(int64_t)(3 + m) * convDim + c];
+    for (int t = 0; t < CT; t++) {
+        float v[2];
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            float acc = 0.0f;
+            acc += win[h][t] * w[h][0];
+            acc += win[h][t + 1] * w[h][1];
+            acc += win[h][t + 2] * w[h][2];
+            acc += win[h][t + 3] * w[h][3];
+            v[h] = gd_silu(acc);
+        }
+        if (norm) {                              // wave-uniform
+            float ss = 0.0f;
+            ss += v[0] * v[0];
+            ss += v[1] * v[1];
+            ss = gd_wave_sum(ss);
+            const float sc = 1.0f / sqrtf(ss + eps);
+            v[0] *= sc;
+            v[1] *= sc;
+        }
+        if (n0 + t < N) {
+            out[(int64_t)(n0 + t) * convDim + c[0]] = v[0];
+            out[(int64_t)(n0 + t) * convDim + c[1]] = v[1];
+        }
     }
+    if (n0 == 0) {
+        // New ring: the inputs of tokens N-3 .. N-1, the old ring where those
+        // precede token 0 (in win: slot j holds token j - 3).
 #pragma unroll
-    for (int j = 0; j < 3; j++) ring[(int64_t)j * convDim + c] = r[j];
+        for (int h = 0; h < 2; h++) {
+            float nr[3];
+#pragma unroll
+            for (int j = 0; j < 3; j++) {
+                const int m = N - 3 + j;
+                nr[j] = m < 0 ? win[h][3 + m] : proj[(int64_t)m * stride + c[h]];
+            }
+#pragma unroll
+            for (int j = 0; j < 3; j++) ring[(int64_t)j * convDim + c[h]] = nr[j];
+        }
+    }
+    if (r == 0) {
+        for (int i = lane; i < CT * nV; i += 64) {
+            const int n = n0 + i / nV, hh = i % nV;
+            if (n >= N) break;
+            const float *row = proj + (int64_t)n * stride;
+            beta[(int64_t)n * nV + hh] = gd_sigmoid(row[off_b + hh]);
+            g[(int64_t)n * nV + hh] = gd_softplus(row[off_a + hh] + dt[hh]) * aNeg[hh];
+        }
+    }
 }
 
 // o <- rmsnorm_d(o) * w * silu(z), written as f16 for the out projection
@@ -722,13 +764,10 @@ int forward(gd_stack *st, int N, bool decode) {
                                  GD_F32, st->proj + off_a, st->proj + off_b, ly.dt, ly.a_neg,
                                  ly.rec_state, st->o32, qScale, eps));
             } else {
-                K_(k_conv4_fir, dim3(gd_blocks((int64_t)N * st->convDim, 256)), dim3(256), 0, s,
-                   st->proj, (int64_t)RP, ly.conv_state, ly.conv_w, st->conv_out, st->convDim, N);
-                K_(k_conv4_ring, dim3(gd_blocks(st->convDim, 256)), dim3(256), 0, s, st->proj,
-                   (int64_t)RP, ly.conv_state, st->convDim, N);
-                K_(k_gate, dim3(gd_blocks((int64_t)N * nV, 256)), dim3(256), 0, s, st->proj,
-                   (int64_t)RP, off_b, off_a, ly.dt, ly.a_neg, st->beta, st->g, nV, N);
-                R_(gd_l2norm_rows(ctx, st->conv_out, c.d_state, 2 * nK, st->convDim, N, eps));
+                const int64_t tasks = (int64_t)(st->convDim / HD) * ((N + CT - 1) / CT);
+                K_(k_gdn_conv_prefill, dim3(gd_blocks(tasks, 4)), dim3(256), 0, s, st->proj,
+                   (int64_t)RP, ly.conv_state, ly.conv_w, st->conv_out, st->convDim, 2 * nK, N, eps,
+                   off_b, off_a, ly.dt, ly.a_neg, st->beta, st->g, nV);
                 R_(gd_gdn_prefill(ctx, N, nV, nK, c.d_state, c.d_state, st->conv_out,
                                   st->convDim, st->conv_out + st->keyDim, st->convDim,
                                   st->conv_out + 2 * st->keyDim, st->convDim, GD_F32, st->g,

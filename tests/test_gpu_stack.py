@@ -3,7 +3,7 @@ token-by-token CPU restatement of BonsaiEngine / GDN.step / Attn.step, on a
 small random-init geometry: 4 layers (3 GDN + 1 gated attention), GQA on both
 the GDN heads (4 value / 2 key) and the attention heads (4 q / 2 kv), a
 40-token prompt over two prefill chunks (32 + 8, crossing KV pages of 16),
-then decode steps and graph-replayed generation.
+then decode steps and graph-replayed generation (also a 34-token prompt, 32 + 2).
 
 The oracle stages every mat-vec input and cached K/V in f16, as the
 reference's GPU path does (Kernels.metal:428, MetalKVPool.swift); the GPU
@@ -60,8 +60,11 @@ def margin_ok(logits):
     return top[1] - top[0] > 1e-2 * max(1.0, np.abs(logits).max())
 
 
-@pytest.mark.parametrize("nk", [2, 4])   # 4: every value head has its own key head
-def test_stack_prefill_decode_generate(ctx, nk):
+# nk = 4: every value head has its own key head.  A 34-token prompt ends with
+# a 2-token chunk, shorter than the conv window: its new conv ring mixes the
+# old ring with the chunk's inputs.
+@pytest.mark.parametrize("nk,plen", [(2, 40), (4, 40), (4, 34)])
+def test_stack_prefill_decode_generate(ctx, nk, plen):
     """nk = 2 shares key heads between value heads (separate conv, step and
     gated-norm kernels in decode); nk = 4 takes the fused one-launch step."""
     cfg, st = make_stack(ctx, n_k_head=nk)
@@ -69,7 +72,7 @@ def test_stack_prefill_decode_generate(ctx, nk):
     try:
         read = tensor_reader(ctx, st)
         ref = O.Stack(cfg, read, stage_f16=True, threads=8)
-        ids = (np.arange(40) * 37 % cfg["n_vocab"]).astype(np.int32)
+        ids = (np.arange(plen) * 37 % cfg["n_vocab"]).astype(np.int32)
         nxt = C.c_int32()
         logits = np.empty(cfg["n_vocab"], np.float32)
         ctx.check(lib.gd_stack_prefill(st, ids.ctypes.data, ids.size, C.byref(nxt),
@@ -91,7 +94,7 @@ def test_stack_prefill_decode_generate(ctx, nk):
             tok = int(np.argmax(ref_logits))
         pos = C.c_int64()
         ctx.check(lib.gd_stack_position(st, C.byref(pos)))
-        assert pos.value == 46
+        assert pos.value == plen + 6
         # Graph-replayed generation continues from the GPU's last pick.
         gen = np.empty(5, np.int32)
         tok = nxt.value
