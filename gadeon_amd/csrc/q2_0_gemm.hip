@@ -94,15 +94,17 @@ template <int MT, int NT, int NW> struct Stage {
 // blocks (128 K)
 // [z * bps, min((z+1) * bps, K/128)) of K for split z.  X is f16.  YT: 0 =
 // f32, 1 = f16.  With nz > 1 the output is f32 partials at Y + z * T * R.
-// glu_ff > 0 (NT = 1, one split): W is [gate; up] with glu_ff rows each and
-// the output is SwiGLU, Yv[t][r] = f16(silu(gate_r . x_t) * (up_r . x_t)),
-// r < glu_ff: lanes 0..15 of a wave's fragment take gate rows g .. g+15 and
-// lanes 16..31 up rows glu_ff + g .., so one shuffle pairs them.
+// glu_ff > 0 (one split): W is [gate; up] with glu_ff rows each and the
+// output is SwiGLU, Yv[t][r] = f16(silu(gate_r . x_t) * (up_r . x_t)) for
+// the columns glu_r0 <= r < glu_end of this launch (Yv has glu_ff columns):
+// lanes 0..15 of a wave's fragment take gate rows g .. g+15 and lanes
+// 16..31 up rows glu_ff + g .., so one shuffle pairs them; each wave holds
+// NT such fragments.
 template <int MT, int NT, int NW, int YT>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) void q2_0_gemm_kernel(
         const uint8_t *__restrict__ codes, const uint16_t *__restrict__ scales,
         const void *__restrict__ Xv, void *__restrict__ Yv, int T, int K, int R, int bps,
-        int nrt, int nz, int per, int glu_ff) {
+        int nrt, int nz, int per, int glu_ff, int glu_r0, int glu_end) {
     using St = Stage<MT, NT, NW>;
     constexpr int BT = St::BT;
     __shared__ __attribute__((aligned(16))) uint8_t lds[2 * St::BYTES];
@@ -118,8 +120,9 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int li = lane & 31, lh = lane >> 5;
     const int t0 = tt * BT;
-    // This wave's first row (SwiGLU: first gate row, 16 per wave).
-    const int rw = glu_ff ? rt * (16 * NW) + wave * 16 : rt * (NW * NT * 32) + wave * (NT * 32);
+    // This wave's first row (SwiGLU: first gate row, 16 per fragment).
+    const int rw = glu_ff ? glu_r0 + rt * (16 * NW * NT) + wave * (16 * NT)
+                          : rt * (NW * NT * 32) + wave * (NT * 32);
     const int nblk = K >> 7;
     const int csteps = (nblk + 3) >> 2;
     const int bgroups = (nblk + 15) >> 4;
@@ -132,7 +135,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
     const __amdgpu_buffer_rsrc_t xrs =
             gd_rsrc((const char *)Xv + (size_t)t0 * K * 2, (uint32_t)min(BT, T - t0) * K * 2);
     const int g0 = rw >> 4, rgroups = (R + 15) >> 4;
-    const uint32_t gvalid = (uint32_t)max(0, min(glu_ff ? (glu_ff >> 4) + 1 : 2 * NT, rgroups - g0));
+    const uint32_t gvalid = (uint32_t)max(0, min(glu_ff ? (glu_ff >> 4) + NT : 2 * NT, rgroups - g0));
     const __amdgpu_buffer_rsrc_t crs =
             gd_rsrc(codes + ((size_t)g0 * csteps << 11), gvalid * (uint32_t)csteps * 2048u);
     const __amdgpu_buffer_rsrc_t srs =
@@ -156,7 +159,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
     uint32_t cvo[NT], svo[NT];
 #pragma unroll
     for (int n = 0; n < NT; n++) {
-        const int g = glu_ff ? ((li >> 4) ? (glu_ff >> 4) : 0) : 2 * n + (li >> 4);
+        const int g = glu_ff ? n + ((li >> 4) ? (glu_ff >> 4) : 0) : 2 * n + (li >> 4);
         cvo[n] = ((uint32_t)(g * csteps) << 11) + ((uint32_t)lh << 10) + ((li & 15) << 4);
         svo[n] = ((uint32_t)g * bgroups * 256 + (li & 15)) * 2;
     }
@@ -266,25 +269,28 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
         // (the first half v < 8, the second v >= 8), trading one shuffle
         // per pair of values.
         const bool gl = li < 16;
-        const int g = rw + (li & 15);
         const __amdgpu_buffer_rsrc_t ors =
                 gd_rsrc((uint16_t *)Yv + (size_t)t0 * glu_ff, (uint32_t)rows_t * glu_ff * 2u);
-        const uint32_t obase = ((uint32_t)(4 * lh + (gl ? 0 : 16)) * glu_ff + g) * 2u;
-        if (g < glu_ff) {
 #pragma unroll
-            for (int m = 0; m < MT; m++)
+        for (int n = 0; n < NT; n++) {
+            const int g = rw + 16 * n + (li & 15);
+            const uint32_t obase = ((uint32_t)(4 * lh + (gl ? 0 : 16)) * glu_ff + g) * 2u;
+            if (g < glu_end) {
 #pragma unroll
-                for (int q = 0; q < 8; q++) {
-                    // Both elements first, then a select: a lane-dependent
-                    // index would compile to a 16-way select chain.
-                    const float lo = acc[m][0][q], hi = acc[m][0][8 + q];
-                    const float other = __shfl_xor(gl ? hi : lo, 16, 64);
-                    const float mine = gl ? lo : hi;
-                    const float gate = gl ? mine : other, up = gl ? other : mine;
-                    const float sg = gate * __builtin_amdgcn_rcpf(1.0f + __expf(-gate));
-                    const uint32_t so = (uint32_t)(m * 32 + 8 * (q >> 2) + (q & 3)) * glu_ff * 2u;
-                    __builtin_amdgcn_raw_buffer_store_b16(gd_f2h(sg * up), ors, obase + so, 0, 0);
-                }
+                for (int m = 0; m < MT; m++)
+#pragma unroll
+                    for (int q = 0; q < 8; q++) {
+                        // Both elements first, then a select: a lane-dependent
+                        // index would compile to a 16-way select chain.
+                        const float lo = acc[m][n][q], hi = acc[m][n][8 + q];
+                        const float other = __shfl_xor(gl ? hi : lo, 16, 64);
+                        const float mine = gl ? lo : hi;
+                        const float gate = gl ? mine : other, up = gl ? other : mine;
+                        const float sg = gate * __builtin_amdgcn_rcpf(1.0f + __expf(-gate));
+                        const uint32_t so = (uint32_t)(m * 32 + 8 * (q >> 2) + (q & 3)) * glu_ff * 2u;
+                        __builtin_amdgcn_raw_buffer_store_b16(gd_f2h(sg * up), ors, obase + so, 0, 0);
+                    }
+            }
         }
         return;
     }
@@ -335,7 +341,7 @@ __global__ __launch_bounds__(256) void q2_0_gemm_reduce(const float *__restrict_
 }
 
 typedef void (*gemm_fn)(const uint8_t *, const uint16_t *, const void *, void *, int, int, int,
-                        int, int, int, int, int);
+                        int, int, int, int, int, int, int);
 
 template <int MT, int NT, int NW>
 gemm_fn pick(int yt) {
@@ -352,6 +358,7 @@ gemm_fn kernel_for(int mt, int nt, int nw, int yt) {
         if (mt == 4 && nt == 1) return pick<4, 1, 4>(yt);
         if (mt == 2 && nt == 2) return pick<2, 2, 4>(yt);
         if (mt == 2 && nt == 1) return pick<2, 1, 4>(yt);
+        if (mt == 1 && nt == 1) return pick<1, 1, 4>(yt);
     } else if (nw == 8) {
         if (mt == 4 && nt == 2) return pick<4, 2, 8>(yt);
         if (mt == 4 && nt == 1) return pick<4, 1, 8>(yt);
@@ -375,6 +382,28 @@ __global__ __launch_bounds__(256) void gemm_x_to_f16(const float *__restrict__ X
 }  // namespace
 
 int gd_check_q2w(gd_ctx *ctx, const gd_q2w *w, const char *who);
+
+namespace {
+
+// Measured per-CU times of every tile (us per 128-K block of a round with
+// k = 1, 2, 3 resident workgroups; `occ` of them fit on a CU).
+struct Shape { int mt, nt, nw, occ; double t[3]; };
+constexpr Shape SHAPES[9] = {{1, 1, 4, 3, {0.660, 1.000, 1.390}},
+                             {2, 1, 4, 3, {0.600, 1.016, 1.571}}, {4, 1, 4, 2, {1.124, 1.762, 0}},
+                             {2, 2, 4, 3, {1.133, 1.866, 2.701}}, {4, 2, 4, 1, {1.807, 0, 0}},
+                             {2, 1, 8, 2, {0.978, 1.760, 0}},     {4, 1, 8, 1, {1.524, 0, 0}},
+                             {2, 2, 8, 1, {1.763, 0, 0}},         {4, 2, 8, 1, {2.497, 0, 0}}};
+
+// Time of `units` workgroups of tile sh dealt evenly over the CUs, each
+// running bps blocks: the busiest CU runs ceil(units / CUs) of them, occ at
+// a time.
+double round_cost(const Shape &sh, int64_t units, int cus, int bps) {
+    const int64_t n = (units + cus - 1) / cus;
+    const int64_t q = n / sh.occ, r = n % sh.occ;
+    return bps * (q * sh.t[sh.occ - 1] + (r ? sh.t[r - 1] : 0.0));
+}
+
+}  // namespace
 
 // Tile shape, waves per workgroup and K split for a T x K x R product, from
 // a cost model fitted to MI355X timings of every plan on the stack's six
@@ -403,23 +432,16 @@ gd_gemm_plan gd_gemm_choose(gd_ctx *ctx, int64_t T, int64_t K, int64_t R, int x_
             return gd_gemm_plan{mt, nt, nz_of(s), nw};
     }
     const int cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
-    struct Shape { int mt, nt, nw, occ; double t[3]; };
-    const Shape shapes[8] = {{2, 1, 4, 3, {0.600, 1.016, 1.571}}, {4, 1, 4, 2, {1.124, 1.762, 0}},
-                             {2, 2, 4, 3, {1.133, 1.866, 2.701}}, {4, 2, 4, 1, {1.807, 0, 0}},
-                             {2, 1, 8, 2, {0.978, 1.760, 0}},     {4, 1, 8, 1, {1.524, 0, 0}},
-                             {2, 2, 8, 1, {1.763, 0, 0}},         {4, 2, 8, 1, {2.497, 0, 0}}};
     constexpr double CS = 0.162;                        // us per MB of split partials
     gd_gemm_plan best{4, 1, 1};
     double best_cost = 1e30;
-    for (const Shape &sh : shapes) {
+    for (const Shape &sh : SHAPES) {
         const int64_t tiles = ((T + sh.mt * 32 - 1) / (sh.mt * 32)) *
                               ((R + sh.nw * sh.nt * 32 - 1) / (sh.nw * sh.nt * 32));
         for (int s = 1; s <= 8; s++) {
             const int bps = (nblk + s - 1) / s, nz = (nblk + bps - 1) / bps;
             if (nz < s) break;                            // no more distinct splits
-            const int64_t n = (tiles * nz + cus - 1) / cus;
-            const int64_t q = n / sh.occ, r = n % sh.occ;
-            double cost = bps * (q * sh.t[sh.occ - 1] + (r ? sh.t[r - 1] : 0.0));
+            double cost = round_cost(sh, tiles * nz, cus, bps);
             if (nz > 1) cost += CS * (2.0 * nz + 1) * (double)T * R * 4 / 1e6;
             if (cost < best_cost) {
                 best_cost = cost;
@@ -446,28 +468,68 @@ int gd_gemm_launch(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, int x
     const int64_t units = (int64_t)gd_blocks(T, p.mt * 32) * nz * nrt;
     const int per = (int)((units + 7) / 8);
     hipLaunchKernelGGL(f, dim3(8 * per), dim3(64 * p.nw), 0, ctx->stream, (const uint8_t *)w->codes,
-                       (const uint16_t *)w->scales, X, Y, (int)T, K, R, bps, nrt, nz, per, 0);
+                       (const uint16_t *)w->scales, X, Y, (int)T, K, R, bps, nrt, nz, per, 0, 0, 0);
     GD_LAUNCHED(ctx, "q2_0_gemm");
     return GD_OK;
 }
 
 // SwiGLU GEMM: w holds [gate; up] (R = 2 * ff rows), X f16 [T][K], out f16
-// [T][ff] = silu(gate . x) * (up . x).  Tiles of 128 tokens by 64 gate rows
-// (and their 64 up rows), K unsplit.
+// [T][ff] = silu(gate . x) * (up . x), K unsplit.  A tile of NW waves with
+// NT fragments each covers 16 NW NT output columns.  The columns run as one
+// launch, or as two: the largest whole rounds of one tile (the big tiles
+// are the fastest per FLOP, but ff = 17408 = 17 * 2^10 never fills whole
+// rounds of them) and the rest with another -- whichever the cost model
+// (the GEMM planner's measured tile times, plus ~2 us for a second launch)
+// finds cheaper.  GADEON_GLU_CFG="MT,NT,NW" forces one launch of that tile.
 int gd_gemm_glu(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, uint16_t *out) {
     const int K = (int)w->K, R = (int)w->R, ff = R / 2;
     GD_REQUIRE(ctx, R % 32 == 0 && T > 0 && K % 128 == 0 && R < (1 << 22), "gd_gemm_glu: R=%d "
                "must hold two halves of 16-row groups (and be below 4194304)", R);
-    // Four waves: eight (one workgroup per CU) measured 7% slower here.
-    constexpr int nw = 4;
-    gemm_fn f = kernel_for(4, 1, nw, 0);
-    const int nrt = gd_blocks(ff, 16 * nw);
-    const int64_t units = (int64_t)gd_blocks(T, 128) * nrt;
-    const int per = (int)((units + 7) / 8);
-    hipLaunchKernelGGL(f, dim3(8 * per), dim3(64 * nw), 0, ctx->stream, (const uint8_t *)w->codes,
-                       (const uint16_t *)w->scales, X, (void *)out, (int)T, K, R, K / 128, nrt, 1,
-                       per, ff);
-    GD_LAUNCHED(ctx, "q2_0_gemm_glu");
+    const int nblk = K / 128;
+    const int cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
+    auto cols = [](const Shape &sh) { return 16 * sh.nw * sh.nt; };
+    auto tiles_t = [&](const Shape &sh) { return (T + sh.mt * 32 - 1) / (sh.mt * 32); };
+    auto cost = [&](const Shape &sh, int ncols) {
+        return round_cost(sh, tiles_t(sh) * ((ncols + cols(sh) - 1) / cols(sh)), cus, nblk);
+    };
+    struct Part { const Shape *sh; int r0, r1; };
+    Part parts[2] = {{nullptr, 0, ff}, {nullptr, ff, ff}};
+    double best = 1e30;
+    static const char *force = getenv("GADEON_GLU_CFG");
+    int fmt = 0, fnt = 0, fnw = 0;
+    const bool forced = force && sscanf(force, "%d,%d,%d", &fmt, &fnt, &fnw) == 3;
+    for (const Shape &a : SHAPES) {
+        if (forced && !(a.mt == fmt && a.nt == fnt && a.nw == fnw)) continue;
+        const double c1 = cost(a, ff);
+        if (c1 < best) { best = c1; parts[0] = {&a, 0, ff}; parts[1] = {nullptr, ff, ff}; }
+        if (forced) continue;
+        // Whole rounds of a: rounds * CUs * occ units of tiles_t(a) token tiles each.
+        const int64_t per_round = (int64_t)cus * a.occ;
+        if (per_round % tiles_t(a)) continue;
+        const int64_t colt = per_round / tiles_t(a) * cols(a);   // columns per round
+        const int main_cols = (int)(ff / colt * colt);
+        if (main_cols == 0 || main_cols == ff) continue;
+        for (const Shape &b : SHAPES) {
+            const double c2 = cost(a, main_cols) + cost(b, ff - main_cols) + 2.0;
+            if (c2 < best) {
+                best = c2;
+                parts[0] = {&a, 0, main_cols};
+                parts[1] = {&b, main_cols, ff};
+            }
+        }
+    }
+    GD_REQUIRE(ctx, parts[0].sh, "gd_gemm_glu: no tile for GADEON_GLU_CFG=%s", force ? force : "");
+    for (const Part &pt : parts) {
+        if (!pt.sh || pt.r1 <= pt.r0) continue;
+        gemm_fn f = kernel_for(pt.sh->mt, pt.sh->nt, pt.sh->nw, 0);
+        const int nrt = gd_blocks(pt.r1 - pt.r0, cols(*pt.sh));
+        const int64_t units = tiles_t(*pt.sh) * nrt;
+        const int per = (int)((units + 7) / 8);
+        hipLaunchKernelGGL(f, dim3(8 * per), dim3(64 * pt.sh->nw), 0, ctx->stream,
+                           (const uint8_t *)w->codes, (const uint16_t *)w->scales, X, (void *)out,
+                           (int)T, K, R, nblk, nrt, 1, per, ff, pt.r0, pt.r1);
+        GD_LAUNCHED(ctx, "q2_0_gemm_glu");
+    }
     return GD_OK;
 }
 

@@ -184,10 +184,11 @@ int gd_q2_0_gemm(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X,
                  int x_dtype, void *Y, int y_dtype);
 
 /* gd_q2_0_gemm with an explicit plan: workgroups of nw waves (4 or 8), each
- * wave mt*32 tokens by nt*32 weight rows, (mt, nt) in {(2,1), (4,1), (2,2),
- * (4,2), (8,1)} ((8,1) with 4 waves only), and K split `split` ways (1..16;
- * partials summed in the context workspace).  For tuning and for tests that
- * cover every kernel variant; no counterpart in the reference. */
+ * wave mt*32 tokens by nt*32 weight rows, (mt, nt) in {(1,1), (2,1), (4,1),
+ * (2,2), (4,2), (8,1)} ((1,1) and (8,1) with 4 waves only), and K split
+ * `split` ways (1..16; partials summed in the context workspace).  For
+ * tuning and for tests that cover every kernel variant; no counterpart in
+ * the reference. */
 int gd_q2_0_gemm_plan(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X,
                       int x_dtype, void *Y, int y_dtype, int mt, int nt, int split, int nw);
 

@@ -245,7 +245,7 @@ def test_gemm_vs_oracle(ctx, T, K, R, xt, yt):
 
 
 # (mt, nt, waves per workgroup): every kernel the planner can pick.
-PLANS_F16 = [(2, 1, 4), (4, 1, 4), (2, 2, 4), (4, 2, 4), (8, 1, 4),
+PLANS_F16 = [(1, 1, 4), (2, 1, 4), (4, 1, 4), (2, 2, 4), (4, 2, 4), (8, 1, 4),
              (2, 1, 8), (4, 1, 8), (2, 2, 8), (4, 2, 8)]
 PLANS_F32 = PLANS_F16                   # f32 X is rounded to f16 once, then any tile
 
@@ -279,11 +279,15 @@ def silu(v):
     return v / (1.0 + np.exp(-v))
 
 
-@pytest.mark.parametrize("T,K,ff", [(512, 5120, 17408), (37, 1024, 208), (1, 256, 16)])
+@pytest.mark.parametrize("T,K,ff", [(512, 5120, 17408), (512, 256, 17408), (37, 1024, 208),
+                                    (1, 256, 16)])
 def test_gemm_swiglu_vs_oracle(ctx, T, K, ff):
     """SwiGLU epilogue: f16(silu(X gate^T) * (X up^T)) against the oracle
     GEMV rows (ragged T and ff = 208, 13 groups of 16, exercise partial
-    tiles); the full-size case samples 64 gate rows."""
+    tiles).  At T=512, ff=17408 the columns run as two launches (16384
+    columns of 256-column tiles, then 1024 of another tile): K=256 checks
+    every column, the full-size case the launch and tile boundaries and 64
+    sampled columns."""
     R = 2 * ff
     blocks = O.lcg_q2_0(K, R, K + ff)
     w = upload_w(ctx, blocks, K, R)
@@ -291,10 +295,14 @@ def test_gemm_swiglu_vs_oracle(ctx, T, K, ff):
     dX, dO = ctx.put(Xh.view(np.uint16)), ctx.alloc(T * ff * 2)
     ctx.gd_q2_0_gemm_swiglu(C.byref(w), T, dX, dO)
     out = ctx.get(dO, (T, ff), np.float16).astype(np.float32)
-    rows = np.arange(ff) if ff <= 1024 else np.random.default_rng(3).choice(ff, 64, replace=False)
+    if ff <= 1024 or K <= 256:
+        rows = np.arange(ff)
+    else:
+        edges = [0, 15, 16, 255, 256, 16383, 16384, 16399, 17407]
+        rows = np.union1d(edges, np.random.default_rng(3).choice(ff, 64, replace=False))
     blk = blocks.reshape(R, -1)
     g = np.ascontiguousarray(blk[rows]); u = np.ascontiguousarray(blk[rows + ff])
-    toks = range(T) if T <= 64 else (0, 1, 200, T - 1)
+    toks = range(T) if T <= 64 else (0, 1, 63, 64, 127, 128, 200, 255, 256, T - 1)
     for t in toks:
         x = Xh[t].astype(np.float32)
         gv = O.q2_0_matvec(g, K, len(rows), x, threads=8)
@@ -336,7 +344,7 @@ def test_gemm_plan_rejects_unknown_tile(ctx):
     for xt in (ga.F16, ga.F32):
         with pytest.raises(RuntimeError, match="no kernel"):
             ctx.gd_q2_0_gemm_plan(C.byref(w), 4, dX, xt, dY, ga.F32, 3, 1, 1, 4)
-    for mt, nt, split, nw in ((4, 2, 0, 4), (8, 1, 1, 8), (4, 1, 1, 6)):
+    for mt, nt, split, nw in ((4, 2, 0, 4), (8, 1, 1, 8), (1, 1, 1, 8), (4, 1, 1, 6)):
         with pytest.raises(RuntimeError, match="no kernel"):
             ctx.gd_q2_0_gemm_plan(C.byref(w), 4, dX, ga.F16, dY, ga.F32, mt, nt, split, nw)
     ctx.free(dX)
