@@ -263,6 +263,30 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
     // dropped; the whole offset is in the vector operand, which the bounds
     // check covers).
     const int rows_t = min(BT, T - t0);
+    if (glu_ff && nz > 1) {
+        // K split: f32 partials P[z][t][2 n] of this launch's n = glu_end -
+        // glu_r0 columns, gate column c at c, its up partner at n + c (lane
+        // li < 16 holds gate rows, li >= 16 the up rows); q2_0_glu_reduce
+        // sums them and applies the SwiGLU.
+        const int ncol = glu_end - glu_r0;
+        const __amdgpu_buffer_rsrc_t prs = gd_rsrc(
+                (float *)Yv + ((size_t)z * T + t0) * 2 * ncol, (uint32_t)rows_t * 2u * ncol * 4u);
+#pragma unroll
+        for (int n = 0; n < NT; n++) {
+            const int c = rw + 16 * n + (li & 15) - glu_r0;
+            if (c >= ncol) continue;
+            const uint32_t pbase = ((uint32_t)(4 * lh) * 2u * ncol + (li < 16 ? c : ncol + c)) * 4u;
+#pragma unroll
+            for (int m = 0; m < MT; m++)
+#pragma unroll
+                for (int v = 0; v < 16; v++) {
+                    const uint32_t po = (uint32_t)(m * 32 + 8 * (v >> 2) + (v & 3)) * 2u * ncol * 4u;
+                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[m][n][v]), prs,
+                                                          pbase + po, 0, 0);
+                }
+        }
+        return;
+    }
     if (glu_ff) {
         // Lane li < 16 holds gate row g = rw + li, lane li + 16 the matching
         // up row: each half finishes eight of a fragment's sixteen tokens
@@ -379,6 +403,25 @@ __global__ __launch_bounds__(256) void gemm_x_to_f16(const float *__restrict__ X
     *(u32x2 *)(X16 + i) = u32x2{lo, hi};
 }
 
+// SwiGLU of K-split partials: out[t][r0 + c] = f16(silu(sum_z P[z][t][c]) *
+// sum_z P[z][t][n + c]) for c < n, partials summed in z order.  Thread per
+// (t, c).
+__global__ __launch_bounds__(256) void q2_0_glu_reduce(const float *__restrict__ P,
+                                                       uint16_t *__restrict__ out, int T, int n,
+                                                       int nz, int ff, int r0) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)T * n) return;
+    const int t = (int)(i / n), c = (int)(i % n);
+    float g = 0.f, u = 0.f;
+    for (int z = 0; z < nz; z++) {
+        const float *row = P + ((int64_t)z * T + t) * 2 * n;
+        g += row[c];
+        u += row[n + c];
+    }
+    const float sg = g * __builtin_amdgcn_rcpf(1.0f + __expf(-g));
+    out[(int64_t)t * ff + r0 + c] = gd_f2h(sg * u);
+}
+
 }  // namespace
 
 int gd_check_q2w(gd_ctx *ctx, const gd_q2w *w, const char *who);
@@ -393,6 +436,8 @@ constexpr Shape SHAPES[9] = {{1, 1, 4, 3, {0.660, 1.000, 1.390}},
                              {2, 2, 4, 3, {1.133, 1.866, 2.701}}, {4, 2, 4, 1, {1.807, 0, 0}},
                              {2, 1, 8, 2, {0.978, 1.760, 0}},     {4, 1, 8, 1, {1.524, 0, 0}},
                              {2, 2, 8, 1, {1.763, 0, 0}},         {4, 2, 8, 1, {2.497, 0, 0}}};
+
+constexpr double CS = 0.162;                            // us per MB of split partials
 
 // Time of `units` workgroups of tile sh dealt evenly over the CUs, each
 // running bps blocks: the busiest CU runs ceil(units / CUs) of them, occ at
@@ -432,7 +477,6 @@ gd_gemm_plan gd_gemm_choose(gd_ctx *ctx, int64_t T, int64_t K, int64_t R, int x_
             return gd_gemm_plan{mt, nt, nz_of(s), nw};
     }
     const int cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
-    constexpr double CS = 0.162;                        // us per MB of split partials
     gd_gemm_plan best{4, 1, 1};
     double best_cost = 1e30;
     for (const Shape &sh : SHAPES) {
@@ -489,19 +533,28 @@ int gd_gemm_glu(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, uint16_t
     const int cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
     auto cols = [](const Shape &sh) { return 16 * sh.nw * sh.nt; };
     auto tiles_t = [&](const Shape &sh) { return (T + sh.mt * 32 - 1) / (sh.mt * 32); };
-    auto cost = [&](const Shape &sh, int ncols) {
-        return round_cost(sh, tiles_t(sh) * ((ncols + cols(sh) - 1) / cols(sh)), cus, nblk);
+    // One launch of tile sh over ncols columns, K split into nz parts (the
+    // partials' round trip and the reduce launch added).
+    auto cost = [&](const Shape &sh, int ncols, int nz) {
+        const int bps = (nblk + nz - 1) / nz;
+        double c = round_cost(sh, tiles_t(sh) * ((ncols + cols(sh) - 1) / cols(sh)) * nz, cus, bps);
+        if (nz > 1) c += CS * (2.0 * nz + 1) * (double)T * 2 * ncols * 4 / 1e6 + 2.0;
+        return c;
     };
-    struct Part { const Shape *sh; int r0, r1; };
-    Part parts[2] = {{nullptr, 0, ff}, {nullptr, ff, ff}};
+    auto splits = [&](int s) {                          // distinct K splits only
+        const int bps = (nblk + s - 1) / s;
+        return (nblk + bps - 1) / bps;
+    };
+    struct Part { const Shape *sh; int r0, r1, nz; };
+    Part parts[2] = {{nullptr, 0, ff, 1}, {nullptr, ff, ff, 1}};
     double best = 1e30;
     static const char *force = getenv("GADEON_GLU_CFG");
     int fmt = 0, fnt = 0, fnw = 0;
     const bool forced = force && sscanf(force, "%d,%d,%d", &fmt, &fnt, &fnw) == 3;
     for (const Shape &a : SHAPES) {
         if (forced && !(a.mt == fmt && a.nt == fnt && a.nw == fnw)) continue;
-        const double c1 = cost(a, ff);
-        if (c1 < best) { best = c1; parts[0] = {&a, 0, ff}; parts[1] = {nullptr, ff, ff}; }
+        const double c1 = cost(a, ff, 1);
+        if (c1 < best) { best = c1; parts[0] = {&a, 0, ff, 1}; parts[1] = {nullptr, ff, ff, 1}; }
         if (forced) continue;
         // Whole rounds of a: rounds * CUs * occ units of tiles_t(a) token tiles each.
         const int64_t per_round = (int64_t)cus * a.occ;
@@ -509,26 +562,41 @@ int gd_gemm_glu(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, uint16_t
         const int64_t colt = per_round / tiles_t(a) * cols(a);   // columns per round
         const int main_cols = (int)(ff / colt * colt);
         if (main_cols == 0 || main_cols == ff) continue;
-        for (const Shape &b : SHAPES) {
-            const double c2 = cost(a, main_cols) + cost(b, ff - main_cols) + 2.0;
-            if (c2 < best) {
-                best = c2;
-                parts[0] = {&a, 0, main_cols};
-                parts[1] = {&b, main_cols, ff};
+        for (const Shape &b : SHAPES)
+            for (int s = 1; s <= 8; s *= 2) {
+                const int nz = splits(s);
+                if (nz < s) break;
+                const double c2 = cost(a, main_cols, 1) + cost(b, ff - main_cols, nz) + 2.0;
+                if (c2 < best) {
+                    best = c2;
+                    parts[0] = {&a, 0, main_cols, 1};
+                    parts[1] = {&b, main_cols, ff, nz};
+                }
             }
-        }
     }
     GD_REQUIRE(ctx, parts[0].sh, "gd_gemm_glu: no tile for GADEON_GLU_CFG=%s", force ? force : "");
     for (const Part &pt : parts) {
         if (!pt.sh || pt.r1 <= pt.r0) continue;
+        const int ncol = pt.r1 - pt.r0;
+        const int bps = (nblk + pt.nz - 1) / pt.nz;
+        void *dst = out;
+        if (pt.nz > 1) {
+            int rc = gd_ctx_workspace(ctx, (size_t)pt.nz * T * 2 * ncol * 4, &dst);
+            if (rc) return rc;
+        }
         gemm_fn f = kernel_for(pt.sh->mt, pt.sh->nt, pt.sh->nw, 0);
-        const int nrt = gd_blocks(pt.r1 - pt.r0, cols(*pt.sh));
-        const int64_t units = tiles_t(*pt.sh) * nrt;
+        const int nrt = gd_blocks(ncol, cols(*pt.sh));
+        const int64_t units = tiles_t(*pt.sh) * pt.nz * nrt;
         const int per = (int)((units + 7) / 8);
         hipLaunchKernelGGL(f, dim3(8 * per), dim3(64 * pt.sh->nw), 0, ctx->stream,
-                           (const uint8_t *)w->codes, (const uint16_t *)w->scales, X, (void *)out,
-                           (int)T, K, R, nblk, nrt, 1, per, ff, pt.r0, pt.r1);
+                           (const uint8_t *)w->codes, (const uint16_t *)w->scales, X, dst, (int)T,
+                           K, R, bps, nrt, pt.nz, per, ff, pt.r0, pt.r1);
         GD_LAUNCHED(ctx, "q2_0_gemm_glu");
+        if (pt.nz > 1) {
+            hipLaunchKernelGGL(q2_0_glu_reduce, dim3(gd_blocks(T * ncol, 256)), dim3(256), 0,
+                               ctx->stream, (const float *)dst, out, (int)T, ncol, pt.nz, ff, pt.r0);
+            GD_LAUNCHED(ctx, "q2_0_glu_reduce");
+        }
     }
     return GD_OK;
 }
