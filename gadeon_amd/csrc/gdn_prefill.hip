@@ -371,7 +371,10 @@ struct ScanChunk {
 
 template <int CP, typename IO, typename OT>
 __global__ __launch_bounds__(256) void gdn_scan(ScanArgs a) {
-    __shared__ __attribute__((aligned(16))) float Sf[DK][NCOL + 4];          // S[i][j] slice
+    // S slice transposed, St[j][i] = S[i][j0 + j]: the split reads 8 key rows
+    // of one column and the update 4, each as contiguous 16-byte reads
+    // (rows of 132 floats put the 16 columns of one read on distinct banks).
+    __shared__ __attribute__((aligned(16))) float St[NCOL][DK + 4];
     __shared__ __attribute__((aligned(16))) f16 Sh[NCOL][PADK], Sl[NCOL][PADK];  // S^T split
     __shared__ __attribute__((aligned(16))) f16 Dh[NCOL][CP + 8], Dl[NCOL][CP + 8];  // delta^T
     __shared__ __attribute__((aligned(16))) f16 Eh[NCOL][CP + 8], El[NCOL][CP + 8];  // decayed
@@ -397,7 +400,7 @@ __global__ __launch_bounds__(256) void gdn_scan(ScanArgs a) {
 
     for (int e = tid; e < DK * NCOL; e += 256) {
         const int i = e / NCOL, j = e % NCOL;
-        Sf[i][j] = Sg[(size_t)i * DV + j0 + j];
+        St[j][i] = Sg[(size_t)i * DV + j0 + j];
     }
 
     // The operands of chunk c, loaded in three groups, each refilled for the
@@ -463,7 +466,7 @@ __global__ __launch_bounds__(256) void gdn_scan(ScanArgs a) {
             const int j = e / (DK / 8), i8 = (e % (DK / 8)) * 8;
             float sv[8];
 #pragma unroll
-            for (int q = 0; q < 8; q++) sv[q] = Sf[i8 + q][j];
+            for (int q = 0; q < 8; q++) sv[q] = St[j][i8 + q];
             f16x8 h, l;
             split8(sv, h, l);
             *(f16x8 *)&Sh[j][i8] = h;
@@ -556,7 +559,7 @@ __global__ __launch_bounds__(256) void gdn_scan(ScanArgs a) {
                 const int j = ct * 16 + lr;
                 f32x4 acc;
 #pragma unroll
-                for (int v = 0; v < 4; v++) acc[v] = decay * Sf[ib + kg * 4 + v][j];
+                for (int v = 0; v < 4; v++) acc[v] = decay * St[j][ib + kg * 4 + v];
 #pragma unroll
                 for (int ks = 0; ks < CP / 32; ks++) {
                     const int s0 = ks * 32 + kg * 8;
@@ -564,7 +567,7 @@ __global__ __launch_bounds__(256) void gdn_scan(ScanArgs a) {
                     acc = mfma(k.ka[rt][ks], *(const f16x8 *)&El[j][s0], acc);
                 }
 #pragma unroll
-                for (int v = 0; v < 4; v++) Sf[ib + kg * 4 + v][j] = acc[v];
+                for (int v = 0; v < 4; v++) St[j][ib + kg * 4 + v] = acc[v];
             }
         }
         loadK(c + 1);
@@ -577,7 +580,7 @@ __global__ __launch_bounds__(256) void gdn_scan(ScanArgs a) {
     __syncthreads();
     for (int e = tid; e < DK * NCOL; e += 256) {
         const int i = e / NCOL, j = e % NCOL;
-        Sg[(size_t)i * DV + j0 + j] = Sf[i][j];
+        Sg[(size_t)i * DV + j0 + j] = St[j][i];
     }
 }
 
