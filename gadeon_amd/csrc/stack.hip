@@ -484,43 +484,65 @@ __global__ __launch_bounds__(256) void k_attn_prefill(
     }
 }
 
-// Decode attention for one query token, split over keys (flash decoding):
-// block (head h, split sp) has 4 waves; each wave takes whole keys with a lane
-// holding 2 of the 128 dims, and keeps an online-softmax partial.  The block
-// merges its waves and writes (max, sum, acc[128]) for the split to a
-// workspace; k_attn_combine merges the splits (Attention.swift:108-134).
+// Decode attention for one query token, split over keys (flash decoding),
+// with the per-token preparation of k_attn_prep folded in: block (head h,
+// split sp) of 256 threads normalizes and rotates its own q (threads 0..127;
+// the same arithmetic as k_attn_prep), and the split that holds key pos (the
+// new token) forms the new k and v itself (threads 128..255), rounded to f16
+// as the cache stores them, and uses them for key pos instead of reading the
+// cache.  The first q head of each kv group appends them to the cache for
+// later steps; no block of this launch reads the cache at pos.  Each of the
+// 4 waves takes whole keys with a lane holding 2 of the 128 dims and keeps an
+// online-softmax partial; the block merges its waves and writes (max, sum,
+// acc[128]) for the split; k_attn_combine merges the splits
+// (Attention.swift:108-134).
 constexpr int DSPLIT = 16;      // key splits per head
 __global__ __launch_bounds__(256) void k_attn_decode(
-        const float *q, const uint16_t *kc, const uint16_t *vc, const int32_t *page_table,
-        const int32_t *pos_ptr, float *part, int H, int HKV, int block, float scale) {
+        const float *proj, const float *q_norm, const float *k_norm, uint16_t *kc, uint16_t *vc,
+        const int32_t *page_table, const int32_t *pos_ptr, float *part, int H, int HKV, int block,
+        float scale, int n_rot, float base, float eps) {
     __shared__ float wm[4], wl[4];
     __shared__ float wacc[4][HD];
+    __shared__ float nrm[2][HD], rot[2][HD], vnew[HD], red[4];
     const int h = blockIdx.x, sp = blockIdx.y, t = threadIdx.x;
     const int lane = t & 63, w = t >> 6;
     const int kvh = h / (H / HKV), kvDim = HKV * HD;
-    const int T = *pos_ptr + 1;
-    const float q0 = q[(int64_t)h * HD + 2 * lane] * scale;
-    const float q1 = q[(int64_t)h * HD + 2 * lane + 1] * scale;
-    float m = -INFINITY, l = 0.f, a0 = 0.f, a1 = 0.f;
-    // Wave w of split sp takes keys j = (sp * 4 + w) + 64 * i.  The next
-    // key's page-table entry and K/V values are requested before this key's
-    // arithmetic, so each key waits only for loads issued a key earlier.
-    constexpr int STEP = DSPLIT * 4;
-    auto kv_base = [&](int j) { return kv_slot(page_table, j, block) * kvDim + kvh * HD + 2 * lane; };
-    int j = sp * 4 + w;
-    uint32_t kn = 0, vn = 0;
-    if (j < T) {
-        const int64_t b0 = kv_base(j);
-        kn = *(const uint32_t *)(kc + b0);
-        vn = *(const uint32_t *)(vc + b0);
-    }
-    for (; j < T; j += STEP) {
-        const uint32_t kk = kn, vv = vn;
-        if (j + STEP < T) {
-            const int64_t bn = kv_base(j + STEP);
-            kn = *(const uint32_t *)(kc + bn);
-            vn = *(const uint32_t *)(vc + bn);
+    const int pos = *pos_ptr, T = pos + 1;
+    const bool has_pos = sp == (pos >> 2) % DSPLIT;      // wave pos & 3 of this split takes key pos
+    // q of head h (hf = 0) and k of kv head kvh (hf = 1): RMS norm over the
+    // head, then the partial NEOX rope, as k_attn_prep.
+    {
+        const int hf = t >> 7, i = t & (HD - 1);
+        const float x = hf == 0 ? proj[h * 2 * HD + i] : proj[2 * H * HD + kvh * HD + i];
+        const float sq = gd_wave_sum(x * x);
+        if (lane == 0) red[w] = sq;
+        __syncthreads();
+        const float ss = red[2 * hf] + red[2 * hf + 1];
+        const float sc = 1.0f / sqrtf(ss / (float)HD + eps);
+        float y = x * sc * (hf == 0 ? q_norm[i] : k_norm[i]);
+        nrm[hf][i] = y;
+        __syncthreads();
+        const int half = n_rot / 2;
+        if (i < n_rot) {
+            const int jj = i < half ? i : i - half;
+            const float freq = powf(base, -2.0f * (float)jj / (float)n_rot);
+            const float ang = (float)pos * freq;
+            const float c = cosf(ang), sn = sinf(ang);
+            y = i < half ? nrm[hf][i] * c - nrm[hf][i + half] * sn
+                         : nrm[hf][i - half] * sn + nrm[hf][i] * c;
         }
+        rot[hf][i] = y;
+        if (hf == 1) vnew[i] = proj[2 * H * HD + HKV * HD + kvh * HD + i];
+        __syncthreads();
+        if (hf == 1 && has_pos && h % (H / HKV) == 0) {
+            const int64_t slot = (int64_t)page_table[pos / block] * block + pos % block;
+            kc[slot * kvDim + kvh * HD + i] = gd_f2h(y);
+            vc[slot * kvDim + kvh * HD + i] = gd_f2h(vnew[i]);
+        }
+    }
+    const float q0 = rot[0][2 * lane] * scale, q1 = rot[0][2 * lane + 1] * scale;
+    float m = -INFINITY, l = 0.f, a0 = 0.f, a1 = 0.f;
+    auto consume = [&](uint32_t kk, uint32_t vv) {
         float s = q0 * gd_h2f((uint16_t)(kk & 0xffff)) + q1 * gd_h2f((uint16_t)(kk >> 16));
         s = gd_wave_sum(s);
         const float mn = fmaxf(m, s);
@@ -529,7 +551,33 @@ __global__ __launch_bounds__(256) void k_attn_decode(
         a0 = fmaf(p, gd_h2f((uint16_t)(vv & 0xffff)), a0 * al);
         a1 = fmaf(p, gd_h2f((uint16_t)(vv >> 16)), a1 * al);
         m = mn;
+    };
+    // Cached keys j < pos: wave w of split sp takes j = (sp * 4 + w) + 64 * i.
+    // The next key's page-table entry and K/V values are requested before
+    // this key's arithmetic, so each key waits only for loads issued a key
+    // earlier.
+    constexpr int STEP = DSPLIT * 4;
+    auto kv_base = [&](int j) { return kv_slot(page_table, j, block) * kvDim + kvh * HD + 2 * lane; };
+    int j = sp * 4 + w;
+    uint32_t kn = 0, vn = 0;
+    if (j < pos) {
+        const int64_t b0 = kv_base(j);
+        kn = *(const uint32_t *)(kc + b0);
+        vn = *(const uint32_t *)(vc + b0);
     }
+    for (; j < pos; j += STEP) {
+        const uint32_t kk = kn, vv = vn;
+        if (j + STEP < pos) {
+            const int64_t bn = kv_base(j + STEP);
+            kn = *(const uint32_t *)(kc + bn);
+            vn = *(const uint32_t *)(vc + bn);
+        }
+        consume(kk, vv);
+    }
+    // Key pos, from this block's own copy (f16, as cached).
+    if (has_pos && w == (pos & 3))
+        consume((uint32_t)gd_f2h(rot[1][2 * lane]) | ((uint32_t)gd_f2h(rot[1][2 * lane + 1]) << 16),
+                (uint32_t)gd_f2h(vnew[2 * lane]) | ((uint32_t)gd_f2h(vnew[2 * lane + 1]) << 16));
     if (lane == 0) { wm[w] = m; wl[w] = l; }
     wacc[w][2 * lane] = a0;
     wacc[w][2 * lane + 1] = a1;
@@ -549,7 +597,8 @@ __global__ __launch_bounds__(256) void k_attn_decode(
     }
 }
 
-__global__ void k_attn_combine(const float *part, const float *gate, uint16_t *out) {
+// gate: the raw gate of head h at gate + h * gstride (sigmoid applied here).
+__global__ void k_attn_combine(const float *part, const float *gate, int gstride, uint16_t *out) {
     const int h = blockIdx.x, t = threadIdx.x;      // HD threads
     const float *p = part + (int64_t)h * DSPLIT * (HD + 2);
     float M = -INFINITY;
@@ -561,7 +610,7 @@ __global__ void k_attn_combine(const float *part, const float *gate, uint16_t *o
         L += p[s * (HD + 2) + HD + 1] * f;
         A += p[s * (HD + 2) + t] * f;
     }
-    out[(int64_t)h * HD + t] = gd_f2h(A / L * gd_sigmoid(gate[(int64_t)h * HD + t]));
+    out[(int64_t)h * HD + t] = gd_f2h(A / L * gd_sigmoid(gate[(int64_t)h * gstride + t]));
 }
 
 // Greedy pick: index of the first maximum (BonsaiEngine.argmax, :187-191).
@@ -778,15 +827,19 @@ int forward(gd_stack *st, int N, bool decode) {
                 K_(k_onorm_silu, dim3(gd_blocks((int64_t)N * nV, 4)), dim3(256), 0, s, st->o32,
                    st->proj, (int64_t)RP, off_z, ly.ssm_norm, st->a16, nV, N, eps);
         } else {
-            K_(k_attn_prep, dim3(N, H + HKV), dim3(HD), 0, s, st->proj, (int64_t)RP, ly.q_norm,
-               ly.k_norm, st->q32, st->gate32, ly.kc, ly.vc, st->page_table, st->dpos, H, HKV,
-               c.n_rot, c.rope_base, c.kv_block, eps);
             const float scale = 1.0f / sqrtf((float)HD);
             if (decode) {
-                K_(k_attn_decode, dim3(H, DSPLIT), dim3(256), 0, s, st->q32, ly.kc, ly.vc,
-                   st->page_table, st->dpos, st->attn_part, H, HKV, c.kv_block, scale);
-                K_(k_attn_combine, dim3(H), dim3(HD), 0, s, st->attn_part, st->gate32, st->a16);
+                // One token: q/k preparation and the cache append happen
+                // inside the attention launch.
+                K_(k_attn_decode, dim3(H, DSPLIT), dim3(256), 0, s, st->proj, ly.q_norm, ly.k_norm,
+                   ly.kc, ly.vc, st->page_table, st->dpos, st->attn_part, H, HKV, c.kv_block, scale,
+                   c.n_rot, c.rope_base, eps);
+                K_(k_attn_combine, dim3(H), dim3(HD), 0, s, st->attn_part, st->proj + HD, 2 * HD,
+                   st->a16);
             } else {
+                K_(k_attn_prep, dim3(N, H + HKV), dim3(HD), 0, s, st->proj, (int64_t)RP, ly.q_norm,
+                   ly.k_norm, st->q32, st->gate32, ly.kc, ly.vc, st->page_table, st->dpos, H, HKV,
+                   c.n_rot, c.rope_base, c.kv_block, eps);
                 K_(k_attn_prefill, dim3(H, gd_blocks(N, AQ)), dim3(256), 0, s, st->q32,
                    st->gate32, ly.kc, ly.vc, st->page_table, st->dpos, st->a16, H, HKV, N,
                    c.kv_block, scale);
