@@ -659,27 +659,39 @@ __global__ __launch_bounds__(128) void k_argmax_final(const float *pv, const int
 __global__ __launch_bounds__(1024) void k_add_rmsnorm(float *x, const float *y, const float *w,
                                                       uint16_t *out, int n, float eps,
                                                       int nsplit, int64_t ystride) {
+    // Thread t holds elements 4t + 4096 k (k < 4, n <= 16384) in registers
+    // between the sum and the normalization, so h is read and written once.
     __shared__ float red[16];
     const int64_t row = blockIdx.x;
     float *xr = x + row * n;
     const float *yr = y ? y + row * n : nullptr;
     float ss = 0.f;
-    for (int i = threadIdx.x * 4; i < n; i += blockDim.x * 4) {
-        f32x4 a = *(const f32x4 *)(xr + i);
-        if (yr) {
-            for (int z = 0; z < nsplit; z++) a += *(const f32x4 *)(yr + z * ystride + i);
-            *(f32x4 *)(xr + i) = a;
+    f32x4 v[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int i = threadIdx.x * 4 + k * 4096;
+        if (i < n) {
+            f32x4 a = *(const f32x4 *)(xr + i);
+            if (yr) {
+                for (int z = 0; z < nsplit; z++) a += *(const f32x4 *)(yr + z * ystride + i);
+                *(f32x4 *)(xr + i) = a;
+            }
+            ss += a[0] * a[0] + a[1] * a[1] + a[2] * a[2] + a[3] * a[3];
+            v[k] = a;
         }
-        ss += a[0] * a[0] + a[1] * a[1] + a[2] * a[2] + a[3] * a[3];
     }
     ss = gd_block_sum(ss, red);
     const float s = 1.0f / sqrtf(ss / (float)n + eps);
-    for (int i = threadIdx.x * 4; i < n; i += blockDim.x * 4) {
-        const f32x4 a = *(const f32x4 *)(xr + i);
-        const f32x4 ww = *(const f32x4 *)(w + i);
-        const uint32_t lo = (uint32_t)gd_f2h(a[0] * s * ww[0]) | ((uint32_t)gd_f2h(a[1] * s * ww[1]) << 16);
-        const uint32_t hi = (uint32_t)gd_f2h(a[2] * s * ww[2]) | ((uint32_t)gd_f2h(a[3] * s * ww[3]) << 16);
-        *(u32x2 *)(out + row * n + i) = u32x2{lo, hi};   // n % 4 == 0: 8-byte aligned
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int i = threadIdx.x * 4 + k * 4096;
+        if (i < n) {
+            const f32x4 a = v[k];
+            const f32x4 ww = *(const f32x4 *)(w + i);
+            const uint32_t lo = (uint32_t)gd_f2h(a[0] * s * ww[0]) | ((uint32_t)gd_f2h(a[1] * s * ww[1]) << 16);
+            const uint32_t hi = (uint32_t)gd_f2h(a[2] * s * ww[2]) | ((uint32_t)gd_f2h(a[3] * s * ww[3]) << 16);
+            *(u32x2 *)(out + row * n + i) = u32x2{lo, hi};   // n % 4 == 0: 8-byte aligned
+        }
     }
 }
 
