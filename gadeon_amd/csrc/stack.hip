@@ -78,18 +78,28 @@ __global__ __launch_bounds__(256) void k_gdn_conv_prefill(
     const int r = (int)(task % nrows), n0 = (int)(task / nrows) * CT;
     const int lane = threadIdx.x & 63;
     const int c[2] = {r * HD + lane, r * HD + 64 + lane};
-    float w[2][4], win[2][CT + 3];
+    // Every load of both channels goes out before any value is used: the
+    // weights, then both candidates of every window slot at clamped,
+    // in-range addresses (the value is selected afterwards; loads under a
+    // branch each waited for the one before).
+    float w[2][4], win[2][CT + 3], pr[2][CT + 3], rr[2][3];
 #pragma unroll
     for (int h = 0; h < 2; h++) {
         const f32x4 wv = *(const f32x4 *)(cw + (int64_t)c[h] * 4);
         w[h][0] = wv[0]; w[h][1] = wv[1]; w[h][2] = wv[2]; w[h][3] = wv[3];
 #pragma unroll
+        for (int j = 0; j < CT + 3; j++)
+            pr[h][j] = proj[(int64_t)min(max(n0 - 3 + j, 0), N - 1) * stride + c[h]];
+#pragma unroll
+        for (int j = 0; j < 3; j++) rr[h][j] = ring[(int64_t)j * convDim + c[h]];
+    }
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+#pragma unroll
         for (int j = 0; j < CT + 3; j++) {
             const int m = n0 - 3 + j;            // token of window slot j
-            win[h][j] = m < 0 ? ring[(int64_t)(3 + m) * convDim + c[h]]
-                      : m < N ? proj[(int64_t)m * stride + c[h]] : 0.f;
+            win[h][j] = m < 0 ? rr[h][3 + m < 0 ? 0 : 3 + m] : m < N ? pr[h][j] : 0.f;
         }
-    }
     const bool norm = r < nqk_rows;
 #pragma unroll
     for (int t = 0; t < CT; t++) {
