@@ -97,29 +97,6 @@ __device__ __forceinline__ f16x8 cvt8(const Raw8<IO> &r, bool ok) {
     return h;
 }
 
-// Eight consecutive activations (f16 or f32) as f16, zero when !ok.
-template <typename IO>
-__device__ __forceinline__ f16x8 load8(const void *base, int64_t idx, bool ok) {
-    f16x8 r;
-    if constexpr (sizeof(IO) == 2) {
-        const u32x4 v = ok ? *(const u32x4 *)((const uint16_t *)base + idx) : u32x4{0, 0, 0, 0};
-        r = __builtin_bit_cast(f16x8, v);
-    } else {
-        f32x4 a = f32x4{0.f, 0.f, 0.f, 0.f}, b = a;
-        if (ok) {
-            const f32x4 *p = (const f32x4 *)((const float *)base + idx);
-            a = p[0];
-            b = p[1];
-        }
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            r[e] = (f16)a[e];
-            r[4 + e] = (f16)b[e];
-        }
-    }
-    return r;
-}
-
 struct Work {
     f16 *Wh, *Wl;     // [u][CP][DK]
     float *U;         // [u][CP][DV]
@@ -159,16 +136,27 @@ __global__ __launch_bounds__(256) void gdn_prep(PrepArgs a) {
 
     // Rows of K and Q (and V, kept in registers until Q is done): thread e
     // handles 8 consecutive elements of row e / 16.
+    // Every load goes out before any is converted (rows past the chunk read
+    // token 0 and are zeroed at conversion): loads under a branch, converted
+    // on arrival, waited for one by one.
     constexpr int NE = CP * DK / 8 / 256;                   // entries per thread
     f16x8 vreg[NE];
+    Raw8<IO> rk[NE], rq[NE], rv[NE];
+#pragma unroll
+    for (int n = 0; n < NE; n++) {
+        const int e = tid + 256 * n, t = e >> 4, i8 = (e & 15) * 8;
+        const int64_t tok = t0 + (t < L ? t : 0);
+        rk[n] = load_raw8<IO>(a.k, tok * a.k_stride + (int64_t)hk * DK + i8);
+        rq[n] = load_raw8<IO>(a.q, tok * a.q_stride + (int64_t)hk * DK + i8);
+        rv[n] = load_raw8<IO>(a.v, tok * a.v_stride + (int64_t)hv * DV + i8);
+    }
 #pragma unroll
     for (int n = 0; n < NE; n++) {
         const int e = tid + 256 * n, t = e >> 4, i8 = (e & 15) * 8;
         const bool ok = t < L;
-        const int64_t tok = t0 + (ok ? t : 0);
-        *(f16x8 *)&Ks[t][i8] = load8<IO>(a.k, tok * a.k_stride + (int64_t)hk * DK + i8, ok);
-        *(f16x8 *)&QVs[t][i8] = load8<IO>(a.q, tok * a.q_stride + (int64_t)hk * DK + i8, ok);
-        vreg[n] = load8<IO>(a.v, tok * a.v_stride + (int64_t)hv * DV + i8, ok);
+        *(f16x8 *)&Ks[t][i8] = cvt8<IO>(rk[n], ok);
+        *(f16x8 *)&QVs[t][i8] = cvt8<IO>(rq[n], ok);
+        vreg[n] = cvt8<IO>(rv[n], ok);
     }
     if (wave == 0) {
         // Inclusive cumulative gate inside the chunk (wave prefix sum); rows
