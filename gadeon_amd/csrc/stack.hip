@@ -293,44 +293,62 @@ __global__ void k_onorm_silu(const float *o, const float *proj, int64_t stride, 
 // the q half of the fused [q | gate] pair, RMS-normalize it with q_norm and
 // rotate it; kv heads normalize + rotate k and append k, v to the f16 cache
 // at the token's position (Attention.swift:79-107).
-__global__ void k_attn_prep(const float *proj, int64_t stride, const float *q_norm,
-                            const float *k_norm, float *q_out, float *gate_out, uint16_t *kc,
-                            uint16_t *vc, const int32_t *page_table, const int32_t *pos_ptr,
-                            int H, int HKV, int n_rot, float base, int block, float eps) {
-    __shared__ float buf[HD];
-    __shared__ float red[2];
-    const int n = blockIdx.x, h = blockIdx.y, i = threadIdx.x;
+__global__ __launch_bounds__(256) void k_attn_prep(
+        const float *proj, int64_t stride, const float *q_norm, const float *k_norm, float *q_out,
+        float *gate_out, uint16_t *kc, uint16_t *vc, const int32_t *page_table,
+        const int32_t *pos_ptr, int N, int H, int HKV, int n_rot, float base, int block, float eps) {
+    // One wave per (token n, head h < H + HKV): lane l holds dims l and l + 64.
+    const int64_t task = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (task >= (int64_t)N * (H + HKV)) return;
+    const int n = (int)(task / (H + HKV)), h = (int)(task % (H + HKV)), lane = threadIdx.x & 63;
     const int pos = *pos_ptr + n;
     const float *row = proj + (int64_t)n * stride;
     const bool is_q = h < H;
     const int kh = h - H;
-    const float x = is_q ? row[h * 2 * HD + i] : row[2 * H * HD + kh * HD + i];
+    const float *src = is_q ? row + h * 2 * HD : row + 2 * H * HD + kh * HD;
+    const float *nw = is_q ? q_norm : k_norm;
+    const float x0 = src[lane], x1 = src[lane + 64];
+    const float w0 = nw[lane], w1 = nw[lane + 64];
     // RMS norm over the head (Kern.rmsnormRows, Kernels.swift:26-37).
-    float ss = gd_wave_sum(x * x);
-    if ((i & 63) == 0) red[i >> 6] = ss;
-    __syncthreads();
-    ss = red[0] + red[1];
-    const float s = 1.0f / sqrtf(ss / (float)HD + eps);
-    float y = x * s * (is_q ? q_norm[i] : k_norm[i]);
-    buf[i] = y;
-    __syncthreads();
-    // Partial NEOX rope on the first n_rot dims (Kern.ropeNeox, Kernels.swift:66-84).
+    const float ss = gd_wave_sum(x0 * x0 + x1 * x1);
+    const float sc = 1.0f / sqrtf(ss / (float)HD + eps);
+    const float y0 = x0 * sc * w0, y1 = x1 * sc * w1;
+    // Partial NEOX rope on the first n_rot dims (Kern.ropeNeox,
+    // Kernels.swift:66-84): dim i pairs with i +- n_rot/2, held by another
+    // lane (or the other half of this one).
     const int half = n_rot / 2;
-    if (i < n_rot) {
-        const int j = i < half ? i : i - half;
-        const float freq = powf(base, -2.0f * (float)j / (float)n_rot);
-        const float ang = (float)pos * freq;
-        const float c = cosf(ang), sn = sinf(ang);
-        y = i < half ? buf[i] * c - buf[i + half] * sn : buf[i - half] * sn + buf[i] * c;
+    float r[2] = {y0, y1};
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        const int i = lane + 64 * k;
+        const int ip = i < half ? i + half : i - half;          // partner dim
+        const float mine = k ? y1 : y0;
+        // Both halves from the partner's lane; this lane picks the one it needs.
+        const float p0 = __shfl(y0, ip & 63, 64), p1 = __shfl(y1, ip & 63, 64);
+        const float pv = ip < 64 ? p0 : p1;
+        if (i < n_rot) {
+            const int jj = i < half ? i : i - half;
+            const float freq = powf(base, -2.0f * (float)jj / (float)n_rot);
+            const float ang = (float)pos * freq;
+            const float c = cosf(ang), sn = sinf(ang);
+            r[k] = i < half ? mine * c - pv * sn : pv * sn + mine * c;
+        }
     }
     if (is_q) {
-        q_out[((int64_t)n * H + h) * HD + i] = y;
-        gate_out[((int64_t)n * H + h) * HD + i] = row[h * 2 * HD + HD + i];
+        float *qo = q_out + ((int64_t)n * H + h) * HD;
+        float *go = gate_out + ((int64_t)n * H + h) * HD;
+        qo[lane] = r[0];
+        qo[lane + 64] = r[1];
+        go[lane] = row[h * 2 * HD + HD + lane];
+        go[lane + 64] = row[h * 2 * HD + HD + lane + 64];
     } else {
         const int kvDim = HKV * HD;
         const int64_t slot = (int64_t)page_table[pos / block] * block + pos % block;
-        kc[slot * kvDim + kh * HD + i] = gd_f2h(y);
-        vc[slot * kvDim + kh * HD + i] = gd_f2h(row[2 * H * HD + HKV * HD + kh * HD + i]);
+        const float *vs = row + 2 * H * HD + HKV * HD + kh * HD;
+        kc[slot * kvDim + kh * HD + lane] = gd_f2h(r[0]);
+        kc[slot * kvDim + kh * HD + lane + 64] = gd_f2h(r[1]);
+        vc[slot * kvDim + kh * HD + lane] = gd_f2h(vs[lane]);
+        vc[slot * kvDim + kh * HD + lane + 64] = gd_f2h(vs[lane + 64]);
     }
 }
 
@@ -859,9 +877,9 @@ int forward(gd_stack *st, int N, bool decode) {
                 K_(k_attn_combine, dim3(H), dim3(HD), 0, s, st->attn_part, st->proj + HD, 2 * HD,
                    st->a16);
             } else {
-                K_(k_attn_prep, dim3(N, H + HKV), dim3(HD), 0, s, st->proj, (int64_t)RP, ly.q_norm,
-                   ly.k_norm, st->q32, st->gate32, ly.kc, ly.vc, st->page_table, st->dpos, H, HKV,
-                   c.n_rot, c.rope_base, c.kv_block, eps);
+                K_(k_attn_prep, dim3(gd_blocks((int64_t)N * (H + HKV), 4)), dim3(256), 0, s, st->proj,
+                   (int64_t)RP, ly.q_norm, ly.k_norm, st->q32, st->gate32, ly.kc, ly.vc,
+                   st->page_table, st->dpos, N, H, HKV, c.n_rot, c.rope_base, c.kv_block, eps);
                 K_(k_attn_prefill, dim3(H, gd_blocks(N, AQ)), dim3(256), 0, s, st->q32,
                    st->gate32, ly.kc, ly.vc, st->page_table, st->dpos, st->a16, H, HKV, N,
                    c.kv_block, scale);
