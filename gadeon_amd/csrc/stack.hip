@@ -537,17 +537,30 @@ __global__ __launch_bounds__(256) void k_attn_decode(
     const int kvh = h / (H / HKV), kvDim = HKV * HD;
     const int pos = *pos_ptr, T = pos + 1;
     const bool has_pos = sp == (pos >> 2) % DSPLIT;      // wave pos & 3 of this split takes key pos
+    // The first cached key of this wave is requested before the q/k work
+    // below, which does not depend on it.
+    constexpr int STEP = DSPLIT * 4;
+    auto kv_base = [&](int j) { return kv_slot(page_table, j, block) * kvDim + kvh * HD + 2 * lane; };
+    int j = sp * 4 + w;
+    uint32_t kn = 0, vn = 0;
+    if (j < pos) {
+        const int64_t b0 = kv_base(j);
+        kn = *(const uint32_t *)(kc + b0);
+        vn = *(const uint32_t *)(vc + b0);
+    }
     // q of head h (hf = 0) and k of kv head kvh (hf = 1): RMS norm over the
     // head, then the partial NEOX rope, as k_attn_prep.
     {
         const int hf = t >> 7, i = t & (HD - 1);
         const float x = hf == 0 ? proj[h * 2 * HD + i] : proj[2 * H * HD + kvh * HD + i];
+        const float nw = hf == 0 ? q_norm[i] : k_norm[i];
+        const float vx = proj[2 * H * HD + HKV * HD + kvh * HD + i];
         const float sq = gd_wave_sum(x * x);
         if (lane == 0) red[w] = sq;
         __syncthreads();
         const float ss = red[2 * hf] + red[2 * hf + 1];
         const float sc = 1.0f / sqrtf(ss / (float)HD + eps);
-        float y = x * sc * (hf == 0 ? q_norm[i] : k_norm[i]);
+        float y = x * sc * nw;
         nrm[hf][i] = y;
         __syncthreads();
         const int half = n_rot / 2;
@@ -560,7 +573,7 @@ __global__ __launch_bounds__(256) void k_attn_decode(
                          : nrm[hf][i - half] * sn + nrm[hf][i] * c;
         }
         rot[hf][i] = y;
-        if (hf == 1) vnew[i] = proj[2 * H * HD + HKV * HD + kvh * HD + i];
+        if (hf == 1) vnew[i] = vx;
         __syncthreads();
         if (hf == 1 && has_pos && h % (H / HKV) == 0) {
             const int64_t slot = (int64_t)page_table[pos / block] * block + pos % block;
@@ -584,15 +597,6 @@ __global__ __launch_bounds__(256) void k_attn_decode(
     // The next key's page-table entry and K/V values are requested before
     // this key's arithmetic, so each key waits only for loads issued a key
     // earlier.
-    constexpr int STEP = DSPLIT * 4;
-    auto kv_base = [&](int j) { return kv_slot(page_table, j, block) * kvDim + kvh * HD + 2 * lane; };
-    int j = sp * 4 + w;
-    uint32_t kn = 0, vn = 0;
-    if (j < pos) {
-        const int64_t b0 = kv_base(j);
-        kn = *(const uint32_t *)(kc + b0);
-        vn = *(const uint32_t *)(vc + b0);
-    }
     for (; j < pos; j += STEP) {
         const uint32_t kk = kn, vv = vn;
         if (j + STEP < pos) {
