@@ -66,9 +66,20 @@ __global__ void k_conv4(const float *proj, int64_t stride, float *ring, const fl
 // (earlier tokens than 0), so it alone writes the new ring, after its reads.
 // The row-0 waves also compute the gates of their tokens.
 constexpr int CT = 4;                        // tokens per wave task
+// Sum of the NP split-K partials of proj[idx] (pstride floats apart), in split order.
+template <int NP>
+__device__ __forceinline__ float psum(const float *proj, int64_t pstride, int64_t idx) {
+    float a = proj[idx];
+#pragma unroll
+    for (int p = 1; p < NP; p++) a += proj[p * pstride + idx];
+    return a;
+}
 static_assert(CT >= 3, "only the first task of a row may reach back into the ring");
+// proj holds NP split-K partials of the in_proj output, pstride floats
+// apart, summed as they are read.
+template <int NP>
 __global__ __launch_bounds__(256) void k_gdn_conv_prefill(
-        const float *proj, int64_t stride, float *ring, const float *cw, float *out,
+        const float *proj, int64_t stride, int64_t pstride, float *ring, const float *cw, float *out,
         int convDim, int nqk_rows, int N, float eps, int off_b, int off_a, const float *dt,
         const float *aNeg, float *beta, float *g, int nV) {
     const int nrows = convDim / HD;
@@ -89,7 +100,7 @@ __global__ __launch_bounds__(256) void k_gdn_conv_prefill(
         w[h][0] = wv[0]; w[h][1] = wv[1]; w[h][2] = wv[2]; w[h][3] = wv[3];
 #pragma unroll
         for (int j = 0; j < CT + 3; j++)
-            pr[h][j] = proj[(int64_t)min(max(n0 - 3 + j, 0), N - 1) * stride + c[h]];
+            pr[h][j] = psum<NP>(proj, pstride, (int64_t)min(max(n0 - 3 + j, 0), N - 1) * stride + c[h]);
 #pragma unroll
         for (int j = 0; j < 3; j++) rr[h][j] = ring[(int64_t)j * convDim + c[h]];
     }
@@ -136,7 +147,7 @@ __global__ __launch_bounds__(256) void k_gdn_conv_prefill(
 #pragma unroll
             for (int j = 0; j < 3; j++) {
                 const int m = N - 3 + j;
-                nr[j] = m < 0 ? win[h][3 + m] : proj[(int64_t)m * stride + c[h]];
+                nr[j] = m < 0 ? win[h][3 + m] : psum<NP>(proj, pstride, (int64_t)m * stride + c[h]);
             }
 #pragma unroll
             for (int j = 0; j < 3; j++) ring[(int64_t)j * convDim + c[h]] = nr[j];
@@ -146,9 +157,9 @@ __global__ __launch_bounds__(256) void k_gdn_conv_prefill(
         for (int i = lane; i < CT * nV; i += 64) {
             const int n = n0 + i / nV, hh = i % nV;
             if (n >= N) break;
-            const float *row = proj + (int64_t)n * stride;
-            beta[(int64_t)n * nV + hh] = gd_sigmoid(row[off_b + hh]);
-            g[(int64_t)n * nV + hh] = gd_softplus(row[off_a + hh] + dt[hh]) * aNeg[hh];
+            const int64_t rb = (int64_t)n * stride;
+            beta[(int64_t)n * nV + hh] = gd_sigmoid(psum<NP>(proj, pstride, rb + off_b + hh));
+            g[(int64_t)n * nV + hh] = gd_softplus(psum<NP>(proj, pstride, rb + off_a + hh) + dt[hh]) * aNeg[hh];
         }
     }
 }
@@ -273,8 +284,11 @@ __global__ __launch_bounds__(64 * GS_W) void k_gdn_step(
     }
 }
 
-__global__ void k_onorm_silu(const float *o, const float *proj, int64_t stride, int off_z,
-                             const float *w, uint16_t *out, int nV, int N, float eps) {
+// proj holds NP split-K partials of the in_proj output, pstride floats
+// apart, summed here in split order (as q2_0_gemm_reduce sums them).
+template <int NP>
+__global__ void k_onorm_silu(const float *o, const float *proj, int64_t stride, int64_t pstride,
+                             int off_z, const float *w, uint16_t *out, int nV, int N, float eps) {
     const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     if (row >= N * nV) return;
     const int lane = threadIdx.x & 63;
@@ -284,12 +298,18 @@ __global__ void k_onorm_silu(const float *o, const float *proj, int64_t stride, 
     const float ss = gd_wave_sum(a * a + b * b);
     const float s = 1.0f / sqrtf(ss / (float)HD + eps);
     const float *z = proj + (int64_t)n * stride + off_z + h * HD;
+    float z0 = z[lane], z1 = z[lane + 64];
+#pragma unroll
+    for (int p = 1; p < NP; p++) {
+        z0 += z[p * pstride + lane];
+        z1 += z[p * pstride + lane + 64];
+    }
     uint16_t *dst = out + (int64_t)row * HD;
-    dst[lane] = gd_f2h(a * s * w[lane] * gd_silu(z[lane]));
-    dst[lane + 64] = gd_f2h(b * s * w[lane + 64] * gd_silu(z[lane + 64]));
+    dst[lane] = gd_f2h(a * s * w[lane] * gd_silu(z0));
+    dst[lane + 64] = gd_f2h(b * s * w[lane + 64] * gd_silu(z1));
 }
 
-// Attention prep, one block of HD threads per (token, head): q heads take
+// Attention prep (prefill), one wave per (token, head): q heads take
 // the q half of the fused [q | gate] pair, RMS-normalize it with q_norm and
 // rotate it; kv heads normalize + rotate k and append k, v to the f16 cache
 // at the token's position (Attention.swift:79-107).
@@ -830,6 +850,9 @@ int forward(gd_stack *st, int N, bool decode) {
     for (int il = 0; il < c.n_layer; il++) {
         StackLayer &ly = st->L[il];
         const int RP = ly.rec ? st->rp_rec : st->rp_att;
+        // in_proj output: proj, or np split-K partials of it at pin.
+        const float *pin = st->proj;
+        int np = 1;
         if (decode) {
             if (il == 0) {
                 R_(gd_gemv_mfma_norm(ctx, &ly.in_proj, hcur, nullptr, 0, 0, ly.attn_norm, eps,
@@ -838,6 +861,19 @@ int forward(gd_stack *st, int N, bool decode) {
                 R_(gd_gemv_mfma_norm(ctx, &ly.in_proj, hcur, st->contrib, nd, E, ly.attn_norm, eps,
                                      hnext, st->proj));
                 std::swap(hcur, hnext);
+            }
+        } else if (ly.rec) {
+            // A split-K plan leaves its partials in contrib (free between the
+            // residual add and out_proj); the conv front end and the gated
+            // norm sum them as they read (up to 4, as contrib allows).
+            const gd_gemm_plan pi = gd_gemm_choose(ctx, N, ly.in_proj.K, ly.in_proj.R, GD_F16);
+            if (pi.split > 1 && pi.split <= 4 &&
+                (size_t)pi.split * N * RP <= (size_t)8 * st->c.max_batch * E) {
+                R_(gd_gemm_launch(ctx, &ly.in_proj, N, st->xn16, GD_F16, st->contrib, GD_F32, pi));
+                pin = st->contrib;
+                np = pi.split;
+            } else {
+                R_(gd_q2_0_gemm(ctx, &ly.in_proj, N, st->xn16, GD_F16, st->proj, GD_F32));
             }
         } else {
             R_(gd_q2_0_gemm(ctx, &ly.in_proj, N, st->xn16, GD_F16, st->proj, GD_F32));
@@ -858,9 +894,12 @@ int forward(gd_stack *st, int N, bool decode) {
                                  ly.rec_state, st->o32, qScale, eps));
             } else {
                 const int64_t tasks = (int64_t)(st->convDim / HD) * ((N + CT - 1) / CT);
-                K_(k_gdn_conv_prefill, dim3(gd_blocks(tasks, 4)), dim3(256), 0, s, st->proj,
-                   (int64_t)RP, ly.conv_state, ly.conv_w, st->conv_out, st->convDim, 2 * nK, N, eps,
-                   off_b, off_a, ly.dt, ly.a_neg, st->beta, st->g, nV);
+                const int64_t pstr = (int64_t)N * RP;
+#define GD_CONV(NP_) K_(k_gdn_conv_prefill<NP_>, dim3(gd_blocks(tasks, 4)), dim3(256), 0, s, pin, \
+                        (int64_t)RP, pstr, ly.conv_state, ly.conv_w, st->conv_out, st->convDim, \
+                        2 * nK, N, eps, off_b, off_a, ly.dt, ly.a_neg, st->beta, st->g, nV)
+                if (np == 1) GD_CONV(1); else if (np == 2) GD_CONV(2); else if (np == 3) GD_CONV(3); else GD_CONV(4);
+#undef GD_CONV
                 R_(gd_gdn_prefill(ctx, N, nV, nK, c.d_state, c.d_state, st->conv_out,
                                   st->convDim, st->conv_out + st->keyDim, st->convDim,
                                   st->conv_out + 2 * st->keyDim, st->convDim, GD_F32, st->g,
@@ -868,8 +907,13 @@ int forward(gd_stack *st, int N, bool decode) {
                                   64));
             }
             if (!(decode && nK == nV && c.d_state == HD))
-                K_(k_onorm_silu, dim3(gd_blocks((int64_t)N * nV, 4)), dim3(256), 0, s, st->o32,
-                   st->proj, (int64_t)RP, off_z, ly.ssm_norm, st->a16, nV, N, eps);
+            {
+                const int64_t pstr = (int64_t)N * RP;
+#define GD_ONORM(NP_) K_(k_onorm_silu<NP_>, dim3(gd_blocks((int64_t)N * nV, 4)), dim3(256), 0, s, \
+                         st->o32, pin, (int64_t)RP, pstr, off_z, ly.ssm_norm, st->a16, nV, N, eps)
+                if (np == 1) GD_ONORM(1); else if (np == 2) GD_ONORM(2); else if (np == 3) GD_ONORM(3); else GD_ONORM(4);
+#undef GD_ONORM
+            }
         } else {
             const float scale = 1.0f / sqrtf((float)HD);
             if (decode) {
