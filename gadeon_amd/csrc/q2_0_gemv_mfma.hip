@@ -567,8 +567,11 @@ int gd_gemv_ksplit(gd_ctx *ctx, int64_t K, int64_t R) {
     double best_cost = 1e30;
     for (int z = 1; z <= 4; z++) {
         const Split sp = plan(nsets, steps, z, cus, LDS_BYTES - xlds, 1);
+        // Items of the busiest workgroup (~0.2 us each), plus what each
+        // extra partial costs the consumer that sums it (~0.6-0.9 us
+        // measured on the fused-input GEMV: four items).
         const double cost = (double)((sp.grid * sp.nz + cus - 1) / cus) * sp.per * sp.ksteps +
-                            2.0 * (sp.nz - 1);
+                            4.0 * (sp.nz - 1);
         if (cost < best_cost - 1e-9) {
             best_cost = cost;
             best = sp.nz;
