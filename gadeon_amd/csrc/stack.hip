@@ -486,7 +486,9 @@ __global__ __launch_bounds__(256) void k_attn_prefill(
         bmax = fmaxf(bmax, __shfl_xor(bmax, 16, 64));
         bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
         const float mn = fmaxf(m, bmax);                  // finite: key k0 <= my_pos
-        const float alpha = expf(m - mn);
+        // The softmax exponents are <= 0 (or -inf for masked keys: 0), where
+        // the hardware exp2 behind __expf is accurate to a few ulp.
+        const float alpha = __expf(m - mn);
         m = mn;
         l *= alpha;
 #pragma unroll
@@ -496,7 +498,7 @@ __global__ __launch_bounds__(256) void k_attn_prefill(
         for (int kt = 0; kt < 2; kt++)
 #pragma unroll
             for (int v = 0; v < 4; v++) {
-                const float pv = expf(sc[kt][v] - mn);
+                const float pv = __expf(sc[kt][v] - mn);
                 l += pv;
                 const f16 hi = (f16)pv;
                 ph[4 * kt + v] = hi;
