@@ -285,9 +285,9 @@ def test_gemm_swiglu_vs_oracle(ctx, T, K, ff):
     """SwiGLU epilogue: f16(silu(X gate^T) * (X up^T)) against the oracle
     GEMV rows (ragged T and ff = 208, 13 groups of 16, exercise partial
     tiles).  At T=512, ff=17408 the columns run as two launches (16384
-    columns of 256-column tiles, then 1024 of another tile): K=256 checks
-    every column, the full-size case the launch and tile boundaries and 64
-    sampled columns."""
+    columns of 256-column tiles, then 1024 of another tile, K-split at
+    K=5120): every column is checked, on ten tokens around the token-tile
+    boundaries when T is large."""
     R = 2 * ff
     blocks = O.lcg_q2_0(K, R, K + ff)
     w = upload_w(ctx, blocks, K, R)
@@ -295,11 +295,7 @@ def test_gemm_swiglu_vs_oracle(ctx, T, K, ff):
     dX, dO = ctx.put(Xh.view(np.uint16)), ctx.alloc(T * ff * 2)
     ctx.gd_q2_0_gemm_swiglu(C.byref(w), T, dX, dO)
     out = ctx.get(dO, (T, ff), np.float16).astype(np.float32)
-    if ff <= 1024 or K <= 256:
-        rows = np.arange(ff)
-    else:
-        edges = [0, 15, 16, 255, 256, 16383, 16384, 16399, 17407]
-        rows = np.union1d(edges, np.random.default_rng(3).choice(ff, 64, replace=False))
+    rows = np.arange(ff)
     blk = blocks.reshape(R, -1)
     g = np.ascontiguousarray(blk[rows]); u = np.ascontiguousarray(blk[rows + ff])
     toks = range(T) if T <= 64 else (0, 1, 63, 64, 127, 128, 200, 255, 256, T - 1)
@@ -309,6 +305,10 @@ def test_gemm_swiglu_vs_oracle(ctx, T, K, ff):
         uv = O.q2_0_matvec(u, K, len(rows), x, threads=8)
         want = (silu(gv) * uv).astype(np.float16).astype(np.float32)
         assert rel_diff(out[t, rows], want) < 2e-3, t
+        # The last 1024 columns on their own (the second launch at ff=17408),
+        # so that an error there is not diluted by the rest of the row.
+        tail = slice(max(0, ff - 1024), ff)
+        assert rel_diff(out[t, tail], want[tail]) < 2e-3, t
     ctx.free(dX)
     ctx.free(dO)
     free_w(ctx, w)
