@@ -62,12 +62,14 @@ def margin_ok(logits):
 
 # nk = 4: every value head has its own key head.  A 34-token prompt ends with
 # a 2-token chunk, shorter than the conv window: its new conv ring mixes the
-# old ring with the chunk's inputs.
-@pytest.mark.parametrize("nk,plen", [(2, 40), (4, 40), (4, 34)])
-def test_stack_prefill_decode_generate(ctx, nk, plen):
+# old ring with the chunk's inputs.  max_batch = 64 takes the 40-token prompt
+# as one chunk, where the GDN in_proj's split-K partials fit the residual
+# partials buffer and are summed by the kernels that read them.
+@pytest.mark.parametrize("nk,plen,mb", [(2, 40, 32), (4, 40, 32), (4, 34, 32), (2, 40, 64)])
+def test_stack_prefill_decode_generate(ctx, nk, plen, mb):
     """nk = 2 shares key heads between value heads (separate conv, step and
     gated-norm kernels in decode); nk = 4 takes the fused one-launch step."""
-    cfg, st = make_stack(ctx, n_k_head=nk)
+    cfg, st = make_stack(ctx, n_k_head=nk, max_batch=mb)
     lib = ctx.lib
     try:
         read = tensor_reader(ctx, st)
