@@ -179,6 +179,9 @@ __global__ __launch_bounds__(256) void gdn_prep(PrepArgs a) {
     // K K^T -> A (s < t) and Q K^T -> P (s <= t), lower tiles on the matrix
     // cores; P's upper tiles are written as zeros.
     constexpr int NB = CP / 16;
+    // Unrolled: a wave's tiles are independent, so their LDS reads, MFMA
+    // chains and stores can overlap.
+#pragma unroll
     for (int tile = wave; tile < 2 * NB * NB; tile += 4) {
         const bool isP = tile >= NB * NB;
         const int tt = isP ? tile - NB * NB : tile;
