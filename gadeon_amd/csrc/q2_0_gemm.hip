@@ -518,13 +518,15 @@ int gd_gemm_launch(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, int x
 }
 
 // SwiGLU GEMM: w holds [gate; up] (R = 2 * ff rows), X f16 [T][K], out f16
-// [T][ff] = silu(gate . x) * (up . x), K unsplit.  A tile of NW waves with
-// NT fragments each covers 16 NW NT output columns.  The columns run as one
-// launch, or as two: the largest whole rounds of one tile (the big tiles
-// are the fastest per FLOP, but ff = 17408 = 17 * 2^10 never fills whole
-// rounds of them) and the rest with another -- whichever the cost model
-// (the GEMM planner's measured tile times, plus ~2 us for a second launch)
-// finds cheaper.  GADEON_GLU_CFG="MT,NT,NW" forces one launch of that tile.
+// [T][ff] = silu(gate . x) * (up . x).  A tile of NW waves with NT fragments
+// each covers 16 NW NT output columns.  The columns run as one launch, or as
+// two: the largest whole rounds of one tile (the big tiles are the fastest
+// per FLOP, but ff = 17408 = 17 * 2^10 never fills whole rounds of them) and
+// the rest with another, whose K may be split (gate/up partials in the
+// context workspace, then q2_0_glu_reduce) -- whichever the cost model (the
+// GEMM planner's measured tile times, the partials' round trip, ~2 us per
+// extra launch) finds cheaper.  GADEON_GLU_CFG="MT,NT,NW" forces one unsplit
+// launch of that tile.
 int gd_gemm_glu(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, uint16_t *out) {
     const int K = (int)w->K, R = (int)w->R, ff = R / 2;
     GD_REQUIRE(ctx, R % 32 == 0 && T > 0 && K % 128 == 0 && R < (1 << 22), "gd_gemm_glu: R=%d "
