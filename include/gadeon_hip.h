@@ -196,7 +196,9 @@ int gd_q2_0_gemm_plan(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X,
  * (R = 2 ff rows, ff a multiple of 16), X f16 [T][K], out f16 [T][ff] =
  * silu(X gate^T) * (X up^T), as gd_q2_0_gemm (f32 Y) followed by the
  * reference's silu_mul (Kernels.metal:1118-1139) and an f16 rounding, without
- * the f32 intermediate.  No counterpart in the reference as one call. */
+ * the f32 intermediate (the columns of a second launch may go through f32
+ * K-split partials in the context workspace, which the call may grow).  No
+ * counterpart in the reference as one call. */
 int gd_q2_0_gemm_swiglu(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X,
                         uint16_t *out);
 
