@@ -188,6 +188,11 @@ __global__ __launch_bounds__(64 * GS_W) void k_gdn_step(
     const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     float *Sh = S + (int64_t)h * HD * HD;
+    // The gated norm's inputs (wave 0, at the end) are requested first, so
+    // they are in registers by then.
+    const float *zr = proj + off_z + h * HD;
+    const float zv0 = wave == 0 ? zr[lane] : 0.f, zv1 = wave == 0 ? zr[lane + 64] : 0.f;
+    const float nw0 = wave == 0 ? onw[lane] : 0.f, nw1 = wave == 0 ? onw[lane + 64] : 0.f;
     // State loads first: they are the bandwidth.
     float s0[GS_R], s1[GS_R];
 #pragma unroll
@@ -278,9 +283,8 @@ __global__ __launch_bounds__(64 * GS_W) void k_gdn_step(
         o1 *= rq * qScale;
         const float ss = gd_wave_sum(o0 * o0 + o1 * o1);
         const float sc = 1.0f / sqrtf(ss / (float)HD + eps);
-        const float *z = proj + off_z + h * HD;
-        out[h * HD + lane] = gd_f2h(o0 * sc * onw[lane] * gd_silu(z[lane]));
-        out[h * HD + lane + 64] = gd_f2h(o1 * sc * onw[lane + 64] * gd_silu(z[lane + 64]));
+        out[h * HD + lane] = gd_f2h(o0 * sc * nw0 * gd_silu(zv0));
+        out[h * HD + lane + 64] = gd_f2h(o1 * sc * nw1 * gd_silu(zv1));
     }
 }
 
