@@ -27,6 +27,7 @@ _PROTOS = {
     "or_q2_0_dequant": (None, [_vp, _sz, _vp]),
     "or_q2_0_matvec": (None, [_vp, _i64, _i64, _vp, _vp, _i]),
     "or_q2_0_matvec_f64": (None, [_vp, _i64, _i64, _vp, _vp]),
+    "or_q2_0_matmat": (None, [_vp, _i64, _i64, _i64, _vp, _vp, _i]),
     "or_silu": (_f, [_f]),
     "or_sigmoid": (_f, [_f]),
     "or_softplus": (_f, [_f]),
@@ -111,6 +112,15 @@ def q2_0_matvec(blocks: np.ndarray, K: int, M: int, x: np.ndarray, threads: int 
     x = np.ascontiguousarray(x, np.float32)
     out = np.empty(M, np.float32)
     lib().or_q2_0_matvec(P(blocks), K, M, P(x), P(out), threads)
+    return out
+
+
+def q2_0_matmat(blocks: np.ndarray, K: int, M: int, X: np.ndarray, threads: int = 1) -> np.ndarray:
+    """X [T][K] -> [T][M]: T mat-vecs, each bit-identical to q2_0_matvec."""
+    X = np.ascontiguousarray(X, np.float32)
+    T = X.shape[0]
+    out = np.empty((T, M), np.float32)
+    lib().or_q2_0_matmat(P(blocks), K, M, T, P(X), P(out), threads)
     return out
 
 
@@ -239,19 +249,30 @@ class OrStack(C.Structure):
 
 
 _PROTOS["or_stack_token"] = (None, [C.POINTER(OrStack), _i, _i, _vp, _vp])
+_PROTOS["or_stack_prefill"] = (None, [C.POINTER(OrStack), _vp, _i, _i, _vp, _vp])
+
+STAGE_MV, STAGE_KV = 1, 2       # OR_STAGE_* of gd_oracle.h
 
 
 class Stack:
-    """CPU restatement of BonsaiEngine (token by token) over given weights.
+    """CPU restatement of BonsaiEngine over given weights.
 
     `tensors(layer, name)` must return a GGUF-block uint8 array for Q2_0
-    tensors and an f32 array otherwise (layer -1: global tensors)."""
+    tensors and an f32 array otherwise (layer -1: global tensors).
+
+    With stage_f16, `prefill` rounds every mat-vec input to f16 (the reference
+    GPU prefill GEMM stages half tiles, Kernels.metal:428) and `token` does not
+    (its decode GEMV reads f32 x, Kernels.metal:32-40) unless decode_f16 is
+    set; cached K/V are always rounded (half KV pages)."""
 
     Q2 = {"rec": ("attn_qkv", "attn_gate", "ssm_beta", "ssm_alpha", "ssm_out"),
           "att": ("attn_q", "attn_k", "attn_v", "attn_output")}
 
-    def __init__(self, cfg: dict, tensors, stage_f16: bool = True, threads: int = 8):
+    def __init__(self, cfg: dict, tensors, stage_f16: bool = True, threads: int = 8,
+                 decode_f16: bool = False):
         self.cfg = cfg
+        self.stage_prefill = (STAGE_MV | STAGE_KV) if stage_f16 else 0
+        self.stage_decode = (STAGE_KV | (STAGE_MV if decode_f16 else 0)) if stage_f16 else 0
         self.keep = []
         n = cfg["n_layer"]
         self.layers = (OrStackLayer * n)()
@@ -285,7 +306,7 @@ class Stack:
                   "rope_base", "eps", "n_vocab", "d_state", "n_k_head", "n_v_head", "d_conv",
                   "max_ctx"):
             setattr(st, k, cfg[k])
-        st.stage_f16 = 1 if stage_f16 else 0
+        st.stage_f16 = self.stage_decode
         st.threads = threads
         st.layers = self.layers
         st.embd = ptr(tensors(-1, "token_embd"))
@@ -294,11 +315,24 @@ class Stack:
         self.pos = 0
 
     def token(self, tok: int):
-        """Advance one token; returns (hidden, logits)."""
+        """Advance one token (decode); returns (hidden, logits)."""
         h = np.empty(self.cfg["n_embd"], np.float32)
         lg = np.empty(self.cfg["n_vocab"], np.float32)
+        self.st.stage_f16 = self.stage_decode
         lib().or_stack_token(C.byref(self.st), tok, self.pos, P(h), P(lg))
         self.pos += 1
+        return h, lg
+
+    def prefill(self, ids):
+        """Advance over a prompt chunk (the same per-token arithmetic as
+        `token` per id, with prefill staging); returns the last token's
+        (hidden, logits)."""
+        ids = np.ascontiguousarray(ids, np.int32)
+        h = np.empty(self.cfg["n_embd"], np.float32)
+        lg = np.empty(self.cfg["n_vocab"], np.float32)
+        self.st.stage_f16 = self.stage_prefill
+        lib().or_stack_prefill(C.byref(self.st), P(ids), ids.size, self.pos, P(h), P(lg))
+        self.pos += ids.size
         return h, lg
 
     def layer_state(self, il: int, name: str) -> np.ndarray:

@@ -159,8 +159,21 @@ struct mv_job {
     float *out;
 };
 
+/* x with its bits cleared unless `bit` is set: adding it to a sum is the same
+ * as adding x under `if (bit)`, since the sums below start at +0 and so are
+ * never -0 (s + (+0) == s exactly for every other s). */
+static inline float masked(float x, uint32_t bit) {
+    uint32_t u;
+    memcpy(&u, &x, 4);
+    u &= 0u - bit;
+    memcpy(&x, &u, 4);
+    return x;
+}
+
 /* Quant.swift:53-73, one row: per block lo/hi/sy sums in weight order, then
- * acc += d * (lo + 2*hi - sy). */
+ * acc += d * (lo + 2*hi - sy).  The conditional adds of the reference
+ * (`if code & 1 { lo += x }`) are written as adds of masked values, which give
+ * the same sums without a data-dependent branch per weight. */
 static void *mv_rows(void *arg) {
     const struct mv_job *j = (const struct mv_job *)arg;
     const int64_t nblk = j->K / 128, rowBytes = nblk * 34;
@@ -173,11 +186,11 @@ static void *mv_rows(void *arg) {
             const uint8_t *qs = p + 2;
             float lo = 0, hi = 0, sy = 0;
             for (int jj = 0; jj < 128; jj++) {
-                const uint8_t code = (qs[jj >> 2] >> ((jj & 3) << 1)) & 3;
+                const uint32_t code = (qs[jj >> 2] >> ((jj & 3) << 1)) & 3;
                 const float xv = j->x[k + jj];
                 sy += xv;
-                if (code & 1) lo += xv;
-                if (code & 2) hi += xv;
+                lo += masked(xv, code & 1);
+                hi += masked(xv, code >> 1);
             }
             acc += d * (lo + 2 * hi - sy);
             p += 34;
@@ -188,21 +201,102 @@ static void *mv_rows(void *arg) {
     return NULL;
 }
 
+static void run_jobs(void *(*fn)(void *), void *jobs, size_t job_size, int n) {
+    pthread_t tid[256];
+    if (n == 1) { fn(jobs); return; }
+    for (int t = 0; t < n; t++) pthread_create(&tid[t], NULL, fn, (char *)jobs + t * job_size);
+    for (int t = 0; t < n; t++) pthread_join(tid[t], NULL);
+}
+
 void or_q2_0_matvec(const uint8_t *w, int64_t K, int64_t M, const float *x, float *out,
                     int threads) {
     if (threads < 1) threads = 1;
     if (threads > M) threads = (int)(M > 0 ? M : 1);
     struct mv_job jobs[256];
-    pthread_t tid[256];
     if (threads > 256) threads = 256;
     for (int t = 0; t < threads; t++) {
         jobs[t].w = w; jobs[t].K = K; jobs[t].x = x; jobs[t].out = out;
         jobs[t].m0 = M * t / threads;
         jobs[t].m1 = M * (t + 1) / threads;
     }
-    if (threads == 1) { mv_rows(&jobs[0]); return; }
-    for (int t = 0; t < threads; t++) pthread_create(&tid[t], NULL, mv_rows, &jobs[t]);
-    for (int t = 0; t < threads; t++) pthread_join(tid[t], NULL);
+    run_jobs(mv_rows, jobs, sizeof jobs[0], threads);
+}
+
+/* ---- the same mat-vec for T tokens at once ---------------------------------
+ * The reference CPU engine has no batched Q2_0 kernel: prefill is T separate
+ * Q2_0.matvec calls (BonsaiEngine.swift:33-37).  or_q2_0_matmat computes
+ * exactly those T results: each token's lo/hi/sy/acc sums are formed in
+ * mv_rows's order, and only the lanes of a vector hold different tokens.  A
+ * thread takes a range of rows and walks them block by block for one tile of
+ * MM_TT tokens, so the tile's x slice of a block stays in L1. */
+#define MM_TT 16
+typedef float mm_vf __attribute__((vector_size(MM_TT * 4)));
+typedef uint32_t mm_vu __attribute__((vector_size(MM_TT * 4)));
+
+struct mm_job {
+    const uint8_t *w;
+    int64_t K, m0, m1, T, Tp;
+    const float *xt;       /* [Tp/MM_TT][K][MM_TT], zero padded */
+    float *acc;            /* [m1-m0][MM_TT] scratch */
+    float *out;            /* [T][M] */
+    int64_t M;
+};
+
+__attribute__((target_clones("avx512f", "avx2", "default")))
+static void *mm_rows(void *arg) {
+    const struct mm_job *j = (const struct mm_job *)arg;
+    const int64_t nblk = j->K / 128, rowBytes = nblk * 34, nr = j->m1 - j->m0;
+    for (int64_t t0 = 0; t0 < j->Tp; t0 += MM_TT) {
+        const float *xt = j->xt + t0 * j->K;
+        mm_vf *acc = (mm_vf *)j->acc;
+        for (int64_t r = 0; r < nr; r++) acc[r] = (mm_vf){0};
+        for (int64_t b = 0; b < nblk; b++) {
+            const mm_vf *xb = (const mm_vf *)(xt + b * 128 * MM_TT);
+            for (int64_t r = 0; r < nr; r++) {
+                const uint8_t *p = j->w + (j->m0 + r) * rowBytes + b * 34;
+                const float d = or_h2f((uint16_t)(p[0] | (p[1] << 8)));
+                const uint8_t *qs = p + 2;
+                mm_vf lo = {0}, hi = {0}, sy = {0};
+                for (int jj = 0; jj < 128; jj++) {
+                    const uint32_t code = (qs[jj >> 2] >> ((jj & 3) << 1)) & 3;
+                    const mm_vf xv = xb[jj];
+                    const mm_vu m1 = (mm_vu){0} - (code & 1), m2 = (mm_vu){0} - (code >> 1);
+                    sy += xv;
+                    lo += (mm_vf)((mm_vu)xv & m1);
+                    hi += (mm_vf)((mm_vu)xv & m2);
+                }
+                acc[r] += d * (lo + 2 * hi - sy);
+            }
+        }
+        for (int64_t r = 0; r < nr; r++)
+            for (int t = 0; t < MM_TT && t0 + t < j->T; t++)
+                j->out[(t0 + t) * j->M + j->m0 + r] = acc[r][t];
+    }
+    return NULL;
+}
+
+void or_q2_0_matmat(const uint8_t *w, int64_t K, int64_t M, int64_t T, const float *X,
+                    float *out, int threads) {
+    if (T <= 0 || M <= 0) return;
+    if (threads < 1) threads = 1;
+    if (threads > M) threads = (int)M;
+    if (threads > 256) threads = 256;
+    const int64_t Tp = (T + MM_TT - 1) / MM_TT * MM_TT;
+    float *xt = (float *)aligned_alloc(64, (size_t)(Tp * K * 4));
+    for (int64_t t0 = 0; t0 < Tp; t0 += MM_TT)
+        for (int64_t k = 0; k < K; k++)
+            for (int t = 0; t < MM_TT; t++)
+                xt[t0 * K + k * MM_TT + t] = t0 + t < T ? X[(t0 + t) * K + k] : 0.0f;
+    struct mm_job jobs[256];
+    float *acc = (float *)aligned_alloc(64, (size_t)(M * MM_TT * 4));
+    for (int t = 0; t < threads; t++) {
+        const int64_t m0 = M * t / threads, m1 = M * (t + 1) / threads;
+        struct mm_job jb = {w, K, m0, m1, T, Tp, xt, acc + m0 * MM_TT, out, M};
+        jobs[t] = jb;
+    }
+    run_jobs(mm_rows, jobs, sizeof jobs[0], threads);
+    free(acc);
+    free(xt);
 }
 
 void or_q2_0_matvec_f64(const uint8_t *w, int64_t K, int64_t M, const double *x, double *out) {

@@ -36,6 +36,10 @@ void or_q2_0_dequant(const uint8_t *blocks, size_t n, float *out);
 /* Quant.swift:36-77; rows split over `threads` pthreads (concurrentPerform, :52). */
 void or_q2_0_matvec(const uint8_t *w, int64_t K, int64_t M, const float *x, float *out,
                     int threads);
+/* The same T times over X[T][K] -> out[T][M] (token t's result is bit-identical
+ * to or_q2_0_matvec of X[t]; prefill is T mat-vecs, BonsaiEngine.swift:33-37). */
+void or_q2_0_matmat(const uint8_t *w, int64_t K, int64_t M, int64_t T, const float *X,
+                    float *out, int threads);
 /* Independent f64 brute force: out[m] = sum_k (code-1)*d*x[k] in double. */
 void or_q2_0_matvec_f64(const uint8_t *w, int64_t K, int64_t M, const double *x, double *out);
 
@@ -103,16 +107,23 @@ typedef struct or_stack {
     int n_layer, n_embd, n_ff, n_head, n_head_kv, head_dim, n_rot;
     float rope_base, eps;
     int n_vocab, d_state, n_k_head, n_v_head, d_conv, max_ctx;
-    int stage_f16;     /* round matvec inputs and K/V to f16 as the reference GPU does */
+    int stage_f16;     /* OR_STAGE_* bits: f16 rounding as the reference GPU path does */
     int threads;
     or_stack_layer *layers;
     const uint8_t *embd;                        /* tied token_embd / lm_head */
     const float *out_norm;
 } or_stack;
 
+#define OR_STAGE_MV 1   /* mat-vec inputs (the prefill GEMM's half tiles, Kernels.metal:428) */
+#define OR_STAGE_KV 2   /* cached K/V (half KV pages, Kernels.metal:1446-1457) */
+
 /* BonsaiEngine.forward for one token at position pos: hidden_out[n_embd] is
  * the post-final-norm hidden; logits_out[n_vocab] may be NULL. */
 void or_stack_token(or_stack *st, int token, int pos, float *hidden_out, float *logits_out);
+/* T tokens at positions pos0.. with the same per-token arithmetic as T calls
+ * of or_stack_token, run layer by layer; hidden/logits of the last token. */
+void or_stack_prefill(or_stack *st, const int *tokens, int T, int pos0, float *hidden_out,
+                      float *logits_out);
 
 #ifdef __cplusplus
 }

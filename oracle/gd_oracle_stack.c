@@ -5,10 +5,19 @@
  * Follows BonsaiEngine.forward (LLM/src/SIMD/BonsaiEngine.swift:155-178),
  * GDN.step (LLM/src/SIMD/GDN.swift:20-120) and Attn.step
  * (LLM/src/SIMD/Attention.swift:72-139) in their operation order, all f32.
- * With stage_f16 set, the input of every Q2_0 mat-vec and every cached K/V
- * value is rounded to f16 first: the reference GPU path stages GEMM operands
- * as half (Kernels.metal:428) and keeps its KV pages half (MetalKVPool.swift,
+ * stage_f16 is a bit set: OR_STAGE_MV rounds the input of every Q2_0 mat-vec
+ * to f16 first, as the reference GPU's prefill GEMM stages its operands
+ * (Kernels.metal:428; its decode GEMV reads f32 x, Kernels.metal:32-40, so a
+ * caller leaves the bit clear for decode); OR_STAGE_KV rounds every cached
+ * K/V value, as the reference's half KV pages hold them (MetalKVPool.swift,
  * kv_append Kernels.metal:1446-1457).
+ *
+ * or_stack_prefill runs T tokens layer by layer with the same per-token
+ * arithmetic as T calls of or_stack_token: a layer's mat-vecs go through
+ * or_q2_0_matmat (bit-identical per token), and the recurrent and attention
+ * steps walk the tokens in order, so token t sees exactly the states tokens
+ * < t left.  Only the hidden of the last token reaches the final norm and the
+ * logits, which is all a prefill returns.
  */
 #include "gd_oracle.h"
 
@@ -16,31 +25,36 @@
 #include <stdlib.h>
 #include <string.h>
 
-static void stage(const or_stack *st, const float *x, float *y, int64_t n) {
-    for (int64_t i = 0; i < n; i++) y[i] = st->stage_f16 ? or_h2f(or_f2h(x[i])) : x[i];
+static void stage(int on, const float *x, float *y, int64_t n) {
+    for (int64_t i = 0; i < n; i++) y[i] = on ? or_h2f(or_f2h(x[i])) : x[i];
 }
 
 static void matvec(const or_stack *st, const uint8_t *w, int64_t K, int64_t M, const float *x,
                    float *out) {
     float *xs = (float *)malloc(sizeof(float) * K);
-    stage(st, x, xs, K);
+    stage(st->stage_f16 & OR_STAGE_MV, x, xs, K);
     or_q2_0_matvec(w, K, M, xs, out, st->threads);
     free(xs);
 }
 
-/* GDN.step (GDN.swift:20-120) */
-static void gdn_step(or_stack *st, or_stack_layer *L, const float *n, float *out) {
+/* T mat-vecs: X [T][K] -> out [T][M]. */
+static void matmat(const or_stack *st, const uint8_t *w, int64_t K, int64_t M, int64_t T,
+                   const float *X, float *out) {
+    float *xs = (float *)malloc(sizeof(float) * K * T);
+    stage(st->stage_f16 & OR_STAGE_MV, X, xs, K * T);
+    or_q2_0_matmat(w, K, M, T, xs, out, st->threads);
+    free(xs);
+}
+
+/* The recurrent part of GDN.step (GDN.swift:39-115) for one token, from its
+ * projections qkv [convDim], z [valDim], bp, ap [nV] to the gated output o
+ * [valDim] (the input of ssm_out); qkv is used as scratch. */
+static void gdn_token(or_stack *st, or_stack_layer *L, float *qkv, const float *z,
+                      const float *bp, const float *ap, float *o) {
     const int dS = st->d_state, nK = st->n_k_head, nV = st->n_v_head;
     const int keyDim = dS * nK, valDim = dS * nV, convDim = 2 * keyDim + valDim;
-    const int E = st->n_embd;
-    float *qkv = malloc(sizeof(float) * convDim), *z = malloc(sizeof(float) * valDim);
-    float *bp = malloc(sizeof(float) * nV), *ap = malloc(sizeof(float) * nV);
     float *beta = malloc(sizeof(float) * nV), *g = malloc(sizeof(float) * nV);
-    float *conv = malloc(sizeof(float) * convDim), *o = malloc(sizeof(float) * valDim);
-    matvec(st, L->wqkv, E, convDim, n, qkv);
-    matvec(st, L->wgate, E, valDim, n, z);
-    matvec(st, L->wbeta, E, nV, n, bp);
-    matvec(st, L->walpha, E, nV, n, ap);
+    float *conv = malloc(sizeof(float) * convDim);
     or_gdn_gate(bp, ap, L->dt, L->a_neg, beta, g, nV, nV);
     or_gdn_conv(qkv, L->conv_state, L->conv_w, conv, convDim, st->d_conv);
     or_l2norm_rows(conv, dS, nK, st->eps);               /* q */
@@ -50,34 +64,60 @@ static void gdn_step(or_stack *st, or_stack_layer *L, const float *n, float *out
                 qScale);
     or_rmsnorm_rows(o, dS, nV, L->ssm_norm, st->eps);
     for (int i = 0; i < valDim; i++) o[i] *= or_silu(z[i]);
-    matvec(st, L->ssm_out, valDim, E, o, out);
-    free(qkv); free(z); free(bp); free(ap); free(beta); free(g); free(conv); free(o);
+    free(beta); free(g); free(conv);
 }
 
-/* Attn.step (Attention.swift:72-139), KV cache held contiguously by position. */
-static void attn_step(or_stack *st, or_stack_layer *L, const float *n, int pos, float *out) {
-    const int hd = st->head_dim, nH = st->n_head, nKV = st->n_head_kv, E = st->n_embd;
+/* GDN.step (GDN.swift:20-120) over T tokens: nrm [T][E] -> out [T][E]. */
+static void gdn_layer(or_stack *st, or_stack_layer *L, int T, const float *nrm, float *out) {
+    const int dS = st->d_state, nK = st->n_k_head, nV = st->n_v_head;
+    const int keyDim = dS * nK, valDim = dS * nV, convDim = 2 * keyDim + valDim;
+    const int E = st->n_embd;
+    float *qkv = malloc(sizeof(float) * convDim * T), *z = malloc(sizeof(float) * valDim * T);
+    float *bp = malloc(sizeof(float) * nV * T), *ap = malloc(sizeof(float) * nV * T);
+    float *o = malloc(sizeof(float) * valDim * T);
+    if (T == 1) {
+        matvec(st, L->wqkv, E, convDim, nrm, qkv);
+        matvec(st, L->wgate, E, valDim, nrm, z);
+        matvec(st, L->wbeta, E, nV, nrm, bp);
+        matvec(st, L->walpha, E, nV, nrm, ap);
+    } else {
+        matmat(st, L->wqkv, E, convDim, T, nrm, qkv);
+        matmat(st, L->wgate, E, valDim, T, nrm, z);
+        matmat(st, L->wbeta, E, nV, T, nrm, bp);
+        matmat(st, L->walpha, E, nV, T, nrm, ap);
+    }
+    for (int t = 0; t < T; t++)
+        gdn_token(st, L, qkv + (int64_t)t * convDim, z + (int64_t)t * valDim, bp + (int64_t)t * nV,
+                  ap + (int64_t)t * nV, o + (int64_t)t * valDim);
+    if (T == 1) matvec(st, L->ssm_out, valDim, E, o, out);
+    else matmat(st, L->ssm_out, valDim, E, T, o, out);
+    free(qkv); free(z); free(bp); free(ap); free(o);
+}
+
+/* The attention part of Attn.step (Attention.swift:79-134) for one token at
+ * position pos, from its projections qFull [2 nH hd] (per head q | gate), k, v
+ * [nKV hd] to the gated output ao [nH hd] (the input of wo).  The KV cache is
+ * held contiguously by position. */
+static void attn_token(or_stack *st, or_stack_layer *L, const float *qFull, float *k, float *v,
+                       int pos, float *ao) {
+    const int hd = st->head_dim, nH = st->n_head, nKV = st->n_head_kv;
     const int group = nH / nKV, kvDim = hd * nKV;
-    float *qFull = malloc(sizeof(float) * hd * 2 * nH), *q = malloc(sizeof(float) * hd * nH);
-    float *gate = malloc(sizeof(float) * hd * nH);
-    float *k = malloc(sizeof(float) * kvDim), *v = malloc(sizeof(float) * kvDim);
-    matvec(st, L->wq, E, hd * 2 * nH, n, qFull);
+    float *q = malloc(sizeof(float) * hd * nH), *gate = malloc(sizeof(float) * hd * nH);
     for (int h = 0; h < nH; h++)
         for (int i = 0; i < hd; i++) {
             q[h * hd + i] = qFull[h * hd * 2 + i];
             gate[h * hd + i] = qFull[h * hd * 2 + hd + i];
         }
-    matvec(st, L->wk, E, kvDim, n, k);
-    matvec(st, L->wv, E, kvDim, n, v);
     or_rmsnorm_rows(q, hd, nH, L->q_norm, st->eps);
     or_rmsnorm_rows(k, hd, nKV, L->k_norm, st->eps);
     or_rope_neox(q, hd, nH, st->n_rot, st->rope_base, pos);
     or_rope_neox(k, hd, nKV, st->n_rot, st->rope_base, pos);
-    stage(st, k, L->kcache + (int64_t)pos * kvDim, kvDim);      /* kv.append */
-    stage(st, v, L->vcache + (int64_t)pos * kvDim, kvDim);
+    stage(st->stage_f16 & OR_STAGE_KV, k, L->kcache + (int64_t)pos * kvDim, kvDim);  /* kv.append */
+    stage(st->stage_f16 & OR_STAGE_KV, v, L->vcache + (int64_t)pos * kvDim, kvDim);
     const int T = pos + 1;
     const float scale = 1 / sqrtf((float)hd);
-    float *scores = malloc(sizeof(float) * T), *ao = calloc((size_t)hd * nH, sizeof(float));
+    float *scores = malloc(sizeof(float) * T);
+    for (int i = 0; i < hd * nH; i++) ao[i] = 0;
     for (int h = 0; h < nH; h++) {
         const int kvh = h / group;
         for (int t = 0; t < T; t++) {
@@ -94,31 +134,76 @@ static void attn_step(or_stack *st, or_stack_layer *L, const float *n, int pos, 
         }
     }
     for (int i = 0; i < hd * nH; i++) ao[i] *= or_sigmoid(gate[i]);
-    matvec(st, L->wo, hd * nH, E, ao, out);
-    free(qFull); free(q); free(gate); free(k); free(v); free(scores); free(ao);
+    free(q); free(gate); free(scores);
+}
+
+/* Attn.step (Attention.swift:72-139) over T tokens at positions pos0 ..:
+ * nrm [T][E] -> out [T][E]. */
+static void attn_layer(or_stack *st, or_stack_layer *L, int T, const float *nrm, int pos0,
+                       float *out) {
+    const int hd = st->head_dim, nH = st->n_head, nKV = st->n_head_kv, E = st->n_embd;
+    const int kvDim = hd * nKV, qf = hd * 2 * nH;
+    float *qFull = malloc(sizeof(float) * qf * T), *k = malloc(sizeof(float) * kvDim * T);
+    float *v = malloc(sizeof(float) * kvDim * T), *ao = malloc(sizeof(float) * hd * nH * T);
+    if (T == 1) {
+        matvec(st, L->wq, E, qf, nrm, qFull);
+        matvec(st, L->wk, E, kvDim, nrm, k);
+        matvec(st, L->wv, E, kvDim, nrm, v);
+    } else {
+        matmat(st, L->wq, E, qf, T, nrm, qFull);
+        matmat(st, L->wk, E, kvDim, T, nrm, k);
+        matmat(st, L->wv, E, kvDim, T, nrm, v);
+    }
+    for (int t = 0; t < T; t++)
+        attn_token(st, L, qFull + (int64_t)t * qf, k + (int64_t)t * kvDim, v + (int64_t)t * kvDim,
+                   pos0 + t, ao + (int64_t)t * hd * nH);
+    if (T == 1) matvec(st, L->wo, hd * nH, E, ao, out);
+    else matmat(st, L->wo, hd * nH, E, T, ao, out);
+    free(qFull); free(k); free(v); free(ao);
+}
+
+/* BonsaiEngine.forward (BonsaiEngine.swift:155-178) for T tokens at positions
+ * pos0 .. pos0+T-1, layer by layer; the last token's final hidden and logits. */
+static void forward(or_stack *st, const int *tokens, int T, int pos0, float *hidden_out,
+                    float *logits_out) {
+    const int E = st->n_embd, FF = st->n_ff;
+    const int64_t rowBytes = E / 128 * 34;
+    float *x = malloc(sizeof(float) * E * T), *nrm = malloc(sizeof(float) * E * T);
+    float *a = malloc(sizeof(float) * E * T), *gt = malloc(sizeof(float) * FF * T);
+    float *up = malloc(sizeof(float) * FF * T);
+    for (int t = 0; t < T; t++)                                             /* embed */
+        or_q2_0_dequant(st->embd + (int64_t)tokens[t] * rowBytes, E, x + (int64_t)t * E);
+    for (int il = 0; il < st->n_layer; il++) {
+        or_stack_layer *L = &st->layers[il];
+        for (int t = 0; t < T; t++)
+            or_rmsnorm(x + (int64_t)t * E, L->attn_norm, nrm + (int64_t)t * E, E, st->eps);
+        if (L->rec) gdn_layer(st, L, T, nrm, a);
+        else attn_layer(st, L, T, nrm, pos0, a);
+        for (int64_t i = 0; i < (int64_t)E * T; i++) x[i] += a[i];
+        for (int t = 0; t < T; t++)
+            or_rmsnorm(x + (int64_t)t * E, L->post_norm, nrm + (int64_t)t * E, E, st->eps);
+        if (T == 1) {                                                       /* ffn */
+            matvec(st, L->ffn_gate, E, FF, nrm, gt);
+            matvec(st, L->ffn_up, E, FF, nrm, up);
+        } else {
+            matmat(st, L->ffn_gate, E, FF, T, nrm, gt);
+            matmat(st, L->ffn_up, E, FF, T, nrm, up);
+        }
+        for (int64_t i = 0; i < (int64_t)FF * T; i++) gt[i] = or_silu(gt[i]) * up[i];
+        if (T == 1) matvec(st, L->ffn_down, FF, E, gt, a);
+        else matmat(st, L->ffn_down, FF, E, T, gt, a);
+        for (int64_t i = 0; i < (int64_t)E * T; i++) x[i] += a[i];
+    }
+    or_rmsnorm(x + (int64_t)(T - 1) * E, st->out_norm, hidden_out, E, st->eps);
+    if (logits_out) matvec(st, st->embd, E, st->n_vocab, hidden_out, logits_out);
+    free(x); free(nrm); free(a); free(gt); free(up);
 }
 
 void or_stack_token(or_stack *st, int token, int pos, float *hidden_out, float *logits_out) {
-    const int E = st->n_embd, FF = st->n_ff;
-    const int64_t rowBytes = E / 128 * 34;
-    float *x = malloc(sizeof(float) * E), *nrm = malloc(sizeof(float) * E);
-    float *a = malloc(sizeof(float) * E), *gt = malloc(sizeof(float) * FF);
-    float *up = malloc(sizeof(float) * FF);
-    or_q2_0_dequant(st->embd + (int64_t)token * rowBytes, E, x);          /* embed */
-    for (int il = 0; il < st->n_layer; il++) {
-        or_stack_layer *L = &st->layers[il];
-        or_rmsnorm(x, L->attn_norm, nrm, E, st->eps);
-        if (L->rec) gdn_step(st, L, nrm, a);
-        else attn_step(st, L, nrm, pos, a);
-        for (int i = 0; i < E; i++) x[i] += a[i];
-        or_rmsnorm(x, L->post_norm, nrm, E, st->eps);
-        matvec(st, L->ffn_gate, E, FF, nrm, gt);                          /* ffn */
-        matvec(st, L->ffn_up, E, FF, nrm, up);
-        for (int i = 0; i < FF; i++) gt[i] = or_silu(gt[i]) * up[i];
-        matvec(st, L->ffn_down, FF, E, gt, a);
-        for (int i = 0; i < E; i++) x[i] += a[i];
-    }
-    or_rmsnorm(x, st->out_norm, hidden_out, E, st->eps);
-    if (logits_out) matvec(st, st->embd, E, st->n_vocab, hidden_out, logits_out);
-    free(x); free(nrm); free(a); free(gt); free(up);
+    forward(st, &token, 1, pos, hidden_out, logits_out);
+}
+
+void or_stack_prefill(or_stack *st, const int *tokens, int T, int pos0, float *hidden_out,
+                      float *logits_out) {
+    if (T > 0) forward(st, tokens, T, pos0, hidden_out, logits_out);
 }

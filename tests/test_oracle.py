@@ -230,3 +230,49 @@ def test_conv_is_causal_fir():
     pre = np.stack([sum(xp[n + j] * cw[:, j] for j in range(kc)) for n in range(N)])
     assert np.allclose(out, pre / (1 + np.exp(-pre)), atol=1e-5)
     assert np.array_equal(ring.reshape(kc - 1, convDim), x[-(kc - 1):])
+
+
+@pytest.mark.parametrize("d,scale", [(128, 1.0), (128, 1e-4), (64, 30.0)])
+def test_l2norm_rows_pins(d, scale):
+    """Kern.l2normRows (Kernels.swift:41-52): x / sqrt(sum(x^2) + eps), with
+    the SUM of squares (not the mean, Kernels.swift:39-40) and eps inside the
+    root.  Rows of scale 1e-4 have sum(x^2) ~ d*1e-8, comparable to eps, so
+    eps placement shows; any row's result times its own norm gives x back."""
+    eps = 1e-6
+    rng = np.random.default_rng(d)
+    x = (rng.standard_normal((5, d)) * scale).astype(np.float32)
+    y = O.l2norm_rows(x.ravel(), d, eps).reshape(5, d)
+    x64 = x.astype(np.float64)
+    want = x64 / np.sqrt((x64 ** 2).sum(1, keepdims=True) + eps)
+    assert np.allclose(y, want, rtol=2e-6, atol=1e-9)
+    # a mean-based norm would differ by sqrt(d); without eps, by the eps term
+    mean_based = x64 / np.sqrt((x64 ** 2).mean(1, keepdims=True) + eps)
+    assert not np.allclose(y, mean_based, rtol=1e-2)
+    if scale == 1.0:
+        assert np.allclose((y.astype(np.float64) ** 2).sum(1), 1.0, atol=1e-5)
+    if scale == 1e-4:
+        no_eps = x64 / np.sqrt((x64 ** 2).sum(1, keepdims=True))
+        assert not np.allclose(y, no_eps, rtol=1e-3)
+
+
+def test_gate_per_head_indexing():
+    """GDN.swift:39-42 over several tokens: element i belongs to value head
+    h = i % nV and takes dt[h] and aNeg[h]; beta = sigmoid(b),
+    g = softplus(a + dt[h]) * aNeg[h], against logaddexp in f64."""
+    nV, T = 5, 7
+    rng = np.random.default_rng(17)
+    b = rng.normal(0, 2, T * nV).astype(np.float32)
+    a = rng.normal(0, 2, T * nV).astype(np.float32)
+    dt = np.linspace(-1.5, 2.0, nV).astype(np.float32)            # distinct per head
+    aNeg = -np.exp(np.linspace(-1.0, 1.0, nV)).astype(np.float32)
+    beta, g = O.gdn_gate(b, a, dt, aNeg, nV)
+    h = np.arange(T * nV) % nV
+    a64, b64 = a.astype(np.float64), b.astype(np.float64)
+    want_b = 1.0 / (1.0 + np.exp(-b64))
+    want_g = np.logaddexp(0.0, a64 + dt[h].astype(np.float64)) * aNeg[h].astype(np.float64)
+    assert np.allclose(beta, want_b, rtol=1e-6, atol=1e-7)
+    assert np.allclose(g, want_g, rtol=2e-6, atol=1e-7)
+    # a transposed head map (i // T) would not pass
+    h2 = np.arange(T * nV) // T
+    wrong = np.logaddexp(0.0, a64 + dt[h2].astype(np.float64)) * aNeg[h2].astype(np.float64)
+    assert not np.allclose(g, wrong, rtol=1e-3)

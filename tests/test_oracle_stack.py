@@ -151,3 +151,104 @@ def test_attention_first_position_is_gated_value():
     a = mv(T, "attn_output", nh * hd, E, ao.reshape(-1))
     want = O.rmsnorm((x + a).astype(np.float32), T["output_norm"], cfg["eps"])
     assert np.allclose(h, want, rtol=2e-5, atol=2e-5)
+
+
+GCFG = dict(n_layer=1, n_embd=256, n_ff=256, n_head=4, n_head_kv=2, head_dim=128, n_rot=64,
+            rope_base=1e7, eps=1e-6, n_vocab=64, attn_interval=9, d_state=128, n_k_head=1,
+            n_v_head=2, d_conv=4, max_ctx=8)
+
+
+def make_gdn_tensors(cfg, zero=("ffn_down",)):
+    E, FF, dS = cfg["n_embd"], cfg["n_ff"], cfg["d_state"]
+    nK, nV = cfg["n_k_head"], cfg["n_v_head"]
+    convDim, valDim = (2 * nK + nV) * dS, nV * dS
+    rng = np.random.default_rng(6)
+    T = {}
+    shapes = {"attn_qkv": (E, convDim), "attn_gate": (E, valDim), "ssm_beta": (E, nV),
+              "ssm_alpha": (E, nV), "ssm_out": (valDim, E), "ffn_gate": (E, FF), "ffn_up": (E, FF),
+              "ffn_down": (FF, E)}
+    for i, (name, (K, R)) in enumerate(shapes.items()):
+        T[name] = q2_blocks(K, R, 200 + i, name in zero)
+    T["token_embd"] = q2_blocks(E, cfg["n_vocab"], 98)
+    for name, n in (("attn_norm", E), ("post_attention_norm", E), ("output_norm", E),
+                    ("ssm_norm", dS)):
+        T[name] = rng.uniform(0.8, 1.2, n).astype(np.float32)
+    T["ssm_conv1d"] = rng.uniform(-0.5, 0.5, convDim * cfg["d_conv"]).astype(np.float32)
+    T["ssm_dt"] = rng.uniform(-0.5, 0.5, nV).astype(np.float32)
+    T["ssm_a"] = -rng.uniform(0.3, 2.0, nV).astype(np.float32)
+    return T
+
+
+def test_stack_gdn_layer_matches_its_definition():
+    """The stack oracle's GDN layer (GDN.step, GDN.swift:20-120, inside
+    BonsaiEngine.forward) against an independent f64 build of the same layer
+    from numpy formulas and the pinned f64 scan: projections (f64 brute-force
+    mat-vec), gates, causal conv + silu with the ring carried across tokens,
+    L2 norm of q and k, the delta-rule scan, per-head RMSNorm times ssm_norm,
+    times silu(z), then ssm_out.  ffn_down = 0, so hidden = rmsnorm(x + layer
+    output).  Three tokens, so the conv ring and the state carry over; one key
+    head shared by two value heads (hk = hv % nK)."""
+    cfg = dict(GCFG)
+    T = make_gdn_tensors(cfg)
+    st = O.Stack(cfg, lambda layer, name: T[name], stage_f16=False, threads=2)
+    E, dS, nK, nV, eps = cfg["n_embd"], cfg["d_state"], cfg["n_k_head"], cfg["n_v_head"], cfg["eps"]
+    keyDim, valDim = nK * dS, nV * dS
+    convDim = 2 * keyDim + valDim
+    mv64 = lambda name, K, R, x: O.q2_0_matvec_f64(T[name], K, R, np.asarray(x, np.float64))
+    rms = lambda x, w: x / np.sqrt(np.mean(x ** 2) + eps) * w
+    silu = lambda x: x / (1 + np.exp(-x))
+    cw = T["ssm_conv1d"].astype(np.float64).reshape(convDim, 4)
+    hist = np.zeros((3, convDim))                       # previous three conv inputs
+    S = np.zeros(nV * dS * dS)
+    for pos, tok in enumerate((9, 40, 9)):
+        h, _ = st.token(tok)
+        x = O.q2_0_dequant(T["token_embd"][tok * E // 128 * 34:(tok + 1) * E // 128 * 34],
+                           E).astype(np.float64)
+        n = rms(x, T["attn_norm"].astype(np.float64))
+        qkv, z = mv64("attn_qkv", E, convDim, n), mv64("attn_gate", E, valDim, n)
+        bp, ap = mv64("ssm_beta", E, nV, n), mv64("ssm_alpha", E, nV, n)
+        beta = 1 / (1 + np.exp(-bp))
+        g = np.logaddexp(0, ap + T["ssm_dt"]) * T["ssm_a"]
+        win = np.vstack([hist, qkv])                    # tokens t-3 .. t
+        conv = silu((win.T * cw).sum(1))
+        hist = win[1:]
+        q = conv[:keyDim].reshape(nK, dS)
+        k = conv[keyDim:2 * keyDim].reshape(nK, dS)
+        q = q / np.sqrt((q ** 2).sum(1, keepdims=True) + eps)
+        k = k / np.sqrt((k ** 2).sum(1, keepdims=True) + eps)
+        v = conv[2 * keyDim:]
+        o = O.gdn_scan_f64(q.ravel(), k.ravel(), v, g, beta, S, nV, nK, dS, 1 / np.sqrt(dS))
+        o = o.reshape(nV, dS)
+        o = o / np.sqrt(np.mean(o ** 2, 1, keepdims=True) + eps) * T["ssm_norm"]
+        o = o.ravel() * silu(z)
+        a = mv64("ssm_out", valDim, E, o)
+        want = rms(x + a, T["output_norm"].astype(np.float64))
+        assert np.allclose(h, want, rtol=1e-4, atol=1e-4 * np.abs(want).max()), pos
+        assert np.allclose(st.layer_state(0, "ssm_state"), S, rtol=1e-4,
+                           atol=1e-4 * np.abs(S).max()), pos
+
+
+def test_prefill_is_token_serial():
+    """or_stack_prefill (layer by layer, batched mat-vecs) equals token-by-token
+    or_stack_token bit for bit: hidden, logits and every state, on a hybrid
+    geometry (GDN layers with nK < nV and a gated attention layer), with and
+    without f16 staging, over two chunks."""
+    cfg = dict(n_layer=4, n_embd=256, n_ff=384, n_head=4, n_head_kv=2, head_dim=128, n_rot=64,
+               rope_base=1e7, eps=1e-6, n_vocab=300, attn_interval=2, d_state=128, n_k_head=1,
+               n_v_head=2, d_conv=4, max_ctx=40)
+    Tg = make_gdn_tensors(cfg, zero=())
+    Ta = make_tensors(dict(cfg, n_vocab=cfg["n_vocab"]))
+    tensors = lambda layer, name: Tg[name] if name in Tg else Ta[name]
+    ids = (np.arange(29) * 13 % cfg["n_vocab"]).astype(np.int32)
+    for stage in (False, True):
+        a = O.Stack(cfg, tensors, stage_f16=stage, threads=3, decode_f16=True)
+        b = O.Stack(cfg, tensors, stage_f16=stage, threads=2, decode_f16=True)
+        ha, la = a.prefill(ids[:17])
+        ha, la = a.prefill(ids[17:])
+        for t in ids:
+            hb, lb = b.token(int(t))
+        assert np.array_equal(ha, hb) and np.array_equal(la, lb)
+        for il in (0, 2):
+            assert np.array_equal(a.layer_state(il, "ssm_state"), b.layer_state(il, "ssm_state"))
+        # one more decode token from both
+        assert np.array_equal(a.token(5)[1], b.token(5)[1])
