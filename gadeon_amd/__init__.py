@@ -50,6 +50,10 @@ _PROTOS = {
     "gd_copy": (_i, [_vp, _vp, _vp, _sz]),
     "gd_fill_u32": (_i, [_vp, _vp, C.c_uint32, _sz]),
     "gd_cast": (_i, [_vp, _vp, _i, _vp, _i, _sz]),
+    "gd_graph_begin": (_i, [_vp]),
+    "gd_graph_end": (_i, [_vp, C.POINTER(_vp)]),
+    "gd_graph_launch": (_i, [_vp, _vp]),
+    "gd_graph_destroy": (None, [_vp]),
     "gd_sync": (_i, [_vp]),
     "gd_timer_start": (_i, [_vp]),
     "gd_timer_stop": (_i, [_vp, _fp]),

@@ -15,11 +15,12 @@
 // exceeds 1 and nothing overflows however long the decay runs.
 //
 // MI355X design.  Every product above runs on v_mfma_f32_16x16x32_f16 with
-// f32 accumulation.  q, k, v enter as f16 (f32 inputs are rounded once, at
-// load, so every use of a token sees the same values).  Operands that are f32
-// by nature -- S, delta, T, beta e^G k, beta v, P -- are split into
+// f32 accumulation.  Operands that are f32 -- S, delta, T, beta e^G k,
+// beta v, P, and q, k, v themselves when they arrive as f32 -- are split into
 // hi = f16(x) and lo = f16(x - hi) and multiplied as hi*hi + hi*lo + lo*hi
-// (about 22 significant bits), so the result tracks the f32 recurrence.
+// (about 22 significant bits), so the result tracks the f32 recurrence of the
+// reference's prefill scan.  f16 q, k, v (BASELINE's prefill inputs) are used
+// as they are.
 //   gdn_prep  (value head, chunk): K K^T and Q K^T on the matrix cores give A
 //             and P; I + A is inverted in 16 x 16 blocks (diagonal blocks by
 //             forward substitution, one wave each, then the blocks below in
@@ -33,7 +34,7 @@
 //             serial part across workgroups.
 // Workspace per (head, chunk) unit, CP = max(32, C) rows (rows past the
 // chunk's tokens are zero): W hi/lo [CP][128] f16, U [CP][128] f32, P hi/lo
-// [CP][CP] f16, K^T [128][CP] f16, G [CP] f32.
+// [CP][CP] f16, K^T (hi, and lo for f32 k) [128][CP] f16, G [CP] f32.
 #include "gd_internal.h"
 
 namespace {
@@ -97,11 +98,29 @@ __device__ __forceinline__ f16x8 cvt8(const Raw8<IO> &r, bool ok) {
     return h;
 }
 
+// hi/lo split of the eight f32 values of a raw load (zeros when !ok).
+template <typename IO>
+__device__ __forceinline__ void split_raw8(const Raw8<IO> &r, bool ok, f16x8 &hi, f16x8 &lo) {
+    float x[8];
+    if constexpr (sizeof(IO) == 4) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            x[e] = ok ? r.a[e] : 0.f;
+            x[4 + e] = ok ? r.b[e] : 0.f;
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; e++) x[e] = 0.f;      // not used for f16 inputs
+    }
+    split8(x, hi, lo);
+}
+
 struct Work {
     f16 *Wh, *Wl;     // [u][CP][DK]
     float *U;         // [u][CP][DV]
     f16 *Ph, *Pl;     // [u][CP][CP]
     f16 *KT;          // [u][DK][CP]
+    f16 *KTl;         // [u][DK][CP], f32 k only: k - f16(k)
     float *G;         // [u][CP]
 };
 
@@ -117,10 +136,18 @@ struct PrepArgs {
 
 template <int CP, typename IO>
 __global__ __launch_bounds__(256) void gdn_prep(PrepArgs a) {
+    // f32 q, k, v: hi/lo pairs.  The lo halves of K and Q are needed only
+    // until A and P are formed, so they share the space of Xh and Xl, which
+    // are first written after that (and X, Y are then formed from the f32
+    // inputs themselves, re-read from L2).
+    constexpr bool HL = sizeof(IO) == 4;
     __shared__ __attribute__((aligned(16))) f16 Ks[CP][PADK];
     __shared__ __attribute__((aligned(16))) f16 QVs[CP][PADK];     // Q, later V
     __shared__ __attribute__((aligned(16))) f16 Xh[DK][CP + 8], Xl[DK][CP + 8];
     __shared__ __attribute__((aligned(16))) f16 Yh[DV][CP + 8], Yl[DV][CP + 8];
+    static_assert(sizeof(Xh) >= sizeof(Ks), "K lo must fit where Xh lives");
+    f16 (*Kl)[PADK] = reinterpret_cast<f16 (*)[PADK]>(&Xh[0][0]);
+    f16 (*Ql)[PADK] = reinterpret_cast<f16 (*)[PADK]>(&Xl[0][0]);
     __shared__ __attribute__((aligned(16))) float Af[CP][CP + 4];
     __shared__ __attribute__((aligned(16))) float Tf[CP][CP + 4];
     __shared__ __attribute__((aligned(16))) float Ms[(CP / 16 - 1) * 256];   // block products
@@ -154,9 +181,19 @@ __global__ __launch_bounds__(256) void gdn_prep(PrepArgs a) {
     for (int n = 0; n < NE; n++) {
         const int e = tid + 256 * n, t = e >> 4, i8 = (e & 15) * 8;
         const bool ok = t < L;
-        *(f16x8 *)&Ks[t][i8] = cvt8<IO>(rk[n], ok);
-        *(f16x8 *)&QVs[t][i8] = cvt8<IO>(rq[n], ok);
-        vreg[n] = cvt8<IO>(rv[n], ok);
+        if constexpr (HL) {
+            f16x8 h, l;
+            split_raw8<IO>(rk[n], ok, h, l);
+            *(f16x8 *)&Ks[t][i8] = h;
+            *(f16x8 *)&Kl[t][i8] = l;
+            split_raw8<IO>(rq[n], ok, h, l);
+            *(f16x8 *)&QVs[t][i8] = h;
+            *(f16x8 *)&Ql[t][i8] = l;
+        } else {
+            *(f16x8 *)&Ks[t][i8] = cvt8<IO>(rk[n], ok);
+            *(f16x8 *)&QVs[t][i8] = cvt8<IO>(rq[n], ok);
+            vreg[n] = cvt8<IO>(rv[n], ok);
+        }
     }
     if (wave == 0) {
         // Inclusive cumulative gate inside the chunk (wave prefix sum); rows
@@ -193,7 +230,14 @@ __global__ __launch_bounds__(256) void gdn_prep(PrepArgs a) {
                 const f16x8 av = isP ? *(const f16x8 *)&QVs[ti * 16 + lr][k0 + kg * 8]
                                      : *(const f16x8 *)&Ks[ti * 16 + lr][k0 + kg * 8];
                 const f16x8 bv = *(const f16x8 *)&Ks[si * 16 + lr][k0 + kg * 8];
-                acc = mfma(av, bv, acc);
+                if constexpr (HL) {
+                    const f16x8 al = isP ? *(const f16x8 *)&Ql[ti * 16 + lr][k0 + kg * 8]
+                                         : *(const f16x8 *)&Kl[ti * 16 + lr][k0 + kg * 8];
+                    const f16x8 bl = *(const f16x8 *)&Kl[si * 16 + lr][k0 + kg * 8];
+                    acc = mfma3(av, al, bv, bl, acc);
+                } else {
+                    acc = mfma(av, bv, acc);
+                }
             }
         }
         const int s = si * 16 + lr;
@@ -213,11 +257,13 @@ __global__ __launch_bounds__(256) void gdn_prep(PrepArgs a) {
         }
     }
     __syncthreads();
-    // V replaces Q.
+    // V replaces Q (f16 inputs; f32 ones are re-read for Y below).
+    if constexpr (!HL) {
 #pragma unroll
-    for (int n = 0; n < NE; n++) {
-        const int e = tid + 256 * n, t = e >> 4, i8 = (e & 15) * 8;
-        *(f16x8 *)&QVs[t][i8] = vreg[n];
+        for (int n = 0; n < NE; n++) {
+            const int e = tid + 256 * n, t = e >> 4, i8 = (e & 15) * 8;
+            *(f16x8 *)&QVs[t][i8] = vreg[n];
+        }
     }
     __syncthreads();
 
@@ -274,16 +320,38 @@ __global__ __launch_bounds__(256) void gdn_prep(PrepArgs a) {
     // B operands of T X and T Y, and K^T to the workspace for the scan's
     // state update (its A operand): entry (8 tokens s .. s+7, i), lanes
     // along i so that the row reads of K and V hit distinct banks.
+    // f32 inputs: k and v come from global memory (the chunk was read moments
+    // ago, so from L2), every load of an entry issued before any is used, at
+    // clamped rows (rows past the chunk are zeroed on use).
     for (int e = tid; e < DK * (CP / 8); e += 256) {
         const int s8 = (e / DK) * 8, i = e % DK;
         float xv[8], yv[8];
-        f16x8 kv;
+        f16x8 kv, kl;
+        if constexpr (HL) {
+            float kf[8], vf[8];
 #pragma unroll
-        for (int q = 0; q < 8; q++) {
-            const int s = s8 + q;
-            kv[q] = Ks[s][i];
-            xv[q] = BEs[s] * (float)kv[q];
-            yv[q] = Bs[s] * (float)QVs[s][i];
+            for (int q = 0; q < 8; q++) {
+                const int64_t tok = t0 + (s8 + q < L ? s8 + q : 0);
+                kf[q] = ((const float *)a.k)[tok * a.k_stride + (int64_t)hk * DK + i];
+                vf[q] = ((const float *)a.v)[tok * a.v_stride + (int64_t)hv * DV + i];
+            }
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                const int s = s8 + q;
+                const float kk = s < L ? kf[q] : 0.f, vv = s < L ? vf[q] : 0.f;
+                kv[q] = (f16)kk;
+                kl[q] = (f16)(kk - (float)kv[q]);
+                xv[q] = BEs[s] * kk;
+                yv[q] = Bs[s] * vv;
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                const int s = s8 + q;
+                kv[q] = Ks[s][i];
+                xv[q] = BEs[s] * (float)kv[q];
+                yv[q] = Bs[s] * (float)QVs[s][i];
+            }
         }
         f16x8 h, l;
         split8(xv, h, l);
@@ -293,6 +361,7 @@ __global__ __launch_bounds__(256) void gdn_prep(PrepArgs a) {
         *(f16x8 *)&Yh[i][s8] = h;
         *(f16x8 *)&Yl[i][s8] = l;
         *(f16x8 *)&a.w.KT[((size_t)u * DK + i) * CP + s8] = kv;
+        if constexpr (HL) *(f16x8 *)&a.w.KTl[((size_t)u * DK + i) * CP + s8] = kl;
     }
     if (tid < CP) a.w.G[(size_t)u * CP + tid] = Gs[tid];
     __syncthreads();
@@ -358,6 +427,7 @@ struct ScanChunk {
     Raw8<IO> qr[DK / 32];                 // Q row 16*wave + lr (row 0 past the chunk), raw
     f16x8 ph[CP / 32], pl[CP / 32];       // P row 16*wave + lr
     f16x8 ka[2][CP / 32];                 // K^T rows 32*wave + 16*rt + lr
+    f16x8 kal[sizeof(IO) == 4 ? 2 : 1][CP / 32];   // their lo halves (f32 k)
 };
 
 template <int CP, typename IO, typename OT>
@@ -443,9 +513,11 @@ __global__ __launch_bounds__(256) void gdn_scan(ScanArgs a) {
 #pragma unroll
         for (int rt = 0; rt < 2; rt++)
 #pragma unroll
-            for (int ks = 0; ks < CP / 32; ks++)
-                k.ka[rt][ks] = *(const f16x8 *)&a.w.KT[(u * DK + wave * 32 + rt * 16 + lr) * CP +
-                                                        ks * 32 + kg * 8];
+            for (int ks = 0; ks < CP / 32; ks++) {
+                const size_t ki = (u * DK + wave * 32 + rt * 16 + lr) * CP + ks * 32 + kg * 8;
+                k.ka[rt][ks] = *(const f16x8 *)&a.w.KT[ki];
+                if constexpr (sizeof(IO) == 4) k.kal[rt][ks] = *(const f16x8 *)&a.w.KTl[ki];
+            }
     };
 
     auto process = [&](int c) {
@@ -514,9 +586,16 @@ __global__ __launch_bounds__(256) void gdn_scan(ScanArgs a) {
 #pragma unroll
                 for (int ks = 0; ks < DK / 32; ks++) {
                     const int i0 = ks * 32 + kg * 8;
-                    const f16x8 qa = cvt8<IO>(k.qr[ks], tb + lr < L);
-                    acc = mfma(qa, *(const f16x8 *)&Sh[j][i0], acc);
-                    acc = mfma(qa, *(const f16x8 *)&Sl[j][i0], acc);
+                    if constexpr (sizeof(IO) == 4) {
+                        f16x8 qh, ql;
+                        split_raw8<IO>(k.qr[ks], tb + lr < L, qh, ql);
+                        acc = mfma3(qh, ql, *(const f16x8 *)&Sh[j][i0],
+                                    *(const f16x8 *)&Sl[j][i0], acc);
+                    } else {
+                        const f16x8 qa = cvt8<IO>(k.qr[ks], tb + lr < L);
+                        acc = mfma(qa, *(const f16x8 *)&Sh[j][i0], acc);
+                        acc = mfma(qa, *(const f16x8 *)&Sl[j][i0], acc);
+                    }
                 }
 #pragma unroll
                 for (int v = 0; v < 4; v++) acc[v] *= a.qScale * expf(Gs[tb + kg * 4 + v]);
@@ -554,8 +633,13 @@ __global__ __launch_bounds__(256) void gdn_scan(ScanArgs a) {
 #pragma unroll
                 for (int ks = 0; ks < CP / 32; ks++) {
                     const int s0 = ks * 32 + kg * 8;
-                    acc = mfma(k.ka[rt][ks], *(const f16x8 *)&Eh[j][s0], acc);
-                    acc = mfma(k.ka[rt][ks], *(const f16x8 *)&El[j][s0], acc);
+                    if constexpr (sizeof(IO) == 4) {
+                        acc = mfma3(k.ka[rt][ks], k.kal[rt][ks], *(const f16x8 *)&Eh[j][s0],
+                                    *(const f16x8 *)&El[j][s0], acc);
+                    } else {
+                        acc = mfma(k.ka[rt][ks], *(const f16x8 *)&Eh[j][s0], acc);
+                        acc = mfma(k.ka[rt][ks], *(const f16x8 *)&El[j][s0], acc);
+                    }
                 }
 #pragma unroll
                 for (int v = 0; v < 4; v++) St[j][ib + kg * 4 + v] = acc[v];
@@ -631,10 +715,11 @@ extern "C" int gd_gdn_prefill(gd_ctx *ctx, int64_t T, int nV, int nK, int dk, in
     const size_t wbytes = units * CP * DK * 2;          // each of Wh, Wl
     const size_t ubytes = units * CP * DV * 4;
     const size_t pbytes = units * CP * CP * 2;          // each of Ph, Pl
-    const size_t kbytes = units * DK * CP * 2;
+    const size_t kbytes = units * DK * CP * 2;          // K^T hi; lo too for f32 k
+    const size_t nkt = io_dtype == GD_F32 ? 2 : 1;
     const size_t gbytes = units * CP * 4;
     void *ws = nullptr;
-    int rc = gd_ctx_workspace(ctx, 2 * wbytes + ubytes + 2 * pbytes + kbytes + gbytes, &ws);
+    int rc = gd_ctx_workspace(ctx, 2 * wbytes + ubytes + 2 * pbytes + nkt * kbytes + gbytes, &ws);
     if (rc) return rc;
     uint8_t *p = (uint8_t *)ws;
     Work w;
@@ -644,6 +729,8 @@ extern "C" int gd_gdn_prefill(gd_ctx *ctx, int64_t T, int nV, int nK, int dk, in
     w.Ph = (f16 *)p;            p += pbytes;
     w.Pl = (f16 *)p;            p += pbytes;
     w.KT = (f16 *)p;            p += kbytes;
+    w.KTl = nkt == 2 ? (f16 *)p : nullptr;
+    p += (nkt - 1) * kbytes;
     w.G = (float *)p;
 
     PrepArgs pa{q, k, v, q_stride, k_stride, v_stride, g, beta, w, T, nV, nK, C, nchunks, qScale};

@@ -216,6 +216,58 @@ extern "C" int gd_timer_stop(gd_ctx *ctx, float *ms) {
     return GD_OK;
 }
 
+// ------------------------------------------------------------ graph capture
+
+struct gd_graph {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+extern "C" int gd_graph_begin(gd_ctx *ctx) {
+    GD_CHECK_CTX(ctx);
+    GD_HIP(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    return GD_OK;
+}
+
+extern "C" int gd_graph_end(gd_ctx *ctx, gd_graph **out) {
+    GD_CHECK_CTX(ctx);
+    if (out) *out = nullptr;
+    hipGraph_t graph = nullptr;
+    const hipError_t e = hipStreamEndCapture(ctx->stream, &graph);
+    if (e != hipSuccess) {
+        if (graph) (void)hipGraphDestroy(graph);
+        return gd_hip_fail(ctx, e, "gd_graph_end: hipStreamEndCapture");
+    }
+    if (!out) {
+        (void)hipGraphDestroy(graph);
+        return gd_fail(ctx, GD_EINVAL, "gd_graph_end: null out pointer (capture discarded)");
+    }
+    gd_graph *g = new gd_graph();
+    g->graph = graph;
+    const hipError_t ei = hipGraphInstantiate(&g->exec, graph, nullptr, nullptr, 0);
+    if (ei != hipSuccess) {
+        (void)hipGraphDestroy(graph);
+        delete g;
+        return gd_hip_fail(ctx, ei, "gd_graph_end: hipGraphInstantiate");
+    }
+    *out = g;
+    return GD_OK;
+}
+
+extern "C" int gd_graph_launch(gd_ctx *ctx, gd_graph *g) {
+    GD_CHECK_CTX(ctx);
+    GD_REQUIRE(ctx, g && g->exec, "gd_graph_launch: null graph");
+    GD_HIP(ctx, hipGraphLaunch(g->exec, ctx->stream));
+    return GD_OK;
+}
+
+extern "C" void gd_graph_destroy(gd_graph *g) {
+    if (!g) return;
+    if (g->exec) (void)hipGraphExecDestroy(g->exec);
+    if (g->graph) (void)hipGraphDestroy(g->graph);
+    delete g;
+}
+
 // ---------------------------------------------------------------- host codec
 
 extern "C" int gd_q2_0_pack(const uint8_t *codes, const uint16_t *scales, size_t n,

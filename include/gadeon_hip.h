@@ -91,6 +91,23 @@ int gd_sync(gd_ctx *ctx);
 int gd_timer_start(gd_ctx *ctx);
 int gd_timer_stop(gd_ctx *ctx, float *ms);
 
+/* ---- recorded command sequences ---------------------------------------------
+ * The reference encodes all dispatches of a token or chunk into one Metal
+ * command buffer and commits it once (MetalEngine.swift:657-728).  Here the
+ * compute entries called between gd_graph_begin and gd_graph_end are recorded
+ * into a HIP graph instead of running; gd_graph_launch replays the recording
+ * on the context stream with the same arguments (pointers, shapes), so one
+ * host call issues the whole sequence.  Only enqueue-only entries may be
+ * recorded: no gd_sync, gd_download, gd_upload, gd_alloc/free or timer calls,
+ * and no entry that has to grow the context workspace (run it once before
+ * recording).  A failing entry inside a recording leaves the capture open;
+ * gd_graph_end then fails and discards it. */
+typedef struct gd_graph gd_graph;
+int gd_graph_begin(gd_ctx *ctx);
+int gd_graph_end(gd_ctx *ctx, gd_graph **out);
+int gd_graph_launch(gd_ctx *ctx, gd_graph *g);
+void gd_graph_destroy(gd_graph *g);
+
 /* ---- Q2_0 codec (host; no GPU needed) -------------------------------------
  * The reference only decodes Q2_0 (Quant.swift:15-30); these are its exact
  * inverse.  Code c in {0,1,2,3} means weight (c-1)*d; code of weight j of a

@@ -341,4 +341,7 @@ class Stack:
         if name == "ssm_state":
             n = cfg["n_v_head"] * cfg["d_state"] ** 2
             return np.ctypeslib.as_array(C.cast(L.rec_state, C.POINTER(C.c_float)), (n,)).copy()
+        if name == "ssm_conv_state":
+            n = (cfg["d_conv"] - 1) * (2 * cfg["n_k_head"] + cfg["n_v_head"]) * cfg["d_state"]
+            return np.ctypeslib.as_array(C.cast(L.conv_state, C.POINTER(C.c_float)), (n,)).copy()
         raise KeyError(name)

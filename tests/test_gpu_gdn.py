@@ -236,3 +236,34 @@ def test_decode_chain_equals_prefill(ctx):
                           None, dS_b, do1, 1 / np.sqrt(dS), EPS)
         assert rel_diff(ctx.get(do1, (nV, dS), np.float16), o_pre[t]) < 2e-3, t
     assert rel_diff(ctx.get(dS_b, S.size, np.float32), ctx.get(dS_a, S.size, np.float32)) < 2e-3
+
+
+@pytest.mark.parametrize("T,nV,nK,C", [(130, 4, 2, 64), (45, 2, 2, 32)])
+def test_prefill_f32_inputs_keep_f32_precision(ctx, T, nV, nK, C):
+    """f32 q, k, v that f16 cannot hold exactly (the stack's conv outputs):
+    the chunked prefill carries them as hi + lo f16 pairs, so o and S follow
+    the f64 sequential scan to ~1e-5 (o, whose P delta term sums many
+    products, to < 1e-4) -- well inside what rounding q, k, v to f16 would
+    cost (a few 1e-4, the reference's prefill scan being f32,
+    Kernels.metal:1574-1625)."""
+    dS = 128
+    rng = np.random.default_rng(T)
+    q = rng.standard_normal((T, nK, dS))
+    k = rng.standard_normal((T, nK, dS))
+    q = (q / np.linalg.norm(q, axis=-1, keepdims=True)).astype(np.float32)
+    k = (k / np.linalg.norm(k, axis=-1, keepdims=True)).astype(np.float32)
+    v = rng.standard_normal((T, nV, dS)).astype(np.float32)
+    beta = sigmoid(rng.standard_normal((T, nV))).astype(np.float32)
+    g = (-softplus(rng.standard_normal((T, nV)))).astype(np.float32)
+    S = (rng.standard_normal((nV, dS, dS)) * 0.02).astype(np.float32)
+    dq, dk, dv = ctx.put(q), ctx.put(k), ctx.put(v)
+    dg, db, dS_ = ctx.put(g), ctx.put(beta), ctx.put(S)
+    do = ctx.alloc(T * nV * dS * 4)
+    ctx.gd_gdn_prefill(T, nV, nK, dS, dS, dq, nK * dS, dk, nK * dS, dv, nV * dS, ga.F32, dg, db,
+                       dS_, do, nV * dS, ga.F32, 1 / np.sqrt(dS), C)
+    S_ref = S.astype(np.float64).copy()
+    o_ref = O.gdn_sequential(q, k, v, g, beta, S_ref, 1 / np.sqrt(dS), f64=True)
+    ro = rel_diff(ctx.get(do, (T, nV, dS), np.float32), o_ref)
+    rs = rel_diff(ctx.get(dS_, S.size, np.float32), S_ref)
+    print(f"f32 io T={T}: o relDiff {ro:.2e}, S relDiff {rs:.2e}")
+    assert ro < 1e-4 and rs < 1e-5

@@ -391,3 +391,110 @@ def test_invalid_shapes_are_errors(ctx):
     assert b"multiple of 128" in lib.gd_last_error(ctx.h)
     bad = ga.Q2W(None, None, 128, 1)
     assert lib.gd_q2_0_gemv(ctx.h, C.byref(bad), None, ga.F16, None) == ga.GD_EINVAL
+
+
+def big_blocks(x, blocks_idx, lo, hi, seed):
+    """x with the 128-element blocks `blocks_idx` rescaled so their max |x|
+    lies in [lo, hi] (the GEMV stages such blocks with an extra power-of-two
+    scale, since x * 16 would overflow f16)."""
+    rng = np.random.default_rng(seed)
+    x = x.copy()
+    for b in blocks_idx:
+        seg = x[b * 128:(b + 1) * 128]
+        target = rng.uniform(lo, hi)
+        x[b * 128:(b + 1) * 128] = seg / np.abs(seg).max() * target
+    return x
+
+
+@pytest.mark.parametrize("xt", [ga.F16, ga.F32])
+@pytest.mark.parametrize("K,R,ksplit", [(5120, 777, 1), (17408, 5120, 3), (1024, 3072, 1)])
+def test_gemv_large_x_blocks(ctx, xt, K, R, ksplit):
+    """Blocks of x with max |x| in [3e3, 3e4] (SwiGLU outputs feeding
+    ffn_down, or large norm weights, reach them): the per-block rescale path,
+    in f16 and f32 x and in K-split partials, against the oracle at the plain
+    GEMV's tolerance."""
+    blocks = O.lcg_q2_0(K, R, K + 3 * R)
+    w = upload_w(ctx, blocks, K, R)
+    nb = K // 128
+    big = sorted({0, 1, nb // 2, nb - 1, 5 % nb})
+    x = big_blocks(O.lcg_normal(K, 17), big, 3e3, 3e4, K)
+    if xt == ga.F16:
+        xh = x.astype(np.float16)
+        x_ref = xh.astype(np.float32)
+        dx = ctx.put(xh.view(np.uint16))
+    else:
+        x_ref = x.astype(np.float32)
+        dx = ctx.put(x_ref)
+    dy = ctx.alloc(ksplit * R * 4)
+    ns = C.c_int()
+    ctx.gd_q2_0_gemv_split(C.byref(w), dx, xt, dy, ksplit, C.byref(ns))
+    y = ctx.get(dy, (ns.value, R), np.float32).sum(0)
+    want = O.q2_0_matvec(blocks, K, R, x_ref, threads=8)
+    assert rel_diff(y, want) < 1e-4
+    free_w(ctx, w)
+    ctx.free(dx)
+    ctx.free(dy)
+
+
+def test_gemv_norm_large_norm_weight(ctx):
+    """Fused add + RMSNorm input whose norm weight is large on some blocks,
+    so the staged f16 x reaches |x| in the thousands there."""
+    K, R, eps = 5120, 999, 1e-6
+    blocks = O.lcg_q2_0(K, R, 4242)
+    w = upload_w(ctx, blocks, K, R)
+    h = O.lcg_normal(K, 3, 0.0, 2.0)
+    wn = big_blocks(np.ones(K, np.float32) * 0.9, [2, 17, 39], 4e3, 1.5e4, 9).astype(np.float32)
+    dh, dwn, dy = ctx.put(h), ctx.put(wn), ctx.alloc(R * 4)
+    ctx.gd_q2_0_gemv_norm(C.byref(w), dh, None, 0, 0, dwn, eps, None, dy, None)
+    x16 = O.rmsnorm(h[None], wn, eps)[0].astype(np.float16)
+    assert np.abs(x16.astype(np.float32)).max() > 2048
+    want = O.q2_0_matvec(blocks, K, R, x16.astype(np.float32), threads=8)
+    assert rel_diff(ctx.get(dy, R, np.float32), want) < 1e-3
+    for p in (dh, dwn, dy):
+        ctx.free(p)
+    free_w(ctx, w)
+
+
+def test_graph_replays_recorded_calls(ctx):
+    """gd_graph_begin/end record GEMVs on three distinct matrices and a cast;
+    each replay, with eager work and synchronizations in between, gives the
+    eager results again."""
+    K, R = 1024, 3072
+    mats = [O.lcg_q2_0(K, R, 300 + i) for i in range(3)]
+    ws = [upload_w(ctx, b, K, R) for b in mats]
+    xh = O.lcg_normal_f16(K, 8)
+    dx = ctx.put(xh.view(np.uint16))
+    dys = [ctx.alloc(R * 4) for _ in ws]
+    d16 = ctx.alloc(R * 2)
+
+    def record():
+        for w, dy in zip(ws, dys):
+            ctx.gd_q2_0_gemv(C.byref(w), dx, ga.F16, dy)
+        ctx.gd_cast(dys[0], ga.F32, d16, ga.F16, R)
+
+    record()
+    eager = [ctx.get(dy, R, np.float32) for dy in dys]
+    eager16 = ctx.get(d16, R, np.uint16)
+    for i, b in enumerate(mats):
+        assert rel_diff(eager[i], O.q2_0_matvec(b, K, R, xh.astype(np.float32), 8)) < 1e-4
+    ctx.check(ctx.lib.gd_graph_begin(ctx.h))
+    record()
+    g = C.c_void_p()
+    ctx.check(ctx.lib.gd_graph_end(ctx.h, C.byref(g)))
+    try:
+        for rep in range(3):
+            for dy in dys:
+                ctx.gd_fill_u32(dy, 0x7fc00000, R)        # NaN, so a skipped write shows
+            ctx.gd_fill_u32(d16, 0, R // 2)
+            ctx.sync()
+            ctx.check(ctx.lib.gd_graph_launch(ctx.h, g))
+            ctx.sync()
+            for i, dy in enumerate(dys):
+                assert np.array_equal(ctx.get(dy, R, np.float32), eager[i]), (rep, i)
+            assert np.array_equal(ctx.get(d16, R, np.uint16), eager16), rep
+    finally:
+        ctx.lib.gd_graph_destroy(g)
+    for p in dys + [dx, d16]:
+        ctx.free(p)
+    for w in ws:
+        free_w(ctx, w)
