@@ -86,6 +86,8 @@ _PROTOS = {
                            _vp, _f, _f]),
     "gd_gdn_prefill": (_i, [_vp, _i64, _i, _i, _i, _i, _vp, _i64, _vp, _i64, _vp, _i64, _i,
                             _vp, _vp, _vp, _vp, _i64, _i, _f, _i]),
+    "gd_gdn_prefill_noalloc": (_i, [_vp, _i64, _i, _i, _i, _i, _vp, _i64, _vp, _i64, _vp, _i64, _i,
+                            _vp, _vp, _vp, _vp, _i64, _i, _f, _i]),
     "gd_rand_uniform": (_i, [_vp, _vp, _sz, _u64, _f, _f]),
     "gd_rand_normal": (_i, [_vp, _vp, _i, _sz, _u64, _f, _f]),
     "gd_rand_q2w": (_i, [_vp, _Q2WP, _u64, _f, _f]),

@@ -20,8 +20,14 @@ struct gd_ctx {
     int num_cus = 0;
     void *ws = nullptr;          // grow-only workspace (chunked GDN prefill)
     size_t ws_bytes = 0;
+    // This device's copy of the allocation-free prefill's scratch array
+    // (hipGetSymbolAddress at context creation; null if that failed).
+    void *prefill_scratch = nullptr;
     std::string err;
 };
+
+// Look up this device's address of the prefill scratch array (device current).
+int gd_prefill_scratch_attach(gd_ctx *ctx);
 
 // Record `msg` as the context's last error and return `code`.
 int gd_fail(gd_ctx *ctx, int code, const char *fmt, ...);

@@ -681,24 +681,26 @@ int launch(gd_ctx *ctx, const PrepArgs &pa, const ScanArgs &sa, int io_dtype, in
 
 int gd_ctx_workspace(gd_ctx *ctx, size_t bytes, void **out);
 
-extern "C" int gd_gdn_prefill(gd_ctx *ctx, int64_t T, int nV, int nK, int dk, int dv,
-                              const void *q, int64_t q_stride, const void *k, int64_t k_stride,
-                              const void *v, int64_t v_stride, int io_dtype, const float *g,
-                              const float *beta, float *S, void *o, int64_t o_stride,
-                              int o_dtype, float qScale, int C) {
-    GD_CHECK_CTX(ctx);
-    GD_REQUIRE(ctx, q && k && v && g && beta && S && o, "gd_gdn_prefill: null pointer");
-    GD_REQUIRE(ctx, dk == DK && dv == DV, "gd_gdn_prefill: dk=%d dv=%d (takes 128/128)", dk, dv);
-    GD_REQUIRE(ctx, C == 16 || C == 32 || C == 64, "gd_gdn_prefill: chunk %d not 16/32/64", C);
-    GD_REQUIRE(ctx, nV > 0 && nK > 0 && T >= 0, "gd_gdn_prefill: nV=%d nK=%d T=%lld", nV, nK,
+namespace {
+
+// Checks the arguments; *bytes receives the scratch the call needs (0 for T = 0).
+int prefill_check(gd_ctx *ctx, const char *fn, int64_t T, int nV, int nK, int dk, int dv,
+                  const void *q, int64_t q_stride, const void *k, int64_t k_stride,
+                  const void *v, int64_t v_stride, int io_dtype, const float *g,
+                  const float *beta, float *S, void *o, int64_t o_stride, int o_dtype, int C,
+                  size_t *bytes) {
+    GD_REQUIRE(ctx, q && k && v && g && beta && S && o, "%s: null pointer", fn);
+    GD_REQUIRE(ctx, dk == DK && dv == DV, "%s: dk=%d dv=%d (takes 128/128)", fn, dk, dv);
+    GD_REQUIRE(ctx, C == 16 || C == 32 || C == 64, "%s: chunk %d not 16/32/64", fn, C);
+    GD_REQUIRE(ctx, nV > 0 && nK > 0 && T >= 0, "%s: nV=%d nK=%d T=%lld", fn, nV, nK,
                (long long)T);
-    GD_REQUIRE(ctx, io_dtype == GD_F32 || io_dtype == GD_F16, "gd_gdn_prefill: bad io dtype");
-    GD_REQUIRE(ctx, o_dtype == GD_F32 || o_dtype == GD_F16, "gd_gdn_prefill: bad o dtype");
+    GD_REQUIRE(ctx, io_dtype == GD_F32 || io_dtype == GD_F16, "%s: bad io dtype", fn);
+    GD_REQUIRE(ctx, o_dtype == GD_F32 || o_dtype == GD_F16, "%s: bad o dtype", fn);
     GD_REQUIRE(ctx, q_stride >= (int64_t)nK * dk && k_stride >= (int64_t)nK * dk &&
                         v_stride >= (int64_t)nV * dv && o_stride >= (int64_t)nV * dv,
-               "gd_gdn_prefill: strides smaller than a token row");
+               "%s: strides smaller than a token row", fn);
     // A chunk's output rows are stored through one 32-bit buffer range.
-    GD_REQUIRE(ctx, o_stride <= (1 << 24), "gd_gdn_prefill: o_stride %lld above 2^24",
+    GD_REQUIRE(ctx, o_stride <= (1 << 24), "%s: o_stride %lld above 2^24", fn,
                (long long)o_stride);
     // Rows are read 8 elements at a time.
     const int vec = io_dtype == GD_F16 ? 8 : 4;
@@ -706,9 +708,25 @@ extern "C" int gd_gdn_prefill(gd_ctx *ctx, int64_t T, int nV, int nK, int dk, in
     GD_REQUIRE(ctx, q_stride % 8 == 0 && k_stride % 8 == 0 && v_stride % 8 == 0 &&
                         ((uintptr_t)q % (vec * esz)) == 0 && ((uintptr_t)k % (vec * esz)) == 0 &&
                         ((uintptr_t)v % (vec * esz)) == 0,
-               "gd_gdn_prefill: q/k/v rows must be 8-element strided and %d-byte aligned",
-               vec * esz);
+               "%s: q/k/v rows must be 8-element strided and %d-byte aligned", fn, vec * esz);
+    *bytes = 0;
     if (T == 0) return GD_OK;
+    const size_t units = (size_t)nV * (size_t)((T + C - 1) / C);
+    const size_t CP = C < 32 ? 32 : C;
+    const size_t nkt = io_dtype == GD_F32 ? 2 : 1;
+    // Wh, Wl; U; Ph, Pl; K^T (hi, lo); G -- the layout prefill_run carves.
+    *bytes = units * (2 * CP * DK * 2 + CP * DV * 4 + 2 * CP * CP * 2 + nkt * DK * CP * 2 +
+                      CP * 4);
+    return GD_OK;
+}
+
+// Launches prep + scan with their per-(head, chunk) operands in ws (at least
+// the bytes prefill_check computed).  Every byte of ws the scan reads is
+// written by prep in the same call, so ws needs no clearing.
+int prefill_run(gd_ctx *ctx, void *ws, int64_t T, int nV, int nK, const void *q,
+                int64_t q_stride, const void *k, int64_t k_stride, const void *v,
+                int64_t v_stride, int io_dtype, const float *g, const float *beta, float *S,
+                void *o, int64_t o_stride, int o_dtype, float qScale, int C) {
     const int nchunks = (int)((T + C - 1) / C);
     const int CP = C < 32 ? 32 : C;
     const size_t units = (size_t)nV * nchunks;
@@ -717,10 +735,6 @@ extern "C" int gd_gdn_prefill(gd_ctx *ctx, int64_t T, int nV, int nK, int dk, in
     const size_t pbytes = units * CP * CP * 2;          // each of Ph, Pl
     const size_t kbytes = units * DK * CP * 2;          // K^T hi; lo too for f32 k
     const size_t nkt = io_dtype == GD_F32 ? 2 : 1;
-    const size_t gbytes = units * CP * 4;
-    void *ws = nullptr;
-    int rc = gd_ctx_workspace(ctx, 2 * wbytes + ubytes + 2 * pbytes + nkt * kbytes + gbytes, &ws);
-    if (rc) return rc;
     uint8_t *p = (uint8_t *)ws;
     Work w;
     w.Wh = (f16 *)p;            p += wbytes;
@@ -737,6 +751,67 @@ extern "C" int gd_gdn_prefill(gd_ctx *ctx, int64_t T, int nV, int nK, int dk, in
     ScanArgs sa{q, q_stride, w, S, o, o_stride, T, nV, nK, C, nchunks, qScale};
     return CP == 64 ? launch<64>(ctx, pa, sa, io_dtype, o_dtype)
                     : launch<32>(ctx, pa, sa, io_dtype, o_dtype);
+}
+
+// Scratch of gd_gdn_prefill_noalloc: a file-scope device array, so the entry
+// needs no allocation.  Each device holds its own copy until the process
+// ends; host code reaches it only through the address hipGetSymbolAddress
+// returns for the current device (kept per context), never through the
+// array's name.  Every call on a device shares it.
+constexpr size_t PREFILL_SCRATCH_BYTES = GD_GDN_PREFILL_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[PREFILL_SCRATCH_BYTES];
+
+}  // namespace
+
+int gd_prefill_scratch_attach(gd_ctx *ctx) {
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) {
+        ctx->prefill_scratch = nullptr;
+        return gd_hip_fail(ctx, e, "prefill scratch: hipGetSymbolAddress");
+    }
+    ctx->prefill_scratch = p;
+    return GD_OK;
+}
+
+extern "C" int gd_gdn_prefill(gd_ctx *ctx, int64_t T, int nV, int nK, int dk, int dv,
+                              const void *q, int64_t q_stride, const void *k, int64_t k_stride,
+                              const void *v, int64_t v_stride, int io_dtype, const float *g,
+                              const float *beta, float *S, void *o, int64_t o_stride,
+                              int o_dtype, float qScale, int C) {
+    GD_CHECK_CTX(ctx);
+    size_t bytes = 0;
+    int rc = prefill_check(ctx, "gd_gdn_prefill", T, nV, nK, dk, dv, q, q_stride, k, k_stride, v,
+                           v_stride, io_dtype, g, beta, S, o, o_stride, o_dtype, C, &bytes);
+    if (rc || T == 0) return rc;
+    void *ws = nullptr;
+    if ((rc = gd_ctx_workspace(ctx, bytes, &ws))) return rc;
+    return prefill_run(ctx, ws, T, nV, nK, q, q_stride, k, k_stride, v, v_stride, io_dtype, g,
+                       beta, S, o, o_stride, o_dtype, qScale, C);
+}
+
+extern "C" int gd_gdn_prefill_noalloc(gd_ctx *ctx, int64_t T, int nV, int nK, int dk, int dv,
+                                      const void *q, int64_t q_stride, const void *k,
+                                      int64_t k_stride, const void *v, int64_t v_stride,
+                                      int io_dtype, const float *g, const float *beta, float *S,
+                                      void *o, int64_t o_stride, int o_dtype, float qScale,
+                                      int C) {
+    GD_CHECK_CTX(ctx);
+    size_t bytes = 0;
+    int rc = prefill_check(ctx, "gd_gdn_prefill_noalloc", T, nV, nK, dk, dv, q, q_stride, k,
+                           k_stride, v, v_stride, io_dtype, g, beta, S, o, o_stride, o_dtype, C,
+                           &bytes);
+    if (rc || T == 0) return rc;
+    GD_REQUIRE(ctx, bytes <= PREFILL_SCRATCH_BYTES,
+               "gd_gdn_prefill_noalloc: needs %zu bytes of scratch for nV=%d x %lld chunks of "
+               "%d, above its fixed %zu (GD_GDN_PREFILL_SCRATCH_BYTES); split T or use "
+               "gd_gdn_prefill", bytes, nV, (long long)((T + C - 1) / C), C,
+               PREFILL_SCRATCH_BYTES);
+    GD_REQUIRE(ctx, ctx->prefill_scratch != nullptr,
+               "gd_gdn_prefill_noalloc: the scratch array's device address could not be "
+               "looked up when the context was created");
+    return prefill_run(ctx, ctx->prefill_scratch, T, nV, nK, q, q_stride, k, k_stride, v,
+                       v_stride, io_dtype, g, beta, S, o, o_stride, o_dtype, qScale, C);
 }
 
 extern "C" int gd_gdn_scan_batch(gd_ctx *ctx, const float *convOutN, int keyDim, int valueDim,

@@ -62,6 +62,10 @@ extern "C" int gd_ctx_create(int device, gd_ctx **out) {
     }
     hipDeviceProp_t p;
     if (hipGetDeviceProperties(&p, device) == hipSuccess) c->num_cus = p.multiProcessorCount;
+    // A failed lookup leaves prefill_scratch null: only gd_gdn_prefill_noalloc
+    // needs it, and it reports the failure then.
+    (void)gd_prefill_scratch_attach(c);
+    c->err.clear();
     *out = c;
     return GD_OK;
 }

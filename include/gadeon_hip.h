@@ -316,6 +316,26 @@ int gd_gdn_prefill(gd_ctx *ctx, int64_t T, int nV, int nK, int dk, int dv,
                    void *o, int64_t o_stride, int o_dtype, float qScale,
                    int C);
 
+/* gd_gdn_prefill for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * No counterpart in the reference.  Same arguments and results as
+ * gd_gdn_prefill, whose per-chunk operands go through a context workspace
+ * that may grow with hipMalloc; here they live in a fixed device array of
+ * GD_GDN_PREFILL_SCRATCH_BYTES per GPU, held until the process ends, and the
+ * call allocates nothing.  Shapes needing more are rejected with GD_EINVAL:
+ * the scratch takes nV * ceil(T/C) * b bytes, b = 98,560 (f16 io) or 114,944
+ * (f32 io) at C = 64, so e.g. 16 heads fit T <= 1152 (f32) / 1344 (f16).
+ * Every call on a GPU shares the array (nothing in it needs to start at
+ * zero: each call writes all it reads), so calls that overlap on one GPU --
+ * from two streams or threads -- race. */
+#define GD_GDN_PREFILL_SCRATCH_BYTES (32u << 20)
+int gd_gdn_prefill_noalloc(gd_ctx *ctx, int64_t T, int nV, int nK, int dk, int dv,
+                           const void *q, int64_t q_stride, const void *k,
+                           int64_t k_stride, const void *v, int64_t v_stride,
+                           int io_dtype, const float *g, const float *beta, float *S,
+                           void *o, int64_t o_stride, int o_dtype, float qScale,
+                           int C);
+
 /* ---- synthetic data on the device -----------------------------------------
  * Counter-addressable copy of the reference's test LCG
  * (MetalSelfTest.swift:12-21): element i of stream `seed` is the (i+1)-th
