@@ -1,0 +1,560 @@
+// The Q2_0 GEMV on the matrix cores as a device function, shared by the
+// standalone GEMV kernel (q2_0_gemv_mfma.hip) and the persistent decode
+// kernel (decode.hip).
+//
+// Same result as q2_0_gemv (Kernels.metal:30-119) and Q2_0.matvec
+// (Quant.swift:36-77): per block d * (sum(code*x) - sum(x)), f32 throughout.
+//
+// MI355X design.  v_mfma_f32_4x4x4f16 (16 independent 4x4x4 products per
+// instruction) does the multiply-adds; the VALU only unpacks codes.
+//   * A operand: the weights are stored in 2 KiB tiles (16 rows x 512 K) in
+//     the order the 64 lanes need them: lane l holds one Q2_0 block (32 code
+//     bytes) of row l%16, block l/16 of the step, read as two 16-byte loads
+//     at lane*16 and 1024 + lane*16, so every load instruction of a wave is
+//     one contiguous 1 KiB.  As a 4x4x4 lane, l is row l%4 of MFMA block
+//     l/4: MFMA block m covers rows 4*(m%4) .. 4*(m%4)+3 of Q2 block m/4.
+//     Codes k and k+8 of a code dword land in the two f16 halves of an
+//     operand dword by a mask alone (codes 2, 3, 4 sit at bits 4, 6, 8), or
+//     by a mask after one of two shared shifts (w << 4 for codes 0, 1; w >> 6
+//     for 5, 6, 7): ten VALU ops per 16 weights.  A half is then exactly
+//     c * 2^(p-24) for bit position p (an f16 subnormal), and the x it meets
+//     is staged pre-scaled by 2^(8-p), so every product is c * x * 2^-16.
+//     Positions below 4 are not used: the matrix cores lose precision on
+//     those subnormals (measured), while 4, 6 and 8 stay within about 1e-6
+//     of the exact sum.  A block whose x would overflow f16 after the x16
+//     pre-scale is staged scaled down by a power of two 2^-e, undone later.
+//   * B operand: every lane reads the staged x of its own Q2 block, so the
+//     four output columns of an MFMA block hold the same products and
+//     column 0 is used (the lanes of one block read one LDS address, which
+//     the LDS broadcasts).  x is staged once per workgroup in LDS, already
+//     permuted into the (k, k+8) pair order of the unpack and pre-scaled,
+//     with zero blocks past the last one for a short final step.  f32 x is
+//     split into hi = f16(x) and lo = f16((x - hi) * 2^11), two B operands
+//     accumulated apart and recombined in f32.
+//   * Work split.  A "set" is one 16-row group; an "item" is one tile (one
+//     chunk step of 512 K of one set).  Every workgroup gets the same number
+//     of consecutive sets (and, with a K split, one range of steps).  Its
+//     waves take the workgroup's items one at a time from an LDS counter, so
+//     a wave whose loads come back late simply takes fewer items (with a
+//     fixed share per wave, the workgroup waited about 3 us for its slowest
+//     wave).  An item's products are scaled by their block scales d, sum(x)
+//     of each block is subtracted, and the item's 16 row partials go to LDS;
+//     after one barrier each row is summed over its steps in step order, so
+//     the result does not depend on which wave took which item.
+//   * Latency.  Each wave keeps the next P tiles in flight (a register ring),
+//     each with the four scales its item needs (one 8-byte load).  Tiles,
+//     scales and x are read with bounds-checked buffer loads: a load past
+//     the end returns zeros without a memory access, so every load in the
+//     main loop is unconditional and the compiler waits only for the tile an
+//     item needs.  x is requested before the tiles (loads return in order).
+//     A caller that runs several GEMVs back to back in one kernel can issue
+//     the next GEMV's first ring loads (gemv::prefetch) before it waits for
+//     that GEMV's input: weights do not depend on it.
+//   * Coherent mode (CO).  Inside one persistent kernel, a GEMV's input was
+//     written moments earlier by other workgroups, possibly on another XCD
+//     (each XCD has its own L2).  Then x, the residual and its partials are
+//     read, and y / the SwiGLU output / h' written, with sc0|sc1 buffer
+//     accesses, which go to the coherent memory side instead of an L2.
+#pragma once
+
+#include "gd_internal.h"
+
+namespace gemv {
+
+constexpr int XB = 68;    // LDS dwords per staged x block
+// Dynamic LDS available beside a kernel's few static words.
+constexpr size_t LDS_BYTES = 160 * 1024 - 2048;
+// Waves per workgroup (all share one staged copy of x) and tiles in flight
+// per wave.  Measured on the decode shapes: 16 waves and 2 tiles beat 4 or 8
+// waves and 3 or 4 tiles everywhere.
+constexpr int NW = 16, P = 2;
+constexpr int CP_NT = 2;     // cache policy: non-temporal (streamed once)
+constexpr int COH = 0x11;    // cache policy: sc0 | sc1 (coherent across XCDs)
+
+// LDS bytes of the x staging: the x planes (two for f32 x), then the block
+// sums and exponents of x.
+__host__ __device__ inline size_t xlds_bytes(int nblk, bool hl) {
+    return (size_t)(nblk + 5) * XB * 4 * (hl ? 2 : 1) + (size_t)((nblk + 1) & ~1) * 8;
+}
+
+// Operand dword m holds codes (m, m+8) of w at bit position POS[m] of its
+// two f16 halves; the x pair it meets is pre-scaled by XSCALE[m] = 2^(8-POS[m]).
+__device__ __forceinline__ void unpack_dword(uint32_t w, uint32_t (&t)[8]) {
+    constexpr uint32_t M4 = 0x00300030u, M6 = 0x00C000C0u, M8 = 0x03000300u;
+    const uint32_t u = w << 4, v = w >> 6;
+    t[0] = u & M4;     // code 0 at bit 4
+    t[1] = u & M6;     // code 1 at bit 6
+    t[2] = w & M4;     // code 2 at bit 4
+    t[3] = w & M6;     // code 3 at bit 6
+    t[4] = w & M8;     // code 4 at bit 8
+    t[5] = v & M4;     // code 5 at bit 4
+    t[6] = v & M6;     // code 6 at bit 6
+    t[7] = v & M8;     // code 7 at bit 8
+}
+__device__ constexpr float XSCALE[8] = {16.f, 4.f, 16.f, 4.f, 1.f, 16.f, 4.f, 1.f};
+
+// Two f32 -> two f16 (RNE) in one dword.
+__device__ __forceinline__ uint32_t pack_h2(float a, float b) {
+    return (uint32_t)gd_f2h(a) | ((uint32_t)gd_f2h(b) << 16);
+}
+
+// x values of one staging entry (16 consecutive elements of one block).
+// XT = 0: f16 x; 1: f32 x; 2: f32 residual h (+ delta) normalized in the
+// staging (x = f16(rmsnorm(h + delta) * w)), then used as f16 x.
+template <int XT> struct XChunk;
+template <> struct XChunk<0> { u32x4 lo, hi; };
+template <> struct XChunk<1> { f32x4 f[4]; };
+template <> struct XChunk<2> { f32x4 f[4], d[4], w[4]; };
+
+// SwiGLU output: with pair_sets > 0, W is [gate; up] with pair_sets sets
+// (16 rows) in each half, a workgroup takes gate sets k .. and the matching
+// up sets pair_sets + k .., and out[r] = f16(silu(gate_r . x) * (up_r . x))
+// replaces y.
+struct GluOut {
+    uint16_t *out;
+    int pair_sets;
+};
+
+// Fused input of the XT = 2 variant.
+struct NormIn {
+    const float *delta;      // nd partials delta + z * dstride added to h first
+    const float *w;          // norm weight [K]
+    float *hout;             // h + delta, written by workgroup 0 (null: not kept)
+    float eps;
+    int nd;                  // partials in delta (0: none)
+    int dstride;             // floats between partials
+};
+
+// One GEMV: W (codes, scales) [R][K], x, y; the work split (sets per
+// workgroup `per`, K split into nz ranges of ksteps steps, gx workgroups per
+// range: workgroup wg takes sets (wg % gx) * per .. of range wg / gx, and
+// workgroups wg >= gx * nz have none).
+struct Task {
+    const uint8_t *codes;
+    const uint16_t *scales;
+    const void *x;
+    float *y;
+    int K, R, nsets, per, ksteps, nz, gx;
+    NormIn nin;
+    GluOut glu;
+};
+
+// The register ring of a wave: P tiles with their scales and item numbers.
+struct Ring {
+    u32x4 t[P][2];
+    u32x2 sc[P];
+    int it[P];
+};
+
+// Buffer resource over `bytes` bytes at p (raw: no stride).  Loads at an
+// offset past the end return zeros without touching memory, which keeps
+// every load of the main loop unconditional.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes,
+                                             0x00020000);
+}
+
+// What one workgroup does of task t.
+struct Geo {
+    int s0, L, set_lo, npair, nset_wg, wsets, total, steps, bgroups, up_shift;
+    uint32_t Lmag;
+    int bz;
+};
+
+__device__ __forceinline__ Geo geometry(const Task &t, int wg) {
+    Geo g;
+    const int nblk = t.K >> 7;
+    g.steps = (nblk + 3) >> 2;
+    g.bgroups = (nblk + 15) >> 4;
+    const int bx = wg % t.gx;
+    g.bz = wg / t.gx;
+    // K split z = bz: steps [s0, s1) of every set.  Item i is step s0 + i % L
+    // of set i / L (set-major).
+    g.s0 = g.bz * t.ksteps;
+    const int s1 = min(g.steps, g.s0 + t.ksteps);
+    g.L = max(0, s1 - g.s0);
+    // Sets of this workgroup, numbered c = 0 .. nset_wg-1 in LDS and in the
+    // item space; set c is set set_lo + c of W.  With SwiGLU, nsets counts
+    // gate sets, c < npair are gate sets and the rest their up sets, set
+    // set_lo + pair_sets + c - npair of W.
+    g.set_lo = bx * t.per;
+    g.npair = g.bz < t.nz ? max(0, min(t.per, t.nsets - g.set_lo)) : 0;
+    g.nset_wg = t.glu.pair_sets ? 2 * g.npair : g.npair;
+    g.wsets = t.glu.pair_sets ? t.glu.pair_sets + g.npair : g.npair;   // sets spanned in W
+    g.total = g.nset_wg * g.L;                                         // items
+    g.up_shift = t.glu.pair_sets ? t.glu.pair_sets - g.npair : 0;
+    // Item i is set i / L: the quotient by multiply-high (exact for i < 2^16
+    // and L <= 128, which the host guarantees).
+    g.Lmag = g.L <= 1 ? 0u : (uint32_t)((0x100000000ull + g.L - 1) / g.L);
+    return g;
+}
+
+__device__ __forceinline__ int set_of(const Geo &g, int it) {
+    return g.L <= 1 ? it : (int)__umulhi((uint32_t)it, g.Lmag);
+}
+
+// Loads of item `it`: its tile, and for the lanes of column 0 the scales of
+// rows 4*rq .. 4*rq+3 of their block 4*s + kb (the other lanes load
+// nothing).  The address arithmetic has no branch (the compiler's wait
+// counting is exact only over straight-line loads): an item past the last
+// gets the offset 0xfffff000, beyond every resource.
+__device__ __forceinline__ void issue(const Task &t, const Geo &g, int it, u32x4 (&cw)[2],
+                                      u32x2 &sc) {
+    const int lane = threadIdx.x & 63;
+    const int j = lane & 3, rq = (lane >> 2) & 3, kb = lane >> 4;
+    const __amdgpu_buffer_rsrc_t trs =
+            make_rsrc(t.codes + (size_t)g.set_lo * g.steps * 2048, (uint32_t)g.wsets * g.steps * 2048u);
+    const __amdgpu_buffer_rsrc_t srs =
+            make_rsrc(t.scales + (size_t)g.set_lo * g.bgroups * 256, (uint32_t)g.wsets * g.bgroups * 512u);
+    auto pick = [](uint32_t off, uint32_t dead) { return (off & ~dead) | (dead & 0xfffff000u); };
+    const int c = set_of(g, it), s = g.s0 + (it - c * g.L);
+    const int ps = c + (c >= g.npair ? g.up_shift : 0);
+    const uint32_t dead = (uint32_t)((g.total - 1 - it) >> 31);      // all ones past the end
+    const uint32_t off = pick((uint32_t)(ps * g.steps + s) * 2048u + lane * 16, dead);
+    cw[0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(trs, off, 0, CP_NT));
+    cw[1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(trs, off + 1024, 0, CP_NT));
+    const uint32_t si = (uint32_t)((ps * g.bgroups + (s >> 2)) * 16 + 4 * (s & 3) + kb) * 32 + 8 * rq;
+    const uint32_t other = (uint32_t)-(int)(j != 0);
+    sc = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(srs, pick(si, dead | other), 0, 0));
+}
+
+// The first ring loads of task t for this wave (items p * NW + wave), so
+// they are in flight before the caller waits for t's input.
+__device__ __forceinline__ void prefetch(const Task &t, int wg, Ring &rg) {
+    const Geo g = geometry(t, wg);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+#pragma unroll
+    for (int p = 0; p < P; p++) {
+        rg.it[p] = p * NW + wave;
+        issue(t, g, rg.it[p], rg.t[p], rg.sc[p]);
+    }
+}
+
+// Runs task t's share of workgroup wg.  lds: the dynamic LDS (x staging,
+// then the item partials).  With `prefetched`, rg already holds the loads
+// prefetch(t, wg, rg) issued.  XT: 0 = f16 x, 1 = f32 x (hi + lo split),
+// 2 = normalized residual (see XChunk).  KBP: item partials kept per Q2
+// block (4 per row) in LDS, summed with the rest of the row at the end;
+// otherwise summed across the block lanes first (needs 4x less LDS, for very
+// long K).  CO: coherent input reads and output writes (see above).
+// All 64 * NW threads of the workgroup must call it.
+template <int XT, bool KBP, bool CO>
+__device__ void run(const Task &t, int wg, uint32_t *lds, Ring &rg, bool prefetched) {
+    constexpr int MT = 64 * NW;
+    constexpr bool HL = XT == 1;                          // x carried as f16 hi + lo
+    constexpr int XPOL = CO ? COH : 0;                    // cache policy of x reads
+    __shared__ __align__(16) int next_item;               // next item to take
+    const Geo g = geometry(t, wg);
+    const int K = t.K, R = t.R;
+    const int nblk = K >> 7;
+    // LDS: x planes, block b at dword XB*b (64 pair dwords + 4 of padding, so
+    // the blocks one load instruction reads start on different banks), then
+    // zero blocks for the blocks of a short last step past K; per-block sum
+    // and exponent of x (nblk rounded up to even, so that what follows is
+    // 16-byte aligned); the row partials of every item.
+    const int xstride = (nblk + 5) * XB;                   // dwords per x plane
+    uint32_t *xp = lds;                                    // hi (or f16) pairs
+    uint32_t *xq = lds + xstride;                          // lo plane (f32 x only)
+    float *sx = (float *)(lds + (HL ? 2 : 1) * xstride);   // [nblk] block sums of x
+    float *ex = sx + ((nblk + 1) & ~1);                    // [nblk] 2^(16+e_b)
+    float *part = ex + ((nblk + 1) & ~1);                  // [items][4 blocks if KBP][16 rows]
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // Lane l holds row l%16 of Q2 block l/16 of a step (the tile order); as
+    // a 4x4x4 MFMA lane it is row / column j = l%4 of MFMA block l/4, which
+    // covers rows 4*rq .. 4*rq+3 (rq = l/4 % 4) of Q2 block kb = l/16.
+    const int j = lane & 3, rq = (lane >> 2) & 3, kb = lane >> 4;
+    float *y = t.y + (size_t)g.bz * R;
+    const int L = g.L, s0 = g.s0, set_lo = g.set_lo, npair = g.npair, total = g.total;
+    // A workgroup with no items (more workgroups than sets) still stages
+    // nothing and returns after the caller's shared barrier points.
+    if (total == 0) return;
+
+    // Staging entry e = (block e/8, chunk e%8): its x loads are issued before
+    // the tile prefetch, so waiting for them leaves the tiles in flight.
+    const int nstage = (nblk + 5) * 8;
+    // Entries past the last x block (the zero blocks, and threads with no
+    // entry) read past the end of x: zeros, without a memory access.
+    const NormIn &nin = t.nin;
+    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(t.x, (uint32_t)K * (XT ? 4u : 2u));
+    const __amdgpu_buffer_rsrc_t drs =
+            make_rsrc(nin.delta, nin.nd ? (uint32_t)((nin.nd - 1) * nin.dstride + K) * 4u : 0u);
+    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(nin.w, XT == 2 ? (uint32_t)K * 4u : 0u);
+    auto load_x = [&](int e) {
+        const int off = e < nblk * 8 ? (e >> 3) * 128 + 16 * (e & 7) : K;   // element offset
+        XChunk<XT> c;
+        if constexpr (XT == 0) {
+            c.lo = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, off * 2, 0, XPOL));
+            c.hi = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, off * 2 + 16, 0, XPOL));
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                c.f[q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, off * 4 + 16 * q, 0, XPOL));
+            if constexpr (XT == 2) {
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    c.d[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    // Entries past K (off == K) must read zeros: at z * dstride
+                    // + K lies the next partial.
+                    for (int z = 0; z < nin.nd; z++)
+                        c.d[q] += __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                drs, off < K ? (uint32_t)((z * nin.dstride + off) * 4 + 16 * q)
+                                             : 0xfffff000u, 0, XPOL));
+                    c.w[q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs, off * 4 + 16 * q, 0, 0));
+                }
+            }
+        }
+        return c;
+    };
+    XChunk<XT> xc = load_x(threadIdx.x);
+    // Keep the x loads ahead of the tile prefetch in the instruction stream:
+    // loads complete in issue order, so x issued after the tiles would only
+    // arrive behind them.
+    __builtin_amdgcn_sched_barrier(0);
+
+    // Ring slot p starts with item p * NW + wave; each later item is taken
+    // from the workgroup counter when a slot frees up.  One tile goes out
+    // before the staging, the rest of the ring after it, so x (needed first)
+    // does not queue behind the whole grid's prefetch.
+    if (!prefetched) {
+#pragma unroll
+        for (int p = 0; p < P; p++) rg.it[p] = p * NW + wave;
+        issue(t, g, rg.it[0], rg.t[0], rg.sc[0]);
+    }
+    if (threadIdx.x == 0) next_item = NW * P;
+
+    // Stage x: pair p = 8i + k of block b holds (x[b,16i+k], x[b,16i+k+8]) *
+    // XSCALE[k] * 2^-e_b.  Thread (b, i) forms the 8 pairs of x[16i ..
+    // 16i+15] in registers and writes them as 32 bytes; the block's sum and
+    // max|x| come from 8-lane shuffles.  e_b = 0 unless max|x| >= 2048.
+    auto stage = [&](const int e, const XChunk<XT> &xc) {
+        const int bb = e >> 3, i = e & 7;
+        float sum = 0.f, amax = 0.f;
+        f32x4 f[4];
+        if constexpr (XT == 0) {
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                const uint32_t d = q < 4 ? xc.lo[q] : xc.hi[q - 4];
+                f[q >> 1][2 * (q & 1)] = gd_h2f((uint16_t)(d & 0xffff));
+                f[q >> 1][2 * (q & 1) + 1] = gd_h2f((uint16_t)(d >> 16));
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; q++) f[q] = xc.f[q];
+        }
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                sum += f[q][j];
+                amax = fmaxf(amax, fabsf(f[q][j]));
+            }
+        sum += __shfl_xor(sum, 1, 64);
+        sum += __shfl_xor(sum, 2, 64);
+        sum += __shfl_xor(sum, 4, 64);
+        amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+        amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+        amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+        // amax < 2^(E-126) for f32 exponent field E; amax * 16 * 2^-eb < 2^15.
+        const int eb = min(111, max(0, (int)((__float_as_uint(amax) >> 23) & 0xff) - 137));
+        const float down = __uint_as_float((uint32_t)(127 - eb) << 23);    // 2^-eb
+        u32x4 p0, p1, q0, q1;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            // pair k = (x[16i+k], x[16i+k+8]) = (f[k/4][k%4], f[2+k/4][k%4])
+            const float xa = f[k >> 2][k & 3] * down, xb = f[2 + (k >> 2)][k & 3] * down;
+            const float ha = (float)(f16)xa, hb = (float)(f16)xb;
+            const uint32_t hp = pack_h2(ha * XSCALE[k], hb * XSCALE[k]);
+            if (k < 4) p0[k] = hp; else p1[k - 4] = hp;
+            if (HL) {
+                const uint32_t lp = pack_h2((xa - ha) * (0x1p11f * XSCALE[k]),
+                                            (xb - hb) * (0x1p11f * XSCALE[k]));
+                if (k < 4) q0[k] = lp; else q1[k - 4] = lp;
+            }
+        }
+        if (e < nstage) {
+            u32x4 *dst = (u32x4 *)(xp + bb * XB + 8 * i);
+            dst[0] = p0;
+            dst[1] = p1;
+            if (HL) {
+                u32x4 *dq = (u32x4 *)(xq + bb * XB + 8 * i);
+                dq[0] = q0;
+                dq[1] = q1;
+            }
+            if (i == 0 && bb < nblk) {
+                sx[bb] = sum;
+                ex[bb] = __uint_as_float((uint32_t)(127 + 16 + eb) << 23);   // 2^(16+eb)
+            }
+        }
+    };
+    // The first entry is straight-line code after the tile prefetch, so its
+    // wait for x leaves the tiles in flight; further entries (K long enough
+    // that (K/128 + 5) * 8 > threads) follow in a loop.
+    if constexpr (XT == 2) {
+        // x = f16(rmsnorm(h + delta) * w), as a separate add + norm kernel
+        // followed by an f16 GEMV would form it; one entry per thread (the
+        // host checks), entries past K load zeros.  Workgroup 0 keeps h +
+        // delta for the next residual add.
+        __shared__ float ssr[NW];
+        float ss = 0.f;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            xc.f[q] += xc.d[q];
+            ss += xc.f[q][0] * xc.f[q][0] + xc.f[q][1] * xc.f[q][1] +
+                  xc.f[q][2] * xc.f[q][2] + xc.f[q][3] * xc.f[q][3];
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        if (lane == 0) ssr[wave] = ss;
+        if (wg == 0 && nin.hout && threadIdx.x < nblk * 8) {
+            const uint32_t ho = (uint32_t)((threadIdx.x >> 3) * 128 + 16 * (threadIdx.x & 7)) * 4u;
+            const __amdgpu_buffer_rsrc_t hrs = make_rsrc(nin.hout, (uint32_t)K * 4u);
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, xc.f[q]), hrs,
+                                                       ho + 16 * q, 0, XPOL);
+        }
+        __syncthreads();
+        float tot = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) tot += ssr[w];
+        const float rs = 1.0f / sqrtf(tot / (float)K + nin.eps);
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+#pragma unroll
+            for (int c = 0; c < 4; c++) xc.f[q][c] = (float)(f16)(xc.f[q][c] * rs * xc.w[q][c]);
+    }
+    stage(threadIdx.x, xc);
+    if constexpr (XT != 2)
+        for (int e = threadIdx.x + MT; e < nstage; e += MT) stage(e, load_x(e));
+    if (!prefetched) {
+#pragma unroll
+        for (int p = 1; p < P; p++) issue(t, g, rg.it[p], rg.t[p], rg.sc[p]);
+    }
+    __syncthreads();
+
+    // One item (set c, step s): the four Q2 blocks 4s .. 4s+3 of 16 rows.
+    // Every lane reads x of its own block kb, so the four columns of an
+    // MFMA block hold the same products (only column 0 is used; a lane
+    // group of one kb reads one address, which the LDS broadcasts).
+    // Accumulator chains: f16 x uses two, f32 x two for hi and two for lo.
+    auto step = [&](const int it, u32x4 (&tile)[2], u32x2 &sc) {
+        const int c = set_of(g, it), s = s0 + (it - c * L);
+        // MFMA block mb = lane/4 multiplies rows 4*rq .. 4*rq+3 of Q2 block
+        // 4s + kb by four K values.  Blocks past the last (a short final
+        // step) read zero-staged x and give zero products.
+        const int blk = 4 * s + kb;
+        const u32x4 *src = (const u32x4 *)(xp + blk * XB);
+        const u32x4 *srq = (const u32x4 *)(xq + blk * XB);
+        f32x4 acc[4];
+#pragma unroll
+        for (int d = 0; d < 8; d++) {
+            uint32_t tt[8];
+            unpack_dword(tile[d >> 2][d & 3], tt);
+#pragma unroll
+            for (int q = 0; q < 2; q++) {
+                // Pairs 4q .. 4q+3 of chunk d: two MFMAs of four K values.
+                const u32x4 bx = src[2 * d + q];
+                const f16x4 a0 = __builtin_bit_cast(f16x4, u32x2{tt[4 * q], tt[4 * q + 1]});
+                const f16x4 a1 = __builtin_bit_cast(f16x4, u32x2{tt[4 * q + 2], tt[4 * q + 3]});
+                const f32x4 z{0.f, 0.f, 0.f, 0.f};
+                // The first product of a chain starts it from zero.
+                const bool first = d == 0 && q == 0;
+                acc[0] = __builtin_amdgcn_mfma_f32_4x4x4f16(
+                        a0, __builtin_bit_cast(f16x4, u32x2{bx[0], bx[1]}), first ? z : acc[0], 0, 0, 0);
+                acc[1] = __builtin_amdgcn_mfma_f32_4x4x4f16(
+                        a1, __builtin_bit_cast(f16x4, u32x2{bx[2], bx[3]}), first ? z : acc[1], 0, 0, 0);
+                if (HL) {
+                    const u32x4 bq = srq[2 * d + q];
+                    acc[2] = __builtin_amdgcn_mfma_f32_4x4x4f16(
+                            a0, __builtin_bit_cast(f16x4, u32x2{bq[0], bq[1]}), first ? z : acc[2], 0, 0, 0);
+                    acc[3] = __builtin_amdgcn_mfma_f32_4x4x4f16(
+                            a1, __builtin_bit_cast(f16x4, u32x2{bq[2], bq[3]}), first ? z : acc[3], 0, 0, 0);
+                }
+            }
+        }
+        // Lane (j, rq, kb) has rows 4*rq + v of block 4s + kb; every product
+        // entered as c * x * 2^(-16-e_b) (lo with x 2^11).
+        const bool live = blk < nblk;
+        const int bj = min(blk, nblk - 1);
+        const float sxj = sx[bj], exj = ex[bj];
+        const float dsc[4] = {gd_h2f((uint16_t)(sc[0] & 0xffff)), gd_h2f((uint16_t)(sc[0] >> 16)),
+                              gd_h2f((uint16_t)(sc[1] & 0xffff)), gd_h2f((uint16_t)(sc[1] >> 16))};
+        f32x4 r;
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const float cx = HL ? (acc[0][v] + acc[1][v]) + (acc[2][v] + acc[3][v]) * 0x1p-11f
+                                : acc[0][v] + acc[1][v];
+            r[v] = live ? dsc[v] * (cx * exj - sxj) : 0.f;
+        }
+        if constexpr (KBP) {
+            if (j == 0) *(f32x4 *)(part + (it * 4 + kb) * 16 + 4 * rq) = r;
+        } else {
+            // Sum the item's four blocks (lanes kb = 0 .. 3).
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                r[v] += __shfl_xor(r[v], 16, 64);
+                r[v] += __shfl_xor(r[v], 32, 64);
+            }
+            if (j == 0 && kb == 0) *(f32x4 *)(part + it * 16 + 4 * rq) = r;
+        }
+    };
+    // Items are consumed in the order they were taken and a wave's items
+    // only grow, so once slot 0 is past the last item the wave is done.  The
+    // loop has no other exit and every refill is issued (past the end: no
+    // memory access), so each item waits only for its own loads.
+    while (rg.it[0] < total) {
+#pragma unroll
+        for (int p = 0; p < P; p++) {
+            int gi = 0;
+            if (lane == 0) gi = atomicAdd(&next_item, 1);
+            if (rg.it[p] < total) step(rg.it[p], rg.t[p], rg.sc[p]);
+            rg.it[p] = __builtin_amdgcn_readfirstlane(gi);
+            issue(t, g, rg.it[p], rg.t[p], rg.sc[p]);
+        }
+    }
+    __syncthreads();
+    // Rows: four adjacent threads per row, thread q summing its share of
+    // the row's partials (KBP: block q of every step; else steps q, q+4,
+    // ...), then the four added in lane order: the same order every time.
+    constexpr int PI = KBP ? 4 : 1;                      // partials per item and row
+    auto quarter = [&](int c, int r, int q) {
+        const float *pp = part + c * L * PI * 16 + r;
+        float acc = 0.f;
+        if constexpr (KBP)
+            for (int i = 0; i < L; i++) acc += pp[(i * 4 + q) * 16];
+        else
+            for (int i = q; i < L; i += 4) acc += pp[i * 16];
+        return acc;
+    };
+    // Quad lanes by DPP quad_perm (1,0,3,2) then (2,3,0,1): each lane adds
+    // its neighbour's value, so the four hold the same sum.
+    auto combine = [](float a) {
+        a += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(a), 0xB1, 0xF, 0xF, false));
+        return a + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(a), 0x4E, 0xF, 0xF, false));
+    };
+    const GluOut &glu = t.glu;
+    const __amdgpu_buffer_rsrc_t yrs = make_rsrc(y, (uint32_t)R * 4u);
+    const __amdgpu_buffer_rsrc_t ors = make_rsrc(glu.out, glu.pair_sets ? (uint32_t)glu.pair_sets * 32u : 0u);
+    const int nrow = (glu.pair_sets ? npair : g.nset_wg) * 16;
+    for (int base = 0; base < nrow * 4; base += MT) {   // uniform trip count: shuffles stay whole
+        const int i = (base + threadIdx.x) >> 2, q = threadIdx.x & 3;
+        const bool ok = i < nrow;
+        const int c = ok ? i >> 4 : 0, r = i & 15;
+        if (glu.pair_sets) {
+            const float gv = combine(ok ? quarter(c, r, q) : 0.f);
+            const float u = combine(ok ? quarter(npair + c, r, q) : 0.f);
+            if (ok && q == 0)
+                __builtin_amdgcn_raw_buffer_store_b16(gd_f2h(gd_silu(gv) * u), ors,
+                                                      (uint32_t)(set_lo * 16 + i) * 2u, 0, XPOL);
+        } else {
+            const float v = combine(ok ? quarter(c, r, q) : 0.f);
+            if (ok && q == 0 && set_lo * 16 + i < R)
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), yrs,
+                                                      (uint32_t)(set_lo * 16 + i) * 4u, 0, XPOL);
+        }
+    }
+}
+
+}  // namespace gemv
