@@ -1,6 +1,5 @@
-// The Q2_0 GEMV on the matrix cores as a device function, shared by the
-// standalone GEMV kernel (q2_0_gemv_mfma.hip) and the persistent decode
-// kernel (decode.hip).
+// The Q2_0 GEMV on the matrix cores as a device function (gemv::run), the
+// body of the GEMV kernel in q2_0_gemv_mfma.hip.
 //
 // Same result as q2_0_gemv (Kernels.metal:30-119) and Q2_0.matvec
 // (Quant.swift:36-77): per block d * (sum(code*x) - sum(x)), f32 throughout.
@@ -47,14 +46,6 @@
 //     the end returns zeros without a memory access, so every load in the
 //     main loop is unconditional and the compiler waits only for the tile an
 //     item needs.  x is requested before the tiles (loads return in order).
-//     A caller that runs several GEMVs back to back in one kernel can issue
-//     the next GEMV's first ring loads (gemv::prefetch) before it waits for
-//     that GEMV's input: weights do not depend on it.
-//   * Coherent mode (CO).  Inside one persistent kernel, a GEMV's input was
-//     written moments earlier by other workgroups, possibly on another XCD
-//     (each XCD has its own L2).  Then x, the residual and its partials are
-//     read, and y / the SwiGLU output / h' written, with sc0|sc1 buffer
-//     accesses, which go to the coherent memory side instead of an L2.
 #pragma once
 
 #include "gd_internal.h"
@@ -69,7 +60,6 @@ constexpr size_t LDS_BYTES = 160 * 1024 - 2048;
 // waves and 3 or 4 tiles everywhere.
 constexpr int NW = 16, P = 2;
 constexpr int CP_NT = 2;     // cache policy: non-temporal (streamed once)
-constexpr int COH = 0x11;    // cache policy: sc0 | sc1 (coherent across XCDs)
 
 // LDS bytes of the x staging: the x planes (two for f32 x), then the block
 // sums and exponents of x.
@@ -218,31 +208,16 @@ __device__ __forceinline__ void issue(const Task &t, const Geo &g, int it, u32x4
     sc = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(srs, pick(si, dead | other), 0, 0));
 }
 
-// The first ring loads of task t for this wave (items p * NW + wave), so
-// they are in flight before the caller waits for t's input.
-__device__ __forceinline__ void prefetch(const Task &t, int wg, Ring &rg) {
-    const Geo g = geometry(t, wg);
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-#pragma unroll
-    for (int p = 0; p < P; p++) {
-        rg.it[p] = p * NW + wave;
-        issue(t, g, rg.it[p], rg.t[p], rg.sc[p]);
-    }
-}
-
 // Runs task t's share of workgroup wg.  lds: the dynamic LDS (x staging,
-// then the item partials).  With `prefetched`, rg already holds the loads
-// prefetch(t, wg, rg) issued.  XT: 0 = f16 x, 1 = f32 x (hi + lo split),
-// 2 = normalized residual (see XChunk).  KBP: item partials kept per Q2
-// block (4 per row) in LDS, summed with the rest of the row at the end;
-// otherwise summed across the block lanes first (needs 4x less LDS, for very
-// long K).  CO: coherent input reads and output writes (see above).
+// then the item partials).  XT: 0 = f16 x, 1 = f32 x (hi + lo split), 2 =
+// normalized residual (see XChunk).  KBP: item partials kept per Q2 block (4
+// per row) in LDS, summed with the rest of the row at the end; otherwise
+// summed across the block lanes first (needs 4x less LDS, for very long K).
 // All 64 * NW threads of the workgroup must call it.
-template <int XT, bool KBP, bool CO>
-__device__ void run(const Task &t, int wg, uint32_t *lds, Ring &rg, bool prefetched) {
+template <int XT, bool KBP>
+__device__ void run(const Task &t, int wg, uint32_t *lds) {
     constexpr int MT = 64 * NW;
     constexpr bool HL = XT == 1;                          // x carried as f16 hi + lo
-    constexpr int XPOL = CO ? COH : 0;                    // cache policy of x reads
     __shared__ __align__(16) int next_item;               // next item to take
     const Geo g = geometry(t, wg);
     const int K = t.K, R = t.R;
@@ -267,9 +242,6 @@ __device__ void run(const Task &t, int wg, uint32_t *lds, Ring &rg, bool prefetc
     const int j = lane & 3, rq = (lane >> 2) & 3, kb = lane >> 4;
     float *y = t.y + (size_t)g.bz * R;
     const int L = g.L, s0 = g.s0, set_lo = g.set_lo, npair = g.npair, total = g.total;
-    // A workgroup with no items (more workgroups than sets) still stages
-    // nothing and returns after the caller's shared barrier points.
-    if (total == 0) return;
 
     // Staging entry e = (block e/8, chunk e%8): its x loads are issued before
     // the tile prefetch, so waiting for them leaves the tiles in flight.
@@ -285,12 +257,12 @@ __device__ void run(const Task &t, int wg, uint32_t *lds, Ring &rg, bool prefetc
         const int off = e < nblk * 8 ? (e >> 3) * 128 + 16 * (e & 7) : K;   // element offset
         XChunk<XT> c;
         if constexpr (XT == 0) {
-            c.lo = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, off * 2, 0, XPOL));
-            c.hi = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, off * 2 + 16, 0, XPOL));
+            c.lo = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, off * 2, 0, 0));
+            c.hi = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, off * 2 + 16, 0, 0));
         } else {
 #pragma unroll
             for (int q = 0; q < 4; q++)
-                c.f[q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, off * 4 + 16 * q, 0, XPOL));
+                c.f[q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, off * 4 + 16 * q, 0, 0));
             if constexpr (XT == 2) {
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
@@ -300,7 +272,7 @@ __device__ void run(const Task &t, int wg, uint32_t *lds, Ring &rg, bool prefetc
                     for (int z = 0; z < nin.nd; z++)
                         c.d[q] += __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
                                 drs, off < K ? (uint32_t)((z * nin.dstride + off) * 4 + 16 * q)
-                                             : 0xfffff000u, 0, XPOL));
+                                             : 0xfffff000u, 0, 0));
                     c.w[q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs, off * 4 + 16 * q, 0, 0));
                 }
             }
@@ -317,11 +289,10 @@ __device__ void run(const Task &t, int wg, uint32_t *lds, Ring &rg, bool prefetc
     // from the workgroup counter when a slot frees up.  One tile goes out
     // before the staging, the rest of the ring after it, so x (needed first)
     // does not queue behind the whole grid's prefetch.
-    if (!prefetched) {
+    Ring rg;
 #pragma unroll
-        for (int p = 0; p < P; p++) rg.it[p] = p * NW + wave;
-        issue(t, g, rg.it[0], rg.t[0], rg.sc[0]);
-    }
+    for (int p = 0; p < P; p++) rg.it[p] = p * NW + wave;
+    issue(t, g, rg.it[0], rg.t[0], rg.sc[0]);
     if (threadIdx.x == 0) next_item = NW * P;
 
     // Stage x: pair p = 8i + k of block b holds (x[b,16i+k], x[b,16i+k+8]) *
@@ -413,7 +384,7 @@ __device__ void run(const Task &t, int wg, uint32_t *lds, Ring &rg, bool prefetc
 #pragma unroll
             for (int q = 0; q < 4; q++)
                 __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, xc.f[q]), hrs,
-                                                       ho + 16 * q, 0, XPOL);
+                                                       ho + 16 * q, 0, 0);
         }
         __syncthreads();
         float tot = 0.f;
@@ -428,10 +399,8 @@ __device__ void run(const Task &t, int wg, uint32_t *lds, Ring &rg, bool prefetc
     stage(threadIdx.x, xc);
     if constexpr (XT != 2)
         for (int e = threadIdx.x + MT; e < nstage; e += MT) stage(e, load_x(e));
-    if (!prefetched) {
 #pragma unroll
-        for (int p = 1; p < P; p++) issue(t, g, rg.it[p], rg.t[p], rg.sc[p]);
-    }
+    for (int p = 1; p < P; p++) issue(t, g, rg.it[p], rg.t[p], rg.sc[p]);
     __syncthreads();
 
     // One item (set c, step s): the four Q2 blocks 4s .. 4s+3 of 16 rows.
@@ -547,12 +516,12 @@ __device__ void run(const Task &t, int wg, uint32_t *lds, Ring &rg, bool prefetc
             const float u = combine(ok ? quarter(npair + c, r, q) : 0.f);
             if (ok && q == 0)
                 __builtin_amdgcn_raw_buffer_store_b16(gd_f2h(gd_silu(gv) * u), ors,
-                                                      (uint32_t)(set_lo * 16 + i) * 2u, 0, XPOL);
+                                                      (uint32_t)(set_lo * 16 + i) * 2u, 0, 0);
         } else {
             const float v = combine(ok ? quarter(c, r, q) : 0.f);
             if (ok && q == 0 && set_lo * 16 + i < R)
                 __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), yrs,
-                                                      (uint32_t)(set_lo * 16 + i) * 4u, 0, XPOL);
+                                                      (uint32_t)(set_lo * 16 + i) * 4u, 0, 0);
         }
     }
 }

@@ -1,8 +1,7 @@
 // Q2_0 GEMV on the matrix cores: y[r] = sum_k W[r,k] x[k], as one kernel
 // launch.  The kernel body, with its design notes, is gemv::run
-// (gemv_core.h), which the persistent decode kernel (decode.hip) shares; this
-// file holds the standalone kernel and the host side: the work split, the
-// K-split choice and the entry points the C ABI and the stack call.
+// (gemv_core.h); this file holds the kernel and the host side: the work
+// split, the K-split choice and the entry points the C ABI and the stack call.
 #include "gemv_core.h"
 
 namespace {
@@ -16,8 +15,7 @@ using gemv::xlds_bytes;
 template <int XT, bool KBP>
 __global__ __launch_bounds__(64 * NW) void q2_0_gemv_mfma_kernel(gemv::Task t) {
     extern __shared__ __align__(16) uint32_t lds[];
-    gemv::Ring rg;
-    gemv::run<XT, KBP, false>(t, (int)(blockIdx.y * gridDim.x + blockIdx.x), lds, rg, false);
+    gemv::run<XT, KBP>(t, (int)(blockIdx.y * gridDim.x + blockIdx.x), lds);
 }
 
 // Work split of a GEMV: `per` consecutive sets per workgroup, K cut into nz
@@ -89,22 +87,6 @@ int launch(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, size_t xlds,
 
 }  // namespace
 
-// The task a GEMV launch would run, for a kernel that runs several GEMVs
-// (decode.hip): f16 x (XT 0) or the fused add + RMSNorm input (XT 2, with
-// nin, optionally SwiGLU output), on `cus` workgroups; *lds the dynamic LDS
-// it needs, *kbp its partial layout.
-int gd_gemv_task(gd_ctx *ctx, const gd_q2w *w, int xt, const void *x, float *y, int ksplit,
-                 const gemv::NormIn &nin, uint16_t *glu_out, int cus, gemv::Task *t,
-                 size_t *lds, bool *kbp) {
-    const int nblk = (int)(w->K >> 7);
-    const size_t xlds = xlds_bytes(nblk, false);
-    GD_REQUIRE(ctx, xt == 0 || xt == 2, "gd_gemv_task: x type %d", xt);
-    GD_REQUIRE(ctx, xt == 0 || (nblk + 5) * 8 <= 1024, "gd_gemv_task: K=%lld too long",
-               (long long)w->K);
-    GD_REQUIRE(ctx, !glu_out || w->R % 32 == 0, "gd_gemv_task: SwiGLU needs R = 2 x 16k rows");
-    const GluOut glu{glu_out, glu_out ? (int)(w->R / 32) : 0};
-    return make_task(ctx, w, x, y, xlds, nin, glu_out ? 1 : ksplit, glu, cus, t, lds, kbp);
-}
 
 // GEMV on the matrix cores for f16 or f32 x (the caller has checked w, x, y).
 // ksplit > 1 cuts K into that many splits whose partial rows go to y + z * R
