@@ -1,0 +1,686 @@
+// Gated GQA attention over an f16 paged KV cache, for head dims 128 and 256.
+//
+// Reference: Attn.step (LLM/src/SIMD/Attention.swift:72-139) and the Metal
+// dispatches MetalEnc.splitQGate / kvAppend / attnPaged (MetalEnc.swift:
+// 656-706), splitQGateBatch / ropeBatch / kvAppendBatch (:780-847) and
+// attnBatch (:966-1025), driven by MetalEngine.attnLayer / attnBatchLayer
+// (MetalEngine.swift:405-451, 756-796).  Per head h with kv head h / (nH/nKV):
+// softmax over positions t <= pos of (q . k_t) * scale, times v_t, then times
+// sigmoid(gate) when gated.  K and V are cached as f16 (half pages,
+// MetalKVPool.swift), addressed through a page table: position p lives in
+// page table[p / P] at slot p % P.  The reference's page table holds page
+// addresses (bindless); here it holds page indices into one pool allocation,
+// which is how a HIP caller would lay pages out.
+//
+// MI355X design:
+//   * Decode (one query): flash decoding, DSPLIT key splits per head; each
+//     wave takes whole keys, a lane holding HD/64 consecutive dims, with an
+//     online softmax; a block merges its waves and writes (max, sum,
+//     acc[HD]); a combine kernel merges the splits with the output gate.  The
+//     stack's variant folds in the per-token preparation (split of q|gate,
+//     RMS norm, partial NEOX rope, the cache append), so the new key never
+//     round-trips through the cache within the step.
+//   * Prefill (N queries): flash attention on the matrix cores, block (head,
+//     64 queries); keys in blocks of 32 through LDS; S^T = K Q^T and O^T +=
+//     V^T P^T on v_mfma_f32_16x16x32_f16 with the key order inside the MFMA
+//     K dimension permuted so that P stays in registers; q and P as f16
+//     hi + lo pairs (about 22 bits), K and V the f16 cache, f32 accumulation.
+#include "gd_internal.h"
+
+#include <type_traits>
+
+namespace {
+
+constexpr int DSPLIT = 16;      // key splits per head (decode)
+constexpr int AQ = 64, AK = 32; // queries per prefill block, keys per LDS block
+
+__device__ __forceinline__ int64_t kv_slot(const int32_t *pt, int pos, int block) {
+    return (int64_t)pt[pos / block] * block + pos % block;
+}
+
+// Partial NEOX rope of dim i (< n_rot) of a head whose values are `mine` (dim
+// i) and `pv` (its partner i +- n_rot/2), at position pos (Kern.ropeNeox,
+// Kernels.swift:66-84).
+__device__ __forceinline__ float rope_dim(int i, float mine, float pv, int n_rot, float base,
+                                          int pos) {
+    const int half = n_rot / 2;
+    const int jj = i < half ? i : i - half;
+    const float freq = powf(base, -2.0f * (float)jj / (float)n_rot);
+    const float ang = (float)pos * freq;
+    const float c = cosf(ang), sn = sinf(ang);
+    return i < half ? mine * c - pv * sn : pv * sn + mine * c;
+}
+
+// ---------------------------------------------------------------- prefill prep
+
+// Attention prep (prefill), one wave per (token, head): q heads take the q
+// half of the fused [q | gate] pair, RMS-normalize it with q_norm and rotate
+// it; kv heads normalize + rotate k and append k, v to the f16 cache at the
+// token's position (Attention.swift:79-107).  Lane l holds dims l + 64 s.
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_prep(
+        const float *proj, int64_t stride, const float *q_norm, const float *k_norm, float *q_out,
+        float *gate_out, uint16_t *kc, uint16_t *vc, const int32_t *page_table,
+        const int32_t *pos_ptr, int N, int H, int HKV, int n_rot, float base, int block, float eps) {
+    constexpr int S = HD / 64;
+    const int64_t task = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (task >= (int64_t)N * (H + HKV)) return;
+    const int n = (int)(task / (H + HKV)), h = (int)(task % (H + HKV)), lane = threadIdx.x & 63;
+    const int pos = *pos_ptr + n;
+    const float *row = proj + (int64_t)n * stride;
+    const bool is_q = h < H;
+    const int kh = h - H;
+    const float *src = is_q ? row + h * 2 * HD : row + 2 * H * HD + kh * HD;
+    const float *nw = is_q ? q_norm : k_norm;
+    float x[S], y[S];
+    float ss = 0.f;
+#pragma unroll
+    for (int s = 0; s < S; s++) {
+        x[s] = src[lane + 64 * s];
+        ss += x[s] * x[s];
+    }
+    // RMS norm over the head (Kern.rmsnormRows, Kernels.swift:26-37).
+    ss = gd_wave_sum(ss);
+    const float sc = 1.0f / sqrtf(ss / (float)HD + eps);
+#pragma unroll
+    for (int s = 0; s < S; s++) y[s] = x[s] * sc * nw[lane + 64 * s];
+    // Dim i pairs with i +- n_rot/2, held by another lane (or slot).
+    const int half = n_rot / 2;
+    float r[S];
+#pragma unroll
+    for (int k = 0; k < S; k++) {
+        const int i = lane + 64 * k;
+        const int ip = i < half ? i + half : i - half;          // partner dim
+        float p[S];
+#pragma unroll
+        for (int s = 0; s < S; s++) p[s] = __shfl(y[s], ip & 63, 64);
+        float pv = p[0];
+#pragma unroll
+        for (int s = 1; s < S; s++) pv = (ip >> 6) == s ? p[s] : pv;
+        r[k] = i < n_rot ? rope_dim(i, y[k], pv, n_rot, base, pos) : y[k];
+    }
+    if (is_q) {
+        float *qo = q_out + ((int64_t)n * H + h) * HD;
+        float *go = gate_out + ((int64_t)n * H + h) * HD;
+#pragma unroll
+        for (int s = 0; s < S; s++) {
+            qo[lane + 64 * s] = r[s];
+            go[lane + 64 * s] = row[h * 2 * HD + HD + lane + 64 * s];
+        }
+    } else {
+        const int kvDim = HKV * HD;
+        const int64_t slot = kv_slot(page_table, pos, block);
+        const float *vs = row + 2 * H * HD + HKV * HD + kh * HD;
+#pragma unroll
+        for (int s = 0; s < S; s++) {
+            kc[slot * kvDim + kh * HD + lane + 64 * s] = gd_f2h(r[s]);
+            vc[slot * kvDim + kh * HD + lane + 64 * s] = gd_f2h(vs[lane + 64 * s]);
+        }
+    }
+}
+
+// ---------------------------------------------------------------- prefill
+
+// Causal prefill attention with the sigmoid output gate (Attention.swift:
+// 108-134), flash style on the matrix cores.  Block (head h, 64 queries):
+// wave w owns queries 16w .. 16w+15; keys stream through LDS in blocks of
+// 32 (K as [key][d], V transposed as [d][key]).  Per block a wave forms
+// S^T = K Q^T (v_mfma_f32_16x16x32_f16, lane = one query column and four
+// keys of each 16-key tile), updates its online softmax per query, and adds
+// V^T P^T into O^T.  The C layout of S^T is already the B operand of V^T P^T
+// once the MFMA's K index 8g + e (g = lane / 16) stands for key 4g + e
+// (e < 4) or 16 + 4g + e - 4: the A operand (V^T) reads the same keys, so P
+// never goes through LDS.  q and P enter as f16 hi + lo pairs (about 22
+// bits), K and V are the f16 cache itself, accumulation is f32.  Queries sit
+// at positions pos0 + n with pos0 = *pos_ptr (if not null) + pos_add.
+template <int HD, typename OT>
+__global__ __launch_bounds__(256) void k_attn_prefill(
+        const float *q, const float *gate, const uint16_t *kc, const uint16_t *vc,
+        const int32_t *page_table, const int32_t *pos_ptr, int pos_add, OT *out, int H, int HKV,
+        int N, int block, float scale, int gated) {
+    constexpr int CH = HD / 64;                           // 8-dim chunks a thread stages per operand
+    __shared__ __attribute__((aligned(16))) f16 Ks[AK][HD + 8];
+    __shared__ __attribute__((aligned(16))) f16 Vt[HD][AK + 8];
+    const int h = blockIdx.x, q0 = blockIdx.y * AQ;
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int lq = lane & 15, g = lane >> 4;
+    const int kvh = h / (H / HKV);
+    const int kvDim = HKV * HD;
+    const int pos0 = (pos_ptr ? *pos_ptr : 0) + pos_add;
+    const int n = q0 + 16 * w + lq;                       // this lane's query
+    const bool valid = n < N;
+    const int my_pos = pos0 + (valid ? n : N - 1);
+    // B operand of S^T: q[n][32 ks + 8 g + e] * scale, split hi + lo.
+    f16x8 qh[HD / 32], ql[HD / 32];
+    {
+        const float *qrow = q + ((int64_t)(valid ? n : N - 1) * H + h) * HD;
+#pragma unroll
+        for (int ks = 0; ks < HD / 32; ks++) {
+            const f32x4 a = *(const f32x4 *)(qrow + 32 * ks + 8 * g);
+            const f32x4 b = *(const f32x4 *)(qrow + 32 * ks + 8 * g + 4);
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float v = (e < 4 ? a[e] : b[e - 4]) * scale;
+                qh[ks][e] = (f16)v;
+                ql[ks][e] = (f16)(v - (float)qh[ks][e]);
+            }
+        }
+    }
+    f32x4 acc[HD / 16];                                   // O^T rows 16 dt + 4 g + v
+#pragma unroll
+    for (int dt = 0; dt < HD / 16; dt++) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m = -INFINITY, l = 0.f;                         // this lane's keys only
+    const int last = pos0 + min(q0 + AQ, N) - 1;          // last key any query here needs
+    // Staging: thread t loads dims d0 .. d0 + HD/8 - 1 of key t / 8 of the
+    // block.  The loads run ahead of the arithmetic: block k0 + AK's K and V
+    // rows are requested before block k0's MFMAs, and the page-table entry
+    // they need one block earlier still, so no block waits for a memory
+    // round trip (blocks past `last` clamp to it: loaded, never used).
+    const int sk = t >> 3, d0 = (t & 7) * (HD / 8);
+    auto page_of = [&](int k0) { return page_table[min(k0 + sk, last) / block]; };
+    u32x4 kv[2 * CH];                                     // K chunks, then V chunks
+    auto fetch = [&](int k0, int page) {
+        const int p = min(k0 + sk, last);
+        const int64_t base = ((int64_t)page * block + p % block) * kvDim + kvh * HD + d0;
+#pragma unroll
+        for (int c = 0; c < CH; c++) {
+            kv[c] = *(const u32x4 *)(kc + base + 8 * c);
+            kv[CH + c] = *(const u32x4 *)(vc + base + 8 * c);
+        }
+    };
+    fetch(0, page_of(0));
+    int page_next = page_of(AK);
+    for (int k0 = 0; k0 <= last; k0 += AK) {
+        __syncthreads();
+#pragma unroll
+        for (int c = 0; c < CH; c++) {
+            *(u32x4 *)&Ks[sk][d0 + 8 * c] = kv[c];
+            const f16x8 va = __builtin_bit_cast(f16x8, kv[CH + c]);
+#pragma unroll
+            for (int e = 0; e < 8; e++) Vt[d0 + 8 * c + e][sk] = va[e];
+        }
+        __syncthreads();
+        fetch(k0 + AK, page_next);
+        page_next = page_of(k0 + 2 * AK);
+        // Keep the loads here: the compiler would sink them below the MFMAs,
+        // next to the LDS writes that wait for them.
+        __builtin_amdgcn_sched_barrier(0);
+        // S^T tiles kt = 0, 1: keys 16 kt + 4 g + v for query lq.
+        f32x4 sc[2];
+#pragma unroll
+        for (int kt = 0; kt < 2; kt++) {
+            sc[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < HD / 32; ks++) {
+                const f16x8 ka = *(const f16x8 *)&Ks[16 * kt + lq][32 * ks + 8 * g];
+                sc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qh[ks], sc[kt], 0, 0, 0);
+                sc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, ql[ks], sc[kt], 0, 0, 0);
+            }
+        }
+        // Causal mask (and the clamped duplicates past `last`), then the
+        // online softmax of query lq over its lane group's keys.
+        float bmax = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int kp = k0 + 16 * kt + 4 * g + v;
+                if (kp > my_pos) sc[kt][v] = -INFINITY;
+                bmax = fmaxf(bmax, sc[kt][v]);
+            }
+        bmax = fmaxf(bmax, __shfl_xor(bmax, 16, 64));
+        bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
+        const float mn = fmaxf(m, bmax);                  // finite: key k0 <= my_pos
+        // The softmax exponents are <= 0 (or -inf for masked keys: 0), where
+        // the hardware exp2 behind __expf is accurate to a few ulp.
+        const float alpha = __expf(m - mn);
+        m = mn;
+        l *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < HD / 16; dt++) acc[dt] *= alpha;
+        f16x8 ph, pl;
+#pragma unroll
+        for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const float pv = __expf(sc[kt][v] - mn);
+                l += pv;
+                const f16 hi = (f16)pv;
+                ph[4 * kt + v] = hi;
+                pl[4 * kt + v] = (f16)(pv - (float)hi);
+            }
+        // O^T += V^T P^T: A lane row d = 16 dt + lq, the same 8 keys.
+#pragma unroll
+        for (int dt = 0; dt < HD / 16; dt++) {
+            const f16 *vr = &Vt[16 * dt + lq][0];
+            const f16x4 v0 = *(const f16x4 *)(vr + 4 * g), v1 = *(const f16x4 *)(vr + 16 + 4 * g);
+            const f16x8 va = f16x8{v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+            acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, ph, acc[dt], 0, 0, 0);
+            acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl, acc[dt], 0, 0, 0);
+        }
+    }
+    // Total weight of query lq: the four lane groups' partial sums.
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    if (valid) {
+        const float inv = 1.0f / l;
+        const float *grow = gate + ((int64_t)n * H + h) * HD;
+        OT *orow = out + ((int64_t)n * H + h) * HD;
+#pragma unroll
+        for (int dt = 0; dt < HD / 16; dt++) {
+            const int d = 16 * dt + 4 * g;
+            float o[4];
+            if (gated) {
+                const f32x4 gv = *(const f32x4 *)(grow + d);
+#pragma unroll
+                for (int v = 0; v < 4; v++) o[v] = acc[dt][v] * inv * gd_sigmoid(gv[v]);
+            } else {
+#pragma unroll
+                for (int v = 0; v < 4; v++) o[v] = acc[dt][v] * inv;
+            }
+            if constexpr (sizeof(OT) == 2) {
+                *(uint64_t *)(orow + d) = (uint64_t)gd_f2h(o[0]) | ((uint64_t)gd_f2h(o[1]) << 16) |
+                                          ((uint64_t)gd_f2h(o[2]) << 32) | ((uint64_t)gd_f2h(o[3]) << 48);
+            } else {
+                *(f32x4 *)(orow + d) = f32x4{o[0], o[1], o[2], o[3]};
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------- decode
+
+// Decode attention for one query token, split over keys (flash decoding):
+// block (head h, split sp) of 2 HD threads (NWD = HD / 32 waves).
+//   FUSED (the stack): the block prepares its own q from the fused
+//   projection row (split of q|gate, RMS norm, rope; threads 0..HD-1) and the
+//   new k and v (threads HD..2HD-1), rounded to f16 as the cache stores them;
+//   the split that holds key pos uses them for that key instead of reading
+//   the cache, and the first q head of each kv group appends them.  No block
+//   reads the cache at pos.
+//   Otherwise (gd_attn_paged): q arrives prepared, the T keys lo .. T-1 are
+//   all cached.
+// Each wave takes whole keys j = lo + NWD sp + w + STEP i with a lane holding
+// HD/64 consecutive dims, keeping an online-softmax partial; the block
+// merges its waves and writes (max, sum, acc[HD]) for the split; the combine
+// kernel merges the splits (Attention.swift:108-134).
+template <int HD, bool FUSED>
+__global__ __launch_bounds__(2 * HD) void k_attn_decode(
+        const float *src, const float *q_norm, const float *k_norm, uint16_t *kc, uint16_t *vc,
+        const int32_t *page_table, const int32_t *pos_ptr, int T, int lo, float *part, int H,
+        int HKV, int block, float scale, int n_rot, float base, float eps) {
+    constexpr int NT = 2 * HD, NWD = NT / 64, DPL = HD / 64, WPH = HD / 64;
+    constexpr int STEP = DSPLIT * NWD;
+    __shared__ float wm[NWD], wl[NWD];
+    __shared__ float wacc[NWD][HD];
+    __shared__ float nrm[2][HD], rot[2][HD], vnew[HD], red[NWD];
+    const int h = blockIdx.x, sp = blockIdx.y, t = threadIdx.x;
+    const int lane = t & 63, w = t >> 6;
+    const int kvh = h / (H / HKV), kvDim = HKV * HD;
+    // Keys read from the cache: [lo, pos) for the stack (pos = the new
+    // token's position, taken from its registers), [lo, T) otherwise.
+    const int pos = FUSED ? *pos_ptr : T;
+    const bool has_pos = FUSED && sp == (pos / NWD) % DSPLIT;   // wave pos % NWD takes key pos
+    auto kv_base = [&](int j) {
+        return kv_slot(page_table, j, block) * kvDim + kvh * HD + DPL * lane;
+    };
+    // A lane's DPL f16 dims of one key: one dword (HD 128) or two (HD 256).
+    using U = typename std::conditional<DPL == 2, uint32_t, u32x2>::type;
+    auto ld = [&](const uint16_t *p) { return *(const U *)p; };
+    auto word = [](const U &u, int i) -> uint32_t {
+        if constexpr (DPL == 2) return u;
+        else return u[i];
+    };
+    // The first cached key of this wave is requested before the q/k work
+    // below, which does not depend on it.
+    int j = lo + sp * NWD + w;
+    U kn{}, vn{};
+    if (j < pos) {
+        const int64_t b0 = kv_base(j);
+        kn = ld(kc + b0);
+        vn = ld(vc + b0);
+    }
+    if constexpr (FUSED) {
+        // q of head h (hf = 0) and k of kv head kvh (hf = 1): RMS norm over
+        // the head, then the partial NEOX rope, as k_attn_prep.
+        const int H2 = 2 * H * HD;
+        const int hf = t / HD, i = t % HD;
+        const float x = hf == 0 ? src[h * 2 * HD + i] : src[H2 + kvh * HD + i];
+        const float nw = hf == 0 ? q_norm[i] : k_norm[i];
+        const float vx = src[H2 + HKV * HD + kvh * HD + i];
+        const float sq = gd_wave_sum(x * x);
+        if (lane == 0) red[w] = sq;
+        __syncthreads();
+        float ss = 0.f;
+#pragma unroll
+        for (int k = 0; k < WPH; k++) ss += red[hf * WPH + k];
+        const float sc = 1.0f / sqrtf(ss / (float)HD + eps);
+        float y = x * sc * nw;
+        nrm[hf][i] = y;
+        __syncthreads();
+        const int half = n_rot / 2;
+        if (i < n_rot)
+            y = rope_dim(i, nrm[hf][i], i < half ? nrm[hf][i + half] : nrm[hf][i - half], n_rot,
+                         base, pos);
+        rot[hf][i] = y;
+        if (hf == 1) vnew[i] = vx;
+        __syncthreads();
+        if (hf == 1 && has_pos && h % (H / HKV) == 0) {
+            const int64_t slot = kv_slot(page_table, pos, block);
+            kc[slot * kvDim + kvh * HD + i] = gd_f2h(y);
+            vc[slot * kvDim + kvh * HD + i] = gd_f2h(vnew[i]);
+        }
+    } else {
+        if (t < HD) rot[0][t] = src[(int64_t)h * HD + t];
+        __syncthreads();
+    }
+    float qv[DPL], a[DPL];
+#pragma unroll
+    for (int e = 0; e < DPL; e++) {
+        qv[e] = rot[0][DPL * lane + e] * scale;
+        a[e] = 0.f;
+    }
+    float m = -INFINITY, l = 0.f;
+    auto consume = [&](U kk, U vv) {
+        float s = 0.f;
+#pragma unroll
+        for (int e = 0; e < DPL; e++)
+            s += qv[e] * gd_h2f((uint16_t)((word(kk, e >> 1) >> (16 * (e & 1))) & 0xffff));
+        s = gd_wave_sum(s);
+        const float mn = fmaxf(m, s);
+        const float al = expf(m - mn), p = expf(s - mn);
+        l = l * al + p;
+#pragma unroll
+        for (int e = 0; e < DPL; e++)
+            a[e] = fmaf(p, gd_h2f((uint16_t)((word(vv, e >> 1) >> (16 * (e & 1))) & 0xffff)), a[e] * al);
+        m = mn;
+    };
+    // Cached keys: the next key's page-table entry and K/V values are
+    // requested before this key's arithmetic, so each key waits only for
+    // loads issued a key earlier.
+    for (; j < pos; j += STEP) {
+        const U kk = kn, vv = vn;
+        if (j + STEP < pos) {
+            const int64_t bn = kv_base(j + STEP);
+            kn = ld(kc + bn);
+            vn = ld(vc + bn);
+        }
+        consume(kk, vv);
+    }
+    if constexpr (FUSED) {
+        // Key pos, from this block's own copy (f16, as cached).
+        if (has_pos && w == pos % NWD) {
+            uint32_t kw[DPL / 2], vw[DPL / 2];
+#pragma unroll
+            for (int e = 0; e < DPL / 2; e++) {
+                kw[e] = (uint32_t)gd_f2h(rot[1][DPL * lane + 2 * e]) |
+                        ((uint32_t)gd_f2h(rot[1][DPL * lane + 2 * e + 1]) << 16);
+                vw[e] = (uint32_t)gd_f2h(vnew[DPL * lane + 2 * e]) |
+                        ((uint32_t)gd_f2h(vnew[DPL * lane + 2 * e + 1]) << 16);
+            }
+            U kk, vv;
+            if constexpr (DPL == 2) { kk = kw[0]; vv = vw[0]; }
+            else { kk = u32x2{kw[0], kw[1]}; vv = u32x2{vw[0], vw[1]}; }
+            consume(kk, vv);
+        }
+    }
+    if (lane == 0) { wm[w] = m; wl[w] = l; }
+#pragma unroll
+    for (int e = 0; e < DPL; e++) wacc[w][DPL * lane + e] = a[e];
+    __syncthreads();
+    if (t < HD) {
+        float M = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < NWD; i++) M = fmaxf(M, wm[i]);
+        float L = 0.f, A = 0.f;
+#pragma unroll
+        for (int i = 0; i < NWD; i++) {
+            const float f = wm[i] == -INFINITY ? 0.f : expf(wm[i] - M);
+            L += wl[i] * f;
+            A += wacc[i][t] * f;
+        }
+        float *p = part + ((int64_t)h * DSPLIT + sp) * (HD + 2);
+        p[t] = A;
+        if (t == 0) { p[HD] = M; p[HD + 1] = L; }
+    }
+}
+
+// Merges the DSPLIT partials of head h (HD threads): out[h][d] = A / L,
+// times sigmoid of the raw gate gate[h * gstride + d] when gated.
+template <int HD, typename OT>
+__global__ void k_attn_combine(const float *part, const float *gate, int gstride, int gated,
+                               OT *out) {
+    const int h = blockIdx.x, t = threadIdx.x;
+    const float *p = part + (int64_t)h * DSPLIT * (HD + 2);
+    float M = -INFINITY;
+    for (int s = 0; s < DSPLIT; s++) M = fmaxf(M, p[s * (HD + 2) + HD]);
+    float L = 0.f, A = 0.f;
+    for (int s = 0; s < DSPLIT; s++) {
+        const float ms = p[s * (HD + 2) + HD];
+        const float f = ms == -INFINITY ? 0.f : expf(ms - M);
+        L += p[s * (HD + 2) + HD + 1] * f;
+        A += p[s * (HD + 2) + t] * f;
+    }
+    float o = A / L;
+    if (gated) o *= gd_sigmoid(gate[(int64_t)h * gstride + t]);
+    if constexpr (sizeof(OT) == 2) out[(int64_t)h * HD + t] = gd_f2h(o);
+    else out[(int64_t)h * HD + t] = o;
+}
+
+// ---------------------------------------------------------------- glue
+
+// qFull [N][nH][2 hd] (per head q | gate, Attention.swift:84-93) -> q, gate.
+__global__ void k_split_q_gate(const float *qf, float *q, float *gate, int hd, int64_t total) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;   // over N * nH * hd
+    if (i >= total) return;
+    const int64_t head = i / hd, d = i % hd;
+    q[i] = qf[head * 2 * hd + d];
+    gate[i] = qf[head * 2 * hd + hd + d];
+}
+
+// x [N][nH][hd] f32, in place: the first n_rot dims of each head rotated
+// NEOX-style at position base_pos + n (Kern.ropeNeox, Kernels.swift:66-84).
+__global__ void k_rope(float *x, int hd, int nH, int n_rot, float base, int base_pos,
+                       int64_t total) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;   // over N * nH * n_rot/2
+    if (i >= total) return;
+    const int half = n_rot / 2;
+    const int j = (int)(i % half);
+    const int64_t head = i / half;
+    const int n = (int)(head / nH);
+    float *p = x + head * hd;
+    const float freq = powf(base, -2.0f * (float)j / (float)n_rot);
+    const float ang = (float)(base_pos + n) * freq;
+    const float c = cosf(ang), s = sinf(ang);
+    const float a = p[j], b = p[j + half];
+    p[j] = a * c - b * s;
+    p[j + half] = a * s + b * c;
+}
+
+// k, v [N][kvDim] f32 -> the f16 cache at positions base_pos + n.
+__global__ void k_kv_append(const float *k, const float *v, uint16_t *kc, uint16_t *vc,
+                            const int32_t *page_table, int kv_dim, int base_pos, int block,
+                            int64_t total) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;   // over N * kvDim
+    if (i >= total) return;
+    const int n = (int)(i / kv_dim), d = (int)(i % kv_dim);
+    const int64_t slot = kv_slot(page_table, base_pos + n, block);
+    kc[slot * kv_dim + d] = gd_f2h(k[i]);
+    vc[slot * kv_dim + d] = gd_f2h(v[i]);
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------- launchers
+
+int gd_attn_prep_launch(gd_ctx *ctx, int hd, const float *proj, int64_t stride,
+                        const float *q_norm, const float *k_norm, float *q_out, float *gate_out,
+                        uint16_t *kc, uint16_t *vc, const int32_t *page_table,
+                        const int32_t *pos_ptr, int N, int H, int HKV, int n_rot, float base,
+                        int block, float eps) {
+    const dim3 grid(gd_blocks((int64_t)N * (H + HKV), 4));
+    if (hd == 128)
+        hipLaunchKernelGGL(k_attn_prep<128>, grid, dim3(256), 0, ctx->stream, proj, stride,
+                           q_norm, k_norm, q_out, gate_out, kc, vc, page_table, pos_ptr, N, H,
+                           HKV, n_rot, base, block, eps);
+    else
+        hipLaunchKernelGGL(k_attn_prep<256>, grid, dim3(256), 0, ctx->stream, proj, stride,
+                           q_norm, k_norm, q_out, gate_out, kc, vc, page_table, pos_ptr, N, H,
+                           HKV, n_rot, base, block, eps);
+    GD_LAUNCHED(ctx, "k_attn_prep");
+    return GD_OK;
+}
+
+int gd_attn_prefill_launch(gd_ctx *ctx, int hd, const float *q, const float *gate,
+                           const uint16_t *kc, const uint16_t *vc, const int32_t *page_table,
+                           const int32_t *pos_ptr, int pos_add, void *out, int out_dtype, int H,
+                           int HKV, int N, int block, float scale, int gated) {
+    const dim3 grid((unsigned)H, gd_blocks(N, AQ));
+#define GD_AP(HD_, OT_) hipLaunchKernelGGL((k_attn_prefill<HD_, OT_>), grid, dim3(256), 0, \
+        ctx->stream, q, gate, kc, vc, page_table, pos_ptr, pos_add, (OT_ *)out, H, HKV, N, block, \
+        scale, gated)
+    if (hd == 128) { if (out_dtype == GD_F16) GD_AP(128, uint16_t); else GD_AP(128, float); }
+    else { if (out_dtype == GD_F16) GD_AP(256, uint16_t); else GD_AP(256, float); }
+#undef GD_AP
+    GD_LAUNCHED(ctx, "k_attn_prefill");
+    return GD_OK;
+}
+
+// Fused decode (the stack): split + combine into f16 out.
+int gd_attn_decode_launch(gd_ctx *ctx, int hd, const float *proj, const float *q_norm,
+                          const float *k_norm, uint16_t *kc, uint16_t *vc,
+                          const int32_t *page_table, const int32_t *pos_ptr, float *part,
+                          uint16_t *out, int H, int HKV, int block, float scale, int n_rot,
+                          float base, float eps) {
+    const dim3 grid((unsigned)H, DSPLIT);
+    if (hd == 128) {
+        hipLaunchKernelGGL((k_attn_decode<128, true>), grid, dim3(256), 0, ctx->stream, proj,
+                           q_norm, k_norm, kc, vc, page_table, pos_ptr, 0, 0, part, H, HKV, block,
+                           scale, n_rot, base, eps);
+        GD_LAUNCHED(ctx, "k_attn_decode");
+        hipLaunchKernelGGL((k_attn_combine<128, uint16_t>), dim3(H), dim3(128), 0, ctx->stream,
+                           part, proj + 128, 2 * 128, 1, out);
+    } else {
+        hipLaunchKernelGGL((k_attn_decode<256, true>), grid, dim3(512), 0, ctx->stream, proj,
+                           q_norm, k_norm, kc, vc, page_table, pos_ptr, 0, 0, part, H, HKV, block,
+                           scale, n_rot, base, eps);
+        GD_LAUNCHED(ctx, "k_attn_decode");
+        hipLaunchKernelGGL((k_attn_combine<256, uint16_t>), dim3(H), dim3(256), 0, ctx->stream,
+                           part, proj + 256, 2 * 256, 1, out);
+    }
+    GD_LAUNCHED(ctx, "k_attn_combine");
+    return GD_OK;
+}
+
+size_t gd_attn_part_floats(int hd, int H) { return (size_t)H * DSPLIT * (hd + 2); }
+
+// ---------------------------------------------------------------- C ABI
+
+extern "C" int gd_split_q_gate(gd_ctx *ctx, const float *q_full, float *q, float *gate, int hd,
+                               int n_head, int64_t N) {
+    GD_CHECK_CTX(ctx);
+    GD_REQUIRE(ctx, q_full && q && gate && hd > 0 && n_head > 0 && N >= 0,
+               "gd_split_q_gate: bad arguments");
+    const int64_t total = N * n_head * hd;
+    if (!total) return GD_OK;
+    hipLaunchKernelGGL(k_split_q_gate, dim3(gd_blocks(total, 256)), dim3(256), 0, ctx->stream,
+                       q_full, q, gate, hd, total);
+    GD_LAUNCHED(ctx, "gd_split_q_gate");
+    return GD_OK;
+}
+
+extern "C" int gd_rope(gd_ctx *ctx, float *x, int head_dim, int n_head, int n_rot, float base,
+                       int base_pos, int64_t N) {
+    GD_CHECK_CTX(ctx);
+    GD_REQUIRE(ctx, x && head_dim > 0 && n_head > 0 && N >= 0 && base_pos >= 0,
+               "gd_rope: bad arguments");
+    GD_REQUIRE(ctx, n_rot > 0 && n_rot % 2 == 0 && n_rot <= head_dim,
+               "gd_rope: n_rot %d must be even and at most head_dim %d", n_rot, head_dim);
+    const int64_t total = N * n_head * (n_rot / 2);
+    if (!total) return GD_OK;
+    hipLaunchKernelGGL(k_rope, dim3(gd_blocks(total, 256)), dim3(256), 0, ctx->stream, x,
+                       head_dim, n_head, n_rot, base, base_pos, total);
+    GD_LAUNCHED(ctx, "gd_rope");
+    return GD_OK;
+}
+
+extern "C" int gd_kv_append(gd_ctx *ctx, const float *k, const float *v, uint16_t *k_cache,
+                            uint16_t *v_cache, const int32_t *page_table, int kv_dim,
+                            int base_pos, int page_size, int64_t N) {
+    GD_CHECK_CTX(ctx);
+    GD_REQUIRE(ctx, k && v && k_cache && v_cache && page_table && kv_dim > 0 && page_size > 0 &&
+                        base_pos >= 0 && N >= 0,
+               "gd_kv_append: bad arguments");
+    const int64_t total = N * kv_dim;
+    if (!total) return GD_OK;
+    hipLaunchKernelGGL(k_kv_append, dim3(gd_blocks(total, 256)), dim3(256), 0, ctx->stream, k, v,
+                       k_cache, v_cache, page_table, kv_dim, base_pos, page_size, total);
+    GD_LAUNCHED(ctx, "gd_kv_append");
+    return GD_OK;
+}
+
+namespace {
+
+int check_attn(gd_ctx *ctx, const char *fn, int hd, int n_head, int n_head_kv, int kv_dim,
+               int page_size, int gated, const void *gate) {
+    GD_REQUIRE(ctx, hd == 128 || hd == 256, "%s: head_dim %d (takes 128 or 256)", fn, hd);
+    GD_REQUIRE(ctx, n_head > 0 && n_head_kv > 0 && n_head % n_head_kv == 0,
+               "%s: n_head %d not a multiple of n_head_kv %d", fn, n_head, n_head_kv);
+    GD_REQUIRE(ctx, kv_dim == hd * n_head_kv, "%s: kv_dim %d != head_dim * n_head_kv", fn, kv_dim);
+    GD_REQUIRE(ctx, page_size > 0, "%s: page size %d", fn, page_size);
+    GD_REQUIRE(ctx, gated == 0 || (gated == 1 && gate), "%s: gated must be 0 or 1 (with gate)", fn);
+    return GD_OK;
+}
+
+}  // namespace
+
+extern "C" int gd_attn_paged(gd_ctx *ctx, const float *q, const uint16_t *k_cache,
+                             const uint16_t *v_cache, const int32_t *page_table,
+                             const float *gate, float *out, float *part, int hd, int n_head,
+                             int n_head_kv, int T, int kv_dim, int page_size, float scale,
+                             int gated, int lo) {
+    GD_CHECK_CTX(ctx);
+    GD_REQUIRE(ctx, q && k_cache && v_cache && page_table && out && part,
+               "gd_attn_paged: null pointer");
+    int rc = check_attn(ctx, "gd_attn_paged", hd, n_head, n_head_kv, kv_dim, page_size, gated, gate);
+    if (rc) return rc;
+    GD_REQUIRE(ctx, T > 0 && lo >= 0 && lo < T, "gd_attn_paged: keys [lo=%d, T=%d) empty", lo, T);
+    const dim3 grid((unsigned)n_head, DSPLIT);
+    uint16_t *kc = const_cast<uint16_t *>(k_cache), *vc = const_cast<uint16_t *>(v_cache);
+    if (hd == 128) {
+        hipLaunchKernelGGL((k_attn_decode<128, false>), grid, dim3(256), 0, ctx->stream, q,
+                           nullptr, nullptr, kc, vc, page_table, nullptr, T, lo, part, n_head,
+                           n_head_kv, page_size, scale, 0, 0.f, 0.f);
+        GD_LAUNCHED(ctx, "gd_attn_paged");
+        hipLaunchKernelGGL((k_attn_combine<128, float>), dim3(n_head), dim3(128), 0, ctx->stream,
+                           part, gate, 128, gated, out);
+    } else {
+        hipLaunchKernelGGL((k_attn_decode<256, false>), grid, dim3(512), 0, ctx->stream, q,
+                           nullptr, nullptr, kc, vc, page_table, nullptr, T, lo, part, n_head,
+                           n_head_kv, page_size, scale, 0, 0.f, 0.f);
+        GD_LAUNCHED(ctx, "gd_attn_paged");
+        hipLaunchKernelGGL((k_attn_combine<256, float>), dim3(n_head), dim3(256), 0, ctx->stream,
+                           part, gate, 256, gated, out);
+    }
+    GD_LAUNCHED(ctx, "gd_attn_paged combine");
+    return GD_OK;
+}
+
+extern "C" int gd_attn_batch(gd_ctx *ctx, const float *q, const uint16_t *k_cache,
+                             const uint16_t *v_cache, const int32_t *page_table,
+                             const float *gate, float *out, int hd, int n_head, int n_head_kv,
+                             int kv_dim, int page_size, float scale, int base_pos, int64_t N,
+                             int gated, int window) {
+    GD_CHECK_CTX(ctx);
+    GD_REQUIRE(ctx, q && k_cache && v_cache && page_table && out, "gd_attn_batch: null pointer");
+    int rc = check_attn(ctx, "gd_attn_batch", hd, n_head, n_head_kv, kv_dim, page_size, gated, gate);
+    if (rc) return rc;
+    GD_REQUIRE(ctx, base_pos >= 0 && N >= 0 && N < (1LL << 31), "gd_attn_batch: base_pos/N");
+    GD_REQUIRE(ctx, window == 0, "gd_attn_batch: window %d (only 0, the whole history)", window);
+    GD_REQUIRE(ctx, ((uintptr_t)q | (uintptr_t)out | (uintptr_t)(gated ? gate : q)) % 16 == 0,
+               "gd_attn_batch: q, gate and out must be 16-byte aligned");
+    if (!N) return GD_OK;
+    return gd_attn_prefill_launch(ctx, hd, q, gated ? gate : q, k_cache, v_cache, page_table,
+                                  nullptr, base_pos, out, GD_F32, n_head, n_head_kv, (int)N,
+                                  page_size, scale, gated);
+}

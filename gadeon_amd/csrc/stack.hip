@@ -28,7 +28,7 @@
 
 namespace {
 
-constexpr int HD = 128;   // head_dim / d_state handled by the fused kernels
+constexpr int HD = 128;   // d_state handled by the fused GDN kernels
 
 // ------------------------------------------------------------------ kernels
 
@@ -313,364 +313,6 @@ __global__ void k_onorm_silu(const float *o, const float *proj, int64_t stride, 
     dst[lane + 64] = gd_f2h(b * s * w[lane + 64] * gd_silu(z1));
 }
 
-// Attention prep (prefill), one wave per (token, head): q heads take
-// the q half of the fused [q | gate] pair, RMS-normalize it with q_norm and
-// rotate it; kv heads normalize + rotate k and append k, v to the f16 cache
-// at the token's position (Attention.swift:79-107).
-__global__ __launch_bounds__(256) void k_attn_prep(
-        const float *proj, int64_t stride, const float *q_norm, const float *k_norm, float *q_out,
-        float *gate_out, uint16_t *kc, uint16_t *vc, const int32_t *page_table,
-        const int32_t *pos_ptr, int N, int H, int HKV, int n_rot, float base, int block, float eps) {
-    // One wave per (token n, head h < H + HKV): lane l holds dims l and l + 64.
-    const int64_t task = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (task >= (int64_t)N * (H + HKV)) return;
-    const int n = (int)(task / (H + HKV)), h = (int)(task % (H + HKV)), lane = threadIdx.x & 63;
-    const int pos = *pos_ptr + n;
-    const float *row = proj + (int64_t)n * stride;
-    const bool is_q = h < H;
-    const int kh = h - H;
-    const float *src = is_q ? row + h * 2 * HD : row + 2 * H * HD + kh * HD;
-    const float *nw = is_q ? q_norm : k_norm;
-    const float x0 = src[lane], x1 = src[lane + 64];
-    const float w0 = nw[lane], w1 = nw[lane + 64];
-    // RMS norm over the head (Kern.rmsnormRows, Kernels.swift:26-37).
-    const float ss = gd_wave_sum(x0 * x0 + x1 * x1);
-    const float sc = 1.0f / sqrtf(ss / (float)HD + eps);
-    const float y0 = x0 * sc * w0, y1 = x1 * sc * w1;
-    // Partial NEOX rope on the first n_rot dims (Kern.ropeNeox,
-    // Kernels.swift:66-84): dim i pairs with i +- n_rot/2, held by another
-    // lane (or the other half of this one).
-    const int half = n_rot / 2;
-    float r[2] = {y0, y1};
-#pragma unroll
-    for (int k = 0; k < 2; k++) {
-        const int i = lane + 64 * k;
-        const int ip = i < half ? i + half : i - half;          // partner dim
-        const float mine = k ? y1 : y0;
-        // Both halves from the partner's lane; this lane picks the one it needs.
-        const float p0 = __shfl(y0, ip & 63, 64), p1 = __shfl(y1, ip & 63, 64);
-        const float pv = ip < 64 ? p0 : p1;
-        if (i < n_rot) {
-            const int jj = i < half ? i : i - half;
-            const float freq = powf(base, -2.0f * (float)jj / (float)n_rot);
-            const float ang = (float)pos * freq;
-            const float c = cosf(ang), sn = sinf(ang);
-            r[k] = i < half ? mine * c - pv * sn : pv * sn + mine * c;
-        }
-    }
-    if (is_q) {
-        float *qo = q_out + ((int64_t)n * H + h) * HD;
-        float *go = gate_out + ((int64_t)n * H + h) * HD;
-        qo[lane] = r[0];
-        qo[lane + 64] = r[1];
-        go[lane] = row[h * 2 * HD + HD + lane];
-        go[lane + 64] = row[h * 2 * HD + HD + lane + 64];
-    } else {
-        const int kvDim = HKV * HD;
-        const int64_t slot = (int64_t)page_table[pos / block] * block + pos % block;
-        const float *vs = row + 2 * H * HD + HKV * HD + kh * HD;
-        kc[slot * kvDim + kh * HD + lane] = gd_f2h(r[0]);
-        kc[slot * kvDim + kh * HD + lane + 64] = gd_f2h(r[1]);
-        vc[slot * kvDim + kh * HD + lane] = gd_f2h(vs[lane]);
-        vc[slot * kvDim + kh * HD + lane + 64] = gd_f2h(vs[lane + 64]);
-    }
-}
-
-__device__ __forceinline__ int64_t kv_slot(const int32_t *pt, int pos, int block) {
-    return (int64_t)pt[pos / block] * block + pos % block;
-}
-
-// Causal prefill attention with the sigmoid output gate (Attention.swift:
-// 108-134), flash style on the matrix cores.  Block (head h, 64 queries):
-// wave w owns queries 16w .. 16w+15; keys stream through LDS in blocks of
-// 32 (K as [key][d], V transposed as [d][key]).  Per block a wave forms
-// S^T = K Q^T (v_mfma_f32_16x16x32_f16, lane = one query column and four
-// keys of each 16-key tile), updates its online softmax per query, and adds
-// V^T P^T into O^T.  The C layout of S^T is already the B operand of V^T P^T
-// once the MFMA's K index 8g + e (g = lane / 16) stands for key 4g + e
-// (e < 4) or 16 + 4g + e - 4: the A operand (V^T) reads the same keys, so P
-// never goes through LDS.  q and P enter as f16 hi + lo pairs (about 22
-// bits), K and V are the f16 cache itself, accumulation is f32.
-constexpr int AQ = 64, AK = 32;
-__global__ __launch_bounds__(256) void k_attn_prefill(
-        const float *q, const float *gate, const uint16_t *kc, const uint16_t *vc,
-        const int32_t *page_table, const int32_t *pos_ptr, uint16_t *out, int H, int HKV,
-        int N, int block, float scale) {
-    __shared__ __attribute__((aligned(16))) f16 Ks[AK][HD + 8];
-    __shared__ __attribute__((aligned(16))) f16 Vt[HD][AK + 8];
-    const int h = blockIdx.x, q0 = blockIdx.y * AQ;
-    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-    const int lq = lane & 15, g = lane >> 4;
-    const int kvh = h / (H / HKV);
-    const int kvDim = HKV * HD;
-    const int pos0 = *pos_ptr;
-    const int n = q0 + 16 * w + lq;                       // this lane's query
-    const bool valid = n < N;
-    const int my_pos = pos0 + (valid ? n : N - 1);
-    // B operand of S^T: q[n][32 ks + 8 g + e] * scale, split hi + lo.
-    f16x8 qh[HD / 32], ql[HD / 32];
-    {
-        const float *qrow = q + ((int64_t)(valid ? n : N - 1) * H + h) * HD;
-#pragma unroll
-        for (int ks = 0; ks < HD / 32; ks++) {
-            const f32x4 a = *(const f32x4 *)(qrow + 32 * ks + 8 * g);
-            const f32x4 b = *(const f32x4 *)(qrow + 32 * ks + 8 * g + 4);
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const float v = (e < 4 ? a[e] : b[e - 4]) * scale;
-                qh[ks][e] = (f16)v;
-                ql[ks][e] = (f16)(v - (float)qh[ks][e]);
-            }
-        }
-    }
-    f32x4 acc[HD / 16];                                   // O^T rows 16 dt + 4 g + v
-#pragma unroll
-    for (int dt = 0; dt < HD / 16; dt++) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float m = -INFINITY, l = 0.f;                         // this lane's keys only
-    const int last = pos0 + min(q0 + AQ, N) - 1;          // last key any query here needs
-    // Staging: thread t loads 16 dims (d0 .. d0+15) of key t / 8 of the block.
-    // The loads run ahead of the arithmetic: block k0 + AK's K and V rows are
-    // requested before block k0's MFMAs, and the page-table entry they need
-    // one block earlier still, so no block waits for a memory round trip
-    // (blocks past `last` clamp to it: loaded, never used).
-    const int sk = t >> 3, d0 = (t & 7) * 16;
-    auto page_of = [&](int k0) { return page_table[min(k0 + sk, last) / block]; };
-    u32x4 kv[4];                                          // K lo, K hi, V lo, V hi
-    auto fetch = [&](int k0, int page) {
-        const int p = min(k0 + sk, last);
-        const int64_t base = ((int64_t)page * block + p % block) * kvDim + kvh * HD + d0;
-        kv[0] = *(const u32x4 *)(kc + base);
-        kv[1] = *(const u32x4 *)(kc + base + 8);
-        kv[2] = *(const u32x4 *)(vc + base);
-        kv[3] = *(const u32x4 *)(vc + base + 8);
-    };
-    fetch(0, page_of(0));
-    int page_next = page_of(AK);
-    for (int k0 = 0; k0 <= last; k0 += AK) {
-        __syncthreads();
-        {
-            *(u32x4 *)&Ks[sk][d0] = kv[0];
-            *(u32x4 *)&Ks[sk][d0 + 8] = kv[1];
-            const f16x8 va = __builtin_bit_cast(f16x8, kv[2]), vb = __builtin_bit_cast(f16x8, kv[3]);
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                Vt[d0 + e][sk] = va[e];
-                Vt[d0 + 8 + e][sk] = vb[e];
-            }
-        }
-        __syncthreads();
-        fetch(k0 + AK, page_next);
-        page_next = page_of(k0 + 2 * AK);
-        // Keep the loads here: the compiler would sink them below the MFMAs,
-        // next to the LDS writes that wait for them.
-        __builtin_amdgcn_sched_barrier(0);
-        // S^T tiles kt = 0, 1: keys 16 kt + 4 g + v for query lq.
-        f32x4 sc[2];
-#pragma unroll
-        for (int kt = 0; kt < 2; kt++) {
-            sc[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int ks = 0; ks < HD / 32; ks++) {
-                const f16x8 ka = *(const f16x8 *)&Ks[16 * kt + lq][32 * ks + 8 * g];
-                sc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qh[ks], sc[kt], 0, 0, 0);
-                sc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, ql[ks], sc[kt], 0, 0, 0);
-            }
-        }
-        // Causal mask (and the clamped duplicates past `last`), then the
-        // online softmax of query lq over its lane group's keys.
-        float bmax = -INFINITY;
-#pragma unroll
-        for (int kt = 0; kt < 2; kt++)
-#pragma unroll
-            for (int v = 0; v < 4; v++) {
-                const int kp = k0 + 16 * kt + 4 * g + v;
-                if (kp > my_pos) sc[kt][v] = -INFINITY;
-                bmax = fmaxf(bmax, sc[kt][v]);
-            }
-        bmax = fmaxf(bmax, __shfl_xor(bmax, 16, 64));
-        bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
-        const float mn = fmaxf(m, bmax);                  // finite: key k0 <= my_pos
-        // The softmax exponents are <= 0 (or -inf for masked keys: 0), where
-        // the hardware exp2 behind __expf is accurate to a few ulp.
-        const float alpha = __expf(m - mn);
-        m = mn;
-        l *= alpha;
-#pragma unroll
-        for (int dt = 0; dt < HD / 16; dt++) acc[dt] *= alpha;
-        f16x8 ph, pl;
-#pragma unroll
-        for (int kt = 0; kt < 2; kt++)
-#pragma unroll
-            for (int v = 0; v < 4; v++) {
-                const float pv = __expf(sc[kt][v] - mn);
-                l += pv;
-                const f16 hi = (f16)pv;
-                ph[4 * kt + v] = hi;
-                pl[4 * kt + v] = (f16)(pv - (float)hi);
-            }
-        // O^T += V^T P^T: A lane row d = 16 dt + lq, the same 8 keys.
-#pragma unroll
-        for (int dt = 0; dt < HD / 16; dt++) {
-            const f16 *vr = &Vt[16 * dt + lq][0];
-            const f16x4 v0 = *(const f16x4 *)(vr + 4 * g), v1 = *(const f16x4 *)(vr + 16 + 4 * g);
-            const f16x8 va = f16x8{v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-            acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, ph, acc[dt], 0, 0, 0);
-            acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl, acc[dt], 0, 0, 0);
-        }
-    }
-    // Total weight of query lq: the four lane groups' partial sums.
-    l += __shfl_xor(l, 16, 64);
-    l += __shfl_xor(l, 32, 64);
-    if (valid) {
-        const float inv = 1.0f / l;
-        const float *grow = gate + ((int64_t)n * H + h) * HD;
-        uint16_t *orow = out + ((int64_t)n * H + h) * HD;
-#pragma unroll
-        for (int dt = 0; dt < HD / 16; dt++) {
-            const int d = 16 * dt + 4 * g;
-            const f32x4 gv = *(const f32x4 *)(grow + d);
-            uint16_t o[4];
-#pragma unroll
-            for (int v = 0; v < 4; v++) o[v] = gd_f2h(acc[dt][v] * inv * gd_sigmoid(gv[v]));
-            *(uint64_t *)(orow + d) = (uint64_t)o[0] | ((uint64_t)o[1] << 16) |
-                                      ((uint64_t)o[2] << 32) | ((uint64_t)o[3] << 48);
-        }
-    }
-}
-
-// Decode attention for one query token, split over keys (flash decoding),
-// with the per-token preparation of k_attn_prep folded in: block (head h,
-// split sp) of 256 threads normalizes and rotates its own q (threads 0..127;
-// the same arithmetic as k_attn_prep), and the split that holds key pos (the
-// new token) forms the new k and v itself (threads 128..255), rounded to f16
-// as the cache stores them, and uses them for key pos instead of reading the
-// cache.  The first q head of each kv group appends them to the cache for
-// later steps; no block of this launch reads the cache at pos.  Each of the
-// 4 waves takes whole keys with a lane holding 2 of the 128 dims and keeps an
-// online-softmax partial; the block merges its waves and writes (max, sum,
-// acc[128]) for the split; k_attn_combine merges the splits
-// (Attention.swift:108-134).
-constexpr int DSPLIT = 16;      // key splits per head
-__global__ __launch_bounds__(256) void k_attn_decode(
-        const float *proj, const float *q_norm, const float *k_norm, uint16_t *kc, uint16_t *vc,
-        const int32_t *page_table, const int32_t *pos_ptr, float *part, int H, int HKV, int block,
-        float scale, int n_rot, float base, float eps) {
-    __shared__ float wm[4], wl[4];
-    __shared__ float wacc[4][HD];
-    __shared__ float nrm[2][HD], rot[2][HD], vnew[HD], red[4];
-    const int h = blockIdx.x, sp = blockIdx.y, t = threadIdx.x;
-    const int lane = t & 63, w = t >> 6;
-    const int kvh = h / (H / HKV), kvDim = HKV * HD;
-    const int pos = *pos_ptr, T = pos + 1;
-    const bool has_pos = sp == (pos >> 2) % DSPLIT;      // wave pos & 3 of this split takes key pos
-    // The first cached key of this wave is requested before the q/k work
-    // below, which does not depend on it.
-    constexpr int STEP = DSPLIT * 4;
-    auto kv_base = [&](int j) { return kv_slot(page_table, j, block) * kvDim + kvh * HD + 2 * lane; };
-    int j = sp * 4 + w;
-    uint32_t kn = 0, vn = 0;
-    if (j < pos) {
-        const int64_t b0 = kv_base(j);
-        kn = *(const uint32_t *)(kc + b0);
-        vn = *(const uint32_t *)(vc + b0);
-    }
-    // q of head h (hf = 0) and k of kv head kvh (hf = 1): RMS norm over the
-    // head, then the partial NEOX rope, as k_attn_prep.
-    {
-        const int hf = t >> 7, i = t & (HD - 1);
-        const float x = hf == 0 ? proj[h * 2 * HD + i] : proj[2 * H * HD + kvh * HD + i];
-        const float nw = hf == 0 ? q_norm[i] : k_norm[i];
-        const float vx = proj[2 * H * HD + HKV * HD + kvh * HD + i];
-        const float sq = gd_wave_sum(x * x);
-        if (lane == 0) red[w] = sq;
-        __syncthreads();
-        const float ss = red[2 * hf] + red[2 * hf + 1];
-        const float sc = 1.0f / sqrtf(ss / (float)HD + eps);
-        float y = x * sc * nw;
-        nrm[hf][i] = y;
-        __syncthreads();
-        const int half = n_rot / 2;
-        if (i < n_rot) {
-            const int jj = i < half ? i : i - half;
-            const float freq = powf(base, -2.0f * (float)jj / (float)n_rot);
-            const float ang = (float)pos * freq;
-            const float c = cosf(ang), sn = sinf(ang);
-            y = i < half ? nrm[hf][i] * c - nrm[hf][i + half] * sn
-                         : nrm[hf][i - half] * sn + nrm[hf][i] * c;
-        }
-        rot[hf][i] = y;
-        if (hf == 1) vnew[i] = vx;
-        __syncthreads();
-        if (hf == 1 && has_pos && h % (H / HKV) == 0) {
-            const int64_t slot = (int64_t)page_table[pos / block] * block + pos % block;
-            kc[slot * kvDim + kvh * HD + i] = gd_f2h(y);
-            vc[slot * kvDim + kvh * HD + i] = gd_f2h(vnew[i]);
-        }
-    }
-    const float q0 = rot[0][2 * lane] * scale, q1 = rot[0][2 * lane + 1] * scale;
-    float m = -INFINITY, l = 0.f, a0 = 0.f, a1 = 0.f;
-    auto consume = [&](uint32_t kk, uint32_t vv) {
-        float s = q0 * gd_h2f((uint16_t)(kk & 0xffff)) + q1 * gd_h2f((uint16_t)(kk >> 16));
-        s = gd_wave_sum(s);
-        const float mn = fmaxf(m, s);
-        const float al = expf(m - mn), p = expf(s - mn);
-        l = l * al + p;
-        a0 = fmaf(p, gd_h2f((uint16_t)(vv & 0xffff)), a0 * al);
-        a1 = fmaf(p, gd_h2f((uint16_t)(vv >> 16)), a1 * al);
-        m = mn;
-    };
-    // Cached keys j < pos: wave w of split sp takes j = (sp * 4 + w) + 64 * i.
-    // The next key's page-table entry and K/V values are requested before
-    // this key's arithmetic, so each key waits only for loads issued a key
-    // earlier.
-    for (; j < pos; j += STEP) {
-        const uint32_t kk = kn, vv = vn;
-        if (j + STEP < pos) {
-            const int64_t bn = kv_base(j + STEP);
-            kn = *(const uint32_t *)(kc + bn);
-            vn = *(const uint32_t *)(vc + bn);
-        }
-        consume(kk, vv);
-    }
-    // Key pos, from this block's own copy (f16, as cached).
-    if (has_pos && w == (pos & 3))
-        consume((uint32_t)gd_f2h(rot[1][2 * lane]) | ((uint32_t)gd_f2h(rot[1][2 * lane + 1]) << 16),
-                (uint32_t)gd_f2h(vnew[2 * lane]) | ((uint32_t)gd_f2h(vnew[2 * lane + 1]) << 16));
-    if (lane == 0) { wm[w] = m; wl[w] = l; }
-    wacc[w][2 * lane] = a0;
-    wacc[w][2 * lane + 1] = a1;
-    __syncthreads();
-    if (t < HD) {
-        float M = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
-        float L = 0.f, A = 0.f;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float f = wm[i] == -INFINITY ? 0.f : expf(wm[i] - M);
-            L += wl[i] * f;
-            A += wacc[i][t] * f;
-        }
-        float *p = part + ((int64_t)h * DSPLIT + sp) * (HD + 2);
-        p[t] = A;
-        if (t == 0) { p[HD] = M; p[HD + 1] = L; }
-    }
-}
-
-// gate: the raw gate of head h at gate + h * gstride (sigmoid applied here).
-__global__ void k_attn_combine(const float *part, const float *gate, int gstride, uint16_t *out) {
-    const int h = blockIdx.x, t = threadIdx.x;      // HD threads
-    const float *p = part + (int64_t)h * DSPLIT * (HD + 2);
-    float M = -INFINITY;
-    for (int s = 0; s < DSPLIT; s++) M = fmaxf(M, p[s * (HD + 2) + HD]);
-    float L = 0.f, A = 0.f;
-    for (int s = 0; s < DSPLIT; s++) {
-        const float ms = p[s * (HD + 2) + HD];
-        const float f = ms == -INFINITY ? 0.f : expf(ms - M);
-        L += p[s * (HD + 2) + HD + 1] * f;
-        A += p[s * (HD + 2) + t] * f;
-    }
-    out[(int64_t)h * HD + t] = gd_f2h(A / L * gd_sigmoid(gate[(int64_t)h * gstride + t]));
-}
-
 // Greedy pick: index of the first maximum (BonsaiEngine.argmax, :187-191).
 // Pass 1: per-block (max, first index) pairs; pass 2 (one block) reduces them.
 __device__ __forceinline__ void argmax_merge(float &best, int &idx, float ob, int oi) {
@@ -921,22 +563,21 @@ int forward(gd_stack *st, int N, bool decode) {
 #undef GD_ONORM
             }
         } else {
-            const float scale = 1.0f / sqrtf((float)HD);
+            const int hd = c.head_dim;
+            const float scale = 1.0f / sqrtf((float)hd);
             if (decode) {
                 // One token: q/k preparation and the cache append happen
                 // inside the attention launch.
-                K_(k_attn_decode, dim3(H, DSPLIT), dim3(256), 0, s, st->proj, ly.q_norm, ly.k_norm,
-                   ly.kc, ly.vc, st->page_table, st->dpos, st->attn_part, H, HKV, c.kv_block, scale,
-                   c.n_rot, c.rope_base, eps);
-                K_(k_attn_combine, dim3(H), dim3(HD), 0, s, st->attn_part, st->proj + HD, 2 * HD,
-                   st->a16);
+                R_(gd_attn_decode_launch(ctx, hd, st->proj, ly.q_norm, ly.k_norm, ly.kc, ly.vc,
+                                         st->page_table, st->dpos, st->attn_part, st->a16, H, HKV,
+                                         c.kv_block, scale, c.n_rot, c.rope_base, eps));
             } else {
-                K_(k_attn_prep, dim3(gd_blocks((int64_t)N * (H + HKV), 4)), dim3(256), 0, s, st->proj,
-                   (int64_t)RP, ly.q_norm, ly.k_norm, st->q32, st->gate32, ly.kc, ly.vc,
-                   st->page_table, st->dpos, N, H, HKV, c.n_rot, c.rope_base, c.kv_block, eps);
-                K_(k_attn_prefill, dim3(H, gd_blocks(N, AQ)), dim3(256), 0, s, st->q32,
-                   st->gate32, ly.kc, ly.vc, st->page_table, st->dpos, st->a16, H, HKV, N,
-                   c.kv_block, scale);
+                R_(gd_attn_prep_launch(ctx, hd, st->proj, (int64_t)RP, ly.q_norm, ly.k_norm, st->q32,
+                                       st->gate32, ly.kc, ly.vc, st->page_table, st->dpos, N, H,
+                                       HKV, c.n_rot, c.rope_base, c.kv_block, eps));
+                R_(gd_attn_prefill_launch(ctx, hd, st->q32, st->gate32, ly.kc, ly.vc,
+                                          st->page_table, st->dpos, 0, st->a16, GD_F16, H, HKV, N,
+                                          c.kv_block, scale, 1));
             }
         }
         // Output projections feed only the residual add: a split-K plan
@@ -1021,14 +662,15 @@ extern "C" int gd_stack_create(gd_ctx *ctx, const gd_stack_config *cfg, uint64_t
     GD_REQUIRE(ctx, cfg && out, "gd_stack_create: null argument");
     const gd_stack_config &c = *cfg;
     GD_REQUIRE(ctx, c.n_layer > 0 && c.attn_interval > 0, "gd_stack_create: bad layer count");
-    GD_REQUIRE(ctx, c.head_dim == HD && c.d_state == HD,
-               "gd_stack_create: head_dim and d_state must be 128");
+    GD_REQUIRE(ctx, (c.head_dim == 128 || c.head_dim == 256) && c.d_state == HD,
+               "gd_stack_create: head_dim must be 128 or 256 and d_state 128");
     GD_REQUIRE(ctx, c.d_conv == 4, "gd_stack_create: d_conv must be 4");
     GD_REQUIRE(ctx, c.n_head > 0 && c.n_head_kv > 0 && c.n_head % c.n_head_kv == 0,
                "gd_stack_create: n_head must be a multiple of n_head_kv");
     GD_REQUIRE(ctx, c.n_k_head > 0 && c.n_v_head % c.n_k_head == 0,
                "gd_stack_create: n_v_head must be a multiple of n_k_head");
-    GD_REQUIRE(ctx, c.n_rot > 0 && c.n_rot <= HD && c.n_rot % 2 == 0, "gd_stack_create: n_rot");
+    GD_REQUIRE(ctx, c.n_rot > 0 && c.n_rot <= c.head_dim && c.n_rot % 2 == 0,
+               "gd_stack_create: n_rot");
     GD_REQUIRE(ctx, c.n_embd % 128 == 0 && c.n_ff % 128 == 0 && c.n_vocab > 0,
                "gd_stack_create: n_embd and n_ff must be multiples of 128");
     GD_REQUIRE(ctx, c.n_embd <= 15744,
@@ -1044,7 +686,8 @@ extern "C" int gd_stack_create(gd_ctx *ctx, const gd_stack_config *cfg, uint64_t
     st->valDim = HD * c.n_v_head;
     st->convDim = 2 * st->keyDim + st->valDim;
     st->rp_rec = st->convDim + st->valDim + 2 * c.n_v_head;
-    st->rp_att = 2 * c.n_head * HD + 2 * c.n_head_kv * HD;
+    const int hd = c.head_dim;
+    st->rp_att = 2 * c.n_head * hd + 2 * c.n_head_kv * hd;
     st->max_pages = (c.max_ctx + c.kv_block - 1) / c.kv_block;
     const int E = c.n_embd, FF = c.n_ff, B = c.max_batch;
     int rc = GD_OK;
@@ -1068,10 +711,10 @@ extern "C" int gd_stack_create(gd_ctx *ctx, const gd_stack_config *cfg, uint64_t
             C_(salloc_t(st, (size_t)c.n_v_head * HD * HD, &ly.rec_state));
         } else {
             C_(q2w_make(st, E, st->rp_att, next_seed(), &ly.in_proj));
-            C_(q2w_make(st, (int64_t)c.n_head * HD, E, next_seed(), &ly.out_proj));
-            C_(f32_make(st, HD, next_seed(), 0.8f, 1.2f, &ly.q_norm));
-            C_(f32_make(st, HD, next_seed(), 0.8f, 1.2f, &ly.k_norm));
-            const size_t kv = (size_t)st->max_pages * c.kv_block * c.n_head_kv * HD;
+            C_(q2w_make(st, (int64_t)c.n_head * hd, E, next_seed(), &ly.out_proj));
+            C_(f32_make(st, hd, next_seed(), 0.8f, 1.2f, &ly.q_norm));
+            C_(f32_make(st, hd, next_seed(), 0.8f, 1.2f, &ly.k_norm));
+            const size_t kv = (size_t)st->max_pages * c.kv_block * c.n_head_kv * hd;
             C_(salloc_t(st, kv, &ly.kc));
             C_(salloc_t(st, kv, &ly.vc));
         }
@@ -1093,14 +736,14 @@ extern "C" int gd_stack_create(gd_ctx *ctx, const gd_stack_config *cfg, uint64_t
     C_(salloc_t(st, (size_t)8 * B * E, &st->contrib));
     C_(salloc_t(st, (size_t)B * c.n_v_head, &st->beta));
     C_(salloc_t(st, (size_t)B * c.n_v_head, &st->g));
-    C_(salloc_t(st, (size_t)B * c.n_head * HD, &st->q32));
-    C_(salloc_t(st, (size_t)B * c.n_head * HD, &st->gate32));
+    C_(salloc_t(st, (size_t)B * c.n_head * hd, &st->q32));
+    C_(salloc_t(st, (size_t)B * c.n_head * hd, &st->gate32));
     C_(salloc_t(st, (size_t)c.n_vocab, &st->logits));
-    C_(salloc_t(st, (size_t)c.n_head * DSPLIT * (HD + 2), &st->attn_part));
+    C_(salloc_t(st, gd_attn_part_floats(hd, c.n_head), &st->attn_part));
     C_(salloc_t(st, (size_t)AMAX_BLOCKS, &st->amax_v));
     C_(salloc_t(st, (size_t)AMAX_BLOCKS, &st->amax_i));
     C_(salloc_t(st, (size_t)B * E, &st->xn16));
-    const int a16n = std::max(std::max(st->valDim, c.n_head * HD), FF);
+    const int a16n = std::max(std::max(st->valDim, c.n_head * hd), FF);
     C_(salloc_t(st, (size_t)B * a16n, &st->a16));
     C_(salloc_t(st, (size_t)B, &st->ids));
     C_(salloc_t(st, 1, &st->dpos));
@@ -1275,13 +918,13 @@ extern "C" int gd_stack_tensor(gd_stack *st, int layer, const char *name, gd_q2w
         if (n == "ssm_conv_state") return f(ly.conv_state, (int64_t)3 * cd);
         if (n == "ssm_state") return f(ly.rec_state, (int64_t)nv * HD * HD);
     } else {
-        const int qf = 2 * c.n_head * HD, kv = c.n_head_kv * HD;
+        const int hd = c.head_dim, qf = 2 * c.n_head * hd, kv = c.n_head_kv * hd;
         if (n == "attn_q") return q(ly.in_proj, 0, qf);
         if (n == "attn_k") return q(ly.in_proj, qf, qf + kv);
         if (n == "attn_v") return q(ly.in_proj, qf + kv, qf + 2 * kv);
         if (n == "attn_output") return q(ly.out_proj);
-        if (n == "attn_q_norm") return f(ly.q_norm, HD);
-        if (n == "attn_k_norm") return f(ly.k_norm, HD);
+        if (n == "attn_q_norm") return f(ly.q_norm, hd);
+        if (n == "attn_k_norm") return f(ly.k_norm, hd);
     }
     return gd_fail(ctx, GD_EINVAL, "gd_stack_tensor: layer %d has no tensor '%s'", layer, name);
 }

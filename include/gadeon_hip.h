@@ -265,6 +265,57 @@ int gd_silu_mul(gd_ctx *ctx, float *a, const float *b, int64_t n);
 int gd_mul_silu(gd_ctx *ctx, float *a, const float *b, int64_t n);
 int gd_add(gd_ctx *ctx, float *x, const float *y, int64_t n);
 
+/* ---- gated GQA attention over an f16 paged KV cache ---------------------------
+ * Head dims 128 and 256.  The cache of one attention layer is a pool of
+ * pages of `page_size` positions, each position kv_dim = head_dim * n_head_kv
+ * f16 values (k_cache and v_cache); position p lives in page page_table[p /
+ * page_size] at slot p % page_size.  The reference's table holds page
+ * addresses (MetalKVPool.swift: bindless kAddr / vAddr); this one holds page
+ * indices into one allocation.  q, k, v rows are f32 [tokens][heads][head_dim]
+ * as in MetalEnc. */
+
+/* q_full [N][n_head][2 head_dim] (per head q | gate, the hybrid's fused
+ * projection) -> q and gate [N][n_head][head_dim].  MetalEnc.splitQGate(Batch)
+ * (MetalEnc.swift:656-665, 780-791), Attention.swift:84-93. */
+int gd_split_q_gate(gd_ctx *ctx, const float *q_full, float *q, float *gate,
+                    int head_dim, int n_head, int64_t N);
+
+/* Partial NEOX rope in place on x [N][n_head][head_dim]: dims i < n_rot/2 and
+ * i + n_rot/2 of each head turn by (base_pos + n) * base^(-2i/n_rot).
+ * MetalEnc.rope / ropeBatch (MetalEnc.swift:560-569, 817-828), Kern.ropeNeox
+ * (Kernels.swift:66-84). */
+int gd_rope(gd_ctx *ctx, float *x, int head_dim, int n_head, int n_rot, float base,
+            int base_pos, int64_t N);
+
+/* k, v [N][kv_dim] f32 -> the cache at positions base_pos .. base_pos+N-1,
+ * rounded to f16.  MetalEnc.kvAppend / kvAppendBatch (MetalEnc.swift:667-677,
+ * 830-847), kv_append / kv_append_batch (Kernels.metal:1446-1466, 1726-1766). */
+int gd_kv_append(gd_ctx *ctx, const float *k, const float *v, uint16_t *k_cache,
+                 uint16_t *v_cache, const int32_t *page_table, int kv_dim, int base_pos,
+                 int page_size, int64_t N);
+
+/* One query per head over cached positions lo .. T-1 (the token's own k, v
+ * appended first): out[h] = softmax((q_h . k_t) * scale) . v_t, times
+ * sigmoid(gate[h]) when gated (1; 0: plain).  q, gate, out [n_head][head_dim]
+ * f32.  part: scratch of n_head * 16 * (head_dim + 2) floats (the key-split
+ * partials).  MetalEnc.attnPaged (MetalEnc.swift:679-706), attn_head
+ * (Kernels.metal:1423-1445). */
+int gd_attn_paged(gd_ctx *ctx, const float *q, const uint16_t *k_cache,
+                  const uint16_t *v_cache, const int32_t *page_table, const float *gate,
+                  float *out, float *part, int head_dim, int n_head, int n_head_kv, int T,
+                  int kv_dim, int page_size, float scale, int gated, int lo);
+
+/* N causal queries at positions base_pos + n over the cached positions
+ * 0 .. base_pos + n (their own keys appended first): qN, gateN, outN
+ * [N][n_head][head_dim] f32, 16-byte aligned.  window must be 0 (the whole
+ * history; the reference's sliding window serves another model family).
+ * MetalEnc.attnBatch (MetalEnc.swift:966-1025), attn_batch / attn_batch_mm
+ * (Kernels.metal:1767-2022). */
+int gd_attn_batch(gd_ctx *ctx, const float *q, const uint16_t *k_cache,
+                  const uint16_t *v_cache, const int32_t *page_table, const float *gate,
+                  float *out, int head_dim, int n_head, int n_head_kv, int kv_dim,
+                  int page_size, float scale, int base_pos, int64_t N, int gated, int window);
+
 /* ---- GDN recurrence -----------------------------------------------------------
  * State S[nV][dS][dS] f32, key-major: S[h][i*dS + j], i = key, j = value
  * (GDN.swift:9-16, Kernels.metal:1225).  Head map hk = hv % nK
@@ -365,7 +416,7 @@ typedef struct gd_stack_config {
     int n_ff;           /* 17408 */
     int n_head;         /* 40 (attention q heads) */
     int n_head_kv;      /* 8 */
-    int head_dim;       /* 128 */
+    int head_dim;       /* 128 (attention head dim: 128 or 256) */
     int n_rot;          /* 64 (partial NEOX rope) */
     float rope_base;    /* 1e7 */
     float eps;          /* 1e-6 */

@@ -206,6 +206,21 @@ def test_stack_past_position_64(ctx, nk):
         ctx.lib.gd_stack_destroy(st)
 
 
+def test_stack_head_dim_256(ctx):
+    """The reference 27B's attention and GDN shape pattern (Model.swift:11-32:
+    head_dim 256, 6 q heads per kv head; more value heads than key heads),
+    scaled down: 6 q / 1 kv heads of 256, GDN 4 value / 2 key heads; a
+    70-token prompt over two chunks, decode and generate."""
+    cfg, st = make_stack(ctx, head_dim=256, n_head=6, n_head_kv=1, n_k_head=2, n_v_head=4,
+                         max_batch=48)
+    try:
+        ids = ((np.arange(70) * 29 + 3) % cfg["n_vocab"]).astype(np.int32)
+        print("\nstack head_dim 256, 6/1 heads", flush=True)
+        run_parity(ctx, cfg, st, ids, n_decode=6, n_gen=6, chain=False)
+    finally:
+        ctx.lib.gd_stack_destroy(st)
+
+
 def test_stack_config4_geometry(ctx):
     """BASELINE config 4 at its own per-layer geometry (4 of its 64 layers):
     a 512-id random prompt in one prefill chunk, 8 decode steps, 8 generate
