@@ -108,6 +108,21 @@ _PROTOS = {
                          C.POINTER(_i64)]),
     "gd_stack_position": (_i, [_vp, C.POINTER(_i64)]),
     "gd_stack_generate": (_i, [_vp, _i, _vp]),
+    "gd_q2_0_repack_rows": (_i, [_vp, _vp, _u64, _i64, _i64, _Q2WP]),
+    "gd_gguf_open": (_i, [C.c_char_p, C.POINTER(_vp)]),
+    "gd_gguf_close": (None, [_vp]),
+    "gd_gguf_info": (_i, [_vp, C.POINTER(_i64), C.POINTER(_i64), C.POINTER(_i)]),
+    "gd_gguf_tensor": (_i, [_vp, C.c_char_p, C.POINTER(_i), C.POINTER(_i64), C.POINTER(_i),
+                        C.POINTER(_vp), C.POINTER(_sz)]),
+    "gd_gguf_get_int": (_i, [_vp, C.c_char_p, C.POINTER(_i64)]),
+    "gd_gguf_get_float": (_i, [_vp, C.c_char_p, C.POINTER(C.c_double)]),
+    "gd_gguf_get_bool": (_i, [_vp, C.c_char_p, C.POINTER(_i)]),
+    "gd_gguf_get_string": (_i, [_vp, C.c_char_p, C.POINTER(C.c_char_p)]),
+    "gd_gguf_get_floats": (_i, [_vp, C.c_char_p, C.POINTER(C.POINTER(C.c_double)),
+                            C.POINTER(_i64)]),
+    "gd_gguf_get_ints": (_i, [_vp, C.c_char_p, C.POINTER(C.POINTER(_i64)), C.POINTER(_i64)]),
+    "gd_gguf_stack_config": (_i, [_vp, C.POINTER(StackConfig)]),
+    "gd_stack_create_from_gguf": (_i, [_vp, _vp, _i, _i, _i, C.POINTER(_vp)]),
 }
 
 _lib = None
@@ -209,6 +224,85 @@ class Context:
                 self.lib.gd_free(self.h, p)
             self._bufs.clear()
             self.lib.gd_ctx_destroy(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+
+class GGUF:
+    """A GGUF file opened by the library's host reader (gd_gguf_*, no device
+    needed).  Tensors come back as read-only numpy views of the mapping."""
+
+    def __init__(self, path: os.PathLike | str):
+        self.lib = load()
+        h = _vp()
+        rc = self.lib.gd_gguf_open(os.fsencode(path), C.byref(h))
+        if rc != GD_OK:
+            raise GDError(rc, self.lib.gd_last_error(None).decode())
+        self.h = h
+
+    def _check(self, rc: int) -> None:
+        if rc != GD_OK:
+            raise GDError(rc, self.lib.gd_last_error(None).decode())
+
+    def info(self) -> tuple[int, int, int]:
+        nt, nkv, ver = _i64(), _i64(), _i()
+        self._check(self.lib.gd_gguf_info(self.h, C.byref(nt), C.byref(nkv), C.byref(ver)))
+        return nt.value, nkv.value, ver.value
+
+    def tensor(self, name: str) -> tuple[tuple[int, ...], int, np.ndarray]:
+        """(dims with ne0 first, ggml type, raw bytes as a uint8 array)."""
+        nd, ty, data, nb = _i(), _i(), _vp(), _sz()
+        dims = (_i64 * 4)()
+        self._check(self.lib.gd_gguf_tensor(self.h, name.encode(), C.byref(nd), dims,
+                                            C.byref(ty), C.byref(data), C.byref(nb)))
+        buf = (C.c_uint8 * nb.value).from_address(data.value)
+        arr = np.frombuffer(buf, np.uint8)
+        arr.flags.writeable = False
+        return tuple(dims[:nd.value]), ty.value, arr
+
+    def int(self, key: str) -> int:
+        v = _i64()
+        self._check(self.lib.gd_gguf_get_int(self.h, key.encode(), C.byref(v)))
+        return v.value
+
+    def float(self, key: str) -> float:
+        v = C.c_double()
+        self._check(self.lib.gd_gguf_get_float(self.h, key.encode(), C.byref(v)))
+        return v.value
+
+    def bool(self, key: str) -> bool:
+        v = _i()
+        self._check(self.lib.gd_gguf_get_bool(self.h, key.encode(), C.byref(v)))
+        return bool(v.value)
+
+    def floats(self, key: str) -> list[float]:
+        v, n = C.POINTER(C.c_double)(), _i64()
+        self._check(self.lib.gd_gguf_get_floats(self.h, key.encode(), C.byref(v), C.byref(n)))
+        return [v[i] for i in range(n.value)]
+
+    def string(self, key: str) -> str:
+        v = C.c_char_p()
+        self._check(self.lib.gd_gguf_get_string(self.h, key.encode(), C.byref(v)))
+        return v.value.decode()
+
+    def ints(self, key: str) -> list[int]:
+        v, n = C.POINTER(_i64)(), _i64()
+        self._check(self.lib.gd_gguf_get_ints(self.h, key.encode(), C.byref(v), C.byref(n)))
+        return [v[i] for i in range(n.value)]
+
+    def stack_config(self) -> StackConfig:
+        c = StackConfig()
+        self._check(self.lib.gd_gguf_stack_config(self.h, C.byref(c)))
+        return c
+
+    def close(self) -> None:
+        if getattr(self, "h", None):
+            self.lib.gd_gguf_close(self.h)
             self.h = None
 
     def __enter__(self):

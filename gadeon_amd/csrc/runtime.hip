@@ -341,14 +341,14 @@ extern "C" int gd_q2w_free(gd_ctx *ctx, gd_q2w *w) {
     return rc ? rc : rc2;
 }
 
-// One thread per 34-byte GGUF block (row-major order).  The GGUF side is only
+// One thread per 34-byte GGUF block (row-major order) of rows [row0, ...).  The GGUF side is only
 // 2-byte aligned, so it is read as 17 halfwords; the code bytes go to their
 // two 16-byte slots of the row group's tile, the scale to its slot.
 __global__ void gd_repack_kernel(const uint16_t *src, uint8_t *codes, uint16_t *scales,
-                                 int64_t nblk, int64_t nblocks) {
+                                 int64_t nblk, int64_t row0, int64_t nblocks) {
     const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (b >= nblocks) return;
-    const int64_t row = b / nblk, blk = b % nblk;
+    const int64_t row = row0 + b / nblk, blk = b % nblk;
     const int64_t steps = (nblk + 3) / 4, bgroups = (nblk + 15) / 16;
     const uint16_t *p = src + b * (GD_Q2_0_BLOCK_BYTES / 2);
     scales[gd_q2_scale_idx(row, blk, bgroups)] = p[0];
@@ -393,17 +393,29 @@ static int check_q2w(gd_ctx *ctx, const gd_q2w *w, const char *who) {
 }
 int gd_check_q2w(gd_ctx *ctx, const gd_q2w *w, const char *who) { return check_q2w(ctx, w, who); }
 
+extern "C" int gd_q2_0_repack_rows(gd_ctx *ctx, const void *gguf, uint64_t woff, int64_t row0,
+                                   int64_t nrows, gd_q2w *w) {
+    GD_CHECK_CTX(ctx);
+    int rc = check_q2w(ctx, w, "gd_q2_0_repack_rows");
+    if (rc) return rc;
+    GD_REQUIRE(ctx, gguf && woff % 2 == 0, "gd_q2_0_repack_rows: null source or odd offset");
+    GD_REQUIRE(ctx, row0 >= 0 && nrows >= 0 && row0 + nrows <= w->R,
+               "gd_q2_0_repack_rows: rows [%lld, %lld) outside [0, %lld)", (long long)row0,
+               (long long)(row0 + nrows), (long long)w->R);
+    const int64_t nblk = w->K / GD_Q2_0_QK, nb = nrows * nblk;
+    if (!nb) return GD_OK;
+    hipLaunchKernelGGL(gd_repack_kernel, dim3(gd_blocks(nb, 256)), dim3(256), 0, ctx->stream,
+                       (const uint16_t *)((const uint8_t *)gguf + woff), (uint8_t *)w->codes,
+                       (uint16_t *)w->scales, nblk, row0, nb);
+    GD_LAUNCHED(ctx, "gd_repack_kernel");
+    return GD_OK;
+}
+
 extern "C" int gd_q2_0_repack(gd_ctx *ctx, const void *gguf, uint64_t woff, gd_q2w *w) {
     GD_CHECK_CTX(ctx);
     int rc = check_q2w(ctx, w, "gd_q2_0_repack");
     if (rc) return rc;
-    GD_REQUIRE(ctx, gguf && woff % 2 == 0, "gd_q2_0_repack: null source or odd offset");
-    const int64_t nblk = w->K / GD_Q2_0_QK, nb = w->R * nblk;
-    hipLaunchKernelGGL(gd_repack_kernel, dim3(gd_blocks(nb, 256)), dim3(256), 0, ctx->stream,
-                       (const uint16_t *)((const uint8_t *)gguf + woff), (uint8_t *)w->codes,
-                       (uint16_t *)w->scales, nblk, nb);
-    GD_LAUNCHED(ctx, "gd_repack_kernel");
-    return GD_OK;
+    return gd_q2_0_repack_rows(ctx, gguf, woff, 0, w->R, w);
 }
 
 extern "C" int gd_q2_0_export_rows(gd_ctx *ctx, const gd_q2w *w, int64_t row0, int64_t nrows,

@@ -424,6 +424,7 @@ struct gd_stack {
     int keyDim = 0, valDim = 0, convDim = 0, rp_rec = 0, rp_att = 0, max_pages = 0;
     std::vector<StackLayer> L;
     gd_q2w embd{};
+    gd_q2w head{};               // lm_head: a copy of embd when tied (Model.swift:145)
     float *out_norm = nullptr;
     int32_t *page_table = nullptr;
     // scratch
@@ -435,6 +436,7 @@ struct gd_stack {
     uint16_t *xn16 = nullptr, *a16 = nullptr;
     int32_t *ids = nullptr, *dpos = nullptr, *dtok = nullptr;
     int64_t pos = 0;
+    bool random = true;          // weights drawn from the seed (else loaded)
     std::atomic<bool> stop{false};
     std::vector<void *> allocs;
     hipGraphExec_t decode_exec = nullptr;
@@ -457,18 +459,20 @@ int salloc_t(gd_stack *st, size_t count, T **p) {
     return rc;
 }
 
+// Weight allocation; with st->random set the weights are also filled from the
+// seeded device streams, otherwise a loader fills them afterwards.
 int q2w_make(gd_stack *st, int64_t K, int64_t R, uint64_t seed, gd_q2w *w) {
     int rc = gd_q2w_alloc(st->ctx, K, R, w);
     if (rc) return rc;
     st->allocs.push_back(w->codes);
     st->allocs.push_back(w->scales);
-    return gd_rand_q2w(st->ctx, w, seed, 0.01f, 0.05f);
+    return st->random ? gd_rand_q2w(st->ctx, w, seed, 0.01f, 0.05f) : GD_OK;
 }
 
 int f32_make(gd_stack *st, int64_t n, uint64_t seed, float lo, float hi, float **p) {
     int rc = salloc_t(st, (size_t)n, p);
     if (rc) return rc;
-    return gd_rand_uniform(st->ctx, *p, (size_t)n, seed, lo, hi);
+    return st->random ? gd_rand_uniform(st->ctx, *p, (size_t)n, seed, lo, hi) : GD_OK;
 }
 
 // One chunk of N tokens whose embeddings are already in st->x (f32 [N][E]):
@@ -623,12 +627,12 @@ int forward(gd_stack *st, int N, bool decode) {
                st->out_norm, st->xn16, E, eps, nsplit, (int64_t)N * E);
         }
     }
-    // Tied lm_head on the last token, greedy pick, position bump.
+    // lm_head on the last token, greedy pick, position bump.
     if (decode)
-        R_(gd_gemv_mfma_norm(ctx, &st->embd, hcur, st->contrib, nd, E, st->out_norm, eps,
+        R_(gd_gemv_mfma_norm(ctx, &st->head, hcur, st->contrib, nd, E, st->out_norm, eps,
                              nullptr, st->logits));
     else
-        R_(gd_q2_0_gemv(ctx, &st->embd, st->xn16, GD_F16, st->logits));
+        R_(gd_q2_0_gemv(ctx, &st->head, st->xn16, GD_F16, st->logits));
     K_(k_argmax_part, dim3(AMAX_BLOCKS), dim3(256), 0, s, st->logits, c.n_vocab, st->amax_v,
        st->amax_i);
     K_(k_argmax_final, dim3(1), dim3(AMAX_BLOCKS), 0, s, st->amax_v, st->amax_i, st->dtok);
@@ -656,8 +660,13 @@ extern "C" void gd_stack_destroy(gd_stack *st) {
     delete st;
 }
 
-extern "C" int gd_stack_create(gd_ctx *ctx, const gd_stack_config *cfg, uint64_t seed,
-                               gd_stack **out) {
+namespace {
+
+// Allocate a stack of geometry *cfg.  random: draw every weight from `seed`
+// (gd_stack_create); otherwise leave the weights for a loader.  untied: give
+// the lm_head its own matrix instead of sharing the token embedding.
+int create(gd_ctx *ctx, const gd_stack_config *cfg, uint64_t seed, bool random, bool untied,
+           gd_stack **out) {
     GD_CHECK_CTX(ctx);
     GD_REQUIRE(ctx, cfg && out, "gd_stack_create: null argument");
     const gd_stack_config &c = *cfg;
@@ -682,6 +691,7 @@ extern "C" int gd_stack_create(gd_ctx *ctx, const gd_stack_config *cfg, uint64_t
     gd_stack *st = new gd_stack();
     st->ctx = ctx;
     st->c = c;
+    st->random = random;
     st->keyDim = HD * c.n_k_head;
     st->valDim = HD * c.n_v_head;
     st->convDim = 2 * st->keyDim + st->valDim;
@@ -723,6 +733,10 @@ extern "C" int gd_stack_create(gd_ctx *ctx, const gd_stack_config *cfg, uint64_t
     }
     C_(q2w_make(st, E, c.n_vocab, next_seed(), &st->embd));
     C_(f32_make(st, E, next_seed(), 0.8f, 1.2f, &st->out_norm));
+    if (untied)
+        C_(q2w_make(st, E, c.n_vocab, next_seed(), &st->head));
+    else
+        st->head = st->embd;
     C_(salloc_t(st, (size_t)st->max_pages, &st->page_table));
     hipLaunchKernelGGL(k_iota, dim3(gd_blocks(st->max_pages, 256)), dim3(256), 0, ctx->stream,
                        st->page_table, st->max_pages);
@@ -752,6 +766,13 @@ extern "C" int gd_stack_create(gd_ctx *ctx, const gd_stack_config *cfg, uint64_t
 #undef C_
     *out = st;
     return GD_OK;
+}
+
+}  // namespace
+
+extern "C" int gd_stack_create(gd_ctx *ctx, const gd_stack_config *cfg, uint64_t seed,
+                               gd_stack **out) {
+    return create(ctx, cfg, seed, true, false, out);
 }
 
 extern "C" int gd_stack_reset(gd_stack *st) {
@@ -894,6 +915,7 @@ extern "C" int gd_stack_tensor(gd_stack *st, int layer, const char *name, gd_q2w
     };
     if (layer < 0) {
         if (n == "token_embd") return q(st->embd);
+        if (n == "output") return q(st->head);
         if (n == "output_norm") return f(st->out_norm, c.n_embd);
         return gd_fail(ctx, GD_EINVAL, "gd_stack_tensor: no global tensor '%s'", name);
     }
@@ -927,4 +949,124 @@ extern "C" int gd_stack_tensor(gd_stack *st, int layer, const char *name, gd_q2w
         if (n == "attn_k_norm") return f(ly.k_norm, hd);
     }
     return gd_fail(ctx, GD_EINVAL, "gd_stack_tensor: layer %d has no tensor '%s'", layer, name);
+}
+
+// ------------------------------------------------------------ GGUF weights
+
+namespace {
+
+// Tensors the stack reads, by the short names of gd_stack_tensor, for one
+// layer kind (Model.swift:100-130) and for the whole model (:139-145).
+const char *const k_common[] = {"attn_norm", "post_attention_norm", "ffn_gate", "ffn_up",
+                                "ffn_down"};
+const char *const k_rec[] = {"attn_qkv", "attn_gate", "ssm_beta", "ssm_alpha", "ssm_out",
+                             "ssm_conv1d", "ssm_dt", "ssm_a", "ssm_norm"};
+const char *const k_att[] = {"attn_q", "attn_k", "attn_v", "attn_output", "attn_q_norm",
+                             "attn_k_norm"};
+
+// The file's name for short name `name` of layer il (-1: global), as the
+// reference looks it up (Model.swift:100-145): "<name>.weight", except the
+// bias ssm_dt.bias and the bare ssm_a.
+std::string gguf_name(int il, const std::string &name) {
+    std::string s = il < 0 ? name : "blk." + std::to_string(il) + "." + name;
+    if (name == "ssm_dt") return s + ".bias";
+    if (name == "ssm_a") return s;
+    return s + ".weight";
+}
+
+struct Item { int il; const char *name; };
+
+std::vector<Item> load_list(const gd_stack *st) {
+    std::vector<Item> v = {{-1, "token_embd"}, {-1, "output_norm"}};
+    if (st->head.codes != st->embd.codes) v.push_back({-1, "output"});
+    for (int il = 0; il < st->c.n_layer; il++) {
+        for (const char *n : k_common) v.push_back({il, n});
+        if (st->L[il].rec)
+            for (const char *n : k_rec) v.push_back({il, n});
+        else
+            for (const char *n : k_att) v.push_back({il, n});
+    }
+    return v;
+}
+
+// Upload one tensor of the file into its place in the stack: a Q2_0 matrix
+// through the device staging buffer into its rows of the fused matrix, an
+// f32 vector straight to its buffer.  Shapes and types must match exactly.
+int load_tensor(gd_stack *st, const gd_gguf *g, const Item &it, void *staging,
+                size_t staging_bytes) {
+    gd_ctx *ctx = st->ctx;
+    gd_q2w w{};
+    int64_t row0 = 0, count = 0;
+    float *f32 = nullptr;
+    int rc = gd_stack_tensor(st, it.il, it.name, &w, &row0, &f32, &count);
+    if (rc) return rc;
+    const std::string gn = gguf_name(it.il, it.name);
+    int ndim = 0, type = -1;
+    int64_t dims[4];
+    const void *data = nullptr;
+    size_t bytes = 0;
+    if (gd_gguf_tensor(g, gn.c_str(), &ndim, dims, &type, &data, &bytes) != GD_OK)
+        return gd_fail(ctx, GD_EINVAL, "gd_stack_create_from_gguf: missing tensor %s", gn.c_str());
+    if (f32) {
+        const int64_t n = dims[0] * dims[1] * dims[2] * dims[3];
+        GD_REQUIRE(ctx, type == 0 && n == count,
+                   "gd_stack_create_from_gguf: %s must be f32 with %lld elements (type %d, %lld)",
+                   gn.c_str(), (long long)count, type, (long long)n);
+        GD_REQUIRE(ctx, std::string(it.name) != "ssm_conv1d" || dims[0] == st->c.d_conv,
+                   "gd_stack_create_from_gguf: %s must be [d_conv, conv_dim]", gn.c_str());
+        return gd_upload(ctx, f32, data, bytes);
+    }
+    GD_REQUIRE(ctx, type == 42 && ndim == 2 && dims[0] == w.K && dims[1] == count,
+               "gd_stack_create_from_gguf: %s must be Q2_0 [%lld, %lld] (type %d, [%lld, %lld])",
+               gn.c_str(), (long long)w.K, (long long)count, type, (long long)dims[0],
+               (long long)(ndim > 1 ? dims[1] : 1));
+    GD_REQUIRE(ctx, bytes <= staging_bytes, "gd_stack_create_from_gguf: staging too small");
+    // The copy waits for the previous repack on the same stream, then the
+    // host waits for the copy, so one staging buffer serves every tensor.
+    if ((rc = gd_upload(ctx, staging, data, bytes))) return rc;
+    return gd_q2_0_repack_rows(ctx, staging, 0, row0, count, &w);
+}
+
+}  // namespace
+
+extern "C" int gd_stack_create_from_gguf(gd_ctx *ctx, const gd_gguf *g, int kv_block,
+                                         int max_ctx, int max_batch, gd_stack **out) {
+    GD_CHECK_CTX(ctx);
+    GD_REQUIRE(ctx, g && out, "gd_stack_create_from_gguf: null argument");
+    *out = nullptr;
+    gd_stack_config c{};
+    if (gd_gguf_stack_config(g, &c) != GD_OK)
+        return gd_fail(ctx, GD_EINVAL, "%s", gd_last_error(nullptr));
+    c.kv_block = kv_block;
+    c.max_ctx = max_ctx;
+    c.max_batch = max_batch;
+    // An absent output.weight means the lm_head is the token embedding
+    // (Model.swift:145).
+    const bool untied = gd_gguf_tensor(g, "output.weight", nullptr, nullptr, nullptr, nullptr,
+                                       nullptr) == GD_OK;
+    gd_stack *st = nullptr;
+    int rc = create(ctx, &c, 0, false, untied, &st);
+    if (rc) return rc;
+    const std::vector<Item> items = load_list(st);
+    size_t staging_bytes = 0;
+    for (const Item &it : items) {
+        int type = -1;
+        size_t bytes = 0;
+        if (gd_gguf_tensor(g, gguf_name(it.il, it.name).c_str(), nullptr, nullptr, &type, nullptr,
+                           &bytes) == GD_OK && type == 42)
+            staging_bytes = std::max(staging_bytes, bytes);
+    }
+    void *staging = nullptr;
+    if ((rc = gd_alloc(ctx, staging_bytes, &staging))) { gd_stack_destroy(st); return rc; }
+    for (const Item &it : items)
+        if ((rc = load_tensor(st, g, it, staging, staging_bytes))) break;
+    if (rc == GD_OK) rc = gd_sync(ctx);
+    const int rc2 = gd_free(ctx, staging);
+    if (rc == GD_OK) rc = rc2;
+    if (rc) {
+        gd_stack_destroy(st);
+        return rc;
+    }
+    *out = st;
+    return GD_OK;
 }

@@ -146,6 +146,12 @@ int gd_q2w_free(gd_ctx *ctx, gd_q2w *w);
 /* Repack R rows of GGUF Q2_0 blocks already in device memory (at byte offset
  * woff of `gguf`, the MetalEnc WeightRef.local) into the planes of w. */
 int gd_q2_0_repack(gd_ctx *ctx, const void *gguf, uint64_t woff, gd_q2w *w);
+/* Repack nrows rows of GGUF blocks (device memory, byte offset woff) into rows
+ * [row0, row0+nrows) of w: one GGUF tensor into its slice of a fused
+ * projection (MetalContext.swift:146-191 maps each tensor as its own window;
+ * here tensors that read the same input share one matrix). */
+int gd_q2_0_repack_rows(gd_ctx *ctx, const void *gguf, uint64_t woff, int64_t row0,
+                        int64_t nrows, gd_q2w *w);
 /* Host GGUF blocks -> freshly allocated device planes (upload + repack). */
 int gd_q2_0_upload(gd_ctx *ctx, const void *host_blocks, int64_t K, int64_t R,
                    gd_q2w *w);
@@ -463,11 +469,55 @@ int gd_stack_request_stop(gd_stack *st);
  * ("attn_norm", "attn_qkv", "attn_gate", "ssm_beta", "ssm_alpha", "ssm_dt",
  * "ssm_a", "ssm_conv1d", "ssm_norm", "ssm_out", "attn_q", "attn_k", "attn_v",
  * "attn_output", "attn_q_norm", "attn_k_norm", "post_attention_norm",
- * "ffn_gate", "ffn_up", "ffn_down", "token_embd", "output_norm",
+ * "ffn_gate", "ffn_up", "ffn_down", "token_embd", "output" (the lm_head,
+ * token_embd's matrix when tied), "output_norm",
  * "ssm_conv_state", "ssm_state"). */
 int gd_stack_tensor(gd_stack *st, int layer, const char *name, gd_q2w *w,
                     int64_t *row0, float **f32, int64_t *count);
 int gd_stack_position(gd_stack *st, int64_t *pos);
+
+/* ---- GGUF v3 reader (host only): GGUF.swift:45-117 ---------------------------
+ * gd_gguf_open maps the file read-only and parses the header, the metadata and
+ * the tensor directory; tensor data starts at the first multiple of
+ * general.alignment (default 32) after the directory (GGUF.swift:83-99).  All
+ * reads are bounds-checked: a truncated or corrupt file fails with GD_EINVAL.
+ * These entries need no device and no context; their failures are reported
+ * by gd_last_error(NULL).  Pointers handed out stay valid until
+ * gd_gguf_close. */
+typedef struct gd_gguf gd_gguf;
+
+int gd_gguf_open(const char *path, gd_gguf **out);          /* GGUF(path:) */
+void gd_gguf_close(gd_gguf *g);
+int gd_gguf_info(const gd_gguf *g, int64_t *n_tensors, int64_t *n_kv, int *version);
+/* GGUF.tensor(name) / maybe(name): dims (ne0 fastest; unused dims 1), ggml
+ * type (0 f32, 1 f16, 42 Q2_0, ...), a pointer to its bytes in the mapping
+ * and their count.  Any out pointer may be NULL; an absent name fails.
+ * gd_gguf_open rejects a file with a tensor type outside GGUFType
+ * (GGUF.swift:7-14), as the reference does, or whose bytes pass the end. */
+int gd_gguf_tensor(const gd_gguf *g, const char *name, int *ndim, int64_t dims[4],
+                   int *type, const void **data, size_t *bytes);
+/* Metadata, GGUF.int / double / bool / string / ints / doubles
+ * (GGUF.swift:121-172): get_int reads integer types of any width (not bool,
+ * as GGUF.int); get_float reads f32/f64 and integers; get_bool reads bool and
+ * integers; arrays of integers or bools read as int64, of f32/f64 as double.
+ * An absent key or one of another type fails. */
+int gd_gguf_get_int(const gd_gguf *g, const char *key, int64_t *v);
+int gd_gguf_get_float(const gd_gguf *g, const char *key, double *v);
+int gd_gguf_get_bool(const gd_gguf *g, const char *key, int *v);
+int gd_gguf_get_string(const gd_gguf *g, const char *key, const char **v);
+int gd_gguf_get_ints(const gd_gguf *g, const char *key, const int64_t **v, int64_t *n);
+int gd_gguf_get_floats(const gd_gguf *g, const char *key, const double **v, int64_t *n);
+/* BonsaiConfig(gguf) (Model.swift:39-69) for the qwen35 hybrid; kv_block,
+ * max_ctx and max_batch are left 0 (they are runtime choices). */
+int gd_gguf_stack_config(const gd_gguf *g, gd_stack_config *cfg);
+/* BonsaiModel(path:) + upload (Model.swift:133-148, MetalContext.swift:
+ * 146-191): a stack whose weights are the file's tensors, repacked into the
+ * fused matrices.  The lm_head is output.weight when present, else the token
+ * embedding (Model.swift:145).  Every tensor the stack reads must be present
+ * with its exact shape: Q2_0 matrices, f32 norms/conv/dt/a.  The file may be
+ * closed once this returns. */
+int gd_stack_create_from_gguf(gd_ctx *ctx, const gd_gguf *g, int kv_block, int max_ctx,
+                              int max_batch, gd_stack **out);
 
 #ifdef __cplusplus
 }

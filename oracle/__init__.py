@@ -245,7 +245,8 @@ class OrStack(C.Structure):
                                   "n_rot")] + [("rope_base", _f), ("eps", _f)] + \
                [(n, _i) for n in ("n_vocab", "d_state", "n_k_head", "n_v_head", "d_conv",
                                   "max_ctx", "stage_f16", "threads")] + \
-               [("layers", C.POINTER(OrStackLayer)), ("embd", _vp), ("out_norm", _vp)]
+               [("layers", C.POINTER(OrStackLayer)), ("embd", _vp), ("out_norm", _vp),
+                ("head", _vp)]
 
 
 _PROTOS["or_stack_token"] = (None, [C.POINTER(OrStack), _i, _i, _vp, _vp])
@@ -263,13 +264,14 @@ class Stack:
     With stage_f16, `prefill` rounds every mat-vec input to f16 (the reference
     GPU prefill GEMM stages half tiles, Kernels.metal:428) and `token` does not
     (its decode GEMV reads f32 x, Kernels.metal:32-40) unless decode_f16 is
-    set; cached K/V are always rounded (half KV pages)."""
+    set; cached K/V are always rounded (half KV pages).  With untied the
+    lm_head is tensors(-1, "output"), else the token embedding (Model.swift:145)."""
 
     Q2 = {"rec": ("attn_qkv", "attn_gate", "ssm_beta", "ssm_alpha", "ssm_out"),
           "att": ("attn_q", "attn_k", "attn_v", "attn_output")}
 
     def __init__(self, cfg: dict, tensors, stage_f16: bool = True, threads: int = 8,
-                 decode_f16: bool = False):
+                 decode_f16: bool = False, untied: bool = False):
         self.cfg = cfg
         self.stage_prefill = (STAGE_MV | STAGE_KV) if stage_f16 else 0
         self.stage_decode = (STAGE_KV | (STAGE_MV if decode_f16 else 0)) if stage_f16 else 0
@@ -311,6 +313,7 @@ class Stack:
         st.layers = self.layers
         st.embd = ptr(tensors(-1, "token_embd"))
         st.out_norm = ptr(tensors(-1, "output_norm"))
+        st.head = ptr(tensors(-1, "output")) if untied else None
         self.st = st
         self.pos = 0
 

@@ -110,8 +110,10 @@ typedef struct or_stack {
     int stage_f16;     /* OR_STAGE_* bits: f16 rounding as the reference GPU path does */
     int threads;
     or_stack_layer *layers;
-    const uint8_t *embd;                        /* tied token_embd / lm_head */
+    const uint8_t *embd;                        /* token_embd */
     const float *out_norm;
+    const uint8_t *head;                        /* output.weight; NULL: tied to embd
+                                                   (Model.swift:145) */
 } or_stack;
 
 #define OR_STAGE_MV 1   /* mat-vec inputs (the prefill GEMM's half tiles, Kernels.metal:428) */

@@ -195,7 +195,8 @@ static void forward(or_stack *st, const int *tokens, int T, int pos0, float *hid
         for (int64_t i = 0; i < (int64_t)E * T; i++) x[i] += a[i];
     }
     or_rmsnorm(x + (int64_t)(T - 1) * E, st->out_norm, hidden_out, E, st->eps);
-    if (logits_out) matvec(st, st->embd, E, st->n_vocab, hidden_out, logits_out);
+    if (logits_out)
+        matvec(st, st->head ? st->head : st->embd, E, st->n_vocab, hidden_out, logits_out);
     free(x); free(nrm); free(a); free(gt); free(up);
 }
 
