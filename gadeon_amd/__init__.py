@@ -109,6 +109,11 @@ _PROTOS = {
     "gd_stack_position": (_i, [_vp, C.POINTER(_i64)]),
     "gd_stack_generate": (_i, [_vp, _i, _vp]),
     "gd_q2_0_repack_rows": (_i, [_vp, _vp, _u64, _i64, _i64, _Q2WP]),
+    "gd_stack_bookmark": (_i, [_vp, C.POINTER(_vp)]),
+    "gd_stack_restore": (_i, [_vp, _vp]),
+    "gd_bookmark_free": (None, [_vp]),
+    "gd_stack_serialize": (_i, [_vp, _vp, _vp, _sz, C.POINTER(_sz)]),
+    "gd_stack_deserialize": (_i, [_vp, _vp, _sz, C.POINTER(_vp)]),
     "gd_gguf_open": (_i, [C.c_char_p, C.POINTER(_vp)]),
     "gd_gguf_close": (None, [_vp]),
     "gd_gguf_info": (_i, [_vp, C.POINTER(_i64), C.POINTER(_i64), C.POINTER(_i)]),

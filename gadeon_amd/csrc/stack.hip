@@ -23,6 +23,7 @@
 
 #include <atomic>
 #include <cmath>
+#include <cstring>
 #include <string>
 #include <vector>
 
@@ -437,6 +438,7 @@ struct gd_stack {
     int32_t *ids = nullptr, *dpos = nullptr, *dtok = nullptr;
     int64_t pos = 0;
     bool random = true;          // weights drawn from the seed (else loaded)
+    bool have_pick = false;      // dtok holds the last greedy pick
     std::atomic<bool> stop{false};
     std::vector<void *> allocs;
     hipGraphExec_t decode_exec = nullptr;
@@ -789,6 +791,7 @@ extern "C" int gd_stack_reset(gd_stack *st) {
     if ((rc = gd_fill_u32(ctx, st->dpos, 0, 1)) || (rc = gd_fill_u32(ctx, st->dtok, 0, 1)))
         return rc;
     st->pos = 0;
+    st->have_pick = false;
     st->stop.store(false);
     return gd_sync(ctx);
 }
@@ -818,6 +821,7 @@ extern "C" int gd_stack_prefill(gd_stack *st, const int32_t *ids, int n, int32_t
             (rc = forward(st, N, false)))
             return rc;
         st->pos += N;
+        st->have_pick = true;
     }
     return finish(st, next, logits);
 }
@@ -834,6 +838,7 @@ extern "C" int gd_stack_decode(gd_stack *st, int32_t token, int32_t *next, float
         (rc = forward(st, 1, true)))
         return rc;
     st->pos += 1;
+    st->have_pick = true;
     return finish(st, next, logits);
 }
 
@@ -843,6 +848,8 @@ extern "C" int gd_stack_generate(gd_stack *st, int n, int32_t *tokens) {
     GD_REQUIRE(ctx, n >= 0 && tokens, "gd_stack_generate: bad arguments");
     GD_REQUIRE(ctx, st->pos + n <= st->c.max_ctx, "gd_stack_generate: context full");
     if (n == 0) return GD_OK;
+    GD_REQUIRE(ctx, st->have_pick,
+               "gd_stack_generate: no previous pick to continue from (prefill or decode first)");
     int rc;
     // GADEON_STACK_EAGER=1 launches every step's kernels directly instead of
     // replaying the captured graph (same kernels and results; for profilers
@@ -1068,5 +1075,305 @@ extern "C" int gd_stack_create_from_gguf(gd_ctx *ctx, const gd_gguf *g, int kv_b
         return rc;
     }
     *out = st;
+    return GD_OK;
+}
+
+// ------------------------------------------------------------ bookmarks
+
+// A snapshot of the generation state in device memory: position, the last
+// pick, every GDN layer's conv ring and recurrent state, and every attention
+// layer's cached K/V over positions [0, pos).  MetalEngine.Bookmark
+// (MetalEngine.swift:455-483) shares append-only KV pages; this pool's slots
+// are reused after a reset, so the used span is copied instead (an HBM copy
+// of 2 x pos x kv_dim halves per attention layer).
+struct gd_bookmark {
+    gd_ctx *ctx = nullptr;
+    gd_stack_config c{};
+    int64_t pos = 0;
+    bool have_pick = false;
+    void *buf = nullptr;         // [pick | conv, rec per GDN layer | k, v per attention layer]
+};
+
+namespace {
+
+struct BmLayout {
+    size_t conv = 0, rec = 0, kv = 0, total = 0;   // element counts per layer; bytes
+    std::vector<size_t> off;                       // per layer: byte offset of its first array
+};
+
+size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+BmLayout bm_layout(const gd_stack *st, int64_t pos) {
+    BmLayout l;
+    l.conv = (size_t)(st->c.d_conv - 1) * st->convDim;
+    l.rec = (size_t)st->c.n_v_head * HD * HD;
+    l.kv = (size_t)pos * st->c.n_head_kv * st->c.head_dim;
+    size_t o = 256;                                  // the pick
+    for (const StackLayer &ly : st->L) {
+        l.off.push_back(o);
+        o += ly.rec ? align256(l.conv * 4) + align256(l.rec * 4) : 2 * align256(l.kv * 2);
+    }
+    l.total = o;
+    return l;
+}
+
+bool same_geometry(const gd_stack_config &a, const gd_stack_config &b) {
+    return a.n_layer == b.n_layer && a.attn_interval == b.attn_interval &&
+           a.n_embd == b.n_embd && a.d_conv == b.d_conv && a.n_k_head == b.n_k_head &&
+           a.n_v_head == b.n_v_head && a.d_state == b.d_state && a.n_head_kv == b.n_head_kv &&
+           a.head_dim == b.head_dim;
+}
+
+int d2d(gd_ctx *ctx, void *dst, const void *src, size_t bytes) {
+    return bytes ? gd_copy(ctx, dst, src, bytes) : GD_OK;
+}
+
+// Little-endian i64 and f32-run writer / bounds-checked reader of
+// MetalEngine.serialize's byte format (MetalEngine.swift:490-584).
+struct Out {
+    uint8_t *p;
+    size_t cap, n = 0;
+    void put(const void *src, size_t b) {
+        if (p && n + b <= cap) memcpy(p + n, src, b);
+        n += b;
+    }
+    void i64(int64_t v) { put(&v, 8); }
+};
+
+struct In {
+    const uint8_t *p;
+    size_t len, n = 0;
+    bool bad = false;
+    int64_t i64() {
+        int64_t v = 0;
+        if (bad || len - n < 8) { bad = true; return 0; }
+        memcpy(&v, p + n, 8);
+        n += 8;
+        return v;
+    }
+    // A run of `want` floats: its count must be `want`; returns its bytes.
+    const uint8_t *floats(size_t want) {
+        const int64_t c = i64();
+        if (bad || c < 0 || (size_t)c != want || (len - n) / 4 < want) { bad = true; return nullptr; }
+        const uint8_t *r = p + n;
+        n += want * 4;
+        return r;
+    }
+};
+
+}  // namespace
+
+extern "C" int gd_stack_bookmark(gd_stack *st, gd_bookmark **out) {
+    if (!st) return GD_EINVAL;
+    gd_ctx *ctx = st->ctx;
+    GD_REQUIRE(ctx, out, "gd_stack_bookmark: null out pointer");
+    *out = nullptr;
+    const BmLayout l = bm_layout(st, st->pos);
+    gd_bookmark *b = new gd_bookmark();
+    b->ctx = ctx;
+    b->c = st->c;
+    b->pos = st->pos;
+    b->have_pick = st->have_pick;
+    int rc = gd_alloc(ctx, l.total, &b->buf);
+    uint8_t *base = (uint8_t *)b->buf;
+    if (rc == GD_OK) rc = d2d(ctx, base, st->dtok, 4);
+    for (int il = 0; rc == GD_OK && il < st->c.n_layer; il++) {
+        const StackLayer &ly = st->L[il];
+        uint8_t *d = base + l.off[il];
+        if (ly.rec) {
+            if ((rc = d2d(ctx, d, ly.conv_state, l.conv * 4)) == GD_OK)
+                rc = d2d(ctx, d + align256(l.conv * 4), ly.rec_state, l.rec * 4);
+        } else if ((rc = d2d(ctx, d, ly.kc, l.kv * 2)) == GD_OK) {
+            rc = d2d(ctx, d + align256(l.kv * 2), ly.vc, l.kv * 2);
+        }
+    }
+    if (rc == GD_OK) rc = gd_sync(ctx);
+    if (rc) {
+        gd_bookmark_free(b);
+        return rc;
+    }
+    *out = b;
+    return GD_OK;
+}
+
+extern "C" void gd_bookmark_free(gd_bookmark *b) {
+    if (!b) return;
+    if (b->buf) gd_free(b->ctx, b->buf);
+    delete b;
+}
+
+extern "C" int gd_stack_restore(gd_stack *st, const gd_bookmark *b) {
+    if (!st) return GD_EINVAL;
+    gd_ctx *ctx = st->ctx;
+    GD_REQUIRE(ctx, b && b->buf, "gd_stack_restore: null bookmark");
+    GD_REQUIRE(ctx, b->ctx == ctx, "gd_stack_restore: bookmark of another context");
+    GD_REQUIRE(ctx, same_geometry(b->c, st->c) && b->pos <= st->c.max_ctx,
+               "gd_stack_restore: bookmark of another geometry (or beyond max_ctx)");
+    const BmLayout l = bm_layout(st, b->pos);
+    const uint8_t *base = (const uint8_t *)b->buf;
+    int rc = d2d(ctx, st->dtok, base, 4);
+    for (int il = 0; rc == GD_OK && il < st->c.n_layer; il++) {
+        StackLayer &ly = st->L[il];
+        const uint8_t *s = base + l.off[il];
+        if (ly.rec) {
+            if ((rc = d2d(ctx, ly.conv_state, s, l.conv * 4)) == GD_OK)
+                rc = d2d(ctx, ly.rec_state, s + align256(l.conv * 4), l.rec * 4);
+        } else if ((rc = d2d(ctx, ly.kc, s, l.kv * 2)) == GD_OK) {
+            rc = d2d(ctx, ly.vc, s + align256(l.kv * 2), l.kv * 2);
+        }
+    }
+    const uint32_t pos32 = (uint32_t)b->pos;
+    if (rc == GD_OK) rc = gd_fill_u32(ctx, st->dpos, pos32, 1);
+    if (rc == GD_OK) rc = gd_sync(ctx);
+    if (rc) return rc;
+    st->pos = b->pos;
+    st->have_pick = b->have_pick;
+    st->stop.store(false);
+    return GD_OK;
+}
+
+extern "C" int gd_stack_serialize(gd_stack *st, const gd_bookmark *b, void *buf, size_t cap,
+                                  size_t *len) {
+    if (!st) return GD_EINVAL;
+    gd_ctx *ctx = st->ctx;
+    GD_REQUIRE(ctx, b && b->buf && len, "gd_stack_serialize: null argument");
+    GD_REQUIRE(ctx, b->ctx == ctx && same_geometry(b->c, st->c),
+               "gd_stack_serialize: bookmark of another stack geometry or context");
+    const BmLayout l = bm_layout(st, b->pos);
+    // Size pass (no data), then, given room, the bytes.
+    auto emit = [&](Out &o, const uint8_t *host) {
+        o.i64(b->pos);
+        o.i64(0);                                              // ropeShift: text only
+        for (int part = 0; part < 2; part++) {                 // conv dict, then rec dict
+            int64_t n = 0;
+            for (const StackLayer &ly : st->L) n += ly.rec;
+            o.i64(n);
+            for (int il = 0; il < st->c.n_layer; il++) {
+                if (!st->L[il].rec) continue;
+                const size_t cnt = part ? l.rec : l.conv;
+                o.i64(il);
+                o.i64((int64_t)cnt);
+                const size_t at = l.off[il] + (part ? align256(l.conv * 4) : 0);
+                o.put(host ? host + at : nullptr, cnt * 4);
+            }
+        }
+        int64_t na = 0;
+        for (const StackLayer &ly : st->L) na += !ly.rec;
+        o.i64(na);
+        std::vector<float> wide(host ? l.kv : 0);
+        for (int il = 0; il < st->c.n_layer; il++) {
+            if (st->L[il].rec) continue;
+            o.i64(il);
+            o.i64(b->pos);
+            for (int kv = 0; kv < 2; kv++) {                   // half pages widened to f32
+                o.i64((int64_t)l.kv);
+                if (host) {
+                    const _Float16 *h = (const _Float16 *)(host + l.off[il] +
+                                                           kv * align256(l.kv * 2));
+                    for (size_t i = 0; i < l.kv; i++) wide[i] = (float)h[i];
+                }
+                o.put(host ? wide.data() : nullptr, l.kv * 4);
+            }
+        }
+    };
+    Out sizer{nullptr, 0};
+    emit(sizer, nullptr);
+    *len = sizer.n;
+    if (!buf) return GD_OK;
+    GD_REQUIRE(ctx, cap >= sizer.n, "gd_stack_serialize: buffer of %zu bytes, need %zu", cap,
+               sizer.n);
+    std::vector<uint8_t> host(l.total);
+    int rc = gd_download(ctx, host.data(), b->buf, l.total);
+    if (rc) return rc;
+    Out o{(uint8_t *)buf, cap};
+    emit(o, host.data());
+    return GD_OK;
+}
+
+extern "C" int gd_stack_deserialize(gd_stack *st, const void *data, size_t n,
+                                    gd_bookmark **out) {
+    if (!st) return GD_EINVAL;
+    gd_ctx *ctx = st->ctx;
+    GD_REQUIRE(ctx, data && out, "gd_stack_deserialize: null argument");
+    *out = nullptr;
+    In in{(const uint8_t *)data, n};
+    const int64_t pos = in.i64(), rope_shift = in.i64();
+    GD_REQUIRE(ctx, !in.bad && pos >= 0 && pos <= st->c.max_ctx,
+               "gd_stack_deserialize: position %lld outside [0, max_ctx %d]", (long long)pos,
+               st->c.max_ctx);
+    GD_REQUIRE(ctx, rope_shift == 0,
+               "gd_stack_deserialize: ropeShift %lld (image spans) is not supported",
+               (long long)rope_shift);
+    const BmLayout l = bm_layout(st, pos);
+    std::vector<uint8_t> host(l.total, 0);
+    // Each dict must list exactly this stack's GDN (or attention) layers, in
+    // ascending order, as serialize writes them.
+    for (int part = 0; part < 2; part++) {
+        const int64_t cnt = in.i64();
+        int il = -1;
+        for (int64_t k = 0; k < cnt && !in.bad; k++) {
+            const int64_t want = [&] {
+                for (int j = il + 1; j < st->c.n_layer; j++) if (st->L[j].rec) return j;
+                return -1;
+            }();
+            const int64_t got = in.i64();
+            GD_REQUIRE(ctx, !in.bad && want >= 0 && got == want,
+                       "gd_stack_deserialize: GDN layer %lld where %lld was expected",
+                       (long long)got, (long long)want);
+            il = (int)got;
+            const size_t c = part ? l.rec : l.conv;
+            const uint8_t *src = in.floats(c);
+            GD_REQUIRE(ctx, !in.bad, "gd_stack_deserialize: layer %d state: bad count or "
+                       "truncated", il);
+            memcpy(host.data() + l.off[il] + (part ? align256(l.conv * 4) : 0), src, c * 4);
+        }
+        int64_t nrec = 0;
+        for (const StackLayer &ly : st->L) nrec += ly.rec;
+        GD_REQUIRE(ctx, !in.bad && cnt == nrec,
+                   "gd_stack_deserialize: %lld GDN layers in the data, the stack has %lld",
+                   (long long)cnt, (long long)nrec);
+    }
+    const int64_t na = in.i64();
+    int64_t natt = 0;
+    for (const StackLayer &ly : st->L) natt += !ly.rec;
+    GD_REQUIRE(ctx, !in.bad && na == natt,
+               "gd_stack_deserialize: %lld attention layers in the data, the stack has %lld",
+               (long long)na, (long long)natt);
+    int il = -1;
+    for (int64_t k = 0; k < na; k++) {
+        int want = -1;
+        for (int j = il + 1; j < st->c.n_layer; j++) if (!st->L[j].rec) { want = j; break; }
+        const int64_t got = in.i64(), len = in.i64();
+        GD_REQUIRE(ctx, !in.bad && got == want && len == pos,
+                   "gd_stack_deserialize: attention layer %lld with %lld positions where "
+                   "layer %d with %lld was expected", (long long)got, (long long)len, want,
+                   (long long)pos);
+        il = want;
+        for (int kv = 0; kv < 2; kv++) {
+            const uint8_t *src = in.floats(l.kv);
+            GD_REQUIRE(ctx, !in.bad, "gd_stack_deserialize: layer %d K/V: bad count or "
+                       "truncated", il);
+            // f32 back to the cache's halves, round to nearest even.
+            _Float16 *h = (_Float16 *)(host.data() + l.off[il] + kv * align256(l.kv * 2));
+            for (size_t i = 0; i < l.kv; i++) {
+                float f;
+                memcpy(&f, src + 4 * i, 4);
+                h[i] = (_Float16)f;
+            }
+        }
+    }
+    GD_REQUIRE(ctx, in.n == n, "gd_stack_deserialize: %zu trailing bytes", n - in.n);
+    gd_bookmark *b = new gd_bookmark();
+    b->ctx = ctx;
+    b->c = st->c;
+    b->pos = pos;
+    b->have_pick = false;        // the format carries no pick: decode a token first
+    int rc = gd_alloc(ctx, l.total, &b->buf);
+    if (rc == GD_OK) rc = gd_upload(ctx, b->buf, host.data(), l.total);
+    if (rc) {
+        gd_bookmark_free(b);
+        return rc;
+    }
+    *out = b;
     return GD_OK;
 }

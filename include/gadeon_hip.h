@@ -476,6 +476,30 @@ int gd_stack_tensor(gd_stack *st, int layer, const char *name, gd_q2w *w,
                     int64_t *row0, float **f32, int64_t *count);
 int gd_stack_position(gd_stack *st, int64_t *pos);
 
+/* ---- Bookmarks: MetalEngine.bookmark / restore / serialize / deserialize -------
+ * (MetalEngine.swift:455-584).  A bookmark is a device-memory snapshot of the
+ * generation state: position, the last greedy pick, each GDN layer's conv ring
+ * and recurrent state, each attention layer's K/V over positions [0, pos).
+ * It stays valid across later decode, reset and prefill calls and can be
+ * restored any number of times, into the stack it came from or another of
+ * the same geometry on the same context.  gd_stack_serialize writes the bytes
+ * of MetalEngine.serialize: i64 pos, i64 ropeShift (0), the conv and the rec
+ * dicts (i64 count, then per GDN layer in ascending order i64 layer, i64 n,
+ * n f32), and the KV dict (i64 count, then per attention layer i64 layer,
+ * i64 len, i64 n, n f32 of K, i64 n, n f32 of V, each [len][n_head_kv *
+ * head_dim]); all little-endian, KV widened from the cache's halves.  Call it
+ * with buf NULL to get the size in *len.  gd_stack_deserialize checks every
+ * count and layer index against the stack and returns a bookmark to restore;
+ * that format carries no pick, so after restoring it the next call must be
+ * gd_stack_decode (gd_stack_generate fails until then). */
+typedef struct gd_bookmark gd_bookmark;
+
+int gd_stack_bookmark(gd_stack *st, gd_bookmark **out);
+int gd_stack_restore(gd_stack *st, const gd_bookmark *b);
+void gd_bookmark_free(gd_bookmark *b);
+int gd_stack_serialize(gd_stack *st, const gd_bookmark *b, void *buf, size_t cap, size_t *len);
+int gd_stack_deserialize(gd_stack *st, const void *data, size_t n, gd_bookmark **out);
+
 /* ---- GGUF v3 reader (host only): GGUF.swift:45-117 ---------------------------
  * gd_gguf_open maps the file read-only and parses the header, the metadata and
  * the tensor directory; tensor data starts at the first multiple of
