@@ -272,10 +272,12 @@ def run_stack(ctx, ga, args) -> dict:
     nxt = C.c_int32()
     ms = C.c_float()
     try:
+        tg_on = args.workload != "pp"
         for _ in range(args.warmup):                 # extend(512) + 8 decodes, then reset
             ctx.check(lib.gd_stack_reset(h))
             ctx.check(lib.gd_stack_prefill(h, ids.ctypes.data, PP, C.byref(nxt), None))
-            ctx.check(lib.gd_stack_generate(h, 8, gen.ctypes.data))
+            if tg_on:
+                ctx.check(lib.gd_stack_generate(h, 8, gen.ctypes.data))
         pp_ms, tg_ms = [], []
         for i in range(args.steps):
             ctx.check(lib.gd_stack_reset(h))
@@ -283,6 +285,9 @@ def run_stack(ctx, ga, args) -> dict:
             ctx.check(lib.gd_stack_prefill(h, ids.ctypes.data, PP, C.byref(nxt), None))
             ctx.gd_timer_stop(C.byref(ms))
             pp_ms.append(ms.value)
+            if not tg_on:
+                log(f"pass {i}: pp{PP} {pp_ms[-1]:.1f} ms")
+                continue
             ctx.gd_timer_start()
             ctx.check(lib.gd_stack_generate(h, TG, gen.ctypes.data))
             ctx.gd_timer_stop(C.byref(ms))
@@ -290,11 +295,14 @@ def run_stack(ctx, ga, args) -> dict:
             log(f"pass {i}: pp{PP} {pp_ms[-1]:.1f} ms, tg{TG} {tg_ms[-1]:.1f} ms, "
                 f"first tokens {nxt.value} {list(gen[:4])}")
         cpu = None
-        if args.cpu_seconds > 0:
+        if args.cpu_seconds > 0 and tg_on:
             cpu = cpu_baseline_stack(ctx, ga, h, c, args.cpu_seconds)
     finally:
         lib.gd_stack_destroy(h)
     pp = sum(pp_ms) / len(pp_ms)
+    if not tg_ms:
+        return {"pp_ms": pp, "pp_tok_s": PP / (pp * 1e-3),
+                "pp_tflops": stack_flops_pp(c, PP) / (pp * 1e-3) / 1e12, "pp_ms_all": pp_ms}
     tg = sum(tg_ms) / len(tg_ms)
     wb = stack_weight_bytes(c)
     return {"pp_ms": pp, "tg_ms": tg, "pp_tok_s": PP / (pp * 1e-3), "tg_tok_s": TG / (tg * 1e-3),
@@ -492,9 +500,10 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=3,
                     help="timed passes (stack: one pp512 + tg128 pass each)")
     ap.add_argument("--warmup", type=int, default=1)
-    ap.add_argument("--workload", choices=("stack", "kernels", "roofline"), default="stack",
+    ap.add_argument("--workload", choices=("stack", "kernels", "roofline", "pp"), default="stack",
                     help="stack: config 4 (the metric); kernels: configs 0-3; roofline: only "
-                         "the roofline GEMV/GEMM and a calibration copy (for rocprofv3 runs)")
+                         "the roofline GEMV/GEMM and a calibration copy; pp: only the config-4 "
+                         "pp512 passes (the last two for rocprofv3 runs)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -508,6 +517,10 @@ def main() -> int:
             r = run_stack(ctx, ga, args)
             r["kernels"] = kernel_rooflines(ctx, ga, 20)
             r["configs"] = run_configs(ctx, ga, 3, 1)
+        elif args.workload == "pp":
+            r = run_stack(ctx, ga, args)
+            print(json.dumps({"workload": "config 4 pp512 only", **r}))
+            return 0
         elif args.workload == "roofline":
             r = kernel_rooflines(ctx, ga, 40)
             r["calibration"] = calibration_copy(ctx, ga)

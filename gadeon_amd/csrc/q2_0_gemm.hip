@@ -532,6 +532,10 @@ int gd_gemm_glu(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, uint16_t
     GD_REQUIRE(ctx, R % 32 == 0 && T > 0 && K % 128 == 0 && R < (1 << 22), "gd_gemm_glu: R=%d "
                "must hold two halves of 16-row groups (and be below 4194304)", R);
     const int nblk = K / 128;
+    // A wave's code resource spans the gate rows from its own on plus the up
+    // rows (ff/16 + NT row groups, NT <= 2) as a 32-bit byte range.
+    GD_REQUIRE(ctx, (uint64_t)(R / 32 + 2) * (uint64_t)((nblk + 3) / 4) * 2048u < (1ULL << 32),
+               "gd_gemm_glu: K=%d R=%d spans 4 GiB of codes in one buffer resource", K, R);
     const int cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
     auto cols = [](const Shape &sh) { return 16 * sh.nw * sh.nt; };
     auto tiles_t = [&](const Shape &sh) { return (T + sh.mt * 32 - 1) / (sh.mt * 32); };

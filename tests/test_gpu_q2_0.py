@@ -352,6 +352,25 @@ def test_gemm_plan_rejects_unknown_tile(ctx):
     ctx.gd_q2w_free(C.byref(w))
 
 
+def test_gemm_swiglu_rejects_4gib_code_span(ctx):
+    """ff = 17408 with K = 985088: one wave's code resource (gate rows from its
+    own on, then the up rows) would span 4 GiB of codes, past what its 32-bit
+    byte range holds.  The matrix is real (8.6 GB of zero codes), so had the
+    shape been taken, the launch would only have read zeros."""
+    K, R = 985088, 2 * 17408
+    w = ga.Q2W()
+    ctx.gd_q2w_alloc(K, R, C.byref(w))
+    dX = ctx.alloc(K * 2)
+    dO = ctx.alloc(R // 2 * 2)
+    try:
+        with pytest.raises(RuntimeError, match="4 GiB"):
+            ctx.gd_q2_0_gemm_swiglu(C.byref(w), 1, dX, dO)
+    finally:
+        ctx.free(dX)
+        ctx.free(dO)
+        ctx.gd_q2w_free(C.byref(w))
+
+
 def test_gemm_full_size_sampled_rows(ctx):
     """BASELINE config 1 shapes at full size: every output row against the GPU
     GEMV of the same weights (independent kernel), and 48 sampled rows x all
