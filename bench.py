@@ -215,7 +215,7 @@ def cpu_baseline_gemv(seconds: float = 10.0) -> dict:
     x = O.lcg_normal_f16(K, 2).astype(np.float32)
     O.q2_0_matvec(blocks, K, R, x, threads)
     n, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
+    while time.perf_counter() - t0 < seconds or n == 0:
         O.q2_0_matvec(blocks, K, R, x, threads)
         n += 1
     dt = (time.perf_counter() - t0) / n

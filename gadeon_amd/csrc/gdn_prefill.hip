@@ -27,11 +27,12 @@
 //             levels of block products, all 256 threads); then W = T X and
 //             U = T Y (the UT transform) on the matrix cores.  The chunks are
 //             independent.
-//   gdn_scan  (value head, 16 columns of S): walks the chunks in order with
-//             its slice of S resident in LDS: delta = U - W S, O = qScale
-//             e^G (Q S) + P delta, S <- e^{G_L} S + K^T (e^{G_L-G} delta).
-//             Value columns of S are independent, which is what splits the
-//             serial part across workgroups.
+//   gdn_scan  (value head, 16 columns of S): walks the chunks in order:
+//             delta = U - W S, S <- e^{G_L} S + K^T (e^{G_L-G} delta) on one
+//             group of four waves (the serial chain, S in its registers),
+//             O = qScale e^G (Q S) + P delta one chunk behind on a second
+//             group, off the chain.  Value columns of S are independent,
+//             which is what splits the serial part across workgroups.
 // Workspace per (head, chunk) unit, CP = max(32, C) rows (rows past the
 // chunk's tokens are zero): W hi/lo [CP][128] f16, U [CP][128] f32, P hi/lo
 // [CP][CP] f16, K^T (hi, and lo for f32 k) [128][CP] f16, G [CP] f32.
@@ -153,7 +154,14 @@ __global__ __launch_bounds__(256) void gdn_prep(PrepArgs a) {
     __shared__ __attribute__((aligned(16))) float Ms[(CP / 16 - 1) * 256];   // block products
     __shared__ float Gs[CP], Bs[CP], BEs[CP];               // G, beta, beta e^G
 
-    const int hv = blockIdx.x / a.nchunks, c = blockIdx.x % a.nchunks;
+    // Workgroup b runs on XCD b % 8.  When the units divide by 8, XCD x takes
+    // the contiguous units x * units/8 .., so a head's chunks are written into
+    // the L2 of the XCD whose scan workgroups read them (the scan deals each
+    // head's column slices to one XCD in the same order).
+    const int units = (int)gridDim.x;
+    const int ub = units % 8 == 0 ? (int)((blockIdx.x & 7) * (units >> 3) + (blockIdx.x >> 3))
+                                  : (int)blockIdx.x;
+    const int hv = ub / a.nchunks, c = ub % a.nchunks;
     const int hk = hv % a.nK;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t t0 = (int64_t)c * a.C;
@@ -416,33 +424,43 @@ struct ScanArgs {
     float qScale;
 };
 
-// One chunk's operands of this thread, all independent of S: each group is
-// loaded while the previous chunk's later phases run, so the serial walk over
-// chunks waits on little but its own LDS.
+// The scan's workgroup is two groups of four waves.  The chain group walks the
+// recurrence: per chunk delta = U - W S, then S <- e^{G_L} S + K^T (e^{G_L-G}
+// delta), which is all the next chunk waits for.  The output group computes O
+// = qScale e^G (Q S) + P delta one chunk behind, beside the chain: Q S while
+// the chain updates S, P delta while it forms the next delta.  The split of S
+// (hi/lo, the B operand of W S and Q S), delta and G are double-buffered in
+// LDS by chunk parity, so neither group overwrites what the other still reads.
+constexpr int SCAN_THREADS = 512;     // chain group: threads 0..255, output group 256..511
+
+// The chain group's operands of one chunk, all independent of S, loaded one
+// phase ahead of their use: W, U and G after delta, K^T after the update.
 template <int CP, typename IO>
-struct ScanChunk {
+struct ChainRegs {
     float g;                              // G[tid] (tid < CP)
     f16x8 wh[DK / 32], wl[DK / 32];       // W rows 16*wave + lr
     float uv[NCOL / 16][4];               // U rows 16*wave + 4*kg + v, this lane's column
-    Raw8<IO> qr[DK / 32];                 // Q row 16*wave + lr (row 0 past the chunk), raw
-    f16x8 ph[CP / 32], pl[CP / 32];       // P row 16*wave + lr
     f16x8 ka[2][CP / 32];                 // K^T rows 32*wave + 16*rt + lr
     f16x8 kal[sizeof(IO) == 4 ? 2 : 1][CP / 32];   // their lo halves (f32 k)
 };
 
+// The output group's operands of one chunk: Q (raw) and P.
+template <int CP, typename IO>
+struct OutRegs {
+    Raw8<IO> qr[DK / 32];                 // Q row 16*wave + lr (row 0 past the chunk), raw
+    f16x8 ph[CP / 32], pl[CP / 32];       // P row 16*wave + lr
+};
+
 template <int CP, typename IO, typename OT>
-__global__ __launch_bounds__(256) void gdn_scan(ScanArgs a) {
-    // S slice transposed, St[j][i] = S[i][j0 + j]: the split reads 8 key rows
-    // of one column and the update 4, each as contiguous 16-byte reads
-    // (rows of 132 floats put the 16 columns of one read on distinct banks).
-    __shared__ __attribute__((aligned(16))) float St[NCOL][DK + 4];
-    __shared__ __attribute__((aligned(16))) f16 Sh[NCOL][PADK], Sl[NCOL][PADK];  // S^T split
-    __shared__ __attribute__((aligned(16))) f16 Dh[NCOL][CP + 8], Dl[NCOL][CP + 8];  // delta^T
+__global__ __launch_bounds__(SCAN_THREADS) void gdn_scan(ScanArgs a) {
+    __shared__ __attribute__((aligned(16))) f16 Sh[2][NCOL][PADK], Sl[2][NCOL][PADK];  // S^T split
+    __shared__ __attribute__((aligned(16))) f16 Dh[2][NCOL][CP + 8], Dl[2][NCOL][CP + 8];  // delta^T
     __shared__ __attribute__((aligned(16))) f16 Eh[NCOL][CP + 8], El[NCOL][CP + 8];  // decayed
-    __shared__ float Gs[CP];
+    __shared__ float Gs[2][CP];
 
     constexpr int NCB = DV / NCOL;
     static_assert(NCB % 8 == 0, "the grid must split evenly over the 8 XCDs");
+    static_assert(NCOL == 16, "one 16-column MFMA tile per lane group");
     // Workgroup b runs on XCD b % 8.  The NCB column slices of one head read
     // the same chunk operands (W, P, K^T, Q), so they are dealt to one XCD:
     // unit u = (b % 8) * (grid / 8) + b / 8, head u / NCB, so each chunk is
@@ -450,34 +468,34 @@ __global__ __launch_bounds__(256) void gdn_scan(ScanArgs a) {
     const int u = (int)((blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3));
     const int hv = u / NCB, j0 = (u % NCB) * NCOL;
     const int hk = hv % a.nK;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x & 255, lane = tid & 63, wave = tid >> 6;
+    // A wave's role as a scalar: the group branches below are jumps, so no
+    // wave ever steps through another group's barriers with its lanes off.
+    const int wbase = __builtin_amdgcn_readfirstlane((int)threadIdx.x);
+    const bool chain = wbase < 256;
     const int lr = lane & 15, kg = lane >> 4;
-    // This wave owns 16 chunk rows (with CP = 64 every wave does: a constant,
-    // so no load below sits in a branch, which keeps the compiler's wait
-    // counts exact).
+    // A wave owns 16 chunk rows (with CP = 64 every wave does: a constant, so
+    // no load below sits in a branch, which keeps the compiler's wait counts
+    // exact).
     const bool rows = CP / 16 >= 4 || wave < CP / 16;
     const int tb = wave * 16;
     float *Sg = a.S + (size_t)hv * DK * DV;
-
-    for (int e = tid; e < DK * NCOL; e += 256) {
-        const int i = e / NCOL, j = e % NCOL;
-        St[j][i] = Sg[(size_t)i * DV + j0 + j];
-    }
-
-    // The operands of chunk c, loaded in three groups, each refilled for the
-    // next chunk as soon as its phase of this chunk has used it: W, U and G
-    // after delta, Q and P after O, K^T after the state update.  One set of
-    // registers (two full sets made the compiler reuse registers that loads
-    // in flight were still to write, and wait for every load).
-    ScanChunk<CP, IO> k;
     auto unit = [&](int c) { return (size_t)hv * a.nchunks + min(c, a.nchunks - 1); };
-    auto loadW = [&](int c) {
-        const size_t u = unit(c);
-        k.g = a.w.G[u * CP + min(tid, CP - 1)];         // used by tid < CP
+
+    // Chain group: S entries (rows 32*wave + 16*rt + 4*kg + v, column lr)
+    // live in registers, as the state update's accumulators lay them out.
+    // A group's operands for chunk c + 1 are loaded as soon as chunk c has
+    // used them: W, U and G after delta, K^T after the update, P after
+    // P delta, Q after Q S.  (Two register sets, loading two chunks ahead,
+    // measured slower.)
+    float st[2][4];
+    auto loadW = [&](int c, ChainRegs<CP, IO> &k) {
+        const size_t un = unit(c);
+        k.g = a.w.G[un * CP + min(tid, CP - 1)];        // used by tid < CP
         if (rows) {
 #pragma unroll
             for (int ks = 0; ks < DK / 32; ks++) {
-                const size_t wi = (u * CP + tb + lr) * DK + ks * 32 + kg * 8;
+                const size_t wi = (un * CP + tb + lr) * DK + ks * 32 + kg * 8;
                 k.wh[ks] = *(const f16x8 *)&a.w.Wh[wi];
                 k.wl[ks] = *(const f16x8 *)&a.w.Wl[wi];
             }
@@ -485,12 +503,102 @@ __global__ __launch_bounds__(256) void gdn_scan(ScanArgs a) {
             for (int ct = 0; ct < NCOL / 16; ct++)
 #pragma unroll
                 for (int v = 0; v < 4; v++)
-                    k.uv[ct][v] = a.w.U[(u * CP + tb + kg * 4 + v) * DV + j0 + ct * 16 + lr];
+                    k.uv[ct][v] = a.w.U[(un * CP + tb + kg * 4 + v) * DV + j0 + ct * 16 + lr];
         }
     };
-    auto loadQP = [&](int c) {
+    auto loadK = [&](int c, ChainRegs<CP, IO> &k) {
+        const size_t un = unit(c);
+#pragma unroll
+        for (int rt = 0; rt < 2; rt++)
+#pragma unroll
+            for (int ks = 0; ks < CP / 32; ks++) {
+                const size_t ki = (un * DK + wave * 32 + rt * 16 + lr) * CP + ks * 32 + kg * 8;
+                k.ka[rt][ks] = *(const f16x8 *)&a.w.KT[ki];
+                if constexpr (sizeof(IO) == 4) k.kal[rt][ks] = *(const f16x8 *)&a.w.KTl[ki];
+            }
+    };
+    // Split this lane's S entries into the hi/lo planes of buffer b.
+    auto split_own = [&](int b) {
+#pragma unroll
+        for (int rt = 0; rt < 2; rt++) {
+            const int i = wave * 32 + rt * 16 + kg * 4;
+            f16 h[4], l[4];
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                h[v] = (f16)st[rt][v];
+                l[v] = (f16)(st[rt][v] - (float)h[v]);
+            }
+            *(f16x4 *)&Sh[b][lr][i] = f16x4{h[0], h[1], h[2], h[3]};
+            *(f16x4 *)&Sl[b][lr][i] = f16x4{l[0], l[1], l[2], l[3]};
+        }
+    };
+    // One chunk of the chain: its two barriers, delta, the state update.
+    auto chain_chunk = [&](int c, ChainRegs<CP, IO> &k) {
+        const int b = c & 1;
+        __syncthreads();
+        // delta = U - W S (rows 16*wave ..), then delta^T and its decayed
+        // copy e^{G_L - G_t} delta^T, split, to LDS.
+        const float gl = Gs[b][CP - 1];                 // G of the chunk's last token
+        if (rows) {
+            const int j = lr;
+            f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < DK / 32; ks++) {
+                const int i0 = ks * 32 + kg * 8;
+                acc = mfma3(k.wh[ks], k.wl[ks], *(const f16x8 *)&Sh[b][j][i0],
+                            *(const f16x8 *)&Sl[b][j][i0], acc);
+            }
+            f16 dh[4], dl[4], eh[4], el[4];
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int t = tb + kg * 4 + v;
+                const float d = k.uv[0][v] - acc[v];
+                const float ed = expf(gl - Gs[b][t]) * d;
+                dh[v] = (f16)d;
+                dl[v] = (f16)(d - (float)dh[v]);
+                eh[v] = (f16)ed;
+                el[v] = (f16)(ed - (float)eh[v]);
+            }
+            const int tq = tb + kg * 4;
+            *(f16x4 *)&Dh[b][j][tq] = f16x4{dh[0], dh[1], dh[2], dh[3]};
+            *(f16x4 *)&Dl[b][j][tq] = f16x4{dl[0], dl[1], dl[2], dl[3]};
+            *(f16x4 *)&Eh[j][tq] = f16x4{eh[0], eh[1], eh[2], eh[3]};
+            *(f16x4 *)&El[j][tq] = f16x4{el[0], el[1], el[2], el[3]};
+        }
+        loadW(c + 1, k);
+        __syncthreads();
+        // S <- e^{G_L} S + K^T (e^{G_L - G} delta): rows 32*wave .. +31,
+        // then its split into the other buffer and chunk c+1's G.
+        const float decay = expf(gl);
+#pragma unroll
+        for (int rt = 0; rt < 2; rt++) {
+            const int j = lr;
+            f32x4 acc;
+#pragma unroll
+            for (int v = 0; v < 4; v++) acc[v] = decay * st[rt][v];
+#pragma unroll
+            for (int ks = 0; ks < CP / 32; ks++) {
+                const int s0 = ks * 32 + kg * 8;
+                if constexpr (sizeof(IO) == 4) {
+                    acc = mfma3(k.ka[rt][ks], k.kal[rt][ks], *(const f16x8 *)&Eh[j][s0],
+                                *(const f16x8 *)&El[j][s0], acc);
+                } else {
+                    acc = mfma(k.ka[rt][ks], *(const f16x8 *)&Eh[j][s0], acc);
+                    acc = mfma(k.ka[rt][ks], *(const f16x8 *)&El[j][s0], acc);
+                }
+            }
+#pragma unroll
+            for (int v = 0; v < 4; v++) st[rt][v] = acc[v];
+        }
+        split_own(b ^ 1);
+        if (tid < CP) Gs[b ^ 1][tid] = k.g;                // chunk c + 1's G
+        loadK(c + 1, k);
+    };
+
+    // Output group.
+    f32x4 oacc = f32x4{0.f, 0.f, 0.f, 0.f};
+    auto loadQ = [&](int c, OutRegs<CP, IO> &o) {
         c = min(c, a.nchunks - 1);
-        const size_t u = unit(c);
         const int64_t t0 = (int64_t)c * a.C;
         const int L = (int)min((int64_t)a.C, a.T - t0);
         if (rows) {
@@ -498,164 +606,120 @@ __global__ __launch_bounds__(256) void gdn_scan(ScanArgs a) {
             const bool rok = tr < L;
 #pragma unroll
             for (int ks = 0; ks < DK / 32; ks++)
-                k.qr[ks] = load_raw8<IO>(a.q, (t0 + (rok ? tr : 0)) * a.q_stride + (int64_t)hk * DK +
+                o.qr[ks] = load_raw8<IO>(a.q, (t0 + (rok ? tr : 0)) * a.q_stride + (int64_t)hk * DK +
                                                   ks * 32 + kg * 8);
-#pragma unroll
-            for (int ks = 0; ks < CP / 32; ks++) {
-                const size_t pi = (u * CP + tr) * CP + ks * 32 + kg * 8;
-                k.ph[ks] = *(const f16x8 *)&a.w.Ph[pi];
-                k.pl[ks] = *(const f16x8 *)&a.w.Pl[pi];
-            }
         }
     };
-    auto loadK = [&](int c) {
-        const size_t u = unit(c);
-#pragma unroll
-        for (int rt = 0; rt < 2; rt++)
-#pragma unroll
-            for (int ks = 0; ks < CP / 32; ks++) {
-                const size_t ki = (u * DK + wave * 32 + rt * 16 + lr) * CP + ks * 32 + kg * 8;
-                k.ka[rt][ks] = *(const f16x8 *)&a.w.KT[ki];
-                if constexpr (sizeof(IO) == 4) k.kal[rt][ks] = *(const f16x8 *)&a.w.KTl[ki];
-            }
-    };
-
-    auto process = [&](int c) {
-        const int64_t t0 = (int64_t)c * a.C;
-        const int L = (int)min((int64_t)a.C, a.T - t0);
-        __syncthreads();
-        // S^T split (B operand of W S and Q S): entry (j, 8 rows i .. i+7).
-        for (int e = tid; e < NCOL * (DK / 8); e += 256) {
-            const int j = e / (DK / 8), i8 = (e % (DK / 8)) * 8;
-            float sv[8];
-#pragma unroll
-            for (int q = 0; q < 8; q++) sv[q] = St[j][i8 + q];
-            f16x8 h, l;
-            split8(sv, h, l);
-            *(f16x8 *)&Sh[j][i8] = h;
-            *(f16x8 *)&Sl[j][i8] = l;
-        }
-        if (tid < CP) Gs[tid] = k.g;
-        __syncthreads();
-        const float gl = Gs[CP - 1];                    // G of the chunk's last token
-
-        // delta = U - W S (rows 16*wave ..), then delta^T and its decayed
-        // copy e^{G_L - G_t} delta^T, split, to LDS.
+    auto loadP = [&](int c, OutRegs<CP, IO> &o) {
+        const size_t un = unit(c);
         if (rows) {
 #pragma unroll
-            for (int ct = 0; ct < NCOL / 16; ct++) {
-                const int j = ct * 16 + lr;
-                f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int ks = 0; ks < DK / 32; ks++) {
-                    const int i0 = ks * 32 + kg * 8;
-                    acc = mfma3(k.wh[ks], k.wl[ks], *(const f16x8 *)&Sh[j][i0],
-                                *(const f16x8 *)&Sl[j][i0], acc);
-                }
-                f16 dh[4], dl[4], eh[4], el[4];
-#pragma unroll
-                for (int v = 0; v < 4; v++) {
-                    const int t = tb + kg * 4 + v;
-                    const float d = k.uv[ct][v] - acc[v];
-                    const float ed = expf(gl - Gs[t]) * d;
-                    dh[v] = (f16)d;
-                    dl[v] = (f16)(d - (float)dh[v]);
-                    eh[v] = (f16)ed;
-                    el[v] = (f16)(ed - (float)eh[v]);
-                }
-                const int tq = tb + kg * 4;
-                *(f16x4 *)&Dh[j][tq] = f16x4{dh[0], dh[1], dh[2], dh[3]};
-                *(f16x4 *)&Dl[j][tq] = f16x4{dl[0], dl[1], dl[2], dl[3]};
-                *(f16x4 *)&Eh[j][tq] = f16x4{eh[0], eh[1], eh[2], eh[3]};
-                *(f16x4 *)&El[j][tq] = f16x4{el[0], el[1], el[2], el[3]};
+            for (int ks = 0; ks < CP / 32; ks++) {
+                const size_t pi = (un * CP + tb + lr) * CP + ks * 32 + kg * 8;
+                o.ph[ks] = *(const f16x8 *)&a.w.Ph[pi];
+                o.pl[ks] = *(const f16x8 *)&a.w.Pl[pi];
             }
         }
-        loadW(c + 1);
-        __syncthreads();
-
-        // O = qScale e^{G_t} (Q S) + P delta for the chunk's tokens.
-        // Output rows t0 .. t0+L-1 through a bounds-checked buffer resource.
+    };
+    // O of chunk c, first part: qScale e^{G_t} (Q S_c) into oacc.
+    auto out_qs = [&](int c, const OutRegs<CP, IO> &o) {
+        const int b = c & 1;
+        const int64_t t0 = (int64_t)c * a.C;
+        const int L = (int)min((int64_t)a.C, a.T - t0);
+        if (rows) {
+            const int j = lr;
+            f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < DK / 32; ks++) {
+                const int i0 = ks * 32 + kg * 8;
+                if constexpr (sizeof(IO) == 4) {
+                    f16x8 qh, ql;
+                    split_raw8<IO>(o.qr[ks], tb + lr < L, qh, ql);
+                    acc = mfma3(qh, ql, *(const f16x8 *)&Sh[b][j][i0], *(const f16x8 *)&Sl[b][j][i0],
+                                acc);
+                } else {
+                    const f16x8 qa = cvt8<IO>(o.qr[ks], tb + lr < L);
+                    acc = mfma(qa, *(const f16x8 *)&Sh[b][j][i0], acc);
+                    acc = mfma(qa, *(const f16x8 *)&Sl[b][j][i0], acc);
+                }
+            }
+#pragma unroll
+            for (int v = 0; v < 4; v++) acc[v] *= a.qScale * expf(Gs[b][tb + kg * 4 + v]);
+            oacc = acc;
+        }
+    };
+    // Second part: + P delta_c, then the chunk's output rows (rows t >= L
+    // lie past the bounds-checked resource: their stores are dropped).
+    auto out_pd = [&](int c, const OutRegs<CP, IO> &o) {
+        const int b = c & 1;
+        const int64_t t0 = (int64_t)c * a.C;
+        const int L = (int)min((int64_t)a.C, a.T - t0);
         const __amdgpu_buffer_rsrc_t ors = gd_rsrc((OT *)a.o + t0 * a.o_stride,
                                                    (uint32_t)L * (uint32_t)a.o_stride * sizeof(OT));
         const uint32_t obase = (uint32_t)hv * DV + j0;
         if (rows) {
+            const int j = lr;
+            f32x4 acc = oacc;
 #pragma unroll
-            for (int ct = 0; ct < NCOL / 16; ct++) {
-                const int j = ct * 16 + lr;
-                f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int ks = 0; ks < CP / 32; ks++) {
+                const int s0 = ks * 32 + kg * 8;
+                acc = mfma3(o.ph[ks], o.pl[ks], *(const f16x8 *)&Dh[b][j][s0],
+                            *(const f16x8 *)&Dl[b][j][s0], acc);
+            }
 #pragma unroll
-                for (int ks = 0; ks < DK / 32; ks++) {
-                    const int i0 = ks * 32 + kg * 8;
-                    if constexpr (sizeof(IO) == 4) {
-                        f16x8 qh, ql;
-                        split_raw8<IO>(k.qr[ks], tb + lr < L, qh, ql);
-                        acc = mfma3(qh, ql, *(const f16x8 *)&Sh[j][i0],
-                                    *(const f16x8 *)&Sl[j][i0], acc);
-                    } else {
-                        const f16x8 qa = cvt8<IO>(k.qr[ks], tb + lr < L);
-                        acc = mfma(qa, *(const f16x8 *)&Sh[j][i0], acc);
-                        acc = mfma(qa, *(const f16x8 *)&Sl[j][i0], acc);
-                    }
-                }
-#pragma unroll
-                for (int v = 0; v < 4; v++) acc[v] *= a.qScale * expf(Gs[tb + kg * 4 + v]);
-#pragma unroll
-                for (int ks = 0; ks < CP / 32; ks++) {
-                    const int s0 = ks * 32 + kg * 8;
-                    acc = mfma3(k.ph[ks], k.pl[ks], *(const f16x8 *)&Dh[j][s0],
-                                *(const f16x8 *)&Dl[j][s0], acc);
-                }
-                // Rows t >= L lie past the resource: the store is dropped.
-#pragma unroll
-                for (int v = 0; v < 4; v++) {
-                    const uint32_t oo =
-                            ((uint32_t)(tb + kg * 4 + v) * (uint32_t)a.o_stride + obase + j) * sizeof(OT);
-                    if constexpr (sizeof(OT) == 4)
-                        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[v]), ors, oo, 0, 0);
-                    else
-                        __builtin_amdgcn_raw_buffer_store_b16(gd_f2h(acc[v]), ors, oo, 0, 0);
-                }
+            for (int v = 0; v < 4; v++) {
+                const uint32_t oo =
+                        ((uint32_t)(tb + kg * 4 + v) * (uint32_t)a.o_stride + obase + j) * sizeof(OT);
+                if constexpr (sizeof(OT) == 4)
+                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[v]), ors, oo, 0, 0);
+                else
+                    __builtin_amdgcn_raw_buffer_store_b16(gd_f2h(acc[v]), ors, oo, 0, 0);
             }
         }
-        loadQP(c + 1);
-
-        // S <- e^{G_L} S + K^T (e^{G_L - G} delta): rows 32*wave .. +31.
-        const float decay = expf(gl);
-#pragma unroll
-        for (int rt = 0; rt < 2; rt++) {
-            const int ib = wave * 32 + rt * 16;
-#pragma unroll
-            for (int ct = 0; ct < NCOL / 16; ct++) {
-                const int j = ct * 16 + lr;
-                f32x4 acc;
-#pragma unroll
-                for (int v = 0; v < 4; v++) acc[v] = decay * St[j][ib + kg * 4 + v];
-#pragma unroll
-                for (int ks = 0; ks < CP / 32; ks++) {
-                    const int s0 = ks * 32 + kg * 8;
-                    if constexpr (sizeof(IO) == 4) {
-                        acc = mfma3(k.ka[rt][ks], k.kal[rt][ks], *(const f16x8 *)&Eh[j][s0],
-                                    *(const f16x8 *)&El[j][s0], acc);
-                    } else {
-                        acc = mfma(k.ka[rt][ks], *(const f16x8 *)&Eh[j][s0], acc);
-                        acc = mfma(k.ka[rt][ks], *(const f16x8 *)&El[j][s0], acc);
-                    }
-                }
-#pragma unroll
-                for (int v = 0; v < 4; v++) St[j][ib + kg * 4 + v] = acc[v];
-            }
+    };
+    // One chunk of the output group: its two barriers, P delta of chunk
+    // c - 1, Q S of chunk c.
+    auto out_chunk = [&](int c, OutRegs<CP, IO> &o) {
+        __syncthreads();
+        if (c > 0) {
+            out_pd(c - 1, o);
+            loadP(c, o);
         }
-        loadK(c + 1);
+        __syncthreads();
+        out_qs(c, o);
+        loadQ(c + 1, o);
     };
 
-    loadW(0);
-    loadQP(0);
-    loadK(0);
-    for (int c = 0; c < a.nchunks; c++) process(c);
-    __syncthreads();
-    for (int e = tid; e < DK * NCOL; e += 256) {
-        const int i = e / NCOL, j = e % NCOL;
-        Sg[(size_t)i * DV + j0 + j] = St[j][i];
+    // Each group runs its own loop over the chunks (one merged loop would join
+    // the groups' load streams at every phase, and the compiler's wait counts
+    // would then wait for loads a group does not need).  Both loops pass the
+    // same barriers: two per chunk and one after the last, 2 * nchunks + 1.
+    if (chain) {
+        ChainRegs<CP, IO> k;
+        // Prologue: S_0 into registers, its split into buffer 0, G of chunk 0.
+#pragma unroll
+        for (int rt = 0; rt < 2; rt++)
+#pragma unroll
+            for (int v = 0; v < 4; v++)
+                st[rt][v] = Sg[(size_t)(wave * 32 + rt * 16 + kg * 4 + v) * DV + j0 + lr];
+        loadW(0, k);
+        loadK(0, k);
+        split_own(0);
+        if (tid < CP) Gs[0][tid] = k.g;
+        for (int c = 0; c < a.nchunks; c++) chain_chunk(c, k);
+        __syncthreads();
+#pragma unroll
+        for (int rt = 0; rt < 2; rt++)
+#pragma unroll
+            for (int v = 0; v < 4; v++)
+                Sg[(size_t)(wave * 32 + rt * 16 + kg * 4 + v) * DV + j0 + lr] = st[rt][v];
+    } else {
+        OutRegs<CP, IO> o;
+        loadQ(0, o);
+        loadP(0, o);
+        for (int c = 0; c < a.nchunks; c++) out_chunk(c, o);
+        __syncthreads();
+        out_pd(a.nchunks - 1, o);
     }
 }
 
@@ -669,7 +733,7 @@ int launch(gd_ctx *ctx, const PrepArgs &pa, const ScanArgs &sa, int io_dtype, in
     GD_LAUNCHED(ctx, "gdn_prep");
     const dim3 grid((unsigned)(sa.nV * (DV / NCOL)));
 #define GD_SCAN(IO, OT) \
-    hipLaunchKernelGGL((gdn_scan<CP, IO, OT>), grid, dim3(256), 0, ctx->stream, sa)
+    hipLaunchKernelGGL((gdn_scan<CP, IO, OT>), grid, dim3(SCAN_THREADS), 0, ctx->stream, sa)
     if (io_dtype == GD_F32) { if (o_dtype == GD_F32) GD_SCAN(float, float); else GD_SCAN(float, uint16_t); }
     else { if (o_dtype == GD_F32) GD_SCAN(uint16_t, float); else GD_SCAN(uint16_t, uint16_t); }
 #undef GD_SCAN
