@@ -32,7 +32,7 @@ class StackConfig(C.Structure):
     _fields_ = [(n, _i) for n in ("n_layer", "n_embd", "n_ff", "n_head", "n_head_kv", "head_dim",
                                   "n_rot")] + [("rope_base", _f), ("eps", _f)] + \
                [(n, _i) for n in ("n_vocab", "attn_interval", "d_state", "n_k_head", "n_v_head",
-                                  "d_conv", "kv_block", "max_ctx", "max_batch")]
+                                  "d_conv", "kv_block", "max_ctx", "max_batch", "dense")]
 
 
 _Q2WP = C.POINTER(Q2W)

@@ -53,14 +53,15 @@ __device__ __forceinline__ float rope_dim(int i, float mine, float pv, int n_rot
 
 // ---------------------------------------------------------------- prefill prep
 
-// Attention prep (prefill), one wave per (token, head): q heads take the q
-// half of the fused [q | gate] pair, RMS-normalize it with q_norm and rotate
+// Attention prep (prefill), one wave per (token, head): q heads take their q
+// (the first half of the hybrid's fused [q | gate] pair, qs = 2 HD, or the
+// dense model's plain q, qs = HD), RMS-normalize it with q_norm and rotate
 // it; kv heads normalize + rotate k and append k, v to the f16 cache at the
 // token's position (Attention.swift:79-107).  Lane l holds dims l + 64 s.
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_prep(
-        const float *proj, int64_t stride, const float *q_norm, const float *k_norm, float *q_out,
-        float *gate_out, uint16_t *kc, uint16_t *vc, const int32_t *page_table,
+        const float *proj, int64_t stride, int qs, const float *q_norm, const float *k_norm,
+        float *q_out, float *gate_out, uint16_t *kc, uint16_t *vc, const int32_t *page_table,
         const int32_t *pos_ptr, int N, int H, int HKV, int n_rot, float base, int block, float eps) {
     constexpr int S = HD / 64;
     const int64_t task = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -70,7 +71,7 @@ __global__ __launch_bounds__(256) void k_attn_prep(
     const float *row = proj + (int64_t)n * stride;
     const bool is_q = h < H;
     const int kh = h - H;
-    const float *src = is_q ? row + h * 2 * HD : row + 2 * H * HD + kh * HD;
+    const float *src = is_q ? row + h * qs : row + H * qs + kh * HD;
     const float *nw = is_q ? q_norm : k_norm;
     float x[S], y[S];
     float ss = 0.f;
@@ -105,12 +106,12 @@ __global__ __launch_bounds__(256) void k_attn_prep(
 #pragma unroll
         for (int s = 0; s < S; s++) {
             qo[lane + 64 * s] = r[s];
-            go[lane + 64 * s] = row[h * 2 * HD + HD + lane + 64 * s];
+            if (qs == 2 * HD) go[lane + 64 * s] = row[h * qs + HD + lane + 64 * s];
         }
     } else {
         const int kvDim = HKV * HD;
         const int64_t slot = kv_slot(page_table, pos, block);
-        const float *vs = row + 2 * H * HD + HKV * HD + kh * HD;
+        const float *vs = row + H * qs + HKV * HD + kh * HD;
 #pragma unroll
         for (int s = 0; s < S; s++) {
             kc[slot * kvDim + kh * HD + lane + 64 * s] = gd_f2h(r[s]);
@@ -292,8 +293,9 @@ __global__ __launch_bounds__(256) void k_attn_prefill(
 
 // Decode attention for one query token, split over keys (flash decoding):
 // block (head h, split sp) of 2 HD threads (NWD = HD / 32 waves).
-//   FUSED (the stack): the block prepares its own q from the fused
-//   projection row (split of q|gate, RMS norm, rope; threads 0..HD-1) and the
+//   FUSED (the stack): the block prepares its own q from the projection row
+//   (q of head h at h qs: the q half of a [q | gate] pair when qs = 2 HD,
+//   plain q when qs = HD; RMS norm, rope; threads 0..HD-1) and the
 //   new k and v (threads HD..2HD-1), rounded to f16 as the cache stores them;
 //   the split that holds key pos uses them for that key instead of reading
 //   the cache, and the first q head of each kv group appends them.  No block
@@ -306,9 +308,9 @@ __global__ __launch_bounds__(256) void k_attn_prefill(
 // kernel merges the splits (Attention.swift:108-134).
 template <int HD, bool FUSED>
 __global__ __launch_bounds__(2 * HD) void k_attn_decode(
-        const float *src, const float *q_norm, const float *k_norm, uint16_t *kc, uint16_t *vc,
-        const int32_t *page_table, const int32_t *pos_ptr, int T, int lo, float *part, int H,
-        int HKV, int block, float scale, int n_rot, float base, float eps) {
+        const float *src, int qs, const float *q_norm, const float *k_norm, uint16_t *kc,
+        uint16_t *vc, const int32_t *page_table, const int32_t *pos_ptr, int T, int lo, float *part,
+        int H, int HKV, int block, float scale, int n_rot, float base, float eps) {
     constexpr int NT = 2 * HD, NWD = NT / 64, DPL = HD / 64, WPH = HD / 64;
     constexpr int STEP = DSPLIT * NWD;
     __shared__ float wm[NWD], wl[NWD];
@@ -343,9 +345,9 @@ __global__ __launch_bounds__(2 * HD) void k_attn_decode(
     if constexpr (FUSED) {
         // q of head h (hf = 0) and k of kv head kvh (hf = 1): RMS norm over
         // the head, then the partial NEOX rope, as k_attn_prep.
-        const int H2 = 2 * H * HD;
+        const int H2 = H * qs;
         const int hf = t / HD, i = t % HD;
-        const float x = hf == 0 ? src[h * 2 * HD + i] : src[H2 + kvh * HD + i];
+        const float x = hf == 0 ? src[h * qs + i] : src[H2 + kvh * HD + i];
         const float nw = hf == 0 ? q_norm[i] : k_norm[i];
         const float vx = src[H2 + HKV * HD + kvh * HD + i];
         const float sq = gd_wave_sum(x * x);
@@ -513,18 +515,18 @@ __global__ void k_kv_append(const float *k, const float *v, uint16_t *kc, uint16
 
 // ---------------------------------------------------------------- launchers
 
-int gd_attn_prep_launch(gd_ctx *ctx, int hd, const float *proj, int64_t stride,
+int gd_attn_prep_launch(gd_ctx *ctx, int hd, const float *proj, int64_t stride, int qs,
                         const float *q_norm, const float *k_norm, float *q_out, float *gate_out,
                         uint16_t *kc, uint16_t *vc, const int32_t *page_table,
                         const int32_t *pos_ptr, int N, int H, int HKV, int n_rot, float base,
                         int block, float eps) {
     const dim3 grid(gd_blocks((int64_t)N * (H + HKV), 4));
     if (hd == 128)
-        hipLaunchKernelGGL(k_attn_prep<128>, grid, dim3(256), 0, ctx->stream, proj, stride,
+        hipLaunchKernelGGL(k_attn_prep<128>, grid, dim3(256), 0, ctx->stream, proj, stride, qs,
                            q_norm, k_norm, q_out, gate_out, kc, vc, page_table, pos_ptr, N, H,
                            HKV, n_rot, base, block, eps);
     else
-        hipLaunchKernelGGL(k_attn_prep<256>, grid, dim3(256), 0, ctx->stream, proj, stride,
+        hipLaunchKernelGGL(k_attn_prep<256>, grid, dim3(256), 0, ctx->stream, proj, stride, qs,
                            q_norm, k_norm, q_out, gate_out, kc, vc, page_table, pos_ptr, N, H,
                            HKV, n_rot, base, block, eps);
     GD_LAUNCHED(ctx, "k_attn_prep");
@@ -546,27 +548,29 @@ int gd_attn_prefill_launch(gd_ctx *ctx, int hd, const float *q, const float *gat
     return GD_OK;
 }
 
-// Fused decode (the stack): split + combine into f16 out.
-int gd_attn_decode_launch(gd_ctx *ctx, int hd, const float *proj, const float *q_norm,
+// Fused decode (the stack): split + combine into f16 out.  qs = 2 hd: the
+// hybrid's fused [q | gate] rows, output gated; qs = hd: plain q, ungated.
+int gd_attn_decode_launch(gd_ctx *ctx, int hd, const float *proj, int qs, const float *q_norm,
                           const float *k_norm, uint16_t *kc, uint16_t *vc,
                           const int32_t *page_table, const int32_t *pos_ptr, float *part,
                           uint16_t *out, int H, int HKV, int block, float scale, int n_rot,
                           float base, float eps) {
     const dim3 grid((unsigned)H, DSPLIT);
+    const int gated = qs == 2 * hd;
     if (hd == 128) {
-        hipLaunchKernelGGL((k_attn_decode<128, true>), grid, dim3(256), 0, ctx->stream, proj,
+        hipLaunchKernelGGL((k_attn_decode<128, true>), grid, dim3(256), 0, ctx->stream, proj, qs,
                            q_norm, k_norm, kc, vc, page_table, pos_ptr, 0, 0, part, H, HKV, block,
                            scale, n_rot, base, eps);
         GD_LAUNCHED(ctx, "k_attn_decode");
         hipLaunchKernelGGL((k_attn_combine<128, uint16_t>), dim3(H), dim3(128), 0, ctx->stream,
-                           part, proj + 128, 2 * 128, 1, out);
+                           part, proj + 128, 2 * 128, gated, out);
     } else {
-        hipLaunchKernelGGL((k_attn_decode<256, true>), grid, dim3(512), 0, ctx->stream, proj,
+        hipLaunchKernelGGL((k_attn_decode<256, true>), grid, dim3(512), 0, ctx->stream, proj, qs,
                            q_norm, k_norm, kc, vc, page_table, pos_ptr, 0, 0, part, H, HKV, block,
                            scale, n_rot, base, eps);
         GD_LAUNCHED(ctx, "k_attn_decode");
         hipLaunchKernelGGL((k_attn_combine<256, uint16_t>), dim3(H), dim3(256), 0, ctx->stream,
-                           part, proj + 256, 2 * 256, 1, out);
+                           part, proj + 256, 2 * 256, gated, out);
     }
     GD_LAUNCHED(ctx, "k_attn_combine");
     return GD_OK;
@@ -649,14 +653,14 @@ extern "C" int gd_attn_paged(gd_ctx *ctx, const float *q, const uint16_t *k_cach
     uint16_t *kc = const_cast<uint16_t *>(k_cache), *vc = const_cast<uint16_t *>(v_cache);
     if (hd == 128) {
         hipLaunchKernelGGL((k_attn_decode<128, false>), grid, dim3(256), 0, ctx->stream, q,
-                           nullptr, nullptr, kc, vc, page_table, nullptr, T, lo, part, n_head,
+                           128, nullptr, nullptr, kc, vc, page_table, nullptr, T, lo, part, n_head,
                            n_head_kv, page_size, scale, 0, 0.f, 0.f);
         GD_LAUNCHED(ctx, "gd_attn_paged");
         hipLaunchKernelGGL((k_attn_combine<128, float>), dim3(n_head), dim3(128), 0, ctx->stream,
                            part, gate, 128, gated, out);
     } else {
         hipLaunchKernelGGL((k_attn_decode<256, false>), grid, dim3(512), 0, ctx->stream, q,
-                           nullptr, nullptr, kc, vc, page_table, nullptr, T, lo, part, n_head,
+                           256, nullptr, nullptr, kc, vc, page_table, nullptr, T, lo, part, n_head,
                            n_head_kv, page_size, scale, 0, 0.f, 0.f);
         GD_LAUNCHED(ctx, "gd_attn_paged");
         hipLaunchKernelGGL((k_attn_combine<256, float>), dim3(n_head), dim3(256), 0, ctx->stream,

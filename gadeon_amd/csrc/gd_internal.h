@@ -60,8 +60,10 @@ int gd_gemm_glu(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, uint16_t
 // Attention kernels (attention.hip) for head dims 128 and 256, as the stack
 // launches them: prefill prep (q/k norm + rope + cache append), flash
 // prefill (out f16 or f32), fused decode (prep + split + combine, f16 out),
-// and the size of the decode split partials.
-int gd_attn_prep_launch(gd_ctx *ctx, int hd, const float *proj, int64_t stride,
+// and the size of the decode split partials.  qs is the per-head q stride of
+// the projection rows: 2 hd for fused [q | gate] pairs (gated output), hd
+// for plain q (ungated).
+int gd_attn_prep_launch(gd_ctx *ctx, int hd, const float *proj, int64_t stride, int qs,
                         const float *q_norm, const float *k_norm, float *q_out, float *gate_out,
                         uint16_t *kc, uint16_t *vc, const int32_t *page_table,
                         const int32_t *pos_ptr, int N, int H, int HKV, int n_rot, float base,
@@ -70,7 +72,7 @@ int gd_attn_prefill_launch(gd_ctx *ctx, int hd, const float *q, const float *gat
                            const uint16_t *kc, const uint16_t *vc, const int32_t *page_table,
                            const int32_t *pos_ptr, int pos_add, void *out, int out_dtype, int H,
                            int HKV, int N, int block, float scale, int gated);
-int gd_attn_decode_launch(gd_ctx *ctx, int hd, const float *proj, const float *q_norm,
+int gd_attn_decode_launch(gd_ctx *ctx, int hd, const float *proj, int qs, const float *q_norm,
                           const float *k_norm, uint16_t *kc, uint16_t *vc,
                           const int32_t *page_table, const int32_t *pos_ptr, float *part,
                           uint16_t *out, int H, int HKV, int block, float scale, int n_rot,

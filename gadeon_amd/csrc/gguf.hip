@@ -310,9 +310,10 @@ extern "C" int gd_gguf_stack_config(const gd_gguf *g, gd_stack_config *cfg) {
     std::string arch = "qwen35";
     auto a = g->meta.find("general.architecture");
     if (a != g->meta.end() && a->second.kind == 2) arch = a->second.s;
-    if (arch != "qwen35")
-        return fail("gd_gguf_stack_config: architecture '%s' is not the qwen35 GDN hybrid",
-                    arch.c_str());
+    if (arch != "qwen35" && arch != "qwen3")
+        return fail("gd_gguf_stack_config: architecture '%s' is neither the qwen35 GDN hybrid "
+                    "nor the dense qwen3", arch.c_str());
+    const bool dense = arch == "qwen3";
     auto get = [&](const char *key, bool required, double dflt, double *v) -> bool {
         auto it = g->meta.find(arch + "." + key);
         if (it == g->meta.end() || (it->second.kind != 0 && it->second.kind != 1)) {
@@ -326,22 +327,30 @@ extern "C" int gd_gguf_stack_config(const gd_gguf *g, gd_stack_config *cfg) {
         *v = it->second.kind == 1 ? it->second.f : (double)it->second.i;
         return true;
     };
-    double e, ff, nl, nh, nkv, hd, rot, base, eps, ai, ds, nk, nv, inner, dc;
+    double e, ff, nl, nh, nkv, hd, rot, base, eps;
+    // The dense lineage has every layer attention and no ssm geometry
+    // (Model.swift:55-59); the hybrid reads it.
+    double ai = 1, ds = 0, nk = 0, nv = 0, inner = 0, dc = 0;
     if (!get("embedding_length", true, 0, &e) || !get("feed_forward_length", true, 0, &ff) ||
         !get("block_count", true, 0, &nl) || !get("attention.head_count", true, 0, &nh) ||
         !get("attention.head_count_kv", true, 0, &nkv) ||
         !get("attention.key_length", true, 0, &hd) ||
         !get("rope.dimension_count", false, hd, &rot) || !get("rope.freq_base", true, 0, &base) ||
-        !get("attention.layer_norm_rms_epsilon", true, 0, &eps) ||
-        !get("full_attention_interval", false, 4, &ai) || !get("ssm.state_size", true, 0, &ds) ||
-        !get("ssm.group_count", true, 0, &nk) || !get("ssm.time_step_rank", true, 0, &nv) ||
-        !get("ssm.inner_size", true, 0, &inner) || !get("ssm.conv_kernel", true, 0, &dc))
+        !get("attention.layer_norm_rms_epsilon", true, 0, &eps))
+        return GD_EINVAL;
+    if (!dense &&
+        (!get("full_attention_interval", false, 4, &ai) || !get("ssm.state_size", true, 0, &ds) ||
+         !get("ssm.group_count", true, 0, &nk) || !get("ssm.time_step_rank", true, 0, &nv) ||
+         !get("ssm.inner_size", true, 0, &inner) || !get("ssm.conv_kernel", true, 0, &dc)))
         return GD_EINVAL;
     const double ints[] = {e, ff, nl, nh, nkv, hd, rot, ai, ds, nk, nv, inner, dc};
-    for (double v : ints)
-        if (!(v >= 1 && v < (double)(1 << 30)) || v != (double)(int64_t)v)
+    for (int i = 0; i < (int)(sizeof ints / sizeof ints[0]); i++) {
+        const double v = ints[i];
+        const bool ssm = i >= 8;   // zero on the dense lineage
+        if (!(v >= (dense && ssm ? 0 : 1) && v < (double)(1 << 30)) || v != (double)(int64_t)v)
             return fail("gd_gguf_stack_config: a geometry key holds %s, not a positive integer",
                         std::to_string(v).c_str());
+    }
     auto t = g->tensors.find("token_embd.weight");
     if (t == g->tensors.end() || t->second.ndim != 2)
         return fail("gd_gguf_stack_config: no 2-D tensor token_embd.weight", "");
@@ -368,6 +377,7 @@ extern "C" int gd_gguf_stack_config(const gd_gguf *g, gd_stack_config *cfg) {
     c.n_k_head = (int)nk;
     c.n_v_head = (int)nv;
     c.d_conv = (int)dc;
+    c.dense = dense ? 1 : 0;
     *cfg = c;
     return GD_OK;
 }

@@ -1,6 +1,8 @@
-// A random-init Bonsai-shape hybrid stack: Gated DeltaNet layers with a gated
-// full-attention layer every `attn_interval`-th, each followed by a SwiGLU FFN,
-// all linears Q2_0.  It is the HIP counterpart of the reference's GPU engine
+// A Bonsai-shape stack (random-init, or loaded from a GGUF file): the qwen35
+// hybrid has Gated DeltaNet layers with a gated full-attention layer every
+// `attn_interval`-th; the dense qwen3 lineage (cfg.dense) has plain ungated
+// attention in every layer (Model.swift:1-69).  Each layer is followed by a
+// SwiGLU FFN, all linears Q2_0.  It is the HIP counterpart of the reference's GPU engine
 // (MetalEngine.extend / decode, LLM/src/Metal/MetalEngine.swift:183-296,
 // 367-451, 657-796) and follows the op order of the CPU oracle
 // BonsaiEngine.forward (LLM/src/SIMD/BonsaiEngine.swift:155-178), GDN.step
@@ -9,7 +11,7 @@
 // MI355X layout choices:
 //   * Projections that read the same input are stored as one Q2_0 matrix and
 //     run as one GEMM/GEMV: GDN [qkv | z | beta | alpha], attention
-//     [q|gate | k | v], FFN [gate | up].  Rows of a Q2_0 plane are
+//     [q|gate | k | v] (dense: [q | k | v]), FFN [gate | up].  Rows of a Q2_0 plane are
 //     contiguous, so each original tensor is a row range of the fused one.
 //   * Activations feeding a Q2_0 GEMM/GEMV are written as f16 by the kernel
 //     that produces them (the reference stages GEMM inputs as half,
@@ -571,19 +573,22 @@ int forward(gd_stack *st, int N, bool decode) {
         } else {
             const int hd = c.head_dim;
             const float scale = 1.0f / sqrtf((float)hd);
+            // Per-head q stride of the projection rows: the hybrid's fused
+            // [q | gate] pairs, or the dense model's plain q (ungated).
+            const int qs = c.dense ? hd : 2 * hd;
             if (decode) {
                 // One token: q/k preparation and the cache append happen
                 // inside the attention launch.
-                R_(gd_attn_decode_launch(ctx, hd, st->proj, ly.q_norm, ly.k_norm, ly.kc, ly.vc,
+                R_(gd_attn_decode_launch(ctx, hd, st->proj, qs, ly.q_norm, ly.k_norm, ly.kc, ly.vc,
                                          st->page_table, st->dpos, st->attn_part, st->a16, H, HKV,
                                          c.kv_block, scale, c.n_rot, c.rope_base, eps));
             } else {
-                R_(gd_attn_prep_launch(ctx, hd, st->proj, (int64_t)RP, ly.q_norm, ly.k_norm, st->q32,
+                R_(gd_attn_prep_launch(ctx, hd, st->proj, (int64_t)RP, qs, ly.q_norm, ly.k_norm, st->q32,
                                        st->gate32, ly.kc, ly.vc, st->page_table, st->dpos, N, H,
                                        HKV, c.n_rot, c.rope_base, c.kv_block, eps));
                 R_(gd_attn_prefill_launch(ctx, hd, st->q32, st->gate32, ly.kc, ly.vc,
                                           st->page_table, st->dpos, 0, st->a16, GD_F16, H, HKV, N,
-                                          c.kv_block, scale, 1));
+                                          c.kv_block, scale, c.dense ? 0 : 1));
             }
         }
         // Output projections feed only the residual add: a split-K plan
@@ -673,13 +678,23 @@ int create(gd_ctx *ctx, const gd_stack_config *cfg, uint64_t seed, bool random, 
     GD_REQUIRE(ctx, cfg && out, "gd_stack_create: null argument");
     const gd_stack_config &c = *cfg;
     GD_REQUIRE(ctx, c.n_layer > 0 && c.attn_interval > 0, "gd_stack_create: bad layer count");
-    GD_REQUIRE(ctx, (c.head_dim == 128 || c.head_dim == 256) && c.d_state == HD,
-               "gd_stack_create: head_dim must be 128 or 256 and d_state 128");
-    GD_REQUIRE(ctx, c.d_conv == 4, "gd_stack_create: d_conv must be 4");
+    GD_REQUIRE(ctx, c.dense == 0 || c.dense == 1, "gd_stack_create: dense must be 0 or 1");
+    GD_REQUIRE(ctx, c.head_dim == 128 || c.head_dim == 256,
+               "gd_stack_create: head_dim must be 128 or 256");
+    if (c.dense) {
+        // Every layer attention (Model.swift:55-59): no GDN geometry.
+        GD_REQUIRE(ctx, c.attn_interval == 1 && c.d_state == 0 && c.n_k_head == 0 &&
+                        c.n_v_head == 0 && c.d_conv == 0,
+                   "gd_stack_create: a dense stack has attn_interval 1 and d_state, n_k_head, "
+                   "n_v_head, d_conv 0");
+    } else {
+        GD_REQUIRE(ctx, c.d_state == HD, "gd_stack_create: d_state must be 128");
+        GD_REQUIRE(ctx, c.d_conv == 4, "gd_stack_create: d_conv must be 4");
+        GD_REQUIRE(ctx, c.n_k_head > 0 && c.n_v_head % c.n_k_head == 0,
+                   "gd_stack_create: n_v_head must be a multiple of n_k_head");
+    }
     GD_REQUIRE(ctx, c.n_head > 0 && c.n_head_kv > 0 && c.n_head % c.n_head_kv == 0,
                "gd_stack_create: n_head must be a multiple of n_head_kv");
-    GD_REQUIRE(ctx, c.n_k_head > 0 && c.n_v_head % c.n_k_head == 0,
-               "gd_stack_create: n_v_head must be a multiple of n_k_head");
     GD_REQUIRE(ctx, c.n_rot > 0 && c.n_rot <= c.head_dim && c.n_rot % 2 == 0,
                "gd_stack_create: n_rot");
     GD_REQUIRE(ctx, c.n_embd % 128 == 0 && c.n_ff % 128 == 0 && c.n_vocab > 0,
@@ -694,12 +709,12 @@ int create(gd_ctx *ctx, const gd_stack_config *cfg, uint64_t seed, bool random, 
     st->ctx = ctx;
     st->c = c;
     st->random = random;
-    st->keyDim = HD * c.n_k_head;
-    st->valDim = HD * c.n_v_head;
+    st->keyDim = c.d_state * c.n_k_head;
+    st->valDim = c.d_state * c.n_v_head;
     st->convDim = 2 * st->keyDim + st->valDim;
     st->rp_rec = st->convDim + st->valDim + 2 * c.n_v_head;
     const int hd = c.head_dim;
-    st->rp_att = 2 * c.n_head * hd + 2 * c.n_head_kv * hd;
+    st->rp_att = (c.dense ? 1 : 2) * c.n_head * hd + 2 * c.n_head_kv * hd;
     st->max_pages = (c.max_ctx + c.kv_block - 1) / c.kv_block;
     const int E = c.n_embd, FF = c.n_ff, B = c.max_batch;
     int rc = GD_OK;
@@ -929,7 +944,9 @@ extern "C" int gd_stack_tensor(gd_stack *st, int layer, const char *name, gd_q2w
     GD_REQUIRE(ctx, layer < c.n_layer, "gd_stack_tensor: layer %d out of range", layer);
     StackLayer &ly = st->L[layer];
     if (n == "attn_norm") return f(ly.attn_norm, c.n_embd);
-    if (n == "post_attention_norm") return f(ly.post_norm, c.n_embd);
+    // The pre-FFN norm: the dense lineage's file calls it ffn_norm
+    // (Model.swift:103-106).
+    if (n == (c.dense ? "ffn_norm" : "post_attention_norm")) return f(ly.post_norm, c.n_embd);
     if (n == "ffn_gate") return q(ly.gate_up, 0, c.n_ff);
     if (n == "ffn_up") return q(ly.gate_up, c.n_ff, 2 * (int64_t)c.n_ff);
     if (n == "ffn_down") return q(ly.down);
@@ -947,7 +964,8 @@ extern "C" int gd_stack_tensor(gd_stack *st, int layer, const char *name, gd_q2w
         if (n == "ssm_conv_state") return f(ly.conv_state, (int64_t)3 * cd);
         if (n == "ssm_state") return f(ly.rec_state, (int64_t)nv * HD * HD);
     } else {
-        const int hd = c.head_dim, qf = 2 * c.n_head * hd, kv = c.n_head_kv * hd;
+        const int hd = c.head_dim, qf = (c.dense ? 1 : 2) * c.n_head * hd,
+                  kv = c.n_head_kv * hd;
         if (n == "attn_q") return q(ly.in_proj, 0, qf);
         if (n == "attn_k") return q(ly.in_proj, qf, qf + kv);
         if (n == "attn_v") return q(ly.in_proj, qf + kv, qf + 2 * kv);
@@ -964,8 +982,7 @@ namespace {
 
 // Tensors the stack reads, by the short names of gd_stack_tensor, for one
 // layer kind (Model.swift:100-130) and for the whole model (:139-145).
-const char *const k_common[] = {"attn_norm", "post_attention_norm", "ffn_gate", "ffn_up",
-                                "ffn_down"};
+const char *const k_common[] = {"attn_norm", "ffn_gate", "ffn_up", "ffn_down"};
 const char *const k_rec[] = {"attn_qkv", "attn_gate", "ssm_beta", "ssm_alpha", "ssm_out",
                              "ssm_conv1d", "ssm_dt", "ssm_a", "ssm_norm"};
 const char *const k_att[] = {"attn_q", "attn_k", "attn_v", "attn_output", "attn_q_norm",
@@ -988,6 +1005,7 @@ std::vector<Item> load_list(const gd_stack *st) {
     if (st->head.codes != st->embd.codes) v.push_back({-1, "output"});
     for (int il = 0; il < st->c.n_layer; il++) {
         for (const char *n : k_common) v.push_back({il, n});
+        v.push_back({il, st->c.dense ? "ffn_norm" : "post_attention_norm"});
         if (st->L[il].rec)
             for (const char *n : k_rec) v.push_back({il, n});
         else
@@ -1118,7 +1136,7 @@ BmLayout bm_layout(const gd_stack *st, int64_t pos) {
 }
 
 bool same_geometry(const gd_stack_config &a, const gd_stack_config &b) {
-    return a.n_layer == b.n_layer && a.attn_interval == b.attn_interval &&
+    return a.n_layer == b.n_layer && a.attn_interval == b.attn_interval && a.dense == b.dense &&
            a.n_embd == b.n_embd && a.d_conv == b.d_conv && a.n_k_head == b.n_k_head &&
            a.n_v_head == b.n_v_head && a.d_state == b.d_state && a.n_head_kv == b.n_head_kv &&
            a.head_dim == b.head_dim;

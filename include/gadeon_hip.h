@@ -412,10 +412,11 @@ int gd_rand_normal(gd_ctx *ctx, void *out, int dtype, size_t n, uint64_t seed,
  * `seed`), scales RNE-f16 of lo + (hi-lo)*u over stream seed+1. */
 int gd_rand_q2w(gd_ctx *ctx, gd_q2w *w, uint64_t seed, float lo, float hi);
 
-/* ---- Bonsai-shape hybrid stack (config 4) --------------------------------------
- * A random-init 64-layer GDN/attention hybrid driven exactly like
- * MetalEngine.extend / decode (MetalEngine.swift:183-257, 657-728) and the
- * CPU oracle BonsaiEngine.forward (BonsaiEngine.swift:155-178). */
+/* ---- Bonsai-shape stack (config 4) -----------------------------------------------
+ * A GDN/attention hybrid (qwen35, e.g. the random-init 64-layer config 4) or
+ * a dense all-attention qwen3 stack, driven exactly like MetalEngine.extend /
+ * decode (MetalEngine.swift:183-257, 405-451, 657-796) and the CPU oracle
+ * BonsaiEngine.forward (BonsaiEngine.swift:155-178). */
 typedef struct gd_stack_config {
     int n_layer;        /* 64 */
     int n_embd;         /* 5120 */
@@ -435,6 +436,10 @@ typedef struct gd_stack_config {
     int kv_block;       /* 16 positions per KV page */
     int max_ctx;        /* KV capacity in positions */
     int max_batch;      /* largest prefill chunk (tokens) */
+    int dense;          /* 0: qwen35 hybrid; 1: dense qwen3 lineage (BonsaiConfig.dense,
+                           Model.swift:23-25): attention in every layer
+                           (attn_interval 1), q projected without a gate, output
+                           ungated; d_state, n_k_head, n_v_head, d_conv 0 */
 } gd_stack_config;
 
 typedef struct gd_stack gd_stack;
@@ -531,8 +536,11 @@ int gd_gguf_get_bool(const gd_gguf *g, const char *key, int *v);
 int gd_gguf_get_string(const gd_gguf *g, const char *key, const char **v);
 int gd_gguf_get_ints(const gd_gguf *g, const char *key, const int64_t **v, int64_t *n);
 int gd_gguf_get_floats(const gd_gguf *g, const char *key, const double **v, int64_t *n);
-/* BonsaiConfig(gguf) (Model.swift:39-69) for the qwen35 hybrid; kv_block,
- * max_ctx and max_batch are left 0 (they are runtime choices). */
+/* BonsaiConfig(gguf) (Model.swift:39-69): general.architecture "qwen35" (the
+ * default when absent) gives the hybrid, "qwen3" the dense lineage (dense 1,
+ * attn_interval 1, no ssm keys read); rope.dimension_count defaults to
+ * key_length.  kv_block, max_ctx and max_batch are left 0 (they are runtime
+ * choices). */
 int gd_gguf_stack_config(const gd_gguf *g, gd_stack_config *cfg);
 /* BonsaiModel(path:) + upload (Model.swift:133-148, MetalContext.swift:
  * 146-191): a stack whose weights are the file's tensors, repacked into the

@@ -244,7 +244,7 @@ class OrStack(C.Structure):
     _fields_ = [(n, _i) for n in ("n_layer", "n_embd", "n_ff", "n_head", "n_head_kv", "head_dim",
                                   "n_rot")] + [("rope_base", _f), ("eps", _f)] + \
                [(n, _i) for n in ("n_vocab", "d_state", "n_k_head", "n_v_head", "d_conv",
-                                  "max_ctx", "stage_f16", "threads")] + \
+                                  "max_ctx", "stage_f16", "threads", "dense")] + \
                [("layers", C.POINTER(OrStackLayer)), ("embd", _vp), ("out_norm", _vp),
                 ("head", _vp)]
 
@@ -265,7 +265,10 @@ class Stack:
     GPU prefill GEMM stages half tiles, Kernels.metal:428) and `token` does not
     (its decode GEMV reads f32 x, Kernels.metal:32-40) unless decode_f16 is
     set; cached K/V are always rounded (half KV pages).  With untied the
-    lm_head is tensors(-1, "output"), else the token embedding (Model.swift:145)."""
+    lm_head is tensors(-1, "output"), else the token embedding (Model.swift:145).
+    cfg["dense"] (default 0) selects the dense qwen3 lineage: every layer
+    attention, plain q, ungated output, the pre-FFN norm named ffn_norm
+    (Model.swift:23-25, 103-106)."""
 
     Q2 = {"rec": ("attn_qkv", "attn_gate", "ssm_beta", "ssm_alpha", "ssm_out"),
           "att": ("attn_q", "attn_k", "attn_v", "attn_output")}
@@ -290,7 +293,8 @@ class Stack:
             L = self.layers[il]
             L.rec = 1 if (il + 1) % cfg["attn_interval"] != 0 else 0
             get = lambda name: ptr(tensors(il, name))
-            L.attn_norm, L.post_norm = get("attn_norm"), get("post_attention_norm")
+            L.attn_norm = get("attn_norm")
+            L.post_norm = get("ffn_norm" if cfg.get("dense") else "post_attention_norm")
             L.ffn_gate, L.ffn_up, L.ffn_down = get("ffn_gate"), get("ffn_up"), get("ffn_down")
             if L.rec:
                 L.wqkv, L.wgate, L.wbeta, L.walpha, L.ssm_out = (get(x) for x in self.Q2["rec"])
@@ -310,6 +314,7 @@ class Stack:
             setattr(st, k, cfg[k])
         st.stage_f16 = self.stage_decode
         st.threads = threads
+        st.dense = 1 if cfg.get("dense") else 0
         st.layers = self.layers
         st.embd = ptr(tensors(-1, "token_embd"))
         st.out_norm = ptr(tensors(-1, "output_norm"))

@@ -89,8 +89,8 @@ void or_gdn_decode_batch(int B, int nV, int nK, int dS, float *q, float *k, cons
                          const float *g, const float *beta, float *S, float *o, float qScale,
                          float eps, int threads);
 
-/* ---- hybrid stack (BonsaiEngine.swift:134-191, GDN.swift:20-120,
- *      Attention.swift:72-139) ------------------------------------------------- */
+/* ---- Bonsai stack: the qwen35 hybrid or the dense qwen3 lineage
+ *      (BonsaiEngine.swift:134-191, GDN.swift:20-120, Attention.swift:72-139) -- */
 typedef struct or_stack_layer {
     int rec;                                    /* 1 = GDN layer, 0 = attention */
     const float *attn_norm, *post_norm;
@@ -109,6 +109,7 @@ typedef struct or_stack {
     int n_vocab, d_state, n_k_head, n_v_head, d_conv, max_ctx;
     int stage_f16;     /* OR_STAGE_* bits: f16 rounding as the reference GPU path does */
     int threads;
+    int dense;         /* 1: the dense qwen3 lineage (plain q, ungated attention) */
     or_stack_layer *layers;
     const uint8_t *embd;                        /* token_embd */
     const float *out_norm;

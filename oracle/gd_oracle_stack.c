@@ -95,18 +95,20 @@ static void gdn_layer(or_stack *st, or_stack_layer *L, int T, const float *nrm, 
 }
 
 /* The attention part of Attn.step (Attention.swift:79-134) for one token at
- * position pos, from its projections qFull [2 nH hd] (per head q | gate), k, v
- * [nKV hd] to the gated output ao [nH hd] (the input of wo).  The KV cache is
- * held contiguously by position. */
+ * position pos, from its projections qFull (hybrid: [2 nH hd], per head
+ * q | gate; dense: [nH hd], plain q), k, v [nKV hd] to the output ao [nH hd]
+ * (the input of wo), gated by sigmoid(gate) on the hybrid only
+ * (Attention.swift:81-93, 132-134).  The KV cache is held contiguously by
+ * position. */
 static void attn_token(or_stack *st, or_stack_layer *L, const float *qFull, float *k, float *v,
                        int pos, float *ao) {
     const int hd = st->head_dim, nH = st->n_head, nKV = st->n_head_kv;
-    const int group = nH / nKV, kvDim = hd * nKV;
+    const int group = nH / nKV, kvDim = hd * nKV, qs = st->dense ? hd : 2 * hd;
     float *q = malloc(sizeof(float) * hd * nH), *gate = malloc(sizeof(float) * hd * nH);
     for (int h = 0; h < nH; h++)
         for (int i = 0; i < hd; i++) {
-            q[h * hd + i] = qFull[h * hd * 2 + i];
-            gate[h * hd + i] = qFull[h * hd * 2 + hd + i];
+            q[h * hd + i] = qFull[h * qs + i];
+            gate[h * hd + i] = st->dense ? 0 : qFull[h * qs + hd + i];
         }
     or_rmsnorm_rows(q, hd, nH, L->q_norm, st->eps);
     or_rmsnorm_rows(k, hd, nKV, L->k_norm, st->eps);
@@ -133,7 +135,8 @@ static void attn_token(or_stack *st, or_stack_layer *L, const float *qFull, floa
             for (int i = 0; i < hd; i++) ao[h * hd + i] += w * vt[i];
         }
     }
-    for (int i = 0; i < hd * nH; i++) ao[i] *= or_sigmoid(gate[i]);
+    if (!st->dense)
+        for (int i = 0; i < hd * nH; i++) ao[i] *= or_sigmoid(gate[i]);
     free(q); free(gate); free(scores);
 }
 
@@ -142,7 +145,7 @@ static void attn_token(or_stack *st, or_stack_layer *L, const float *qFull, floa
 static void attn_layer(or_stack *st, or_stack_layer *L, int T, const float *nrm, int pos0,
                        float *out) {
     const int hd = st->head_dim, nH = st->n_head, nKV = st->n_head_kv, E = st->n_embd;
-    const int kvDim = hd * nKV, qf = hd * 2 * nH;
+    const int kvDim = hd * nKV, qf = hd * (st->dense ? 1 : 2) * nH;
     float *qFull = malloc(sizeof(float) * qf * T), *k = malloc(sizeof(float) * kvDim * T);
     float *v = malloc(sizeof(float) * kvDim * T), *ao = malloc(sizeof(float) * hd * nH * T);
     if (T == 1) {

@@ -69,9 +69,14 @@ def write(path: Path | str, kvs, tensors, alignment: int = 32, version: int = 3)
     return path
 
 
-def stack_kvs(cfg: dict, arch: str = "qwen35", drop=()) -> list:
+def stack_kvs(cfg: dict, arch: str | None = None, drop=()) -> list:
     """The metadata BonsaiConfig reads for a stack of geometry cfg (the
-    gd_stack_config field names).  Keys named in `drop` are left out."""
+    gd_stack_config field names): "qwen35" keys, or for cfg["dense"] the
+    dense lineage's "qwen3" keys, which have no ssm geometry, no attention
+    interval and no rope.dimension_count (Model.swift:45-59).  Keys named in
+    `drop` are left out."""
+    dense = bool(cfg.get("dense"))
+    arch = arch or ("qwen3" if dense else "qwen35")
     a = arch + "."
     kvs = [("general.architecture", STR, arch),
            (a + "embedding_length", U32, cfg["n_embd"]),
@@ -81,16 +86,19 @@ def stack_kvs(cfg: dict, arch: str = "qwen35", drop=()) -> list:
            (a + "attention.head_count_kv", U32, cfg["n_head_kv"]),
            (a + "attention.key_length", U32, cfg["head_dim"]),
            (a + "attention.value_length", U32, cfg["head_dim"]),
-           (a + "rope.dimension_count", U32, cfg["n_rot"]),
-           (a + "rope.dimension_sections", ARR, (I32, [11, 11, 10, 0])),
            (a + "rope.freq_base", F32, cfg["rope_base"]),
-           (a + "attention.layer_norm_rms_epsilon", F32, cfg["eps"]),
-           (a + "full_attention_interval", U32, cfg["attn_interval"]),
-           (a + "ssm.state_size", U32, cfg["d_state"]),
-           (a + "ssm.group_count", U32, cfg["n_k_head"]),
-           (a + "ssm.time_step_rank", U32, cfg["n_v_head"]),
-           (a + "ssm.inner_size", U32, cfg["d_state"] * cfg["n_v_head"]),
-           (a + "ssm.conv_kernel", U32, cfg["d_conv"])]
+           (a + "attention.layer_norm_rms_epsilon", F32, cfg["eps"])]
+    if dense:
+        assert cfg["n_rot"] == cfg["head_dim"], "the dense file rotates whole heads"
+        return [kv for kv in kvs if kv[0] not in drop]
+    kvs += [(a + "rope.dimension_count", U32, cfg["n_rot"]),
+            (a + "rope.dimension_sections", ARR, (I32, [11, 11, 10, 0])),
+            (a + "full_attention_interval", U32, cfg["attn_interval"]),
+            (a + "ssm.state_size", U32, cfg["d_state"]),
+            (a + "ssm.group_count", U32, cfg["n_k_head"]),
+            (a + "ssm.time_step_rank", U32, cfg["n_v_head"]),
+            (a + "ssm.inner_size", U32, cfg["d_state"] * cfg["n_v_head"]),
+            (a + "ssm.conv_kernel", U32, cfg["d_conv"])]
     return [kv for kv in kvs if kv[0] not in drop]
 
 

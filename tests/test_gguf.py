@@ -1,6 +1,7 @@
 """The library's GGUF v3 reader (gd_gguf_*, host only, no device): metadata of
 every value type, tensor placement under the default and a custom alignment,
-the qwen35 geometry BonsaiConfig reads, and corrupt files as errors.  Follows
+the qwen35 and qwen3 geometries BonsaiConfig reads, and corrupt files as
+errors.  Follows
 LLM/src/Shared/GGUF.swift:45-284 and Model.swift:39-69."""
 import struct
 
@@ -113,6 +114,33 @@ def test_stack_config_from_metadata(tmp_path, lib):
     assert c.n_rot == cfg["head_dim"] and c.attn_interval == 4
 
 
+def test_dense_stack_config(tmp_path, lib):
+    """general.architecture "qwen3": the dense lineage (Model.swift:41-59) --
+    every layer attention, no ssm geometry read (none in the file), the whole
+    head rotated when rope.dimension_count is absent."""
+    cfg = dict(STACK_CFG, dense=1, attn_interval=1, d_state=0, n_k_head=0, n_v_head=0,
+               d_conv=0, n_rot=128, rope_base=1e6)
+    emb = np.zeros((cfg["n_vocab"], 2 * 34), np.uint8)
+    ts = [("token_embd.weight", [256, cfg["n_vocab"]], W.GGML_Q2_0, emb.tobytes())]
+    kvs = W.stack_kvs(cfg)
+    assert not any(".ssm." in k or "rope.dimension_count" in k for k, _, _ in kvs)
+    path = W.write(tmp_path / "dense.gguf", kvs, ts)
+    with ga.GGUF(path) as g:
+        c = g.stack_config()
+    for k, v in cfg.items():
+        assert getattr(c, k) == pytest.approx(v, rel=1e-7), k
+    # An explicit rope.dimension_count is honoured on the dense lineage too.
+    path = W.write(tmp_path / "dense_rot.gguf",
+                   kvs + [("qwen3.rope.dimension_count", W.U32, 64)], ts)
+    with ga.GGUF(path) as g:
+        assert g.stack_config().n_rot == 64
+    # The hybrid needs its ssm keys; a qwen35 file without them is rejected.
+    path = W.write(tmp_path / "no_ssm.gguf", W.stack_kvs(cfg, arch="qwen35"), ts)
+    with ga.GGUF(path) as g:
+        with pytest.raises(ga.GDError, match="missing numeric key qwen35"):
+            g.stack_config()
+
+
 @pytest.mark.parametrize("case", ["arch", "missing", "inner", "width", "nonint"])
 def test_stack_config_rejects(tmp_path, lib, case):
     rng = np.random.default_rng(3)
@@ -120,7 +148,7 @@ def test_stack_config_rejects(tmp_path, lib, case):
     width = 384 if case == "width" else 256
     emb = np.zeros((STACK_CFG["n_vocab"], width // 128 * 34), np.uint8) if case == "width" else emb
     ts = [("token_embd.weight", [width, STACK_CFG["n_vocab"]], W.GGML_Q2_0, emb.tobytes())]
-    kvs = W.stack_kvs(STACK_CFG, arch="qwen3" if case == "arch" else "qwen35",
+    kvs = W.stack_kvs(STACK_CFG, arch="llama" if case == "arch" else "qwen35",
                       drop=("qwen35.ssm.state_size",) if case == "missing" else ())
     if case == "inner":
         kvs = [(k, t, 1000 if k.endswith("inner_size") else v) for k, t, v in kvs]
@@ -128,7 +156,7 @@ def test_stack_config_rejects(tmp_path, lib, case):
         kvs = [(k, W.F32 if k.endswith("block_count") else t, 2.5 if k.endswith("block_count")
                 else v) for k, t, v in kvs]
     path = W.write(tmp_path / "e.gguf", kvs, ts)
-    msg = {"arch": "qwen35", "missing": "state_size", "inner": "inner_size", "width": "width",
+    msg = {"arch": "neither the qwen35", "missing": "state_size", "inner": "inner_size", "width": "width",
            "nonint": "positive integer"}[case]
     with ga.GGUF(path) as g:
         with pytest.raises(ga.GDError, match=msg):

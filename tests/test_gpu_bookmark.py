@@ -16,7 +16,7 @@ import numpy as np
 import pytest
 
 import gadeon_amd as ga
-from test_gpu_stack import CFG, make_stack, tensor_reader
+from test_gpu_stack import CFG, DENSE, make_stack, tensor_reader
 
 pytestmark = pytest.mark.gpu
 
@@ -154,9 +154,13 @@ def parse(data: bytes, cfg):
     return pos, shift, conv, rec, kv
 
 
-def test_serialize_format_and_round_trip(ctx):
-    cfg, st = make_stack(ctx, seed=23)
-    _, st2 = make_stack(ctx, seed=23)
+@pytest.mark.parametrize("dense", [False, True])
+def test_serialize_format_and_round_trip(ctx, dense):
+    """dense: the qwen3 lineage's bookmark has empty conv and rec dictionaries
+    and a K/V entry for every layer."""
+    over = DENSE if dense else {}
+    cfg, st = make_stack(ctx, seed=23, **over)
+    _, st2 = make_stack(ctx, seed=23, **over)
     bm = bm2 = None
     try:
         ids = (np.arange(37) * 13 % cfg["n_vocab"]).astype(np.int32)   # a partial KV page

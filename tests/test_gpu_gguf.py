@@ -4,7 +4,9 @@ BonsaiModel(path:) + upload (Model.swift:133-148, MetalContext.swift:146-191).
 A seeded random stack is exported tensor by tensor under the reference's
 names (Model.swift:100-145) into a GGUF v3 file written by tests/gguf_writer;
 the stack loaded from that file must hold byte-identical weights and give
-bit-identical logits, picks and generations (same kernels on the same bytes).
+bit-identical logits, picks and generations (same kernels on the same bytes),
+for the qwen35 hybrid and for the dense qwen3 lineage (its own metadata keys
+and its ffn_norm name).
 With an output.weight in the file the lm_head is that matrix (the untied
 branch of Model.swift:145), checked against the CPU oracle.  Files that lack
 a tensor or hold one of the wrong type or shape are rejected by name."""
@@ -16,12 +18,12 @@ import pytest
 import gadeon_amd as ga
 import oracle as O
 from conftest import rel_diff
-from test_gpu_stack import CFG, THREADS, TOL, make_stack, tensor_reader
+from test_gpu_stack import CFG, DENSE, THREADS, TOL, make_stack, tensor_reader
 from tests import gguf_writer as W
 
 pytestmark = pytest.mark.gpu
 
-COMMON = ("attn_norm", "post_attention_norm", "ffn_gate", "ffn_up", "ffn_down")
+COMMON = ("attn_norm", "ffn_gate", "ffn_up", "ffn_down")
 REC = ("attn_qkv", "attn_gate", "ssm_beta", "ssm_alpha", "ssm_out", "ssm_conv1d", "ssm_dt",
        "ssm_a", "ssm_norm")
 ATT = ("attn_q", "attn_k", "attn_v", "attn_output", "attn_q_norm", "attn_k_norm")
@@ -47,7 +49,8 @@ def export(ctx, cfg, st):
     put(-1, "output_norm")
     for il in range(cfg["n_layer"]):
         rec = (il + 1) % cfg["attn_interval"] != 0
-        for name in COMMON + (REC if rec else ATT):
+        post = "ffn_norm" if cfg.get("dense") else "post_attention_norm"
+        for name in COMMON + (post,) + (REC if rec else ATT):
             put(il, name)
     return out
 
@@ -79,8 +82,9 @@ def run(ctx, st, ids, n_dec=3, n_gen=4):
     return out, picks, list(gen)
 
 
-def test_gguf_round_trip_is_bit_identical(ctx, tmp_path):
-    cfg, a = make_stack(ctx, seed=11)
+@pytest.mark.parametrize("dense", [False, True])
+def test_gguf_round_trip_is_bit_identical(ctx, tmp_path, dense):
+    cfg, a = make_stack(ctx, seed=11, **(DENSE if dense else {}))
     b = None
     try:
         tensors = export(ctx, cfg, a)
@@ -89,8 +93,9 @@ def test_gguf_round_trip_is_bit_identical(ctx, tmp_path):
         with ga.GGUF(path) as g:
             c = g.stack_config()
             for k in ("n_layer", "n_embd", "n_ff", "n_head", "n_head_kv", "head_dim", "n_rot",
-                      "n_vocab", "attn_interval", "d_state", "n_k_head", "n_v_head", "d_conv"):
-                assert getattr(c, k) == cfg[k], k
+                      "n_vocab", "attn_interval", "d_state", "n_k_head", "n_v_head", "d_conv",
+                      "dense"):
+                assert getattr(c, k) == cfg.get(k, 0), k
         b = load(ctx, path, cfg)
         # The loaded stack holds the file's bytes (repack, then export back).
         loaded = export(ctx, cfg, b)

@@ -12,7 +12,11 @@ Geometries:
     5120, FFN 17408, 40 q / 8 kv heads of 128, 16/16 GDN heads, vocab 151936,
     kv pages of 16 -- with 4 layers (3 GDN + 1 attention), one 512-token
     prefill chunk (the T=512 GEMM plans, split-K partials, two-launch SwiGLU),
-    then decode and generate steps.
+    then decode and generate steps;
+  * dense: the qwen3 lineage (Model.swift:1-69; every layer plain ungated
+    attention with the whole head rotated), small and at the reference 1.7B's
+    per-layer geometry (hidden 2048, FFN 6144, 16 q / 8 kv heads of 128,
+    vocab 151936) with 4 of its 28 layers.
 
 The oracle's prefill rounds every mat-vec input to f16, as the reference
 GPU prefill GEMM stages half tiles (Kernels.metal:428); this build does the
@@ -46,6 +50,12 @@ CFG = dict(n_layer=4, n_embd=256, n_ff=512, n_head=4, n_head_kv=2, head_dim=128,
 CONFIG4 = dict(n_layer=4, n_embd=5120, n_ff=17408, n_head=40, n_head_kv=8, head_dim=128,
                n_rot=64, rope_base=1e7, eps=1e-6, n_vocab=151936, attn_interval=4, d_state=128,
                n_k_head=16, n_v_head=16, d_conv=4, kv_block=16, max_ctx=544, max_batch=512)
+# The dense qwen3 lineage: no GDN geometry, attention in every layer, the
+# whole head rotated.
+DENSE = dict(dense=1, attn_interval=1, d_state=0, n_k_head=0, n_v_head=0, d_conv=0, n_rot=128,
+             rope_base=1e6)
+DENSE_1P7B = dict(DENSE, n_layer=4, n_embd=2048, n_ff=6144, n_head=16, n_head_kv=8,
+                  head_dim=128, n_vocab=151936, kv_block=16, max_ctx=256, max_batch=128)
 TOL = 5e-3          # logits
 TOL_STATE = 2e-3    # GDN recurrent state and conv ring (the last three in_proj rows)
 TOL_STATE_F32 = 5e-3  # the same against f32 decode inputs (this build decodes in f16)
@@ -235,6 +245,31 @@ def test_stack_config4_geometry(ctx):
         ctx.lib.gd_stack_destroy(st)
 
 
+def test_stack_dense(ctx):
+    """The dense lineage's attention path (plain q rows, ungated prefill and
+    decode, whole-head rope) through prefill over two chunks, decode and
+    generate, reset and chained decode."""
+    cfg, st = make_stack(ctx, seed=31, max_batch=32, **DENSE)
+    try:
+        ids = (np.arange(45) * 41 % cfg["n_vocab"]).astype(np.int32)
+        print("\nstack dense, 4 attention layers, prompt 45", flush=True)
+        run_parity(ctx, cfg, st, ids, n_decode=6, n_gen=5)
+    finally:
+        ctx.lib.gd_stack_destroy(st)
+
+
+def test_stack_dense_1p7b_geometry(ctx):
+    """The reference 1.7B's per-layer geometry (Model.swift:5-7) with 4 of its
+    28 layers: a 128-id prompt in one chunk, 6 decode and 6 generate steps."""
+    cfg, st = make_stack(ctx, seed=32, **DENSE_1P7B)
+    try:
+        ids = np.random.default_rng(17).integers(0, cfg["n_vocab"], 128).astype(np.int32)
+        print("\nstack dense 1.7B geometry, 4 layers, prompt 128", flush=True)
+        run_parity(ctx, cfg, st, ids, n_decode=6, n_gen=6, chain=False)
+    finally:
+        ctx.lib.gd_stack_destroy(st)
+
+
 def test_stack_rejects_bad_input(ctx):
     cfg, st = make_stack(ctx, n_layer=4)
     lib = ctx.lib
@@ -252,3 +287,8 @@ def test_stack_rejects_bad_input(ctx):
     sc = ga.StackConfig(**dict(CFG, head_dim=64))
     h = C.c_void_p()
     assert lib.gd_stack_create(ctx.h, C.byref(sc), 1, C.byref(h)) == ga.GD_EINVAL
+    # A dense stack has attention in every layer and no GDN geometry.
+    for bad in (dict(DENSE, attn_interval=4), dict(DENSE, d_state=128), dict(DENSE, dense=2)):
+        sc = ga.StackConfig(**dict(CFG, **bad))
+        assert lib.gd_stack_create(ctx.h, C.byref(sc), 1, C.byref(h)) == ga.GD_EINVAL
+        assert b"dense" in lib.gd_last_error(ctx.h)

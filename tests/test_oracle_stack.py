@@ -153,6 +153,59 @@ def test_attention_first_position_is_gated_value():
     assert np.allclose(h, want, rtol=2e-5, atol=2e-5)
 
 
+DCFG = dict(CFG, dense=1, n_rot=128, rope_base=1e6, d_state=0, n_k_head=0, n_v_head=0,
+            d_conv=0)
+
+
+def make_dense_tensors(cfg, zero=("ffn_down",)):
+    """The dense lineage's layer: q without a gate (wq [E, nh hd]) and the
+    pre-FFN norm named ffn_norm (Model.swift:100-130)."""
+    T = make_tensors(cfg, zero)
+    E, hd, nh = cfg["n_embd"], cfg["head_dim"], cfg["n_head"]
+    T["attn_q"] = q2_blocks(E, nh * hd, 150)
+    T["ffn_norm"] = T.pop("post_attention_norm")
+    return T
+
+
+def test_dense_attention_is_ungated_softmax_attention():
+    """The dense branch of Attn.step (Attention.swift:81-83, 132-134) over two
+    positions, against a direct numpy statement: plain q from wq, q/k RMS
+    norms, full-head NEOX rope at each position, softmax over the cached keys
+    and no output gate; with ffn_down = 0 the hidden state is x + wo . ao.
+    At position 0 the attention output is the value itself."""
+    cfg = dict(DCFG)
+    T = make_dense_tensors(cfg)
+    st = stack_of(cfg, T)
+    E, hd, nh, nkv = cfg["n_embd"], cfg["head_dim"], cfg["n_head"], cfg["n_head_kv"]
+    eps, rot, base = cfg["eps"], cfg["n_rot"], cfg["rope_base"]
+    keys, vals = [], []
+    for pos, tok in enumerate((11, 40)):
+        h, _ = st.token(tok)
+        x = O.q2_0_dequant(T["token_embd"][tok * E // 128 * 34:(tok + 1) * E // 128 * 34], E)
+        n = O.rmsnorm(x, T["attn_norm"], eps)
+        q = mv(T, "attn_q", E, nh * hd, n).reshape(nh, hd).astype(np.float64)
+        k = mv(T, "attn_k", E, nkv * hd, n).reshape(nkv, hd).astype(np.float64)
+        v = mv(T, "attn_v", E, nkv * hd, n).reshape(nkv, hd).astype(np.float64)
+        rms = lambda a, w: a / np.sqrt((a * a).mean(axis=1, keepdims=True) + eps) * w
+        q, k = rms(q, T["attn_q_norm"]), rms(k, T["attn_k_norm"])
+        q = O.rope_neox(q.astype(np.float32).reshape(-1), hd, rot, base, pos).reshape(nh, hd)
+        k = O.rope_neox(k.astype(np.float32).reshape(-1), hd, rot, base, pos).reshape(nkv, hd)
+        keys.append(k.astype(np.float64))
+        vals.append(v)
+        ao = np.empty((nh, hd))
+        for hh in range(nh):
+            g = hh // (nh // nkv)
+            s = np.array([q[hh] @ kk[g] for kk in keys]) / np.sqrt(hd)
+            p = np.exp(s - s.max())
+            p /= p.sum()
+            ao[hh] = sum(pi * vv[g] for pi, vv in zip(p, vals))
+        if pos == 0:
+            assert np.allclose(ao, v[np.arange(nh) // (nh // nkv)])
+        a = mv(T, "attn_output", nh * hd, E, ao.reshape(-1))
+        want = O.rmsnorm((x + a).astype(np.float32), T["output_norm"], eps)
+        assert np.allclose(h, want, rtol=5e-5, atol=5e-5), pos
+
+
 GCFG = dict(n_layer=1, n_embd=256, n_ff=256, n_head=4, n_head_kv=2, head_dim=128, n_rot=64,
             rope_base=1e7, eps=1e-6, n_vocab=64, attn_interval=9, d_state=128, n_k_head=1,
             n_v_head=2, d_conv=4, max_ctx=8)
