@@ -36,8 +36,10 @@ int gd_ctx_workspace(gd_ctx *ctx, size_t bytes, void **out);
 // Map a HIP error to a GD code with a message naming `what`.
 int gd_hip_fail(gd_ctx *ctx, hipError_t e, const char *what);
 // Matrix-core GEMV (checked by the caller); ksplit > 1 writes K-split partial
-// rows to y + z * R.
-int gd_gemv_mfma(gd_ctx *ctx, const gd_q2w *w, const void *x, int x_dtype, float *y, int ksplit);
+// rows to y + z * R.  bias (if not null, f32 [R]) is added to the rows of
+// split 0.
+int gd_gemv_mfma(gd_ctx *ctx, const gd_q2w *w, const void *x, int x_dtype, float *y, int ksplit,
+                 const float *bias = nullptr);
 // GEMV of x = f16(rmsnorm(h + sum of nd delta partials) * normw); hout <- the
 // sum if not null.
 // glu_out (if not null): w = [gate; up] and glu_out = f16(silu(gate x) * up x)

@@ -124,6 +124,7 @@ struct Task {
     const uint16_t *scales;
     const void *x;
     float *y;
+    const float *bias;       // added to the rows of K range 0 (null: none)
     int K, R, nsets, per, ksteps, nz, gx;
     NormIn nin;
     GluOut glu;
@@ -280,6 +281,13 @@ __device__ void run(const Task &t, int wg, uint32_t *lds) {
         return c;
     };
     XChunk<XT> xc = load_x(threadIdx.x);
+    // The bias of this thread's row in the first pass of the row sums at the
+    // end (K range 0 only), requested with x so its latency is hidden.
+    const __amdgpu_buffer_rsrc_t brs = make_rsrc(t.bias, t.bias && g.bz == 0 ? (uint32_t)R * 4u : 0u);
+    auto bias_at = [&](int row) {
+        return __builtin_amdgcn_raw_buffer_load_b32(brs, (uint32_t)row * 4u, 0, 0);
+    };
+    const uint32_t b0 = bias_at(set_lo * 16 + (threadIdx.x >> 2));
     // Keep the x loads ahead of the tile prefetch in the instruction stream:
     // loads complete in issue order, so x issued after the tiles would only
     // arrive behind them.
@@ -518,7 +526,9 @@ __device__ void run(const Task &t, int wg, uint32_t *lds) {
                 __builtin_amdgcn_raw_buffer_store_b16(gd_f2h(gd_silu(gv) * u), ors,
                                                       (uint32_t)(set_lo * 16 + i) * 2u, 0, 0);
         } else {
-            const float v = combine(ok ? quarter(c, r, q) : 0.f);
+            // Rows past R read bias zero (outside the resource).
+            const uint32_t bv = base == 0 ? b0 : bias_at(set_lo * 16 + i);
+            const float v = combine(ok ? quarter(c, r, q) : 0.f) + __uint_as_float(bv);
             if (ok && q == 0 && set_lo * 16 + i < R)
                 __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), yrs,
                                                       (uint32_t)(set_lo * 16 + i) * 4u, 0, 0);

@@ -47,8 +47,8 @@ Split plan(int64_t nsets, int steps, int ksplit, int64_t cus, size_t lds_free, i
 // The task of one GEMV launch on `cus` workgroups, its LDS bytes and whether
 // it keeps per-block partials.
 int make_task(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, size_t xlds,
-              const NormIn &nin, int ksplit, const GluOut &glu, int cus, gemv::Task *t,
-              size_t *lds_out, bool *kbp) {
+              const NormIn &nin, int ksplit, const GluOut &glu, int cus, const float *bias,
+              gemv::Task *t, size_t *lds_out, bool *kbp) {
     const int64_t K = w->K, R = w->R;
     const int nblk = (int)(K >> 7), steps = (nblk + 3) / 4;
     // SwiGLU: split over gate sets, each bringing its up set along.
@@ -62,7 +62,7 @@ int make_task(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, size_t xlds
     GD_REQUIRE(ctx, lds <= LDS_BYTES && sp.grid < (1LL << 31) && sp.ksteps <= 128 &&
                         sp.per * rows_per_set * sp.ksteps < (1 << 16),
                "gd_q2_0_gemv: K=%lld R=%lld does not fit", (long long)K, (long long)R);
-    *t = gemv::Task{(const uint8_t *)w->codes, (const uint16_t *)w->scales, x, y, (int)K, (int)R,
+    *t = gemv::Task{(const uint8_t *)w->codes, (const uint16_t *)w->scales, x, y, bias, (int)K, (int)R,
                     (int)nsets, (int)sp.per, sp.ksteps, sp.nz, (int)sp.grid, nin, glu};
     *lds_out = lds;
     *kbp = sp.kbp;
@@ -72,12 +72,12 @@ int make_task(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, size_t xlds
 template <int XT>
 int launch(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, size_t xlds,
            const NormIn &nin = NormIn{nullptr, nullptr, nullptr, 0.f, 0, 0}, int ksplit = 1,
-           const GluOut &glu = GluOut{nullptr, 0}) {
+           const GluOut &glu = GluOut{nullptr, 0}, const float *bias = nullptr) {
     const int cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
     gemv::Task t;
     size_t lds;
     bool kbp;
-    int rc = make_task(ctx, w, x, y, xlds, nin, ksplit, glu, cus, &t, &lds, &kbp);
+    int rc = make_task(ctx, w, x, y, xlds, nin, ksplit, glu, cus, bias, &t, &lds, &kbp);
     if (rc) return rc;
     auto kern = kbp ? q2_0_gemv_mfma_kernel<XT, true> : q2_0_gemv_mfma_kernel<XT, false>;
     hipLaunchKernelGGL(kern, dim3((unsigned)t.gx, t.nz), dim3(64 * NW), lds, ctx->stream, t);
@@ -90,9 +90,10 @@ int launch(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, size_t xlds,
 
 // GEMV on the matrix cores for f16 or f32 x (the caller has checked w, x, y).
 // ksplit > 1 cuts K into that many splits whose partial rows go to y + z * R
-// (the caller sums them; gd_gemv_ksplit says how many there are).
+// (the caller sums them; gd_gemv_ksplit says how many there are).  bias (if
+// not null) is added to the rows of split 0.
 int gd_gemv_mfma(gd_ctx *ctx, const gd_q2w *w, const void *x, int x_dtype, float *y,
-                 int ksplit) {
+                 int ksplit, const float *bias) {
     const int64_t K = w->K;
     const int XT = x_dtype == GD_F32 ? 1 : 0;
     const int nblk = (int)(K >> 7);
@@ -101,7 +102,9 @@ int gd_gemv_mfma(gd_ctx *ctx, const gd_q2w *w, const void *x, int x_dtype, float
                "gd_q2_0_gemv: K=%lld too long for LDS staging of %s x", (long long)K,
                XT ? "f32" : "f16");
     const NormIn none{nullptr, nullptr, nullptr, 0.f, 0, 0};
-    return XT ? launch<1>(ctx, w, x, y, xlds, none, ksplit) : launch<0>(ctx, w, x, y, xlds, none, ksplit);
+    const GluOut noglu{nullptr, 0};
+    return XT ? launch<1>(ctx, w, x, y, xlds, none, ksplit, noglu, bias)
+              : launch<0>(ctx, w, x, y, xlds, none, ksplit, noglu, bias);
 }
 
 // K splits (1..4) for an f16-x GEMV whose partial rows the consumer can sum:

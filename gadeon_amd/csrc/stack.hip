@@ -432,7 +432,6 @@ struct gd_stack {
     int32_t *page_table = nullptr;
     // scratch
     float *x = nullptr, *proj = nullptr, *conv_out = nullptr, *o32 = nullptr, *contrib = nullptr;
-    float *x2 = nullptr;         // decode: second residual buffer (ping-pong with x)
     float *beta = nullptr, *g = nullptr, *q32 = nullptr, *gate32 = nullptr, *logits = nullptr;
     float *attn_part = nullptr, *amax_v = nullptr;
     int *amax_i = nullptr;
@@ -493,13 +492,17 @@ int forward(gd_stack *st, int N, bool decode) {
 #define R_(call) do { if ((rc = (call)) != GD_OK) return rc; } while (0)
 #define K_(name, ...) do { hipLaunchKernelGGL(name, __VA_ARGS__); GD_LAUNCHED(ctx, #name); } while (0)
     // Prefill: attn_norm of layer 0 here; every later norm is fused with the
-    // residual add that precedes it (k_add_rmsnorm).  Decode: each add +
-    // norm is fused into the x staging of the GEMV that consumes it, with the
-    // residual alternating between x and x2 (hcur holds the live one).
-    float *hcur = st->x, *hnext = st->x2;
-    // Decode projections into the residual (out_proj, down) may split K;
-    // their consumer, the next fused-norm GEMV, sums the nd partials.
+    // residual add that precedes it (k_add_rmsnorm).  Decode: the projections
+    // into the residual (out_proj, down) may split K into nd partials, the
+    // first of which carries the residual x as its bias; the next fused-norm
+    // GEMV sums the partials, normalizes in its x staging and writes the sum
+    // back to x (which no kernel reads by then).
     int nd = 0;
+    auto consume = [&](const gd_q2w *w, const float *normw, float *hout, float *y,
+                       uint16_t *glu) {
+        return gd_gemv_mfma_norm(ctx, w, st->contrib, nd > 1 ? st->contrib + E : nullptr, nd - 1,
+                                 E, normw, eps, hout, y, glu);
+    };
     if (!decode)
         K_(k_add_rmsnorm, dim3(N), dim3(1024), 0, s, st->x, (const float *)nullptr,
            st->L[0].attn_norm, st->xn16, E, eps, 0, (int64_t)0);
@@ -510,14 +513,11 @@ int forward(gd_stack *st, int N, bool decode) {
         const float *pin = st->proj;
         int np = 1;
         if (decode) {
-            if (il == 0) {
-                R_(gd_gemv_mfma_norm(ctx, &ly.in_proj, hcur, nullptr, 0, 0, ly.attn_norm, eps,
+            if (il == 0)
+                R_(gd_gemv_mfma_norm(ctx, &ly.in_proj, st->x, nullptr, 0, 0, ly.attn_norm, eps,
                                      nullptr, st->proj));
-            } else {
-                R_(gd_gemv_mfma_norm(ctx, &ly.in_proj, hcur, st->contrib, nd, E, ly.attn_norm, eps,
-                                     hnext, st->proj));
-                std::swap(hcur, hnext);
-            }
+            else
+                R_(consume(&ly.in_proj, ly.attn_norm, st->x, st->proj, nullptr));
         } else if (ly.rec) {
             // A split-K plan leaves its partials in contrib (free between the
             // residual add and out_proj); the conv front end and the gated
@@ -596,7 +596,7 @@ int forward(gd_stack *st, int N, bool decode) {
         int nsplit = 1;
         if (decode) {
             nd = gd_gemv_ksplit(ctx, ly.out_proj.K, ly.out_proj.R);
-            R_(gd_gemv_mfma(ctx, &ly.out_proj, st->a16, GD_F16, st->contrib, nd));
+            R_(gd_gemv_mfma(ctx, &ly.out_proj, st->a16, GD_F16, st->contrib, nd, st->x));
         } else {
             const gd_gemm_plan p = gd_gemm_choose(ctx, N, ly.out_proj.K, ly.out_proj.R, GD_F16);
             nsplit = p.split;
@@ -604,9 +604,7 @@ int forward(gd_stack *st, int N, bool decode) {
         }
         // gate_up with SwiGLU in its epilogue: a16 = silu(gate x) * (up x).
         if (decode) {
-            R_(gd_gemv_mfma_norm(ctx, &ly.gate_up, hcur, st->contrib, nd, E, ly.post_norm, eps,
-                                 hnext, st->proj, st->a16));
-            std::swap(hcur, hnext);
+            R_(consume(&ly.gate_up, ly.post_norm, st->x, st->proj, st->a16));
         } else {
             K_(k_add_rmsnorm, dim3(N), dim3(1024), 0, s, st->x, st->contrib, ly.post_norm,
                st->xn16, E, eps, nsplit, (int64_t)N * E);
@@ -615,7 +613,7 @@ int forward(gd_stack *st, int N, bool decode) {
         nsplit = 1;
         if (decode) {
             nd = gd_gemv_ksplit(ctx, ly.down.K, ly.down.R);
-            R_(gd_gemv_mfma(ctx, &ly.down, st->a16, GD_F16, st->contrib, nd));
+            R_(gd_gemv_mfma(ctx, &ly.down, st->a16, GD_F16, st->contrib, nd, st->x));
         } else {
             const gd_gemm_plan p = gd_gemm_choose(ctx, N, ly.down.K, ly.down.R, GD_F16);
             nsplit = p.split;
@@ -636,8 +634,7 @@ int forward(gd_stack *st, int N, bool decode) {
     }
     // lm_head on the last token, greedy pick, position bump.
     if (decode)
-        R_(gd_gemv_mfma_norm(ctx, &st->head, hcur, st->contrib, nd, E, st->out_norm, eps,
-                             nullptr, st->logits));
+        R_(consume(&st->head, st->out_norm, nullptr, st->logits, nullptr));
     else
         R_(gd_q2_0_gemv(ctx, &st->head, st->xn16, GD_F16, st->logits));
     K_(k_argmax_part, dim3(AMAX_BLOCKS), dim3(256), 0, s, st->logits, c.n_vocab, st->amax_v,
@@ -759,7 +756,6 @@ int create(gd_ctx *ctx, const gd_stack_config *cfg, uint64_t seed, bool random, 
                        st->page_table, st->max_pages);
     const int maxproj = std::max(std::max(st->rp_rec, st->rp_att), 2 * FF);
     C_(salloc_t(st, (size_t)B * E, &st->x));
-    C_(salloc_t(st, (size_t)E, &st->x2));
     C_(salloc_t(st, (size_t)B * maxproj, &st->proj));
     C_(salloc_t(st, (size_t)B * st->convDim, &st->conv_out));
     C_(salloc_t(st, (size_t)B * st->valDim, &st->o32));
