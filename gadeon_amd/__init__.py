@@ -114,6 +114,8 @@ _PROTOS = {
     "gd_bookmark_free": (None, [_vp]),
     "gd_stack_serialize": (_i, [_vp, _vp, _vp, _sz, C.POINTER(_sz)]),
     "gd_stack_deserialize": (_i, [_vp, _vp, _sz, C.POINTER(_vp)]),
+    "gd_stack_serialize_gdns": (_i, [_vp, _vp, _vp, _sz, C.POINTER(_sz)]),
+    "gd_stack_deserialize_gdns": (_i, [_vp, _vp, _sz, C.POINTER(_vp)]),
     "gd_gguf_open": (_i, [C.c_char_p, C.POINTER(_vp)]),
     "gd_gguf_close": (None, [_vp]),
     "gd_gguf_info": (_i, [_vp, C.POINTER(_i64), C.POINTER(_i64), C.POINTER(_i)]),

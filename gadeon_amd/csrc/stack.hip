@@ -1304,6 +1304,187 @@ extern "C" int gd_stack_serialize(gd_stack *st, const gd_bookmark *b, void *buf,
     return GD_OK;
 }
 
+// ------------------------------------------------- parked-state bytes (GDNS)
+
+namespace {
+
+// BonsaiEngine's parked-state format (BonsaiEngine.swift:65-112, through
+// StateBytes.swift): the magic "GDNS" and an i64 version 1, the position, per
+// GDN layer its conv ring then its state, per attention layer its length and
+// its K pages then its V pages, each page a run of KVCache.pageP = 512
+// positions x kv_dim f32 (Attention.swift:15-40).
+constexpr char GDNS_MAGIC[4] = {'G', 'D', 'N', 'S'};
+constexpr int64_t GDNS_VERSION = 1, GDNS_PAGE = 512;
+
+// Finish a bookmark from host bytes in the device layout.
+int bookmark_from_host(gd_stack *st, const std::vector<uint8_t> &host, int64_t pos,
+                       gd_bookmark **out) {
+    gd_ctx *ctx = st->ctx;
+    gd_bookmark *b = new gd_bookmark();
+    b->ctx = ctx;
+    b->c = st->c;
+    b->pos = pos;
+    b->have_pick = false;        // neither format carries a pick: decode a token first
+    int rc = gd_alloc(ctx, host.size(), &b->buf);
+    if (rc == GD_OK) rc = gd_upload(ctx, b->buf, host.data(), host.size());
+    if (rc) {
+        gd_bookmark_free(b);
+        return rc;
+    }
+    *out = b;
+    return GD_OK;
+}
+
+}  // namespace
+
+extern "C" int gd_stack_serialize_gdns(gd_stack *st, const gd_bookmark *b, void *buf,
+                                       size_t cap, size_t *len) {
+    if (!st) return GD_EINVAL;
+    gd_ctx *ctx = st->ctx;
+    GD_REQUIRE(ctx, b && b->buf && len, "gd_stack_serialize_gdns: null argument");
+    GD_REQUIRE(ctx, b->ctx == ctx && same_geometry(b->c, st->c),
+               "gd_stack_serialize_gdns: bookmark of another stack geometry or context");
+    const BmLayout l = bm_layout(st, b->pos);
+    const size_t kvd = (size_t)st->c.n_head_kv * st->c.head_dim;
+    const int64_t npages = (b->pos + GDNS_PAGE - 1) / GDNS_PAGE;
+    const size_t page = (size_t)GDNS_PAGE * kvd;
+    auto emit = [&](Out &o, const uint8_t *host) {
+        o.put(GDNS_MAGIC, 4);
+        o.i64(GDNS_VERSION);
+        o.i64(b->pos);
+        int64_t nrec = 0, natt = 0;
+        for (const StackLayer &ly : st->L) (ly.rec ? nrec : natt)++;
+        o.i64(nrec);
+        for (int il = 0; il < st->c.n_layer; il++) {
+            if (!st->L[il].rec) continue;
+            o.i64(il);
+            o.i64((int64_t)l.conv);
+            o.put(host ? host + l.off[il] : nullptr, l.conv * 4);
+            o.i64((int64_t)l.rec);
+            o.put(host ? host + l.off[il] + align256(l.conv * 4) : nullptr, l.rec * 4);
+        }
+        o.i64(natt);
+        std::vector<float> wide(host ? page : 0);
+        for (int il = 0; il < st->c.n_layer; il++) {
+            if (st->L[il].rec) continue;
+            o.i64(il);
+            o.i64(b->pos);
+            o.i64(npages);
+            for (int kv = 0; kv < 2; kv++)                      // K pages, then V pages
+                for (int64_t pg = 0; pg < npages; pg++) {
+                    o.i64((int64_t)page);
+                    if (host) {
+                        // Positions past pos are zero, as a fresh page holds.
+                        const _Float16 *h = (const _Float16 *)(host + l.off[il] +
+                                                               kv * align256(l.kv * 2));
+                        const size_t lo = (size_t)pg * page;
+                        const size_t hi = std::min(lo + page, l.kv);
+                        for (size_t i = lo; i < lo + page; i++)
+                            wide[i - lo] = i < hi ? (float)h[i] : 0.f;
+                    }
+                    o.put(host ? wide.data() : nullptr, page * 4);
+                }
+        }
+    };
+    Out sizer{nullptr, 0};
+    emit(sizer, nullptr);
+    *len = sizer.n;
+    if (!buf) return GD_OK;
+    GD_REQUIRE(ctx, cap >= sizer.n, "gd_stack_serialize_gdns: buffer of %zu bytes, need %zu",
+               cap, sizer.n);
+    std::vector<uint8_t> host(l.total);
+    int rc = gd_download(ctx, host.data(), b->buf, l.total);
+    if (rc) return rc;
+    Out o{(uint8_t *)buf, cap};
+    emit(o, host.data());
+    return GD_OK;
+}
+
+extern "C" int gd_stack_deserialize_gdns(gd_stack *st, const void *data, size_t n,
+                                         gd_bookmark **out) {
+    if (!st) return GD_EINVAL;
+    gd_ctx *ctx = st->ctx;
+    GD_REQUIRE(ctx, data && out, "gd_stack_deserialize_gdns: null argument");
+    *out = nullptr;
+    // BonsaiEngine.deserialize refuses bytes without its header
+    // (StateBytes.readHeader); so does this.
+    GD_REQUIRE(ctx, n >= 12 && memcmp(data, GDNS_MAGIC, 4) == 0,
+               "gd_stack_deserialize_gdns: no GDNS header (not a parked state)");
+    In in{(const uint8_t *)data, n, 4};
+    const int64_t version = in.i64();
+    GD_REQUIRE(ctx, version == GDNS_VERSION,
+               "gd_stack_deserialize_gdns: version %lld, this build reads %lld",
+               (long long)version, (long long)GDNS_VERSION);
+    const int64_t pos = in.i64();
+    GD_REQUIRE(ctx, !in.bad && pos >= 0 && pos <= st->c.max_ctx,
+               "gd_stack_deserialize_gdns: position %lld outside [0, max_ctx %d]",
+               (long long)pos, st->c.max_ctx);
+    const BmLayout l = bm_layout(st, pos);
+    std::vector<uint8_t> host(l.total, 0);
+    int64_t nrec = 0, natt = 0;
+    for (const StackLayer &ly : st->L) (ly.rec ? nrec : natt)++;
+    // The layers must be exactly this stack's, in ascending order.
+    auto next_layer = [&](int after, bool rec) {
+        for (int j = after + 1; j < st->c.n_layer; j++)
+            if (st->L[j].rec == rec) return j;
+        return -1;
+    };
+    const int64_t cnt = in.i64();
+    GD_REQUIRE(ctx, !in.bad && cnt == nrec,
+               "gd_stack_deserialize_gdns: %lld GDN layers in the data, the stack has %lld",
+               (long long)cnt, (long long)nrec);
+    int il = -1;
+    for (int64_t k = 0; k < cnt; k++) {
+        const int want = next_layer(il, true);
+        const int64_t got = in.i64();
+        GD_REQUIRE(ctx, !in.bad && got == want,
+                   "gd_stack_deserialize_gdns: GDN layer %lld where %d was expected",
+                   (long long)got, want);
+        il = want;
+        const uint8_t *conv = in.floats(l.conv);
+        const uint8_t *rec = conv ? in.floats(l.rec) : nullptr;
+        GD_REQUIRE(ctx, !in.bad, "gd_stack_deserialize_gdns: layer %d state: bad count or "
+                   "truncated", il);
+        memcpy(host.data() + l.off[il], conv, l.conv * 4);
+        memcpy(host.data() + l.off[il] + align256(l.conv * 4), rec, l.rec * 4);
+    }
+    const int64_t na = in.i64();
+    GD_REQUIRE(ctx, !in.bad && na == natt,
+               "gd_stack_deserialize_gdns: %lld attention layers in the data, the stack has "
+               "%lld", (long long)na, (long long)natt);
+    const size_t kvd = (size_t)st->c.n_head_kv * st->c.head_dim;
+    const size_t page = (size_t)GDNS_PAGE * kvd;
+    const int64_t npages = (pos + GDNS_PAGE - 1) / GDNS_PAGE;
+    il = -1;
+    for (int64_t k = 0; k < na; k++) {
+        const int want = next_layer(il, false);
+        const int64_t got = in.i64(), len = in.i64(), np = in.i64();
+        GD_REQUIRE(ctx, !in.bad && got == want && len == pos && np == npages,
+                   "gd_stack_deserialize_gdns: attention layer %lld with %lld positions in %lld "
+                   "pages where layer %d with %lld in %lld was expected", (long long)got,
+                   (long long)len, (long long)np, want, (long long)pos, (long long)npages);
+        il = want;
+        for (int kv = 0; kv < 2; kv++) {
+            _Float16 *h = (_Float16 *)(host.data() + l.off[il] + kv * align256(l.kv * 2));
+            for (int64_t pg = 0; pg < npages; pg++) {
+                const uint8_t *src = in.floats(page);
+                GD_REQUIRE(ctx, !in.bad, "gd_stack_deserialize_gdns: layer %d %s page %lld: "
+                           "not %zu floats, or truncated", il, kv ? "V" : "K", (long long)pg,
+                           page);
+                // Positions below pos, rounded to the cache's halves (nearest even).
+                const size_t lo = (size_t)pg * page, m = std::min(page, l.kv - lo);
+                for (size_t i = 0; i < m; i++) {
+                    float f;
+                    memcpy(&f, src + 4 * i, 4);
+                    h[lo + i] = (_Float16)f;
+                }
+            }
+        }
+    }
+    GD_REQUIRE(ctx, in.n == n, "gd_stack_deserialize_gdns: %zu trailing bytes", n - in.n);
+    return bookmark_from_host(st, host, pos, out);
+}
+
 extern "C" int gd_stack_deserialize(gd_stack *st, const void *data, size_t n,
                                     gd_bookmark **out) {
     if (!st) return GD_EINVAL;
@@ -1377,17 +1558,5 @@ extern "C" int gd_stack_deserialize(gd_stack *st, const void *data, size_t n,
         }
     }
     GD_REQUIRE(ctx, in.n == n, "gd_stack_deserialize: %zu trailing bytes", n - in.n);
-    gd_bookmark *b = new gd_bookmark();
-    b->ctx = ctx;
-    b->c = st->c;
-    b->pos = pos;
-    b->have_pick = false;        // the format carries no pick: decode a token first
-    int rc = gd_alloc(ctx, l.total, &b->buf);
-    if (rc == GD_OK) rc = gd_upload(ctx, b->buf, host.data(), l.total);
-    if (rc) {
-        gd_bookmark_free(b);
-        return rc;
-    }
-    *out = b;
-    return GD_OK;
+    return bookmark_from_host(st, host, pos, out);
 }

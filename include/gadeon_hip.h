@@ -504,6 +504,20 @@ int gd_stack_restore(gd_stack *st, const gd_bookmark *b);
 void gd_bookmark_free(gd_bookmark *b);
 int gd_stack_serialize(gd_stack *st, const gd_bookmark *b, void *buf, size_t cap, size_t *len);
 int gd_stack_deserialize(gd_stack *st, const void *data, size_t n, gd_bookmark **out);
+/* The same bookmark in the CPU engine's parked-state bytes, BonsaiEngine.serialize /
+ * deserialize (BonsaiEngine.swift:65-112, StateBytes.swift:11-72): the magic "GDNS",
+ * i64 version 1, i64 pos, i64 count of GDN layers, then per GDN layer in ascending
+ * order i64 layer, i64 n, n f32 of its conv ring, i64 n, n f32 of its state; i64
+ * count of attention layers, then per attention layer i64 layer, i64 len, i64
+ * pages, that many K pages then as many V pages, each i64 n, n f32 of 512 positions
+ * (KVCache.pageP) x n_head_kv * head_dim, positions past len zero.  The reader
+ * refuses bytes without that header or version (BonsaiEngine.deserialize returns
+ * nil), and checks every count, layer index and page size against the stack; K/V
+ * are rounded to the cache's halves.  A state parked by the CPU engine thus
+ * resumes on this stack, and the other way round. */
+int gd_stack_serialize_gdns(gd_stack *st, const gd_bookmark *b, void *buf, size_t cap,
+                            size_t *len);
+int gd_stack_deserialize_gdns(gd_stack *st, const void *data, size_t n, gd_bookmark **out);
 
 /* ---- GGUF v3 reader (host only): GGUF.swift:45-117 ---------------------------
  * gd_gguf_open maps the file read-only and parses the header, the metadata and

@@ -352,4 +352,9 @@ class Stack:
         if name == "ssm_conv_state":
             n = (cfg["d_conv"] - 1) * (2 * cfg["n_k_head"] + cfg["n_v_head"]) * cfg["d_state"]
             return np.ctypeslib.as_array(C.cast(L.conv_state, C.POINTER(C.c_float)), (n,)).copy()
+        if name in ("k_cache", "v_cache"):
+            # Positions [0, pos) of an attention layer's cache, [pos][n_head_kv * head_dim].
+            n = self.pos * cfg["n_head_kv"] * cfg["head_dim"]
+            ptr = L.kcache if name == "k_cache" else L.vcache
+            return np.ctypeslib.as_array(C.cast(ptr, C.POINTER(C.c_float)), (max(n, 1),))[:n].copy()
         raise KeyError(name)

@@ -8,7 +8,14 @@ serialize / deserialize (MetalEngine.swift:455-584).
     against the stack's own state), deserialize into a fresh stack of the
     same weights continues bit-identically, and re-serializing gives the same
     bytes;
-  * malformed bytes and bookmarks of another geometry are errors."""
+  * malformed bytes and bookmarks of another geometry are errors;
+  * the CPU engine's parked-state bytes, BonsaiEngine.serialize through
+    StateBytes ("GDNS", BonsaiEngine.swift:65-112): written field by field
+    from the bookmark, with 512-position KV pages across a page boundary; read
+    back bit-identically; a state built from the CPU oracle's own conv rings,
+    recurrent states and K/V resumes on the GPU stack and continues within
+    the stack tolerance of the oracle; malformed headers, versions, pages and
+    truncations are errors."""
 import ctypes as C
 import struct
 
@@ -16,7 +23,9 @@ import numpy as np
 import pytest
 
 import gadeon_amd as ga
-from test_gpu_stack import CFG, DENSE, make_stack, tensor_reader
+import oracle as O
+from conftest import rel_diff
+from test_gpu_stack import CFG, DENSE, THREADS, TOL, make_stack, tensor_reader
 
 pytestmark = pytest.mark.gpu
 
@@ -240,3 +249,205 @@ def test_deserialize_rejects_malformed(ctx):
             ctx.lib.gd_bookmark_free(bm)
         ctx.lib.gd_stack_destroy(st)
         ctx.lib.gd_stack_destroy(other)
+
+
+# ---- the CPU engine's parked-state bytes (GDNS) --------------------------------
+
+PAGE = 512      # KVCache.pageP (Attention.swift:16)
+
+
+def serialize_gdns(ctx, st, bm) -> bytes:
+    n = C.c_size_t()
+    ctx.check(ctx.lib.gd_stack_serialize_gdns(st, bm, None, 0, C.byref(n)))
+    buf = (C.c_uint8 * n.value)()
+    ctx.check(ctx.lib.gd_stack_serialize_gdns(st, bm, buf, n.value, C.byref(n)))
+    return bytes(buf)
+
+
+def deserialize_gdns(ctx, st, data: bytes):
+    h = C.c_void_p()
+    buf = (C.c_uint8 * len(data)).from_buffer_copy(data)
+    ctx.check(ctx.lib.gd_stack_deserialize_gdns(st, buf, len(data), C.byref(h)))
+    return h
+
+
+def parse_gdns(data: bytes):
+    """BonsaiEngine.deserialize's reading order (BonsaiEngine.swift:89-112)."""
+    assert data[:4] == b"GDNS"
+    p = 4
+
+    def i64():
+        nonlocal p
+        v, = struct.unpack_from("<q", data, p)
+        p += 8
+        return v
+
+    def floats():
+        nonlocal p
+        n = i64()
+        a = np.frombuffer(data, np.float32, n, p)
+        p += 4 * n
+        return a
+
+    version, pos = i64(), i64()
+    gdn = {}
+    for _ in range(i64()):
+        il = i64()
+        conv = floats()
+        gdn[il] = (conv, floats())
+    kv = {}
+    for _ in range(i64()):
+        il, length, n = i64(), i64(), i64()
+        kp = [floats() for _ in range(n)]
+        vp = [floats() for _ in range(n)]
+        kv[il] = (length, kp, vp)
+    assert p == len(data)
+    return version, pos, gdn, kv
+
+
+def build_gdns(pos, gdn, kv, kv_dim, version=1) -> bytes:
+    """BonsaiEngine.serialize (BonsaiEngine.swift:65-87) from arrays: gdn maps
+    layer -> (conv, rec), kv maps layer -> (K, V) of shape [pos][kv_dim]."""
+    out = [b"GDNS", struct.pack("<qq", version, pos), struct.pack("<q", len(gdn))]
+
+    def run(a):
+        a = np.ascontiguousarray(a, np.float32).reshape(-1)
+        return struct.pack("<q", a.size) + a.tobytes()
+
+    for il in sorted(gdn):
+        out += [struct.pack("<q", il), run(gdn[il][0]), run(gdn[il][1])]
+    out.append(struct.pack("<q", len(kv)))
+    npages = (pos + PAGE - 1) // PAGE
+    for il in sorted(kv):
+        out.append(struct.pack("<qqq", il, pos, npages))
+        for a in kv[il]:
+            padded = np.zeros((npages * PAGE, kv_dim), np.float32)
+            padded[:pos] = np.asarray(a, np.float32).reshape(pos, kv_dim)
+            out += [run(padded[i * PAGE:(i + 1) * PAGE]) for i in range(npages)]
+    return b"".join(out)
+
+
+@pytest.mark.parametrize("dense", [False, True])
+def test_gdns_format_and_round_trip(ctx, dense):
+    """A 530-position state (two KV pages of 512): the GDNS bytes hold the
+    bookmark's conv rings, states and K/V (the same values as MetalEngine's
+    format, zero past the position), read back bit-identically, and continue
+    the generation bit-identically in a fresh stack."""
+    over = dict(DENSE if dense else {}, max_ctx=640, max_batch=128)
+    cfg, st = make_stack(ctx, seed=26, **over)
+    _, st2 = make_stack(ctx, seed=26, **over)
+    bm = bm2 = None
+    try:
+        ids = (np.arange(530) * 19 % cfg["n_vocab"]).astype(np.int32)
+        first = prefill(ctx, st, ids)
+        bm = bookmark(ctx, st)
+        data = serialize_gdns(ctx, st, bm)
+        version, pos, gdn, kv = parse_gdns(data)
+        assert version == 1 and pos == ids.size
+        rec = [il for il in range(cfg["n_layer"]) if (il + 1) % cfg["attn_interval"]]
+        att = [il for il in range(cfg["n_layer"]) if not (il + 1) % cfg["attn_interval"]]
+        assert list(gdn) == rec and list(kv) == att
+        read = tensor_reader(ctx, st)
+        for il in rec:
+            assert np.array_equal(gdn[il][0], read(il, "ssm_conv_state"))
+            assert np.array_equal(gdn[il][1], read(il, "ssm_state"))
+        # K/V against MetalEngine's format of the same bookmark.
+        _, _, _, _, mkv = parse(serialize(ctx, st, bm), cfg)
+        kv_dim = cfg["n_head_kv"] * cfg["head_dim"]
+        for il in att:
+            length, kp, vp = kv[il]
+            assert length == pos and len(kp) == len(vp) == 2
+            for pages, flat in ((kp, mkv[il][1]), (vp, mkv[il][2])):
+                assert all(p.size == PAGE * kv_dim for p in pages)
+                whole = np.concatenate(pages)
+                assert np.array_equal(whole[:pos * kv_dim], flat)
+                assert not whole[pos * kv_dim:].any()
+        bm2 = deserialize_gdns(ctx, st2, data)
+        assert serialize_gdns(ctx, st2, bm2) == data
+        assert serialize(ctx, st2, bm2) == serialize(ctx, st, bm)
+        ctx.check(ctx.lib.gd_stack_restore(st2, bm2))
+        toks = [first, 7, 123, 9]
+        l1, p1 = decode_run(ctx, st, toks)
+        l2, p2 = decode_run(ctx, st2, toks)
+        assert same(l1, l2) and p1 == p2
+        print(f"\n  GDNS: {len(data)} bytes at position {pos}, two KV pages; fresh stack "
+              "continues bit-identically")
+    finally:
+        for b in (bm, bm2):
+            if b:
+                ctx.lib.gd_bookmark_free(b)
+        ctx.lib.gd_stack_destroy(st)
+        ctx.lib.gd_stack_destroy(st2)
+
+
+def test_gdns_resumes_a_cpu_parked_state(ctx):
+    """The CPU oracle (BonsaiEngine.forward restated) runs a prompt; its own
+    conv rings, recurrent states and K/V, written as BonsaiEngine.serialize
+    bytes, are read into the GPU stack, which then decodes alongside the
+    oracle: logits within the stack tolerance at every step."""
+    cfg, st = make_stack(ctx, seed=27)
+    bm = None
+    try:
+        read = tensor_reader(ctx, st)
+        ref = O.Stack(cfg, read, stage_f16=True, threads=THREADS)
+        ids = (np.arange(37) * 23 % cfg["n_vocab"]).astype(np.int32)
+        _, lg = ref.prefill(ids)
+        rec = [il for il in range(cfg["n_layer"]) if (il + 1) % cfg["attn_interval"]]
+        att = [il for il in range(cfg["n_layer"]) if not (il + 1) % cfg["attn_interval"]]
+        kv_dim = cfg["n_head_kv"] * cfg["head_dim"]
+        data = build_gdns(ids.size,
+                          {il: (ref.layer_state(il, "ssm_conv_state"),
+                                ref.layer_state(il, "ssm_state")) for il in rec},
+                          {il: (ref.layer_state(il, "k_cache"), ref.layer_state(il, "v_cache"))
+                           for il in att}, kv_dim)
+        bm = deserialize_gdns(ctx, st, data)
+        ctx.check(ctx.lib.gd_stack_restore(st, bm))
+        assert position(ctx, st) == ids.size
+        tok = int(np.argmax(lg))
+        worst = 0.0
+        for step in range(6):
+            (glg,), _ = decode_run(ctx, st, [tok])
+            _, rlg = ref.token(tok)
+            r = rel_diff(glg, rlg)
+            worst = max(worst, r)
+            assert r < TOL, (step, r)
+            tok = int(np.argmax(rlg))
+        print(f"\n  CPU-parked state resumed on the GPU: 6 decode steps, worst logits relDiff "
+              f"{worst:.2e}")
+    finally:
+        if bm:
+            ctx.lib.gd_bookmark_free(bm)
+        ctx.lib.gd_stack_destroy(st)
+
+
+def test_gdns_rejects_malformed(ctx):
+    cfg, st = make_stack(ctx, seed=28)
+    bm = None
+    try:
+        prefill(ctx, st, (np.arange(20) * 7 % cfg["n_vocab"]).astype(np.int32))
+        bm = bookmark(ctx, st)
+        data = serialize_gdns(ctx, st, bm)
+
+        def bad(b: bytes, msg: str):
+            with pytest.raises(ga.GDError, match=msg):
+                deserialize_gdns(ctx, st, b)
+
+        bad(data[:8], "no GDNS header")
+        bad(b"GDNX" + data[4:], "no GDNS header")
+        bad(serialize(ctx, st, bm), "no GDNS header")           # MetalEngine's format
+        bad(data[:4] + struct.pack("<q", 2) + data[12:], "version 2")
+        for cut in (12, 20, 28, len(data) // 2, len(data) - 4):
+            bad(data[:cut], "gd_stack_deserialize_gdns")
+        bad(data + b"\0" * 8, "trailing")
+        bad(data[:12] + struct.pack("<q", 10 ** 9) + data[20:], "position")
+        # The last attention layer's first K page claims one float fewer.
+        kv_dim = cfg["n_head_kv"] * cfg["head_dim"]
+        tail = 2 * (8 + PAGE * kv_dim * 4)                      # its K page and V page
+        at = len(data) - tail
+        cnt, = struct.unpack_from("<q", data, at)
+        assert cnt == PAGE * kv_dim
+        bad(data[:at] + struct.pack("<q", cnt - 1) + data[at + 8:], "K page 0")
+    finally:
+        if bm:
+            ctx.lib.gd_bookmark_free(bm)
+        ctx.lib.gd_stack_destroy(st)
