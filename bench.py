@@ -186,6 +186,40 @@ def bench_gdn_decode(ctx, ga, B: int, steps: int, warmup: int) -> dict:
             "frac_hbm": per_step / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
 
 
+def bench_gdn_decode_pool(ctx, ga, B: int, pool: int, steps: int, warmup: int) -> dict:
+    """Config 3 at B sequences with the states streamed from HBM: `pool`
+    independent sets of B states (pool x B MiB, beyond the 256 MB Infinity
+    Cache), step i updating set i % pool, so no step finds its state cached."""
+    H, d = 16, 128
+    n = B * H * d * d
+    dS = ctx.alloc(pool * n * 4)
+    ctx.gd_rand_normal(dS, ga.F32, pool * n, 40, 0.0, 0.02)
+    dq, dk, dv = ctx.alloc(B * H * d * 2), ctx.alloc(B * H * d * 2), ctx.alloc(B * H * d * 2)
+    for i, p in enumerate((dq, dk, dv)):
+        ctx.gd_rand_normal(p, ga.F16, B * H * d, 41 + i, 0.0, 1.0)
+    dg, db = ctx.alloc(B * H * 4), ctx.alloc(B * H * 4)
+    ctx.gd_rand_uniform(dg, B * H, 44, -1.5, -0.1)
+    ctx.gd_rand_uniform(db, B * H, 45, 0.2, 0.8)
+    do = ctx.alloc(B * H * d * 2)
+    step = [0]
+
+    def fn():
+        s = dS + (step[0] % pool) * n * 4
+        step[0] += 1
+        ctx.gd_gdn_decode(B, H, H, d, dq, dk, dv, ga.F16, dg, db, None, None, s, do,
+                          1 / d ** 0.5, 1e-6)
+    for _ in range(max(warmup, pool)):
+        fn()
+    ms = Timer(ctx).ms(fn, steps)
+    for p in (dS, dq, dk, dv, dg, db, do):
+        ctx.free(p)
+    per_step = B * 2_113_664
+    return {"B": B, "pool_sets": pool, "state_mib": pool * n * 4 / 2 ** 20,
+            "us_per_step": ms * 1e3, "gbs": per_step / (ms * 1e-3) / 1e9,
+            "frac_hbm": per_step / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "note": "states rotated over a pool beyond the Infinity Cache: streamed from HBM"}
+
+
 def copy_bandwidth(ctx, nbytes: int = 1 << 30) -> float:
     a, b = ctx.alloc(nbytes), ctx.alloc(nbytes)
     ctx.gd_copy(b, a, nbytes)
@@ -482,9 +516,10 @@ def run_configs(ctx, ga, steps: int, warmup: int) -> dict:
     dec32["note"] = ("B=32 states total 32 MiB and stay resident in the 256 MB Infinity Cache "
                      "across the 128 steps: a cache-resident figure, not an HBM one")
     dec1["note"] = "one 1 MiB state, cache-resident"
+    dec32h = bench_gdn_decode_pool(ctx, ga, 32, 16, 128, warmup)
     return {"copy_gbs": copy, "config0_gemv": gemv, "config1_gemm": gemm,
             "config2_gdn_prefill": pre, "config3_gdn_decode_b1": dec1,
-            "config3_gdn_decode_b32": dec32}
+            "config3_gdn_decode_b32": dec32, "config3_gdn_decode_b32_hbm": dec32h}
 
 
 def run_kernels(ctx, ga, args) -> dict:
