@@ -345,14 +345,21 @@ __global__ __launch_bounds__(256) void k_argmax_part(const float *v, int n, floa
     argmax_block(best, idx, bv, bi, pv + blockIdx.x, pi + blockIdx.x);
 }
 
+// The pick goes to *out and to picks[*pos] (the pick made at that position),
+// then the position advances by n.
 __global__ __launch_bounds__(128) void k_argmax_final(const float *pv, const int *pi,
-                                                      int32_t *out) {
+                                                      int32_t *out, int32_t *picks,
+                                                      int32_t *pos, int n) {
     __shared__ float bv[2];
     __shared__ int bi[2];
     __shared__ float fb;
     __shared__ int fi;
     argmax_block(pv[threadIdx.x], pi[threadIdx.x], bv, bi, &fb, &fi);
-    if (threadIdx.x == 0) *out = fi;
+    if (threadIdx.x == 0) {
+        *out = fi;
+        picks[*pos] = fi;
+        *pos += n;
+    }
 }
 
 // x += y over rows of n, then y16 = rmsnorm(x) * w as f16 (the residual add
@@ -398,8 +405,6 @@ __global__ __launch_bounds__(1024) void k_add_rmsnorm(float *x, const float *y, 
     }
 }
 
-__global__ void k_add_pos(int32_t *pos, int n) { *pos += n; }
-
 __global__ void k_iota(int32_t *p, int n) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) p[i] = i;
@@ -437,6 +442,7 @@ struct gd_stack {
     int *amax_i = nullptr;
     uint16_t *xn16 = nullptr, *a16 = nullptr;
     int32_t *ids = nullptr, *dpos = nullptr, *dtok = nullptr;
+    int32_t *picks = nullptr;    // picks[p]: the greedy pick made at position p
     int64_t pos = 0;
     bool random = true;          // weights drawn from the seed (else loaded)
     bool have_pick = false;      // dtok holds the last greedy pick
@@ -639,8 +645,8 @@ int forward(gd_stack *st, int N, bool decode) {
         R_(gd_q2_0_gemv(ctx, &st->head, st->xn16, GD_F16, st->logits));
     K_(k_argmax_part, dim3(AMAX_BLOCKS), dim3(256), 0, s, st->logits, c.n_vocab, st->amax_v,
        st->amax_i);
-    K_(k_argmax_final, dim3(1), dim3(AMAX_BLOCKS), 0, s, st->amax_v, st->amax_i, st->dtok);
-    K_(k_add_pos, dim3(1), dim3(1), 0, s, st->dpos, N);
+    K_(k_argmax_final, dim3(1), dim3(AMAX_BLOCKS), 0, s, st->amax_v, st->amax_i, st->dtok,
+       st->picks, st->dpos, N);
 #undef K_
 #undef R_
     return GD_OK;
@@ -775,6 +781,7 @@ int create(gd_ctx *ctx, const gd_stack_config *cfg, uint64_t seed, bool random, 
     C_(salloc_t(st, (size_t)B, &st->ids));
     C_(salloc_t(st, 1, &st->dpos));
     C_(salloc_t(st, 1, &st->dtok));
+    C_(salloc_t(st, (size_t)c.max_ctx, &st->picks));
     C_(gd_stack_reset(st));
 #undef C_
     *out = st;
@@ -882,27 +889,19 @@ extern "C" int gd_stack_generate(gd_stack *st, int n, int32_t *tokens) {
         st->decode_graph = graph;
         GD_HIP(ctx, hipGraphInstantiate(&st->decode_exec, graph, nullptr, nullptr, 0));
     }
-    // Each step's pick is copied into a device ring so nothing syncs per token.
-    int32_t *ring = nullptr;
-    if ((rc = gd_alloc(ctx, (size_t)n * 4, (void **)&ring))) return rc;
+    // Each step records its pick at picks[position], so nothing syncs per
+    // token; the n picks are read back once at the end.
     for (int i = 0; i < n; i++) {
         if (eager) {
             if ((rc = gd_q2_0_dequant_rows(ctx, &st->embd, st->dtok, 1, st->x)) ||
-                (rc = forward(st, 1, true))) {
-                gd_free(ctx, ring);
+                (rc = forward(st, 1, true)))
                 return rc;
-            }
         } else {
             hipError_t e = hipGraphLaunch(st->decode_exec, ctx->stream);
-            if (e != hipSuccess) { gd_free(ctx, ring); return gd_hip_fail(ctx, e, "decode graph launch"); }
+            if (e != hipSuccess) return gd_hip_fail(ctx, e, "decode graph launch");
         }
-        hipError_t e;
-        e = hipMemcpyAsync(ring + i, st->dtok, 4, hipMemcpyDeviceToDevice, ctx->stream);
-        if (e != hipSuccess) { gd_free(ctx, ring); return gd_hip_fail(ctx, e, "token copy"); }
     }
-    rc = gd_download(ctx, tokens, ring, (size_t)n * 4);
-    gd_free(ctx, ring);
-    if (rc) return rc;
+    if ((rc = gd_download(ctx, tokens, st->picks + st->pos, (size_t)n * 4))) return rc;
     st->pos += n;
     return GD_OK;
 }
