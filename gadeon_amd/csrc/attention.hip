@@ -142,7 +142,9 @@ __global__ __launch_bounds__(256) void k_attn_prefill(
     constexpr int CH = HD / 64;                           // 8-dim chunks a thread stages per operand
     __shared__ __attribute__((aligned(16))) f16 Ks[AK][HD + 8];
     __shared__ __attribute__((aligned(16))) f16 Vt[HD][AK + 8];
-    const int h = blockIdx.x, q0 = blockIdx.y * AQ;
+    // The last query blocks attend the most keys: they are dispatched first,
+    // so the short ones fill the CUs behind them.
+    const int h = blockIdx.x, q0 = (int)(gridDim.y - 1 - blockIdx.y) * AQ;
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
     const int lq = lane & 15, g = lane >> 4;
     const int kvh = h / (H / HKV);
