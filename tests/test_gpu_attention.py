@@ -7,7 +7,9 @@ sigmoid(gate).  Head dims 128 and 256 with the GQA groups of BASELINE config 4
 (40 / 8) and of the reference's 27B (24 / 4), over ragged page sizes.  Norm-wise
 relative error < 2e-3 (the f16 cache and the hi/lo f16 MFMA operands are the
 error sources); rope and the q|gate split against the oracle / exactly; the
-cache append bit-exact (RNE f16)."""
+cache append bit-exact (RNE f16).  Prompts up to 600 keys (many query
+blocks, dispatched longest first): rows of every query block are checked, and
+a second launch of the same call is bit-identical."""
 import ctypes as C
 
 import numpy as np
@@ -52,7 +54,8 @@ def ref_attention(q, K, V, gate, nkv, t_end):
 
 
 @pytest.mark.parametrize("hd,nh,nkv,page,T", [(128, 40, 8, 16, 77), (256, 24, 4, 16, 130),
-                                              (256, 24, 4, 7, 45), (128, 4, 2, 5, 300)])
+                                              (256, 24, 4, 7, 45), (128, 4, 2, 5, 300),
+                                              (128, 40, 8, 16, 600), (256, 24, 4, 16, 520)])
 def test_decode_and_batch_attention(ctx, hd, nh, nkv, page, T):
     rng = np.random.default_rng(hd + T)
     kv_dim = hd * nkv
@@ -81,8 +84,11 @@ def test_decode_and_batch_attention(ctx, hd, nh, nkv, page, T):
                                   base, t) for t in range(T)]).reshape(T, nh, hd)
     k_ref = np.stack([O.rope_neox(O.rmsnorm_rows(k[t].ravel(), hd, kn, eps), hd, n_rot, base, t)
                       for t in range(T)]).reshape(T, nkv, hd)
-    assert rel_diff(ctx.get(dq, (T, nh, hd), np.float32), q_ref) < 1e-5
-    assert rel_diff(ctx.get(dk, (T, nkv, hd), np.float32), k_ref) < 1e-5
+    # The rotation angle pos * theta carries f32 rounding that grows with the
+    # position (about 600 * 2^-24 rad at T = 600): the bound follows it.
+    rtol = 1e-5 if T <= 300 else 1e-4
+    assert rel_diff(ctx.get(dq, (T, nh, hd), np.float32), q_ref) < rtol
+    assert rel_diff(ctx.get(dk, (T, nkv, hd), np.float32), k_ref) < rtol
     kc, vc, dtab, table, npages = make_cache(ctx, T, kv_dim, page, hd)
     # append in two calls (a prefix, then the rest)
     cut = T // 3
@@ -107,9 +113,14 @@ def test_decode_and_batch_attention(ctx, hd, nh, nkv, page, T):
                           hi - lo, 1, 0)
     got = ctx.get(dout, (T, nh, hd), np.float32)
     q_used = ctx.get(dq, (T, nh, hd), np.float32)
-    for t in (0, 1, cut - 1, cut, T // 2, T - 1):
+    for t in sorted({0, 1, cut - 1, cut, T // 2, T - 1, *range(5, T, 61)}):
         want = ref_attention(q_used[t], K16, V16, gate[t], nkv, t + 1)
         assert rel_diff(got[t], want) < TOL, t
+    # The same launch again: bit-identical.
+    ctx.gd_attn_batch(dq + cut * nh * hd * 4, kc, vc, dtab, dg + cut * nh * hd * 4,
+                      dout + cut * nh * hd * 4, hd, nh, nkv, kv_dim, page, C.c_float(scale), cut,
+                      T - cut, 1, 0)
+    assert np.array_equal(ctx.get(dout, (T, nh, hd), np.float32), got)
     # decode attention of the last token over all T cached keys, gated and not
     part = ctx.alloc(nh * 16 * (hd + 2) * 4)
     dq1 = dq + (T - 1) * nh * hd * 4
