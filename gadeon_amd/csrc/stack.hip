@@ -605,6 +605,7 @@ int forward(gd_stack *st, int N, bool decode) {
             R_(gd_gemv_mfma(ctx, &ly.out_proj, st->a16, GD_F16, st->contrib, nd, st->x));
         } else {
             const gd_gemm_plan p = gd_gemm_choose(ctx, N, ly.out_proj.K, ly.out_proj.R, GD_F16);
+            GD_REQUIRE(ctx, p.split <= 8, "stack: %d split-K partials (contrib holds 8)", p.split);
             nsplit = p.split;
             R_(gd_gemm_launch(ctx, &ly.out_proj, N, st->a16, GD_F16, st->contrib, GD_F32, p));
         }
@@ -622,6 +623,7 @@ int forward(gd_stack *st, int N, bool decode) {
             R_(gd_gemv_mfma(ctx, &ly.down, st->a16, GD_F16, st->contrib, nd, st->x));
         } else {
             const gd_gemm_plan p = gd_gemm_choose(ctx, N, ly.down.K, ly.down.R, GD_F16);
+            GD_REQUIRE(ctx, p.split <= 8, "stack: %d split-K partials (contrib holds 8)", p.split);
             nsplit = p.split;
             R_(gd_gemm_launch(ctx, &ly.down, N, st->a16, GD_F16, st->contrib, GD_F32, p));
         }
