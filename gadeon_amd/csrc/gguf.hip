@@ -169,7 +169,11 @@ extern "C" int gd_gguf_open(const char *path, gd_gguf **out) {
         if (t == 9) {                                            // array
             const uint32_t et = c.get<uint32_t>();
             const uint64_t n = c.get<uint64_t>();
-            if (n > g->size) { c.bad = true; break; }
+            // Each element takes at least its scalar's bytes (a string its
+            // length): a count the rest of the file cannot hold is corruption,
+            // caught before any element is stored.
+            const uint64_t least = et <= 1 || et == 7 ? 1 : et <= 3 ? 2 : et <= 6 ? 4 : 8;
+            if (c.bad || n > (g->size - c.pos) / least) { c.bad = true; break; }
             // Bool elements read as 0/1 integers (GGUF.swift:263-275).
             v.kind = et == 8 ? 5 : (et == 6 || et == 12) ? 4 : 3;
             for (uint64_t k = 0; k < n && !c.bad; k++) {

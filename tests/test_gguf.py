@@ -195,6 +195,14 @@ def test_corrupt_files_are_errors(tmp_path, lib):
     assert not opens(W.encode(KVS, [("f", [6, 5000], W.GGML_F32, ts[0][3])]))
     assert not opens(W.encode(KVS, [("q", [100, 3], W.GGML_Q2_0, ts[1][3])]))  # not whole blocks
     assert not opens(W.encode(KVS, [("f", [1, 1, 1, 1, 30], W.GGML_F32, ts[0][3])]))
+    # An array whose count the rest of the file cannot hold (2^40 u8 elements,
+    # 2^37 strings) is an error.
+    arr = W.encode([("a", W.ARR, (W.U8, [1, 2, 3]))], [])
+    i = arr.find(b"a") + 1 + 4 + 4                                  # past key, type, elem type
+    assert not opens(arr[:i] + struct.pack("<Q", 2 ** 40) + arr[i + 8:])
+    arr = W.encode([("a", W.ARR, (W.STR, ["x"]))], [])
+    i = arr.find(b"a") + 1 + 4 + 4
+    assert not opens(arr[:i] + struct.pack("<Q", 2 ** 37) + arr[i + 8:])
     # Nonexistent path.
     with pytest.raises(ga.GDError, match="cannot open"):
         ga.GGUF(tmp_path / "absent.gguf")
