@@ -2,17 +2,37 @@
 // body of the GEMV kernel in q2_0_gemv_mfma.hip.
 //
 // Same result as q2_0_gemv (Kernels.metal:30-119) and Q2_0.matvec
-// (Quant.swift:36-77): per block d * (sum(code*x) - sum(x)), f32 throughout.
+// (Quant.swift:36-77): per block d * (sum(code*x) - sum(x)), accumulated in
+// f32 (the precision of each body is below).
 //
-// MI355X design.  v_mfma_f32_4x4x4f16 (16 independent 4x4x4 products per
-// instruction) does the multiply-adds; the VALU only unpacks codes.
-//   * A operand: the weights are stored in 2 KiB tiles (16 rows x 512 K) in
-//     the order the 64 lanes need them: lane l holds one Q2_0 block (32 code
+// MI355X design.  Two item bodies share the work split below.
+//   * Tiles.  The weights are stored in 2 KiB tiles (16 rows x 512 K) in the
+//     order the 64 lanes need them: lane l holds one Q2_0 block (32 code
 //     bytes) of row l%16, block l/16 of the step, read as two 16-byte loads
 //     at lane*16 and 1024 + lane*16, so every load instruction of a wave is
-//     one contiguous 1 KiB.  As a 4x4x4 lane, l is row l%4 of MFMA block
-//     l/4: MFMA block m covers rows 4*(m%4) .. 4*(m%4)+3 of Q2 block m/4.
-//     Codes k and k+8 of a code dword land in the two f16 halves of an
+//     one contiguous 1 KiB.
+//   * fp4 body (F4, every K whose staging fits LDS: up to about 30K).
+//     v_mfma_scale_f32_16x16x128_f8f6f4 with fp4 (e2m1) weights and e4m3 x.
+//     A lane of that MFMA holds row l%16 and K 32*(l/16) .. +31, which the
+//     tile order makes one Q2 block per lane group: a code c in the low two
+//     bits of a nibble is the e2m1 value c/2, so 16 codes become two operand
+//     dwords by w & 0x33333333 and (w >> 2) & 0x33333333 (three VALU ops per
+//     16 weights; an A scale of 2 restores c).  x is staged per workgroup as
+//     e4m3 pieces, x = 2^e (p0 + p1/16 + p2/256 [+ p3/4096]) with e per Q2
+//     block: three pieces hold an f16 value exactly (four give f32 x about
+//     20 bits).  B column 4q + j carries piece j of block q and is zero
+//     elsewhere, so one MFMA's 16 columns hold the four blocks' piece sums
+//     apart; the piece scales 2^(e - 4j) ride in the E8M0 B scales.  Four
+//     MFMAs cover an item; a quad of lanes then adds the pieces and applies
+//     d (sum c x - sum x) per block.  Precision: the matrix cores add each
+//     group of 8 products aligned to the largest, keeping about 13 bits
+//     below it (measured), so a small x beside a much larger one in the same
+//     group of 8 loses low bits: relDiff against the f64 oracle is about
+//     4e-6 for N(0,1) x and 1.7e-4 with every 97th element 3000x larger.
+//   * f16 body (longer K).  v_mfma_f32_4x4x4f16 (16 independent 4x4x4
+//     products per instruction); as a 4x4x4 lane, l is row l%4 of MFMA
+//     block l/4: MFMA block m covers rows 4*(m%4) .. 4*(m%4)+3 of Q2 block
+//     m/4.  Codes k and k+8 of a code dword land in the two f16 halves of an
 //     operand dword by a mask alone (codes 2, 3, 4 sit at bits 4, 6, 8), or
 //     by a mask after one of two shared shifts (w << 4 for codes 0, 1; w >> 6
 //     for 5, 6, 7): ten VALU ops per 16 weights.  A half is then exactly
@@ -22,14 +42,10 @@
 //     those subnormals (measured), while 4, 6 and 8 stay within about 1e-6
 //     of the exact sum.  A block whose x would overflow f16 after the x16
 //     pre-scale is staged scaled down by a power of two 2^-e, undone later.
-//   * B operand: every lane reads the staged x of its own Q2 block, so the
-//     four output columns of an MFMA block hold the same products and
-//     column 0 is used (the lanes of one block read one LDS address, which
-//     the LDS broadcasts).  x is staged once per workgroup in LDS, already
-//     permuted into the (k, k+8) pair order of the unpack and pre-scaled,
-//     with zero blocks past the last one for a short final step.  f32 x is
-//     split into hi = f16(x) and lo = f16((x - hi) * 2^11), two B operands
-//     accumulated apart and recombined in f32.
+//     Every lane reads the staged x of its own Q2 block, so the four output
+//     columns of an MFMA block hold the same products and column 0 is used.
+//     f32 x is split into hi = f16(x) and lo = f16((x - hi) * 2^11), two B
+//     operands accumulated apart and recombined in f32.
 //   * Work split.  A "set" is one 16-row group; an "item" is one tile (one
 //     chunk step of 512 K of one set).  Every workgroup gets the same number
 //     of consecutive sets (and, with a K split, one range of steps).  Its
@@ -66,6 +82,17 @@ constexpr int CP_NT = 2;     // cache policy: non-temporal (streamed once)
 __host__ __device__ inline size_t xlds_bytes(int nblk, bool hl) {
     return (size_t)(nblk + 5) * XB * 4 * (hl ? 2 : 1) + (size_t)((nblk + 1) & ~1) * 8;
 }
+
+// The fp4 variant (F4) stages x as e4m3 pieces: per Q2 block, 8 chunks of 16
+// elements x 4 piece slots of 16 bytes, then 64 bytes of padding (the block
+// stride, 576 = 64 mod 256, puts the four blocks of a step on different LDS
+// banks); the block sums and scale exponents follow.
+constexpr int F4_BLK = 576;
+__host__ __device__ inline size_t xlds_bytes_f4(int nblk) {
+    return (size_t)(nblk + 5) * F4_BLK + (size_t)((nblk + 1) & ~1) * 8;
+}
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 // Operand dword m holds codes (m, m+8) of w at bit position POS[m] of its
 // two f16 halves; the x pair it meets is pre-scaled by XSCALE[m] = 2^(8-POS[m]).
@@ -189,10 +216,13 @@ __device__ __forceinline__ int set_of(const Geo &g, int it) {
 // nothing).  The address arithmetic has no branch (the compiler's wait
 // counting is exact only over straight-line loads): an item past the last
 // gets the offset 0xfffff000, beyond every resource.
+// F4: the loading lanes are those of piece 0 (lane % 4 == 0); lane l takes
+// rows 4*(l/16) .. +3 of block 4s + (l/4) % 4.
+template <bool F4>
 __device__ __forceinline__ void issue(const Task &t, const Geo &g, int it, u32x4 (&cw)[2],
                                       u32x2 &sc) {
     const int lane = threadIdx.x & 63;
-    const int j = lane & 3, rq = (lane >> 2) & 3, kb = lane >> 4;
+    const int j = lane & 3, rq = F4 ? lane >> 4 : (lane >> 2) & 3, kb = F4 ? (lane >> 2) & 3 : lane >> 4;
     const __amdgpu_buffer_rsrc_t trs =
             make_rsrc(t.codes + (size_t)g.set_lo * g.steps * 2048, (uint32_t)g.wsets * g.steps * 2048u);
     const __amdgpu_buffer_rsrc_t srs =
@@ -215,10 +245,11 @@ __device__ __forceinline__ void issue(const Task &t, const Geo &g, int it, u32x4
 // per row) in LDS, summed with the rest of the row at the end; otherwise
 // summed across the block lanes first (needs 4x less LDS, for very long K).
 // All 64 * NW threads of the workgroup must call it.
-template <int XT, bool KBP>
+template <int XT, bool KBP, bool F4>
 __device__ void run(const Task &t, int wg, uint32_t *lds) {
     constexpr int MT = 64 * NW;
-    constexpr bool HL = XT == 1;                          // x carried as f16 hi + lo
+    constexpr bool HL = XT == 1 && !F4;                   // x carried as f16 hi + lo
+    constexpr int NJ = XT == 1 ? 4 : 3;                   // F4: e4m3 pieces of x
     __shared__ __align__(16) int next_item;               // next item to take
     const Geo g = geometry(t, wg);
     const int K = t.K, R = t.R;
@@ -227,13 +258,15 @@ __device__ void run(const Task &t, int wg, uint32_t *lds) {
     // the blocks one load instruction reads start on different banks), then
     // zero blocks for the blocks of a short last step past K; per-block sum
     // and exponent of x (nblk rounded up to even, so that what follows is
-    // 16-byte aligned); the row partials of every item.
+    // 16-byte aligned); the row partials of every item.  F4: the e4m3 piece
+    // blocks (F4_BLK bytes each) in place of the planes.
     const int xstride = (nblk + 5) * XB;                   // dwords per x plane
     uint32_t *xp = lds;                                    // hi (or f16) pairs
     uint32_t *xq = lds + xstride;                          // lo plane (f32 x only)
-    float *sx = (float *)(lds + (HL ? 2 : 1) * xstride);   // [nblk] block sums of x
-    float *ex = sx + ((nblk + 1) & ~1);                    // [nblk] 2^(16+e_b)
+    float *sx = (float *)(lds + (F4 ? (nblk + 5) * (F4_BLK / 4) : (HL ? 2 : 1) * xstride));
+    float *ex = sx + ((nblk + 1) & ~1);                    // [nblk] 2^(16+e_b); F4: E8M0 byte
     float *part = ex + ((nblk + 1) & ~1);                  // [items][4 blocks if KBP][16 rows]
+    uint8_t *xsb = (uint8_t *)lds;                         // F4 piece blocks
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -300,7 +333,7 @@ __device__ void run(const Task &t, int wg, uint32_t *lds) {
     Ring rg;
 #pragma unroll
     for (int p = 0; p < P; p++) rg.it[p] = p * NW + wave;
-    issue(t, g, rg.it[0], rg.t[0], rg.sc[0]);
+    issue<F4>(t, g, rg.it[0], rg.t[0], rg.sc[0]);
     if (threadIdx.x == 0) next_item = NW * P;
 
     // Stage x: pair p = 8i + k of block b holds (x[b,16i+k], x[b,16i+k+8]) *
@@ -335,6 +368,70 @@ __device__ void run(const Task &t, int wg, uint32_t *lds) {
         amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
         amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
         amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+        if constexpr (F4) {
+            // x = 2^e (p0 + p1/16 + p2/256 [+ p3/4096]), e4m3 pieces with
+            // max|x| 2^-e in [128, 256): p0 = e4m3(x 2^-e), each later piece
+            // the e4m3 of 16 times what is left.  Piece j of the chunk goes
+            // to slot j as 16 bytes, the even elements first (the order the
+            // fp4 unpack gives the weights).  The block's sum is that of the
+            // pieces, so d (sum c x - sum x) cancels where c = 1.
+            const int fe = (int)((__float_as_uint(amax) >> 23) & 0xff) - 127;
+            const int eb = amax > 0.f ? min(120, max(-114, fe - 7)) : 0;
+            const float down = __uint_as_float((uint32_t)(127 - eb) << 23);   // 2^-eb
+            float tsum = 0.f;      // f32 x: what the pieces leave out, x 16^NJ
+            u32x4 pc[4];
+#pragma unroll
+            for (int dw = 0; dw < 4; dw++) {
+                uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+                for (int hf = 0; hf < 2; hf++) {
+                    // Bytes 2hf, 2hf+1 of dword dw: elements t0, t0 + 2.
+                    const int t0 = 8 * (dw & 1) + (dw >> 1) + 4 * hf;
+                    float a = f[t0 >> 2][t0 & 3] * down, b = f[(t0 + 2) >> 2][(t0 + 2) & 3] * down;
+#pragma unroll
+                    for (int jj = 0; jj < NJ; jj++) {
+                        const int o = (int)w[jj];
+                        w[jj] = (uint32_t)(hf ? __builtin_amdgcn_cvt_pk_fp8_f32(a, b, o, true)
+                                              : __builtin_amdgcn_cvt_pk_fp8_f32(a, b, o, false));
+                        // f16 x: three pieces hold it exactly (bar elements
+                        // 2^-14 of the block's max), so the last needs no
+                        // remainder.
+                        if (XT == 1 || jj < NJ - 1) {
+                            const int n = (int)w[jj];
+                            const f32x2 pv = hf ? __builtin_amdgcn_cvt_pk_f32_fp8(n, true)
+                                                : __builtin_amdgcn_cvt_pk_f32_fp8(n, false);
+                            a = (a - pv[0]) * 16.f;
+                            b = (b - pv[1]) * 16.f;
+                        }
+                    }
+                    if (XT == 1) tsum += a + b;
+                }
+#pragma unroll
+                for (int jj = 0; jj < 4; jj++) pc[jj][dw] = w[jj];
+            }
+            if (XT == 1) {
+                tsum += __shfl_xor(tsum, 1, 64);
+                tsum += __shfl_xor(tsum, 2, 64);
+                tsum += __shfl_xor(tsum, 4, 64);
+            }
+            if (e < nstage) {
+                u32x4 *dst = (u32x4 *)(xsb + bb * F4_BLK + 64 * i);
+#pragma unroll
+                for (int jj = 0; jj < 4; jj++) dst[jj] = pc[jj];
+                if (i == 7) {   // the padding: read as zeros by the idle lanes
+                    u32x4 *pad = (u32x4 *)(xsb + bb * F4_BLK + 512);
+#pragma unroll
+                    for (int jj = 0; jj < 4; jj++) pad[jj] = u32x4{0u, 0u, 0u, 0u};
+                }
+                if (i == 0 && bb < nblk) {
+                    // sum of the pieces: sum x less what they leave out
+                    sx[bb] = XT == 1 ? sum - tsum * 0x1p-16f * __uint_as_float((uint32_t)(127 + eb) << 23)
+                                     : sum;
+                    ((int *)ex)[bb] = 127 + eb;
+                }
+            }
+            return;
+        }
         // amax < 2^(E-126) for f32 exponent field E; amax * 16 * 2^-eb < 2^15.
         const int eb = min(111, max(0, (int)((__float_as_uint(amax) >> 23) & 0xff) - 137));
         const float down = __uint_as_float((uint32_t)(127 - eb) << 23);    // 2^-eb
@@ -408,7 +505,7 @@ __device__ void run(const Task &t, int wg, uint32_t *lds) {
     if constexpr (XT != 2)
         for (int e = threadIdx.x + MT; e < nstage; e += MT) stage(e, load_x(e));
 #pragma unroll
-    for (int p = 1; p < P; p++) issue(t, g, rg.it[p], rg.t[p], rg.sc[p]);
+    for (int p = 1; p < P; p++) issue<F4>(t, g, rg.it[p], rg.t[p], rg.sc[p]);
     __syncthreads();
 
     // One item (set c, step s): the four Q2 blocks 4s .. 4s+3 of 16 rows.
@@ -418,6 +515,71 @@ __device__ void run(const Task &t, int wg, uint32_t *lds) {
     // Accumulator chains: f16 x uses two, f32 x two for hi and two for lo.
     auto step = [&](const int it, u32x4 (&tile)[2], u32x2 &sc) {
         const int c = set_of(g, it), s = s0 + (it - c * L);
+        if constexpr (F4) {
+            // v_mfma_scale_f32_16x16x128_f8f6f4, A = fp4 weights, B = e4m3 x.
+            // A lane l holds row l%16 and K 32*(l/16) .. +31 of an MFMA,
+            // which this tile order makes Q2 block l/16 of the step: MFMA m
+            // takes code dwords 2m, 2m+1 (codes 32m .. 32m+31 of the block),
+            // even codes then odd, each c in the low two bits of a nibble,
+            // i.e. the e2m1 value c/2 (scale 2 restores c).  B column n =
+            // 4q + jp holds piece jp of block q's x and is zero elsewhere,
+            // so C[row][4q + jp] sums block q alone.  B lane l (column l%16)
+            // holds K 16*(l/16) .. +15 in bytes 0-15 and 64 + 16*(l/16) ..
+            // +15 in bytes 16-31: its data is chunk 2m + (l/16)%2 of block
+            // q, in the low half for q < 2 and the high half for q >= 2, and
+            // only where q%2 == (l/16)/2; the other half (and lanes jp >= NJ)
+            // read a zero region placed on other banks.  The B scale of lane
+            // l (column l%16, K block l/16) is 2^(e_q - 4 jp) where l/16 is q.
+            const int q = (lane >> 2) & 3, jp = lane & 3, G = lane >> 4;
+            const int blk = 4 * s + q;
+            const bool act = (q & 1) == (G >> 1) && jp < NJ;
+            const uint32_t zb = (uint32_t)((nblk + 3) * F4_BLK + 255) & ~255u;
+            const uint32_t dat = (uint32_t)(blk * F4_BLK + ((G & 1) * 4 + jp) * 16);
+            const uint32_t zer = zb + (uint32_t)((((q + (G & 1)) & 3) * 64) + jp * 16);
+            const uint32_t alo = act && q < 2 ? dat : zer, ahi = act && q >= 2 ? dat : zer;
+            const int bj = min(blk, nblk - 1);
+            const int ev = ((const int *)ex)[bj];
+            const int sb = G == q ? ev - 4 * jp : 127;
+            constexpr uint32_t M = 0x33333333u;
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int m = 0; m < 4; m++) {
+                const uint32_t w0 = tile[m >> 1][2 * (m & 1)], w1 = tile[m >> 1][2 * (m & 1) + 1];
+                const i32x8 a = {(int)(w0 & M), (int)((w0 >> 2) & M), (int)(w1 & M),
+                                 (int)((w1 >> 2) & M), 0, 0, 0, 0};
+                const u32x4 lo = *(const u32x4 *)(xsb + alo + m * 128);
+                const u32x4 hi = *(const u32x4 *)(xsb + ahi + m * 128);
+                const i32x8 b = {(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3],
+                                 (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+                acc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, acc, 4, 0, 0, 128, 0, sb);
+            }
+            // Lane l holds rows 4G + v, column l%16: sum the pieces (the
+            // quad), then d (x . c - sum x) for block q.
+            auto quad = [](float v) {
+                v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));
+                return v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));
+            };
+            const bool live = blk < nblk;
+            const float sxq = sx[bj];
+            const float dsc[4] = {gd_h2f((uint16_t)(sc[0] & 0xffff)), gd_h2f((uint16_t)(sc[0] >> 16)),
+                                  gd_h2f((uint16_t)(sc[1] & 0xffff)), gd_h2f((uint16_t)(sc[1] >> 16))};
+            f32x4 r;
+#pragma unroll
+            for (int v = 0; v < 4; v++) r[v] = quad(acc[v]);   // every lane: DPP reads its quad
+#pragma unroll
+            for (int v = 0; v < 4; v++) r[v] = live ? dsc[v] * (r[v] - sxq) : 0.f;
+            if constexpr (KBP) {
+                if (jp == 0) *(f32x4 *)(part + (it * 4 + q) * 16 + 4 * G) = r;
+            } else {
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    r[v] += __shfl_xor(r[v], 4, 64);
+                    r[v] += __shfl_xor(r[v], 8, 64);
+                }
+                if (lane == 16 * G) *(f32x4 *)(part + it * 16 + 4 * G) = r;
+            }
+            return;
+        }
         // MFMA block mb = lane/4 multiplies rows 4*rq .. 4*rq+3 of Q2 block
         // 4s + kb by four K values.  Blocks past the last (a short final
         // step) read zero-staged x and give zero products.
@@ -488,7 +650,7 @@ __device__ void run(const Task &t, int wg, uint32_t *lds) {
             if (lane == 0) gi = atomicAdd(&next_item, 1);
             if (rg.it[p] < total) step(rg.it[p], rg.t[p], rg.sc[p]);
             rg.it[p] = __builtin_amdgcn_readfirstlane(gi);
-            issue(t, g, rg.it[p], rg.t[p], rg.sc[p]);
+            issue<F4>(t, g, rg.it[p], rg.t[p], rg.sc[p]);
         }
     }
     __syncthreads();

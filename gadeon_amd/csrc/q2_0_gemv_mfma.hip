@@ -12,10 +12,19 @@ using gemv::NW;
 using gemv::NormIn;
 using gemv::xlds_bytes;
 
-template <int XT, bool KBP>
+template <int XT, bool KBP, bool F4>
 __global__ __launch_bounds__(64 * NW) void q2_0_gemv_mfma_kernel(gemv::Task t) {
     extern __shared__ __align__(16) uint32_t lds[];
-    gemv::run<XT, KBP>(t, (int)(blockIdx.y * gridDim.x + blockIdx.x), lds);
+    gemv::run<XT, KBP, F4>(t, (int)(blockIdx.y * gridDim.x + blockIdx.x), lds);
+}
+
+// x staging bytes of a GEMV over nblk Q2 blocks: the fp4 kernel's where its
+// staging and one set's per-block partials fit, else the f16 kernel's.
+struct XStage { size_t bytes; bool f4; };
+XStage x_stage(int nblk, bool f32x) {
+    const size_t f4 = gemv::xlds_bytes_f4(nblk);
+    if (f4 + (size_t)256 * ((nblk + 3) / 4) <= LDS_BYTES) return {f4, true};
+    return {xlds_bytes(nblk, f32x), false};
 }
 
 // Work split of a GEMV: `per` consecutive sets per workgroup, K cut into nz
@@ -70,16 +79,17 @@ int make_task(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, size_t xlds
 }
 
 template <int XT>
-int launch(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, size_t xlds,
+int launch(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, XStage xs,
            const NormIn &nin = NormIn{nullptr, nullptr, nullptr, 0.f, 0, 0}, int ksplit = 1,
            const GluOut &glu = GluOut{nullptr, 0}, const float *bias = nullptr) {
     const int cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
     gemv::Task t;
     size_t lds;
     bool kbp;
-    int rc = make_task(ctx, w, x, y, xlds, nin, ksplit, glu, cus, bias, &t, &lds, &kbp);
+    int rc = make_task(ctx, w, x, y, xs.bytes, nin, ksplit, glu, cus, bias, &t, &lds, &kbp);
     if (rc) return rc;
-    auto kern = kbp ? q2_0_gemv_mfma_kernel<XT, true> : q2_0_gemv_mfma_kernel<XT, false>;
+    auto kern = xs.f4 ? (kbp ? q2_0_gemv_mfma_kernel<XT, true, true> : q2_0_gemv_mfma_kernel<XT, false, true>)
+                      : (kbp ? q2_0_gemv_mfma_kernel<XT, true, false> : q2_0_gemv_mfma_kernel<XT, false, false>);
     hipLaunchKernelGGL(kern, dim3((unsigned)t.gx, t.nz), dim3(64 * NW), lds, ctx->stream, t);
     GD_LAUNCHED(ctx, "q2_0_gemv_mfma");
     return GD_OK;
@@ -97,14 +107,14 @@ int gd_gemv_mfma(gd_ctx *ctx, const gd_q2w *w, const void *x, int x_dtype, float
     const int64_t K = w->K;
     const int XT = x_dtype == GD_F32 ? 1 : 0;
     const int nblk = (int)(K >> 7);
-    const size_t xlds = xlds_bytes(nblk, XT);
-    GD_REQUIRE(ctx, xlds + (size_t)64 * ((nblk + 3) / 4) <= LDS_BYTES,
+    const XStage xs = x_stage(nblk, XT);
+    GD_REQUIRE(ctx, xs.bytes + (size_t)64 * ((nblk + 3) / 4) <= LDS_BYTES,
                "gd_q2_0_gemv: K=%lld too long for LDS staging of %s x", (long long)K,
                XT ? "f32" : "f16");
     const NormIn none{nullptr, nullptr, nullptr, 0.f, 0, 0};
     const GluOut noglu{nullptr, 0};
-    return XT ? launch<1>(ctx, w, x, y, xlds, none, ksplit, noglu, bias)
-              : launch<0>(ctx, w, x, y, xlds, none, ksplit, noglu, bias);
+    return XT ? launch<1>(ctx, w, x, y, xs, none, ksplit, noglu, bias)
+              : launch<0>(ctx, w, x, y, xs, none, ksplit, noglu, bias);
 }
 
 // K splits (1..4) for an f16-x GEMV whose partial rows the consumer can sum:
@@ -114,7 +124,7 @@ int gd_gemv_mfma(gd_ctx *ctx, const gd_q2w *w, const void *x, int x_dtype, float
 // splits the launch will actually make.
 int gd_gemv_ksplit(gd_ctx *ctx, int64_t K, int64_t R) {
     const int nblk = (int)(K >> 7), steps = (nblk + 3) / 4;
-    const size_t xlds = xlds_bytes(nblk, false);
+    const size_t xlds = x_stage(nblk, false).bytes;
     if (K % 128 || xlds + (size_t)64 * steps > LDS_BYTES) return 1;
     const int cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
     const int64_t nsets = (R + 15) / 16;
@@ -144,11 +154,11 @@ int gd_gemv_mfma_norm(gd_ctx *ctx, const gd_q2w *w, const float *h, const float 
                       int dstride, const float *normw, float eps, float *hout, float *y,
                       uint16_t *glu_out) {
     const int nblk = (int)(w->K >> 7);
-    const size_t xlds = xlds_bytes(nblk, false);
+    const XStage xs = x_stage(nblk, false);
     GD_REQUIRE(ctx, (nblk + 5) * 8 <= 1024, "gd_gemv_norm: K=%lld too long (at most 15744)",
                (long long)w->K);
     GD_REQUIRE(ctx, !glu_out || w->R % 32 == 0, "gd_gemv_norm: SwiGLU needs R = 2 x 16k rows");
     const GluOut glu{glu_out, glu_out ? (int)(w->R / 32) : 0};
-    return launch<2>(ctx, w, h, y, xlds, NormIn{delta, normw, hout, eps, delta ? nd : 0, dstride}, 1,
+    return launch<2>(ctx, w, h, y, xs, NormIn{delta, normw, hout, eps, delta ? nd : 0, dstride}, 1,
                      glu);
 }

@@ -455,6 +455,57 @@ def test_gemv_large_x_blocks(ctx, xt, K, R, ksplit):
     ctx.free(dy)
 
 
+@pytest.mark.parametrize("xt", [ga.F16, ga.F32])
+@pytest.mark.parametrize("K,R", [(5120, 777), (17408, 130), (30720, 48)])
+def test_gemv_sparse_outliers(ctx, xt, K, R):
+    """Every 97th element of x 3000 times larger than the rest (outlier
+    channels).  The fp4 body's matrix cores add products in groups of 8
+    aligned to the largest, so small x beside an outlier lose low bits: the
+    bound is 1e-3 here (measured about 1.7e-4), against the 1e-2 the
+    GEMV contract allows."""
+    blocks = O.lcg_q2_0(K, R, 3 * K + R)
+    w = upload_w(ctx, blocks, K, R)
+    x = O.lcg_normal(K, 23) * np.where(np.arange(K) % 97 == 0, 3000.0, 1.0).astype(np.float32)
+    if xt == ga.F16:
+        xh = x.astype(np.float16)
+        x_ref = xh.astype(np.float32)
+        dx = ctx.put(xh.view(np.uint16))
+    else:
+        x_ref = x.astype(np.float32)
+        dx = ctx.put(x_ref)
+    dy = ctx.alloc(R * 4)
+    ctx.gd_q2_0_gemv(C.byref(w), dx, xt, dy)
+    want = O.q2_0_matvec(blocks, K, R, x_ref, threads=8)
+    assert rel_diff(ctx.get(dy, R, np.float32), want) < 1e-3
+    free_w(ctx, w)
+    ctx.free(dx)
+    ctx.free(dy)
+
+
+@pytest.mark.parametrize("xt,K,R", [(ga.F16, 32768, 100), (ga.F16, 65536, 40), (ga.F32, 32768, 100)])
+def test_gemv_long_k(ctx, xt, K, R):
+    """K past what the fp4 body stages in LDS (about 30K) runs the f16 body,
+    with plain and sparse-outlier x, at the plain GEMV's tolerance."""
+    blocks = O.lcg_q2_0(K, R, K + 11 * R)
+    w = upload_w(ctx, blocks, K, R)
+    for scale in (1.0, 3000.0):
+        x = O.lcg_normal(K, 29) * np.where(np.arange(K) % 97 == 0, scale, 1.0).astype(np.float32)
+        if xt == ga.F16:
+            xh = x.astype(np.float16)
+            x_ref = xh.astype(np.float32)
+            dx = ctx.put(xh.view(np.uint16))
+        else:
+            x_ref = x.astype(np.float32)
+            dx = ctx.put(x_ref)
+        dy = ctx.alloc(R * 4)
+        ctx.gd_q2_0_gemv(C.byref(w), dx, xt, dy)
+        want = O.q2_0_matvec(blocks, K, R, x_ref, threads=8)
+        assert rel_diff(ctx.get(dy, R, np.float32), want) < 1e-4
+        ctx.free(dx)
+        ctx.free(dy)
+    free_w(ctx, w)
+
+
 def test_gemv_norm_large_norm_weight(ctx):
     """Fused add + RMSNorm input whose norm weight is large on some blocks,
     so the staged f16 x reaches |x| in the thousands there."""
