@@ -110,7 +110,33 @@ static inline unsigned gd_blocks(int64_t n, int per) {
 //           (lane = 16*kb + r), one contiguous 1 KiB per load instruction.
 //   scales: [row group][block/16][block%16][r] f16, so the 16 rows of a block
 //           are 32 contiguous bytes.
+//   Inside each code dword (16 codes of a block) the codes are interleaved by
+//   nibble: code i < 8 at bits 4i, code 8 + i at bits 4i + 2.  A mask (w &
+//   0x33333333, or (w >> 2) & 0x33333333) then leaves 8 consecutive codes c
+//   as the e2m1 nibbles c/2, the fp4 operand order of the matrix cores and
+//   of the fp4 -> f16 conversion.
 // Rows past R and blocks past K/128 are padding and hold zeros.
+__host__ __device__ constexpr int gd_q2_bitpos(int i) { return i < 8 ? 4 * i : 4 * (i - 8) + 2; }
+// 2-bit fields of a 16-bit value spread to the low bits of 8 nibbles, and back.
+__host__ __device__ inline uint32_t gd_q2_spread(uint32_t x) {
+    x &= 0xffffu;
+    x = (x | (x << 8)) & 0x00ff00ffu;
+    x = (x | (x << 4)) & 0x0f0f0f0fu;
+    return (x | (x << 2)) & 0x33333333u;
+}
+__host__ __device__ inline uint32_t gd_q2_gather(uint32_t x) {
+    x &= 0x33333333u;
+    x = (x | (x >> 2)) & 0x0f0f0f0fu;
+    x = (x | (x >> 4)) & 0x00ff00ffu;
+    return (x | (x >> 8)) & 0xffffu;
+}
+// A code dword as the GGUF block stores it (code i at bits 2i) <-> device.
+__host__ __device__ inline uint32_t gd_q2_to_dev(uint32_t w) {
+    return gd_q2_spread(w) | (gd_q2_spread(w >> 16) << 2);
+}
+__host__ __device__ inline uint32_t gd_q2_from_dev(uint32_t w) {
+    return gd_q2_gather(w) | (gd_q2_gather(w >> 2) << 16);
+}
 __host__ __device__ inline int64_t gd_q2_steps(int64_t K) { return (K / 128 + 3) / 4; }
 __host__ __device__ inline int64_t gd_q2_bgroups(int64_t K) { return (K / 128 + 15) / 16; }
 __host__ __device__ inline int64_t gd_q2_rgroups(int64_t R) { return (R + 15) / 16; }

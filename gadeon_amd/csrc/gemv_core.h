@@ -94,20 +94,23 @@ __host__ __device__ inline size_t xlds_bytes_f4(int nblk) {
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
-// Operand dword m holds codes (m, m+8) of w at bit position POS[m] of its
-// two f16 halves; the x pair it meets is pre-scaled by XSCALE[m] = 2^(8-POS[m]).
+// Operand dword m holds codes (PA[m], PA[m] + 4) of w (the device order:
+// code i < 8 at bit 4i, 8 + i at 4i + 2, so codes a and a + 4 share a
+// position in the two halves) at bit position POS[m] of its two f16 halves;
+// the x pair it meets is pre-scaled by XSCALE[m] = 2^(8-POS[m]).
 __device__ __forceinline__ void unpack_dword(uint32_t w, uint32_t (&t)[8]) {
     constexpr uint32_t M4 = 0x00300030u, M6 = 0x00C000C0u, M8 = 0x03000300u;
     const uint32_t u = w << 4, v = w >> 6;
-    t[0] = u & M4;     // code 0 at bit 4
-    t[1] = u & M6;     // code 1 at bit 6
-    t[2] = w & M4;     // code 2 at bit 4
-    t[3] = w & M6;     // code 3 at bit 6
-    t[4] = w & M8;     // code 4 at bit 8
-    t[5] = v & M4;     // code 5 at bit 4
-    t[6] = v & M6;     // code 6 at bit 6
-    t[7] = v & M8;     // code 7 at bit 8
+    t[0] = u & M4;     // codes 0, 4 at bit 4
+    t[1] = u & M6;     // codes 8, 12 at bit 6
+    t[2] = w & M4;     // codes 1, 5 at bit 4
+    t[3] = w & M6;     // codes 9, 13 at bit 6
+    t[4] = w & M8;     // codes 2, 6 at bit 8
+    t[5] = v & M4;     // codes 10, 14 at bit 4
+    t[6] = v & M6;     // codes 3, 7 at bit 6
+    t[7] = v & M8;     // codes 11, 15 at bit 8
 }
+__device__ constexpr int PA[8] = {0, 8, 1, 9, 2, 10, 3, 11};
 __device__ constexpr float XSCALE[8] = {16.f, 4.f, 16.f, 4.f, 1.f, 16.f, 4.f, 1.f};
 
 // Two f32 -> two f16 (RNE) in one dword.
@@ -336,7 +339,7 @@ __device__ void run(const Task &t, int wg, uint32_t *lds) {
     issue<F4>(t, g, rg.it[0], rg.t[0], rg.sc[0]);
     if (threadIdx.x == 0) next_item = NW * P;
 
-    // Stage x: pair p = 8i + k of block b holds (x[b,16i+k], x[b,16i+k+8]) *
+    // Stage x: pair p = 8i + k of block b holds (x[b,16i+PA[k]], x[b,16i+PA[k]+4]) *
     // XSCALE[k] * 2^-e_b.  Thread (b, i) forms the 8 pairs of x[16i ..
     // 16i+15] in registers and writes them as 32 bytes; the block's sum and
     // max|x| come from 8-lane shuffles.  e_b = 0 unless max|x| >= 2048.
@@ -372,8 +375,8 @@ __device__ void run(const Task &t, int wg, uint32_t *lds) {
             // x = 2^e (p0 + p1/16 + p2/256 [+ p3/4096]), e4m3 pieces with
             // max|x| 2^-e in [128, 256): p0 = e4m3(x 2^-e), each later piece
             // the e4m3 of 16 times what is left.  Piece j of the chunk goes
-            // to slot j as 16 bytes, the even elements first (the order the
-            // fp4 unpack gives the weights).  The block's sum is that of the
+            // to slot j as 16 bytes in element order (the order the masked
+            // code dwords give the weights).  The block's sum is that of the
             // pieces, so d (sum c x - sum x) cancels where c = 1.
             const int fe = (int)((__float_as_uint(amax) >> 23) & 0xff) - 127;
             const int eb = amax > 0.f ? min(120, max(-114, fe - 7)) : 0;
@@ -385,9 +388,8 @@ __device__ void run(const Task &t, int wg, uint32_t *lds) {
                 uint32_t w[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
                 for (int hf = 0; hf < 2; hf++) {
-                    // Bytes 2hf, 2hf+1 of dword dw: elements t0, t0 + 2.
-                    const int t0 = 8 * (dw & 1) + (dw >> 1) + 4 * hf;
-                    float a = f[t0 >> 2][t0 & 3] * down, b = f[(t0 + 2) >> 2][(t0 + 2) & 3] * down;
+                    // Bytes 2hf, 2hf+1 of dword dw: elements 4dw + 2hf, +1.
+                    float a = f[dw][2 * hf] * down, b = f[dw][2 * hf + 1] * down;
 #pragma unroll
                     for (int jj = 0; jj < NJ; jj++) {
                         const int o = (int)w[jj];
@@ -438,8 +440,9 @@ __device__ void run(const Task &t, int wg, uint32_t *lds) {
         u32x4 p0, p1, q0, q1;
 #pragma unroll
         for (int k = 0; k < 8; k++) {
-            // pair k = (x[16i+k], x[16i+k+8]) = (f[k/4][k%4], f[2+k/4][k%4])
-            const float xa = f[k >> 2][k & 3] * down, xb = f[2 + (k >> 2)][k & 3] * down;
+            // pair k = (x[16i + PA[k]], x[16i + PA[k] + 4])
+            const int ea = PA[k], eb = PA[k] + 4;
+            const float xa = f[ea >> 2][ea & 3] * down, xb = f[eb >> 2][eb & 3] * down;
             const float ha = (float)(f16)xa, hb = (float)(f16)xb;
             const uint32_t hp = pack_h2(ha * XSCALE[k], hb * XSCALE[k]);
             if (k < 4) p0[k] = hp; else p1[k - 4] = hp;
@@ -519,9 +522,10 @@ __device__ void run(const Task &t, int wg, uint32_t *lds) {
             // v_mfma_scale_f32_16x16x128_f8f6f4, A = fp4 weights, B = e4m3 x.
             // A lane l holds row l%16 and K 32*(l/16) .. +31 of an MFMA,
             // which this tile order makes Q2 block l/16 of the step: MFMA m
-            // takes code dwords 2m, 2m+1 (codes 32m .. 32m+31 of the block),
-            // even codes then odd, each c in the low two bits of a nibble,
-            // i.e. the e2m1 value c/2 (scale 2 restores c).  B column n =
+            // takes code dwords 2m, 2m+1 (codes 32m .. 32m+31 of the block,
+            // in order: the device order interleaves a dword's two halves by
+            // nibble), each c in the low two bits of a nibble, i.e. the e2m1
+            // value c/2 (scale 2 restores c).  B column n =
             // 4q + jp holds piece jp of block q's x and is zero elsewhere,
             // so C[row][4q + jp] sums block q alone.  B lane l (column l%16)
             // holds K 16*(l/16) .. +15 in bytes 0-15 and 64 + 16*(l/16) ..

@@ -15,10 +15,11 @@
 //     ring of 128-K blocks (X, each wave's codes and row scales); the next
 //     block's loads go out right after the barrier that opens this one.
 //   * Each lane expands the 2-bit codes of its own B operand in registers to
-//     (code-1)*d in f16 -- exact, as in dq_q2_0_h.  To make a lane's codes
-//     one 16-bit word, the K order inside each 64-K slice is permuted: lane
-//     half h, step s, element e carries K = 32h + 8s + e, for X and W alike
-//     (a sum over K does not care).
+//     (code-1)*d in f16 -- exact, as in dq_q2_0_h -- by the hardware fp4 ->
+//     f16 conversion and one fused multiply-add per two weights.  To make a
+//     lane's codes one masked code dword, the K order inside each 64-K slice
+//     is permuted: lane half h, step s, element e carries K = 32h + 8s + e,
+//     for X and W alike (a sum over K does not care).
 //   * Short-R shapes split K into f32 partials that the caller sums, so that
 //     every CU gets work; a cost model picks the tile and the split.
 #include "gd_internal.h"
@@ -34,23 +35,21 @@ constexpr int BK = 64;           // K per LDS stage (half a Q2_0 block)
 #endif
 constexpr int PD = GD_GEMM_PD;   // K-steps of A/B prefetch in the inner loop
 
-// Eight codes (bits 0..15 of `u`, code i at bits 2i) -> eight f16 of
-// (code-1)*d, in K order.  s = u | u << 14 puts code 2m+1 (bits 4m+2..3) at
-// bits 4m+16..17, so (s >> 4m) & 0x00030003 holds codes 2m and 2m+1 at the
-// bottom of each half; 0x6400 | c is the f16 value 1024 + c, subtracting 1025
-// leaves c - 1 exactly, and the product with d is exact.
-__device__ __forceinline__ f16x8 dequant8(uint32_t u, f16x2 d2) {
-    const f16x2 off = {(f16)-1025.0f, (f16)-1025.0f};
-    const uint32_t sp = u | (u << 14);
+// Eight codes (c in the low two bits of the nibbles of v, in K order: the
+// device order after one mask) -> eight f16 of (code-1)*d.  Each nibble is
+// the e2m1 value c/2, so the fp4 -> f16 conversion with scale 2 gives c
+// exactly, two per instruction, and the fused c*d - d rounds once to the
+// exact (c-1)*d, as dq_q2_0_h's half product is exact.
+__device__ __forceinline__ f16x8 dequant8(uint32_t v, f16x2 d2, f16x2 nd2) {
+    const f16x2 c0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(v, 2.0f, 0);
+    const f16x2 c1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(v, 2.0f, 1);
+    const f16x2 c2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(v, 2.0f, 2);
+    const f16x2 c3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(v, 2.0f, 3);
     u32x4 r;
-#pragma unroll
-    for (int m = 0; m < 4; m++) {
-        uint32_t bits;
-        asm("v_and_or_b32 %0, %1, %2, %3"
-            : "=v"(bits) : "v"(sp >> (4 * m)), "v"(0x00030003u), "s"(0x64006400u));
-        const f16x2 v = __builtin_bit_cast(f16x2, bits) + off;
-        r[m] = __builtin_bit_cast(uint32_t, v * d2);
-    }
+    r[0] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(c0, d2, nd2));
+    r[1] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(c1, d2, nd2));
+    r[2] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(c2, d2, nd2));
+    r[3] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(c3, d2, nd2));
     return __builtin_bit_cast(f16x8, r);
 }
 
@@ -198,12 +197,13 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
     // waits on an LDS read issued PD steps earlier.
     auto compute = [&](int st) {
         const uint8_t *base = lds + st * St::BYTES;
-        f16x2 d2[NT];
+        f16x2 d2[NT], nd2[NT];
         u32x2 cw[2][NT];
 #pragma unroll
         for (int n = 0; n < NT; n++) {
             const f16 d = *(const f16 *)(base + St::S + (wave * NT + n) * 256 + 4 * li);
             d2[n] = f16x2{d, d};
+            nd2[n] = -d2[n];
 #pragma unroll
             for (int h = 0; h < 2; h++)
                 cw[h][n] = *(const u32x2 *)(base + St::C + (wave * NT + n) * 1024 + (h * 32 + li) * 16 + 8 * lh);
@@ -217,8 +217,11 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
         auto build_b = [&](int j, int slot) {
             const int h = j >> 2, ks = j & 3;
 #pragma unroll
-            for (int n = 0; n < NT; n++)
-                b[slot][n] = dequant8((cw[h][n][ks >> 1] >> (16 * (ks & 1))) & 0xffffu, d2[n]);
+            for (int n = 0; n < NT; n++) {
+                // Codes 0..7 of the dword for even ks, 8..15 for odd.
+                const uint32_t w = cw[h][n][ks >> 1];
+                b[slot][n] = dequant8((ks & 1 ? w >> 2 : w) & 0x33333333u, d2[n], nd2[n]);
+            }
         };
 #pragma unroll
         for (int j = 0; j < PD; j++) read_a(j, j);

@@ -36,7 +36,7 @@ __global__ void q2_0_dequant_rows_kernel(const uint8_t *__restrict__ codes,
     for (int i = 0; i < 4; i++) {
         f32x4 v;
 #pragma unroll
-        for (int j = 0; j < 4; j++) v[j] = (float)((int)((word >> (2 * (4 * i + j))) & 3u) - 1) * d;
+        for (int j = 0; j < 4; j++) v[j] = (float)((int)((word >> gd_q2_bitpos(4 * i + j)) & 3u) - 1) * d;
         dst[i] = v;
     }
 }

@@ -342,8 +342,9 @@ extern "C" int gd_q2w_free(gd_ctx *ctx, gd_q2w *w) {
 }
 
 // One thread per 34-byte GGUF block (row-major order) of rows [row0, ...).  The GGUF side is only
-// 2-byte aligned, so it is read as 17 halfwords; the code bytes go to their
-// two 16-byte slots of the row group's tile, the scale to its slot.
+// 2-byte aligned, so it is read as 17 halfwords; the code dwords go, nibble-
+// interleaved, to their two 16-byte slots of the row group's tile, the scale
+// to its slot.
 __global__ void gd_repack_kernel(const uint16_t *src, uint8_t *codes, uint16_t *scales,
                                  int64_t nblk, int64_t row0, int64_t nblocks) {
     const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -357,7 +358,7 @@ __global__ void gd_repack_kernel(const uint16_t *src, uint8_t *codes, uint16_t *
         u32x4 v;
 #pragma unroll
         for (int j = 0; j < 4; j++)
-            v[j] = (uint32_t)p[1 + 8 * h + 2 * j] | ((uint32_t)p[2 + 8 * h + 2 * j] << 16);
+            v[j] = gd_q2_to_dev((uint32_t)p[1 + 8 * h + 2 * j] | ((uint32_t)p[2 + 8 * h + 2 * j] << 16));
         *(u32x4 *)(codes + gd_q2_code_off(row, blk, h, steps)) = v;
     }
 }
@@ -376,8 +377,9 @@ __global__ void gd_export_kernel(const uint8_t *codes, const uint16_t *scales, u
         const u32x4 v = *(const u32x4 *)(codes + gd_q2_code_off(row, blk, h, steps));
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            p[1 + 8 * h + 2 * j] = (uint16_t)(v[j] & 0xffff);
-            p[2 + 8 * h + 2 * j] = (uint16_t)(v[j] >> 16);
+            const uint32_t g = gd_q2_from_dev(v[j]);
+            p[1 + 8 * h + 2 * j] = (uint16_t)(g & 0xffff);
+            p[2 + 8 * h + 2 * j] = (uint16_t)(g >> 16);
         }
     }
 }
@@ -528,7 +530,7 @@ __global__ void gd_rand_codes_kernel(uint8_t *codes, int64_t K, size_t nweights,
         for (int j = 0; j < 16; j++) {
             s = s * GD_LCG_A + GD_LCG_C;
             const uint32_t c = (uint32_t)(((uint64_t)lcg_bits(s) * 3u) >> 31);
-            word |= c << (2 * j);
+            word |= c << gd_q2_bitpos(j);
         }
         v[w] = word;
     }
