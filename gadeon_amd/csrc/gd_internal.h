@@ -57,7 +57,10 @@ gd_gemm_plan gd_gemm_choose(gd_ctx *ctx, int64_t T, int64_t K, int64_t R, int x_
 int gd_gemm_launch(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, int x_dtype, void *Y,
                    int y_dtype, const gd_gemm_plan &p);
 // SwiGLU GEMM: w = [gate; up] (2 * ff rows), f16 X [T][K] -> f16 out [T][ff].
-int gd_gemm_glu(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, uint16_t *out);
+// tile17: -1 the planner's choice, 1 one launch of the 17-fragment (4, 2, 8)
+// tile, 0 the planner's choice among the others.
+int gd_gemm_glu(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, uint16_t *out,
+                int tile17 = -1);
 
 // Attention kernels (attention.hip) for head dims 128 and 256, as the stack
 // launches them: prefill prep (q/k norm + rope + cache append), flash

@@ -25,6 +25,7 @@
 #include "gd_internal.h"
 
 #include <cstdlib>
+#include <type_traits>
 #include <cstdio>
 
 namespace {
@@ -81,11 +82,12 @@ __device__ __forceinline__ void lds_load2(__amdgpu_buffer_rsrc_t r, const void *
 // (lanes 0..31: first half of the block, 32..63: second half, 16 bytes a
 // row) and the 32 row scales (one dword each, the f16 in its low half; the
 // upper 32 dwords repeat them).
-template <int MT, int NT, int NW> struct Stage {
+template <int MT, int NT, int NW, int EX> struct Stage {
     static constexpr int BT = MT * 32;
     static constexpr int XPLANE = BT * 128;
-    static constexpr int X = 0, C = 2 * XPLANE, S = C + NW * NT * 1024;
-    static constexpr int BYTES = S + NW * NT * 256;
+    static constexpr int NF = NW * NT + EX;               // weight fragments
+    static constexpr int X = 0, C = 2 * XPLANE, S = C + NF * 1024;
+    static constexpr int BYTES = S + NF * 256;
 };
 
 // MT x 32 tokens by NW * NT * 32 weight rows per workgroup of NW waves (the
@@ -98,13 +100,18 @@ template <int MT, int NT, int NW> struct Stage {
 // the columns glu_r0 <= r < glu_end of this launch (Yv has glu_ff columns):
 // lanes 0..15 of a wave's fragment take gate rows g .. g+15 and lanes
 // 16..31 up rows glu_ff + g .., so one shuffle pairs them; each wave holds
-// NT such fragments.
-template <int MT, int NT, int NW, int YT>
+// NT such fragments.  EX = 1 (SwiGLU, one split, 4 x 2 x 8 tiles only): the
+// workgroup also holds a seventeenth fragment after its NW * NT, whose 32
+// MFMAs per block the waves share (wave w: token tile w % 4, the K-steps of
+// parity w / 4; waves 4..7 hand their sums to waves 0..3 at the end), so
+// that ff = 17408 = 64 x 272 columns fill one round of 256 workgroups.
+template <int MT, int NT, int NW, int YT, int EX = 0>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) void q2_0_gemm_kernel(
         const uint8_t *__restrict__ codes, const uint16_t *__restrict__ scales,
         const void *__restrict__ Xv, void *__restrict__ Yv, int T, int K, int R, int bps,
         int nrt, int nz, int per, int glu_ff, int glu_r0, int glu_end) {
-    using St = Stage<MT, NT, NW>;
+    static_assert(!EX || (MT == 4 && NT == 2 && NW == 8 && YT == 0), "EX: 4 x 2 x 8 SwiGLU tiles");
+    using St = Stage<MT, NT, NW, EX>;
     constexpr int BT = St::BT;
     __shared__ __attribute__((aligned(16))) uint8_t lds[2 * St::BYTES];
 
@@ -120,8 +127,11 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
     const int li = lane & 31, lh = lane >> 5;
     const int t0 = tt * BT;
     // This wave's first row (SwiGLU: first gate row, 16 per fragment).
-    const int rw = glu_ff ? glu_r0 + rt * (16 * NW * NT) + wave * (16 * NT)
+    const int rw = glu_ff ? glu_r0 + rt * (16 * St::NF) + wave * (16 * NT)
                           : rt * (NW * NT * 32) + wave * (NT * 32);
+    // EX: the extra fragment's first gate row, and this wave's share of it.
+    const int xr = glu_r0 + rt * (16 * St::NF) + 16 * NW * NT;
+    const int xm = wave & 3, xpar = wave >> 2;
     const int nblk = K >> 7;
     const int csteps = (nblk + 3) >> 2;
     const int bgroups = (nblk + 15) >> 4;
@@ -139,6 +149,11 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
             gd_rsrc(codes + ((size_t)g0 * csteps << 11), gvalid * (uint32_t)csteps * 2048u);
     const __amdgpu_buffer_rsrc_t srs =
             gd_rsrc(scales + (size_t)g0 * bgroups * 256, gvalid * (uint32_t)bgroups * 512u);
+    // EX: the extra fragment's gate and up row groups (its loads are wave 0's).
+    const int gx = xr >> 4;
+    const uint32_t gvx = EX ? (uint32_t)max(0, min((glu_ff >> 4) + 1, rgroups - gx)) : 0u;
+    const __amdgpu_buffer_rsrc_t xcrs = gd_rsrc(codes + ((size_t)gx * csteps << 11), gvx * (uint32_t)csteps * 2048u);
+    const __amdgpu_buffer_rsrc_t xsrs = gd_rsrc(scales + (size_t)gx * bgroups * 256, gvx * (uint32_t)bgroups * 512u);
 
     // X loads: 1 KB chunks q = wave + NW i of a stage (plane q / (BT/8), rows
     // 8 (q % (BT/8)) ..); lane l fills physical chunk l%8 of row l/8, which
@@ -162,6 +177,9 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
         cvo[n] = ((uint32_t)(g * csteps) << 11) + ((uint32_t)lh << 10) + ((li & 15) << 4);
         svo[n] = ((uint32_t)g * bgroups * 256 + (li & 15)) * 2;
     }
+    const int gxu = (li >> 4) ? (glu_ff >> 4) : 0;        // EX: gate or up rows
+    const uint32_t xcvo = ((uint32_t)(gxu * csteps) << 11) + ((uint32_t)lh << 10) + ((li & 15) << 4);
+    const uint32_t xsvo = ((uint32_t)gxu * bgroups * 256 + (li & 15)) * 2;
     // Issue every load of block blk into stage st.
     auto issue = [&](int blk, int st) {
         uint8_t *base = lds + st * St::BYTES;
@@ -175,6 +193,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
         for (int n = 0; n < NT; n++) {
             lds_load16(crs, base + St::C + (wave * NT + n) * 1024, cvo[n], cs);
             lds_load2(srs, base + St::S + (wave * NT + n) * 256, svo[n], ss);
+        }
+        if (EX && wave == 0) {
+            lds_load16(xcrs, base + St::C + NW * NT * 1024, xcvo, cs);
+            lds_load2(xsrs, base + St::S + NW * NT * 256, xsvo, ss);
         }
     };
 
@@ -190,12 +212,21 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
         for (int n = 0; n < NT; n++)
 #pragma unroll
             for (int v = 0; v < 16; v++) acc[m][n][v] = 0.f;
+    f32x16 accx;                                          // EX: this wave's share
+#pragma unroll
+    for (int v = 0; v < 16; v++) accx[v] = 0.f;
 
     // One block from stage st: eight K-steps of 16 (two 64-K halves).  The
     // A fragments of step j + PD are read and the B fragments of step j + 1
     // built before step j's MFMAs issue, across the halves, so an MFMA only
-    // waits on an LDS read issued PD steps earlier.
+    // waits on an LDS read issued PD steps earlier.  EX: on the even steps j
+    // the wave also multiplies token tile xm by the extra fragment at K-step
+    // j + xpar, its A fragment and code dword read two steps ahead (by
+    // address: xm and xpar are not constants).
     auto compute = [&](int st) {
+        // EX reads A one step ahead (not PD): the extra fragment's registers
+        // would not fit beside a third A slot.
+        constexpr int PD = ::PD;
         const uint8_t *base = lds + st * St::BYTES;
         f16x2 d2[NT], nd2[NT];
         u32x2 cw[2][NT];
@@ -208,6 +239,22 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
             for (int h = 0; h < 2; h++)
                 cw[h][n] = *(const u32x2 *)(base + St::C + (wave * NT + n) * 1024 + (h * 32 + li) * 16 + 8 * lh);
         }
+        f16x2 dx2, ndx2;
+        f16x8 ax;
+        uint32_t wx = 0;
+        if constexpr (EX) {
+            const f16 d = *(const f16 *)(base + St::S + NW * NT * 256 + 4 * li);
+            dx2 = f16x2{d, d};
+            ndx2 = -dx2;
+        }
+        // The A fragment and code dword of the extra fragment's K-step j +
+        // xpar (j even: the plane and the code dword do not depend on xpar).
+        auto read_ax = [&](int j) {
+            const uint32_t ka = (uint32_t)li * 128 + (((4 * lh + (j & 3) + xpar) ^ xswz(li)) << 4);
+            ax = *(const f16x8 *)(base + St::X + (j >> 2) * St::XPLANE + ka + xm * 4096);
+            wx = *(const uint32_t *)(base + St::C + NW * NT * 1024 + ((j >> 2) * 32 + li) * 16 + 8 * lh +
+                                     4 * ((j & 3) >> 1));
+        };
         f16x8 a[PD + 1][MT], b[2][NT];
         auto read_a = [&](int j, int slot) {
             const uint8_t *xb = base + St::X + (j >> 2) * St::XPLANE;
@@ -226,6 +273,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
 #pragma unroll
         for (int j = 0; j < PD; j++) read_a(j, j);
         build_b(0, 0);
+        if constexpr (EX) read_ax(0);
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             // The reads go out PD steps ahead; the fence keeps the compiler
@@ -240,6 +288,13 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
 #pragma unroll
                 for (int n = 0; n < NT; n++)
                     acc[m][n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[cur][m], b[j & 1][n], acc[m][n], 0, 0, 0);
+            if constexpr (EX) {
+                if ((j & 1) == 0) {
+                    const f16x8 bx = dequant8((wx >> (2 * xpar)) & 0x33333333u, dx2, ndx2);
+                    accx = __builtin_amdgcn_mfma_f32_32x32x16_f16(ax, bx, accx, 0, 0, 0);
+                    if (j + 2 < 8) read_ax(j + 2);
+                }
+            }
         }
     };
 
@@ -298,25 +353,42 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
         const bool gl = li < 16;
         const __amdgpu_buffer_rsrc_t ors =
                 gd_rsrc((uint16_t *)Yv + (size_t)t0 * glu_ff, (uint32_t)rows_t * glu_ff * 2u);
-#pragma unroll
-        for (int n = 0; n < NT; n++) {
-            const int g = rw + 16 * n + (li & 15);
+        // One 32 x 32 accumulator tile: token tile m, this lane's gate row g.
+        auto glu_tile = [&](const f32x16 &t, int m, int g) {
             const uint32_t obase = ((uint32_t)(4 * lh + (gl ? 0 : 16)) * glu_ff + g) * 2u;
             if (g < glu_end) {
 #pragma unroll
-                for (int m = 0; m < MT; m++)
+                for (int q = 0; q < 8; q++) {
+                    // Both elements first, then a select: a lane-dependent
+                    // index would compile to a 16-way select chain.
+                    const float lo = t[q], hi = t[8 + q];
+                    const float other = __shfl_xor(gl ? hi : lo, 16, 64);
+                    const float mine = gl ? lo : hi;
+                    const float gate = gl ? mine : other, up = gl ? other : mine;
+                    const float sg = gate * __builtin_amdgcn_rcpf(1.0f + __expf(-gate));
+                    const uint32_t so = (uint32_t)(m * 32 + 8 * (q >> 2) + (q & 3)) * glu_ff * 2u;
+                    __builtin_amdgcn_raw_buffer_store_b16(gd_f2h(sg * up), ors, obase + so, 0, 0);
+                }
+            }
+        };
 #pragma unroll
-                    for (int q = 0; q < 8; q++) {
-                        // Both elements first, then a select: a lane-dependent
-                        // index would compile to a 16-way select chain.
-                        const float lo = acc[m][n][q], hi = acc[m][n][8 + q];
-                        const float other = __shfl_xor(gl ? hi : lo, 16, 64);
-                        const float mine = gl ? lo : hi;
-                        const float gate = gl ? mine : other, up = gl ? other : mine;
-                        const float sg = gate * __builtin_amdgcn_rcpf(1.0f + __expf(-gate));
-                        const uint32_t so = (uint32_t)(m * 32 + 8 * (q >> 2) + (q & 3)) * glu_ff * 2u;
-                        __builtin_amdgcn_raw_buffer_store_b16(gd_f2h(sg * up), ors, obase + so, 0, 0);
-                    }
+        for (int n = 0; n < NT; n++)
+#pragma unroll
+            for (int m = 0; m < MT; m++) glu_tile(acc[m][n], m, rw + 16 * n + (li & 15));
+        if constexpr (EX) {
+            // Waves 4..7 hand their share of the extra fragment to waves 0..3
+            // (same token tile, the other K-steps) through LDS.
+            __syncthreads();                              // every wave is done with the stages
+            float *xl = (float *)lds;
+            if (xpar) {
+#pragma unroll
+                for (int v = 0; v < 16; v++) xl[(xm * 16 + v) * 64 + lane] = accx[v];
+            }
+            __syncthreads();
+            if (!xpar) {
+#pragma unroll
+                for (int v = 0; v < 16; v++) accx[v] += xl[(xm * 16 + v) * 64 + lane];
+                glu_tile(accx, xm, xr + (li & 15));
             }
         }
         return;
@@ -530,7 +602,8 @@ int gd_gemm_launch(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, int x
 // GEMM planner's measured tile times, the partials' round trip, ~2 us per
 // extra launch) finds cheaper.  GADEON_GLU_CFG="MT,NT,NW" forces one unsplit
 // launch of that tile.
-int gd_gemm_glu(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, uint16_t *out) {
+int gd_gemm_glu(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, uint16_t *out,
+                int tile17) {
     const int K = (int)w->K, R = (int)w->R, ff = R / 2;
     GD_REQUIRE(ctx, R % 32 == 0 && T > 0 && K % 128 == 0 && R < (1 << 22), "gd_gemm_glu: R=%d "
                "must hold two halves of 16-row groups (and be below 4194304)", R);
@@ -558,8 +631,16 @@ int gd_gemm_glu(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, uint16_t
     Part parts[2] = {{nullptr, 0, ff, 1}, {nullptr, ff, ff, 1}};
     double best = 1e30;
     static const char *force = getenv("GADEON_GLU_CFG");
-    int fmt = 0, fnt = 0, fnw = 0;
-    const bool forced = force && sscanf(force, "%d,%d,%d", &fmt, &fnt, &fnw) == 3;
+    int fmt = 0, fnt = 0, fnw = 0, fex = 0;
+    const int nf = force ? sscanf(force, "%d,%d,%d,%d", &fmt, &fnt, &fnw, &fex) : 0;
+    const bool forced = nf >= 3;
+    // The (4, 2, 8) tile with a seventeenth fragment: 272 columns a
+    // workgroup in one launch (ff = 17408 at T = 512: one round of 256).
+    // Its blocks cost the plain tile's by the fragment count.
+    const Shape &t428 = SHAPES[8];
+    const int xcols = 16 * (t428.nw * t428.nt + 1);
+    const double cost_ex =
+            round_cost(t428, tiles_t(t428) * ((ff + xcols - 1) / xcols), cus, nblk) * 17.0 / 16.0;
     for (const Shape &a : SHAPES) {
         if (forced && !(a.mt == fmt && a.nt == fnt && a.nw == fnw)) continue;
         const double c1 = cost(a, ff, 1);
@@ -582,6 +663,17 @@ int gd_gemm_glu(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, uint16_t
                     parts[1] = {&b, main_cols, ff, nz};
                 }
             }
+    }
+    if (tile17 == 1 || (tile17 < 0 && (forced ? (fmt == 4 && fnt == 2 && fnw == 8 && fex == 1)
+                                              : cost_ex < best))) {
+        const int nrt = gd_blocks(ff, xcols);
+        const int64_t units = tiles_t(t428) * nrt;
+        const int per = (int)((units + 7) / 8);
+        hipLaunchKernelGGL((q2_0_gemm_kernel<4, 2, 8, 0, 1>), dim3(8 * per), dim3(64 * 8), 0,
+                           ctx->stream, (const uint8_t *)w->codes, (const uint16_t *)w->scales, X,
+                           (void *)out, (int)T, K, R, nblk, nrt, 1, per, ff, 0, ff);
+        GD_LAUNCHED(ctx, "q2_0_gemm_glu");
+        return GD_OK;
     }
     GD_REQUIRE(ctx, parts[0].sh, "gd_gemm_glu: no tile for GADEON_GLU_CFG=%s", force ? force : "");
     for (const Part &pt : parts) {
@@ -703,5 +795,23 @@ extern "C" int gd_q2_0_gemm_swiglu(gd_ctx *ctx, const gd_q2w *w, int64_t T, cons
                "of 16", (long long)w->R);
     GD_REQUIRE(ctx, w->K <= (1 << 22) && w->R < (1LL << 22) && (size_t)T * w->R < (1ULL << 62),
                "gd_q2_0_gemm_swiglu: shape too large (K and R at most 4194304)");
-    return gd_gemm_glu(ctx, w, T, X, out);
+    return gd_gemm_glu(ctx, w, T, X, out, -1);
+}
+
+extern "C" int gd_q2_0_gemm_swiglu_plan(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X,
+                                        uint16_t *out, int tile17) {
+    GD_CHECK_CTX(ctx);
+    GD_REQUIRE(ctx, tile17 == 0 || tile17 == 1, "gd_q2_0_gemm_swiglu_plan: tile17=%d not 0 or 1",
+               tile17);
+    int rc = gd_check_q2w(ctx, w, "gd_q2_0_gemm_swiglu_plan");
+    if (rc) return rc;
+    GD_REQUIRE(ctx, X && out, "gd_q2_0_gemm_swiglu_plan: null X or out");
+    GD_REQUIRE(ctx, T > 0 && T < (1 << 30), "gd_q2_0_gemm_swiglu_plan: T=%lld out of range",
+               (long long)T);
+    GD_REQUIRE(ctx, ((uintptr_t)X & 15) == 0, "gd_q2_0_gemm_swiglu_plan: X must be 16-byte aligned");
+    GD_REQUIRE(ctx, w->R % 32 == 0, "gd_q2_0_gemm_swiglu_plan: R=%lld is not 2 ff with ff a "
+               "multiple of 16", (long long)w->R);
+    GD_REQUIRE(ctx, w->K <= (1 << 22) && w->R < (1LL << 22) && (size_t)T * w->R < (1ULL << 62),
+               "gd_q2_0_gemm_swiglu_plan: shape too large (K and R at most 4194304)");
+    return gd_gemm_glu(ctx, w, T, X, out, tile17);
 }

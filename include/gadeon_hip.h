@@ -224,6 +224,14 @@ int gd_q2_0_gemm_plan(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X,
  * counterpart in the reference as one call. */
 int gd_q2_0_gemm_swiglu(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X,
                         uint16_t *out);
+/* gd_q2_0_gemm_swiglu with the tile choice made by the caller: tile17 = 1
+ * runs every column in one launch of the 4 x 2 x 8 tile that also holds a
+ * seventeenth 16-column fragment (272 columns a workgroup, what the planner
+ * picks for ff = 17408 at T = 512); tile17 = 0 keeps the planner's choice
+ * among the other tiles.  For tuning and for tests that cover both; no
+ * counterpart in the reference. */
+int gd_q2_0_gemm_swiglu_plan(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X,
+                             uint16_t *out, int tile17);
 
 /* ---- Q2_0 row dequant: MetalEnc.dequantRow / embedBatch ----------------------
  * out[n][k] = (code-1)*d of row ids[n], exactly (f16 * small integer is exact

@@ -314,6 +314,41 @@ def test_gemm_swiglu_vs_oracle(ctx, T, K, ff):
     free_w(ctx, w)
 
 
+@pytest.mark.parametrize("T,K,ff", [(512, 1024, 17408), (300, 1024, 17344), (77, 512, 4352),
+                                    (130, 384, 560)])
+@pytest.mark.parametrize("tile17", [1, 0])
+def test_gemm_swiglu_tile17_vs_oracle(ctx, T, K, ff, tile17):
+    """The 17-fragment tile (272 columns a workgroup: its eight waves share
+    the seventeenth fragment's MFMAs by token tile and K-step parity and add
+    their halves at the end) and the planner's other tiles, on the same
+    inputs: every column against the oracle on tokens of each token tile,
+    with ragged T, ff not a multiple of 272 (the last workgroup's fragments
+    past ff are dropped) and a single partial workgroup (ff = 560)."""
+    R = 2 * ff
+    blocks = O.lcg_q2_0(K, R, 3 * K + ff)
+    w = upload_w(ctx, blocks, K, R)
+    Xh = O.lcg_normal_f16(T * K, 81).reshape(T, K)
+    dX, dO = ctx.put(Xh.view(np.uint16)), ctx.alloc(T * ff * 2)
+    ctx.gd_q2_0_gemm_swiglu_plan(C.byref(w), T, dX, dO, tile17)
+    out = ctx.get(dO, (T, ff), np.float16).astype(np.float32)
+    blk = blocks.reshape(R, -1)
+    g = np.ascontiguousarray(blk[:ff]); u = np.ascontiguousarray(blk[ff:])
+    toks = sorted({0, 31, 32, 127, 128, 200, 255, 256, 300 % T, T - 1} & set(range(T)))
+    for t in toks:
+        x = Xh[t].astype(np.float32)
+        gv = O.q2_0_matvec(g, K, ff, x, threads=8)
+        uv = O.q2_0_matvec(u, K, ff, x, threads=8)
+        want = (silu(gv) * uv).astype(np.float16).astype(np.float32)
+        assert rel_diff(out[t], want) < 2e-3, t
+        # The seventeenth fragment of every workgroup on its own.
+        extra = np.concatenate([np.arange(c, min(c + 16, ff)) for c in range(256, ff, 272)])
+        if len(extra):
+            assert rel_diff(out[t, extra], want[extra]) < 2e-3, t
+    ctx.free(dX)
+    ctx.free(dO)
+    free_w(ctx, w)
+
+
 @pytest.mark.parametrize("K,ff", [(5120, 17408), (1024, 208)])
 def test_gemv_norm_swiglu_vs_oracle(ctx, K, ff):
     """The decode feed-forward input: fused add + norm, [gate; up] GEMV and
