@@ -58,64 +58,88 @@ __device__ __forceinline__ float rope_dim(int i, float mine, float pv, int n_rot
 // dense model's plain q, qs = HD), RMS-normalize it with q_norm and rotate
 // it; kv heads normalize + rotate k and append k, v to the f16 cache at the
 // token's position (Attention.swift:79-107).  Lane l holds dims l + 64 s.
+// A block is one token and PREP_HEADS of its heads (PREP_WAVES waves, heads
+// wave, wave + PREP_WAVES, ..): the rotation's cos and sin depend only on the
+// token, so the block forms them once into LDS (the same powf / cosf / sinf
+// per pair index as rope_dim) instead of once per head.
+constexpr int PREP_WAVES = 4, PREP_HEADS = 12;
 template <int HD>
-__global__ __launch_bounds__(256) void k_attn_prep(
+__global__ __launch_bounds__(64 * PREP_WAVES) void k_attn_prep(
         const float *proj, int64_t stride, int qs, const float *q_norm, const float *k_norm,
         float *q_out, float *gate_out, uint16_t *kc, uint16_t *vc, const int32_t *page_table,
         const int32_t *pos_ptr, int N, int H, int HKV, int n_rot, float base, int block, float eps) {
     constexpr int S = HD / 64;
-    const int64_t task = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (task >= (int64_t)N * (H + HKV)) return;
-    const int n = (int)(task / (H + HKV)), h = (int)(task % (H + HKV)), lane = threadIdx.x & 63;
+    __shared__ float rc[HD / 2], rs[HD / 2];
+    const int groups = (H + HKV + PREP_HEADS - 1) / PREP_HEADS;
+    const int n = (int)(blockIdx.x / groups), g = (int)(blockIdx.x % groups);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int pos = *pos_ptr + n;
-    const float *row = proj + (int64_t)n * stride;
-    const bool is_q = h < H;
-    const int kh = h - H;
-    const float *src = is_q ? row + h * qs : row + H * qs + kh * HD;
-    const float *nw = is_q ? q_norm : k_norm;
-    float x[S], y[S];
-    float ss = 0.f;
-#pragma unroll
-    for (int s = 0; s < S; s++) {
-        x[s] = src[lane + 64 * s];
-        ss += x[s] * x[s];
-    }
-    // RMS norm over the head (Kern.rmsnormRows, Kernels.swift:26-37).
-    ss = gd_wave_sum(ss);
-    const float sc = 1.0f / sqrtf(ss / (float)HD + eps);
-#pragma unroll
-    for (int s = 0; s < S; s++) y[s] = x[s] * sc * nw[lane + 64 * s];
-    // Dim i pairs with i +- n_rot/2, held by another lane (or slot).
     const int half = n_rot / 2;
-    float r[S];
-#pragma unroll
-    for (int k = 0; k < S; k++) {
-        const int i = lane + 64 * k;
-        const int ip = i < half ? i + half : i - half;          // partner dim
-        float p[S];
-#pragma unroll
-        for (int s = 0; s < S; s++) p[s] = __shfl(y[s], ip & 63, 64);
-        float pv = p[0];
-#pragma unroll
-        for (int s = 1; s < S; s++) pv = (ip >> 6) == s ? p[s] : pv;
-        r[k] = i < n_rot ? rope_dim(i, y[k], pv, n_rot, base, pos) : y[k];
+    for (int j = threadIdx.x; j < half; j += 64 * PREP_WAVES) {
+        const float freq = powf(base, -2.0f * (float)j / (float)n_rot);
+        const float ang = (float)pos * freq;
+        rc[j] = cosf(ang);
+        rs[j] = sinf(ang);
     }
-    if (is_q) {
-        float *qo = q_out + ((int64_t)n * H + h) * HD;
-        float *go = gate_out + ((int64_t)n * H + h) * HD;
+    __syncthreads();
+    const float *row = proj + (int64_t)n * stride;
+#pragma unroll
+    for (int t = 0; t < PREP_HEADS / PREP_WAVES; t++) {
+        const int h = g * PREP_HEADS + wave + PREP_WAVES * t;
+        if (h >= H + HKV) break;
+        const bool is_q = h < H;
+        const int kh = h - H;
+        const float *src = is_q ? row + h * qs : row + H * qs + kh * HD;
+        const float *nw = is_q ? q_norm : k_norm;
+        float x[S], y[S];
+        float ss = 0.f;
 #pragma unroll
         for (int s = 0; s < S; s++) {
-            qo[lane + 64 * s] = r[s];
-            if (qs == 2 * HD) go[lane + 64 * s] = row[h * qs + HD + lane + 64 * s];
+            x[s] = src[lane + 64 * s];
+            ss += x[s] * x[s];
         }
-    } else {
-        const int kvDim = HKV * HD;
-        const int64_t slot = kv_slot(page_table, pos, block);
-        const float *vs = row + H * qs + HKV * HD + kh * HD;
+        // RMS norm over the head (Kern.rmsnormRows, Kernels.swift:26-37).
+        ss = gd_wave_sum(ss);
+        const float sc = 1.0f / sqrtf(ss / (float)HD + eps);
 #pragma unroll
-        for (int s = 0; s < S; s++) {
-            kc[slot * kvDim + kh * HD + lane + 64 * s] = gd_f2h(r[s]);
-            vc[slot * kvDim + kh * HD + lane + 64 * s] = gd_f2h(vs[lane + 64 * s]);
+        for (int s = 0; s < S; s++) y[s] = x[s] * sc * nw[lane + 64 * s];
+        // Dim i pairs with i +- n_rot/2, held by another lane (or slot).
+        float r[S];
+#pragma unroll
+        for (int k = 0; k < S; k++) {
+            const int i = lane + 64 * k;
+            const int ip = i < half ? i + half : i - half;          // partner dim
+            float p[S];
+#pragma unroll
+            for (int s = 0; s < S; s++) p[s] = __shfl(y[s], ip & 63, 64);
+            float pv = p[0];
+#pragma unroll
+            for (int s = 1; s < S; s++) pv = (ip >> 6) == s ? p[s] : pv;
+            if (i < n_rot) {
+                const int jj = i < half ? i : i - half;
+                const float c = rc[jj], sn = rs[jj];
+                r[k] = i < half ? y[k] * c - pv * sn : pv * sn + y[k] * c;
+            } else {
+                r[k] = y[k];
+            }
+        }
+        if (is_q) {
+            float *qo = q_out + ((int64_t)n * H + h) * HD;
+            float *go = gate_out + ((int64_t)n * H + h) * HD;
+#pragma unroll
+            for (int s = 0; s < S; s++) {
+                qo[lane + 64 * s] = r[s];
+                if (qs == 2 * HD) go[lane + 64 * s] = row[h * qs + HD + lane + 64 * s];
+            }
+        } else {
+            const int kvDim = HKV * HD;
+            const int64_t slot = kv_slot(page_table, pos, block);
+            const float *vs = row + H * qs + HKV * HD + kh * HD;
+#pragma unroll
+            for (int s = 0; s < S; s++) {
+                kc[slot * kvDim + kh * HD + lane + 64 * s] = gd_f2h(r[s]);
+                vc[slot * kvDim + kh * HD + lane + 64 * s] = gd_f2h(vs[lane + 64 * s]);
+            }
         }
     }
 }
@@ -522,13 +546,15 @@ int gd_attn_prep_launch(gd_ctx *ctx, int hd, const float *proj, int64_t stride, 
                         uint16_t *kc, uint16_t *vc, const int32_t *page_table,
                         const int32_t *pos_ptr, int N, int H, int HKV, int n_rot, float base,
                         int block, float eps) {
-    const dim3 grid(gd_blocks((int64_t)N * (H + HKV), 4));
+    GD_REQUIRE(ctx, n_rot >= 0 && n_rot <= hd && n_rot % 2 == 0, "attention prep: n_rot=%d", n_rot);
+    const dim3 grid((unsigned)((int64_t)N * ((H + HKV + PREP_HEADS - 1) / PREP_HEADS)));
+    const dim3 blk(64 * PREP_WAVES);
     if (hd == 128)
-        hipLaunchKernelGGL(k_attn_prep<128>, grid, dim3(256), 0, ctx->stream, proj, stride, qs,
+        hipLaunchKernelGGL(k_attn_prep<128>, grid, blk, 0, ctx->stream, proj, stride, qs,
                            q_norm, k_norm, q_out, gate_out, kc, vc, page_table, pos_ptr, N, H,
                            HKV, n_rot, base, block, eps);
     else
-        hipLaunchKernelGGL(k_attn_prep<256>, grid, dim3(256), 0, ctx->stream, proj, stride, qs,
+        hipLaunchKernelGGL(k_attn_prep<256>, grid, blk, 0, ctx->stream, proj, stride, qs,
                            q_norm, k_norm, q_out, gate_out, kc, vc, page_table, pos_ptr, N, H,
                            HKV, n_rot, base, block, eps);
     GD_LAUNCHED(ctx, "k_attn_prep");
