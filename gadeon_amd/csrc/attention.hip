@@ -61,7 +61,9 @@ __device__ __forceinline__ float rope_dim(int i, float mine, float pv, int n_rot
 // A block is one token and PREP_HEADS of its heads (PREP_WAVES waves, heads
 // wave, wave + PREP_WAVES, ..): the rotation's cos and sin depend only on the
 // token, so the block forms them once into LDS (the same powf / cosf / sinf
-// per pair index as rope_dim) instead of once per head.
+// per pair index as rope_dim) instead of once per head.  pos_ptr[0] is the
+// first token's position (the KV slot), pos_ptr[1] the rope shift: tokens
+// rotate at position + shift (MetalEngine.swift:432-435).
 constexpr int PREP_WAVES = 4, PREP_HEADS = 12;
 template <int HD>
 __global__ __launch_bounds__(64 * PREP_WAVES) void k_attn_prep(
@@ -73,11 +75,11 @@ __global__ __launch_bounds__(64 * PREP_WAVES) void k_attn_prep(
     const int groups = (H + HKV + PREP_HEADS - 1) / PREP_HEADS;
     const int n = (int)(blockIdx.x / groups), g = (int)(blockIdx.x % groups);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int pos = *pos_ptr + n;
+    const int pos = pos_ptr[0] + n, rpos = pos + pos_ptr[1];
     const int half = n_rot / 2;
     for (int j = threadIdx.x; j < half; j += 64 * PREP_WAVES) {
         const float freq = powf(base, -2.0f * (float)j / (float)n_rot);
-        const float ang = (float)pos * freq;
+        const float ang = (float)rpos * freq;
         rc[j] = cosf(ang);
         rs[j] = sinf(ang);
     }
@@ -387,9 +389,10 @@ __global__ __launch_bounds__(2 * HD) void k_attn_decode(
         nrm[hf][i] = y;
         __syncthreads();
         const int half = n_rot / 2;
+        // Rotated at position + shift (pos_ptr[1]), cached at position.
         if (i < n_rot)
             y = rope_dim(i, nrm[hf][i], i < half ? nrm[hf][i + half] : nrm[hf][i - half], n_rot,
-                         base, pos);
+                         base, pos + pos_ptr[1]);
         rot[hf][i] = y;
         if (hf == 1) vnew[i] = vx;
         __syncthreads();
@@ -578,6 +581,7 @@ int gd_attn_prefill_launch(gd_ctx *ctx, int hd, const float *q, const float *gat
 
 // Fused decode (the stack): split + combine into f16 out.  qs = 2 hd: the
 // hybrid's fused [q | gate] rows, output gated; qs = hd: plain q, ungated.
+// pos_ptr[0] is the token's position, pos_ptr[1] the rope shift.
 int gd_attn_decode_launch(gd_ctx *ctx, int hd, const float *proj, int qs, const float *q_norm,
                           const float *k_norm, uint16_t *kc, uint16_t *vc,
                           const int32_t *page_table, const int32_t *pos_ptr, float *part,

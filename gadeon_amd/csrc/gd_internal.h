@@ -67,7 +67,9 @@ int gd_gemm_glu(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, uint16_t
 // prefill (out f16 or f32), fused decode (prep + split + combine, f16 out),
 // and the size of the decode split partials.  qs is the per-head q stride of
 // the projection rows: 2 hd for fused [q | gate] pairs (gated output), hd
-// for plain q (ungated).
+// for plain q (ungated).  For prep and fused decode, pos_ptr holds two ints:
+// the (first) token's position and the rope shift (rotation at position +
+// shift, KV slot at position).
 int gd_attn_prep_launch(gd_ctx *ctx, int hd, const float *proj, int64_t stride, int qs,
                         const float *q_norm, const float *k_norm, float *q_out, float *gate_out,
                         uint16_t *kc, uint16_t *vc, const int32_t *page_table,

@@ -441,9 +441,14 @@ struct gd_stack {
     float *attn_part = nullptr, *amax_v = nullptr;
     int *amax_i = nullptr;
     uint16_t *xn16 = nullptr, *a16 = nullptr;
-    int32_t *ids = nullptr, *dpos = nullptr, *dtok = nullptr;
+    int32_t *ids = nullptr, *dtok = nullptr;
+    // dpos[0]: the next position; dpos[1]: the rope shift (rope position =
+    // position + shift, MetalEngine.swift:432-435; nonzero only after a
+    // bookmark of a state with image spans is restored).
+    int32_t *dpos = nullptr;
     int32_t *picks = nullptr;    // picks[p]: the greedy pick made at position p
     int64_t pos = 0;
+    int64_t rope_shift = 0;
     bool random = true;          // weights drawn from the seed (else loaded)
     bool have_pick = false;      // dtok holds the last greedy pick
     std::atomic<bool> stop{false};
@@ -781,7 +786,7 @@ int create(gd_ctx *ctx, const gd_stack_config *cfg, uint64_t seed, bool random, 
     const int a16n = std::max(std::max(st->valDim, c.n_head * hd), FF);
     C_(salloc_t(st, (size_t)B * a16n, &st->a16));
     C_(salloc_t(st, (size_t)B, &st->ids));
-    C_(salloc_t(st, 1, &st->dpos));
+    C_(salloc_t(st, 2, &st->dpos));
     C_(salloc_t(st, 1, &st->dtok));
     C_(salloc_t(st, (size_t)c.max_ctx, &st->picks));
     C_(gd_stack_reset(st));
@@ -808,9 +813,10 @@ extern "C" int gd_stack_reset(gd_stack *st) {
                 return rc;
         }
     }
-    if ((rc = gd_fill_u32(ctx, st->dpos, 0, 1)) || (rc = gd_fill_u32(ctx, st->dtok, 0, 1)))
+    if ((rc = gd_fill_u32(ctx, st->dpos, 0, 2)) || (rc = gd_fill_u32(ctx, st->dtok, 0, 1)))
         return rc;
     st->pos = 0;
+    st->rope_shift = 0;
     st->have_pick = false;
     st->stop.store(false);
     return gd_sync(ctx);
@@ -1105,6 +1111,7 @@ struct gd_bookmark {
     gd_ctx *ctx = nullptr;
     gd_stack_config c{};
     int64_t pos = 0;
+    int64_t rope_shift = 0;      // rope position = position + shift
     bool have_pick = false;
     void *buf = nullptr;         // [pick | conv, rec per GDN layer | k, v per attention layer]
 };
@@ -1188,6 +1195,7 @@ extern "C" int gd_stack_bookmark(gd_stack *st, gd_bookmark **out) {
     b->ctx = ctx;
     b->c = st->c;
     b->pos = st->pos;
+    b->rope_shift = st->rope_shift;
     b->have_pick = st->have_pick;
     int rc = gd_alloc(ctx, l.total, &b->buf);
     uint8_t *base = (uint8_t *)b->buf;
@@ -1237,11 +1245,12 @@ extern "C" int gd_stack_restore(gd_stack *st, const gd_bookmark *b) {
             rc = d2d(ctx, ly.vc, s + align256(l.kv * 2), l.kv * 2);
         }
     }
-    const uint32_t pos32 = (uint32_t)b->pos;
-    if (rc == GD_OK) rc = gd_fill_u32(ctx, st->dpos, pos32, 1);
+    if (rc == GD_OK) rc = gd_fill_u32(ctx, st->dpos, (uint32_t)b->pos, 1);
+    if (rc == GD_OK) rc = gd_fill_u32(ctx, st->dpos + 1, (uint32_t)(int32_t)b->rope_shift, 1);
     if (rc == GD_OK) rc = gd_sync(ctx);
     if (rc) return rc;
     st->pos = b->pos;
+    st->rope_shift = b->rope_shift;
     st->have_pick = b->have_pick;
     st->stop.store(false);
     return GD_OK;
@@ -1258,7 +1267,7 @@ extern "C" int gd_stack_serialize(gd_stack *st, const gd_bookmark *b, void *buf,
     // Size pass (no data), then, given room, the bytes.
     auto emit = [&](Out &o, const uint8_t *host) {
         o.i64(b->pos);
-        o.i64(0);                                              // ropeShift: text only
+        o.i64(b->rope_shift);
         for (int part = 0; part < 2; part++) {                 // conv dict, then rec dict
             int64_t n = 0;
             for (const StackLayer &ly : st->L) n += ly.rec;
@@ -1319,12 +1328,13 @@ constexpr int64_t GDNS_VERSION = 1, GDNS_PAGE = 512;
 
 // Finish a bookmark from host bytes in the device layout.
 int bookmark_from_host(gd_stack *st, const std::vector<uint8_t> &host, int64_t pos,
-                       gd_bookmark **out) {
+                       gd_bookmark **out, int64_t rope_shift = 0) {
     gd_ctx *ctx = st->ctx;
     gd_bookmark *b = new gd_bookmark();
     b->ctx = ctx;
     b->c = st->c;
     b->pos = pos;
+    b->rope_shift = rope_shift;
     b->have_pick = false;        // neither format carries a pick: decode a token first
     int rc = gd_alloc(ctx, host.size(), &b->buf);
     if (rc == GD_OK) rc = gd_upload(ctx, b->buf, host.data(), host.size());
@@ -1345,6 +1355,10 @@ extern "C" int gd_stack_serialize_gdns(gd_stack *st, const gd_bookmark *b, void 
     GD_REQUIRE(ctx, b && b->buf && len, "gd_stack_serialize_gdns: null argument");
     GD_REQUIRE(ctx, b->ctx == ctx && same_geometry(b->c, st->c),
                "gd_stack_serialize_gdns: bookmark of another stack geometry or context");
+    // The CPU engine has no image spans, and its bytes no rope shift.
+    GD_REQUIRE(ctx, b->rope_shift == 0,
+               "gd_stack_serialize_gdns: ropeShift %lld has no place in GDNS bytes",
+               (long long)b->rope_shift);
     const BmLayout l = bm_layout(st, b->pos);
     const size_t kvd = (size_t)st->c.n_head_kv * st->c.head_dim;
     const int64_t npages = (b->pos + GDNS_PAGE - 1) / GDNS_PAGE;
@@ -1497,9 +1511,9 @@ extern "C" int gd_stack_deserialize(gd_stack *st, const void *data, size_t n,
     GD_REQUIRE(ctx, !in.bad && pos >= 0 && pos <= st->c.max_ctx,
                "gd_stack_deserialize: position %lld outside [0, max_ctx %d]", (long long)pos,
                st->c.max_ctx);
-    GD_REQUIRE(ctx, rope_shift == 0,
-               "gd_stack_deserialize: ropeShift %lld (image spans) is not supported",
-               (long long)rope_shift);
+    // Rope positions (position + shift) must stay in int32 over the context.
+    GD_REQUIRE(ctx, rope_shift >= -(1LL << 30) && rope_shift <= (1LL << 30),
+               "gd_stack_deserialize: ropeShift %lld out of range", (long long)rope_shift);
     const BmLayout l = bm_layout(st, pos);
     std::vector<uint8_t> host(l.total, 0);
     // Each dict must list exactly this stack's GDN (or attention) layers, in
@@ -1559,5 +1573,5 @@ extern "C" int gd_stack_deserialize(gd_stack *st, const void *data, size_t n,
         }
     }
     GD_REQUIRE(ctx, in.n == n, "gd_stack_deserialize: %zu trailing bytes", n - in.n);
-    return bookmark_from_host(st, host, pos, out);
+    return bookmark_from_host(st, host, pos, out, rope_shift);
 }

@@ -491,12 +491,12 @@ int gd_stack_position(gd_stack *st, int64_t *pos);
 
 /* ---- Bookmarks: MetalEngine.bookmark / restore / serialize / deserialize -------
  * (MetalEngine.swift:455-584).  A bookmark is a device-memory snapshot of the
- * generation state: position, the last greedy pick, each GDN layer's conv ring
+ * generation state: position, rope shift, the last greedy pick, each GDN layer's conv ring
  * and recurrent state, each attention layer's K/V over positions [0, pos).
  * It stays valid across later decode, reset and prefill calls and can be
  * restored any number of times, into the stack it came from or another of
  * the same geometry on the same context.  gd_stack_serialize writes the bytes
- * of MetalEngine.serialize: i64 pos, i64 ropeShift (0), the conv and the rec
+ * of MetalEngine.serialize: i64 pos, i64 ropeShift, the conv and the rec
  * dicts (i64 count, then per GDN layer in ascending order i64 layer, i64 n,
  * n f32), and the KV dict (i64 count, then per attention layer i64 layer,
  * i64 len, i64 n, n f32 of K, i64 n, n f32 of V, each [len][n_head_kv *
@@ -504,7 +504,12 @@ int gd_stack_position(gd_stack *st, int64_t *pos);
  * with buf NULL to get the size in *len.  gd_stack_deserialize checks every
  * count and layer index against the stack and returns a bookmark to restore;
  * that format carries no pick, so after restoring it the next call must be
- * gd_stack_decode (gd_stack_generate fails until then). */
+ * gd_stack_decode (gd_stack_generate fails until then).  ropeShift is what
+ * MetalEngine keeps after an image span compressed the M-RoPE positions:
+ * from then on a token at position p is rotated at p + ropeShift while its
+ * KV slot and causality stay at p (MetalEngine.swift:432-435); restoring a
+ * bookmark restores it, gd_stack_reset clears it (this build has no vision
+ * prefill of its own, so only restored states carry one). */
 typedef struct gd_bookmark gd_bookmark;
 
 int gd_stack_bookmark(gd_stack *st, gd_bookmark **out);
@@ -522,7 +527,8 @@ int gd_stack_deserialize(gd_stack *st, const void *data, size_t n, gd_bookmark *
  * refuses bytes without that header or version (BonsaiEngine.deserialize returns
  * nil), and checks every count, layer index and page size against the stack; K/V
  * are rounded to the cache's halves.  A state parked by the CPU engine thus
- * resumes on this stack, and the other way round. */
+ * resumes on this stack, and the other way round.  The CPU engine has no
+ * image spans: a bookmark with a nonzero ropeShift is refused. */
 int gd_stack_serialize_gdns(gd_stack *st, const gd_bookmark *b, void *buf, size_t cap,
                             size_t *len);
 int gd_stack_deserialize_gdns(gd_stack *st, const void *data, size_t n, gd_bookmark **out);

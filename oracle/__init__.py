@@ -246,7 +246,7 @@ class OrStack(C.Structure):
                [(n, _i) for n in ("n_vocab", "d_state", "n_k_head", "n_v_head", "d_conv",
                                   "max_ctx", "stage_f16", "threads", "dense")] + \
                [("layers", C.POINTER(OrStackLayer)), ("embd", _vp), ("out_norm", _vp),
-                ("head", _vp)]
+                ("head", _vp), ("rope_shift", _i)]
 
 
 _PROTOS["or_stack_token"] = (None, [C.POINTER(OrStack), _i, _i, _vp, _vp])
@@ -321,6 +321,15 @@ class Stack:
         st.head = ptr(tensors(-1, "output")) if untied else None
         self.st = st
         self.pos = 0
+
+    @property
+    def rope_shift(self) -> int:
+        """Rope position = position + rope_shift (MetalEngine.ropeShift)."""
+        return self.st.rope_shift
+
+    @rope_shift.setter
+    def rope_shift(self, v: int):
+        self.st.rope_shift = v
 
     def token(self, tok: int):
         """Advance one token (decode); returns (hidden, logits)."""

@@ -115,6 +115,7 @@ typedef struct or_stack {
     const float *out_norm;
     const uint8_t *head;                        /* output.weight; NULL: tied to embd
                                                    (Model.swift:145) */
+    int rope_shift;    /* rope position = position + rope_shift (MetalEngine.swift:432-435) */
 } or_stack;
 
 #define OR_STAGE_MV 1   /* mat-vec inputs (the prefill GEMM's half tiles, Kernels.metal:428) */

@@ -112,8 +112,9 @@ static void attn_token(or_stack *st, or_stack_layer *L, const float *qFull, floa
         }
     or_rmsnorm_rows(q, hd, nH, L->q_norm, st->eps);
     or_rmsnorm_rows(k, hd, nKV, L->k_norm, st->eps);
-    or_rope_neox(q, hd, nH, st->n_rot, st->rope_base, pos);
-    or_rope_neox(k, hd, nKV, st->n_rot, st->rope_base, pos);
+    /* Rotated at position + ropeShift, cached at position (MetalEngine.swift:432-435). */
+    or_rope_neox(q, hd, nH, st->n_rot, st->rope_base, pos + st->rope_shift);
+    or_rope_neox(k, hd, nKV, st->n_rot, st->rope_base, pos + st->rope_shift);
     stage(st->stage_f16 & OR_STAGE_KV, k, L->kcache + (int64_t)pos * kvDim, kvDim);  /* kv.append */
     stage(st->stage_f16 & OR_STAGE_KV, v, L->vcache + (int64_t)pos * kvDim, kvDim);
     const int T = pos + 1;

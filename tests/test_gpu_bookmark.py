@@ -234,7 +234,7 @@ def test_deserialize_rejects_malformed(ctx):
         for cut in (0, 7, 8, 16, 24, 40, len(data) // 2, len(data) - 4):
             bad(data[:cut], "gd_stack_deserialize")
         bad(data + b"\0" * 4, "trailing")
-        bad(struct.pack("<q", 1) + data[:8] + data[16:], "ropeShift")       # pos 20 -> shift
+        bad(data[:8] + struct.pack("<q", 1 << 40) + data[16:], "ropeShift")   # out of range
         bad(struct.pack("<q", 10 ** 9) + data[8:], "position")
         # The first conv entry names layer 1 instead of 0.
         bad(data[:24] + struct.pack("<q", 1) + data[32:], "GDN layer 1")
@@ -249,6 +249,61 @@ def test_deserialize_rejects_malformed(ctx):
             ctx.lib.gd_bookmark_free(bm)
         ctx.lib.gd_stack_destroy(st)
         ctx.lib.gd_stack_destroy(other)
+
+
+def test_rope_shift_restored_from_bytes(ctx):
+    """MetalEngine.serialize bytes whose ropeShift is nonzero (what MetalEngine
+    keeps after an image span compressed the M-RoPE positions) restore with
+    it: later tokens are rotated at position + shift while their K/V land at
+    their position (MetalEngine.swift:432-435, 459-480).  Decoded against the
+    oracle with the same shift, logits within the stack tolerance; the same
+    tokens without the shift give clearly different logits.  The shift
+    travels with bookmarks and bytes, GDNS bytes (no such field) refuse it,
+    and a reset clears it."""
+    cfg, st = make_stack(ctx, seed=29)
+    _, st2 = make_stack(ctx, seed=29)
+    bms = []
+    try:
+        read = tensor_reader(ctx, st)
+        ref = O.Stack(cfg, read, stage_f16=True, threads=THREADS)
+        ids = (np.arange(41) * 29 % cfg["n_vocab"]).astype(np.int32)
+        prefill(ctx, st, ids)
+        _, rlg = ref.prefill(ids)
+        bms.append(bookmark(ctx, st))
+        data = serialize(ctx, st, bms[-1])
+        assert struct.unpack_from("<q", data, 8)[0] == 0
+        shift = -13
+        bms.append(deserialize(ctx, st2, data[:8] + struct.pack("<q", shift) + data[16:]))
+        ctx.check(ctx.lib.gd_stack_restore(st2, bms[-1]))
+        ref.rope_shift = shift
+        tok, toks, got, worst = int(np.argmax(rlg)), [], [], 0.0
+        for step in range(6):
+            (glg,), _ = decode_run(ctx, st2, [tok])
+            _, r_lg = ref.token(tok)
+            r = rel_diff(glg, r_lg)
+            worst = max(worst, r)
+            assert r < TOL, (step, r)
+            toks.append(tok)
+            got.append(glg)
+            tok = int(np.argmax(r_lg))
+        unshifted, _ = decode_run(ctx, st, toks)
+        apart = min(rel_diff(a, b) for a, b in zip(got, unshifted))
+        assert apart > 10 * TOL, apart
+        bms.append(bookmark(ctx, st2))
+        assert struct.unpack_from("<q", serialize(ctx, st2, bms[-1]), 8)[0] == shift
+        n = C.c_size_t()
+        with pytest.raises(ga.GDError, match="ropeShift"):
+            ctx.check(ctx.lib.gd_stack_serialize_gdns(st2, bms[-1], None, 0, C.byref(n)))
+        ctx.check(ctx.lib.gd_stack_reset(st2))
+        bms.append(bookmark(ctx, st2))
+        assert struct.unpack_from("<q", serialize(ctx, st2, bms[-1]), 8)[0] == 0
+        print(f"\n  ropeShift {shift} restored: 6 decode steps, worst logits relDiff {worst:.2e} "
+              f"(unshifted: at least {apart:.2e} apart)")
+    finally:
+        for b in bms:
+            ctx.lib.gd_bookmark_free(b)
+        ctx.lib.gd_stack_destroy(st)
+        ctx.lib.gd_stack_destroy(st2)
 
 
 # ---- the CPU engine's parked-state bytes (GDNS) --------------------------------

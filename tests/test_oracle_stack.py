@@ -206,6 +206,55 @@ def test_dense_attention_is_ungated_softmax_attention():
         assert np.allclose(h, want, rtol=5e-5, atol=5e-5), pos
 
 
+def test_rope_shift_rotates_at_position_plus_shift():
+    """MetalEngine.ropeShift (MetalEngine.swift:432-435): a token at position p
+    is rotated at p + shift while its K/V are cached at p and causality stays
+    on positions.  Three dense-attention tokens, the shift changed from 0 to 5
+    before the third, against a direct numpy statement (cached keys keep the
+    rotation they were made with).  And RoPE is relative: the same shift on
+    every token from the first changes nothing beyond f32 rounding."""
+    cfg = dict(DCFG)
+    T = make_dense_tensors(cfg)
+    E, hd, nh, nkv = cfg["n_embd"], cfg["head_dim"], cfg["n_head"], cfg["n_head_kv"]
+    eps, rot, base = cfg["eps"], cfg["n_rot"], cfg["rope_base"]
+    toks, shifts = (11, 40, 23), (0, 0, 5)
+    st = stack_of(cfg, T)
+    keys, vals = [], []
+    for pos, (tok, sh) in enumerate(zip(toks, shifts)):
+        st.rope_shift = sh
+        h, _ = st.token(tok)
+        x = O.q2_0_dequant(T["token_embd"][tok * E // 128 * 34:(tok + 1) * E // 128 * 34], E)
+        n = O.rmsnorm(x, T["attn_norm"], eps)
+        q = mv(T, "attn_q", E, nh * hd, n).reshape(nh, hd).astype(np.float64)
+        k = mv(T, "attn_k", E, nkv * hd, n).reshape(nkv, hd).astype(np.float64)
+        v = mv(T, "attn_v", E, nkv * hd, n).reshape(nkv, hd).astype(np.float64)
+        rms = lambda a, w: a / np.sqrt((a * a).mean(axis=1, keepdims=True) + eps) * w
+        q, k = rms(q, T["attn_q_norm"]), rms(k, T["attn_k_norm"])
+        q = O.rope_neox(q.astype(np.float32).reshape(-1), hd, rot, base, pos + sh).reshape(nh, hd)
+        k = O.rope_neox(k.astype(np.float32).reshape(-1), hd, rot, base, pos + sh).reshape(nkv, hd)
+        keys.append(k.astype(np.float64))
+        vals.append(v)
+        ao = np.empty((nh, hd))
+        for hh in range(nh):
+            g = hh // (nh // nkv)
+            s = np.array([q[hh] @ kk[g] for kk in keys]) / np.sqrt(hd)
+            p = np.exp(s - s.max())
+            p /= p.sum()
+            ao[hh] = sum(pi * vv[g] for pi, vv in zip(p, vals))
+        a = mv(T, "attn_output", nh * hd, E, ao.reshape(-1))
+        want = O.rmsnorm((x + a).astype(np.float32), T["output_norm"], eps)
+        assert np.allclose(h, want, rtol=5e-5, atol=5e-5), pos
+    # The shift of the third token mattered: without it the output differs.
+    ref = stack_of(cfg, T)
+    hs = [ref.token(t)[0] for t in toks]
+    assert np.abs(hs[2] - h).max() > 1e-3
+    # One shift for every token: relative positions, hence outputs, unchanged.
+    sh = stack_of(cfg, T)
+    sh.rope_shift = 37
+    for tok, want in zip(toks, hs):
+        assert np.allclose(sh.token(tok)[0], want, rtol=2e-4, atol=2e-4)
+
+
 GCFG = dict(n_layer=1, n_embd=256, n_ff=256, n_head=4, n_head_kv=2, head_dim=128, n_rot=64,
             rope_base=1e7, eps=1e-6, n_vocab=64, attn_interval=9, d_state=128, n_k_head=1,
             n_v_head=2, d_conv=4, max_ctx=8)
