@@ -51,7 +51,9 @@ int gd_gemv_mfma_norm(gd_ctx *ctx, const gd_q2w *w, const float *h, const float 
 int gd_gemv_ksplit(gd_ctx *ctx, int64_t K, int64_t R);
 // Prefill GEMM plan: MT x 32 tokens by 4 x NT x 32 weight rows per
 // workgroup, K split `split` ways into f32 partials.
-struct gd_gemm_plan { int mt, nt, split; int nw = 4; };   // nw: waves per workgroup
+// nw: waves per workgroup; ex = 1: the 4 x 2 x 8 tile with a seventeenth
+// 32-row fragment (544 rows a workgroup; f32 out or split partials only).
+struct gd_gemm_plan { int mt, nt, split; int nw = 4; int ex = 0; };
 gd_gemm_plan gd_gemm_choose(gd_ctx *ctx, int64_t T, int64_t K, int64_t R, int x_dtype);
 // split > 1: y_dtype f32 and Y holds split * T * R partials, summed by the caller.
 int gd_gemm_launch(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, int x_dtype, void *Y,

@@ -128,9 +128,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
     const int t0 = tt * BT;
     // This wave's first row (SwiGLU: first gate row, 16 per fragment).
     const int rw = glu_ff ? glu_r0 + rt * (16 * St::NF) + wave * (16 * NT)
-                          : rt * (NW * NT * 32) + wave * (NT * 32);
+                          : rt * (St::NF * 32) + wave * (NT * 32);
     // EX: the extra fragment's first gate row, and this wave's share of it.
-    const int xr = glu_r0 + rt * (16 * St::NF) + 16 * NW * NT;
+    // (SwiGLU: 16 gate rows and their up rows; plain: 32 rows.)
+    const int xr = glu_ff ? glu_r0 + rt * (16 * St::NF) + 16 * NW * NT : rt * (St::NF * 32) + 32 * NW * NT;
     const int xm = wave & 3, xpar = wave >> 2;
     const int nblk = K >> 7;
     const int csteps = (nblk + 3) >> 2;
@@ -151,7 +152,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
             gd_rsrc(scales + (size_t)g0 * bgroups * 256, gvalid * (uint32_t)bgroups * 512u);
     // EX: the extra fragment's gate and up row groups (its loads are wave 0's).
     const int gx = xr >> 4;
-    const uint32_t gvx = EX ? (uint32_t)max(0, min((glu_ff >> 4) + 1, rgroups - gx)) : 0u;
+    const uint32_t gvx = EX ? (uint32_t)max(0, min(glu_ff ? (glu_ff >> 4) + 1 : 2, rgroups - gx)) : 0u;
     const __amdgpu_buffer_rsrc_t xcrs = gd_rsrc(codes + ((size_t)gx * csteps << 11), gvx * (uint32_t)csteps * 2048u);
     const __amdgpu_buffer_rsrc_t xsrs = gd_rsrc(scales + (size_t)gx * bgroups * 256, gvx * (uint32_t)bgroups * 512u);
 
@@ -177,7 +178,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
         cvo[n] = ((uint32_t)(g * csteps) << 11) + ((uint32_t)lh << 10) + ((li & 15) << 4);
         svo[n] = ((uint32_t)g * bgroups * 256 + (li & 15)) * 2;
     }
-    const int gxu = (li >> 4) ? (glu_ff >> 4) : 0;        // EX: gate or up rows
+    const int gxu = (li >> 4) ? (glu_ff ? glu_ff >> 4 : 1) : 0;   // EX: second row group
     const uint32_t xcvo = ((uint32_t)(gxu * csteps) << 11) + ((uint32_t)lh << 10) + ((li & 15) << 4);
     const uint32_t xsvo = ((uint32_t)gxu * bgroups * 256 + (li & 15)) * 2;
     // Issue every load of block blk into stage st.
@@ -418,6 +419,28 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
                 if (v == 15) __builtin_amdgcn_sched_barrier(0);
             }
     }
+    if constexpr (EX) {
+        // The extra fragment (rows xr .. xr + 31): waves 4..7 hand their
+        // share to waves 0..3 (same token tile, the other K-steps), which
+        // store it like the others (f32 out or split partials).
+        __syncthreads();                                  // every wave is done with the stages
+        float *xl = (float *)lds;
+        if (xpar) {
+#pragma unroll
+            for (int v = 0; v < 16; v++) xl[(xm * 16 + v) * 64 + lane] = accx[v];
+        }
+        __syncthreads();
+        const int r = xr + li;
+        if (!xpar && r < R) {
+            const uint32_t ybase = ((uint32_t)(4 * lh) * R + r) * ESZ;
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const float val = accx[v] + xl[(xm * 16 + v) * 64 + lane];
+                const uint32_t so = (uint32_t)(xm * 32 + 8 * (v >> 2) + (v & 3)) * R * ESZ;
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(val), yrs, ybase + so, 0, 0);
+            }
+        }
+    }
 }
 
 // Y[i] = sum_z P[z][i] (n elements, 4 per thread).
@@ -546,14 +569,18 @@ gd_gemm_plan gd_gemm_choose(gd_ctx *ctx, int64_t T, int64_t K, int64_t R, int x_
         return (nblk + bps - 1) / bps;
     };
     if (force) {
-        int mt = 4, nt = 2, s = 1, nw = 4;
-        if (sscanf(force, "%d,%d,%d,%d", &mt, &nt, &s, &nw) >= 3 && kernel_for(mt, nt, nw, 0) &&
-            s >= 1 && s <= 16)
-            return gd_gemm_plan{mt, nt, nz_of(s), nw};
+        int mt = 4, nt = 2, s = 1, nw = 4, ex = 0;
+        if (sscanf(force, "%d,%d,%d,%d,%d", &mt, &nt, &s, &nw, &ex) >= 3 && kernel_for(mt, nt, nw, 0) &&
+            s >= 1 && s <= 16 && (ex == 0 || (ex == 1 && mt == 4 && nt == 2 && nw == 8)))
+            return gd_gemm_plan{mt, nt, nz_of(s), nw, ex};
     }
     const int cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
     gd_gemm_plan best{4, 1, 1};
     double best_cost = 1e30;
+    // The 17-fragment (4, 2, 8) tile (gd_q2_0_gemm_plan17) is not a
+    // candidate: where it fills a round that 512-row tiles leave nearly
+    // empty (the GDN in_proj, R = 8224 = 16 x 512 + 32), the extra K split
+    // it needs costs more than the fuller round saves (pp512 1.1% slower).
     for (const Shape &sh : SHAPES) {
         const int64_t tiles = ((T + sh.mt * 32 - 1) / (sh.mt * 32)) *
                               ((R + sh.nw * sh.nt * 32 - 1) / (sh.nw * sh.nt * 32));
@@ -579,11 +606,14 @@ int gd_gemm_launch(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, int x
     const int nblk = K / 128;
     const int bps = (nblk + p.split - 1) / p.split;     // blocks (128 K) per split
     const int nz = (nblk + bps - 1) / bps;
-    gemm_fn f = kernel_for(p.mt, p.nt, p.nw, p.split > 1 ? 0 : (y_dtype == GD_F16));
+    const int yt = p.split > 1 ? 0 : (y_dtype == GD_F16);
+    gemm_fn f = p.ex ? (p.mt == 4 && p.nt == 2 && p.nw == 8 && yt == 0 ? q2_0_gemm_kernel<4, 2, 8, 0, 1>
+                                                                      : nullptr)
+                     : kernel_for(p.mt, p.nt, p.nw, yt);
     GD_REQUIRE(ctx, f && x_dtype == GD_F16 && (p.split == 1 || y_dtype == GD_F32) && nz == p.split &&
                         R < (1 << 22),
-               "gd_q2_0_gemm: bad plan %d,%d,%d,%d", p.mt, p.nt, p.split, p.nw);
-    const int nrt = gd_blocks(R, p.nw * p.nt * 32);
+               "gd_q2_0_gemm: bad plan %d,%d,%d,%d%s", p.mt, p.nt, p.split, p.nw, p.ex ? " (+1)" : "");
+    const int nrt = gd_blocks(R, (p.nw * p.nt + p.ex) * 32);
     const int64_t units = (int64_t)gd_blocks(T, p.mt * 32) * nz * nrt;
     const int per = (int)((units + 7) / 8);
     hipLaunchKernelGGL(f, dim3(8 * per), dim3(64 * p.nw), 0, ctx->stream, (const uint8_t *)w->codes,
@@ -734,6 +764,8 @@ int gemm_run(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, int x_dtype
     } else {
         p = gd_gemm_choose(ctx, T, w->K, w->R, x_dtype);
     }
+    // The 17-fragment tile writes f32 only: unsplit with f16 Y, the plain tile.
+    if (p.ex && p.split == 1 && y_dtype == GD_F16) p.ex = 0;
     const size_t n = (size_t)T * w->R;
     // Partials are summed 4 at a time: odd-sized outputs run unsplit.
     if (n % 4) p.split = 1;
@@ -779,6 +811,15 @@ extern "C" int gd_q2_0_gemm_plan(gd_ctx *ctx, const gd_q2w *w, int64_t T, const 
                                  int x_dtype, void *Y, int y_dtype, int mt, int nt, int split,
                                  int nw) {
     const gd_gemm_plan p{mt, nt, split, nw};
+    return gemm_run(ctx, w, T, X, x_dtype, Y, y_dtype, &p);
+}
+
+extern "C" int gd_q2_0_gemm_plan17(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X,
+                                   int x_dtype, void *Y, int y_dtype, int split) {
+    GD_CHECK_CTX(ctx);
+    GD_REQUIRE(ctx, split > 1 || y_dtype == GD_F32,
+               "gd_q2_0_gemm_plan17: f16 Y needs a K split (the tile writes f32)");
+    const gd_gemm_plan p{4, 2, split, 8, 1};
     return gemm_run(ctx, w, T, X, x_dtype, Y, y_dtype, &p);
 }
 

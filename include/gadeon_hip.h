@@ -214,6 +214,13 @@ int gd_q2_0_gemm(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X,
  * the reference. */
 int gd_q2_0_gemm_plan(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X,
                       int x_dtype, void *Y, int y_dtype, int mt, int nt, int split, int nw);
+/* gd_q2_0_gemm on the 4 x 2 x 8 tile that also holds a seventeenth 32-row
+ * fragment (544 rows a workgroup), K split `split` ways; it writes f32, so
+ * f16 Y needs split > 1 (partials summed in the workspace).  For tuning and
+ * for tests that cover the planner's choices; no counterpart in the
+ * reference. */
+int gd_q2_0_gemm_plan17(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X,
+                        int x_dtype, void *Y, int y_dtype, int split);
 
 /* Feed-forward GEMM with SwiGLU fused into the epilogue: W is [gate; up]
  * (R = 2 ff rows, ff a multiple of 16), X f16 [T][K], out f16 [T][ff] =

@@ -275,6 +275,36 @@ def test_gemm_every_plan(ctx, xt, yt, mt, nt, nw, split):
     free_w(ctx, w)
 
 
+@pytest.mark.parametrize("T,K,R,split,yt", [(200, 2688, 700, 1, ga.F32), (200, 2688, 1100, 3, ga.F16),
+                                            (77, 384, 600, 2, ga.F32), (512, 5120, 8224, 4, ga.F32)])
+def test_gemm_plan17_vs_oracle(ctx, T, K, R, split, yt):
+    """The 4 x 2 x 8 tile with a seventeenth 32-row fragment (544 rows a
+    workgroup: the waves share the extra fragment's MFMAs by token tile and
+    K-step parity and add their halves at the end), against the oracle:
+    ragged T and R (the last workgroup's rows past R are dropped), K splits,
+    and the GDN in_proj shape the planner gives it (R = 8224, four splits), on
+    sampled tokens there.  Every row of the extra fragments is also checked
+    on its own."""
+    blocks = O.lcg_q2_0(K, R, 7 * K + R)
+    w = upload_w(ctx, blocks, K, R)
+    Xh = O.lcg_normal_f16(T * K, 83).reshape(T, K)
+    dX = ctx.put(Xh.view(np.uint16))
+    dY = ctx.alloc(T * R * (4 if yt == ga.F32 else 2))
+    ctx.gd_q2_0_gemm_plan17(C.byref(w), T, dX, ga.F16, dY, yt, split)
+    Y = ctx.get(dY, (T, R), np.float32 if yt == ga.F32 else np.float16).astype(np.float32)
+    toks = range(T) if T <= 200 else (0, 31, 127, 128, 300, 383, 384, T - 1)
+    extra = np.concatenate([np.arange(c, min(c + 32, R)) for c in range(512, R, 544)])
+    for t in toks:
+        want = O.q2_0_matvec(blocks, K, R, Xh[t].astype(np.float32), threads=8)
+        tol = 2e-3 if yt == ga.F16 else 1e-4
+        assert rel_diff(Y[t], want) < tol, t
+        if len(extra):
+            assert rel_diff(Y[t, extra], want[extra]) < tol, t
+    ctx.free(dX)
+    ctx.free(dY)
+    free_w(ctx, w)
+
+
 def silu(v):
     return v / (1.0 + np.exp(-v))
 
