@@ -550,8 +550,7 @@ double round_cost(const Shape &sh, int64_t units, int cus, int bps) {
 
 // Tile shape, waves per workgroup and K split for a T x K x R product, from
 // a cost model fitted to MI355X timings of every plan on the stack's six
-// prefill shapes (its picks are the best measured plans on five of them and
-// within timing noise on the sixth):
+// prefill shapes, after a table of measured plans for the stack's own shapes:
 //   * a tile (mt, nt, waves) runs up to `occ` workgroups per CU (its LDS:
 //     two stages of one 128-K block; its registers);
 //   * units are dealt evenly, so the busiest CU runs n = ceil(units / CUs)
@@ -575,6 +574,20 @@ gd_gemm_plan gd_gemm_choose(gd_ctx *ctx, int64_t T, int64_t K, int64_t R, int x_
             return gd_gemm_plan{mt, nt, nz_of(s), nw, ex};
     }
     const int cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
+    // Measured plans for the config-4 stack's prefill shapes at T = 512 on a
+    // full MI355X (the fastest of 29 forced plans, min of three sweeps); the
+    // cost model below mispredicts the 2 x 1 x 4 tile several per CU.
+    struct Tuned { int64_t K, R; gd_gemm_plan p; };
+    static constexpr Tuned TUNED[] = {
+            {5120, 8224, {2, 1, 1, 4}},      // GDN in_proj: 54.0 us (the model's pick 57.4)
+            {5120, 12288, {2, 1, 1, 4}},     // attention in_proj: 63.2 (67.5)
+            {2048, 5120, {2, 1, 1, 8}},      // GDN out_proj: 18.7 (19.5)
+            {5120, 5120, {4, 1, 3, 8}},      // attention out_proj: 36.0 (36.5)
+            {17408, 5120, {4, 1, 3, 8}},     // FFN down: 88.3 (89.8)
+    };
+    if (T == 512 && cus == 256)
+        for (const Tuned &t : TUNED)
+            if (t.K == K && t.R == R) return gd_gemm_plan{t.p.mt, t.p.nt, nz_of(t.p.split), t.p.nw};
     gd_gemm_plan best{4, 1, 1};
     double best_cost = 1e30;
     // The 17-fragment (4, 2, 8) tile (gd_q2_0_gemm_plan17) is not a
