@@ -117,9 +117,9 @@ def bench_gemm(ctx, ga, steps: int, warmup: int) -> dict:
         ctx.gd_rand_normal(dX, ga.F16, T * K, 3, 0.0, 1.0)
         dY = ctx.alloc(T * R * 2)
         fn = lambda: ctx.gd_q2_0_gemm(C.byref(w), T, dX, ga.F16, dY, ga.F16)
-        for _ in range(warmup):
+        for _ in range(max(warmup, 20)):
             fn()
-        ms = Timer(ctx).ms(fn, steps)
+        ms = Timer(ctx).ms(fn, max(steps, 100))
         flop = 2 * T * K * R
         res[name] = {"ms": ms, "tflops": flop / (ms * 1e-3) / 1e12}
         total_ms += ms * (2 if name == "gate_up" else 1)
@@ -150,15 +150,18 @@ def bench_gdn_prefill(ctx, ga, steps: int, warmup: int) -> dict:
     ctx.gd_rand_uniform(db, T * H, 31, 0.2, 0.8)
     dS = ctx.alloc(H * d * d * 4)
     do = ctx.alloc(T * H * d * 2)
-    fn = lambda: ctx.gd_gdn_prefill(T, H, H, d, d, dq, H * d, dk, H * d, dv, H * d, ga.F16, dg,
-                                    db, dS, do, H * d, ga.F16, 1 / d ** 0.5, 64)
-    for _ in range(warmup):
-        fn()
-    ms = Timer(ctx).ms(fn, steps)
+    def run(chunk):
+        fn = lambda: ctx.gd_gdn_prefill(T, H, H, d, d, dq, H * d, dk, H * d, dv, H * d, ga.F16,
+                                        dg, db, dS, do, H * d, ga.F16, 1 / d ** 0.5, chunk)
+        for _ in range(warmup):
+            fn()
+        return Timer(ctx).ms(fn, steps)
+    ms = run(64)        # the configuration's own chunk
+    ms32 = run(32)      # the chunk the stack runs (same recurrence, cheaper UT transform)
     for p in (dq, dk, dv, tmp, dg, db, dS, do):
         ctx.free(p)
     return {"us": ms * 1e3, "gflop": 1.4988, "tflops": 1.4988e9 / (ms * 1e-3) / 1e12,
-            "gbs": 10_551_296 / (ms * 1e-3) / 1e9}
+            "gbs": 10_551_296 / (ms * 1e-3) / 1e9, "us_chunk32": ms32 * 1e3}
 
 
 def bench_gdn_decode(ctx, ga, B: int, steps: int, warmup: int) -> dict:
@@ -473,13 +476,19 @@ def kernel_rooflines(ctx, ga, steps: int, pool: int = 8) -> dict:
     gemm = lambda: ctx.gd_q2_0_gemm(C.byref(ws[0]), T, dx, ga.F16, dy, ga.F32)
     # The prefill's own form of it: [gate; up] with the SwiGLU epilogue, f16 out.
     glu = lambda: ctx.gd_q2_0_gemm_swiglu(C.byref(ws[0]), T, dx, dy)
-    for _ in range(pool):
+    # Long windows after a warm-up: over 10-call windows the same GEMM measured
+    # anywhere from 142 to 176 us on one box (clock transitions), over 200
+    # calls within 2%.  The warm-up runs ~20 ms, since these follow the CPU
+    # baseline's seconds of GPU idle.
+    for _ in range(250 * pool):
         gemv()
-    gemm()
-    glu()
-    gemv_ms = t.ms(gemv, max(steps, 5 * pool))
-    gemm_ms = t.ms(gemm, max(steps, 10))
-    glu_ms = t.ms(glu, max(steps, 10))
+    gemv_ms = t.ms(gemv, max(steps, 50 * pool))
+    for _ in range(20):
+        gemm()
+    gemm_ms = t.ms(gemm, max(steps, 200))
+    for _ in range(20):
+        glu()
+    glu_ms = t.ms(glu, max(steps, 200))
     for w in ws:
         ctx.gd_q2w_free(C.byref(w))
     ctx.free(dx)

@@ -574,11 +574,13 @@ gd_gemm_plan gd_gemm_choose(gd_ctx *ctx, int64_t T, int64_t K, int64_t R, int x_
             return gd_gemm_plan{mt, nt, nz_of(s), nw, ex};
     }
     const int cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
-    // Measured plans for the config-4 stack's prefill shapes at T = 512 on a
-    // full MI355X (the fastest of 29 forced plans, min of three sweeps); the
-    // cost model below mispredicts the 2 x 1 x 4 tile several per CU.
+    // Measured plans for the config-4 stack's prefill shapes and the 17408-row
+    // gate|up at T = 512 on a full MI355X (the fastest of 29-41 forced plans,
+    // min of repeated sweeps); the cost model below mispredicts the 2 x 1 x 4
+    // tile several per CU.
     struct Tuned { int64_t K, R; gd_gemm_plan p; };
     static constexpr Tuned TUNED[] = {
+            {5120, 17408, {2, 1, 1, 4}},     // gate|up, 17408 rows: 98.6 us (105.6)
             {5120, 8224, {2, 1, 1, 4}},      // GDN in_proj: 54.0 us (the model's pick 57.4)
             {5120, 12288, {2, 1, 1, 4}},     // attention in_proj: 63.2 (67.5)
             {2048, 5120, {2, 1, 1, 8}},      // GDN out_proj: 18.7 (19.5)
