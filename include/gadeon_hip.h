@@ -379,7 +379,8 @@ int gd_gdn_decode(gd_ctx *ctx, int B, int nV, int nK, int dS,
  *   q_stride, k_stride, v_stride between tokens), g, beta [T][nV] f32,
  *   S [nV][dk][dv] f32 in/out, o [T][nV][dv] (o_dtype, stride o_stride).
  *   q/k are used as given (normalize first with gd_l2norm_rows).  C is the
- *   chunk length (16, 32 or 64); T need not be a multiple of C.
+ *   chunk length (16, 32 or 64; 32 is the fastest on MI355X at T 128..2048);
+ *   T need not be a multiple of C.
  *   Currently dk == dv == 128. */
 int gd_gdn_prefill(gd_ctx *ctx, int64_t T, int nV, int nK, int dk, int dv,
                    const void *q, int64_t q_stride, const void *k,
