@@ -105,8 +105,12 @@ template <int MT, int NT, int NW, int EX> struct Stage {
 // MFMAs per block the waves share (wave w: token tile w % 4, the K-steps of
 // parity w / 4; waves 4..7 hand their sums to waves 0..3 at the end), so
 // that ff = 17408 = 64 x 272 columns fill one round of 256 workgroups.
+// Two waves per SIMD, except the four-wave tiles of 8 fragments a wave
+// ((8,1) and (4,2) with NW = 4), whose 128 accumulators and operands do not
+// fit two waves' registers: one wave per SIMD, as the planner's tile times
+// assume.
 template <int MT, int NT, int NW, int YT, int EX = 0>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) void q2_0_gemm_kernel(
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 4 && MT * NT == 8 ? 1 : 2))) void q2_0_gemm_kernel(
         const uint8_t *__restrict__ codes, const uint16_t *__restrict__ scales,
         const void *__restrict__ Xv, void *__restrict__ Yv, int T, int K, int R, int bps,
         int nrt, int nz, int per, int glu_ff, int glu_r0, int glu_end) {
