@@ -133,6 +133,24 @@ def bench_gemm(ctx, ga, steps: int, warmup: int) -> dict:
     return res
 
 
+def baseline_gates(ctx, ga, n: int, nV: int, seed: int, dg, db) -> None:
+    """g = -softplus(N(0,1)) and beta = sigmoid(N(0,1)), as BASELINE draws
+    them: gd_gdn_gate of two normal streams with dt = 0 and aNeg = -1."""
+    pre_a, pre_b = ctx.alloc(n * 4), ctx.alloc(n * 4)
+    ctx.gd_rand_normal(pre_a, ga.F32, n, seed, 0.0, 1.0)
+    ctx.gd_rand_normal(pre_b, ga.F32, n, seed + 1, 0.0, 1.0)
+    dt, an = gate_consts(ctx, nV)
+    ctx.gd_gdn_gate(pre_b, pre_a, dt, an, db, dg, nV, n)
+    for p in (pre_a, pre_b, dt, an):
+        ctx.free(p)
+
+
+def gate_consts(ctx, nV: int):
+    """dt = 0 and aNeg = -1 per head: the gate then gives g = -softplus(a)."""
+    import numpy as np
+    return (ctx.put(np.zeros(nV, np.float32)), ctx.put(np.full(nV, -1.0, np.float32)))
+
+
 def bench_gdn_prefill(ctx, ga, steps: int, warmup: int) -> dict:
     """Config 2: T=512, 16 heads, d=128, chunk 64, fp16 q/k/v/o, f32 state."""
     T, H, d = 512, 16, 128
@@ -146,8 +164,7 @@ def bench_gdn_prefill(ctx, ga, steps: int, warmup: int) -> dict:
         ctx.gd_l2norm_rows(tmp, d, H, H * d, T, 1e-6)
         ctx.gd_cast(tmp, ga.F32, p, ga.F16, T * H * d)
     dg, db = ctx.alloc(T * H * 4), ctx.alloc(T * H * 4)
-    ctx.gd_rand_uniform(dg, T * H, 30, -1.5, -0.1)
-    ctx.gd_rand_uniform(db, T * H, 31, 0.2, 0.8)
+    baseline_gates(ctx, ga, T * H, H, 30, dg, db)
     dS = ctx.alloc(H * d * d * 4)
     do = ctx.alloc(T * H * d * 2)
     def run(chunk):
@@ -164,25 +181,35 @@ def bench_gdn_prefill(ctx, ga, steps: int, warmup: int) -> dict:
             "gbs": 10_551_296 / (ms * 1e-3) / 1e9, "us_chunk32": ms32 * 1e3}
 
 
-def bench_gdn_decode(ctx, ga, B: int, steps: int, warmup: int) -> dict:
-    """Config 3: B sequences, 16 heads, 128x128 f32 state, raw f16 q/k, fused
-    L2-norm + gate + delta update; one launch per token step."""
-    H, d = 16, 128
-    dS = ctx.alloc(B * H * d * d * 4)
-    ctx.gd_rand_normal(dS, ga.F32, B * H * d * d, 40, 0.0, 0.02)
+def decode_inputs(ctx, ga, B: int, H: int, d: int):
+    """Config 3's per-step inputs: raw q, k, v ~ N(0,1) f16 (the fused L2
+    norm does real work) and the gate pre-activations a, b ~ N(0,1) with
+    dt = 0, aNeg = -1, so the fused gate forms g = -softplus(N(0,1)) and
+    beta = sigmoid(N(0,1)), BASELINE's draws, inside the step."""
     dq, dk, dv = ctx.alloc(B * H * d * 2), ctx.alloc(B * H * d * 2), ctx.alloc(B * H * d * 2)
     for i, p in enumerate((dq, dk, dv)):
         ctx.gd_rand_normal(p, ga.F16, B * H * d, 41 + i, 0.0, 1.0)
-    dg, db = ctx.alloc(B * H * 4), ctx.alloc(B * H * 4)
-    ctx.gd_rand_uniform(dg, B * H, 44, -1.5, -0.1)
-    ctx.gd_rand_uniform(db, B * H, 45, 0.2, 0.8)
+    da, db = ctx.alloc(B * H * 4), ctx.alloc(B * H * 4)
+    ctx.gd_rand_normal(da, ga.F32, B * H, 44, 0.0, 1.0)
+    ctx.gd_rand_normal(db, ga.F32, B * H, 45, 0.0, 1.0)
+    dt, an = gate_consts(ctx, H)
+    return [dq, dk, dv, da, db, dt, an]
+
+
+def bench_gdn_decode(ctx, ga, B: int, steps: int, warmup: int) -> dict:
+    """Config 3: B sequences, 16 heads, 128x128 f32 state, raw f16 q/k, fused
+    gate + L2-norm + delta update; one launch per token step."""
+    H, d = 16, 128
+    dS = ctx.alloc(B * H * d * d * 4)
+    ctx.gd_rand_normal(dS, ga.F32, B * H * d * d, 40, 0.0, 0.02)
+    dq, dk, dv, da, db, dt, an = bufs = decode_inputs(ctx, ga, B, H, d)
     do = ctx.alloc(B * H * d * 2)
-    fn = lambda: ctx.gd_gdn_decode(B, H, H, d, dq, dk, dv, ga.F16, dg, db, None, None, dS, do,
+    fn = lambda: ctx.gd_gdn_decode(B, H, H, d, dq, dk, dv, ga.F16, da, db, dt, an, dS, do,
                                    1 / d ** 0.5, 1e-6)
     for _ in range(warmup):
         fn()
     ms = Timer(ctx).ms(fn, steps)
-    for p in (dS, dq, dk, dv, dg, db, do):
+    for p in (dS, do, *bufs):
         ctx.free(p)
     per_step = B * 2_113_664
     return {"B": B, "us_per_step": ms * 1e3, "gbs": per_step / (ms * 1e-3) / 1e9,
@@ -197,24 +224,19 @@ def bench_gdn_decode_pool(ctx, ga, B: int, pool: int, steps: int, warmup: int) -
     n = B * H * d * d
     dS = ctx.alloc(pool * n * 4)
     ctx.gd_rand_normal(dS, ga.F32, pool * n, 40, 0.0, 0.02)
-    dq, dk, dv = ctx.alloc(B * H * d * 2), ctx.alloc(B * H * d * 2), ctx.alloc(B * H * d * 2)
-    for i, p in enumerate((dq, dk, dv)):
-        ctx.gd_rand_normal(p, ga.F16, B * H * d, 41 + i, 0.0, 1.0)
-    dg, db = ctx.alloc(B * H * 4), ctx.alloc(B * H * 4)
-    ctx.gd_rand_uniform(dg, B * H, 44, -1.5, -0.1)
-    ctx.gd_rand_uniform(db, B * H, 45, 0.2, 0.8)
+    dq, dk, dv, da, db, dt, an = bufs = decode_inputs(ctx, ga, B, H, d)
     do = ctx.alloc(B * H * d * 2)
     step = [0]
 
     def fn():
         s = dS + (step[0] % pool) * n * 4
         step[0] += 1
-        ctx.gd_gdn_decode(B, H, H, d, dq, dk, dv, ga.F16, dg, db, None, None, s, do,
+        ctx.gd_gdn_decode(B, H, H, d, dq, dk, dv, ga.F16, da, db, dt, an, s, do,
                           1 / d ** 0.5, 1e-6)
     for _ in range(max(warmup, pool)):
         fn()
     ms = Timer(ctx).ms(fn, steps)
-    for p in (dS, dq, dk, dv, dg, db, do):
+    for p in (dS, do, *bufs):
         ctx.free(p)
     per_step = B * 2_113_664
     return {"B": B, "pool_sets": pool, "state_mib": pool * n * 4 / 2 ** 20,
@@ -304,6 +326,8 @@ def run_stack(ctx, ga, args) -> dict:
     log("creating the 64-layer stack (random init on the device) ...")
     ctx.check(ctx.lib.gd_stack_create(ctx.h, C.byref(sc), 2024, C.byref(h)))
     lib = ctx.lib
+    if getattr(args, "eager", False):
+        ctx.check(lib.gd_stack_set_eager(h, 1))
     ids = np.random.default_rng(512).integers(0, c["n_vocab"], PP).astype(np.int32)
     gen = np.empty(TG, np.int32)
     nxt = C.c_int32()
@@ -332,8 +356,10 @@ def run_stack(ctx, ga, args) -> dict:
             log(f"pass {i}: pp{PP} {pp_ms[-1]:.1f} ms, tg{TG} {tg_ms[-1]:.1f} ms, "
                 f"first tokens {nxt.value} {list(gen[:4])}")
         cpu = None
+        pp_vs_decode = None
         if args.cpu_seconds > 0 and tg_on:
             cpu = cpu_baseline_stack(ctx, ga, h, c, args.cpu_seconds)
+            pp_vs_decode = prefill_vs_decode(ctx, h, c, ids)
     finally:
         lib.gd_stack_destroy(h)
     pp = sum(pp_ms) / len(pp_ms)
@@ -342,13 +368,57 @@ def run_stack(ctx, ga, args) -> dict:
                 "pp_tflops": stack_flops_pp(c, PP) / (pp * 1e-3) / 1e12, "pp_ms_all": pp_ms}
     tg = sum(tg_ms) / len(tg_ms)
     wb = stack_weight_bytes(c)
+    if cpu is not None:
+        cpu["parity"]["pp512_vs_decode"] = pp_vs_decode
     return {"pp_ms": pp, "tg_ms": tg, "pp_tok_s": PP / (pp * 1e-3), "tg_tok_s": TG / (tg * 1e-3),
             "pp_tflops": stack_flops_pp(c, PP) / (pp * 1e-3) / 1e12,
             "tg_weight_gbs": wb["total"] / (tg / TG * 1e-3) / 1e9, "weight_bytes": wb,
             "pp_ms_all": pp_ms, "tg_ms_all": tg_ms, "cpu": cpu}
 
 
+def prefill_vs_decode(ctx, h, c, ids) -> dict:
+    """The timed pp512 itself at full depth: the last-token logits of one
+    512-id gd_stack_prefill (T = 512 GEMM plans, 16 chunks of chunked GDN
+    prefill, 512-query flash attention) against 512 token-serial
+    gd_stack_decode steps over the same ids from a reset state, the decode
+    path the oracle checks above.  Both on the GPU; reported against
+    PARITY_64 (the oracle checks above are the ones that fail the run)."""
+    import numpy as np
+    lib = ctx.lib
+    nxt = C.c_int32()
+    a = np.empty(c["n_vocab"], np.float32)
+    b = np.empty(c["n_vocab"], np.float32)
+    ctx.check(lib.gd_stack_reset(h))
+    ctx.check(lib.gd_stack_prefill(h, ids.ctypes.data, len(ids), C.byref(nxt), a.ctypes.data))
+    ctx.check(lib.gd_stack_reset(h))
+    for i, t in enumerate(ids):
+        ctx.check(lib.gd_stack_decode(h, int(t), C.byref(nxt),
+                                      b.ctypes.data if i == len(ids) - 1 else None))
+    r = float(np.abs(a.astype(np.float64) - b).max() / np.abs(b).max())
+    log(f"parity: pp{len(ids)} prefill vs {len(ids)} token-serial decodes, last-token logits "
+        f"relDiff {r:.2e}")
+    return {"tokens": len(ids), "rel_diff": r, "within": r < PARITY_64, "tolerance": PARITY_64,
+            "what": "GPU pp512 prefill vs 512 GPU decode steps on the same ids, last-token "
+                    "logits, 64 layers, full width"}
+
+
 PARITY_64 = 1e-2   # 64-layer logits bound (see cpu_baseline_stack)
+PREFILL_T = 64     # ids in the 64-layer prefill parity chunk
+
+# What the arithmetic of each path is, stated beside "dtype".
+NUMERICS = {
+    "prefill_gemm": "f16 activations x exact f16 (code-1)*d weights on v_mfma_f32_32x32x16_f16, "
+                    "f32 accumulate",
+    "decode_gemv": "f16 x (the reference's decode GEMV reads f32 x) as e4m3 pieces with a "
+                   "per-128-block power-of-two scale (3 pieces hold an f16 exactly), fp4 "
+                   "codes on the scaled v_mfma_scale_f32_16x16x128_f8f6f4; each group of 8 "
+                   "products is summed aligned to its largest with ~13 bits kept, then f32 "
+                   "accumulate (relDiff vs f64: ~4e-6 for N(0,1) x, ~2e-4 with 3000x outliers)",
+    "gdn": "f32 state and recurrence; chunked prefill products on f16 MFMA with hi/lo splits "
+           "of the f32 operands (~22 bits)",
+    "residual_and_norms": "f32",
+    "kv_cache": "f16",
+}
 
 
 def cpu_baseline_stack(ctx, ga, h, c, seconds: float) -> dict:
@@ -419,6 +489,25 @@ def cpu_baseline_stack(ctx, ga, h, c, seconds: float) -> dict:
     if not max(rels16) < PARITY_64:
         raise SystemExit(f"bench: GPU stack logits differ from the oracle (relDiff "
                          f"{max(rels16):.3e} >= {PARITY_64}) on the 64-layer configuration")
+    # The prefill path at full depth: one chunk of PREFILL_T ids through
+    # gd_stack_prefill (GEMMs, chunked GDN prefill over two 32-token chunks,
+    # MFMA flash attention, split-K partials summed by their readers) against
+    # the oracle's BonsaiEngine.forward over the same chunk, f16-staged
+    # mat-vec inputs and K/V as the GPU prefill stages them.
+    pids = ((np.arange(PREFILL_T) * 7919 + 3) % c["n_vocab"]).astype(np.int32)
+    refp = O.Stack(c, cread, stage_f16=True, threads=threads)
+    t0 = time.perf_counter()
+    ref_pl = refp.prefill(pids)[1]
+    tp = time.perf_counter() - t0
+    ctx.check(lib.gd_stack_reset(h))
+    ctx.check(lib.gd_stack_prefill(h, pids.ctypes.data, PREFILL_T, C.byref(nxt),
+                                   logits.ctypes.data))
+    relp = rel(logits, ref_pl)
+    log(f"parity: GPU vs oracle prefill of {PREFILL_T} ids, last-token logits relDiff "
+        f"{relp:.2e} (oracle {tp:.1f} s)")
+    if not relp < PARITY_64:
+        raise SystemExit(f"bench: GPU stack prefill logits differ from the oracle (relDiff "
+                         f"{relp:.3e} >= {PARITY_64}) on the 64-layer configuration")
     return {"value": 1.0 / dt, "unit": "tok/s", "cores": threads, "kind": "port",
             "host_cpu_count": ncpu,
             "sample": f"{n} tokens through the 64-layer stack (token-by-token C restatement of "
@@ -428,6 +517,12 @@ def cpu_baseline_stack(ctx, ga, h, c, seconds: float) -> dict:
             "parity": {"tokens": m, "max_rel_diff": max(rels16), "tolerance": PARITY_64,
                        "what": "GPU gd_stack_decode logits vs the oracle on the same tokens, "
                                "64 layers, full width, f16 decode GEMV inputs on both sides",
+                       "prefill_64": {"tokens": PREFILL_T, "rel_diff": relp,
+                                      "tolerance": PARITY_64,
+                                      "what": f"GPU gd_stack_prefill of {PREFILL_T} ids from a "
+                                              "reset state vs the oracle's forward over the "
+                                              "same chunk (last-token logits), 64 layers, "
+                                              "full width"},
                        "f32_decode_inputs": {"tokens": n, "max_rel_diff": max(rels),
                                              "what": "the same against the reference's f32 "
                                                      "decode inputs (measured deviation)"}}}
@@ -493,14 +588,47 @@ def kernel_rooflines(ctx, ga, steps: int, pool: int = 8) -> dict:
         ctx.gd_q2w_free(C.byref(w))
     ctx.free(dx)
     ctx.free(dy)
+    head = gemv_lm_head(ctx, ga, steps)
     gemv_bytes = R * K * 17 // 64 + K * 2 + R * 4
     return {"gemv": {"shape": f"K={K} R={R} x f16", "us": gemv_ms * 1e3, "bytes": gemv_bytes,
                      "gbs": gemv_bytes / (gemv_ms * 1e-3) / 1e9, "pool": pool},
+            "gemv_lm_head": head,
             "gemm": {"shape": f"T={T} K={K} R={R}", "us": gemm_ms * 1e3,
                      "tflops": 2 * T * K * R / (gemm_ms * 1e-3) / 1e12},
             "gemm_swiglu": {"shape": f"T={T} K={K} R={R} (gate|up, SwiGLU epilogue, f16 out)",
                             "us": glu_ms * 1e3, "flop": 2 * T * K * R,
                             "tflops": 2 * T * K * R / (glu_ms * 1e-3) / 1e12}}
+
+
+def gemv_lm_head(ctx, ga, steps: int, pool: int = 2) -> dict:
+    """The decode lm_head's Q2_0 GEMV at config 4's shape (K=5120, R=151936,
+    f16 x, f32 logits), the largest single weight stream of a token, rotated
+    over `pool` copies (2 x 206.6 MB, beyond the 256 MB Infinity Cache)."""
+    K, R = 5120, 151936
+    ws = []
+    for i in range(pool):
+        w = ga.Q2W()
+        ctx.gd_q2w_alloc(K, R, C.byref(w))
+        ctx.gd_rand_q2w(C.byref(w), 91 + i, 0.01, 0.05)
+        ws.append(w)
+    dx = ctx.alloc(K * 2)
+    ctx.gd_rand_normal(dx, ga.F16, K, 92, 0.0, 1.0)
+    dy = ctx.alloc(R * 4)
+    it = [0]
+
+    def gemv():
+        ctx.gd_q2_0_gemv(C.byref(ws[it[0] % pool]), dx, ga.F16, dy)
+        it[0] += 1
+    for _ in range(100 * pool):
+        gemv()
+    ms = Timer(ctx).ms(gemv, max(steps, 50 * pool))
+    for w in ws:
+        ctx.gd_q2w_free(C.byref(w))
+    ctx.free(dx)
+    ctx.free(dy)
+    nbytes = R * K * 17 // 64 + K * 2 + R * 4
+    return {"shape": f"K={K} R={R} x f16", "us": ms * 1e3, "bytes": nbytes,
+            "gbs": nbytes / (ms * 1e-3) / 1e9, "pool": pool}
 
 
 def calibration_copy(ctx, ga, n: int = 1 << 24) -> dict:
@@ -556,6 +684,9 @@ def main() -> int:
                          "the roofline GEMV/GEMM and a calibration copy; pp: only the config-4 "
                          "pp512 passes (the last two for rocprofv3 runs)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--eager", action="store_true",
+                    help="decode steps as direct launches instead of the captured graph "
+                         "(gd_stack_set_eager; for kernel-trace profiles)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
@@ -583,6 +714,7 @@ def main() -> int:
         ctx.close()
     if args.workload == "stack":
         g = r["kernels"]["gemv"]
+        hd = r["kernels"]["gemv_lm_head"]
         gl = r["kernels"]["gemm_swiglu"]
         out = {
             "metric": BASELINE_METRIC,
@@ -596,6 +728,7 @@ def main() -> int:
             "scaling": "weak",
             "vs_baseline": None,
             "dtype": "f16",
+            "numerics": NUMERICS,
             "data": "synthetic (random-init weights and a random 512-id prompt, generated on "
                     "the device / seeded)",
             "config": {"workload": "config 4: 64-layer Bonsai-27B-shape hybrid stack, Q2_0 "
@@ -611,6 +744,13 @@ def main() -> int:
                                    f"{g['pool']} copies, streamed from HBM)"},
             # pp512's dominant kernel (the value metric's): the FFN gate|up GEMM in
             # the form the prefill runs it, against the dense f16 MFMA peak.
+            # The decode lm_head's GEMV (K=5120, R=151936): the same kernel on
+            # the largest weight stream of a token.
+            "roofline_lm_head": {"bound": "hbm", "achieved": round(hd["gbs"], 1),
+                                 "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                 "frac": round(hd["gbs"] / HBM_PEAK_GBS, 4),
+                                 "kernel": "q2_0_gemv_mfma " + hd["shape"] + " (weights rotated "
+                                           f"over {hd['pool']} copies, streamed from HBM)"},
             "roofline_prefill": {"bound": "mfma", "achieved": round(gl["tflops"], 1),
                                  "peak": FP16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                                  "frac": round(gl["tflops"] / FP16_MFMA_PEAK_TFLOPS, 4),

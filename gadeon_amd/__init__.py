@@ -9,6 +9,7 @@ from __future__ import annotations
 
 import ctypes as C
 import os
+import weakref
 from pathlib import Path
 
 import numpy as np
@@ -106,6 +107,8 @@ _PROTOS = {
     "gd_stack_prefill": (_i, [_vp, _vp, _i, C.POINTER(C.c_int32), _vp]),
     "gd_stack_decode": (_i, [_vp, C.c_int32, C.POINTER(C.c_int32), _vp]),
     "gd_stack_request_stop": (_i, [_vp]),
+    "gd_stack_set_eager": (_i, [_vp, _i]),
+    "gd_stack_should_stop": (_i, [_vp, C.POINTER(_i)]),
     "gd_stack_tensor": (_i, [_vp, _i, C.c_char_p, _Q2WP, C.POINTER(_i64), C.POINTER(_fp),
                          C.POINTER(_i64)]),
     "gd_stack_position": (_i, [_vp, C.POINTER(_i64)]),
@@ -244,7 +247,9 @@ class Context:
 
 class GGUF:
     """A GGUF file opened by the library's host reader (gd_gguf_*, no device
-    needed).  Tensors come back as read-only numpy views of the mapping."""
+    needed).  Tensors come back as read-only numpy views of the mapping; the
+    mapping stays in place until close() has been called AND every view (and
+    every array derived from one) is gone, so a view never outlives it."""
 
     def __init__(self, path: os.PathLike | str):
         self.lib = load()
@@ -253,6 +258,13 @@ class GGUF:
         if rc != GD_OK:
             raise GDError(rc, self.lib.gd_last_error(None).decode())
         self.h = h
+        self._views = 0            # live tensor views of the mapping
+        self._closing = False      # close() called; unmap when the last view goes
+
+    def _handle(self):
+        if self._closing or not self.mapped:
+            raise GDError(GD_EINVAL, "GGUF file is closed")
+        return self.h
 
     def _check(self, rc: int) -> None:
         if rc != GD_OK:
@@ -260,59 +272,79 @@ class GGUF:
 
     def info(self) -> tuple[int, int, int]:
         nt, nkv, ver = _i64(), _i64(), _i()
-        self._check(self.lib.gd_gguf_info(self.h, C.byref(nt), C.byref(nkv), C.byref(ver)))
+        self._check(self.lib.gd_gguf_info(self._handle(), C.byref(nt), C.byref(nkv), C.byref(ver)))
         return nt.value, nkv.value, ver.value
 
     def tensor(self, name: str) -> tuple[tuple[int, ...], int, np.ndarray]:
         """(dims with ne0 first, ggml type, raw bytes as a uint8 array)."""
         nd, ty, data, nb = _i(), _i(), _vp(), _sz()
         dims = (_i64 * 4)()
-        self._check(self.lib.gd_gguf_tensor(self.h, name.encode(), C.byref(nd), dims,
+        self._check(self.lib.gd_gguf_tensor(self._handle(), name.encode(), C.byref(nd), dims,
                                             C.byref(ty), C.byref(data), C.byref(nb)))
         buf = (C.c_uint8 * nb.value).from_address(data.value)
+        # The array (and anything sliced from it) holds buf; buf's finalizer
+        # holds this object, so the mapping outlives every view.
+        self._views += 1
+        weakref.finalize(buf, self._release_view)
         arr = np.frombuffer(buf, np.uint8)
         arr.flags.writeable = False
         return tuple(dims[:nd.value]), ty.value, arr
 
+    def _release_view(self) -> None:
+        self._views -= 1
+        if self._closing and self._views == 0:
+            self._unmap()
+
+    def _unmap(self) -> None:
+        if getattr(self, "h", None):
+            self.lib.gd_gguf_close(self.h)
+            self.h = None
+
+    @property
+    def mapped(self) -> bool:
+        """True while the file mapping is in place."""
+        return bool(getattr(self, "h", None))
+
     def int(self, key: str) -> int:
         v = _i64()
-        self._check(self.lib.gd_gguf_get_int(self.h, key.encode(), C.byref(v)))
+        self._check(self.lib.gd_gguf_get_int(self._handle(), key.encode(), C.byref(v)))
         return v.value
 
     def float(self, key: str) -> float:
         v = C.c_double()
-        self._check(self.lib.gd_gguf_get_float(self.h, key.encode(), C.byref(v)))
+        self._check(self.lib.gd_gguf_get_float(self._handle(), key.encode(), C.byref(v)))
         return v.value
 
     def bool(self, key: str) -> bool:
         v = _i()
-        self._check(self.lib.gd_gguf_get_bool(self.h, key.encode(), C.byref(v)))
+        self._check(self.lib.gd_gguf_get_bool(self._handle(), key.encode(), C.byref(v)))
         return bool(v.value)
 
     def floats(self, key: str) -> list[float]:
         v, n = C.POINTER(C.c_double)(), _i64()
-        self._check(self.lib.gd_gguf_get_floats(self.h, key.encode(), C.byref(v), C.byref(n)))
+        self._check(self.lib.gd_gguf_get_floats(self._handle(), key.encode(), C.byref(v), C.byref(n)))
         return [v[i] for i in range(n.value)]
 
     def string(self, key: str) -> str:
         v = C.c_char_p()
-        self._check(self.lib.gd_gguf_get_string(self.h, key.encode(), C.byref(v)))
+        self._check(self.lib.gd_gguf_get_string(self._handle(), key.encode(), C.byref(v)))
         return v.value.decode()
 
     def ints(self, key: str) -> list[int]:
         v, n = C.POINTER(_i64)(), _i64()
-        self._check(self.lib.gd_gguf_get_ints(self.h, key.encode(), C.byref(v), C.byref(n)))
+        self._check(self.lib.gd_gguf_get_ints(self._handle(), key.encode(), C.byref(v), C.byref(n)))
         return [v[i] for i in range(n.value)]
 
     def stack_config(self) -> StackConfig:
         c = StackConfig()
-        self._check(self.lib.gd_gguf_stack_config(self.h, C.byref(c)))
+        self._check(self.lib.gd_gguf_stack_config(self._handle(), C.byref(c)))
         return c
 
     def close(self) -> None:
-        if getattr(self, "h", None):
-            self.lib.gd_gguf_close(self.h)
-            self.h = None
+        """No further reads; the mapping goes when the last view does."""
+        self._closing = True
+        if self._views == 0:
+            self._unmap()
 
     def __enter__(self):
         return self

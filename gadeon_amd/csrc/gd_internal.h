@@ -47,6 +47,11 @@ int gd_gemv_mfma(gd_ctx *ctx, const gd_q2w *w, const void *x, int x_dtype, float
 int gd_gemv_mfma_norm(gd_ctx *ctx, const gd_q2w *w, const float *h, const float *delta, int nd,
                       int dstride, const float *normw, float eps, float *hout, float *y,
                       uint16_t *glu_out = nullptr);
+// Token-serial gdnScanBatch (gdn_scan_batch, Kernels.metal:1525-1565) for
+// state sizes other than the chunked prefill's 128 (dS <= 1024).
+int gd_gdn_scan_batch_serial(gd_ctx *ctx, const float *convOutN, int keyDim, int valueDim,
+                             int convDim, const float *gN, const float *betaN, float *S,
+                             float *oN, int nV, int nK, int dS, float qScale, int64_t N);
 // K splits an f16-x GEMV of this shape should use (partials summed by the consumer).
 int gd_gemv_ksplit(gd_ctx *ctx, int64_t K, int64_t R);
 // Prefill GEMM plan: MT x 32 tokens by 4 x NT x 32 weight rows per

@@ -332,7 +332,65 @@ __global__ void gd_scan_generic_kernel(const float *q, const float *k, const flo
     o[(int64_t)hv * dS + j] = acc * qScale;
 }
 
+// N tokens of the scan for state sizes the chunked prefill does not take
+// (dS != 128): gdn_scan_batch (Kernels.metal:1525-1565), which
+// MetalEnc.gdnScanBatch dispatches for any dS (MetalEnc.swift:741-778).  One
+// workgroup per value head, thread j owning value column j of S (dS <= 1024),
+// tokens in order; q and k of the token are staged once per workgroup in
+// LDS (the column walks read them at every row), S stays in device memory
+// as in the reference (a head's dS x dS f32 exceeds LDS beyond 181).
+__global__ __launch_bounds__(1024) void gd_scan_batch_serial_kernel(
+        const float *convOutN, const float *gN, const float *betaN, float *S, float *oN, int nV,
+        int nK, int dS, float qScale, int64_t N, int convDim, int keyDim, int valueDim) {
+    extern __shared__ float qk[];                 // [2][dS]: q, k of the token
+    const int hv = blockIdx.x, j = threadIdx.x, hk = hv % nK;
+    float *Sh = S + (int64_t)hv * dS * dS;
+    for (int64_t n = 0; n < N; n++) {
+        const float *row = convOutN + n * convDim;
+        __syncthreads();                          // the previous token's reads are done
+        for (int i = threadIdx.x; i < dS; i += blockDim.x) {
+            qk[i] = row[(int64_t)hk * dS + i];
+            qk[dS + i] = row[keyDim + (int64_t)hk * dS + i];
+        }
+        __syncthreads();
+        if (j >= dS) continue;
+        const float gam = expf(gN[n * nV + hv]), b = betaN[n * nV + hv];
+        const float *k = qk + dS, *q = qk;
+        float sk = 0.0f;
+        for (int i = 0; i < dS; i++) {
+            const float x = Sh[(int64_t)i * dS + j] * gam;
+            Sh[(int64_t)i * dS + j] = x;
+            sk += x * k[i];
+        }
+        const float d = b * (row[2 * (int64_t)keyDim + (int64_t)hv * dS + j] - sk);
+        float acc = 0.0f;
+        for (int i = 0; i < dS; i++) {
+            const float x = Sh[(int64_t)i * dS + j] + k[i] * d;
+            Sh[(int64_t)i * dS + j] = x;
+            acc += x * q[i];
+        }
+        oN[n * valueDim + (int64_t)hv * dS + j] = acc * qScale;
+    }
+}
+
 }  // namespace
+
+// Token-serial gdnScanBatch for any dS up to 1024 (the caller has checked
+// the pointers and the dimensions).
+int gd_gdn_scan_batch_serial(gd_ctx *ctx, const float *convOutN, int keyDim, int valueDim,
+                             int convDim, const float *gN, const float *betaN, float *S,
+                             float *oN, int nV, int nK, int dS, float qScale, int64_t N) {
+    GD_REQUIRE(ctx, dS > 0 && dS <= 1024 && nV > 0 && nK > 0 && nV <= 65535,
+               "gd_gdn_scan_batch: dS=%d nV=%d nK=%d (the token-serial scan takes dS <= 1024)",
+               dS, nV, nK);
+    if (N <= 0) return GD_OK;
+    const int threads = (dS + 63) / 64 * 64;
+    hipLaunchKernelGGL(gd_scan_batch_serial_kernel, dim3(nV), dim3(threads),
+                       (size_t)2 * dS * sizeof(float), ctx->stream, convOutN, gN, betaN, S, oN,
+                       nV, nK, dS, qScale, N, convDim, keyDim, valueDim);
+    GD_LAUNCHED(ctx, "gdn_scan_batch");
+    return GD_OK;
+}
 
 extern "C" int gd_gdn_decode(gd_ctx *ctx, int B, int nV, int nK, int dS, const void *q,
                              const void *k, const void *v, int io_dtype, const float *g_in,

@@ -885,6 +885,12 @@ extern "C" int gd_gdn_scan_batch(gd_ctx *ctx, const float *convOutN, int keyDim,
     GD_REQUIRE(ctx, convOutN && gN && betaN && S && oN, "gd_gdn_scan_batch: null pointer");
     GD_REQUIRE(ctx, keyDim == nK * dS && valueDim == nV * dS && convDim >= 2 * keyDim + valueDim,
                "gd_gdn_scan_batch: keyDim/valueDim/convDim inconsistent with nK, nV, dS");
+    // The chunked prefill holds 128 x 128 states; other sizes take the
+    // token-serial scan, as MetalEnc.gdnScanBatch falls back to
+    // gdn_scan_batch where gdn_scan_batch2 does not fit (MetalEnc.swift:760-777).
+    if (dS != 128)
+        return gd_gdn_scan_batch_serial(ctx, convOutN, keyDim, valueDim, convDim, gN, betaN, S,
+                                        oN, nV, nK, dS, qScale, N);
     return gd_gdn_prefill(ctx, N, nV, nK, dS, dS, convOutN, convDim, convOutN + keyDim, convDim,
                           convOutN + 2 * keyDim, convDim, GD_F32, gN, betaN, S, oN, valueDim,
                           GD_F32, qScale, 64);

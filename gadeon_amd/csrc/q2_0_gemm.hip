@@ -562,21 +562,15 @@ double round_cost(const Shape &sh, int64_t units, int cus, int bps) {
 //     per 128-K block of the split (a CU shared by more workgroups finishes
 //     more of them per us, each one more slowly);
 //   * split partials cost (2s+1) f32 passes over T x R (CS us per MB).
-// GADEON_GEMM_CFG="MT,NT,S[,NW]" forces a plan.
+// The plan depends on the shape and the CU count alone (no process-wide
+// override); gd_q2_0_gemm_plan runs a plan the caller chooses.
 gd_gemm_plan gd_gemm_choose(gd_ctx *ctx, int64_t T, int64_t K, int64_t R, int x_dtype) {
-    static const char *force = getenv("GADEON_GEMM_CFG");
     (void)x_dtype;
     const int nblk = (int)(K / 128);
     auto nz_of = [&](int s) {
         const int bps = (nblk + s - 1) / s;
         return (nblk + bps - 1) / bps;
     };
-    if (force) {
-        int mt = 4, nt = 2, s = 1, nw = 4, ex = 0;
-        if (sscanf(force, "%d,%d,%d,%d,%d", &mt, &nt, &s, &nw, &ex) >= 3 && kernel_for(mt, nt, nw, 0) &&
-            s >= 1 && s <= 16 && (ex == 0 || (ex == 1 && mt == 4 && nt == 2 && nw == 8)))
-            return gd_gemm_plan{mt, nt, nz_of(s), nw, ex};
-    }
     const int cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
     // Measured plans for the config-4 stack's prefill shapes and the 17408-row
     // gate|up at T = 512 on a full MI355X (the fastest of 29-41 forced plans,
@@ -649,8 +643,8 @@ int gd_gemm_launch(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, int x
 // the rest with another, whose K may be split (gate/up partials in the
 // context workspace, then q2_0_glu_reduce) -- whichever the cost model (the
 // GEMM planner's measured tile times, the partials' round trip, ~2 us per
-// extra launch) finds cheaper.  GADEON_GLU_CFG="MT,NT,NW" forces one unsplit
-// launch of that tile.
+// extra launch) finds cheaper.  tile17: 1 forces the 17-fragment tile, 0
+// keeps the plan off it, -1 lets the cost model choose.
 int gd_gemm_glu(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, uint16_t *out,
                 int tile17) {
     const int K = (int)w->K, R = (int)w->R, ff = R / 2;
@@ -679,10 +673,6 @@ int gd_gemm_glu(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, uint16_t
     struct Part { const Shape *sh; int r0, r1, nz; };
     Part parts[2] = {{nullptr, 0, ff, 1}, {nullptr, ff, ff, 1}};
     double best = 1e30;
-    static const char *force = getenv("GADEON_GLU_CFG");
-    int fmt = 0, fnt = 0, fnw = 0, fex = 0;
-    const int nf = force ? sscanf(force, "%d,%d,%d,%d", &fmt, &fnt, &fnw, &fex) : 0;
-    const bool forced = nf >= 3;
     // The (4, 2, 8) tile with a seventeenth fragment: 272 columns a
     // workgroup in one launch (ff = 17408 at T = 512: one round of 256).
     // Its blocks cost the plain tile's by the fragment count.
@@ -691,10 +681,8 @@ int gd_gemm_glu(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, uint16_t
     const double cost_ex =
             round_cost(t428, tiles_t(t428) * ((ff + xcols - 1) / xcols), cus, nblk) * 17.0 / 16.0;
     for (const Shape &a : SHAPES) {
-        if (forced && !(a.mt == fmt && a.nt == fnt && a.nw == fnw)) continue;
         const double c1 = cost(a, ff, 1);
         if (c1 < best) { best = c1; parts[0] = {&a, 0, ff, 1}; parts[1] = {nullptr, ff, ff, 1}; }
-        if (forced) continue;
         // Whole rounds of a: rounds * CUs * occ units of tiles_t(a) token tiles each.
         const int64_t per_round = (int64_t)cus * a.occ;
         if (per_round % tiles_t(a)) continue;
@@ -713,8 +701,7 @@ int gd_gemm_glu(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, uint16_t
                 }
             }
     }
-    if (tile17 == 1 || (tile17 < 0 && (forced ? (fmt == 4 && fnt == 2 && fnw == 8 && fex == 1)
-                                              : cost_ex < best))) {
+    if (tile17 == 1 || (tile17 < 0 && cost_ex < best)) {
         const int nrt = gd_blocks(ff, xcols);
         const int64_t units = tiles_t(t428) * nrt;
         const int per = (int)((units + 7) / 8);
@@ -724,7 +711,7 @@ int gd_gemm_glu(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, uint16_t
         GD_LAUNCHED(ctx, "q2_0_gemm_glu");
         return GD_OK;
     }
-    GD_REQUIRE(ctx, parts[0].sh, "gd_gemm_glu: no tile for GADEON_GLU_CFG=%s", force ? force : "");
+    GD_REQUIRE(ctx, parts[0].sh, "gd_gemm_glu: no tile for ff=%d", ff);
     for (const Part &pt : parts) {
         if (!pt.sh || pt.r1 <= pt.r0) continue;
         const int ncol = pt.r1 - pt.r0;
@@ -783,11 +770,12 @@ int gemm_run(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, int x_dtype
     } else {
         p = gd_gemm_choose(ctx, T, w->K, w->R, x_dtype);
     }
-    // The 17-fragment tile writes f32 only: unsplit with f16 Y, the plain tile.
-    if (p.ex && p.split == 1 && y_dtype == GD_F16) p.ex = 0;
     const size_t n = (size_t)T * w->R;
     // Partials are summed 4 at a time: odd-sized outputs run unsplit.
     if (n % 4) p.split = 1;
+    // The 17-fragment tile writes f32 only: unsplit with f16 Y (also where
+    // the line above just forced it unsplit), the plain tile.
+    if (p.ex && p.split == 1 && y_dtype == GD_F16) p.ex = 0;
     // Workspace: f16 X (f32 X is rounded to f16 once, as the reference
     // stages it, Kernels.metal:428), then the split partials.
     const size_t nx = (size_t)T * w->K;

@@ -451,6 +451,7 @@ struct gd_stack {
     int64_t rope_shift = 0;
     bool random = true;          // weights drawn from the seed (else loaded)
     bool have_pick = false;      // dtok holds the last greedy pick
+    bool eager = false;          // generate: direct launches, not the graph
     std::atomic<bool> stop{false};
     std::vector<void *> allocs;
     hipGraphExec_t decode_exec = nullptr;
@@ -832,6 +833,19 @@ extern "C" int gd_stack_request_stop(gd_stack *st) {
     return GD_OK;
 }
 
+extern "C" int gd_stack_should_stop(gd_stack *st, int *raised) {
+    if (!st || !raised) return GD_EINVAL;
+    *raised = st->stop.load() ? 1 : 0;
+    return GD_OK;
+}
+
+extern "C" int gd_stack_set_eager(gd_stack *st, int eager) {
+    if (!st) return GD_EINVAL;
+    GD_REQUIRE(st->ctx, eager == 0 || eager == 1, "gd_stack_set_eager: eager=%d not 0 or 1", eager);
+    st->eager = eager != 0;
+    return GD_OK;
+}
+
 extern "C" int gd_stack_prefill(gd_stack *st, const int32_t *ids, int n, int32_t *next,
                                 float *logits) {
     if (!st) return GD_EINVAL;
@@ -843,8 +857,12 @@ extern "C" int gd_stack_prefill(gd_stack *st, const int32_t *ids, int n, int32_t
         GD_REQUIRE(ctx, ids[i] >= 0 && ids[i] < st->c.n_vocab, "gd_stack_prefill: id %d out of vocab",
                    ids[i]);
     int rc;
+    // A previous turn's stop must not end this one (MetalEngine.extend clears
+    // the signal first, MetalEngine.swift:183-186); a stop raised while this
+    // prefill runs is seen at the next chunk boundary and stays raised.
+    st->stop.store(false);
     for (int i = 0; i < n; i += st->c.max_batch) {
-        if (st->stop.exchange(false)) return gd_fail(ctx, GD_ESTOPPED, "prefill stopped");
+        if (st->stop.load()) return gd_fail(ctx, GD_ESTOPPED, "prefill stopped");
         const int N = std::min(st->c.max_batch, n - i);
         if ((rc = gd_upload(ctx, st->ids, ids + i, (size_t)N * 4)) ||
             (rc = gd_q2_0_dequant_rows(ctx, &st->embd, st->ids, N, st->x)) ||
@@ -881,10 +899,10 @@ extern "C" int gd_stack_generate(gd_stack *st, int n, int32_t *tokens) {
     GD_REQUIRE(ctx, st->have_pick,
                "gd_stack_generate: no previous pick to continue from (prefill or decode first)");
     int rc;
-    // GADEON_STACK_EAGER=1 launches every step's kernels directly instead of
+    // An eager stack launches every step's kernels directly instead of
     // replaying the captured graph (same kernels and results; for profilers
     // that do not follow graph launches).
-    static const bool eager = getenv("GADEON_STACK_EAGER") != nullptr;
+    const bool eager = st->eager;
     // One decode step reads the previous pick from st->dtok, so the whole step
     // (embed .. argmax, position bump) replays with no host involvement.
     if (!st->decode_exec && !eager) {
@@ -902,8 +920,11 @@ extern "C" int gd_stack_generate(gd_stack *st, int n, int32_t *tokens) {
         GD_HIP(ctx, hipGraphInstantiate(&st->decode_exec, graph, nullptr, nullptr, 0));
     }
     // Each step records its pick at picks[position], so nothing syncs per
-    // token; the n picks are read back once at the end.
-    for (int i = 0; i < n; i++) {
+    // token; the picks are read back once at the end.  A raised stop ends the
+    // loop before its next step (the decode loop's shouldStop gate).
+    int done = 0;
+    for (int i = 0; i < n; i++, done++) {
+        if (st->stop.load()) break;
         if (eager) {
             if ((rc = gd_q2_0_dequant_rows(ctx, &st->embd, st->dtok, 1, st->x)) ||
                 (rc = forward(st, 1, true)))
@@ -913,8 +934,9 @@ extern "C" int gd_stack_generate(gd_stack *st, int n, int32_t *tokens) {
             if (e != hipSuccess) return gd_hip_fail(ctx, e, "decode graph launch");
         }
     }
-    if ((rc = gd_download(ctx, tokens, st->picks + st->pos, (size_t)n * 4))) return rc;
-    st->pos += n;
+    if (done && (rc = gd_download(ctx, tokens, st->picks + st->pos, (size_t)done * 4))) return rc;
+    st->pos += done;
+    if (done < n) return gd_fail(ctx, GD_ESTOPPED, "generate stopped after %d of %d steps", done, n);
     return GD_OK;
 }
 

@@ -351,8 +351,10 @@ int gd_gdn_scan(gd_ctx *ctx, const float *q, const float *k, const float *v,
                 int nV, int nK, int dS, float qScale);
 
 /* N tokens out of the conv output rows convOutN[N][convDim] = [q|k|v]:
- * MetalEnc.gdnScanBatch (MetalEnc.swift:741-778), gdn_scan_batch2
- * (Kernels.metal:1570-1625).  Runs the chunked kernel below. */
+ * MetalEnc.gdnScanBatch (MetalEnc.swift:741-778), which serves any dS with
+ * gdn_scan_batch2 (dS % 32 == 0, dS <= 256) or gdn_scan_batch
+ * (Kernels.metal:1525-1625).  dS = 128 runs the chunked kernel below; any
+ * other dS up to 1024 a token-serial scan in the reference's order. */
 int gd_gdn_scan_batch(gd_ctx *ctx, const float *convOutN, int keyDim,
                       int valueDim, int convDim, const float *gN,
                       const float *betaN, float *S, float *oN, int nV, int nK,
@@ -476,11 +478,26 @@ int gd_stack_decode(gd_stack *st, int32_t token, int32_t *next,
 /* n greedy decode steps continuing from the token the last prefill/decode
  * picked, with no host round trip between steps (the step is captured once
  * as a HIP graph; the picked id stays on the device).  tokens[n] receives the
- * n ids generated.  Equivalent to n chained gd_stack_decode calls. */
+ * n ids generated.  Equivalent to n chained gd_stack_decode calls.  A raised
+ * stop ends it before its next step with GD_ESTOPPED; the steps already made
+ * stay made (tokens[0 .. k) and the position, gd_stack_position, advance by
+ * those k). */
 int gd_stack_generate(gd_stack *st, int n, int32_t *tokens);
-/* Cooperative stop, safe from another thread: the next chunk boundary of a
- * running prefill returns GD_ESTOPPED (MetalEngine.swift:15-25, 79-81). */
+/* Cooperative stop (MetalEngine.requestStop / shouldStop, MetalEngine.swift:
+ * 15-25, 79-81), safe from another thread.  gd_stack_prefill clears the
+ * signal when it starts (a previous turn's stop does not end the next,
+ * MetalEngine.swift:183-186) and returns GD_ESTOPPED at the next chunk
+ * boundary once it is raised; gd_stack_generate checks it before each step.
+ * The signal stays raised until the next prefill or gd_stack_reset;
+ * gd_stack_should_stop reads it (*raised = 1 or 0). */
 int gd_stack_request_stop(gd_stack *st);
+int gd_stack_should_stop(gd_stack *st, int *raised);
+/* eager = 1: gd_stack_generate launches every step's kernels directly
+ * instead of replaying the captured decode graph (the same kernels in the
+ * same order, the same results; for kernel-trace profilers that do not
+ * follow graph launches).  0 (the default) replays the graph.  No
+ * counterpart in the reference (MetalEngine reuses its command buffers). */
+int gd_stack_set_eager(gd_stack *st, int eager);
 
 /* Weight and state introspection for parity tests: tensor `name` of layer
  * `layer` (-1 for global tensors).  A Q2_0 tensor fills *w with the matrix

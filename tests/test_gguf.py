@@ -206,3 +206,29 @@ def test_corrupt_files_are_errors(tmp_path, lib):
     # Nonexistent path.
     with pytest.raises(ga.GDError, match="cannot open"):
         ga.GGUF(tmp_path / "absent.gguf")
+
+
+def test_views_keep_the_mapping(tmp_path, lib):
+    """A tensor view outlives close(): the mapping stays until the last view
+    (and every array sliced from it) is gone; reads through the object
+    itself are refused once it is closed."""
+    import gc
+    rng = np.random.default_rng(5)
+    ts = tensors(rng)
+    path = W.write(tmp_path / "v.gguf", list(KVS), ts)
+    g = ga.GGUF(path)
+    _, _, q = g.tensor("q")
+    part = q[34:68]
+    del q
+    g.close()
+    gc.collect()
+    assert g.mapped
+    assert part.tobytes() == ts[1][3][34:68]
+    with pytest.raises(ga.GDError, match="closed"):
+        g.tensor("f")
+    del part
+    gc.collect()
+    assert not g.mapped
+    with ga.GGUF(path) as g2:                  # no view taken: unmapped at exit
+        g2.info()
+    assert not g2.mapped

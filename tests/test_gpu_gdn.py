@@ -193,9 +193,13 @@ def test_prefill_chunked_vs_sequential(ctx, T, nV, nK, C, io, s0):
     assert rel_diff(ctx.get(dS_, S.size, np.float32), S_ref) < 2e-3
 
 
-def test_scan_batch_conv_layout(ctx):
-    """MetalEnc.gdnScanBatch's packed convOut[N][q|k|v] layout (MetalEnc.swift:741-778)."""
-    N, nK, nV, dS = 70, 4, 8, 128
+@pytest.mark.parametrize("dS", [128, 64, 96, 256, 48])
+def test_scan_batch_conv_layout(ctx, dS):
+    """MetalEnc.gdnScanBatch's packed convOut[N][q|k|v] layout (MetalEnc.swift:741-778),
+    for the state sizes the reference serves: 128 on the chunked prefill, the
+    others (dS % 32 == 0 up to 256 in gdn_scan_batch2, anything else in
+    gdn_scan_batch) on the token-serial scan."""
+    N, nK, nV = 70, 4, 8
     keyDim, valueDim = nK * dS, nV * dS
     convDim = 2 * keyDim + valueDim
     conv = O.lcg_normal(N * convDim, 61).reshape(N, convDim)

@@ -279,9 +279,6 @@ def test_stack_rejects_bad_input(ctx):
         assert b"vocab" in lib.gd_last_error(ctx.h)
         ok = np.arange(cfg["max_ctx"] + 1, dtype=np.int32)
         assert lib.gd_stack_prefill(st, ok.ctypes.data, ok.size, None, None) == ga.GD_EINVAL
-        ctx.check(lib.gd_stack_request_stop(st))
-        ids = np.arange(40, dtype=np.int32)
-        assert lib.gd_stack_prefill(st, ids.ctypes.data, ids.size, None, None) == ga.GD_ESTOPPED
     finally:
         lib.gd_stack_destroy(st)
     sc = ga.StackConfig(**dict(CFG, head_dim=64))
@@ -292,3 +289,55 @@ def test_stack_rejects_bad_input(ctx):
         sc = ga.StackConfig(**dict(CFG, **bad))
         assert lib.gd_stack_create(ctx.h, C.byref(sc), 1, C.byref(h)) == ga.GD_EINVAL
         assert b"dense" in lib.gd_last_error(ctx.h)
+
+
+def test_stack_stop_signal(ctx):
+    """MetalEngine's cooperative stop (MetalEngine.swift:15-25, 79-81,
+    183-186): a raised stop ends generate before its next step and stays
+    raised (shouldStop); the next prefill clears it and runs; a stop raised
+    from another thread during a multi-chunk prefill ends it at a chunk
+    boundary (or the prefill finishes first)."""
+    import threading
+    cfg, st = make_stack(ctx, n_layer=4, max_batch=16, max_ctx=1024)
+    lib = ctx.lib
+    raised = C.c_int()
+    try:
+        ids = np.arange(40, dtype=np.int32)
+        nxt = C.c_int32()
+        ctx.check(lib.gd_stack_prefill(st, ids.ctypes.data, ids.size, C.byref(nxt), None))
+        ctx.check(lib.gd_stack_should_stop(st, C.byref(raised)))
+        assert raised.value == 0
+        toks = np.empty(8, np.int32)
+        ctx.check(lib.gd_stack_request_stop(st))
+        assert lib.gd_stack_generate(st, 8, toks.ctypes.data) == ga.GD_ESTOPPED
+        pos = C.c_int64()
+        ctx.check(lib.gd_stack_position(st, C.byref(pos)))
+        assert pos.value == 40                          # no step was made
+        ctx.check(lib.gd_stack_should_stop(st, C.byref(raised)))
+        assert raised.value == 1                        # stays raised for the decode loop
+        # The next prefill clears it and runs to the end.
+        ctx.check(lib.gd_stack_prefill(st, ids.ctypes.data, ids.size, C.byref(nxt), None))
+        ctx.check(lib.gd_stack_should_stop(st, C.byref(raised)))
+        assert raised.value == 0
+        ctx.check(lib.gd_stack_position(st, C.byref(pos)))
+        assert pos.value == 80
+        ctx.check(lib.gd_stack_generate(st, 8, toks.ctypes.data))
+        # A stop from another thread while 60 chunks of 16 are prefilled.
+        ctx.check(lib.gd_stack_reset(st))
+        long_ids = (np.arange(960) % cfg["n_vocab"]).astype(np.int32)
+        out = {}
+        th = threading.Thread(target=lambda: out.setdefault(
+            "rc", lib.gd_stack_prefill(st, long_ids.ctypes.data, long_ids.size, None, None)))
+        th.start()
+        while th.is_alive():
+            lib.gd_stack_request_stop(st)
+            th.join(0.001)
+        ctx.check(lib.gd_stack_position(st, C.byref(pos)))
+        assert out["rc"] in (ga.GD_OK, ga.GD_ESTOPPED)
+        if out["rc"] == ga.GD_ESTOPPED:
+            assert pos.value % 16 == 0 and pos.value < 960
+        else:
+            assert pos.value == 960
+        ctx.sync()
+    finally:
+        lib.gd_stack_destroy(st)
