@@ -112,6 +112,7 @@ _PROTOS = {
     "gd_stack_tensor": (_i, [_vp, _i, C.c_char_p, _Q2WP, C.POINTER(_i64), C.POINTER(_fp),
                          C.POINTER(_i64)]),
     "gd_stack_position": (_i, [_vp, C.POINTER(_i64)]),
+    "gd_stack_kv_pages": (_i, [_vp, C.POINTER(_i64), C.POINTER(_i64), C.POINTER(_i64)]),
     "gd_stack_generate": (_i, [_vp, _i, _vp]),
     "gd_q2_0_repack_rows": (_i, [_vp, _vp, _u64, _i64, _i64, _Q2WP]),
     "gd_stack_bookmark": (_i, [_vp, C.POINTER(_vp)]),

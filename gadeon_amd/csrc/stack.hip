@@ -26,6 +26,7 @@
 #include <atomic>
 #include <cmath>
 #include <cstring>
+#include <memory>
 #include <string>
 #include <vector>
 
@@ -405,11 +406,6 @@ __global__ __launch_bounds__(1024) void k_add_rmsnorm(float *x, const float *y, 
     }
 }
 
-__global__ void k_iota(int32_t *p, int n) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) p[i] = i;
-}
-
 }  // namespace
 
 // --------------------------------------------------------------- host side
@@ -423,7 +419,90 @@ struct StackLayer {
     float *conv_state = nullptr, *rec_state = nullptr;
     // attention
     float *q_norm = nullptr, *k_norm = nullptr;
-    uint16_t *kc = nullptr, *vc = nullptr;
+    int att = -1;                // attention ordinal: this layer's K and V pools in KvPool
+};
+
+// Paged KV memory of a stack (MetalKVPool, MetalKVPool.swift:1-120, on one
+// device allocation per pool): per attention layer one K and one V pool of
+// `cap` physical pages of kv_block positions x kv_dim halves.  One logical
+// -> physical page table serves every attention layer, since they append in
+// lockstep.  A page is held by the live table and by bookmarks (`refs`); a
+// completed page is never written again, so a bookmark shares it and copies
+// only a partially filled tail page, and a restore gives the live table its
+// own copy of that tail (MetalKVPool.snapshot / restore, :95-120).  When no
+// page is free the pools double (a device copy of the pages so far), so
+// memory follows the context in use and what bookmarks hold.  Bookmarks own a
+// reference to the pool: it outlives the stack while any of them lives.
+struct KvPool {
+    gd_ctx *ctx = nullptr;
+    size_t page_elems = 0;             // halves per page
+    int cap = 0;                       // physical pages per pool
+    std::vector<uint16_t *> k, v;      // [attention layers] pools of cap pages
+    std::vector<int> refs;             // [cap] holders of each page
+    std::vector<int32_t> free;         // pages with no holder (popped from the back)
+    uint64_t generation = 0;           // bumped whenever the pools move
+
+    ~KvPool() {
+        for (uint16_t *p : k) if (p) gd_free(ctx, p);
+        for (uint16_t *p : v) if (p) gd_free(ctx, p);
+    }
+    // Capacity at least `want` pages (doubling), the held pages copied over.
+    int grow(int want) {
+        const int ncap = std::max(want, 2 * cap);
+        std::vector<uint16_t *> nk(k.size(), nullptr), nv(v.size(), nullptr);
+        const size_t bytes = (size_t)ncap * page_elems * 2, old = (size_t)cap * page_elems * 2;
+        int rc = GD_OK;
+        for (size_t a = 0; rc == GD_OK && a < k.size(); a++) {
+            if ((rc = gd_alloc(ctx, bytes, (void **)&nk[a])) == GD_OK)
+                rc = gd_alloc(ctx, bytes, (void **)&nv[a]);
+            if (rc == GD_OK && old && (rc = gd_copy(ctx, nk[a], k[a], old)) == GD_OK)
+                rc = gd_copy(ctx, nv[a], v[a], old);
+        }
+        if (rc == GD_OK) rc = gd_sync(ctx);
+        if (rc) {
+            for (uint16_t *p : nk) if (p) gd_free(ctx, p);
+            for (uint16_t *p : nv) if (p) gd_free(ctx, p);
+            return rc;
+        }
+        for (size_t a = 0; a < k.size(); a++) {
+            if (k[a]) gd_free(ctx, k[a]);
+            if (v[a]) gd_free(ctx, v[a]);
+            k[a] = nk[a];
+            v[a] = nv[a];
+        }
+        refs.resize(ncap, 0);
+        for (int p = ncap - 1; p >= cap; p--) free.push_back(p);   // low pages first
+        cap = ncap;
+        generation++;
+        return GD_OK;
+    }
+    // A free page, held once (the pools grow when none is free).
+    int take(int32_t *page) {
+        if (free.empty()) {
+            const int rc = grow(cap + 1);
+            if (rc) return rc;
+        }
+        *page = free.back();
+        free.pop_back();
+        refs[*page] = 1;
+        return GD_OK;
+    }
+    void hold(int32_t p) { refs[p]++; }
+    void drop(int32_t p) {
+        if (--refs[p] == 0) free.push_back(p);
+    }
+    int held() const { return cap - (int)free.size(); }
+    // Page dst of this pool <- page src of `from` (every attention layer's K and V).
+    int copy_page(int32_t dst, const KvPool &from, int32_t src) {
+        const size_t b = page_elems * 2;
+        int rc = GD_OK;
+        for (size_t a = 0; rc == GD_OK && a < k.size(); a++) {
+            if ((rc = gd_copy(ctx, k[a] + (size_t)dst * page_elems, from.k[a] + (size_t)src * page_elems,
+                              b)) == GD_OK)
+                rc = gd_copy(ctx, v[a] + (size_t)dst * page_elems, from.v[a] + (size_t)src * page_elems, b);
+        }
+        return rc;
+    }
 };
 
 struct gd_stack {
@@ -434,7 +513,9 @@ struct gd_stack {
     gd_q2w embd{};
     gd_q2w head{};               // lm_head: a copy of embd when tied (Model.swift:145)
     float *out_norm = nullptr;
-    int32_t *page_table = nullptr;
+    int32_t *page_table = nullptr;       // device: physical page of each logical page
+    std::shared_ptr<KvPool> kv;
+    std::vector<int32_t> live;           // the table's mapped entries (host copy)
     // scratch
     float *x = nullptr, *proj = nullptr, *conv_out = nullptr, *o32 = nullptr, *contrib = nullptr;
     float *beta = nullptr, *g = nullptr, *q32 = nullptr, *gate32 = nullptr, *logits = nullptr;
@@ -592,17 +673,18 @@ int forward(gd_stack *st, int N, bool decode) {
             // Per-head q stride of the projection rows: the hybrid's fused
             // [q | gate] pairs, or the dense model's plain q (ungated).
             const int qs = c.dense ? hd : 2 * hd;
+            uint16_t *kc = st->kv->k[ly.att], *vc = st->kv->v[ly.att];
             if (decode) {
                 // One token: q/k preparation and the cache append happen
                 // inside the attention launch.
-                R_(gd_attn_decode_launch(ctx, hd, st->proj, qs, ly.q_norm, ly.k_norm, ly.kc, ly.vc,
+                R_(gd_attn_decode_launch(ctx, hd, st->proj, qs, ly.q_norm, ly.k_norm, kc, vc,
                                          st->page_table, st->dpos, st->attn_part, st->a16, H, HKV,
                                          c.kv_block, scale, c.n_rot, c.rope_base, eps));
             } else {
                 R_(gd_attn_prep_launch(ctx, hd, st->proj, (int64_t)RP, qs, ly.q_norm, ly.k_norm, st->q32,
-                                       st->gate32, ly.kc, ly.vc, st->page_table, st->dpos, N, H,
+                                       st->gate32, kc, vc, st->page_table, st->dpos, N, H,
                                        HKV, c.n_rot, c.rope_base, c.kv_block, eps));
-                R_(gd_attn_prefill_launch(ctx, hd, st->q32, st->gate32, ly.kc, ly.vc,
+                R_(gd_attn_prefill_launch(ctx, hd, st->q32, st->gate32, kc, vc,
                                           st->page_table, st->dpos, 0, st->a16, GD_F16, H, HKV, N,
                                           c.kv_block, scale, c.dense ? 0 : 1));
             }
@@ -672,15 +754,58 @@ int finish(gd_stack *st, int32_t *next, float *logits) {
     return GD_OK;
 }
 
+// The captured decode step holds the KV pools' addresses: dropped when the
+// pools move, captured again by the next gd_stack_generate.
+void drop_graph(gd_stack *st) {
+    if (st->decode_exec) (void)hipGraphExecDestroy(st->decode_exec);
+    if (st->decode_graph) (void)hipGraphDestroy(st->decode_graph);
+    st->decode_exec = nullptr;
+    st->decode_graph = nullptr;
+}
+
+// A page of the stack's own pool for the stack to write (its graph dropped
+// if the pools grew).
+int take_page(gd_stack *st, int32_t *page) {
+    const uint64_t gen = st->kv->generation;
+    const int rc = st->kv->take(page);
+    if (st->kv->generation != gen) drop_graph(st);
+    return rc;
+}
+
+// Every logical page of positions [0, upto) mapped to a page of the live
+// table: fresh pages for the ones past its end, their table entries uploaded.
+int map_pages(gd_stack *st, int64_t upto) {
+    const int B = st->c.kv_block;
+    const size_t need = (size_t)((upto + B - 1) / B), first = st->live.size();
+    if (need <= first) return GD_OK;
+    GD_REQUIRE(st->ctx, need <= (size_t)st->max_pages, "stack: %lld positions pass max_ctx %d",
+               (long long)upto, st->c.max_ctx);
+    while (st->live.size() < need) {
+        int32_t p;
+        const int rc = take_page(st, &p);
+        if (rc) return rc;
+        st->live.push_back(p);
+    }
+    return gd_upload(st->ctx, st->page_table + first, st->live.data() + first,
+                     (need - first) * sizeof(int32_t));
+}
+
+// The live table emptied (its pages back to the pool unless a bookmark holds them).
+void release_live(gd_stack *st) {
+    for (int32_t p : st->live) st->kv->drop(p);
+    st->live.clear();
+}
+
 }  // namespace
 
 extern "C" void gd_stack_destroy(gd_stack *st) {
     if (!st) return;
-    if (st->decode_exec) (void)hipGraphExecDestroy(st->decode_exec);
-    if (st->decode_graph) (void)hipGraphDestroy(st->decode_graph);
+    drop_graph(st);
+    if (st->kv) release_live(st);
     for (void *p : st->allocs) gd_free(st->ctx, p);
     delete st;
 }
+
 
 namespace {
 
@@ -737,6 +862,7 @@ int create(gd_ctx *ctx, const gd_stack_config *cfg, uint64_t seed, bool random, 
     uint64_t sd = seed * 1000003ULL;
     auto next_seed = [&]() { sd += 2; return sd; };   // streams use seed and seed+1
     st->L.resize(c.n_layer);
+    int natt = 0;
     for (int il = 0; il < c.n_layer; il++) {
         StackLayer &ly = st->L[il];
         ly.rec = (il + 1) % c.attn_interval != 0;     // Model.swift:37
@@ -756,9 +882,7 @@ int create(gd_ctx *ctx, const gd_stack_config *cfg, uint64_t seed, bool random, 
             C_(q2w_make(st, (int64_t)c.n_head * hd, E, next_seed(), &ly.out_proj));
             C_(f32_make(st, hd, next_seed(), 0.8f, 1.2f, &ly.q_norm));
             C_(f32_make(st, hd, next_seed(), 0.8f, 1.2f, &ly.k_norm));
-            const size_t kv = (size_t)st->max_pages * c.kv_block * c.n_head_kv * hd;
-            C_(salloc_t(st, kv, &ly.kc));
-            C_(salloc_t(st, kv, &ly.vc));
+            ly.att = natt++;
         }
         C_(q2w_make(st, E, 2 * (int64_t)FF, next_seed(), &ly.gate_up));
         C_(q2w_make(st, FF, E, next_seed(), &ly.down));
@@ -770,8 +894,14 @@ int create(gd_ctx *ctx, const gd_stack_config *cfg, uint64_t seed, bool random, 
     else
         st->head = st->embd;
     C_(salloc_t(st, (size_t)st->max_pages, &st->page_table));
-    hipLaunchKernelGGL(k_iota, dim3(gd_blocks(st->max_pages, 256)), dim3(256), 0, ctx->stream,
-                       st->page_table, st->max_pages);
+    // KV pages start at twice what one prefill chunk fills (capped at
+    // max_ctx) and grow on demand.
+    st->kv = std::make_shared<KvPool>();
+    st->kv->ctx = ctx;
+    st->kv->page_elems = (size_t)c.kv_block * c.n_head_kv * hd;
+    st->kv->k.assign(natt, nullptr);
+    st->kv->v.assign(natt, nullptr);
+    C_(st->kv->grow(std::min(st->max_pages, 2 * ((B + c.kv_block - 1) / c.kv_block + 1))));
     const int maxproj = std::max(std::max(st->rp_rec, st->rp_att), 2 * FF);
     C_(salloc_t(st, (size_t)B * E, &st->x));
     C_(salloc_t(st, (size_t)B * maxproj, &st->proj));
@@ -820,6 +950,7 @@ extern "C" int gd_stack_reset(gd_stack *st) {
     }
     if ((rc = gd_fill_u32(ctx, st->dpos, 0, 2)) || (rc = gd_fill_u32(ctx, st->dtok, 0, 1)))
         return rc;
+    release_live(st);
     st->pos = 0;
     st->rope_shift = 0;
     st->have_pick = false;
@@ -864,7 +995,7 @@ extern "C" int gd_stack_prefill(gd_stack *st, const int32_t *ids, int n, int32_t
     for (int i = 0; i < n; i += st->c.max_batch) {
         if (st->stop.load()) return gd_fail(ctx, GD_ESTOPPED, "prefill stopped");
         const int N = std::min(st->c.max_batch, n - i);
-        if ((rc = gd_upload(ctx, st->ids, ids + i, (size_t)N * 4)) ||
+        if ((rc = map_pages(st, st->pos + N)) || (rc = gd_upload(ctx, st->ids, ids + i, (size_t)N * 4)) ||
             (rc = gd_q2_0_dequant_rows(ctx, &st->embd, st->ids, N, st->x)) ||
             (rc = forward(st, N, false)))
             return rc;
@@ -881,7 +1012,7 @@ extern "C" int gd_stack_decode(gd_stack *st, int32_t token, int32_t *next, float
                token);
     GD_REQUIRE(ctx, st->pos + 1 <= st->c.max_ctx, "gd_stack_decode: context full");
     int rc;
-    if ((rc = gd_upload(ctx, st->dtok, &token, 4))) return rc;
+    if ((rc = map_pages(st, st->pos + 1)) || (rc = gd_upload(ctx, st->dtok, &token, 4))) return rc;
     if ((rc = gd_q2_0_dequant_rows(ctx, &st->embd, st->dtok, 1, st->x)) ||
         (rc = forward(st, 1, true)))
         return rc;
@@ -903,6 +1034,7 @@ extern "C" int gd_stack_generate(gd_stack *st, int n, int32_t *tokens) {
     // replaying the captured graph (same kernels and results; for profilers
     // that do not follow graph launches).
     const bool eager = st->eager;
+    if ((rc = map_pages(st, st->pos + n))) return rc;
     // One decode step reads the previous pick from st->dtok, so the whole step
     // (embed .. argmax, position bump) replays with no host involvement.
     if (!st->decode_exec && !eager) {
@@ -937,6 +1069,14 @@ extern "C" int gd_stack_generate(gd_stack *st, int n, int32_t *tokens) {
     if (done && (rc = gd_download(ctx, tokens, st->picks + st->pos, (size_t)done * 4))) return rc;
     st->pos += done;
     if (done < n) return gd_fail(ctx, GD_ESTOPPED, "generate stopped after %d of %d steps", done, n);
+    return GD_OK;
+}
+
+extern "C" int gd_stack_kv_pages(gd_stack *st, int64_t *live, int64_t *held, int64_t *capacity) {
+    if (!st) return GD_EINVAL;
+    if (live) *live = (int64_t)st->live.size();
+    if (held) *held = st->kv->held();
+    if (capacity) *capacity = st->kv->cap;
     return GD_OK;
 }
 
@@ -1127,23 +1267,31 @@ extern "C" int gd_stack_create_from_gguf(gd_ctx *ctx, const gd_gguf *g, int kv_b
 
 // ------------------------------------------------------------ bookmarks
 
-// A snapshot of the generation state in device memory: position, the last
-// pick, every GDN layer's conv ring and recurrent state, and every attention
-// layer's cached K/V over positions [0, pos).  MetalEngine.Bookmark
-// (MetalEngine.swift:455-483) shares append-only KV pages; this pool's slots
-// are reused after a reset, so the used span is copied instead (an HBM copy
-// of 2 x pos x kv_dim halves per attention layer).
+// A snapshot of the generation state (MetalEngine.Bookmark,
+// MetalEngine.swift:455-483): position, rope shift, the last pick and every
+// GDN layer's conv ring and recurrent state, copied whole into one device
+// buffer (the recurrence cannot be paged), and the attention layers' K/V as
+// pages of the stack's pool: completed pages shared with the live table, a
+// partially filled tail page copied (MetalKVPool.snapshot, :102-110), so a
+// bookmark costs O(tail) of KV, not O(context).
 struct gd_bookmark {
     gd_ctx *ctx = nullptr;
     gd_stack_config c{};
     int64_t pos = 0;
     int64_t rope_shift = 0;      // rope position = position + shift
     bool have_pick = false;
-    void *buf = nullptr;         // [pick | conv, rec per GDN layer | k, v per attention layer]
+    void *buf = nullptr;         // [pick | conv, rec per GDN layer]
+    std::shared_ptr<KvPool> kv;  // the pool its pages live in
+    std::vector<int32_t> pages;  // positions [0, pos), kv_block per page
 };
 
 namespace {
 
+// A bookmark's state as one image: the pick, then per layer either its conv
+// ring and recurrent state (f32) or its K and V over [0, pos) (f16), each
+// array 256-byte aligned.  With kv = false (the device buffer of a
+// bookmark) the attention layers take no room; the host image (kv = true)
+// is what the byte formats are written from and read into.
 struct BmLayout {
     size_t conv = 0, rec = 0, kv = 0, total = 0;   // element counts per layer; bytes
     std::vector<size_t> off;                       // per layer: byte offset of its first array
@@ -1151,7 +1299,7 @@ struct BmLayout {
 
 size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
-BmLayout bm_layout(const gd_stack *st, int64_t pos) {
+BmLayout bm_layout(const gd_stack *st, int64_t pos, bool kv = true) {
     BmLayout l;
     l.conv = (size_t)(st->c.d_conv - 1) * st->convDim;
     l.rec = (size_t)st->c.n_v_head * HD * HD;
@@ -1159,10 +1307,96 @@ BmLayout bm_layout(const gd_stack *st, int64_t pos) {
     size_t o = 256;                                  // the pick
     for (const StackLayer &ly : st->L) {
         l.off.push_back(o);
-        o += ly.rec ? align256(l.conv * 4) + align256(l.rec * 4) : 2 * align256(l.kv * 2);
+        o += ly.rec ? align256(l.conv * 4) + align256(l.rec * 4) : kv ? 2 * align256(l.kv * 2) : 0;
     }
     l.total = o;
     return l;
+}
+
+// dst <- the pages of positions [0, pos) given as `src` in pool `from`,
+// held for a new owner in the stack's pool: a complete page of the same
+// pool is shared; a partial tail page, or any page of another pool, is
+// copied into a fresh page (on the context stream).
+int adopt_pages(gd_stack *st, const std::shared_ptr<KvPool> &from, const std::vector<int32_t> &src,
+                int64_t pos, std::vector<int32_t> &dst) {
+    const int64_t B = st->c.kv_block;
+    dst.clear();
+    int rc = GD_OK;
+    for (size_t i = 0; rc == GD_OK && i < src.size(); i++) {
+        const bool tail = (int64_t)(i + 1) * B > pos;
+        if (from == st->kv && !tail) {
+            st->kv->hold(src[i]);
+            dst.push_back(src[i]);
+            continue;
+        }
+        int32_t q;
+        if ((rc = take_page(st, &q)) == GD_OK) {
+            dst.push_back(q);
+            rc = st->kv->copy_page(q, *from, src[i]);
+        }
+    }
+    if (rc) {
+        for (int32_t p : dst) st->kv->drop(p);
+        dst.clear();
+    }
+    return rc;
+}
+
+// K and V of positions [0, pos) of every attention layer, gathered from the
+// pages into one device array [attention layer][K, V][pos][kv_dim] (f16),
+// or scattered back from it.
+int kv_gather(gd_ctx *ctx, const KvPool &pool, const std::vector<int32_t> &pages, int64_t pos,
+              int B, uint16_t *dev, bool scatter) {
+    const size_t pe = pool.page_elems, kvd = pe / B, span = (size_t)pos * kvd;
+    int rc = GD_OK;
+    for (size_t a = 0; a < pool.k.size(); a++)
+        for (int kv = 0; kv < 2; kv++) {
+            uint16_t *base = (kv ? pool.v : pool.k)[a];
+            uint16_t *arr = dev + (2 * a + kv) * span;
+            for (size_t i = 0; rc == GD_OK && i < pages.size(); i++) {
+                const size_t n = std::min((size_t)B, (size_t)pos - i * B) * kvd;
+                uint16_t *pg = base + (size_t)pages[i] * pe;
+                rc = scatter ? gd_copy(ctx, pg, arr + i * B * kvd, n * 2)
+                             : gd_copy(ctx, arr + i * B * kvd, pg, n * 2);
+            }
+        }
+    return rc;
+}
+
+// The host image (bm_layout with K/V) of bookmark b.
+int bookmark_to_host(gd_stack *st, const gd_bookmark *b, std::vector<uint8_t> &host) {
+    gd_ctx *ctx = st->ctx;
+    const BmLayout lh = bm_layout(st, b->pos), ld = bm_layout(st, b->pos, false);
+    host.assign(lh.total, 0);
+    std::vector<uint8_t> dev(ld.total);
+    int rc = gd_download(ctx, dev.data(), b->buf, ld.total);
+    if (rc) return rc;
+    memcpy(host.data(), dev.data(), 4);
+    int natt = 0;
+    for (int il = 0; il < st->c.n_layer; il++) {
+        if (st->L[il].rec)
+            memcpy(host.data() + lh.off[il], dev.data() + ld.off[il],
+                   align256(lh.conv * 4) + lh.rec * 4);
+        else
+            natt++;
+    }
+    if (!natt || !b->pos) return GD_OK;
+    const size_t span = lh.kv;
+    void *tmp = nullptr;
+    if ((rc = gd_alloc(ctx, (size_t)natt * 2 * span * 2, &tmp))) return rc;
+    rc = kv_gather(ctx, *b->kv, b->pages, b->pos, st->c.kv_block, (uint16_t *)tmp, false);
+    std::vector<uint16_t> kvh(rc == GD_OK ? (size_t)natt * 2 * span : 0);
+    if (rc == GD_OK) rc = gd_download(ctx, kvh.data(), tmp, kvh.size() * 2);
+    gd_free(ctx, tmp);
+    if (rc) return rc;
+    for (int il = 0; il < st->c.n_layer; il++) {
+        const StackLayer &ly = st->L[il];
+        if (ly.rec) continue;
+        for (int kv = 0; kv < 2; kv++)
+            memcpy(host.data() + lh.off[il] + kv * align256(span * 2),
+                   kvh.data() + (2 * (size_t)ly.att + kv) * span, span * 2);
+    }
+    return GD_OK;
 }
 
 bool same_geometry(const gd_stack_config &a, const gd_stack_config &b) {
@@ -1216,26 +1450,27 @@ extern "C" int gd_stack_bookmark(gd_stack *st, gd_bookmark **out) {
     gd_ctx *ctx = st->ctx;
     GD_REQUIRE(ctx, out, "gd_stack_bookmark: null out pointer");
     *out = nullptr;
-    const BmLayout l = bm_layout(st, st->pos);
+    const BmLayout l = bm_layout(st, st->pos, false);
     gd_bookmark *b = new gd_bookmark();
     b->ctx = ctx;
     b->c = st->c;
     b->pos = st->pos;
     b->rope_shift = st->rope_shift;
     b->have_pick = st->have_pick;
+    b->kv = st->kv;
     int rc = gd_alloc(ctx, l.total, &b->buf);
     uint8_t *base = (uint8_t *)b->buf;
     if (rc == GD_OK) rc = d2d(ctx, base, st->dtok, 4);
     for (int il = 0; rc == GD_OK && il < st->c.n_layer; il++) {
         const StackLayer &ly = st->L[il];
         uint8_t *d = base + l.off[il];
-        if (ly.rec) {
-            if ((rc = d2d(ctx, d, ly.conv_state, l.conv * 4)) == GD_OK)
-                rc = d2d(ctx, d + align256(l.conv * 4), ly.rec_state, l.rec * 4);
-        } else if ((rc = d2d(ctx, d, ly.kc, l.kv * 2)) == GD_OK) {
-            rc = d2d(ctx, d + align256(l.kv * 2), ly.vc, l.kv * 2);
-        }
+        if (ly.rec && (rc = d2d(ctx, d, ly.conv_state, l.conv * 4)) == GD_OK)
+            rc = d2d(ctx, d + align256(l.conv * 4), ly.rec_state, l.rec * 4);
     }
+    const size_t np = (size_t)((st->pos + st->c.kv_block - 1) / st->c.kv_block);
+    if (rc == GD_OK)
+        rc = adopt_pages(st, st->kv, std::vector<int32_t>(st->live.begin(), st->live.begin() + np),
+                         st->pos, b->pages);
     if (rc == GD_OK) rc = gd_sync(ctx);
     if (rc) {
         gd_bookmark_free(b);
@@ -1247,6 +1482,8 @@ extern "C" int gd_stack_bookmark(gd_stack *st, gd_bookmark **out) {
 
 extern "C" void gd_bookmark_free(gd_bookmark *b) {
     if (!b) return;
+    if (b->kv)
+        for (int32_t p : b->pages) b->kv->drop(p);
     if (b->buf) gd_free(b->ctx, b->buf);
     delete b;
 }
@@ -1258,18 +1495,25 @@ extern "C" int gd_stack_restore(gd_stack *st, const gd_bookmark *b) {
     GD_REQUIRE(ctx, b->ctx == ctx, "gd_stack_restore: bookmark of another context");
     GD_REQUIRE(ctx, same_geometry(b->c, st->c) && b->pos <= st->c.max_ctx,
                "gd_stack_restore: bookmark of another geometry (or beyond max_ctx)");
-    const BmLayout l = bm_layout(st, b->pos);
+    // The live table takes the bookmark's pages (its own copy of a partial
+    // tail, so that a bookmark restored more than once is never written:
+    // MetalKVPool.restore, :111-120), then lets its old pages go.
+    std::vector<int32_t> pages;
+    int rc = adopt_pages(st, b->kv, b->pages, b->pos, pages);
+    if (rc) return rc;
+    release_live(st);
+    st->live = std::move(pages);
+    if (!st->live.empty() &&
+        (rc = gd_upload(ctx, st->page_table, st->live.data(), st->live.size() * sizeof(int32_t))))
+        return rc;
+    const BmLayout l = bm_layout(st, b->pos, false);
     const uint8_t *base = (const uint8_t *)b->buf;
-    int rc = d2d(ctx, st->dtok, base, 4);
+    rc = d2d(ctx, st->dtok, base, 4);
     for (int il = 0; rc == GD_OK && il < st->c.n_layer; il++) {
         StackLayer &ly = st->L[il];
         const uint8_t *s = base + l.off[il];
-        if (ly.rec) {
-            if ((rc = d2d(ctx, ly.conv_state, s, l.conv * 4)) == GD_OK)
-                rc = d2d(ctx, ly.rec_state, s + align256(l.conv * 4), l.rec * 4);
-        } else if ((rc = d2d(ctx, ly.kc, s, l.kv * 2)) == GD_OK) {
-            rc = d2d(ctx, ly.vc, s + align256(l.kv * 2), l.kv * 2);
-        }
+        if (ly.rec && (rc = d2d(ctx, ly.conv_state, s, l.conv * 4)) == GD_OK)
+            rc = d2d(ctx, ly.rec_state, s + align256(l.conv * 4), l.rec * 4);
     }
     if (rc == GD_OK) rc = gd_fill_u32(ctx, st->dpos, (uint32_t)b->pos, 1);
     if (rc == GD_OK) rc = gd_fill_u32(ctx, st->dpos + 1, (uint32_t)(int32_t)b->rope_shift, 1);
@@ -1332,8 +1576,8 @@ extern "C" int gd_stack_serialize(gd_stack *st, const gd_bookmark *b, void *buf,
     if (!buf) return GD_OK;
     GD_REQUIRE(ctx, cap >= sizer.n, "gd_stack_serialize: buffer of %zu bytes, need %zu", cap,
                sizer.n);
-    std::vector<uint8_t> host(l.total);
-    int rc = gd_download(ctx, host.data(), b->buf, l.total);
+    std::vector<uint8_t> host;
+    int rc = bookmark_to_host(st, b, host);
     if (rc) return rc;
     Out o{(uint8_t *)buf, cap};
     emit(o, host.data());
@@ -1352,18 +1596,54 @@ namespace {
 constexpr char GDNS_MAGIC[4] = {'G', 'D', 'N', 'S'};
 constexpr int64_t GDNS_VERSION = 1, GDNS_PAGE = 512;
 
-// Finish a bookmark from host bytes in the device layout.
+// A bookmark from its host image (bm_layout with K/V): the GDN state into
+// its device buffer, the K/V into fresh pages of the stack's pool.
 int bookmark_from_host(gd_stack *st, const std::vector<uint8_t> &host, int64_t pos,
                        gd_bookmark **out, int64_t rope_shift = 0) {
     gd_ctx *ctx = st->ctx;
+    const BmLayout lh = bm_layout(st, pos), ld = bm_layout(st, pos, false);
     gd_bookmark *b = new gd_bookmark();
     b->ctx = ctx;
     b->c = st->c;
     b->pos = pos;
     b->rope_shift = rope_shift;
     b->have_pick = false;        // neither format carries a pick: decode a token first
-    int rc = gd_alloc(ctx, host.size(), &b->buf);
-    if (rc == GD_OK) rc = gd_upload(ctx, b->buf, host.data(), host.size());
+    b->kv = st->kv;
+    std::vector<uint8_t> dev(ld.total, 0);
+    int natt = 0;
+    for (int il = 0; il < st->c.n_layer; il++) {
+        if (st->L[il].rec)
+            memcpy(dev.data() + ld.off[il], host.data() + lh.off[il],
+                   align256(lh.conv * 4) + lh.rec * 4);
+        else
+            natt++;
+    }
+    int rc = gd_alloc(ctx, ld.total, &b->buf);
+    if (rc == GD_OK) rc = gd_upload(ctx, b->buf, dev.data(), ld.total);
+    const size_t np = (size_t)((pos + st->c.kv_block - 1) / st->c.kv_block);
+    for (size_t i = 0; rc == GD_OK && i < np; i++) {
+        int32_t q;
+        if ((rc = take_page(st, &q)) == GD_OK) b->pages.push_back(q);
+    }
+    if (rc == GD_OK && natt && pos) {
+        const size_t span = lh.kv;
+        std::vector<uint16_t> kvh((size_t)natt * 2 * span);
+        for (int il = 0; il < st->c.n_layer; il++) {
+            const StackLayer &ly = st->L[il];
+            if (ly.rec) continue;
+            for (int kv = 0; kv < 2; kv++)
+                memcpy(kvh.data() + (2 * (size_t)ly.att + kv) * span,
+                       host.data() + lh.off[il] + kv * align256(span * 2), span * 2);
+        }
+        void *tmp = nullptr;
+        if ((rc = gd_alloc(ctx, kvh.size() * 2, &tmp)) == GD_OK) {
+            rc = gd_upload(ctx, tmp, kvh.data(), kvh.size() * 2);
+            if (rc == GD_OK)
+                rc = kv_gather(ctx, *st->kv, b->pages, pos, st->c.kv_block, (uint16_t *)tmp, true);
+            if (rc == GD_OK) rc = gd_sync(ctx);
+            gd_free(ctx, tmp);
+        }
+    }
     if (rc) {
         gd_bookmark_free(b);
         return rc;
@@ -1433,8 +1713,8 @@ extern "C" int gd_stack_serialize_gdns(gd_stack *st, const gd_bookmark *b, void 
     if (!buf) return GD_OK;
     GD_REQUIRE(ctx, cap >= sizer.n, "gd_stack_serialize_gdns: buffer of %zu bytes, need %zu",
                cap, sizer.n);
-    std::vector<uint8_t> host(l.total);
-    int rc = gd_download(ctx, host.data(), b->buf, l.total);
+    std::vector<uint8_t> host;
+    int rc = bookmark_to_host(st, b, host);
     if (rc) return rc;
     Out o{(uint8_t *)buf, cap};
     emit(o, host.data());

@@ -513,6 +513,15 @@ int gd_stack_set_eager(gd_stack *st, int eager);
 int gd_stack_tensor(gd_stack *st, int layer, const char *name, gd_q2w *w,
                     int64_t *row0, float **f32, int64_t *count);
 int gd_stack_position(gd_stack *st, int64_t *pos);
+/* KV page accounting (any pointer may be NULL): *live = pages mapped by the
+ * live state, *held = pages of the stack's pool held by the live state or a
+ * bookmark, *capacity = pages each attention layer's K (and V) pool holds.
+ * Pages are kv_block positions; the pool starts at twice a prefill chunk and
+ * doubles on demand (MetalKVPool allocates pages lazily, MetalKVPool.swift:
+ * 53-66); a bookmark shares the completed pages and holds a copy of a partial
+ * tail page (MetalKVPool.snapshot, :102-110).  No counterpart in the
+ * reference as a call: memory accounting and tests. */
+int gd_stack_kv_pages(gd_stack *st, int64_t *live, int64_t *held, int64_t *capacity);
 
 /* ---- Bookmarks: MetalEngine.bookmark / restore / serialize / deserialize -------
  * (MetalEngine.swift:455-584).  A bookmark is a device-memory snapshot of the

@@ -3,7 +3,9 @@ serialize / deserialize (MetalEngine.swift:455-584).
 
   * bookmark, decode, restore, decode again: bit-identical logits and picks,
     and generate from a restored bookmark continues from its pick;
-  * a bookmark outlives a reset and a different prompt (its K/V are its own);
+  * a bookmark outlives a reset and a different prompt, and the stack it came
+    from; it shares the completed KV pages and holds a copy of the partial
+    tail page only;
   * serialize writes MetalEngine.serialize's bytes (checked field by field
     against the stack's own state), deserialize into a fresh stack of the
     same weights continues bit-identically, and re-serializing gives the same
@@ -127,6 +129,94 @@ def test_bookmark_outlives_reset(ctx):
         if bm:
             ctx.lib.gd_bookmark_free(bm)
         ctx.lib.gd_stack_destroy(st)
+
+
+def kv_pages(ctx, st):
+    live, held, cap = C.c_int64(), C.c_int64(), C.c_int64()
+    ctx.check(ctx.lib.gd_stack_kv_pages(st, C.byref(live), C.byref(held), C.byref(cap)))
+    return live.value, held.value, cap.value
+
+
+def test_bookmark_shares_kv_pages(ctx):
+    """KV pages are shared, not copied (MetalKVPool.snapshot / restore,
+    MetalKVPool.swift:95-120): a bookmark at position 1000 (62 full pages of
+    16 and a partial one) takes one page -- its copy of the partial tail --
+    and a restore one more -- the live state's own tail -- while the pool
+    grew from 10 pages by doubling during the prefill.  The restored state
+    continues bit-identically: in the same stack, after a reset and another
+    prompt have reused the freed pages, and in a second stack (pages copied
+    between pools).  A bookmark on a page boundary takes no page."""
+    cfg, st = make_stack(ctx, seed=23, max_ctx=1104, max_batch=64)
+    st2 = bm = bm2 = None
+    try:
+        live, held, cap = kv_pages(ctx, st)
+        assert (live, held, cap) == (0, 0, 10)
+        ids = (np.arange(1000) * 31 % cfg["n_vocab"]).astype(np.int32)
+        first = prefill(ctx, st, ids)
+        live, held, cap = kv_pages(ctx, st)
+        assert live == 63 and held == 63 and 63 <= cap < 2 * 63 + 10
+        bm = bookmark(ctx, st)
+        assert kv_pages(ctx, st)[1] == 64                   # one tail page copied
+        toks = [first, 5, 77, 300, 9]
+        l1, p1 = decode_run(ctx, st, toks)
+        ctx.check(ctx.lib.gd_stack_restore(st, bm))
+        assert kv_pages(ctx, st)[:2] == (63, 64)            # the old tail freed, a new one taken
+        l2, p2 = decode_run(ctx, st, toks)
+        assert same(l1, l2) and p1 == p2
+        # Another prompt on the freed pages; the shared ones stay the bookmark's.
+        ctx.check(ctx.lib.gd_stack_reset(st))
+        assert kv_pages(ctx, st)[:2] == (0, 63)
+        prefill(ctx, st, (np.arange(300) * 7 % cfg["n_vocab"]).astype(np.int32))
+        ctx.check(ctx.lib.gd_stack_restore(st, bm))
+        l3, p3 = decode_run(ctx, st, toks)
+        assert same(l1, l3) and p1 == p3
+        # A second stack of the same weights: its own pool, pages copied in.
+        _, st2 = make_stack(ctx, seed=23, max_ctx=1104, max_batch=64)
+        ctx.check(ctx.lib.gd_stack_restore(st2, bm))
+        assert kv_pages(ctx, st2)[:2] == (63, 63)
+        l4, p4 = decode_run(ctx, st2, toks)
+        assert same(l1, l4) and p1 == p4
+        # On a page boundary nothing is copied.
+        ctx.check(ctx.lib.gd_stack_reset(st2))
+        prefill(ctx, st2, ids[:992])
+        before = kv_pages(ctx, st2)[1]
+        bm2 = bookmark(ctx, st2)
+        assert kv_pages(ctx, st2)[1] == before == 62
+        ctx.lib.gd_bookmark_free(bm)
+        bm = None
+        assert kv_pages(ctx, st)[1] == 63                   # the live state's pages only
+        print(f"\n  KV pages: bookmark at 1000 held 1 extra page; pool capacity {cap}")
+    finally:
+        for b in (bm, bm2):
+            if b:
+                ctx.lib.gd_bookmark_free(b)
+        ctx.lib.gd_stack_destroy(st)
+        if st2:
+            ctx.lib.gd_stack_destroy(st2)
+
+
+def test_bookmark_outlives_its_stack(ctx):
+    """A bookmark holds its pool: the stack it came from can be destroyed and
+    the bookmark still restores into another stack bit-identically."""
+    cfg, st = make_stack(ctx, seed=24)
+    st2 = bm = None
+    try:
+        ids = (np.arange(70) * 5 % cfg["n_vocab"]).astype(np.int32)
+        first = prefill(ctx, st, ids)
+        bm = bookmark(ctx, st)
+        l1, p1 = decode_run(ctx, st, [first, 11, 12])
+        ctx.lib.gd_stack_destroy(st)
+        st = None
+        _, st2 = make_stack(ctx, seed=24)
+        ctx.check(ctx.lib.gd_stack_restore(st2, bm))
+        l2, p2 = decode_run(ctx, st2, [first, 11, 12])
+        assert same(l1, l2) and p1 == p2
+    finally:
+        if bm:
+            ctx.lib.gd_bookmark_free(bm)
+        for s in (st, st2):
+            if s:
+                ctx.lib.gd_stack_destroy(s)
 
 
 def parse(data: bytes, cfg):
