@@ -38,16 +38,39 @@ __device__ __forceinline__ int64_t kv_slot(const int32_t *pt, int pos, int block
     return (int64_t)pt[pos / block] * block + pos % block;
 }
 
+// cos and sin of the rotation of pair jj (< n_rot/2) at position pos
+// (Kern.ropeNeox, Kernels.swift:66-84): from the table rtab[pos][jj] when it
+// holds pos (rows 0 .. rtab_n - 1, formed by k_rope_table with this same
+// arithmetic, so both give the same bits), else computed.
+__device__ __forceinline__ float2 rope_cs(int jj, int n_rot, float base, int pos,
+                                          const float2 *rtab, int rtab_n) {
+    if (rtab && pos >= 0 && pos < rtab_n) return rtab[(int64_t)pos * (n_rot / 2) + jj];
+    const float freq = powf(base, -2.0f * (float)jj / (float)n_rot);
+    const float ang = (float)pos * freq;
+    return make_float2(cosf(ang), sinf(ang));
+}
+
+// The table rope_cs reads: rows of n_rot/2 (cos, sin) pairs for positions
+// 0 .. n-1.
+__global__ void k_rope_table(float2 *tab, int n, int n_rot, float base) {
+    const int half = n_rot / 2;
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t)n * half) return;
+    const int jj = (int)(i % half), pos = (int)(i / half);
+    const float freq = powf(base, -2.0f * (float)jj / (float)n_rot);
+    const float ang = (float)pos * freq;
+    tab[i] = make_float2(cosf(ang), sinf(ang));
+}
+
 // Partial NEOX rope of dim i (< n_rot) of a head whose values are `mine` (dim
 // i) and `pv` (its partner i +- n_rot/2), at position pos (Kern.ropeNeox,
 // Kernels.swift:66-84).
 __device__ __forceinline__ float rope_dim(int i, float mine, float pv, int n_rot, float base,
-                                          int pos) {
+                                          int pos, const float2 *rtab, int rtab_n) {
     const int half = n_rot / 2;
     const int jj = i < half ? i : i - half;
-    const float freq = powf(base, -2.0f * (float)jj / (float)n_rot);
-    const float ang = (float)pos * freq;
-    const float c = cosf(ang), sn = sinf(ang);
+    const float2 cs = rope_cs(jj, n_rot, base, pos, rtab, rtab_n);
+    const float c = cs.x, sn = cs.y;
     return i < half ? mine * c - pv * sn : pv * sn + mine * c;
 }
 
@@ -69,7 +92,8 @@ template <int HD>
 __global__ __launch_bounds__(64 * PREP_WAVES) void k_attn_prep(
         const float *proj, int64_t stride, int qs, const float *q_norm, const float *k_norm,
         float *q_out, float *gate_out, uint16_t *kc, uint16_t *vc, const int32_t *page_table,
-        const int32_t *pos_ptr, int N, int H, int HKV, int n_rot, float base, int block, float eps) {
+        const int32_t *pos_ptr, int N, int H, int HKV, int n_rot, float base, int block, float eps,
+        const float2 *rtab, int rtab_n) {
     constexpr int S = HD / 64;
     __shared__ float rc[HD / 2], rs[HD / 2];
     const int groups = (H + HKV + PREP_HEADS - 1) / PREP_HEADS;
@@ -78,10 +102,9 @@ __global__ __launch_bounds__(64 * PREP_WAVES) void k_attn_prep(
     const int pos = pos_ptr[0] + n, rpos = pos + pos_ptr[1];
     const int half = n_rot / 2;
     for (int j = threadIdx.x; j < half; j += 64 * PREP_WAVES) {
-        const float freq = powf(base, -2.0f * (float)j / (float)n_rot);
-        const float ang = (float)rpos * freq;
-        rc[j] = cosf(ang);
-        rs[j] = sinf(ang);
+        const float2 cs = rope_cs(j, n_rot, base, rpos, rtab, rtab_n);
+        rc[j] = cs.x;
+        rs[j] = cs.y;
     }
     __syncthreads();
     const float *row = proj + (int64_t)n * stride;
@@ -338,7 +361,8 @@ template <int HD, bool FUSED>
 __global__ __launch_bounds__(2 * HD) void k_attn_decode(
         const float *src, int qs, const float *q_norm, const float *k_norm, uint16_t *kc,
         uint16_t *vc, const int32_t *page_table, const int32_t *pos_ptr, int T, int lo, float *part,
-        int H, int HKV, int block, float scale, int n_rot, float base, float eps) {
+        int H, int HKV, int block, float scale, int n_rot, float base, float eps,
+        const float2 *rtab, int rtab_n) {
     constexpr int NT = 2 * HD, NWD = NT / 64, DPL = HD / 64, WPH = HD / 64;
     constexpr int STEP = DSPLIT * NWD;
     __shared__ float wm[NWD], wl[NWD];
@@ -392,7 +416,7 @@ __global__ __launch_bounds__(2 * HD) void k_attn_decode(
         // Rotated at position + shift (pos_ptr[1]), cached at position.
         if (i < n_rot)
             y = rope_dim(i, nrm[hf][i], i < half ? nrm[hf][i + half] : nrm[hf][i - half], n_rot,
-                         base, pos + pos_ptr[1]);
+                         base, pos + pos_ptr[1], rtab, rtab_n);
         rot[hf][i] = y;
         if (hf == 1) vnew[i] = vx;
         __syncthreads();
@@ -548,18 +572,19 @@ int gd_attn_prep_launch(gd_ctx *ctx, int hd, const float *proj, int64_t stride, 
                         const float *q_norm, const float *k_norm, float *q_out, float *gate_out,
                         uint16_t *kc, uint16_t *vc, const int32_t *page_table,
                         const int32_t *pos_ptr, int N, int H, int HKV, int n_rot, float base,
-                        int block, float eps) {
+                        int block, float eps, const float *rope_tab, int rope_n) {
     GD_REQUIRE(ctx, n_rot >= 0 && n_rot <= hd && n_rot % 2 == 0, "attention prep: n_rot=%d", n_rot);
+    const float2 *rtab = (const float2 *)rope_tab;
     const dim3 grid((unsigned)((int64_t)N * ((H + HKV + PREP_HEADS - 1) / PREP_HEADS)));
     const dim3 blk(64 * PREP_WAVES);
     if (hd == 128)
         hipLaunchKernelGGL(k_attn_prep<128>, grid, blk, 0, ctx->stream, proj, stride, qs,
                            q_norm, k_norm, q_out, gate_out, kc, vc, page_table, pos_ptr, N, H,
-                           HKV, n_rot, base, block, eps);
+                           HKV, n_rot, base, block, eps, rtab, rope_n);
     else
         hipLaunchKernelGGL(k_attn_prep<256>, grid, blk, 0, ctx->stream, proj, stride, qs,
                            q_norm, k_norm, q_out, gate_out, kc, vc, page_table, pos_ptr, N, H,
-                           HKV, n_rot, base, block, eps);
+                           HKV, n_rot, base, block, eps, rtab, rope_n);
     GD_LAUNCHED(ctx, "k_attn_prep");
     return GD_OK;
 }
@@ -586,20 +611,21 @@ int gd_attn_decode_launch(gd_ctx *ctx, int hd, const float *proj, int qs, const 
                           const float *k_norm, uint16_t *kc, uint16_t *vc,
                           const int32_t *page_table, const int32_t *pos_ptr, float *part,
                           uint16_t *out, int H, int HKV, int block, float scale, int n_rot,
-                          float base, float eps) {
+                          float base, float eps, const float *rope_tab, int rope_n) {
     const dim3 grid((unsigned)H, DSPLIT);
+    const float2 *rtab = (const float2 *)rope_tab;
     const int gated = qs == 2 * hd;
     if (hd == 128) {
         hipLaunchKernelGGL((k_attn_decode<128, true>), grid, dim3(256), 0, ctx->stream, proj, qs,
                            q_norm, k_norm, kc, vc, page_table, pos_ptr, 0, 0, part, H, HKV, block,
-                           scale, n_rot, base, eps);
+                           scale, n_rot, base, eps, rtab, rope_n);
         GD_LAUNCHED(ctx, "k_attn_decode");
         hipLaunchKernelGGL((k_attn_combine<128, uint16_t>), dim3(H), dim3(128), 0, ctx->stream,
                            part, proj + 128, 2 * 128, gated, out);
     } else {
         hipLaunchKernelGGL((k_attn_decode<256, true>), grid, dim3(512), 0, ctx->stream, proj, qs,
                            q_norm, k_norm, kc, vc, page_table, pos_ptr, 0, 0, part, H, HKV, block,
-                           scale, n_rot, base, eps);
+                           scale, n_rot, base, eps, rtab, rope_n);
         GD_LAUNCHED(ctx, "k_attn_decode");
         hipLaunchKernelGGL((k_attn_combine<256, uint16_t>), dim3(H), dim3(256), 0, ctx->stream,
                            part, proj + 256, 2 * 256, gated, out);
@@ -609,6 +635,15 @@ int gd_attn_decode_launch(gd_ctx *ctx, int hd, const float *proj, int qs, const 
 }
 
 size_t gd_attn_part_floats(int hd, int H) { return (size_t)H * DSPLIT * (hd + 2); }
+
+int gd_rope_table(gd_ctx *ctx, float *tab, int n, int n_rot, float base) {
+    GD_REQUIRE(ctx, tab && n > 0 && n_rot > 0 && n_rot % 2 == 0, "rope table: bad arguments");
+    const int64_t total = (int64_t)n * (n_rot / 2);
+    hipLaunchKernelGGL(k_rope_table, dim3(gd_blocks(total, 256)), dim3(256), 0, ctx->stream,
+                       (float2 *)tab, n, n_rot, base);
+    GD_LAUNCHED(ctx, "k_rope_table");
+    return GD_OK;
+}
 
 // ---------------------------------------------------------------- C ABI
 
@@ -686,14 +721,14 @@ extern "C" int gd_attn_paged(gd_ctx *ctx, const float *q, const uint16_t *k_cach
     if (hd == 128) {
         hipLaunchKernelGGL((k_attn_decode<128, false>), grid, dim3(256), 0, ctx->stream, q,
                            128, nullptr, nullptr, kc, vc, page_table, nullptr, T, lo, part, n_head,
-                           n_head_kv, page_size, scale, 0, 0.f, 0.f);
+                           n_head_kv, page_size, scale, 0, 0.f, 0.f, nullptr, 0);
         GD_LAUNCHED(ctx, "gd_attn_paged");
         hipLaunchKernelGGL((k_attn_combine<128, float>), dim3(n_head), dim3(128), 0, ctx->stream,
                            part, gate, 128, gated, out);
     } else {
         hipLaunchKernelGGL((k_attn_decode<256, false>), grid, dim3(512), 0, ctx->stream, q,
                            256, nullptr, nullptr, kc, vc, page_table, nullptr, T, lo, part, n_head,
-                           n_head_kv, page_size, scale, 0, 0.f, 0.f);
+                           n_head_kv, page_size, scale, 0, 0.f, 0.f, nullptr, 0);
         GD_LAUNCHED(ctx, "gd_attn_paged");
         hipLaunchKernelGGL((k_attn_combine<256, float>), dim3(n_head), dim3(256), 0, ctx->stream,
                            part, gate, 256, gated, out);

@@ -81,7 +81,7 @@ int gd_attn_prep_launch(gd_ctx *ctx, int hd, const float *proj, int64_t stride, 
                         const float *q_norm, const float *k_norm, float *q_out, float *gate_out,
                         uint16_t *kc, uint16_t *vc, const int32_t *page_table,
                         const int32_t *pos_ptr, int N, int H, int HKV, int n_rot, float base,
-                        int block, float eps);
+                        int block, float eps, const float *rope_tab, int rope_n);
 int gd_attn_prefill_launch(gd_ctx *ctx, int hd, const float *q, const float *gate,
                            const uint16_t *kc, const uint16_t *vc, const int32_t *page_table,
                            const int32_t *pos_ptr, int pos_add, void *out, int out_dtype, int H,
@@ -90,8 +90,12 @@ int gd_attn_decode_launch(gd_ctx *ctx, int hd, const float *proj, int qs, const 
                           const float *k_norm, uint16_t *kc, uint16_t *vc,
                           const int32_t *page_table, const int32_t *pos_ptr, float *part,
                           uint16_t *out, int H, int HKV, int block, float scale, int n_rot,
-                          float base, float eps);
+                          float base, float eps, const float *rope_tab, int rope_n);
 size_t gd_attn_part_floats(int hd, int H);
+// The rotation table of prep and fused decode: for positions 0 .. n-1, the
+// n_rot/2 (cos, sin) f32 pairs of the partial NEOX rope (rope positions
+// outside it are computed in the kernels, to the same bits).
+int gd_rope_table(gd_ctx *ctx, float *tab, int n, int n_rot, float base);
 
 #define GD_CHECK_CTX(ctx) \
     do { if (!(ctx)) return GD_EINVAL; } while (0)

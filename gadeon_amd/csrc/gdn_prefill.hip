@@ -123,6 +123,7 @@ struct Work {
     f16 *KT;          // [u][DK][CP]
     f16 *KTl;         // [u][DK][CP], f32 k only: k - f16(k)
     float *G;         // [u][CP]
+    f16 *Qh, *Ql;     // [u][CP][DK], f32 q only: q split as prep forms it, for the scan
 };
 
 struct PrepArgs {
@@ -197,6 +198,11 @@ __global__ __launch_bounds__(256) void gdn_prep(PrepArgs a) {
             split_raw8<IO>(rq[n], ok, h, l);
             *(f16x8 *)&QVs[t][i8] = h;
             *(f16x8 *)&Ql[t][i8] = l;
+            // The scan's output pass reads this split instead of splitting
+            // q again at every chunk (rows past the chunk: zeros).
+            const size_t qi = ((size_t)u * CP + t) * DK + i8;
+            *(f16x8 *)&a.w.Qh[qi] = h;
+            *(f16x8 *)&a.w.Ql[qi] = l;
         } else {
             *(f16x8 *)&Ks[t][i8] = cvt8<IO>(rk[n], ok);
             *(f16x8 *)&QVs[t][i8] = cvt8<IO>(rq[n], ok);
@@ -444,10 +450,12 @@ struct ChainRegs {
     f16x8 kal[sizeof(IO) == 4 ? 2 : 1][CP / 32];   // their lo halves (f32 k)
 };
 
-// The output group's operands of one chunk: Q (raw) and P.
+// The output group's operands of one chunk: Q and P.  f16 q is loaded raw
+// (converted at use); f32 q as the hi/lo split prep stored.
 template <int CP, typename IO>
 struct OutRegs {
-    Raw8<IO> qr[DK / 32];                 // Q row 16*wave + lr (row 0 past the chunk), raw
+    Raw8<IO> qr[sizeof(IO) == 4 ? 1 : DK / 32];   // f16: Q row 16*wave + lr (row 0 past the chunk)
+    f16x8 qh[sizeof(IO) == 4 ? DK / 32 : 1], ql[sizeof(IO) == 4 ? DK / 32 : 1];   // f32: the split
     f16x8 ph[CP / 32], pl[CP / 32];       // P row 16*wave + lr
 };
 
@@ -604,10 +612,20 @@ __global__ __launch_bounds__(SCAN_THREADS) void gdn_scan(ScanArgs a) {
         if (rows) {
             const int tr = tb + lr;
             const bool rok = tr < L;
+            if constexpr (sizeof(IO) == 4) {
+                const size_t un = unit(c);
 #pragma unroll
-            for (int ks = 0; ks < DK / 32; ks++)
-                o.qr[ks] = load_raw8<IO>(a.q, (t0 + (rok ? tr : 0)) * a.q_stride + (int64_t)hk * DK +
-                                                  ks * 32 + kg * 8);
+                for (int ks = 0; ks < DK / 32; ks++) {
+                    const size_t qi = (un * CP + tr) * DK + ks * 32 + kg * 8;
+                    o.qh[ks] = *(const f16x8 *)&a.w.Qh[qi];
+                    o.ql[ks] = *(const f16x8 *)&a.w.Ql[qi];
+                }
+            } else {
+#pragma unroll
+                for (int ks = 0; ks < DK / 32; ks++)
+                    o.qr[ks] = load_raw8<IO>(a.q, (t0 + (rok ? tr : 0)) * a.q_stride +
+                                                      (int64_t)hk * DK + ks * 32 + kg * 8);
+            }
         }
     };
     auto loadP = [&](int c, OutRegs<CP, IO> &o) {
@@ -633,10 +651,8 @@ __global__ __launch_bounds__(SCAN_THREADS) void gdn_scan(ScanArgs a) {
             for (int ks = 0; ks < DK / 32; ks++) {
                 const int i0 = ks * 32 + kg * 8;
                 if constexpr (sizeof(IO) == 4) {
-                    f16x8 qh, ql;
-                    split_raw8<IO>(o.qr[ks], tb + lr < L, qh, ql);
-                    acc = mfma3(qh, ql, *(const f16x8 *)&Sh[b][j][i0], *(const f16x8 *)&Sl[b][j][i0],
-                                acc);
+                    acc = mfma3(o.qh[ks], o.ql[ks], *(const f16x8 *)&Sh[b][j][i0],
+                                *(const f16x8 *)&Sl[b][j][i0], acc);
                 } else {
                     const f16x8 qa = cvt8<IO>(o.qr[ks], tb + lr < L);
                     acc = mfma(qa, *(const f16x8 *)&Sh[b][j][i0], acc);
@@ -778,9 +794,10 @@ int prefill_check(gd_ctx *ctx, const char *fn, int64_t T, int nV, int nK, int dk
     const size_t units = (size_t)nV * (size_t)((T + C - 1) / C);
     const size_t CP = C < 32 ? 32 : C;
     const size_t nkt = io_dtype == GD_F32 ? 2 : 1;
-    // Wh, Wl; U; Ph, Pl; K^T (hi, lo); G -- the layout prefill_run carves.
+    // Wh, Wl; U; Ph, Pl; K^T (hi, lo); G; Q (hi, lo: f32 io) -- the layout
+    // prefill_run carves.
     *bytes = units * (2 * CP * DK * 2 + CP * DV * 4 + 2 * CP * CP * 2 + nkt * DK * CP * 2 +
-                      CP * 4);
+                      CP * 4 + (nkt - 1) * 2 * CP * DK * 2);
     return GD_OK;
 }
 
@@ -809,7 +826,10 @@ int prefill_run(gd_ctx *ctx, void *ws, int64_t T, int nV, int nK, const void *q,
     w.KT = (f16 *)p;            p += kbytes;
     w.KTl = nkt == 2 ? (f16 *)p : nullptr;
     p += (nkt - 1) * kbytes;
-    w.G = (float *)p;
+    w.G = (float *)p;           p += units * CP * 4;
+    w.Qh = nkt == 2 ? (f16 *)p : nullptr;
+    p += (nkt - 1) * wbytes;
+    w.Ql = nkt == 2 ? (f16 *)p : nullptr;
 
     PrepArgs pa{q, k, v, q_stride, k_stride, v_stride, g, beta, w, T, nV, nK, C, nchunks, qScale};
     ScanArgs sa{q, q_stride, w, S, o, o_stride, T, nV, nK, C, nchunks, qScale};

@@ -520,6 +520,7 @@ struct gd_stack {
     float *x = nullptr, *proj = nullptr, *conv_out = nullptr, *o32 = nullptr, *contrib = nullptr;
     float *beta = nullptr, *g = nullptr, *q32 = nullptr, *gate32 = nullptr, *logits = nullptr;
     float *attn_part = nullptr, *amax_v = nullptr;
+    float *rope_tab = nullptr;           // [max_ctx][n_rot/2] (cos, sin), gd_rope_table
     int *amax_i = nullptr;
     uint16_t *xn16 = nullptr, *a16 = nullptr;
     int32_t *ids = nullptr, *dtok = nullptr;
@@ -679,11 +680,12 @@ int forward(gd_stack *st, int N, bool decode) {
                 // inside the attention launch.
                 R_(gd_attn_decode_launch(ctx, hd, st->proj, qs, ly.q_norm, ly.k_norm, kc, vc,
                                          st->page_table, st->dpos, st->attn_part, st->a16, H, HKV,
-                                         c.kv_block, scale, c.n_rot, c.rope_base, eps));
+                                         c.kv_block, scale, c.n_rot, c.rope_base, eps, st->rope_tab,
+                                         c.max_ctx));
             } else {
                 R_(gd_attn_prep_launch(ctx, hd, st->proj, (int64_t)RP, qs, ly.q_norm, ly.k_norm, st->q32,
                                        st->gate32, kc, vc, st->page_table, st->dpos, N, H,
-                                       HKV, c.n_rot, c.rope_base, c.kv_block, eps));
+                                       HKV, c.n_rot, c.rope_base, c.kv_block, eps, st->rope_tab, c.max_ctx));
                 R_(gd_attn_prefill_launch(ctx, hd, st->q32, st->gate32, kc, vc,
                                           st->page_table, st->dpos, 0, st->a16, GD_F16, H, HKV, N,
                                           c.kv_block, scale, c.dense ? 0 : 1));
@@ -915,6 +917,10 @@ int create(gd_ctx *ctx, const gd_stack_config *cfg, uint64_t seed, bool random, 
     C_(salloc_t(st, (size_t)B * c.n_head * hd, &st->gate32));
     C_(salloc_t(st, (size_t)c.n_vocab, &st->logits));
     C_(salloc_t(st, gd_attn_part_floats(hd, c.n_head), &st->attn_part));
+    // Rotations of positions 0 .. max_ctx-1, formed once for every attention
+    // layer and token (a restored rope shift may rotate past them: computed).
+    C_(salloc_t(st, (size_t)c.max_ctx * c.n_rot, &st->rope_tab));
+    C_(gd_rope_table(ctx, st->rope_tab, c.max_ctx, c.n_rot, c.rope_base));
     C_(salloc_t(st, (size_t)AMAX_BLOCKS, &st->amax_v));
     C_(salloc_t(st, (size_t)AMAX_BLOCKS, &st->amax_i));
     C_(salloc_t(st, (size_t)B * E, &st->xn16));

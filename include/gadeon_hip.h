@@ -398,8 +398,8 @@ int gd_gdn_prefill(gd_ctx *ctx, int64_t T, int nV, int nK, int dk, int dv,
  * that may grow with hipMalloc; here they live in a fixed device array of
  * GD_GDN_PREFILL_SCRATCH_BYTES per GPU, held until the process ends, and the
  * call allocates nothing.  Shapes needing more are rejected with GD_EINVAL:
- * the scratch takes nV * ceil(T/C) * b bytes, b = 98,560 (f16 io) or 114,944
- * (f32 io) at C = 64, so e.g. 16 heads fit T <= 1152 (f32) / 1344 (f16).
+ * the scratch takes nV * ceil(T/C) * b bytes, b = 98,560 (f16 io) or 147,712
+ * (f32 io) at C = 64, so e.g. 16 heads fit T <= 896 (f32) / 1344 (f16).
  * Every call on a GPU shares the array (nothing in it needs to start at
  * zero: each call writes all it reads), so calls that overlap on one GPU --
  * from two streams or threads -- race. */
