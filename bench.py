@@ -533,14 +533,14 @@ def cpu_baseline_stack(ctx, ga, h, c, seconds: float) -> dict:
 TRAFFIC_FILE = ROOT / "profiles" / "q2_0_gemv_K5120_R34816_traffic.txt"
 
 
-def gemv_traffic():
-    """HBM bytes per launch of the roofline GEMV as rocprofv3 --pmc measured
+def gemv_traffic(key: str = "traffic_bytes_per_launch"):
+    """HBM bytes per launch of a roofline GEMV as rocprofv3 --pmc measured
     them (FETCH_SIZE + WRITE_SIZE, each scaled by the same counter on a copy
     kernel of known size), read from the committed summary; None if absent."""
     try:
         for line in TRAFFIC_FILE.read_text().splitlines():
-            if line.startswith("traffic_bytes_per_launch:"):
-                return int(line.split(":", 1)[1])
+            if line.startswith(key + ":"):
+                return int(line.split(":", 1)[1].split("#")[0])
     except (OSError, ValueError):
         pass
     return None
@@ -751,6 +751,7 @@ def main() -> int:
             "roofline_lm_head": {"bound": "hbm", "achieved": round(hd["gbs"], 1),
                                  "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                  "frac": round(hd["gbs"] / HBM_PEAK_GBS, 4),
+                                 "traffic": gemv_traffic("lm_head_traffic_bytes_per_launch"),
                                  "kernel": "q2_0_gemv_mfma " + hd["shape"] + " (weights rotated "
                                            f"over {hd['pool']} copies, streamed from HBM)"},
             "roofline_prefill": {"bound": "mfma", "achieved": round(gl["tflops"], 1),
