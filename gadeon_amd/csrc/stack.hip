@@ -435,6 +435,7 @@ struct StackLayer {
 // reference to the pool: it outlives the stack while any of them lives.
 struct KvPool {
     gd_ctx *ctx = nullptr;
+    int block = 0;                     // positions per page
     size_t page_elems = 0;             // halves per page
     int cap = 0;                       // physical pages per pool
     std::vector<uint16_t *> k, v;      // [attention layers] pools of cap pages
@@ -900,6 +901,7 @@ int create(gd_ctx *ctx, const gd_stack_config *cfg, uint64_t seed, bool random, 
     // max_ctx) and grow on demand.
     st->kv = std::make_shared<KvPool>();
     st->kv->ctx = ctx;
+    st->kv->block = c.kv_block;
     st->kv->page_elems = (size_t)c.kv_block * c.n_head_kv * hd;
     st->kv->k.assign(natt, nullptr);
     st->kv->v.assign(natt, nullptr);
@@ -1319,15 +1321,58 @@ BmLayout bm_layout(const gd_stack *st, int64_t pos, bool kv = true) {
     return l;
 }
 
+// K and V of positions [0, pos) of every attention layer, gathered from the
+// pages into one device array [attention layer][K, V][pos][kv_dim] (f16),
+// or scattered back from it.
+int kv_gather(gd_ctx *ctx, const KvPool &pool, const std::vector<int32_t> &pages, int64_t pos,
+              uint16_t *dev, bool scatter) {
+    const int B = pool.block;
+    const size_t pe = pool.page_elems, kvd = pe / B, span = (size_t)pos * kvd;
+    int rc = GD_OK;
+    for (size_t a = 0; a < pool.k.size(); a++)
+        for (int kv = 0; kv < 2; kv++) {
+            uint16_t *base = (kv ? pool.v : pool.k)[a];
+            uint16_t *arr = dev + (2 * a + kv) * span;
+            for (size_t i = 0; rc == GD_OK && i < pages.size(); i++) {
+                const size_t n = std::min((size_t)B, (size_t)pos - i * B) * kvd;
+                uint16_t *pg = base + (size_t)pages[i] * pe;
+                rc = scatter ? gd_copy(ctx, pg, arr + i * B * kvd, n * 2)
+                             : gd_copy(ctx, arr + i * B * kvd, pg, n * 2);
+            }
+        }
+    return rc;
+}
+
 // dst <- the pages of positions [0, pos) given as `src` in pool `from`,
 // held for a new owner in the stack's pool: a complete page of the same
 // pool is shared; a partial tail page, or any page of another pool, is
-// copied into a fresh page (on the context stream).
+// copied into a fresh page (on the context stream); pages of another page
+// size go through a contiguous copy of the positions.
 int adopt_pages(gd_stack *st, const std::shared_ptr<KvPool> &from, const std::vector<int32_t> &src,
                 int64_t pos, std::vector<int32_t> &dst) {
     const int64_t B = st->c.kv_block;
     dst.clear();
     int rc = GD_OK;
+    if (from->block != st->kv->block) {
+        const size_t np = (size_t)((pos + B - 1) / B);
+        for (size_t i = 0; rc == GD_OK && i < np; i++) {
+            int32_t q;
+            if ((rc = take_page(st, &q)) == GD_OK) dst.push_back(q);
+        }
+        void *tmp = nullptr;
+        const size_t bytes = from->k.size() * 2 * (size_t)pos * (from->page_elems / from->block) * 2;
+        if (rc == GD_OK && bytes && (rc = gd_alloc(st->ctx, bytes, &tmp)) == GD_OK) {
+            rc = kv_gather(st->ctx, *from, src, pos, (uint16_t *)tmp, false);
+            if (rc == GD_OK) rc = kv_gather(st->ctx, *st->kv, dst, pos, (uint16_t *)tmp, true);
+            if (rc == GD_OK) rc = gd_sync(st->ctx);
+            gd_free(st->ctx, tmp);
+        }
+        if (rc) {
+            for (int32_t p : dst) st->kv->drop(p);
+            dst.clear();
+        }
+        return rc;
+    }
     for (size_t i = 0; rc == GD_OK && i < src.size(); i++) {
         const bool tail = (int64_t)(i + 1) * B > pos;
         if (from == st->kv && !tail) {
@@ -1345,27 +1390,6 @@ int adopt_pages(gd_stack *st, const std::shared_ptr<KvPool> &from, const std::ve
         for (int32_t p : dst) st->kv->drop(p);
         dst.clear();
     }
-    return rc;
-}
-
-// K and V of positions [0, pos) of every attention layer, gathered from the
-// pages into one device array [attention layer][K, V][pos][kv_dim] (f16),
-// or scattered back from it.
-int kv_gather(gd_ctx *ctx, const KvPool &pool, const std::vector<int32_t> &pages, int64_t pos,
-              int B, uint16_t *dev, bool scatter) {
-    const size_t pe = pool.page_elems, kvd = pe / B, span = (size_t)pos * kvd;
-    int rc = GD_OK;
-    for (size_t a = 0; a < pool.k.size(); a++)
-        for (int kv = 0; kv < 2; kv++) {
-            uint16_t *base = (kv ? pool.v : pool.k)[a];
-            uint16_t *arr = dev + (2 * a + kv) * span;
-            for (size_t i = 0; rc == GD_OK && i < pages.size(); i++) {
-                const size_t n = std::min((size_t)B, (size_t)pos - i * B) * kvd;
-                uint16_t *pg = base + (size_t)pages[i] * pe;
-                rc = scatter ? gd_copy(ctx, pg, arr + i * B * kvd, n * 2)
-                             : gd_copy(ctx, arr + i * B * kvd, pg, n * 2);
-            }
-        }
     return rc;
 }
 
@@ -1390,7 +1414,7 @@ int bookmark_to_host(gd_stack *st, const gd_bookmark *b, std::vector<uint8_t> &h
     const size_t span = lh.kv;
     void *tmp = nullptr;
     if ((rc = gd_alloc(ctx, (size_t)natt * 2 * span * 2, &tmp))) return rc;
-    rc = kv_gather(ctx, *b->kv, b->pages, b->pos, st->c.kv_block, (uint16_t *)tmp, false);
+    rc = kv_gather(ctx, *b->kv, b->pages, b->pos, (uint16_t *)tmp, false);
     std::vector<uint16_t> kvh(rc == GD_OK ? (size_t)natt * 2 * span : 0);
     if (rc == GD_OK) rc = gd_download(ctx, kvh.data(), tmp, kvh.size() * 2);
     gd_free(ctx, tmp);
@@ -1645,7 +1669,7 @@ int bookmark_from_host(gd_stack *st, const std::vector<uint8_t> &host, int64_t p
         if ((rc = gd_alloc(ctx, kvh.size() * 2, &tmp)) == GD_OK) {
             rc = gd_upload(ctx, tmp, kvh.data(), kvh.size() * 2);
             if (rc == GD_OK)
-                rc = kv_gather(ctx, *st->kv, b->pages, pos, st->c.kv_block, (uint16_t *)tmp, true);
+                rc = kv_gather(ctx, *st->kv, b->pages, pos, (uint16_t *)tmp, true);
             if (rc == GD_OK) rc = gd_sync(ctx);
             gd_free(ctx, tmp);
         }

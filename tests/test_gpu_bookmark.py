@@ -195,6 +195,35 @@ def test_bookmark_shares_kv_pages(ctx):
             ctx.lib.gd_stack_destroy(st2)
 
 
+def test_bookmark_restores_across_page_sizes(ctx):
+    """A bookmark of a stack with 16-position KV pages restores into a stack
+    of the same weights with 32-position pages (its positions re-paged) and
+    continues bit-identically; serialized bytes do not depend on the page
+    size."""
+    cfg, st = make_stack(ctx, seed=25)
+    st2 = bm = bm2 = None
+    try:
+        ids = (np.arange(57) * 9 % cfg["n_vocab"]).astype(np.int32)
+        first = prefill(ctx, st, ids)
+        bm = bookmark(ctx, st)
+        l1, p1 = decode_run(ctx, st, [first, 21, 22])
+        _, st2 = make_stack(ctx, seed=25, kv_block=32)
+        ctx.check(ctx.lib.gd_stack_restore(st2, bm))
+        assert kv_pages(ctx, st2)[:2] == (2, 2)            # 57 positions in pages of 32
+        l2, p2 = decode_run(ctx, st2, [first, 21, 22])
+        assert same(l1, l2) and p1 == p2
+        ctx.check(ctx.lib.gd_stack_restore(st2, bm))
+        bm2 = bookmark(ctx, st2)
+        assert serialize(ctx, st2, bm2) == serialize(ctx, st, bm)
+    finally:
+        for b in (bm, bm2):
+            if b:
+                ctx.lib.gd_bookmark_free(b)
+        ctx.lib.gd_stack_destroy(st)
+        if st2:
+            ctx.lib.gd_stack_destroy(st2)
+
+
 def test_bookmark_outlives_its_stack(ctx):
     """A bookmark holds its pool: the stack it came from can be destroyed and
     the bookmark still restores into another stack bit-identically."""
@@ -596,3 +625,34 @@ def test_gdns_rejects_malformed(ctx):
         if bm:
             ctx.lib.gd_bookmark_free(bm)
         ctx.lib.gd_stack_destroy(st)
+
+
+def test_generate_across_pool_growth(ctx):
+    """The KV pool grows (doubling) while a captured decode graph exists: the
+    graph, which holds the pools' addresses, is captured again, and 70 greedy
+    steps over the growth equal 70 chained decodes on a second stack."""
+    cfg, st = make_stack(ctx, seed=26, max_batch=16, max_ctx=128)
+    st2 = None
+    try:
+        _, st2 = make_stack(ctx, seed=26, max_batch=16, max_ctx=128)
+        ids = (np.arange(40) * 17 % cfg["n_vocab"]).astype(np.int32)
+        first = prefill(ctx, st, ids)
+        assert prefill(ctx, st2, ids) == first
+        cap0 = kv_pages(ctx, st)[2]
+        assert cap0 == 4
+        g1 = np.empty(10, np.int32)
+        g2 = np.empty(60, np.int32)
+        ctx.check(ctx.lib.gd_stack_generate(st, 10, g1.ctypes.data))
+        assert kv_pages(ctx, st)[2] == cap0                 # 50 positions: no growth yet
+        ctx.check(ctx.lib.gd_stack_generate(st, 60, g2.ctypes.data))
+        live, held, cap = kv_pages(ctx, st)
+        assert cap > cap0 and live == held == 7             # 110 positions
+        chain, t = [], first
+        for _ in range(70):
+            _, (t,) = decode_run(ctx, st2, [t])
+            chain.append(t)
+        assert list(g1) + list(g2) == chain
+    finally:
+        ctx.lib.gd_stack_destroy(st)
+        if st2:
+            ctx.lib.gd_stack_destroy(st2)
