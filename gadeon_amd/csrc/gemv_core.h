@@ -76,6 +76,10 @@ constexpr size_t LDS_BYTES = 160 * 1024 - 2048;
 // waves and 3 or 4 tiles everywhere.
 constexpr int NW = 16, P = 2;
 constexpr int CP_NT = 2;     // cache policy: non-temporal (streamed once)
+// Residual partials of the fused input that a kernel loads as one group
+// with h and w (the stack's split-K projections leave one or two); the
+// kernel is instantiated for 0 .. ND_UNROLL of them.
+constexpr int ND_UNROLL = 2;
 
 // LDS bytes of the x staging: the x planes (two for f32 x), then the block
 // sums and exponents of x.
@@ -124,7 +128,7 @@ __device__ __forceinline__ uint32_t pack_h2(float a, float b) {
 template <int XT> struct XChunk;
 template <> struct XChunk<0> { u32x4 lo, hi; };
 template <> struct XChunk<1> { f32x4 f[4]; };
-template <> struct XChunk<2> { f32x4 f[4], d[4], w[4]; };
+template <> struct XChunk<2> { f32x4 f[4], w[4], d[ND_UNROLL][4]; };
 
 // SwiGLU output: with pair_sets > 0, W is [gate; up] with pair_sets sets
 // (16 rows) in each half, a workgroup takes gate sets k .. and the matching
@@ -248,8 +252,9 @@ __device__ __forceinline__ void issue(const Task &t, const Geo &g, int it, u32x4
 // per row) in LDS, summed with the rest of the row at the end; otherwise
 // summed across the block lanes first (needs 4x less LDS, for very long K).
 // All 64 * NW threads of the workgroup must call it.
-template <int XT, bool KBP, bool F4>
+template <int XT, bool KBP, bool F4, int ND = 0>
 __device__ void run(const Task &t, int wg, uint32_t *lds) {
+    static_assert(ND >= 0 && ND <= ND_UNROLL && (XT == 2 || ND == 0), "partials: fused input only");
     constexpr int MT = 64 * NW;
     constexpr bool HL = XT == 1 && !F4;                   // x carried as f16 hi + lo
     constexpr int NJ = XT == 1 ? 4 : 3;                   // F4: e4m3 pieces of x
@@ -290,8 +295,20 @@ __device__ void run(const Task &t, int wg, uint32_t *lds) {
     const __amdgpu_buffer_rsrc_t drs =
             make_rsrc(nin.delta, nin.nd ? (uint32_t)((nin.nd - 1) * nin.dstride + K) * 4u : 0u);
     const __amdgpu_buffer_rsrc_t wrs = make_rsrc(nin.w, XT == 2 ? (uint32_t)K * 4u : 0u);
+    // Element offset of staging entry e (K: an entry past the last x block).
+    auto entry_off = [&](int e) { return e < nblk * 8 ? (e >> 3) * 128 + 16 * (e & 7) : K; };
+    // Dwords 4q .. 4q+3 of partial z of the entry at off; entries past K
+    // (off == K) must read zeros (at z * dstride + K lies the next partial),
+    // and so does a partial past nd: an offset outside the resource.
+    auto dload = [&](int off, int z, int q, bool live) {
+        return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                drs, live && off < K ? (uint32_t)((z * nin.dstride + off) * 4 + 16 * q) : 0xfffff000u,
+                0, 0));
+    };
+    // Issues the loads of entry e only (no arithmetic, so that every load of
+    // the entry is in flight before the first wait).
     auto load_x = [&](int e) {
-        const int off = e < nblk * 8 ? (e >> 3) * 128 + 16 * (e & 7) : K;   // element offset
+        const int off = entry_off(e);
         XChunk<XT> c;
         if constexpr (XT == 0) {
             c.lo = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, off * 2, 0, 0));
@@ -301,34 +318,35 @@ __device__ void run(const Task &t, int wg, uint32_t *lds) {
             for (int q = 0; q < 4; q++)
                 c.f[q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, off * 4 + 16 * q, 0, 0));
             if constexpr (XT == 2) {
+                // The first ND partials are loaded here, unconditionally and in
+                // flight with h and w (summing them as they arrive, in a loop
+                // over nd, waited for each load before issuing the next).
+                // Partials past ND are loaded where they are summed.
 #pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    c.d[q] = f32x4{0.f, 0.f, 0.f, 0.f};
-                    // Entries past K (off == K) must read zeros: at z * dstride
-                    // + K lies the next partial.
-                    for (int z = 0; z < nin.nd; z++)
-                        c.d[q] += __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                drs, off < K ? (uint32_t)((z * nin.dstride + off) * 4 + 16 * q)
-                                             : 0xfffff000u, 0, 0));
+                for (int z = 0; z < ND; z++)
+#pragma unroll
+                    for (int q = 0; q < 4; q++) c.d[z][q] = dload(off, z, q, true);
+#pragma unroll
+                for (int q = 0; q < 4; q++)
                     c.w[q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs, off * 4 + 16 * q, 0, 0));
-                }
             }
         }
         return c;
     };
-    XChunk<XT> xc = load_x(threadIdx.x);
+    // Waves with no staging entry issue no x loads: a load instruction
+    // costs the CU's texture path about as much with every lane past the
+    // end (zeros, no memory access) as with live lanes (measured: eight
+    // such b128 loads per thread added about 1 us to a launch).
+    // Every use of xc below is under the same wave-uniform condition, so the
+    // idle waves' copy stays undefined and the branch joins without copies
+    // (a zero-initialized copy made the loading waves wait for x there).
+    const bool xwave = wave * 64 < nstage;
     // The bias of this thread's row in the first pass of the row sums at the
     // end (K range 0 only), requested with x so its latency is hidden.
     const __amdgpu_buffer_rsrc_t brs = make_rsrc(t.bias, t.bias && g.bz == 0 ? (uint32_t)R * 4u : 0u);
     auto bias_at = [&](int row) {
         return __builtin_amdgcn_raw_buffer_load_b32(brs, (uint32_t)row * 4u, 0, 0);
     };
-    const uint32_t b0 = bias_at(set_lo * 16 + (threadIdx.x >> 2));
-    // Keep the x loads ahead of the tile prefetch in the instruction stream:
-    // loads complete in issue order, so x issued after the tiles would only
-    // arrive behind them.
-    __builtin_amdgcn_sched_barrier(0);
-
     // Ring slot p starts with item p * NW + wave; each later item is taken
     // from the workgroup counter when a slot frees up.  One tile goes out
     // before the staging, the rest of the ring after it, so x (needed first)
@@ -336,7 +354,29 @@ __device__ void run(const Task &t, int wg, uint32_t *lds) {
     Ring rg;
 #pragma unroll
     for (int p = 0; p < P; p++) rg.it[p] = p * NW + wave;
-    issue<F4>(t, g, rg.it[0], rg.t[0], rg.sc[0]);
+    uint32_t b0;
+    // After x (loads complete in issue order, so x issued after the tiles
+    // would only arrive behind them): the bias and the first tile.
+    auto head = [&]() {
+        b0 = bias_at(set_lo * 16 + (threadIdx.x >> 2));
+        __builtin_amdgcn_sched_barrier(0);
+        issue<F4>(t, g, rg.it[0], rg.t[0], rg.sc[0]);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // Every use of xc below is under the same wave-uniform condition, so the
+    // idle waves' copy stays undefined and the branch joins without copies
+    // (a zero-initialized copy made the loading waves wait for x there).
+    // The bias and first tile are requested inside each branch, so that
+    // work on x the compiler moves up into the loading branch still comes
+    // after them.
+    XChunk<XT> xc;
+    if (xwave) {
+        xc = load_x(threadIdx.x);
+        __builtin_amdgcn_sched_barrier(0);
+        head();
+    } else {
+        head();
+    }
     if (threadIdx.x == 0) next_item = NW * P;
 
     // Stage x: pair p = 8i + k of block b holds (x[b,16i+PA[k]], x[b,16i+PA[k]+4]) *
@@ -477,14 +517,22 @@ __device__ void run(const Task &t, int wg, uint32_t *lds) {
         // delta for the next residual add.
         __shared__ float ssr[NW];
         float ss = 0.f;
+        if (xwave) {
+            const int xoff = entry_off(threadIdx.x);
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            xc.f[q] += xc.d[q];
-            ss += xc.f[q][0] * xc.f[q][0] + xc.f[q][1] * xc.f[q][1] +
-                  xc.f[q][2] * xc.f[q][2] + xc.f[q][3] * xc.f[q][3];
+            for (int q = 0; q < 4; q++) {
+                // h + ((0 + p0) + p1 ...), the partials in order.
+                f32x4 d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int z = 0; z < ND; z++) d += xc.d[z][q];
+                for (int z = ND; z < nin.nd; z++) d += dload(xoff, z, q, true);
+                xc.f[q] += d;
+                ss += xc.f[q][0] * xc.f[q][0] + xc.f[q][1] * xc.f[q][1] +
+                      xc.f[q][2] * xc.f[q][2] + xc.f[q][3] * xc.f[q][3];
+            }
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
         }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
         if (lane == 0) ssr[wave] = ss;
         if (wg == 0 && nin.hout && threadIdx.x < nblk * 8) {
             const uint32_t ho = (uint32_t)((threadIdx.x >> 3) * 128 + 16 * (threadIdx.x & 7)) * 4u;
@@ -499,12 +547,14 @@ __device__ void run(const Task &t, int wg, uint32_t *lds) {
 #pragma unroll
         for (int w = 0; w < NW; w++) tot += ssr[w];
         const float rs = 1.0f / sqrtf(tot / (float)K + nin.eps);
+        if (xwave) {
 #pragma unroll
-        for (int q = 0; q < 4; q++)
+            for (int q = 0; q < 4; q++)
 #pragma unroll
-            for (int c = 0; c < 4; c++) xc.f[q][c] = (float)(f16)(xc.f[q][c] * rs * xc.w[q][c]);
+                for (int c = 0; c < 4; c++) xc.f[q][c] = (float)(f16)(xc.f[q][c] * rs * xc.w[q][c]);
+        }
     }
-    stage(threadIdx.x, xc);
+    if (xwave) stage(threadIdx.x, xc);
     if constexpr (XT != 2)
         for (int e = threadIdx.x + MT; e < nstage; e += MT) stage(e, load_x(e));
 #pragma unroll

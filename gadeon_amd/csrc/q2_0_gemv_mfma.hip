@@ -12,10 +12,11 @@ using gemv::NW;
 using gemv::NormIn;
 using gemv::xlds_bytes;
 
-template <int XT, bool KBP, bool F4>
+// ND: residual partials of the fused input (XT = 2) loaded with h and w.
+template <int XT, bool KBP, bool F4, int ND>
 __global__ __launch_bounds__(64 * NW) void q2_0_gemv_mfma_kernel(gemv::Task t) {
     extern __shared__ __align__(16) uint32_t lds[];
-    gemv::run<XT, KBP, F4>(t, (int)(blockIdx.y * gridDim.x + blockIdx.x), lds);
+    gemv::run<XT, KBP, F4, ND>(t, (int)(blockIdx.y * gridDim.x + blockIdx.x), lds);
 }
 
 // x staging bytes of a GEMV over nblk Q2 blocks: the fp4 kernel's where its
@@ -88,8 +89,16 @@ int launch(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, XStage xs,
     bool kbp;
     int rc = make_task(ctx, w, x, y, xs.bytes, nin, ksplit, glu, cus, bias, &t, &lds, &kbp);
     if (rc) return rc;
-    auto kern = xs.f4 ? (kbp ? q2_0_gemv_mfma_kernel<XT, true, true> : q2_0_gemv_mfma_kernel<XT, false, true>)
-                      : (kbp ? q2_0_gemv_mfma_kernel<XT, true, false> : q2_0_gemv_mfma_kernel<XT, false, false>);
+    constexpr int NDM = XT == 2 ? gemv::ND_UNROLL : 0;
+    const int nd = std::min(nin.nd, NDM);
+    auto pick = [&](auto ndc) {
+        constexpr int ND = decltype(ndc)::value;
+        return xs.f4 ? (kbp ? q2_0_gemv_mfma_kernel<XT, true, true, ND> : q2_0_gemv_mfma_kernel<XT, false, true, ND>)
+                     : (kbp ? q2_0_gemv_mfma_kernel<XT, true, false, ND> : q2_0_gemv_mfma_kernel<XT, false, false, ND>);
+    };
+    auto kern = nd == 0 ? pick(std::integral_constant<int, 0>{})
+              : nd == 1 ? pick(std::integral_constant<int, NDM >= 1 ? 1 : 0>{})
+                        : pick(std::integral_constant<int, NDM >= 2 ? 2 : 0>{});
     hipLaunchKernelGGL(kern, dim3((unsigned)t.gx, t.nz), dim3(64 * NW), lds, ctx->stream, t);
     GD_LAUNCHED(ctx, "q2_0_gemv_mfma");
     return GD_OK;
