@@ -411,11 +411,14 @@ PREFILL_T = 64     # ids in the 64-layer prefill parity chunk
 NUMERICS = {
     "prefill_gemm": "f16 activations x exact f16 (code-1)*d weights on v_mfma_f32_32x32x16_f16, "
                     "f32 accumulate",
-    "decode_gemv": "f16 x (the reference's decode GEMV reads f32 x) as e4m3 pieces with a "
-                   "per-128-block power-of-two scale (3 pieces hold an f16 exactly), fp4 "
-                   "codes on the scaled v_mfma_scale_f32_16x16x128_f8f6f4; each group of 8 "
-                   "products is summed aligned to its largest with ~13 bits kept, then f32 "
-                   "accumulate (relDiff vs f64: ~4e-6 for N(0,1) x, ~2e-4 with 3000x outliers)",
+    "decode_gemv": "x as e4m3 pieces with a per-128-block power-of-two scale: the norm-fed "
+                   "GEMVs (in_proj, gate|up, lm_head) take (h + partials) * w in f32 as 4 "
+                   "pieces (~20 bits, the reference's decode GEMV reads f32 x) and scale the "
+                   "row sums by 1/rms; the output projections (out_proj, down) take f16 x as "
+                   "3 pieces (exact); fp4 codes on the scaled v_mfma_scale_f32_16x16x128_f8f6f4; "
+                   "each group of 8 products is summed aligned to its largest with ~13 bits "
+                   "kept, then f32 accumulate (relDiff vs f64: ~4e-6 for N(0,1) x, ~2e-4 with "
+                   "3000x outliers)",
     "gdn": "f32 state and recurrence; chunked prefill products on f16 MFMA with hi/lo splits "
            "of the f32 operands (~22 bits)",
     "residual_and_norms": "f32",
@@ -463,8 +466,9 @@ def cpu_baseline_stack(ctx, ga, h, c, seconds: float) -> dict:
         ref_logits.append(ref.token(n * 7 + 1)[1])
         n += 1
     dt = (time.perf_counter() - t0) / n
-    # This build's decode numerics: GEMV inputs staged as f16 (the north
-    # star's fp16-in GEMV).  The bound holds against this oracle; the
+    # This build's decode numerics: the output projections' GEMV inputs
+    # staged as f16 (the north star's fp16-in GEMV), the norm-fed GEMVs'
+    # inputs at f32 precision.  The bound holds against this oracle; the
     # deviation from the f32-input one is reported beside it.  The bound is
     # PARITY_64: the 64-layer random-init stack amplifies rounding-level
     # differences (the oracle against itself, with layer 0's input perturbed
@@ -472,7 +476,7 @@ def cpu_baseline_stack(ctx, ga, h, c, seconds: float) -> dict:
     # layers), so two correct implementations summing in different orders
     # differ by about that much; the 4-layer parity tests hold 5e-3 / 2e-3.
     m = min(n, 4)
-    ref16 = O.Stack(c, cread, stage_f16=True, threads=threads, decode_f16=True)
+    ref16 = O.Stack(c, cread, stage_f16=True, threads=threads, decode_f16="outputs")
     ref16_logits = [ref16.token(i * 7 + 1)[1] for i in range(m)]
     log(f"cpu baseline: {n} tokens, {dt:.2f} s/token on {threads} threads; checking the GPU "
         f"decode of the same tokens ...")
@@ -486,7 +490,7 @@ def cpu_baseline_stack(ctx, ga, h, c, seconds: float) -> dict:
         rels.append(rel(logits, ref_logits[i]))
         if i < m:
             rels16.append(rel(logits, ref16_logits[i]))
-    log(f"parity: GPU vs oracle logits relDiff per token, f16 decode inputs "
+    log(f"parity: GPU vs oracle logits relDiff per token, this build's decode inputs "
         f"{['%.2e' % r for r in rels16]}; f32 decode inputs {['%.2e' % r for r in rels]}")
     if not max(rels16) < PARITY_64:
         raise SystemExit(f"bench: GPU stack logits differ from the oracle (relDiff "
@@ -518,7 +522,7 @@ def cpu_baseline_stack(ctx, ga, h, c, seconds: float) -> dict:
                       f"pp and tg run at this same rate",
             "parity": {"tokens": m, "max_rel_diff": max(rels16), "tolerance": PARITY_64,
                        "what": "GPU gd_stack_decode logits vs the oracle on the same tokens, "
-                               "64 layers, full width, f16 decode GEMV inputs on both sides",
+                               "64 layers, full width, f16 inputs into the output projections on both sides",
                        "prefill_64": {"tokens": PREFILL_T, "rel_diff": relp,
                                       "tolerance": PARITY_64,
                                       "what": f"GPU gd_stack_prefill of {PREFILL_T} ids from a "

@@ -123,8 +123,9 @@ __device__ __forceinline__ uint32_t pack_h2(float a, float b) {
 }
 
 // x values of one staging entry (16 consecutive elements of one block).
-// XT = 0: f16 x; 1: f32 x; 2: f32 residual h (+ delta) normalized in the
-// staging (x = f16(rmsnorm(h + delta) * w)), then used as f16 x.
+// XT = 0: f16 x; 1: f32 x; 2: f32 residual h (+ delta partials) and the
+// norm weight w, staged as x = (h + delta) * w at f32 precision (the row sums
+// are scaled by 1/rms(h + delta)).
 template <int XT> struct XChunk;
 template <> struct XChunk<0> { u32x4 lo, hi; };
 template <> struct XChunk<1> { f32x4 f[4]; };
@@ -256,9 +257,13 @@ template <int XT, bool KBP, bool F4, int ND = 0>
 __device__ void run(const Task &t, int wg, uint32_t *lds) {
     static_assert(ND >= 0 && ND <= ND_UNROLL && (XT == 2 || ND == 0), "partials: fused input only");
     constexpr int MT = 64 * NW;
-    constexpr bool HL = XT == 1 && !F4;                   // x carried as f16 hi + lo
-    constexpr int NJ = XT == 1 ? 4 : 3;                   // F4: e4m3 pieces of x
+    // x at f32 precision: f32 x, and the fused input's h' * w (whose 1/rms
+    // scales the row sums instead).
+    constexpr bool XF = XT != 0;
+    constexpr bool HL = XF && !F4;                        // x carried as f16 hi + lo
+    constexpr int NJ = XF ? 4 : 3;                        // F4: e4m3 pieces of x
     __shared__ __align__(16) int next_item;               // next item to take
+    __shared__ float ssr[NW];                             // XT = 2: per-wave sums of h'^2
     const Geo g = geometry(t, wg);
     const int K = t.K, R = t.R;
     const int nblk = K >> 7;
@@ -438,7 +443,7 @@ __device__ void run(const Task &t, int wg, uint32_t *lds) {
                         // f16 x: three pieces hold it exactly (bar elements
                         // 2^-14 of the block's max), so the last needs no
                         // remainder.
-                        if (XT == 1 || jj < NJ - 1) {
+                        if (XF || jj < NJ - 1) {
                             const int n = (int)w[jj];
                             const f32x2 pv = hf ? __builtin_amdgcn_cvt_pk_f32_fp8(n, true)
                                                 : __builtin_amdgcn_cvt_pk_f32_fp8(n, false);
@@ -446,12 +451,12 @@ __device__ void run(const Task &t, int wg, uint32_t *lds) {
                             b = (b - pv[1]) * 16.f;
                         }
                     }
-                    if (XT == 1) tsum += a + b;
+                    if (XF) tsum += a + b;
                 }
 #pragma unroll
                 for (int jj = 0; jj < 4; jj++) pc[jj][dw] = w[jj];
             }
-            if (XT == 1) {
+            if (XF) {
                 tsum += __shfl_xor(tsum, 1, 64);
                 tsum += __shfl_xor(tsum, 2, 64);
                 tsum += __shfl_xor(tsum, 4, 64);
@@ -467,7 +472,7 @@ __device__ void run(const Task &t, int wg, uint32_t *lds) {
                 }
                 if (i == 0 && bb < nblk) {
                     // sum of the pieces: sum x less what they leave out
-                    sx[bb] = XT == 1 ? sum - tsum * 0x1p-16f * __uint_as_float((uint32_t)(127 + eb) << 23)
+                    sx[bb] = XF ? sum - tsum * 0x1p-16f * __uint_as_float((uint32_t)(127 + eb) << 23)
                                      : sum;
                     ((int *)ex)[bb] = 127 + eb;
                 }
@@ -511,11 +516,13 @@ __device__ void run(const Task &t, int wg, uint32_t *lds) {
     // wait for x leaves the tiles in flight; further entries (K long enough
     // that (K/128 + 5) * 8 > threads) follow in a loop.
     if constexpr (XT == 2) {
-        // x = f16(rmsnorm(h + delta) * w), as a separate add + norm kernel
-        // followed by an f16 GEMV would form it; one entry per thread (the
-        // host checks), entries past K load zeros.  Workgroup 0 keeps h +
-        // delta for the next residual add.
-        __shared__ float ssr[NW];
+        // RMSNorm(h') * w with h' = h + delta: x = h' * w is staged as it is
+        // (f32, four pieces) and the row sums are scaled by 1/rms(h') at the
+        // end, so no barrier for the sum of squares stands between the x
+        // loads and the staging: each wave's share goes to ssr here and is
+        // read after the staging barrier.  One entry per thread (the host
+        // checks), entries past K load zeros.  Workgroup 0 keeps h' for the
+        // next residual add.
         float ss = 0.f;
         if (xwave) {
             const int xoff = entry_off(threadIdx.x);
@@ -542,16 +549,9 @@ __device__ void run(const Task &t, int wg, uint32_t *lds) {
                 __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, xc.f[q]), hrs,
                                                        ho + 16 * q, 0, 0);
         }
-        __syncthreads();
-        float tot = 0.f;
-#pragma unroll
-        for (int w = 0; w < NW; w++) tot += ssr[w];
-        const float rs = 1.0f / sqrtf(tot / (float)K + nin.eps);
         if (xwave) {
 #pragma unroll
-            for (int q = 0; q < 4; q++)
-#pragma unroll
-                for (int c = 0; c < 4; c++) xc.f[q][c] = (float)(f16)(xc.f[q][c] * rs * xc.w[q][c]);
+            for (int q = 0; q < 4; q++) xc.f[q] *= xc.w[q];
         }
     }
     if (xwave) stage(threadIdx.x, xc);
@@ -728,6 +728,15 @@ __device__ void run(const Task &t, int wg, uint32_t *lds) {
         return a + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(a), 0x4E, 0xF, 0xF, false));
     };
     const GluOut &glu = t.glu;
+    // XT = 2: the row sums of W (h' * w) times 1/rms(h'), the sum of squares
+    // added over the waves in wave order.
+    float rs = 1.f;
+    if constexpr (XT == 2) {
+        float tot = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) tot += ssr[w];
+        rs = 1.0f / sqrtf(tot / (float)K + nin.eps);
+    }
     const __amdgpu_buffer_rsrc_t yrs = make_rsrc(y, (uint32_t)R * 4u);
     const __amdgpu_buffer_rsrc_t ors = make_rsrc(glu.out, glu.pair_sets ? (uint32_t)glu.pair_sets * 32u : 0u);
     const int nrow = (glu.pair_sets ? npair : g.nset_wg) * 16;
@@ -736,15 +745,15 @@ __device__ void run(const Task &t, int wg, uint32_t *lds) {
         const bool ok = i < nrow;
         const int c = ok ? i >> 4 : 0, r = i & 15;
         if (glu.pair_sets) {
-            const float gv = combine(ok ? quarter(c, r, q) : 0.f);
-            const float u = combine(ok ? quarter(npair + c, r, q) : 0.f);
+            const float gv = rs * combine(ok ? quarter(c, r, q) : 0.f);
+            const float u = rs * combine(ok ? quarter(npair + c, r, q) : 0.f);
             if (ok && q == 0)
                 __builtin_amdgcn_raw_buffer_store_b16(gd_f2h(gd_silu(gv) * u), ors,
                                                       (uint32_t)(set_lo * 16 + i) * 2u, 0, 0);
         } else {
             // Rows past R read bias zero (outside the resource).
             const uint32_t bv = base == 0 ? b0 : bias_at(set_lo * 16 + i);
-            const float v = combine(ok ? quarter(c, r, q) : 0.f) + __uint_as_float(bv);
+            const float v = rs * combine(ok ? quarter(c, r, q) : 0.f) + __uint_as_float(bv);
             if (ok && q == 0 && set_lo * 16 + i < R)
                 __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), yrs,
                                                       (uint32_t)(set_lo * 16 + i) * 4u, 0, 0);

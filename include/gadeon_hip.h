@@ -182,10 +182,12 @@ int gd_q2_0_gemv_split(gd_ctx *ctx, const gd_q2w *w, const void *x, int x_dtype,
 
 /* Decode GEMV with the residual add and RMSNorm that precede it fused into
  * the x staging: h' = h + sum of nd partials delta + z * delta_stride (nd = 0
- * or delta null: none), x = f16(h' * w_norm / sqrt(mean(h'^2) + eps)),
- * y = W x.  hout (may be null, must not alias h) receives h'.  Same result
- * as gd_add + gd_rmsnorm(.., GD_F16, ..) + gd_q2_0_gemv (MetalEnc.addInplace
- * + rmsnorm + gemv, MetalEnc.swift:213-236, 572-597, 78-99) in one launch
+ * or delta null: none), x = h' * w_norm / sqrt(mean(h'^2) + eps), y = W x,
+ * with x taken at f32 precision (about 20 bits: W (h' * w_norm) formed from
+ * it, then scaled by the 1/rms), as the reference's decode GEMV reads f32 x.
+ * hout (may be null, must not alias h) receives h'.  The result of
+ * gd_add + gd_rmsnorm(.., GD_F32, ..) + gd_q2_0_gemv (MetalEnc.addInplace +
+ * rmsnorm + gemv, MetalEnc.swift:213-236, 572-597, 78-99) in one launch
  * instead of three.  h, delta, w_norm and hout are f32 [K], 16-byte aligned
  * (delta_stride a multiple of 4); K <= 15744.  With glu_out not null, W is
  * [gate; up] (R = 2 ff rows, ff a multiple of 16) and glu_out[r] =

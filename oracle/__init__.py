@@ -252,7 +252,7 @@ class OrStack(C.Structure):
 _PROTOS["or_stack_token"] = (None, [C.POINTER(OrStack), _i, _i, _vp, _vp])
 _PROTOS["or_stack_prefill"] = (None, [C.POINTER(OrStack), _vp, _i, _i, _vp, _vp])
 
-STAGE_MV, STAGE_KV = 1, 2       # OR_STAGE_* of gd_oracle.h
+STAGE_MV, STAGE_KV, STAGE_MVO = 1, 2, 4       # OR_STAGE_* of gd_oracle.h
 
 
 class Stack:
@@ -263,8 +263,11 @@ class Stack:
 
     With stage_f16, `prefill` rounds every mat-vec input to f16 (the reference
     GPU prefill GEMM stages half tiles, Kernels.metal:428) and `token` does not
-    (its decode GEMV reads f32 x, Kernels.metal:32-40) unless decode_f16 is
-    set; cached K/V are always rounded (half KV pages).  With untied the
+    (its decode GEMV reads f32 x, Kernels.metal:32-40) unless decode_f16 says
+    so: True rounds every decode mat-vec input, "outputs" only those of the
+    output projections (ssm_out, attn_output, ffn_down: this build's decode,
+    whose norm-fed GEMVs read their input at f32 precision); cached K/V are
+    always rounded (half KV pages).  With untied the
     lm_head is tensors(-1, "output"), else the token embedding (Model.swift:145).
     cfg["dense"] (default 0) selects the dense qwen3 lineage: every layer
     attention, plain q, ungated output, the pre-FFN norm named ffn_norm
@@ -274,10 +277,13 @@ class Stack:
           "att": ("attn_q", "attn_k", "attn_v", "attn_output")}
 
     def __init__(self, cfg: dict, tensors, stage_f16: bool = True, threads: int = 8,
-                 decode_f16: bool = False, untied: bool = False):
+                 decode_f16: bool | str = False, untied: bool = False):
         self.cfg = cfg
         self.stage_prefill = (STAGE_MV | STAGE_KV) if stage_f16 else 0
-        self.stage_decode = (STAGE_KV | (STAGE_MV if decode_f16 else 0)) if stage_f16 else 0
+        if decode_f16 not in (False, True, "outputs"):
+            raise ValueError(f"decode_f16: {decode_f16!r}")
+        dec = STAGE_MVO if decode_f16 == "outputs" else STAGE_MV if decode_f16 else 0
+        self.stage_decode = (STAGE_KV | dec) if stage_f16 else 0
         self.keep = []
         n = cfg["n_layer"]
         self.layers = (OrStackLayer * n)()

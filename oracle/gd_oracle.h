@@ -120,6 +120,9 @@ typedef struct or_stack {
 
 #define OR_STAGE_MV 1   /* mat-vec inputs (the prefill GEMM's half tiles, Kernels.metal:428) */
 #define OR_STAGE_KV 2   /* cached K/V (half KV pages, Kernels.metal:1446-1457) */
+#define OR_STAGE_MVO 4  /* the inputs of the output projections only (ssm_out, attn_output,
+                           ffn_down): this build's decode, whose norm-fed mat-vecs read
+                           their inputs at f32 precision and the others f16 */
 
 /* BonsaiEngine.forward for one token at position pos: hidden_out[n_embd] is
  * the post-final-norm hidden; logits_out[n_vocab] may be NULL. */

@@ -29,19 +29,25 @@ static void stage(int on, const float *x, float *y, int64_t n) {
     for (int64_t i = 0; i < n; i++) y[i] = on ? or_h2f(or_f2h(x[i])) : x[i];
 }
 
+/* Whether a mat-vec input is rounded to f16: every one with OR_STAGE_MV, an
+ * output projection's (outp) with OR_STAGE_MVO as well. */
+static int stage_mv(const or_stack *st, int outp) {
+    return (st->stage_f16 & OR_STAGE_MV) || (outp && (st->stage_f16 & OR_STAGE_MVO));
+}
+
 static void matvec(const or_stack *st, const uint8_t *w, int64_t K, int64_t M, const float *x,
-                   float *out) {
+                   float *out, int outp) {
     float *xs = (float *)malloc(sizeof(float) * K);
-    stage(st->stage_f16 & OR_STAGE_MV, x, xs, K);
+    stage(stage_mv(st, outp), x, xs, K);
     or_q2_0_matvec(w, K, M, xs, out, st->threads);
     free(xs);
 }
 
 /* T mat-vecs: X [T][K] -> out [T][M]. */
 static void matmat(const or_stack *st, const uint8_t *w, int64_t K, int64_t M, int64_t T,
-                   const float *X, float *out) {
+                   const float *X, float *out, int outp) {
     float *xs = (float *)malloc(sizeof(float) * K * T);
-    stage(st->stage_f16 & OR_STAGE_MV, X, xs, K * T);
+    stage(stage_mv(st, outp), X, xs, K * T);
     or_q2_0_matmat(w, K, M, T, xs, out, st->threads);
     free(xs);
 }
@@ -76,21 +82,21 @@ static void gdn_layer(or_stack *st, or_stack_layer *L, int T, const float *nrm, 
     float *bp = malloc(sizeof(float) * nV * T), *ap = malloc(sizeof(float) * nV * T);
     float *o = malloc(sizeof(float) * valDim * T);
     if (T == 1) {
-        matvec(st, L->wqkv, E, convDim, nrm, qkv);
-        matvec(st, L->wgate, E, valDim, nrm, z);
-        matvec(st, L->wbeta, E, nV, nrm, bp);
-        matvec(st, L->walpha, E, nV, nrm, ap);
+        matvec(st, L->wqkv, E, convDim, nrm, qkv, 0);
+        matvec(st, L->wgate, E, valDim, nrm, z, 0);
+        matvec(st, L->wbeta, E, nV, nrm, bp, 0);
+        matvec(st, L->walpha, E, nV, nrm, ap, 0);
     } else {
-        matmat(st, L->wqkv, E, convDim, T, nrm, qkv);
-        matmat(st, L->wgate, E, valDim, T, nrm, z);
-        matmat(st, L->wbeta, E, nV, T, nrm, bp);
-        matmat(st, L->walpha, E, nV, T, nrm, ap);
+        matmat(st, L->wqkv, E, convDim, T, nrm, qkv, 0);
+        matmat(st, L->wgate, E, valDim, T, nrm, z, 0);
+        matmat(st, L->wbeta, E, nV, T, nrm, bp, 0);
+        matmat(st, L->walpha, E, nV, T, nrm, ap, 0);
     }
     for (int t = 0; t < T; t++)
         gdn_token(st, L, qkv + (int64_t)t * convDim, z + (int64_t)t * valDim, bp + (int64_t)t * nV,
                   ap + (int64_t)t * nV, o + (int64_t)t * valDim);
-    if (T == 1) matvec(st, L->ssm_out, valDim, E, o, out);
-    else matmat(st, L->ssm_out, valDim, E, T, o, out);
+    if (T == 1) matvec(st, L->ssm_out, valDim, E, o, out, 1);
+    else matmat(st, L->ssm_out, valDim, E, T, o, out, 1);
     free(qkv); free(z); free(bp); free(ap); free(o);
 }
 
@@ -150,19 +156,19 @@ static void attn_layer(or_stack *st, or_stack_layer *L, int T, const float *nrm,
     float *qFull = malloc(sizeof(float) * qf * T), *k = malloc(sizeof(float) * kvDim * T);
     float *v = malloc(sizeof(float) * kvDim * T), *ao = malloc(sizeof(float) * hd * nH * T);
     if (T == 1) {
-        matvec(st, L->wq, E, qf, nrm, qFull);
-        matvec(st, L->wk, E, kvDim, nrm, k);
-        matvec(st, L->wv, E, kvDim, nrm, v);
+        matvec(st, L->wq, E, qf, nrm, qFull, 0);
+        matvec(st, L->wk, E, kvDim, nrm, k, 0);
+        matvec(st, L->wv, E, kvDim, nrm, v, 0);
     } else {
-        matmat(st, L->wq, E, qf, T, nrm, qFull);
-        matmat(st, L->wk, E, kvDim, T, nrm, k);
-        matmat(st, L->wv, E, kvDim, T, nrm, v);
+        matmat(st, L->wq, E, qf, T, nrm, qFull, 0);
+        matmat(st, L->wk, E, kvDim, T, nrm, k, 0);
+        matmat(st, L->wv, E, kvDim, T, nrm, v, 0);
     }
     for (int t = 0; t < T; t++)
         attn_token(st, L, qFull + (int64_t)t * qf, k + (int64_t)t * kvDim, v + (int64_t)t * kvDim,
                    pos0 + t, ao + (int64_t)t * hd * nH);
-    if (T == 1) matvec(st, L->wo, hd * nH, E, ao, out);
-    else matmat(st, L->wo, hd * nH, E, T, ao, out);
+    if (T == 1) matvec(st, L->wo, hd * nH, E, ao, out, 1);
+    else matmat(st, L->wo, hd * nH, E, T, ao, out, 1);
     free(qFull); free(k); free(v); free(ao);
 }
 
@@ -187,20 +193,20 @@ static void forward(or_stack *st, const int *tokens, int T, int pos0, float *hid
         for (int t = 0; t < T; t++)
             or_rmsnorm(x + (int64_t)t * E, L->post_norm, nrm + (int64_t)t * E, E, st->eps);
         if (T == 1) {                                                       /* ffn */
-            matvec(st, L->ffn_gate, E, FF, nrm, gt);
-            matvec(st, L->ffn_up, E, FF, nrm, up);
+            matvec(st, L->ffn_gate, E, FF, nrm, gt, 0);
+            matvec(st, L->ffn_up, E, FF, nrm, up, 0);
         } else {
-            matmat(st, L->ffn_gate, E, FF, T, nrm, gt);
-            matmat(st, L->ffn_up, E, FF, T, nrm, up);
+            matmat(st, L->ffn_gate, E, FF, T, nrm, gt, 0);
+            matmat(st, L->ffn_up, E, FF, T, nrm, up, 0);
         }
         for (int64_t i = 0; i < (int64_t)FF * T; i++) gt[i] = or_silu(gt[i]) * up[i];
-        if (T == 1) matvec(st, L->ffn_down, FF, E, gt, a);
-        else matmat(st, L->ffn_down, FF, E, T, gt, a);
+        if (T == 1) matvec(st, L->ffn_down, FF, E, gt, a, 1);
+        else matmat(st, L->ffn_down, FF, E, T, gt, a, 1);
         for (int64_t i = 0; i < (int64_t)E * T; i++) x[i] += a[i];
     }
     or_rmsnorm(x + (int64_t)(T - 1) * E, st->out_norm, hidden_out, E, st->eps);
     if (logits_out)
-        matvec(st, st->head ? st->head : st->embd, E, st->n_vocab, hidden_out, logits_out);
+        matvec(st, st->head ? st->head : st->embd, E, st->n_vocab, hidden_out, logits_out, 0);
     free(x); free(nrm); free(a); free(gt); free(up);
 }
 

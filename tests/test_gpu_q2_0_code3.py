@@ -74,8 +74,8 @@ def test_gemv_norm_code3(ctx, K, R, glu):
     d = O.lcg_normal(K, 92, 0.0, 1.0)
     wn = O.lcg_normal(K, 93, 1.0, 0.2)
     dh, dd, dwn, dho = ctx.put(h), ctx.put(d), ctx.put(wn), ctx.alloc(K * 4)
-    x16 = O.rmsnorm((h + d).astype(np.float32)[None], wn, eps)[0].astype(np.float16)
-    y = O.q2_0_matvec(blocks, K, R, x16.astype(np.float32), threads=8)
+    x = O.rmsnorm((h + d).astype(np.float32)[None], wn, eps)[0]
+    y = O.q2_0_matvec(blocks, K, R, x, threads=8)
     if glu:
         ff = R // 2
         dO = ctx.alloc(ff * 2)
@@ -87,7 +87,7 @@ def test_gemv_norm_code3(ctx, K, R, glu):
     else:
         dy = ctx.alloc(R * 4)
         ctx.gd_q2_0_gemv_norm(C.byref(w), dh, dd, 1, 0, dwn, eps, dho, dy, None)
-        assert rel_diff(ctx.get(dy, R, np.float32), y) < 1e-3
+        assert rel_diff(ctx.get(dy, R, np.float32), y) < 1e-4
         ctx.free(dy)
     for p in (dh, dd, dwn, dho):
         ctx.free(p)

@@ -354,3 +354,32 @@ def test_prefill_is_token_serial():
             assert np.array_equal(a.layer_state(il, "ssm_state"), b.layer_state(il, "ssm_state"))
         # one more decode token from both
         assert np.array_equal(a.token(5)[1], b.token(5)[1])
+
+
+def test_decode_staging_outputs_mode():
+    """decode_f16="outputs" rounds only the inputs of the output projections
+    (ssm_out, attn_output, ffn_down) to f16.  With those three weights zero,
+    their outputs are zero whatever their inputs, so the mode must give the
+    f32 decode's logits bit for bit, while rounding every mat-vec input
+    (decode_f16=True) must not; with them nonzero it must differ from both."""
+    cfg = dict(n_layer=4, n_embd=256, n_ff=384, n_head=4, n_head_kv=2, head_dim=128, n_rot=64,
+               rope_base=1e7, eps=1e-6, n_vocab=300, attn_interval=2, d_state=128, n_k_head=1,
+               n_v_head=2, d_conv=4, max_ctx=40)
+    ids = (np.arange(9) * 13 % cfg["n_vocab"]).astype(np.int32)
+    for zero in (("ssm_out", "attn_output", "ffn_down"), ()):
+        Tg = make_gdn_tensors(cfg, zero=tuple(z for z in zero if z != "attn_output"))
+        Ta = make_tensors(dict(cfg, n_vocab=cfg["n_vocab"]), zero=zero)
+        tensors = lambda layer, name: Tg[name] if name in Tg else Ta[name]
+        out = {}
+        for mode in (False, True, "outputs"):
+            s = O.Stack(cfg, tensors, stage_f16=True, threads=2, decode_f16=mode)
+            s.prefill(ids)
+            out[mode] = np.concatenate([s.token(int(t))[1] for t in (3, 7, 11)])
+        if zero:
+            assert np.array_equal(out["outputs"], out[False])
+            assert not np.array_equal(out[True], out[False])
+        else:
+            assert not np.array_equal(out["outputs"], out[False])
+            assert not np.array_equal(out["outputs"], out[True])
+    with pytest.raises(ValueError):
+        O.Stack(cfg, tensors, decode_f16="inputs")
