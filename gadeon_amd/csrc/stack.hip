@@ -186,8 +186,8 @@ __global__ __launch_bounds__(64 * GS_W) void k_gdn_step(
         int off_a, float qScale, float eps) {
     __shared__ float kq[2][HD];                  // k, q after conv + SiLU
     __shared__ float vs[HD];
-    __shared__ float red[GS_W][2][64];
-    __shared__ float scal[2];
+    __shared__ float red[GS_W][2][64];           // S^T k partials
+    __shared__ float red2[GS_W][2][64];          // readout partials
     __shared__ float gate[2];                    // beta, gamma
     const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -230,14 +230,16 @@ __global__ __launch_bounds__(64 * GS_W) void k_gdn_step(
         gate[1] = expf(gd_softplus(proj[off_a + h] + dt[h]) * aNeg[h]);
     }
     __syncthreads();
-    // Waves 0/1 reduce |k|^2 and |q|^2.
-    if (wave < 2) {
-        const float a = kq[wave][lane], c = kq[wave][lane + 64];
-        const float ss = gd_wave_sum(a * a + c * c);
-        if (lane == 0) scal[wave] = 1.0f / sqrtf(ss + eps);
+    // Every wave reduces |k|^2 and |q|^2 itself (the same sums in the same
+    // order in every wave), which saves a barrier.
+    float rk, rq;
+    {
+        const float a = kq[0][lane], c = kq[0][lane + 64];
+        rk = 1.0f / sqrtf(gd_wave_sum(a * a + c * c) + eps);
+        const float e = kq[1][lane], f = kq[1][lane + 64];
+        rq = 1.0f / sqrtf(gd_wave_sum(e * e + f * f) + eps);
     }
-    __syncthreads();
-    const float rk = scal[0], rq = scal[1], beta = gate[0], gam = gate[1];
+    const float beta = gate[0], gam = gate[1];
     float sk0 = 0.0f, sk1 = 0.0f;
 #pragma unroll
     for (int r = 0; r < GS_R; r++) {
@@ -260,7 +262,6 @@ __global__ __launch_bounds__(64 * GS_W) void k_gdn_step(
     sk0 *= rk;
     sk1 *= rk;
     const float d0 = beta * (vs[lane] - sk0) * rk, d1 = beta * (vs[lane + 64] - sk1) * rk;
-    __syncthreads();                             // red[] is reused below
     float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
     for (int r = 0; r < GS_R; r++) {
@@ -273,15 +274,15 @@ __global__ __launch_bounds__(64 * GS_W) void k_gdn_step(
         Sh[(int64_t)i * HD + lane] = s0[r];
         Sh[(int64_t)i * HD + lane + 64] = s1[r];
     }
-    red[wave][0][lane] = a0;
-    red[wave][1][lane] = a1;
+    red2[wave][0][lane] = a0;
+    red2[wave][1][lane] = a1;
     __syncthreads();
     if (wave == 0) {
         float o0 = 0.0f, o1 = 0.0f;
 #pragma unroll
         for (int w = 0; w < GS_W; w++) {
-            o0 += red[w][0][lane];
-            o1 += red[w][1][lane];
+            o0 += red2[w][0][lane];
+            o1 += red2[w][1][lane];
         }
         o0 *= rq * qScale;
         o1 *= rq * qScale;
