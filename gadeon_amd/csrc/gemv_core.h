@@ -152,8 +152,9 @@ struct NormIn {
 
 // One GEMV: W (codes, scales) [R][K], x, y; the work split (sets per
 // workgroup `per`, K split into nz ranges of ksteps steps, gx workgroups per
-// range: workgroup wg takes sets (wg % gx) * per .. of range wg / gx, and
-// workgroups wg >= gx * nz have none).
+// range: workgroup (bx, bz) takes sets bx * per .. of range bz).  lmag[0] and
+// lmag[1]: ceil(2^32 / L) for the steps L of a range before the last and of
+// the last (0 where L <= 1), the item -> set quotient by multiply-high.
 struct Task {
     const uint8_t *codes;
     const uint16_t *scales;
@@ -161,9 +162,33 @@ struct Task {
     float *y;
     const float *bias;       // added to the rows of K range 0 (null: none)
     int K, R, nsets, per, ksteps, nz, gx;
+    uint32_t lmag[2];
     NormIn nin;
     GluOut glu;
 };
+
+// ceil(2^32 / L) for 1 < L <= 128 (0 otherwise): with it, i / L is
+// umulhi(i, magic) exactly for i < 2^16.
+__host__ __device__ inline uint32_t item_magic(int L) {
+    return L <= 1 ? 0u : (uint32_t)((0x100000000ull + (unsigned)L - 1) / (unsigned)L);
+}
+
+// DPP lane moves within a row of 16 lanes.
+template <int CTRL> __device__ __forceinline__ float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E;            // quad_perm (1,0,3,2), (2,3,0,1)
+constexpr int DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140;  // lane 7-i of 8, 15-i of 16
+
+// op over the 8 lanes of each aligned group of 8, every lane getting the
+// result: the two quad exchanges leave each quad's value in all its lanes,
+// so the half-row mirror (lane i takes lane 7 - i, in the other quad) adds
+// the other quad's value as an exchange with lane i ^ 4 would.
+template <class Op> __device__ __forceinline__ float group8(float v, Op op) {
+    v = op(v, dpp<DPP_XOR1>(v));
+    v = op(v, dpp<DPP_XOR2>(v));
+    return op(v, dpp<DPP_HALF_MIRROR>(v));
+}
 
 // The register ring of a wave: P tiles with their scales and item numbers.
 struct Ring {
@@ -187,13 +212,12 @@ struct Geo {
     int bz;
 };
 
-__device__ __forceinline__ Geo geometry(const Task &t, int wg) {
+__device__ __forceinline__ Geo geometry(const Task &t, int bx, int bz) {
     Geo g;
     const int nblk = t.K >> 7;
     g.steps = (nblk + 3) >> 2;
     g.bgroups = (nblk + 15) >> 4;
-    const int bx = wg % t.gx;
-    g.bz = wg / t.gx;
+    g.bz = bz;
     // K split z = bz: steps [s0, s1) of every set.  Item i is step s0 + i % L
     // of set i / L (set-major).
     g.s0 = g.bz * t.ksteps;
@@ -210,8 +234,8 @@ __device__ __forceinline__ Geo geometry(const Task &t, int wg) {
     g.total = g.nset_wg * g.L;                                         // items
     g.up_shift = t.glu.pair_sets ? t.glu.pair_sets - g.npair : 0;
     // Item i is set i / L: the quotient by multiply-high (exact for i < 2^16
-    // and L <= 128, which the host guarantees).
-    g.Lmag = g.L <= 1 ? 0u : (uint32_t)((0x100000000ull + g.L - 1) / g.L);
+    // and L <= 128, which the host guarantees), the magic from the host.
+    g.Lmag = t.lmag[g.bz == t.nz - 1 ? 1 : 0];
     return g;
 }
 
@@ -247,14 +271,14 @@ __device__ __forceinline__ void issue(const Task &t, const Geo &g, int it, u32x4
     sc = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(srs, pick(si, dead | other), 0, 0));
 }
 
-// Runs task t's share of workgroup wg.  lds: the dynamic LDS (x staging,
+// Runs task t's share of workgroup (bx, bz).  lds: the dynamic LDS (x staging,
 // then the item partials).  XT: 0 = f16 x, 1 = f32 x (hi + lo split), 2 =
 // normalized residual (see XChunk).  KBP: item partials kept per Q2 block (4
 // per row) in LDS, summed with the rest of the row at the end; otherwise
 // summed across the block lanes first (needs 4x less LDS, for very long K).
 // All 64 * NW threads of the workgroup must call it.
 template <int XT, bool KBP, bool F4, int ND = 0>
-__device__ void run(const Task &t, int wg, uint32_t *lds) {
+__device__ void run(const Task &t, int bx, int bz, uint32_t *lds) {
     static_assert(ND >= 0 && ND <= ND_UNROLL && (XT == 2 || ND == 0), "partials: fused input only");
     constexpr int MT = 64 * NW;
     // x at f32 precision: f32 x, and the fused input's h' * w (whose 1/rms
@@ -264,7 +288,7 @@ __device__ void run(const Task &t, int wg, uint32_t *lds) {
     constexpr int NJ = XF ? 4 : 3;                        // F4: e4m3 pieces of x
     __shared__ __align__(16) int next_item;               // next item to take
     __shared__ float ssr[NW];                             // XT = 2: per-wave sums of h'^2
-    const Geo g = geometry(t, wg);
+    const Geo g = geometry(t, bx, bz);
     const int K = t.K, R = t.R;
     const int nblk = K >> 7;
     // LDS: x planes, block b at dword XB*b (64 pair dwords + 4 of padding, so
@@ -410,12 +434,8 @@ __device__ void run(const Task &t, int wg, uint32_t *lds) {
                 sum += f[q][j];
                 amax = fmaxf(amax, fabsf(f[q][j]));
             }
-        sum += __shfl_xor(sum, 1, 64);
-        sum += __shfl_xor(sum, 2, 64);
-        sum += __shfl_xor(sum, 4, 64);
-        amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-        amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-        amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+        sum = group8(sum, [](float a, float b) { return a + b; });
+        amax = group8(amax, [](float a, float b) { return fmaxf(a, b); });
         if constexpr (F4) {
             // x = 2^e (p0 + p1/16 + p2/256 [+ p3/4096]), e4m3 pieces with
             // max|x| 2^-e in [128, 256): p0 = e4m3(x 2^-e), each later piece
@@ -457,9 +477,7 @@ __device__ void run(const Task &t, int wg, uint32_t *lds) {
                 for (int jj = 0; jj < 4; jj++) pc[jj][dw] = w[jj];
             }
             if (XF) {
-                tsum += __shfl_xor(tsum, 1, 64);
-                tsum += __shfl_xor(tsum, 2, 64);
-                tsum += __shfl_xor(tsum, 4, 64);
+                tsum = group8(tsum, [](float a, float b) { return a + b; });
             }
             if (e < nstage) {
                 u32x4 *dst = (u32x4 *)(xsb + bb * F4_BLK + 64 * i);
@@ -537,11 +555,17 @@ __device__ void run(const Task &t, int wg, uint32_t *lds) {
                 ss += xc.f[q][0] * xc.f[q][0] + xc.f[q][1] * xc.f[q][1] +
                       xc.f[q][2] * xc.f[q][2] + xc.f[q][3] * xc.f[q][3];
             }
-#pragma unroll
-            for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+            // The wave's sum: each row of 16 lanes by DPP, then the four
+            // rows (lane 0 keeps it).
+            ss += dpp<DPP_XOR1>(ss);
+            ss += dpp<DPP_XOR2>(ss);
+            ss += dpp<DPP_HALF_MIRROR>(ss);
+            ss += dpp<DPP_MIRROR>(ss);
+            auto row = [&](int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ss), l)); };
+            ss = (row(0) + row(16)) + (row(32) + row(48));
         }
         if (lane == 0) ssr[wave] = ss;
-        if (wg == 0 && nin.hout && threadIdx.x < nblk * 8) {
+        if (bx == 0 && bz == 0 && nin.hout && threadIdx.x < nblk * 8) {
             const uint32_t ho = (uint32_t)((threadIdx.x >> 3) * 128 + 16 * (threadIdx.x & 7)) * 4u;
             const __amdgpu_buffer_rsrc_t hrs = make_rsrc(nin.hout, (uint32_t)K * 4u);
 #pragma unroll

@@ -16,7 +16,7 @@ using gemv::xlds_bytes;
 template <int XT, bool KBP, bool F4, int ND>
 __global__ __launch_bounds__(64 * NW) void q2_0_gemv_mfma_kernel(gemv::Task t) {
     extern __shared__ __align__(16) uint32_t lds[];
-    gemv::run<XT, KBP, F4, ND>(t, (int)(blockIdx.y * gridDim.x + blockIdx.x), lds);
+    gemv::run<XT, KBP, F4, ND>(t, (int)blockIdx.x, (int)blockIdx.y, lds);
 }
 
 // x staging bytes of a GEMV over nblk Q2 blocks: the fp4 kernel's where its
@@ -73,7 +73,9 @@ int make_task(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, size_t xlds
                         sp.per * rows_per_set * sp.ksteps < (1 << 16),
                "gd_q2_0_gemv: K=%lld R=%lld does not fit", (long long)K, (long long)R);
     *t = gemv::Task{(const uint8_t *)w->codes, (const uint16_t *)w->scales, x, y, bias, (int)K, (int)R,
-                    (int)nsets, (int)sp.per, sp.ksteps, sp.nz, (int)sp.grid, nin, glu};
+                    (int)nsets, (int)sp.per, sp.ksteps, sp.nz, (int)sp.grid,
+                    {gemv::item_magic(sp.ksteps), gemv::item_magic(steps - (sp.nz - 1) * sp.ksteps)},
+                    nin, glu};
     *lds_out = lds;
     *kbp = sp.kbp;
     return GD_OK;
