@@ -206,11 +206,34 @@ __device__ __forceinline__ float gd_softplus(float x) {
     return fmaxf(x, 0.0f) + log1pf(expf(-fabsf(x)));
 }
 
-// Sum over the 64 lanes of a wave; every lane gets the total.
+// DPP lane moves within a row of 16 lanes (no LDS round trip, unlike a
+// general shuffle): quad_perm (1,0,3,2) and (2,3,0,1) exchange with lane
+// i ^ 1 and i ^ 2; the half-row mirror takes lane 7 - i of each 8, the row
+// mirror lane 15 - i of each 16.
+template <int CTRL> __device__ __forceinline__ float gd_dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+constexpr int GD_DPP_XOR1 = 0xB1, GD_DPP_XOR2 = 0x4E, GD_DPP_HALF_MIRROR = 0x141,
+              GD_DPP_MIRROR = 0x140;
+
+// Sum over each row of 16 lanes, every lane of the row getting it: after the
+// quad exchanges each quad's lanes hold the same value, so the half-row
+// mirror pairs each lane with one holding the other quad's sum, and the row
+// mirror likewise for the other half-row.  The whole wave must be active.
+__device__ __forceinline__ float gd_row_sum(float v) {
+    v += gd_dpp<GD_DPP_XOR1>(v);
+    v += gd_dpp<GD_DPP_XOR2>(v);
+    v += gd_dpp<GD_DPP_HALF_MIRROR>(v);
+    return v + gd_dpp<GD_DPP_MIRROR>(v);
+}
+
+// Sum over the 64 lanes of a wave, every lane getting the total: the row
+// sums, then the four rows (r0 + r1) + (r2 + r3).  The whole wave must be
+// active.
 __device__ __forceinline__ float gd_wave_sum(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
-    return v;
+    v = gd_row_sum(v);
+    auto row = [&](int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l)); };
+    return (row(0) + row(16)) + (row(32) + row(48));
 }
 
 // Sum over a block of `nthreads` (multiple of 64, <= 1024); `red` is LDS of

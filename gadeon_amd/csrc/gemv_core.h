@@ -173,21 +173,14 @@ __host__ __device__ inline uint32_t item_magic(int L) {
     return L <= 1 ? 0u : (uint32_t)((0x100000000ull + (unsigned)L - 1) / (unsigned)L);
 }
 
-// DPP lane moves within a row of 16 lanes.
-template <int CTRL> __device__ __forceinline__ float dpp(float v) {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
-}
-constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E;            // quad_perm (1,0,3,2), (2,3,0,1)
-constexpr int DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140;  // lane 7-i of 8, 15-i of 16
-
 // op over the 8 lanes of each aligned group of 8, every lane getting the
 // result: the two quad exchanges leave each quad's value in all its lanes,
 // so the half-row mirror (lane i takes lane 7 - i, in the other quad) adds
 // the other quad's value as an exchange with lane i ^ 4 would.
 template <class Op> __device__ __forceinline__ float group8(float v, Op op) {
-    v = op(v, dpp<DPP_XOR1>(v));
-    v = op(v, dpp<DPP_XOR2>(v));
-    return op(v, dpp<DPP_HALF_MIRROR>(v));
+    v = op(v, gd_dpp<GD_DPP_XOR1>(v));
+    v = op(v, gd_dpp<GD_DPP_XOR2>(v));
+    return op(v, gd_dpp<GD_DPP_HALF_MIRROR>(v));
 }
 
 // The register ring of a wave: P tiles with their scales and item numbers.
@@ -555,14 +548,7 @@ __device__ void run(const Task &t, int bx, int bz, uint32_t *lds) {
                 ss += xc.f[q][0] * xc.f[q][0] + xc.f[q][1] * xc.f[q][1] +
                       xc.f[q][2] * xc.f[q][2] + xc.f[q][3] * xc.f[q][3];
             }
-            // The wave's sum: each row of 16 lanes by DPP, then the four
-            // rows (lane 0 keeps it).
-            ss += dpp<DPP_XOR1>(ss);
-            ss += dpp<DPP_XOR2>(ss);
-            ss += dpp<DPP_HALF_MIRROR>(ss);
-            ss += dpp<DPP_MIRROR>(ss);
-            auto row = [&](int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ss), l)); };
-            ss = (row(0) + row(16)) + (row(32) + row(48));
+            ss = gd_wave_sum(ss);
         }
         if (lane == 0) ssr[wave] = ss;
         if (bx == 0 && bz == 0 && nin.hout && threadIdx.x < nblk * 8) {
