@@ -189,6 +189,7 @@ __global__ __launch_bounds__(64 * GS_W) void k_gdn_step(
     __shared__ float red[GS_W][2][64];           // S^T k partials
     __shared__ float red2[GS_W][2][64];          // readout partials
     __shared__ float gate[2];                    // beta, gamma
+    __shared__ float nsq[4];                     // |q|^2, |k|^2 halves
     const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     float *Sh = S + (int64_t)h * HD * HD;
@@ -225,20 +226,16 @@ __global__ __launch_bounds__(64 * GS_W) void k_gdn_step(
         const float y = conv(part * keyDim + h * HD + i);
         if (part < 2) kq[1 - part][i] = y;
         else vs[i] = y;
+        if (wave < 4) {       // q (waves 0, 1) and k (2, 3): this half's sum of squares
+            const float ss = gd_wave_sum(y * y);
+            if (lane == 0) nsq[wave] = ss;
+        }
     } else if (tid == 3 * HD) {
         gate[0] = gd_sigmoid(proj[off_b + h]);
         gate[1] = expf(gd_softplus(proj[off_a + h] + dt[h]) * aNeg[h]);
     }
     __syncthreads();
-    // Every wave reduces |k|^2 and |q|^2 itself (the same sums in the same
-    // order in every wave), which saves a barrier.
-    float rk, rq;
-    {
-        const float a = kq[0][lane], c = kq[0][lane + 64];
-        rk = 1.0f / sqrtf(gd_wave_sum(a * a + c * c) + eps);
-        const float e = kq[1][lane], f = kq[1][lane + 64];
-        rq = 1.0f / sqrtf(gd_wave_sum(e * e + f * f) + eps);
-    }
+    const float rk = 1.0f / sqrtf((nsq[2] + nsq[3]) + eps);
     const float beta = gate[0], gam = gate[1];
     float sk0 = 0.0f, sk1 = 0.0f;
 #pragma unroll
@@ -284,6 +281,7 @@ __global__ __launch_bounds__(64 * GS_W) void k_gdn_step(
             o0 += red2[w][0][lane];
             o1 += red2[w][1][lane];
         }
+        const float rq = 1.0f / sqrtf((nsq[0] + nsq[1]) + eps);
         o0 *= rq * qScale;
         o1 *= rq * qScale;
         const float ss = gd_wave_sum(o0 * o0 + o1 * o1);
