@@ -62,18 +62,6 @@ __global__ void k_rope_table(float2 *tab, int n, int n_rot, float base) {
     tab[i] = make_float2(cosf(ang), sinf(ang));
 }
 
-// Partial NEOX rope of dim i (< n_rot) of a head whose values are `mine` (dim
-// i) and `pv` (its partner i +- n_rot/2), at position pos (Kern.ropeNeox,
-// Kernels.swift:66-84).
-__device__ __forceinline__ float rope_dim(int i, float mine, float pv, int n_rot, float base,
-                                          int pos, const float2 *rtab, int rtab_n) {
-    const int half = n_rot / 2;
-    const int jj = i < half ? i : i - half;
-    const float2 cs = rope_cs(jj, n_rot, base, pos, rtab, rtab_n);
-    const float c = cs.x, sn = cs.y;
-    return i < half ? mine * c - pv * sn : pv * sn + mine * c;
-}
-
 // ---------------------------------------------------------------- prefill prep
 
 // Attention prep (prefill), one wave per (token, head): q heads take their q
@@ -84,7 +72,7 @@ __device__ __forceinline__ float rope_dim(int i, float mine, float pv, int n_rot
 // A block is one token and PREP_HEADS of its heads (PREP_WAVES waves, heads
 // wave, wave + PREP_WAVES, ..): the rotation's cos and sin depend only on the
 // token, so the block forms them once into LDS (the same powf / cosf / sinf
-// per pair index as rope_dim) instead of once per head.  pos_ptr[0] is the
+// per pair index as rope_cs) instead of once per head.  pos_ptr[0] is the
 // first token's position (the KV slot), pos_ptr[1] the rope shift: tokens
 // rotate at position + shift (MetalEngine.swift:432-435).
 constexpr int PREP_WAVES = 4, PREP_HEADS = 12;
@@ -356,7 +344,9 @@ __global__ __launch_bounds__(256) void k_attn_prefill(
 // Each wave takes whole keys j = lo + NWD sp + w + STEP i with a lane holding
 // HD/64 consecutive dims, keeping an online-softmax partial; the block
 // merges its waves and writes (max, sum, acc[HD]) for the split; the combine
-// kernel merges the splits (Attention.swift:108-134).
+// kernel merges the splits (Attention.swift:108-134).  A wave keeps the K
+// and V of its next KB keys in flight (a register ring), their page-table
+// entries one round ahead of them, so a key waits for neither.
 template <int HD, bool FUSED>
 __global__ __launch_bounds__(2 * HD) void k_attn_decode(
         const float *src, int qs, const float *q_norm, const float *k_norm, uint16_t *kc,
@@ -364,20 +354,17 @@ __global__ __launch_bounds__(2 * HD) void k_attn_decode(
         int H, int HKV, int block, float scale, int n_rot, float base, float eps,
         const float2 *rtab, int rtab_n) {
     constexpr int NT = 2 * HD, NWD = NT / 64, DPL = HD / 64, WPH = HD / 64;
-    constexpr int STEP = DSPLIT * NWD;
+    constexpr int STEP = DSPLIT * NWD, KB = 8;
     __shared__ float wm[NWD], wl[NWD];
     __shared__ float wacc[NWD][HD];
     __shared__ float nrm[2][HD], rot[2][HD], vnew[HD], red[NWD];
     const int h = blockIdx.x, sp = blockIdx.y, t = threadIdx.x;
-    const int lane = t & 63, w = t >> 6;
+    const int lane = t & 63, w = __builtin_amdgcn_readfirstlane(t >> 6);
     const int kvh = h / (H / HKV), kvDim = HKV * HD;
     // Keys read from the cache: [lo, pos) for the stack (pos = the new
     // token's position, taken from its registers), [lo, T) otherwise.
     const int pos = FUSED ? *pos_ptr : T;
     const bool has_pos = FUSED && sp == (pos / NWD) % DSPLIT;   // wave pos % NWD takes key pos
-    auto kv_base = [&](int j) {
-        return kv_slot(page_table, j, block) * kvDim + kvh * HD + DPL * lane;
-    };
     // A lane's DPL f16 dims of one key: one dword (HD 128) or two (HD 256).
     using U = typename std::conditional<DPL == 2, uint32_t, u32x2>::type;
     auto ld = [&](const uint16_t *p) { return *(const U *)p; };
@@ -385,15 +372,49 @@ __global__ __launch_bounds__(2 * HD) void k_attn_decode(
         if constexpr (DPL == 2) return u;
         else return u[i];
     };
-    // The first cached key of this wave is requested before the q/k work
-    // below, which does not depend on it.
-    int j = lo + sp * NWD + w;
-    U kn{}, vn{};
-    if (j < pos) {
-        const int64_t b0 = kv_base(j);
-        kn = ld(kc + b0);
-        vn = ld(vc + b0);
-    }
+    // Cached keys of this wave: j0 + STEP i, i < nk.  Every load below is
+    // unconditional (the compiler waits exactly only for straight-line
+    // loads): a key past the last reads position jlast instead, whose page
+    // exists (the new token's, or the last cached key's), and is not used.
+    const int j0 = lo + sp * NWD + w;
+    const int nk = j0 < pos ? (pos - 1 - j0) / STEP + 1 : 0;
+    const int jlast = FUSED ? pos : T - 1;
+    auto kpos = [&](int i) {
+        const int jj = j0 + i * STEP;
+        return jj < pos ? jj : jlast;
+    };
+    // Cache slots of keys i0 .. i0 + KB - 1, lane l holding key i0 + l % KB:
+    // its page-table entry (a load) and its position in the page.
+    struct Slots { int pe, off; };
+    auto entries = [&](int i0) {
+        const int kp = kpos(i0 + (lane & (KB - 1)));
+        return Slots{page_table[kp / block], kp % block};
+    };
+    // K and V of key i, whose slot is in lane i % KB of sl.
+    auto fetch = [&](int i, const Slots &sl, U &kk, U &vv) {
+        const int l = i & (KB - 1);
+        const int64_t slot = (int64_t)__builtin_amdgcn_readlane(sl.pe, l) * block +
+                             __builtin_amdgcn_readlane(sl.off, l);
+        const int64_t b = slot * kvDim + kvh * HD + DPL * lane;
+        kk = ld(kc + b);
+        vv = ld(vc + b);
+    };
+    // The first KB keys' slots go out first; after the q/k inputs, their K
+    // and V, then the next KB keys' slots (the order of the loop below, so
+    // that no loaded register is copied at its end).  Nothing the q/k work
+    // waits for is requested after them: completion is in order, so it would
+    // wait for the keys too.
+    const Slots pg0 = entries(0);
+    __builtin_amdgcn_sched_barrier(0);
+    Slots pg;
+    U kr[KB], vr[KB];
+    auto prime = [&]() {
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int s = 0; s < KB; s++) fetch(s, pg0, kr[s], vr[s]);
+        pg = entries(KB);
+        __builtin_amdgcn_sched_barrier(0);
+    };
     if constexpr (FUSED) {
         // q of head h (hf = 0) and k of kv head kvh (hf = 1): RMS norm over
         // the head, then the partial NEOX rope, as k_attn_prep.
@@ -402,6 +423,15 @@ __global__ __launch_bounds__(2 * HD) void k_attn_decode(
         const float x = hf == 0 ? src[h * qs + i] : src[H2 + kvh * HD + i];
         const float nw = hf == 0 ? q_norm[i] : k_norm[i];
         const float vx = src[H2 + HKV * HD + kvh * HD + i];
+        // The rotation at position + shift (pos_ptr[1]) from its table row
+        // when the table holds it (a dummy read of src otherwise), and the
+        // page entry of the new token's position, which is cached at pos.
+        const int half = n_rot / 2, rpos = pos + pos_ptr[1];
+        const int jj = i < half ? i : (i < n_rot ? i - half : 0);
+        const bool in_tab = rtab && rpos >= 0 && rpos < rtab_n;
+        const float2 tcs = in_tab ? rtab[(int64_t)rpos * half + jj] : *(const float2 *)src;
+        const int pe_new = page_table[pos / block];
+        prime();
         const float sq = gd_wave_sum(x * x);
         if (lane == 0) red[w] = sq;
         __syncthreads();
@@ -412,21 +442,23 @@ __global__ __launch_bounds__(2 * HD) void k_attn_decode(
         float y = x * sc * nw;
         nrm[hf][i] = y;
         __syncthreads();
-        const int half = n_rot / 2;
-        // Rotated at position + shift (pos_ptr[1]), cached at position.
-        if (i < n_rot)
-            y = rope_dim(i, nrm[hf][i], i < half ? nrm[hf][i + half] : nrm[hf][i - half], n_rot,
-                         base, pos + pos_ptr[1], rtab, rtab_n);
+        if (i < n_rot) {
+            const float2 cs = in_tab ? tcs : rope_cs(jj, n_rot, base, rpos, nullptr, 0);
+            const float mine = nrm[hf][i], pv = i < half ? nrm[hf][i + half] : nrm[hf][i - half];
+            y = i < half ? mine * cs.x - pv * cs.y : pv * cs.y + mine * cs.x;
+        }
         rot[hf][i] = y;
         if (hf == 1) vnew[i] = vx;
         __syncthreads();
         if (hf == 1 && has_pos && h % (H / HKV) == 0) {
-            const int64_t slot = kv_slot(page_table, pos, block);
+            const int64_t slot = (int64_t)pe_new * block + pos % block;
             kc[slot * kvDim + kvh * HD + i] = gd_f2h(y);
             vc[slot * kvDim + kvh * HD + i] = gd_f2h(vnew[i]);
         }
     } else {
-        if (t < HD) rot[0][t] = src[(int64_t)h * HD + t];
+        const float qx = t < HD ? src[(int64_t)h * HD + t] : 0.f;
+        prime();
+        if (t < HD) rot[0][t] = qx;
         __syncthreads();
     }
     float qv[DPL], a[DPL];
@@ -450,18 +482,21 @@ __global__ __launch_bounds__(2 * HD) void k_attn_decode(
             a[e] = fmaf(p, gd_h2f((uint16_t)((word(vv, e >> 1) >> (16 * (e & 1))) & 0xffff)), a[e] * al);
         m = mn;
     };
-    // Cached keys: the next key's page-table entry and K/V values are
-    // requested before this key's arithmetic, so each key waits only for
-    // loads issued a key earlier.
-    for (; j < pos; j += STEP) {
-        const U kk = kn, vv = vn;
-        if (j + STEP < pos) {
-            const int64_t bn = kv_base(j + STEP);
-            kn = ld(kc + bn);
-            vn = ld(vc + bn);
+    // Cached keys, KB a round: each slot's key, then the key a round later
+    // into the slot, then the slots of the round after next.  The last round
+    // requests nothing.
+    int i = 0;
+    for (; i + KB < nk; i += KB) {
+#pragma unroll
+        for (int s = 0; s < KB; s++) {
+            consume(kr[s], vr[s]);
+            fetch(i + KB + s, pg, kr[s], vr[s]);
         }
-        consume(kk, vv);
+        pg = entries(i + 2 * KB);
     }
+#pragma unroll
+    for (int s = 0; s < KB; s++)
+        if (i + s < nk) consume(kr[s], vr[s]);
     if constexpr (FUSED) {
         // Key pos, from this block's own copy (f16, as cached).
         if (has_pos && w == pos % NWD) {
