@@ -281,6 +281,17 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 4
         if constexpr (EX) read_ax(0);
 #pragma unroll
         for (int j = 0; j < 8; j++) {
+            // Issue priority falls as the wave advances through the block
+            // (3, 3, 2, 2, 1, 1, 0, 0): a wave that lags the other wave of its
+            // SIMD takes the issue slots first, so both reach the barrier
+            // together instead of the older running ahead.
+            switch (j) {
+                case 0: __builtin_amdgcn_s_setprio(3); break;
+                case 2: __builtin_amdgcn_s_setprio(2); break;
+                case 4: __builtin_amdgcn_s_setprio(1); break;
+                case 6: __builtin_amdgcn_s_setprio(0); break;
+                default: break;
+            }
             // The reads go out PD steps ahead; the fence keeps the compiler
             // from sinking them next to their use, where the MFMA would
             // wait for the LDS round trip.
