@@ -97,6 +97,7 @@ __host__ __device__ inline size_t xlds_bytes_f4(int nblk) {
 }
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef short s16x2 __attribute__((ext_vector_type(2)));
 
 // Operand dword m holds codes (PA[m], PA[m] + 4) of w (the device order:
 // code i < 8 at bit 4i, 8 + i at 4i + 2, so codes a and a + 4 share a
@@ -438,8 +439,15 @@ __device__ void run(const Task &t, int bx, int bz, uint32_t *lds) {
             // pieces, so d (sum c x - sum x) cancels where c = 1.
             const int fe = (int)((__float_as_uint(amax) >> 23) & 0xff) - 127;
             const int eb = amax > 0.f ? min(120, max(-114, fe - 7)) : 0;
-            const float down = __uint_as_float((uint32_t)(127 - eb) << 23);   // 2^-eb
-            float tsum = 0.f;      // f32 x: what the pieces leave out, x 16^NJ
+            // Piece jj is e4m3(r / 2^(eb - 4 jj)) of what the earlier pieces
+            // leave, r, and leaves r - piece * 2^(eb - 4 jj) (exact): the
+            // scaled conversions (which divide by, and multiply back by, the
+            // power of two of their f32 scale; measured) do the scaling, so
+            // r stays in x's own units.
+            float sj[4];
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) sj[jj] = __uint_as_float((uint32_t)(127 + eb - 4 * jj) << 23);
+            float tsum = 0.f;      // f32 x: what the pieces leave out
             u32x4 pc[4];
 #pragma unroll
             for (int dw = 0; dw < 4; dw++) {
@@ -447,21 +455,21 @@ __device__ void run(const Task &t, int bx, int bz, uint32_t *lds) {
 #pragma unroll
                 for (int hf = 0; hf < 2; hf++) {
                     // Bytes 2hf, 2hf+1 of dword dw: elements 4dw + 2hf, +1.
-                    float a = f[dw][2 * hf] * down, b = f[dw][2 * hf + 1] * down;
+                    float a = f[dw][2 * hf], b = f[dw][2 * hf + 1];
 #pragma unroll
                     for (int jj = 0; jj < NJ; jj++) {
-                        const int o = (int)w[jj];
-                        w[jj] = (uint32_t)(hf ? __builtin_amdgcn_cvt_pk_fp8_f32(a, b, o, true)
-                                              : __builtin_amdgcn_cvt_pk_fp8_f32(a, b, o, false));
+                        const s16x2 o = __builtin_bit_cast(s16x2, w[jj]);
+                        w[jj] = __builtin_bit_cast(uint32_t,
+                                                   hf ? __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(o, a, b, sj[jj], true)
+                                                      : __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(o, a, b, sj[jj], false));
                         // f16 x: three pieces hold it exactly (bar elements
                         // 2^-14 of the block's max), so the last needs no
                         // remainder.
                         if (XF || jj < NJ - 1) {
-                            const int n = (int)w[jj];
-                            const f32x2 pv = hf ? __builtin_amdgcn_cvt_pk_f32_fp8(n, true)
-                                                : __builtin_amdgcn_cvt_pk_f32_fp8(n, false);
-                            a = (a - pv[0]) * 16.f;
-                            b = (b - pv[1]) * 16.f;
+                            const f32x2 pv = hf ? __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(w[jj], sj[jj], true)
+                                                : __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(w[jj], sj[jj], false);
+                            a -= pv[0];
+                            b -= pv[1];
                         }
                     }
                     if (XF) tsum += a + b;
@@ -483,8 +491,7 @@ __device__ void run(const Task &t, int bx, int bz, uint32_t *lds) {
                 }
                 if (i == 0 && bb < nblk) {
                     // sum of the pieces: sum x less what they leave out
-                    sx[bb] = XF ? sum - tsum * 0x1p-16f * __uint_as_float((uint32_t)(127 + eb) << 23)
-                                     : sum;
+                    sx[bb] = XF ? sum - tsum : sum;
                     ((int *)ex)[bb] = 127 + eb;
                 }
             }
