@@ -74,6 +74,7 @@ _PROTOS = {
     "gd_q2_0_gemm": (_i, [_vp, _Q2WP, _i64, _vp, _i, _vp, _i]),
     "gd_q2_0_gemm_plan": (_i, [_vp, _Q2WP, _i64, _vp, _i, _vp, _i, _i, _i, _i, _i]),
     "gd_q2_0_gemm_plan17": (_i, [_vp, _Q2WP, _i64, _vp, _i, _vp, _i, _i]),
+    "gd_q2_0_gemm_plan_tail": (_i, [_vp, _Q2WP, _i64, _vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp]),
     "gd_q2_0_dequant_rows": (_i, [_vp, _Q2WP, _vp, _i64, _vp]),
     "gd_split_q_gate": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i64]),
     "gd_rope": (_i, [_vp, _vp, _i, _i, _i, _f, _i, _i64]),

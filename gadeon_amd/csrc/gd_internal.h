@@ -63,6 +63,11 @@ gd_gemm_plan gd_gemm_choose(gd_ctx *ctx, int64_t T, int64_t K, int64_t R, int x_
 // split > 1: y_dtype f32 and Y holds split * T * R partials, summed by the caller.
 int gd_gemm_launch(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, int x_dtype, void *Y,
                    int y_dtype, const gd_gemm_plan &p);
+// An unsplit plain plan over whole row tiles (rows below *tail_r0) plus the
+// rows past them as K-split f32 partials tailY[z][t][r - *tail_r0] in the
+// same launch (*tail_nz: at most, then the count made; summed by the caller).
+int gd_gemm_launch_tail(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, float *Y,
+                        const gd_gemm_plan &p, float *tailY, int *tail_nz, int *tail_r0);
 // SwiGLU GEMM: w = [gate; up] (2 * ff rows), f16 X [T][K] -> f16 out [T][ff].
 // tile17: -1 the planner's choice, 1 one launch of the 17-fragment (4, 2, 8)
 // tile, 0 the planner's choice among the others.

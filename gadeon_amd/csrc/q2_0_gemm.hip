@@ -109,11 +109,18 @@ template <int MT, int NT, int NW, int EX> struct Stage {
 // ((8,1) and (4,2) with NW = 4), whose 128 accumulators and operands do not
 // fit two waves' registers: one wave per SIMD, as the planner's tile times
 // assume.
+// Tail (tail_nz > 0; plain f32 output, one split, no EX): the units above
+// cover the rows below tail_r0 (whole row tiles); the workgroups past them
+// (8 per blocks) take the rows tail_r0 .. R-1 (fewer than a tile's), one per
+// token tile and K split of tail_bps blocks, and write f32 partials
+// tailY[z][t][r - tail_r0], so that a short remainder of rows does not cost
+// a whole extra round of full-K units.
 template <int MT, int NT, int NW, int YT, int EX = 0>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 4 && MT * NT == 8 ? 1 : 2))) void q2_0_gemm_kernel(
         const uint8_t *__restrict__ codes, const uint16_t *__restrict__ scales,
         const void *__restrict__ Xv, void *__restrict__ Yv, int T, int K, int R, int bps,
-        int nrt, int nz, int per, int glu_ff, int glu_r0, int glu_end) {
+        int nrt, int nz, int per, int glu_ff, int glu_r0, int glu_end, float *__restrict__ tailY,
+        int tail_r0, int tail_nz, int tail_bps) {
     static_assert(!EX || (MT == 4 && NT == 2 && NW == 8 && YT == 0), "EX: 4 x 2 x 8 SwiGLU tiles");
     using St = Stage<MT, NT, NW, EX>;
     constexpr int BT = St::BT;
@@ -123,16 +130,31 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 4
     // are numbered token-tile-major and dealt to XCDs in contiguous runs of
     // `per`, so each XCD's L2 holds one or two token tiles of X rather than
     // all of it.
-    const int u = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
-    if (u >= (int)((T + BT - 1) / BT) * nz * nrt) return;
-    const int rt = u % nrt, z = (u / nrt) % nz, tt = u / (nrt * nz);
+    const int main_grid = 8 * per;
+    const bool tail = (int)blockIdx.x >= main_grid;
+    int rt, z, tt;
+    if (!tail) {
+        const int u = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+        if (u >= (int)((T + BT - 1) / BT) * nz * nrt) return;
+        rt = u % nrt;
+        z = (u / nrt) % nz;
+        tt = u / (nrt * nz);
+    } else {
+        const int tu = (int)blockIdx.x - main_grid;
+        rt = 0;
+        z = tu % tail_nz;
+        tt = tu / tail_nz;
+    }
+    // Output rows of this unit start at row0 (tail: tail_r0), in rows of ldy
+    // values (tail: its own narrow partial planes).
+    const int row0 = tail ? tail_r0 : 0, ldy = tail ? R - tail_r0 : R;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int li = lane & 31, lh = lane >> 5;
     const int t0 = tt * BT;
     // This wave's first row (SwiGLU: first gate row, 16 per fragment).
     const int rw = glu_ff ? glu_r0 + rt * (16 * St::NF) + wave * (16 * NT)
-                          : rt * (St::NF * 32) + wave * (NT * 32);
+                          : row0 + rt * (St::NF * 32) + wave * (NT * 32);
     // EX: the extra fragment's first gate row, and this wave's share of it.
     // (SwiGLU: 16 gate rows and their up rows; plain: 32 rows.)
     const int xr = glu_ff ? glu_r0 + rt * (16 * St::NF) + 16 * NW * NT : rt * (St::NF * 32) + 32 * NW * NT;
@@ -140,8 +162,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 4
     const int nblk = K >> 7;
     const int csteps = (nblk + 3) >> 2;
     const int bgroups = (nblk + 15) >> 4;
-    const int b_begin = z * bps;
-    const int b_end = min(b_begin + bps, nblk);
+    const int b_begin = z * (tail ? tail_bps : bps);
+    const int b_end = min(b_begin + (tail ? tail_bps : bps), nblk);
 
     // Buffer resources: X from token t0, codes and scales from this wave's
     // first 16-row group.  Tokens past T and row groups past R lie beyond
@@ -410,18 +432,19 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 4
         return;
     }
     constexpr uint32_t ESZ = YT ? 2 : 4;
+    uint8_t *ybuf = tail ? (uint8_t *)tailY : (uint8_t *)Yv;
     const __amdgpu_buffer_rsrc_t yrs =
-            gd_rsrc((uint8_t *)Yv + ((size_t)z * T * R + (size_t)t0 * R) * ESZ, (uint32_t)rows_t * R * ESZ);
+            gd_rsrc(ybuf + ((size_t)z * T * ldy + (size_t)t0 * ldy) * ESZ, (uint32_t)rows_t * ldy * ESZ);
 #pragma unroll
     for (int n = 0; n < NT; n++) {
         const int r = rw + n * 32 + li;
         if (r >= R) continue;
-        const uint32_t ybase = ((uint32_t)(4 * lh) * R + r) * ESZ;
+        const uint32_t ybase = ((uint32_t)(4 * lh) * ldy + (r - row0)) * ESZ;
 #pragma unroll
         for (int m = 0; m < MT; m++)
 #pragma unroll
             for (int v = 0; v < 16; v++) {
-                const uint32_t so = (uint32_t)(m * 32 + 8 * (v >> 2) + (v & 3)) * R * ESZ;
+                const uint32_t so = (uint32_t)(m * 32 + 8 * (v >> 2) + (v & 3)) * ldy * ESZ;
                 if (YT == 0)
                     // __float_as_uint: hipcc turns a __builtin_bit_cast of a
                     // vector element into element 0 of the vector.
@@ -478,7 +501,7 @@ __global__ __launch_bounds__(256) void q2_0_gemm_reduce(const float *__restrict_
 }
 
 typedef void (*gemm_fn)(const uint8_t *, const uint16_t *, const void *, void *, int, int, int,
-                        int, int, int, int, int, int, int);
+                        int, int, int, int, int, int, int, float *, int, int, int);
 
 template <int MT, int NT, int NW>
 gemm_fn pick(int yt) {
@@ -641,8 +664,36 @@ int gd_gemm_launch(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, int x
     const int64_t units = (int64_t)gd_blocks(T, p.mt * 32) * nz * nrt;
     const int per = (int)((units + 7) / 8);
     hipLaunchKernelGGL(f, dim3(8 * per), dim3(64 * p.nw), 0, ctx->stream, (const uint8_t *)w->codes,
-                       (const uint16_t *)w->scales, X, Y, (int)T, K, R, bps, nrt, nz, per, 0, 0, 0);
+                       (const uint16_t *)w->scales, X, Y, (int)T, K, R, bps, nrt, nz, per, 0, 0, 0,
+                       (float *)nullptr, 0, 0, 0);
     GD_LAUNCHED(ctx, "q2_0_gemm");
+    return GD_OK;
+}
+
+// gd_gemm_launch of an unsplit plain plan over the rows below r0 = R rounded
+// down to the plan's row tiles, with rows r0 .. R-1 as tail units of the same
+// launch: K split into *tail_nz (in: at most; out: the count made) f32
+// partials tailY[z][t][r - r0], which the caller sums; Y's rows from r0 on
+// are not written.  When R is a few rows past whole tiles, the units of those
+// rows would otherwise run the whole K as an extra round on a few CUs.
+int gd_gemm_launch_tail(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, float *Y,
+                        const gd_gemm_plan &p, float *tailY, int *tail_nz, int *tail_r0) {
+    const int K = (int)w->K, R = (int)w->R, nblk = K / 128;
+    const int rows = p.nw * p.nt * 32, r0 = R / rows * rows;
+    gemm_fn f = kernel_for(p.mt, p.nt, p.nw, 0);
+    GD_REQUIRE(ctx, f && p.split == 1 && !p.ex && r0 < R && tailY && tail_nz && *tail_nz >= 1 &&
+                        R < (1 << 22),
+               "gd_gemm_launch_tail: bad plan %d,%d,%d,%d for R=%d", p.mt, p.nt, p.split, p.nw, R);
+    const int tbps = (nblk + *tail_nz - 1) / *tail_nz;
+    const int tnz = (nblk + tbps - 1) / tbps;
+    const int ttiles = (int)gd_blocks(T, p.mt * 32), nrt = r0 / rows;
+    const int per = (int)(((int64_t)ttiles * nrt + 7) / 8);
+    hipLaunchKernelGGL(f, dim3(8 * per + ttiles * tnz), dim3(64 * p.nw), 0, ctx->stream,
+                       (const uint8_t *)w->codes, (const uint16_t *)w->scales, X, (void *)Y, (int)T, K,
+                       R, nblk, nrt, 1, per, 0, 0, 0, tailY, r0, tnz, tbps);
+    GD_LAUNCHED(ctx, "q2_0_gemm_tail");
+    *tail_nz = tnz;
+    *tail_r0 = r0;
     return GD_OK;
 }
 
@@ -718,7 +769,8 @@ int gd_gemm_glu(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, uint16_t
         const int per = (int)((units + 7) / 8);
         hipLaunchKernelGGL((q2_0_gemm_kernel<4, 2, 8, 0, 1>), dim3(8 * per), dim3(64 * 8), 0,
                            ctx->stream, (const uint8_t *)w->codes, (const uint16_t *)w->scales, X,
-                           (void *)out, (int)T, K, R, nblk, nrt, 1, per, ff, 0, ff);
+                           (void *)out, (int)T, K, R, nblk, nrt, 1, per, ff, 0, ff, (float *)nullptr, 0, 0,
+                           0);
         GD_LAUNCHED(ctx, "q2_0_gemm_glu");
         return GD_OK;
     }
@@ -738,7 +790,7 @@ int gd_gemm_glu(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, uint16_t
         const int per = (int)((units + 7) / 8);
         hipLaunchKernelGGL(f, dim3(8 * per), dim3(64 * pt.sh->nw), 0, ctx->stream,
                            (const uint8_t *)w->codes, (const uint16_t *)w->scales, X, dst, (int)T,
-                           K, R, bps, nrt, pt.nz, per, ff, pt.r0, pt.r1);
+                           K, R, bps, nrt, pt.nz, per, ff, pt.r0, pt.r1, (float *)nullptr, 0, 0, 0);
         GD_LAUNCHED(ctx, "q2_0_gemm_glu");
         if (pt.nz > 1) {
             hipLaunchKernelGGL(q2_0_glu_reduce, dim3(gd_blocks(T * ncol, 256)), dim3(256), 0,
@@ -839,6 +891,21 @@ extern "C" int gd_q2_0_gemm_plan17(gd_ctx *ctx, const gd_q2w *w, int64_t T, cons
                "gd_q2_0_gemm_plan17: f16 Y needs a K split (the tile writes f32)");
     const gd_gemm_plan p{4, 2, split, 8, 1};
     return gemm_run(ctx, w, T, X, x_dtype, Y, y_dtype, &p);
+}
+
+extern "C" int gd_q2_0_gemm_plan_tail(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X,
+                                     float *Y, int mt, int nt, int nw, int tail_split,
+                                     float *tailY, int *tail_nz, int *tail_r0) {
+    GD_CHECK_CTX(ctx);
+    int rc = gd_check_q2w(ctx, w, "gd_q2_0_gemm_plan_tail");
+    if (rc) return rc;
+    GD_REQUIRE(ctx, X && Y && tailY && tail_nz && tail_r0 && ((uintptr_t)X & 15) == 0,
+               "gd_q2_0_gemm_plan_tail: null or misaligned pointer");
+    GD_REQUIRE(ctx, T > 0 && T < (1 << 30) && w->K <= (1 << 22) && tail_split >= 1 && tail_split <= 16,
+               "gd_q2_0_gemm_plan_tail: T=%lld K=%lld split=%d out of range", (long long)T,
+               (long long)w->K, tail_split);
+    *tail_nz = tail_split;
+    return gd_gemm_launch_tail(ctx, w, T, X, Y, gd_gemm_plan{mt, nt, 1, nw}, tailY, tail_nz, tail_r0);
 }
 
 extern "C" int gd_q2_0_gemm_swiglu(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X,

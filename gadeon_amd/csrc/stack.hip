@@ -80,12 +80,15 @@ __device__ __forceinline__ float psum(const float *proj, int64_t pstride, int64_
 }
 static_assert(CT >= 3, "only the first task of a row may reach back into the ring");
 // proj holds NP split-K partials of the in_proj output, pstride floats
-// apart, summed as they are read.
+// apart, summed as they are read.  tailp (if not null): the gate columns
+// (off_b .. and off_a .., at or past tail_c0) are tail_np partials
+// tailp[z][n][col - tail_c0] instead, tail_ps floats apart, rows of tail_ld.
 template <int NP>
 __global__ __launch_bounds__(256) void k_gdn_conv_prefill(
         const float *proj, int64_t stride, int64_t pstride, float *ring, const float *cw, float *out,
         int convDim, int nqk_rows, int N, float eps, int off_b, int off_a, const float *dt,
-        const float *aNeg, float *beta, float *g, int nV) {
+        const float *aNeg, float *beta, float *g, int nV, const float *tailp, int tail_c0,
+        int tail_ld, int tail_np, int64_t tail_ps) {
     const int nrows = convDim / HD;
     const int64_t task = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     const int ngroups = (N + CT - 1) / CT;
@@ -158,12 +161,21 @@ __global__ __launch_bounds__(256) void k_gdn_conv_prefill(
         }
     }
     if (r == 0) {
+        // Gate input column col of token n, its partials added in split order.
+        auto gin = [&](int n, int col) {
+            if (tailp) {
+                const float *tp = tailp + (int64_t)n * tail_ld + (col - tail_c0);
+                float a = tp[0];
+                for (int p = 1; p < tail_np; p++) a += tp[p * tail_ps];
+                return a;
+            }
+            return psum<NP>(proj, pstride, (int64_t)n * stride + col);
+        };
         for (int i = lane; i < CT * nV; i += 64) {
             const int n = n0 + i / nV, hh = i % nV;
             if (n >= N) break;
-            const int64_t rb = (int64_t)n * stride;
-            beta[(int64_t)n * nV + hh] = gd_sigmoid(psum<NP>(proj, pstride, rb + off_b + hh));
-            g[(int64_t)n * nV + hh] = gd_softplus(psum<NP>(proj, pstride, rb + off_a + hh) + dt[hh]) * aNeg[hh];
+            beta[(int64_t)n * nV + hh] = gd_sigmoid(gin(n, off_b + hh));
+            g[(int64_t)n * nV + hh] = gd_softplus(gin(n, off_a + hh) + dt[hh]) * aNeg[hh];
         }
     }
 }
@@ -505,6 +517,11 @@ struct KvPool {
     }
 };
 
+// K splits of the GDN in_proj's tail rows (the gate columns past its whole
+// row tiles, gd_gemm_launch_tail): 40 blocks of K at the stack's width make
+// 5-block units, short enough to hide beside the full-K units.
+constexpr int TAIL_SPLITS = 8;
+
 struct gd_stack {
     gd_ctx *ctx = nullptr;
     gd_stack_config c{};
@@ -606,6 +623,9 @@ int forward(gd_stack *st, int N, bool decode) {
         // in_proj output: proj, or np split-K partials of it at pin.
         const float *pin = st->proj;
         int np = 1;
+        // Gate columns left as tail partials by the in_proj GEMM (prefill).
+        const float *tailp = nullptr;
+        int tail_np = 0, tail_r0 = 0;
         if (decode) {
             if (il == 0)
                 R_(gd_gemv_mfma_norm(ctx, &ly.in_proj, st->x, nullptr, 0, 0, ly.attn_norm, eps,
@@ -617,11 +637,23 @@ int forward(gd_stack *st, int N, bool decode) {
             // residual add and out_proj); the conv front end and the gated
             // norm sum them as they read (up to 4, as contrib allows).
             const gd_gemm_plan pi = gd_gemm_choose(ctx, N, ly.in_proj.K, ly.in_proj.R, GD_F16);
+            // An unsplit plan whose row tiles stop short of R by no more
+            // than the gate columns (b, a: the last 2 nV rows) leaves those
+            // as K-split tail partials in contrib (free until out_proj).
+            const int tile_rows = pi.nw * pi.nt * 32;
+            const int off_b = st->convDim + st->valDim;
+            const int64_t r0 = (int64_t)ly.in_proj.R / tile_rows * tile_rows;
             if (pi.split > 1 && pi.split <= 4 &&
                 (size_t)pi.split * N * RP <= (size_t)8 * st->c.max_batch * E) {
                 R_(gd_gemm_launch(ctx, &ly.in_proj, N, st->xn16, GD_F16, st->contrib, GD_F32, pi));
                 pin = st->contrib;
                 np = pi.split;
+            } else if (pi.split == 1 && !pi.ex && r0 < ly.in_proj.R && r0 >= off_b &&
+                       (size_t)TAIL_SPLITS * N * (ly.in_proj.R - r0) <= (size_t)8 * st->c.max_batch * E) {
+                tail_np = TAIL_SPLITS;
+                R_(gd_gemm_launch_tail(ctx, &ly.in_proj, N, st->xn16, st->proj, pi, st->contrib,
+                                       &tail_np, &tail_r0));
+                tailp = st->contrib;
             } else {
                 R_(gd_q2_0_gemm(ctx, &ly.in_proj, N, st->xn16, GD_F16, st->proj, GD_F32));
             }
@@ -647,7 +679,8 @@ int forward(gd_stack *st, int N, bool decode) {
                 const int64_t pstr = (int64_t)N * RP;
 #define GD_CONV(NP_) K_(k_gdn_conv_prefill<NP_>, dim3(gd_blocks(tasks, 4)), dim3(256), 0, s, pin, \
                         (int64_t)RP, pstr, ly.conv_state, ly.conv_w, st->conv_out, st->convDim, \
-                        2 * nK, N, eps, off_b, off_a, ly.dt, ly.a_neg, st->beta, st->g, nV)
+                        2 * nK, N, eps, off_b, off_a, ly.dt, ly.a_neg, st->beta, st->g, nV, tailp, \
+                        tail_r0, RP - tail_r0, tail_np, (int64_t)N * (RP - tail_r0))
                 if (np == 1) GD_CONV(1); else if (np == 2) GD_CONV(2); else if (np == 3) GD_CONV(3); else GD_CONV(4);
 #undef GD_CONV
                 // Chunks of 32 tokens: the 32 x 32 UT transform is cheaper per token

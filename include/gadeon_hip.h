@@ -224,6 +224,18 @@ int gd_q2_0_gemm_plan(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X,
 int gd_q2_0_gemm_plan17(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X,
                         int x_dtype, void *Y, int y_dtype, int split);
 
+/* gd_q2_0_gemm (f16 X, f32 Y) on an unsplit tile (mt, nt, nw as for
+ * gd_q2_0_gemm_plan) over the rows below *tail_r0 = R rounded down to the
+ * tile's rows, with the remaining rows (R must not be a whole number of tiles)
+ * run in the same launch as K-split units: at most tail_split splits,
+ * *tail_nz made, f32 partials tailY[z][t][r - *tail_r0] (summed by the
+ * caller in split order); Y's rows from *tail_r0 on are not written.  The
+ * stack runs its GDN in_proj so (its last 32 rows are the gate columns).
+ * For tests; no counterpart in the reference. */
+int gd_q2_0_gemm_plan_tail(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, float *Y,
+                           int mt, int nt, int nw, int tail_split, float *tailY, int *tail_nz,
+                           int *tail_r0);
+
 /* Feed-forward GEMM with SwiGLU fused into the epilogue: W is [gate; up]
  * (R = 2 ff rows, ff a multiple of 16), X f16 [T][K], out f16 [T][ff] =
  * silu(X gate^T) * (X up^T), as gd_q2_0_gemm (f32 Y) followed by the

@@ -305,6 +305,44 @@ def test_gemm_plan17_vs_oracle(ctx, T, K, R, split, yt):
     free_w(ctx, w)
 
 
+@pytest.mark.parametrize("T,K,R,mt,nt,nw,split", [(512, 5120, 8224, 2, 1, 4, 8), (77, 2688, 700, 2, 1, 4, 3),
+                                                   (200, 384, 100, 4, 1, 8, 2), (33, 1024, 544, 4, 2, 8, 5)])
+def test_gemm_tail_vs_oracle(ctx, T, K, R, mt, nt, nw, split):
+    """An unsplit tile over the whole row tiles, the rows past them (R is not a
+    whole number of tiles) run as K-split partial units of the same launch, as
+    the stack runs its GDN in_proj (R = 8224 on 128-row tiles, its 32 gate rows
+    in 8 splits), against the oracle: Y below the tail, and the tail as the sum
+    of its partials in split order; Y's tail rows are left as they were.  Also
+    a tile wider than R (every row in the tail) and a 512-row tile."""
+    blocks = O.lcg_q2_0(K, R, 5 * K + R)
+    w = upload_w(ctx, blocks, K, R)
+    Xh = O.lcg_normal_f16(T * K, 85).reshape(T, K)
+    dX = ctx.put(Xh.view(np.uint16))
+    dY = ctx.put(np.full((T, R), 7.0, np.float32))
+    dP = ctx.alloc(split * T * R * 4)
+    nz, r0 = C.c_int(), C.c_int()
+    ctx.gd_q2_0_gemm_plan_tail(C.byref(w), T, dX, dY, mt, nt, nw, split, dP, C.byref(nz), C.byref(r0))
+    rows = nw * nt * 32
+    assert r0.value == R // rows * rows and 1 <= nz.value <= split
+    r0 = r0.value
+    Y = ctx.get(dY, (T, R), np.float32)
+    P = ctx.get(dP, (nz.value, T, R - r0), np.float32)
+    tail = P[0].copy()
+    for z in range(1, nz.value):
+        tail += P[z]
+    toks = range(T) if T <= 200 else (0, 63, 64, 255, 256, 300, T - 1)
+    for t in toks:
+        want = O.q2_0_matvec(blocks, K, R, Xh[t].astype(np.float32), threads=8)
+        if r0:
+            assert rel_diff(Y[t, :r0], want[:r0]) < 1e-4, t
+        assert rel_diff(tail[t], want[r0:]) < 1e-4, t
+    assert np.all(Y[:, r0:] == 7.0)
+    ctx.free(dX)
+    ctx.free(dY)
+    ctx.free(dP)
+    free_w(ctx, w)
+
+
 def silu(v):
     return v / (1.0 + np.exp(-v))
 
