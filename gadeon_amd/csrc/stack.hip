@@ -79,6 +79,8 @@ __device__ __forceinline__ float psum(const float *proj, int64_t pstride, int64_
     return a;
 }
 static_assert(CT >= 3, "only the first task of a row may reach back into the ring");
+// Tail partials of the gate columns the prefill front end sums (at most).
+constexpr int TAIL_MAX = 8;
 // proj holds NP split-K partials of the in_proj output, pstride floats
 // apart, summed as they are read.  tailp (if not null): the gate columns
 // (off_b .. and off_a .., at or past tail_c0) are tail_np partials
@@ -162,11 +164,17 @@ __global__ __launch_bounds__(256) void k_gdn_conv_prefill(
     }
     if (r == 0) {
         // Gate input column col of token n, its partials added in split order.
+        // Up to TAIL_MAX partials, every load issued before the first add
+        // (a loop to a runtime count waited for each load in turn).
         auto gin = [&](int n, int col) {
             if (tailp) {
                 const float *tp = tailp + (int64_t)n * tail_ld + (col - tail_c0);
-                float a = tp[0];
-                for (int p = 1; p < tail_np; p++) a += tp[p * tail_ps];
+                float v[TAIL_MAX];
+#pragma unroll
+                for (int p = 0; p < TAIL_MAX; p++) v[p] = tp[(int64_t)min(p, tail_np - 1) * tail_ps];
+                float a = v[0];
+#pragma unroll
+                for (int p = 1; p < TAIL_MAX; p++) a += p < tail_np ? v[p] : 0.f;
                 return a;
             }
             return psum<NP>(proj, pstride, (int64_t)n * stride + col);
@@ -648,7 +656,7 @@ int forward(gd_stack *st, int N, bool decode) {
                 R_(gd_gemm_launch(ctx, &ly.in_proj, N, st->xn16, GD_F16, st->contrib, GD_F32, pi));
                 pin = st->contrib;
                 np = pi.split;
-            } else if (pi.split == 1 && !pi.ex && r0 < ly.in_proj.R && r0 >= off_b &&
+            } else if (pi.split == 1 && !pi.ex && r0 < ly.in_proj.R && r0 >= off_b && TAIL_SPLITS <= TAIL_MAX &&
                        (size_t)TAIL_SPLITS * N * (ly.in_proj.R - r0) <= (size_t)8 * st->c.max_batch * E) {
                 tail_np = TAIL_SPLITS;
                 R_(gd_gemm_launch_tail(ctx, &ly.in_proj, N, st->xn16, st->proj, pi, st->contrib,
