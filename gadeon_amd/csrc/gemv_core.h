@@ -123,14 +123,14 @@ __device__ __forceinline__ uint32_t pack_h2(float a, float b) {
     return (uint32_t)gd_f2h(a) | ((uint32_t)gd_f2h(b) << 16);
 }
 
-// x values of one staging entry (16 consecutive elements of one block).
+// x values of one staging unit (4 NQ consecutive elements of one block).
 // XT = 0: f16 x; 1: f32 x; 2: f32 residual h (+ delta partials) and the
 // norm weight w, staged as x = (h + delta) * w at f32 precision (the row sums
 // are scaled by 1/rms(h + delta)).
-template <int XT> struct XChunk;
-template <> struct XChunk<0> { u32x4 lo, hi; };
-template <> struct XChunk<1> { f32x4 f[4]; };
-template <> struct XChunk<2> { f32x4 f[4], w[4], d[ND_UNROLL][4]; };
+template <int XT, int NQ> struct XChunk;
+template <int NQ> struct XChunk<0, NQ> { u32x4 h[NQ / 2]; };
+template <int NQ> struct XChunk<1, NQ> { f32x4 f[NQ]; };
+template <int NQ> struct XChunk<2, NQ> { f32x4 f[NQ], w[NQ], d[ND_UNROLL][NQ]; };
 
 // SwiGLU output: with pair_sets > 0, W is [gate; up] with pair_sets sets
 // (16 rows) in each half, a workgroup takes gate sets k .. and the matching
@@ -182,6 +182,15 @@ template <class Op> __device__ __forceinline__ float group8(float v, Op op) {
     v = op(v, gd_dpp<GD_DPP_XOR1>(v));
     v = op(v, gd_dpp<GD_DPP_XOR2>(v));
     return op(v, gd_dpp<GD_DPP_HALF_MIRROR>(v));
+}
+// op over the G (8 or 16) lanes of each aligned group: for 16, the row
+// mirror then pairs each lane with one in the other half-row, whose lanes
+// all hold that half's value.
+template <int G, class Op> __device__ __forceinline__ float group(float v, Op op) {
+    static_assert(G == 8 || G == 16, "lane groups of 8 or 16");
+    v = group8(v, op);
+    if constexpr (G == 16) v = op(v, gd_dpp<GD_DPP_MIRROR>(v));
+    return v;
 }
 
 // The register ring of a wave: P tiles with their scales and item numbers.
@@ -270,10 +279,15 @@ __device__ __forceinline__ void issue(const Task &t, const Geo &g, int it, u32x4
 // normalized residual (see XChunk).  KBP: item partials kept per Q2 block (4
 // per row) in LDS, summed with the rest of the row at the end; otherwise
 // summed across the block lanes first (needs 4x less LDS, for very long K).
+// SE: x elements a thread stages (16, or 8 with the fp4 body: twice the
+// threads share the staging, for K up to (1024/16 - 5) blocks).
 // All 64 * NW threads of the workgroup must call it.
-template <int XT, bool KBP, bool F4, int ND = 0>
+template <int XT, bool KBP, bool F4, int ND = 0, int SE = 16>
 __device__ void run(const Task &t, int bx, int bz, uint32_t *lds) {
     static_assert(ND >= 0 && ND <= ND_UNROLL && (XT == 2 || ND == 0), "partials: fused input only");
+    static_assert(SE == 16 || (SE == 8 && F4), "half-entry staging: fp4 body only");
+    constexpr int NQ = SE / 4;                            // f32x4 of x per staging unit
+    constexpr int UPB = 128 / SE;                         // staging units per block
     constexpr int MT = 64 * NW;
     // x at f32 precision: f32 x, and the fused input's h' * w (whose 1/rms
     // scales the row sums instead).
@@ -308,9 +322,10 @@ __device__ void run(const Task &t, int bx, int bz, uint32_t *lds) {
     float *y = t.y + (size_t)g.bz * R;
     const int L = g.L, s0 = g.s0, set_lo = g.set_lo, npair = g.npair, total = g.total;
 
-    // Staging entry e = (block e/8, chunk e%8): its x loads are issued before
-    // the tile prefetch, so waiting for them leaves the tiles in flight.
-    const int nstage = (nblk + 5) * 8;
+    // Staging unit e = (block e/UPB, elements SE (e%UPB) ..): its x loads are
+    // issued before the tile prefetch, so waiting for them leaves the tiles
+    // in flight.
+    const int nstage = (nblk + 5) * UPB;
     // Entries past the last x block (the zero blocks, and threads with no
     // entry) read past the end of x: zeros, without a memory access.
     const NormIn &nin = t.nin;
@@ -318,8 +333,8 @@ __device__ void run(const Task &t, int bx, int bz, uint32_t *lds) {
     const __amdgpu_buffer_rsrc_t drs =
             make_rsrc(nin.delta, nin.nd ? (uint32_t)((nin.nd - 1) * nin.dstride + K) * 4u : 0u);
     const __amdgpu_buffer_rsrc_t wrs = make_rsrc(nin.w, XT == 2 ? (uint32_t)K * 4u : 0u);
-    // Element offset of staging entry e (K: an entry past the last x block).
-    auto entry_off = [&](int e) { return e < nblk * 8 ? (e >> 3) * 128 + 16 * (e & 7) : K; };
+    // Element offset of staging unit e (K: a unit past the last x block).
+    auto entry_off = [&](int e) { return e < nblk * UPB ? (e / UPB) * 128 + SE * (e % UPB) : K; };
     // Dwords 4q .. 4q+3 of partial z of the entry at off; entries past K
     // (off == K) must read zeros (at z * dstride + K lies the next partial),
     // and so does a partial past nd: an offset outside the resource.
@@ -332,13 +347,14 @@ __device__ void run(const Task &t, int bx, int bz, uint32_t *lds) {
     // the entry is in flight before the first wait).
     auto load_x = [&](int e) {
         const int off = entry_off(e);
-        XChunk<XT> c;
+        XChunk<XT, NQ> c;
         if constexpr (XT == 0) {
-            c.lo = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, off * 2, 0, 0));
-            c.hi = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, off * 2 + 16, 0, 0));
+#pragma unroll
+            for (int q = 0; q < NQ / 2; q++)
+                c.h[q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, off * 2 + 16 * q, 0, 0));
         } else {
 #pragma unroll
-            for (int q = 0; q < 4; q++)
+            for (int q = 0; q < NQ; q++)
                 c.f[q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, off * 4 + 16 * q, 0, 0));
             if constexpr (XT == 2) {
                 // The first ND partials are loaded here, unconditionally and in
@@ -348,9 +364,9 @@ __device__ void run(const Task &t, int bx, int bz, uint32_t *lds) {
 #pragma unroll
                 for (int z = 0; z < ND; z++)
 #pragma unroll
-                    for (int q = 0; q < 4; q++) c.d[z][q] = dload(off, z, q, true);
+                    for (int q = 0; q < NQ; q++) c.d[z][q] = dload(off, z, q, true);
 #pragma unroll
-                for (int q = 0; q < 4; q++)
+                for (int q = 0; q < NQ; q++)
                     c.w[q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs, off * 4 + 16 * q, 0, 0));
             }
         }
@@ -392,7 +408,7 @@ __device__ void run(const Task &t, int bx, int bz, uint32_t *lds) {
     // The bias and first tile are requested inside each branch, so that
     // work on x the compiler moves up into the loading branch still comes
     // after them.
-    XChunk<XT> xc;
+    XChunk<XT, NQ> xc;
     if (xwave) {
         xc = load_x(threadIdx.x);
         __builtin_amdgcn_sched_barrier(0);
@@ -406,30 +422,32 @@ __device__ void run(const Task &t, int bx, int bz, uint32_t *lds) {
     // XSCALE[k] * 2^-e_b.  Thread (b, i) forms the 8 pairs of x[16i ..
     // 16i+15] in registers and writes them as 32 bytes; the block's sum and
     // max|x| come from 8-lane shuffles.  e_b = 0 unless max|x| >= 2048.
-    auto stage = [&](const int e, const XChunk<XT> &xc) {
-        const int bb = e >> 3, i = e & 7;
+    auto stage = [&](const int e, const XChunk<XT, NQ> &xc) {
+        // Block bb, 16-element chunk i, half hf of it (SE = 8).
+        const int bb = e / UPB, sub = e % UPB;
+        const int i = SE == 16 ? sub : sub >> 1, hf8 = SE == 16 ? 0 : sub & 1;
         float sum = 0.f, amax = 0.f;
-        f32x4 f[4];
+        f32x4 f[NQ];
         if constexpr (XT == 0) {
 #pragma unroll
-            for (int q = 0; q < 8; q++) {
-                const uint32_t d = q < 4 ? xc.lo[q] : xc.hi[q - 4];
+            for (int q = 0; q < 2 * NQ; q++) {
+                const uint32_t d = xc.h[q >> 2][q & 3];
                 f[q >> 1][2 * (q & 1)] = gd_h2f((uint16_t)(d & 0xffff));
                 f[q >> 1][2 * (q & 1) + 1] = gd_h2f((uint16_t)(d >> 16));
             }
         } else {
 #pragma unroll
-            for (int q = 0; q < 4; q++) f[q] = xc.f[q];
+            for (int q = 0; q < NQ; q++) f[q] = xc.f[q];
         }
 #pragma unroll
-        for (int q = 0; q < 4; q++)
+        for (int q = 0; q < NQ; q++)
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 sum += f[q][j];
                 amax = fmaxf(amax, fabsf(f[q][j]));
             }
-        sum = group8(sum, [](float a, float b) { return a + b; });
-        amax = group8(amax, [](float a, float b) { return fmaxf(a, b); });
+        sum = group<UPB>(sum, [](float a, float b) { return a + b; });
+        amax = group<UPB>(amax, [](float a, float b) { return fmaxf(a, b); });
         if constexpr (F4) {
             // x = 2^e (p0 + p1/16 + p2/256 [+ p3/4096]), e4m3 pieces with
             // max|x| 2^-e in [128, 256): p0 = e4m3(x 2^-e), each later piece
@@ -450,7 +468,7 @@ __device__ void run(const Task &t, int bx, int bz, uint32_t *lds) {
             float tsum = 0.f;      // f32 x: what the pieces leave out
             u32x4 pc[4];
 #pragma unroll
-            for (int dw = 0; dw < 4; dw++) {
+            for (int dw = 0; dw < NQ; dw++) {
                 uint32_t w[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
                 for (int hf = 0; hf < 2; hf++) {
@@ -478,18 +496,21 @@ __device__ void run(const Task &t, int bx, int bz, uint32_t *lds) {
                 for (int jj = 0; jj < 4; jj++) pc[jj][dw] = w[jj];
             }
             if (XF) {
-                tsum = group8(tsum, [](float a, float b) { return a + b; });
+                tsum = group<UPB>(tsum, [](float a, float b) { return a + b; });
             }
             if (e < nstage) {
-                u32x4 *dst = (u32x4 *)(xsb + bb * F4_BLK + 64 * i);
+                uint8_t *dst = xsb + bb * F4_BLK + 64 * i;
 #pragma unroll
-                for (int jj = 0; jj < 4; jj++) dst[jj] = pc[jj];
-                if (i == 7) {   // the padding: read as zeros by the idle lanes
+                for (int jj = 0; jj < 4; jj++) {
+                    if constexpr (SE == 16) *(u32x4 *)(dst + 16 * jj) = pc[jj];
+                    else *(u32x2 *)(dst + 16 * jj + 8 * hf8) = u32x2{pc[jj][0], pc[jj][1]};
+                }
+                if (i == 7 && hf8 == 0) {   // the padding: read as zeros by the idle lanes
                     u32x4 *pad = (u32x4 *)(xsb + bb * F4_BLK + 512);
 #pragma unroll
                     for (int jj = 0; jj < 4; jj++) pad[jj] = u32x4{0u, 0u, 0u, 0u};
                 }
-                if (i == 0 && bb < nblk) {
+                if (sub == 0 && bb < nblk) {
                     // sum of the pieces: sum x less what they leave out
                     sx[bb] = XF ? sum - tsum : sum;
                     ((int *)ex)[bb] = 127 + eb;
@@ -530,22 +551,22 @@ __device__ void run(const Task &t, int bx, int bz, uint32_t *lds) {
             }
         }
     };
-    // The first entry is straight-line code after the tile prefetch, so its
-    // wait for x leaves the tiles in flight; further entries (K long enough
-    // that (K/128 + 5) * 8 > threads) follow in a loop.
+    // The first unit is straight-line code after the tile prefetch, so its
+    // wait for x leaves the tiles in flight; further units (K long enough
+    // that (K/128 + 5) * 128/SE > threads) follow in a loop.
     if constexpr (XT == 2) {
         // RMSNorm(h') * w with h' = h + delta: x = h' * w is staged as it is
         // (f32, four pieces) and the row sums are scaled by 1/rms(h') at the
         // end, so no barrier for the sum of squares stands between the x
         // loads and the staging: each wave's share goes to ssr here and is
-        // read after the staging barrier.  One entry per thread (the host
-        // checks), entries past K load zeros.  Workgroup 0 keeps h' for the
+        // read after the staging barrier.  One unit per thread (the host
+        // checks), units past K load zeros.  Workgroup 0 keeps h' for the
         // next residual add.
         float ss = 0.f;
         if (xwave) {
             const int xoff = entry_off(threadIdx.x);
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
+            for (int q = 0; q < NQ; q++) {
                 // h + ((0 + p0) + p1 ...), the partials in order.
                 f32x4 d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -558,17 +579,17 @@ __device__ void run(const Task &t, int bx, int bz, uint32_t *lds) {
             ss = gd_wave_sum(ss);
         }
         if (lane == 0) ssr[wave] = ss;
-        if (bx == 0 && bz == 0 && nin.hout && threadIdx.x < nblk * 8) {
-            const uint32_t ho = (uint32_t)((threadIdx.x >> 3) * 128 + 16 * (threadIdx.x & 7)) * 4u;
+        if (bx == 0 && bz == 0 && nin.hout && threadIdx.x < nblk * UPB) {
+            const uint32_t ho = (uint32_t)entry_off(threadIdx.x) * 4u;
             const __amdgpu_buffer_rsrc_t hrs = make_rsrc(nin.hout, (uint32_t)K * 4u);
 #pragma unroll
-            for (int q = 0; q < 4; q++)
+            for (int q = 0; q < NQ; q++)
                 __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, xc.f[q]), hrs,
                                                        ho + 16 * q, 0, 0);
         }
         if (xwave) {
 #pragma unroll
-            for (int q = 0; q < 4; q++) xc.f[q] *= xc.w[q];
+            for (int q = 0; q < NQ; q++) xc.f[q] *= xc.w[q];
         }
     }
     if (xwave) stage(threadIdx.x, xc);

@@ -12,11 +12,12 @@ using gemv::NW;
 using gemv::NormIn;
 using gemv::xlds_bytes;
 
-// ND: residual partials of the fused input (XT = 2) loaded with h and w.
-template <int XT, bool KBP, bool F4, int ND>
+// ND: residual partials of the fused input (XT = 2) loaded with h and w;
+// SE: x elements each staging thread converts (8 or 16).
+template <int XT, bool KBP, bool F4, int ND, int SE = 16>
 __global__ __launch_bounds__(64 * NW) void q2_0_gemv_mfma_kernel(gemv::Task t) {
     extern __shared__ __align__(16) uint32_t lds[];
-    gemv::run<XT, KBP, F4, ND>(t, (int)blockIdx.x, (int)blockIdx.y, lds);
+    gemv::run<XT, KBP, F4, ND, SE>(t, (int)blockIdx.x, (int)blockIdx.y, lds);
 }
 
 // x staging bytes of a GEMV over nblk Q2 blocks: the fp4 kernel's where its
@@ -93,8 +94,16 @@ int launch(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, XStage xs,
     if (rc) return rc;
     constexpr int NDM = XT == 2 ? gemv::ND_UNROLL : 0;
     const int nd = std::min(nin.nd, NDM);
+    // The fp4 kernel with per-block partials and f32 x (four pieces) stages 8
+    // elements a thread where all of x then fits one pass of the workgroup's
+    // threads: the staging VALU work is spread over twice the waves.  (With
+    // f16 x, three pieces, 16 a thread measured faster.)
+    const int nblk = (int)(w->K >> 7);
+    const bool se8 = XT != 0 && xs.f4 && kbp && (nblk + 5) * 16 <= 64 * NW;
     auto pick = [&](auto ndc) {
         constexpr int ND = decltype(ndc)::value;
+        if constexpr (XT != 0)
+            if (se8) return q2_0_gemv_mfma_kernel<XT, true, true, ND, 8>;
         return xs.f4 ? (kbp ? q2_0_gemv_mfma_kernel<XT, true, true, ND> : q2_0_gemv_mfma_kernel<XT, false, true, ND>)
                      : (kbp ? q2_0_gemv_mfma_kernel<XT, true, false, ND> : q2_0_gemv_mfma_kernel<XT, false, false, ND>);
     };
