@@ -321,11 +321,14 @@ __device__ void run(const Task &t, int bx, int bz, uint32_t *lds) {
     const int j = lane & 3, rq = (lane >> 2) & 3, kb = lane >> 4;
     float *y = t.y + (size_t)g.bz * R;
     const int L = g.L, s0 = g.s0, set_lo = g.set_lo, npair = g.npair, total = g.total;
+    // x blocks of this workgroup's K range (all of x unless K is split):
+    // blocks xb0 .. xb0 + nbx - 1, staged from LDS block 0.
+    const int xb0 = 4 * s0, nbx = max(0, min(nblk, 4 * (s0 + L)) - xb0);
 
     // Staging unit e = (block e/UPB, elements SE (e%UPB) ..): its x loads are
     // issued before the tile prefetch, so waiting for them leaves the tiles
     // in flight.
-    const int nstage = (nblk + 5) * UPB;
+    const int nstage = (nbx + 5) * UPB;
     // Entries past the last x block (the zero blocks, and threads with no
     // entry) read past the end of x: zeros, without a memory access.
     const NormIn &nin = t.nin;
@@ -334,7 +337,7 @@ __device__ void run(const Task &t, int bx, int bz, uint32_t *lds) {
             make_rsrc(nin.delta, nin.nd ? (uint32_t)((nin.nd - 1) * nin.dstride + K) * 4u : 0u);
     const __amdgpu_buffer_rsrc_t wrs = make_rsrc(nin.w, XT == 2 ? (uint32_t)K * 4u : 0u);
     // Element offset of staging unit e (K: a unit past the last x block).
-    auto entry_off = [&](int e) { return e < nblk * UPB ? (e / UPB) * 128 + SE * (e % UPB) : K; };
+    auto entry_off = [&](int e) { return e < nbx * UPB ? (xb0 + e / UPB) * 128 + SE * (e % UPB) : K; };
     // Dwords 4q .. 4q+3 of partial z of the entry at off; entries past K
     // (off == K) must read zeros (at z * dstride + K lies the next partial),
     // and so does a partial past nd: an offset outside the resource.
@@ -510,7 +513,7 @@ __device__ void run(const Task &t, int bx, int bz, uint32_t *lds) {
 #pragma unroll
                     for (int jj = 0; jj < 4; jj++) pad[jj] = u32x4{0u, 0u, 0u, 0u};
                 }
-                if (sub == 0 && bb < nblk) {
+                if (sub == 0 && bb < nbx) {
                     // sum of the pieces: sum x less what they leave out
                     sx[bb] = XF ? sum - tsum : sum;
                     ((int *)ex)[bb] = 127 + eb;
@@ -545,7 +548,7 @@ __device__ void run(const Task &t, int bx, int bz, uint32_t *lds) {
                 dq[0] = q0;
                 dq[1] = q1;
             }
-            if (i == 0 && bb < nblk) {
+            if (i == 0 && bb < nbx) {
                 sx[bb] = sum;
                 ex[bb] = __uint_as_float((uint32_t)(127 + 16 + eb) << 23);   // 2^(16+eb)
             }
@@ -579,7 +582,7 @@ __device__ void run(const Task &t, int bx, int bz, uint32_t *lds) {
             ss = gd_wave_sum(ss);
         }
         if (lane == 0) ssr[wave] = ss;
-        if (bx == 0 && bz == 0 && nin.hout && threadIdx.x < nblk * UPB) {
+        if (bx == 0 && bz == 0 && nin.hout && threadIdx.x < nbx * UPB) {
             const uint32_t ho = (uint32_t)entry_off(threadIdx.x) * 4u;
             const __amdgpu_buffer_rsrc_t hrs = make_rsrc(nin.hout, (uint32_t)K * 4u);
 #pragma unroll
@@ -623,13 +626,13 @@ __device__ void run(const Task &t, int bx, int bz, uint32_t *lds) {
             // read a zero region placed on other banks.  The B scale of lane
             // l (column l%16, K block l/16) is 2^(e_q - 4 jp) where l/16 is q.
             const int q = (lane >> 2) & 3, jp = lane & 3, G = lane >> 4;
-            const int blk = 4 * s + q;
+            const int blk = 4 * (s - s0) + q;           // staged (local) block
             const bool act = (q & 1) == (G >> 1) && jp < NJ;
-            const uint32_t zb = (uint32_t)((nblk + 3) * F4_BLK + 255) & ~255u;
+            const uint32_t zb = (uint32_t)((nbx + 3) * F4_BLK + 255) & ~255u;
             const uint32_t dat = (uint32_t)(blk * F4_BLK + ((G & 1) * 4 + jp) * 16);
             const uint32_t zer = zb + (uint32_t)((((q + (G & 1)) & 3) * 64) + jp * 16);
             const uint32_t alo = act && q < 2 ? dat : zer, ahi = act && q >= 2 ? dat : zer;
-            const int bj = min(blk, nblk - 1);
+            const int bj = min(blk, nbx - 1);
             const int ev = ((const int *)ex)[bj];
             const int sb = G == q ? ev - 4 * jp : 127;
             constexpr uint32_t M = 0x33333333u;
@@ -651,7 +654,7 @@ __device__ void run(const Task &t, int bx, int bz, uint32_t *lds) {
                 v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));
                 return v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));
             };
-            const bool live = blk < nblk;
+            const bool live = blk < nbx;
             const float sxq = sx[bj];
             const float dsc[4] = {gd_h2f((uint16_t)(sc[0] & 0xffff)), gd_h2f((uint16_t)(sc[0] >> 16)),
                                   gd_h2f((uint16_t)(sc[1] & 0xffff)), gd_h2f((uint16_t)(sc[1] >> 16))};
@@ -675,7 +678,7 @@ __device__ void run(const Task &t, int bx, int bz, uint32_t *lds) {
         // MFMA block mb = lane/4 multiplies rows 4*rq .. 4*rq+3 of Q2 block
         // 4s + kb by four K values.  Blocks past the last (a short final
         // step) read zero-staged x and give zero products.
-        const int blk = 4 * s + kb;
+        const int blk = 4 * (s - s0) + kb;               // staged (local) block
         const u32x4 *src = (const u32x4 *)(xp + blk * XB);
         const u32x4 *srq = (const u32x4 *)(xq + blk * XB);
         f32x4 acc[4];
@@ -707,8 +710,8 @@ __device__ void run(const Task &t, int bx, int bz, uint32_t *lds) {
         }
         // Lane (j, rq, kb) has rows 4*rq + v of block 4s + kb; every product
         // entered as c * x * 2^(-16-e_b) (lo with x 2^11).
-        const bool live = blk < nblk;
-        const int bj = min(blk, nblk - 1);
+        const bool live = blk < nbx;
+        const int bj = min(blk, nbx - 1);
         const float sxj = sx[bj], exj = ex[bj];
         const float dsc[4] = {gd_h2f((uint16_t)(sc[0] & 0xffff)), gd_h2f((uint16_t)(sc[0] >> 16)),
                               gd_h2f((uint16_t)(sc[1] & 0xffff)), gd_h2f((uint16_t)(sc[1] >> 16))};
