@@ -32,7 +32,11 @@
 namespace {
 
 constexpr int DSPLIT = 16;      // key splits per head (decode)
-constexpr int AQ = 64, AK = 32; // queries per prefill block, keys per LDS block
+constexpr int AQ = 64;          // queries per prefill block
+// Keys per LDS block of the prefill: 64 for head dim 128 (each block's loads
+// then have twice the arithmetic to land behind), 32 for 256 (its K and V
+// tiles fill the static LDS at 32).
+template <int HD> constexpr int prefill_keys() { return HD <= 128 ? 64 : 32; }
 
 __device__ __forceinline__ int64_t kv_slot(const int32_t *pt, int pos, int block) {
     return (int64_t)pt[pos / block] * block + pos % block;
@@ -162,13 +166,13 @@ __global__ __launch_bounds__(64 * PREP_WAVES) void k_attn_prep(
 // Causal prefill attention with the sigmoid output gate (Attention.swift:
 // 108-134), flash style on the matrix cores.  Block (head h, 64 queries):
 // wave w owns queries 16w .. 16w+15; keys stream through LDS in blocks of
-// 32 (K as [key][d], V transposed as [d][key]).  Per block a wave forms
+// AK (K as [key][d], V transposed as [d][key]).  Per block a wave forms
 // S^T = K Q^T (v_mfma_f32_16x16x32_f16, lane = one query column and four
 // keys of each 16-key tile), updates its online softmax per query, and adds
-// V^T P^T into O^T.  The C layout of S^T is already the B operand of V^T P^T
-// once the MFMA's K index 8g + e (g = lane / 16) stands for key 4g + e
-// (e < 4) or 16 + 4g + e - 4: the A operand (V^T) reads the same keys, so P
-// never goes through LDS.  q and P enter as f16 hi + lo pairs (about 22
+// V^T P^T into O^T, 32 keys per MFMA.  The C layout of S^T is already the B
+// operand of V^T P^T once the MFMA's K index 8g + e (g = lane / 16) stands
+// for key 4g + e (e < 4) or 16 + 4g + e - 4 of its 32: the A operand (V^T)
+// reads the same keys, so P never goes through LDS.  q and P enter as f16 hi + lo pairs (about 22
 // bits), K and V are the f16 cache itself, accumulation is f32.  Queries sit
 // at positions pos0 + n with pos0 = *pos_ptr (if not null) + pos_add.
 template <int HD, typename OT>
@@ -176,7 +180,10 @@ __global__ __launch_bounds__(256) void k_attn_prefill(
         const float *q, const float *gate, const uint16_t *kc, const uint16_t *vc,
         const int32_t *page_table, const int32_t *pos_ptr, int pos_add, OT *out, int H, int HKV,
         int N, int block, float scale, int gated) {
-    constexpr int CH = HD / 64;                           // 8-dim chunks a thread stages per operand
+    constexpr int AK = prefill_keys<HD>();
+    constexpr int TPK = 256 / AK;                         // staging threads per key
+    constexpr int DPT = HD / TPK;                         // dims a thread stages per key
+    constexpr int CH = DPT / 8;                           // 8-dim chunks a thread stages per operand
     __shared__ __attribute__((aligned(16))) f16 Ks[AK][HD + 8];
     __shared__ __attribute__((aligned(16))) f16 Vt[HD][AK + 8];
     // The last query blocks attend the most keys: they are dispatched first,
@@ -211,12 +218,12 @@ __global__ __launch_bounds__(256) void k_attn_prefill(
     for (int dt = 0; dt < HD / 16; dt++) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
     float m = -INFINITY, l = 0.f;                         // this lane's keys only
     const int last = pos0 + min(q0 + AQ, N) - 1;          // last key any query here needs
-    // Staging: thread t loads dims d0 .. d0 + HD/8 - 1 of key t / 8 of the
+    // Staging: thread t loads dims d0 .. d0 + DPT - 1 of key t / TPK of the
     // block.  The loads run ahead of the arithmetic: block k0 + AK's K and V
     // rows are requested before block k0's MFMAs, and the page-table entry
     // they need one block earlier still, so no block waits for a memory
     // round trip (blocks past `last` clamp to it: loaded, never used).
-    const int sk = t >> 3, d0 = (t & 7) * (HD / 8);
+    const int sk = t / TPK, d0 = (t % TPK) * DPT;
     auto page_of = [&](int k0) { return page_table[min(k0 + sk, last) / block]; };
     u32x4 kv[2 * CH];                                     // K chunks, then V chunks
     auto fetch = [&](int k0, int page) {
@@ -245,10 +252,11 @@ __global__ __launch_bounds__(256) void k_attn_prefill(
         // Keep the loads here: the compiler would sink them below the MFMAs,
         // next to the LDS writes that wait for them.
         __builtin_amdgcn_sched_barrier(0);
-        // S^T tiles kt = 0, 1: keys 16 kt + 4 g + v for query lq.
-        f32x4 sc[2];
+        // S^T tiles kt: keys 16 kt + 4 g + v for query lq.
+        constexpr int NKT = AK / 16;
+        f32x4 sc[NKT];
 #pragma unroll
-        for (int kt = 0; kt < 2; kt++) {
+        for (int kt = 0; kt < NKT; kt++) {
             sc[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < HD / 32; ks++) {
@@ -261,7 +269,7 @@ __global__ __launch_bounds__(256) void k_attn_prefill(
         // online softmax of query lq over its lane group's keys.
         float bmax = -INFINITY;
 #pragma unroll
-        for (int kt = 0; kt < 2; kt++)
+        for (int kt = 0; kt < NKT; kt++)
 #pragma unroll
             for (int v = 0; v < 4; v++) {
                 const int kp = k0 + 16 * kt + 4 * g + v;
@@ -278,26 +286,30 @@ __global__ __launch_bounds__(256) void k_attn_prefill(
         l *= alpha;
 #pragma unroll
         for (int dt = 0; dt < HD / 16; dt++) acc[dt] *= alpha;
-        f16x8 ph, pl;
+        // P of key group kg (keys 32 kg ..): tiles 2 kg and 2 kg + 1.
+        f16x8 ph[AK / 32], pl[AK / 32];
 #pragma unroll
-        for (int kt = 0; kt < 2; kt++)
+        for (int kt = 0; kt < NKT; kt++)
 #pragma unroll
             for (int v = 0; v < 4; v++) {
                 const float pv = __expf(sc[kt][v] - mn);
                 l += pv;
                 const f16 hi = (f16)pv;
-                ph[4 * kt + v] = hi;
-                pl[4 * kt + v] = (f16)(pv - (float)hi);
+                ph[kt >> 1][4 * (kt & 1) + v] = hi;
+                pl[kt >> 1][4 * (kt & 1) + v] = (f16)(pv - (float)hi);
             }
-        // O^T += V^T P^T: A lane row d = 16 dt + lq, the same 8 keys.
+        // O^T += V^T P^T: A lane row d = 16 dt + lq, the same 8 keys of each
+        // group.
 #pragma unroll
-        for (int dt = 0; dt < HD / 16; dt++) {
-            const f16 *vr = &Vt[16 * dt + lq][0];
-            const f16x4 v0 = *(const f16x4 *)(vr + 4 * g), v1 = *(const f16x4 *)(vr + 16 + 4 * g);
-            const f16x8 va = f16x8{v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-            acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, ph, acc[dt], 0, 0, 0);
-            acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl, acc[dt], 0, 0, 0);
-        }
+        for (int kg = 0; kg < AK / 32; kg++)
+#pragma unroll
+            for (int dt = 0; dt < HD / 16; dt++) {
+                const f16 *vr = &Vt[16 * dt + lq][32 * kg];
+                const f16x4 v0 = *(const f16x4 *)(vr + 4 * g), v1 = *(const f16x4 *)(vr + 16 + 4 * g);
+                const f16x8 va = f16x8{v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+                acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, ph[kg], acc[dt], 0, 0, 0);
+                acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl[kg], acc[dt], 0, 0, 0);
+            }
     }
     // Total weight of query lq: the four lane groups' partial sums.
     l += __shfl_xor(l, 16, 64);
