@@ -78,17 +78,19 @@ __global__ void k_rope_table(float2 *tab, int n, int n_rot, float base) {
 // token, so the block forms them once into LDS (the same powf / cosf / sinf
 // per pair index as rope_cs) instead of once per head.  pos_ptr[0] is the
 // first token's position (the KV slot), pos_ptr[1] the rope shift: tokens
-// rotate at position + shift (MetalEngine.swift:432-435).
+// rotate at position + shift (MetalEngine.swift:432-435).  Heads hbeg ..
+// H + HKV - 1 are done (hbeg = H: the kv heads only, for a prefill that
+// prepares its q itself).
 constexpr int PREP_WAVES = 4, PREP_HEADS = 12;
 template <int HD>
 __global__ __launch_bounds__(64 * PREP_WAVES) void k_attn_prep(
         const float *proj, int64_t stride, int qs, const float *q_norm, const float *k_norm,
         float *q_out, float *gate_out, uint16_t *kc, uint16_t *vc, const int32_t *page_table,
         const int32_t *pos_ptr, int N, int H, int HKV, int n_rot, float base, int block, float eps,
-        const float2 *rtab, int rtab_n) {
+        const float2 *rtab, int rtab_n, int hbeg) {
     constexpr int S = HD / 64;
     __shared__ float rc[HD / 2], rs[HD / 2];
-    const int groups = (H + HKV + PREP_HEADS - 1) / PREP_HEADS;
+    const int groups = (H + HKV - hbeg + PREP_HEADS - 1) / PREP_HEADS;
     const int n = (int)(blockIdx.x / groups), g = (int)(blockIdx.x % groups);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int pos = pos_ptr[0] + n, rpos = pos + pos_ptr[1];
@@ -102,7 +104,7 @@ __global__ __launch_bounds__(64 * PREP_WAVES) void k_attn_prep(
     const float *row = proj + (int64_t)n * stride;
 #pragma unroll
     for (int t = 0; t < PREP_HEADS / PREP_WAVES; t++) {
-        const int h = g * PREP_HEADS + wave + PREP_WAVES * t;
+        const int h = hbeg + g * PREP_HEADS + wave + PREP_WAVES * t;
         if (h >= H + HKV) break;
         const bool is_q = h < H;
         const int kh = h - H;
@@ -163,6 +165,21 @@ __global__ __launch_bounds__(64 * PREP_WAVES) void k_attn_prep(
 
 // ---------------------------------------------------------------- prefill
 
+// Where the prefill's queries and output gates come from: (token n, head h)
+// at q + n tstride + h hstride, the gate likewise from gate.  norm null: q
+// already normalized and rotated (k_attn_prep's q_out); else raw projection
+// rows, normalized with norm and rotated (n_rot, base, the table rtab of
+// rtab_n positions) by the prefill itself.
+struct AttnQ {
+    const float *q, *gate;
+    int64_t tstride;
+    int hstride;
+    const float *norm;
+    const float2 *rtab;
+    int rtab_n, n_rot;
+    float base, eps;
+};
+
 // Causal prefill attention with the sigmoid output gate (Attention.swift:
 // 108-134), flash style on the matrix cores.  Block (head h, 64 queries):
 // wave w owns queries 16w .. 16w+15; keys stream through LDS in blocks of
@@ -174,10 +191,14 @@ __global__ __launch_bounds__(64 * PREP_WAVES) void k_attn_prep(
 // for key 4g + e (e < 4) or 16 + 4g + e - 4 of its 32: the A operand (V^T)
 // reads the same keys, so P never goes through LDS.  q and P enter as f16 hi + lo pairs (about 22
 // bits), K and V are the f16 cache itself, accumulation is f32.  Queries sit
-// at positions pos0 + n with pos0 = *pos_ptr (if not null) + pos_add.
+// at positions pos0 + n with pos0 = *pos_ptr (if not null) + pos_add.  With
+// raw projection rows (qsrc.norm set) each lane group of a query holds all
+// of its dims (lane g: 32 ks + 8 g + e), so the q RMS norm is a sum over
+// the four groups and the rotation pairs (i, i + n_rot/2) lie in one lane
+// when n_rot/2 is a multiple of 32 (the host checks).
 template <int HD, typename OT>
 __global__ __launch_bounds__(256) void k_attn_prefill(
-        const float *q, const float *gate, const uint16_t *kc, const uint16_t *vc,
+        AttnQ qsrc, const uint16_t *kc, const uint16_t *vc,
         const int32_t *page_table, const int32_t *pos_ptr, int pos_add, OT *out, int H, int HKV,
         int N, int block, float scale, int gated) {
     constexpr int AK = prefill_keys<HD>();
@@ -197,26 +218,6 @@ __global__ __launch_bounds__(256) void k_attn_prefill(
     const int n = q0 + 16 * w + lq;                       // this lane's query
     const bool valid = n < N;
     const int my_pos = pos0 + (valid ? n : N - 1);
-    // B operand of S^T: q[n][32 ks + 8 g + e] * scale, split hi + lo.
-    f16x8 qh[HD / 32], ql[HD / 32];
-    {
-        const float *qrow = q + ((int64_t)(valid ? n : N - 1) * H + h) * HD;
-#pragma unroll
-        for (int ks = 0; ks < HD / 32; ks++) {
-            const f32x4 a = *(const f32x4 *)(qrow + 32 * ks + 8 * g);
-            const f32x4 b = *(const f32x4 *)(qrow + 32 * ks + 8 * g + 4);
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const float v = (e < 4 ? a[e] : b[e - 4]) * scale;
-                qh[ks][e] = (f16)v;
-                ql[ks][e] = (f16)(v - (float)qh[ks][e]);
-            }
-        }
-    }
-    f32x4 acc[HD / 16];                                   // O^T rows 16 dt + 4 g + v
-#pragma unroll
-    for (int dt = 0; dt < HD / 16; dt++) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float m = -INFINITY, l = 0.f;                         // this lane's keys only
     const int last = pos0 + min(q0 + AQ, N) - 1;          // last key any query here needs
     // Staging: thread t loads dims d0 .. d0 + DPT - 1 of key t / TPK of the
     // block.  The loads run ahead of the arithmetic: block k0 + AK's K and V
@@ -237,6 +238,66 @@ __global__ __launch_bounds__(256) void k_attn_prefill(
     };
     fetch(0, page_of(0));
     int page_next = page_of(AK);
+    // q after the first key block's loads, so their latencies overlap.
+    // B operand of S^T: q[n][32 ks + 8 g + e] * scale, split hi + lo.
+    const int64_t qoff = (int64_t)(valid ? n : N - 1) * qsrc.tstride + (int64_t)h * qsrc.hstride;
+    f16x8 qh[HD / 32], ql[HD / 32];
+    {
+        const float *qrow = qsrc.q + qoff;
+        float x[HD / 32][8];
+#pragma unroll
+        for (int ks = 0; ks < HD / 32; ks++) {
+            const f32x4 a = *(const f32x4 *)(qrow + 32 * ks + 8 * g);
+            const f32x4 b = *(const f32x4 *)(qrow + 32 * ks + 8 * g + 4);
+#pragma unroll
+            for (int e = 0; e < 8; e++) x[ks][e] = e < 4 ? a[e] : b[e - 4];
+        }
+        if (qsrc.norm) {
+            // RMS norm over the head (Kern.rmsnormRows, Kernels.swift:26-37),
+            // then the rotation of k_attn_prep at position + shift.
+            float ss = 0.f;
+#pragma unroll
+            for (int ks = 0; ks < HD / 32; ks++)
+#pragma unroll
+                for (int e = 0; e < 8; e++) ss += x[ks][e] * x[ks][e];
+            ss += __shfl_xor(ss, 16, 64);
+            ss += __shfl_xor(ss, 32, 64);
+            const float sc = 1.0f / sqrtf(ss / (float)HD + qsrc.eps);
+#pragma unroll
+            for (int ks = 0; ks < HD / 32; ks++) {
+                const f32x4 na = *(const f32x4 *)(qsrc.norm + 32 * ks + 8 * g);
+                const f32x4 nb = *(const f32x4 *)(qsrc.norm + 32 * ks + 8 * g + 4);
+#pragma unroll
+                for (int e = 0; e < 8; e++) x[ks][e] = x[ks][e] * sc * (e < 4 ? na[e] : nb[e - 4]);
+            }
+            const int rpos = my_pos + (pos_ptr ? pos_ptr[1] : 0);
+            const int hk = qsrc.n_rot / 64;               // chunk offset of a dim's partner
+#pragma unroll
+            for (int ks = 0; ks < HD / 64; ks++) {
+                if (ks >= hk) break;
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const float2 cs = rope_cs(32 * ks + 8 * g + e, qsrc.n_rot, qsrc.base, rpos,
+                                              qsrc.rtab, qsrc.rtab_n);
+                    const float a = x[ks][e], b = x[ks + hk][e];
+                    x[ks][e] = a * cs.x - b * cs.y;
+                    x[ks + hk][e] = a * cs.y + b * cs.x;
+                }
+            }
+        }
+#pragma unroll
+        for (int ks = 0; ks < HD / 32; ks++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float v = x[ks][e] * scale;
+                qh[ks][e] = (f16)v;
+                ql[ks][e] = (f16)(v - (float)qh[ks][e]);
+            }
+    }
+    f32x4 acc[HD / 16];                                   // O^T rows 16 dt + 4 g + v
+#pragma unroll
+    for (int dt = 0; dt < HD / 16; dt++) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m = -INFINITY, l = 0.f;                         // this lane's keys only
     for (int k0 = 0; k0 <= last; k0 += AK) {
         __syncthreads();
 #pragma unroll
@@ -316,7 +377,7 @@ __global__ __launch_bounds__(256) void k_attn_prefill(
     l += __shfl_xor(l, 32, 64);
     if (valid) {
         const float inv = 1.0f / l;
-        const float *grow = gate + ((int64_t)n * H + h) * HD;
+        const float *grow = qsrc.gate + (int64_t)n * qsrc.tstride + (int64_t)h * qsrc.hstride;
         OT *orow = out + ((int64_t)n * H + h) * HD;
 #pragma unroll
         for (int dt = 0; dt < HD / 16; dt++) {
@@ -619,30 +680,40 @@ int gd_attn_prep_launch(gd_ctx *ctx, int hd, const float *proj, int64_t stride, 
                         const float *q_norm, const float *k_norm, float *q_out, float *gate_out,
                         uint16_t *kc, uint16_t *vc, const int32_t *page_table,
                         const int32_t *pos_ptr, int N, int H, int HKV, int n_rot, float base,
-                        int block, float eps, const float *rope_tab, int rope_n) {
+                        int block, float eps, const float *rope_tab, int rope_n, int hbeg) {
     GD_REQUIRE(ctx, n_rot >= 0 && n_rot <= hd && n_rot % 2 == 0, "attention prep: n_rot=%d", n_rot);
+    GD_REQUIRE(ctx, hbeg == 0 || hbeg == H, "attention prep: first head %d", hbeg);
     const float2 *rtab = (const float2 *)rope_tab;
-    const dim3 grid((unsigned)((int64_t)N * ((H + HKV + PREP_HEADS - 1) / PREP_HEADS)));
+    const dim3 grid((unsigned)((int64_t)N * ((H + HKV - hbeg + PREP_HEADS - 1) / PREP_HEADS)));
     const dim3 blk(64 * PREP_WAVES);
     if (hd == 128)
         hipLaunchKernelGGL(k_attn_prep<128>, grid, blk, 0, ctx->stream, proj, stride, qs,
                            q_norm, k_norm, q_out, gate_out, kc, vc, page_table, pos_ptr, N, H,
-                           HKV, n_rot, base, block, eps, rtab, rope_n);
+                           HKV, n_rot, base, block, eps, rtab, rope_n, hbeg);
     else
         hipLaunchKernelGGL(k_attn_prep<256>, grid, blk, 0, ctx->stream, proj, stride, qs,
                            q_norm, k_norm, q_out, gate_out, kc, vc, page_table, pos_ptr, N, H,
-                           HKV, n_rot, base, block, eps, rtab, rope_n);
+                           HKV, n_rot, base, block, eps, rtab, rope_n, hbeg);
     GD_LAUNCHED(ctx, "k_attn_prep");
     return GD_OK;
 }
 
 int gd_attn_prefill_launch(gd_ctx *ctx, int hd, const float *q, const float *gate,
+                           int64_t q_tstride, int q_hstride, const float *q_norm, int n_rot,
+                           float base, float eps, const float *rope_tab, int rope_n,
                            const uint16_t *kc, const uint16_t *vc, const int32_t *page_table,
                            const int32_t *pos_ptr, int pos_add, void *out, int out_dtype, int H,
                            int HKV, int N, int block, float scale, int gated) {
+    GD_REQUIRE(ctx, !q_norm || (n_rot >= 0 && n_rot <= hd && n_rot % 64 == 0 && pos_ptr),
+               "attention prefill: raw q needs n_rot a multiple of 64 (n_rot=%d) and positions",
+               n_rot);
+    GD_REQUIRE(ctx, q_tstride % 4 == 0 && q_hstride % 4 == 0,
+               "attention prefill: q strides must keep rows 16-byte aligned");
+    const AttnQ qsrc{q, gate, q_tstride, q_hstride, q_norm, (const float2 *)rope_tab, rope_n, n_rot,
+                     base, eps};
     const dim3 grid((unsigned)H, gd_blocks(N, AQ));
 #define GD_AP(HD_, OT_) hipLaunchKernelGGL((k_attn_prefill<HD_, OT_>), grid, dim3(256), 0, \
-        ctx->stream, q, gate, kc, vc, page_table, pos_ptr, pos_add, (OT_ *)out, H, HKV, N, block, \
+        ctx->stream, qsrc, kc, vc, page_table, pos_ptr, pos_add, (OT_ *)out, H, HKV, N, block, \
         scale, gated)
     if (hd == 128) { if (out_dtype == GD_F16) GD_AP(128, uint16_t); else GD_AP(128, float); }
     else { if (out_dtype == GD_F16) GD_AP(256, uint16_t); else GD_AP(256, float); }
@@ -798,7 +869,8 @@ extern "C" int gd_attn_batch(gd_ctx *ctx, const float *q, const uint16_t *k_cach
     GD_REQUIRE(ctx, ((uintptr_t)q | (uintptr_t)out | (uintptr_t)(gated ? gate : q)) % 16 == 0,
                "gd_attn_batch: q, gate and out must be 16-byte aligned");
     if (!N) return GD_OK;
-    return gd_attn_prefill_launch(ctx, hd, q, gated ? gate : q, k_cache, v_cache, page_table,
-                                  nullptr, base_pos, out, GD_F32, n_head, n_head_kv, (int)N,
-                                  page_size, scale, gated);
+    return gd_attn_prefill_launch(ctx, hd, q, gated ? gate : q, (int64_t)n_head * hd, hd, nullptr, 0,
+                                  0.f, 0.f, nullptr, 0, k_cache, v_cache, page_table, nullptr,
+                                  base_pos, out, GD_F32, n_head, n_head_kv, (int)N, page_size,
+                                  scale, gated);
 }

@@ -81,13 +81,19 @@ int gd_gemm_glu(gd_ctx *ctx, const gd_q2w *w, int64_t T, const void *X, uint16_t
 // the projection rows: 2 hd for fused [q | gate] pairs (gated output), hd
 // for plain q (ungated).  For prep and fused decode, pos_ptr holds two ints:
 // the (first) token's position and the rope shift (rotation at position +
-// shift, KV slot at position).
+// shift, KV slot at position).  Prep does heads hbeg .. H + HKV - 1 (hbeg 0
+// or H: kv only).  The prefill reads q (and the gate) of (token n, head h) at
+// q + n q_tstride + h q_hstride; with q_norm set these are raw projection
+// rows that it normalizes and rotates itself (n_rot a multiple of 64,
+// pos_ptr as for prep), else k_attn_prep's output.
 int gd_attn_prep_launch(gd_ctx *ctx, int hd, const float *proj, int64_t stride, int qs,
                         const float *q_norm, const float *k_norm, float *q_out, float *gate_out,
                         uint16_t *kc, uint16_t *vc, const int32_t *page_table,
                         const int32_t *pos_ptr, int N, int H, int HKV, int n_rot, float base,
-                        int block, float eps, const float *rope_tab, int rope_n);
+                        int block, float eps, const float *rope_tab, int rope_n, int hbeg);
 int gd_attn_prefill_launch(gd_ctx *ctx, int hd, const float *q, const float *gate,
+                           int64_t q_tstride, int q_hstride, const float *q_norm, int n_rot,
+                           float base, float eps, const float *rope_tab, int rope_n,
                            const uint16_t *kc, const uint16_t *vc, const int32_t *page_table,
                            const int32_t *pos_ptr, int pos_add, void *out, int out_dtype, int H,
                            int HKV, int N, int block, float scale, int gated);

@@ -724,12 +724,25 @@ int forward(gd_stack *st, int N, bool decode) {
                                          c.kv_block, scale, c.n_rot, c.rope_base, eps, st->rope_tab,
                                          c.max_ctx));
             } else {
+                // The prefill normalizes and rotates q from the projection
+                // rows itself where each rotation pair lies in one of its
+                // lanes (n_rot a multiple of 64); prep then appends k, v only.
+                const bool rawq = c.n_rot % 64 == 0;
                 R_(gd_attn_prep_launch(ctx, hd, st->proj, (int64_t)RP, qs, ly.q_norm, ly.k_norm, st->q32,
                                        st->gate32, kc, vc, st->page_table, st->dpos, N, H,
-                                       HKV, c.n_rot, c.rope_base, c.kv_block, eps, st->rope_tab, c.max_ctx));
-                R_(gd_attn_prefill_launch(ctx, hd, st->q32, st->gate32, kc, vc,
-                                          st->page_table, st->dpos, 0, st->a16, GD_F16, H, HKV, N,
-                                          c.kv_block, scale, c.dense ? 0 : 1));
+                                       HKV, c.n_rot, c.rope_base, c.kv_block, eps, st->rope_tab, c.max_ctx,
+                                       rawq ? H : 0));
+                if (rawq)
+                    R_(gd_attn_prefill_launch(ctx, hd, st->proj, st->proj + hd, (int64_t)RP, qs,
+                                              ly.q_norm, c.n_rot, c.rope_base, eps, st->rope_tab,
+                                              c.max_ctx, kc, vc, st->page_table, st->dpos, 0,
+                                              st->a16, GD_F16, H, HKV, N, c.kv_block, scale,
+                                              c.dense ? 0 : 1));
+                else
+                    R_(gd_attn_prefill_launch(ctx, hd, st->q32, st->gate32, (int64_t)H * hd, hd,
+                                              nullptr, 0, 0.f, 0.f, nullptr, 0, kc, vc,
+                                              st->page_table, st->dpos, 0, st->a16, GD_F16, H, HKV,
+                                              N, c.kv_block, scale, c.dense ? 0 : 1));
             }
         }
         // Output projections feed only the residual add: a split-K plan
