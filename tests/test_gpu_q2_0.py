@@ -588,7 +588,9 @@ def test_gemv_sparse_outliers(ctx, xt, K, R):
 @pytest.mark.parametrize("xt,K,R", [(ga.F16, 32768, 100), (ga.F16, 65536, 40), (ga.F32, 32768, 100)])
 def test_gemv_long_k(ctx, xt, K, R):
     """K past what the fp4 body stages in LDS (about 30K) runs the f16 body,
-    with plain and sparse-outlier x, at the plain GEMV's tolerance."""
+    with plain and sparse-outlier x, at the plain GEMV's tolerance; and as
+    three K-split partials (each workgroup staging only its K range of x),
+    whose sum holds the same bound."""
     blocks = O.lcg_q2_0(K, R, K + 11 * R)
     w = upload_w(ctx, blocks, K, R)
     for scale in (1.0, 3000.0):
@@ -604,8 +606,14 @@ def test_gemv_long_k(ctx, xt, K, R):
         ctx.gd_q2_0_gemv(C.byref(w), dx, xt, dy)
         want = O.q2_0_matvec(blocks, K, R, x_ref, threads=8)
         assert rel_diff(ctx.get(dy, R, np.float32), want) < 1e-4
+        dys, ns = ctx.alloc(3 * R * 4), C.c_int()
+        ctx.gd_q2_0_gemv_split(C.byref(w), dx, xt, dys, 3, C.byref(ns))
+        assert ns.value == 3
+        parts = ctx.get(dys, 3 * R, np.float32).reshape(3, R)
+        assert rel_diff(parts.sum(0), want) < 1e-4
         ctx.free(dx)
         ctx.free(dy)
+        ctx.free(dys)
     free_w(ctx, w)
 
 
