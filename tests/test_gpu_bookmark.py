@@ -378,7 +378,8 @@ def test_rope_shift_restored_from_bytes(ctx):
     oracle with the same shift, logits within the stack tolerance; the same
     tokens without the shift give clearly different logits.  The shift
     travels with bookmarks and bytes, GDNS bytes (no such field) refuse it,
-    and a reset clears it."""
+    and a reset clears it.  A prefill chunk on the shifted state matches the
+    oracle too."""
     cfg, st = make_stack(ctx, seed=29)
     _, st2 = make_stack(ctx, seed=29)
     bms = []
@@ -408,6 +409,15 @@ def test_rope_shift_restored_from_bytes(ctx):
         unshifted, _ = decode_run(ctx, st, toks)
         apart = min(rel_diff(a, b) for a, b in zip(got, unshifted))
         assert apart > 10 * TOL, apart
+        # A prefill chunk on the shifted state: the prefill attention rotates
+        # its q, and prep its k, at position + shift as well.
+        more = (np.arange(9) * 31 % cfg["n_vocab"]).astype(np.int32)
+        lgp, nxt = np.empty(cfg["n_vocab"], np.float32), C.c_int32()
+        ctx.check(ctx.lib.gd_stack_prefill(st2, more.ctypes.data, more.size, C.byref(nxt),
+                                           lgp.ctypes.data))
+        _, r_lgp = ref.prefill(more)
+        rp = rel_diff(lgp, r_lgp)
+        assert rp < TOL, rp
         bms.append(bookmark(ctx, st2))
         assert struct.unpack_from("<q", serialize(ctx, st2, bms[-1]), 8)[0] == shift
         n = C.c_size_t()
@@ -417,7 +427,7 @@ def test_rope_shift_restored_from_bytes(ctx):
         bms.append(bookmark(ctx, st2))
         assert struct.unpack_from("<q", serialize(ctx, st2, bms[-1]), 8)[0] == 0
         print(f"\n  ropeShift {shift} restored: 6 decode steps, worst logits relDiff {worst:.2e} "
-              f"(unshifted: at least {apart:.2e} apart)")
+              f"(unshifted: at least {apart:.2e} apart); a 9-id prefill after them {rp:.2e}")
     finally:
         for b in bms:
             ctx.lib.gd_bookmark_free(b)
