@@ -183,7 +183,7 @@ struct AttnQ {
 // Causal prefill attention with the sigmoid output gate (Attention.swift:
 // 108-134), flash style on the matrix cores.  Block (head h, 64 queries):
 // wave w owns queries 16w .. 16w+15; keys stream through LDS in blocks of
-// AK (K as [key][d], V transposed as [d][key]).  Per block a wave forms
+// AK (K and V as [key][d], V^T read by the transposing LDS read).  Per block a wave forms
 // S^T = K Q^T (v_mfma_f32_16x16x32_f16, lane = one query column and four
 // keys of each 16-key tile), updates its online softmax per query, and adds
 // V^T P^T into O^T, 32 keys per MFMA.  The C layout of S^T is already the B
@@ -206,7 +206,9 @@ __global__ __launch_bounds__(256) void k_attn_prefill(
     constexpr int DPT = HD / TPK;                         // dims a thread stages per key
     constexpr int CH = DPT / 8;                           // 8-dim chunks a thread stages per operand
     __shared__ __attribute__((aligned(16))) f16 Ks[AK][HD + 8];
-    __shared__ __attribute__((aligned(16))) f16 Vt[HD][AK + 8];
+    // V rows padded by 32 bytes, so the 16 rows of a transposing read (below)
+    // spread over the LDS banks (measured 1.5% faster than 16 bytes).
+    __shared__ __attribute__((aligned(16))) f16 Vs[AK][HD + 16];
     // The last query blocks attend the most keys: they are dispatched first,
     // so the short ones fill the CUs behind them.
     const int h = blockIdx.x, q0 = (int)(gridDim.y - 1 - blockIdx.y) * AQ;
@@ -303,9 +305,7 @@ __global__ __launch_bounds__(256) void k_attn_prefill(
 #pragma unroll
         for (int c = 0; c < CH; c++) {
             *(u32x4 *)&Ks[sk][d0 + 8 * c] = kv[c];
-            const f16x8 va = __builtin_bit_cast(f16x8, kv[CH + c]);
-#pragma unroll
-            for (int e = 0; e < 8; e++) Vt[d0 + 8 * c + e][sk] = va[e];
+            *(u32x4 *)&Vs[sk][d0 + 8 * c] = kv[CH + c];
         }
         __syncthreads();
         fetch(k0 + AK, page_next);
@@ -360,13 +360,21 @@ __global__ __launch_bounds__(256) void k_attn_prefill(
                 pl[kt >> 1][4 * (kt & 1) + v] = (f16)(pv - (float)hi);
             }
         // O^T += V^T P^T: A lane row d = 16 dt + lq, the same 8 keys of each
-        // group.
+        // group, read from V as stored ([key][d]) by the transposing LDS
+        // read: within each 16 lanes, lane l receives element l % 4 of the
+        // 8 bytes that lanes l / 4 + 4k (k = 0..3) address, so lane j
+        // addressing dims 16 dt + 4 (j % 4) .. of key 4 g + j / 4 (+ 16)
+        // gives lane l keys 4 g + k (16 + 4 g + k) of dim 16 dt + l.
+        typedef short s16x4 __attribute__((ext_vector_type(4)));
+        typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 #pragma unroll
         for (int kg = 0; kg < AK / 32; kg++)
 #pragma unroll
             for (int dt = 0; dt < HD / 16; dt++) {
-                const f16 *vr = &Vt[16 * dt + lq][32 * kg];
-                const f16x4 v0 = *(const f16x4 *)(vr + 4 * g), v1 = *(const f16x4 *)(vr + 16 + 4 * g);
+                const f16 *vr = &Vs[32 * kg + 4 * g + (lq >> 2)][16 * dt + 4 * (lq & 3)];
+                const f16x4 v0 = __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)vr));
+                const f16x4 v1 = __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (lds_s16x4 *)(vr + 16 * (HD + 16))));
                 const f16x8 va = f16x8{v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
                 acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, ph[kg], acc[dt], 0, 0, 0);
                 acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl[kg], acc[dt], 0, 0, 0);
