@@ -21,10 +21,13 @@
 //     RMS norm, partial NEOX rope, the cache append), so the new key never
 //     round-trips through the cache within the step.
 //   * Prefill (N queries): flash attention on the matrix cores, block (head,
-//     64 queries); keys in blocks of 32 through LDS; S^T = K Q^T and O^T +=
-//     V^T P^T on v_mfma_f32_16x16x32_f16 with the key order inside the MFMA
-//     K dimension permuted so that P stays in registers; q and P as f16
-//     hi + lo pairs (about 22 bits), K and V the f16 cache, f32 accumulation.
+//     64 queries); keys in blocks of 64 (32 for head dim 256) through LDS,
+//     K and V as stored, V^T taken by the transposing LDS read; S^T = K Q^T
+//     and O^T += V^T P^T on v_mfma_f32_16x16x32_f16 with the key order
+//     inside the MFMA K dimension permuted so that P stays in registers; q
+//     and P as f16 hi + lo pairs (about 22 bits), K and V the f16 cache, f32
+//     accumulation.  In the stack the prefill normalizes and rotates q from
+//     the projection rows itself and prep handles the kv heads only.
 #include "gd_internal.h"
 
 #include <type_traits>

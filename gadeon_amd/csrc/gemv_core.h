@@ -426,7 +426,7 @@ __device__ void run(const Task &t, int bx, int bz, uint32_t *lds) {
     // 16i+15] in registers and writes them as 32 bytes; the block's sum and
     // max|x| come from 8-lane shuffles.  e_b = 0 unless max|x| >= 2048.
     auto stage = [&](const int e, const XChunk<XT, NQ> &xc) {
-        // Block bb, 16-element chunk i, half hf of it (SE = 8).
+        // Block bb, 16-element chunk i, half hf8 of it (SE = 8).
         const int bb = e / UPB, sub = e % UPB;
         const int i = SE == 16 ? sub : sub >> 1, hf8 = SE == 16 ? 0 : sub & 1;
         float sum = 0.f, amax = 0.f;
