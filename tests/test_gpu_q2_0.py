@@ -79,10 +79,12 @@ def test_dequant_rows_exact(ctx):
     free_w(ctx, w)
 
 
-# The last two hold more row sets than the GPU keeps resident, so workgroups
-# take several sets and sets are cut between waves.
+# (640, 50001) and (5120, 20500) hold more row sets than the GPU keeps
+# resident, so workgroups take several sets and sets are cut between waves;
+# K = 7552 is the longest x staged 8 elements a thread (f32 x: one pass of
+# the workgroup's 1024 threads), 7680 the shortest staged 16 a thread.
 GEMV_SHAPES = [(1024, 3072), (128, 5), (384, 37), (2048, 1000), (5120, 777), (17408, 130),
-               (6144, 64), (640, 50001), (5120, 20500)]
+               (6144, 64), (640, 50001), (5120, 20500), (7552, 300), (7680, 300)]
 
 
 @pytest.mark.parametrize("K,R", GEMV_SHAPES)
@@ -111,7 +113,8 @@ def test_gemv_vs_oracle(ctx, K, R, xt):
 
 
 @pytest.mark.parametrize("K,R,with_delta", [(5120, 777, True), (5120, 34816, True),
-                                            (1024, 300, False), (15744, 64, True)])
+                                            (1024, 300, False), (15744, 64, True),
+                                            (7552, 200, True), (7680, 200, True)])
 def test_gemv_norm_vs_oracle_and_unfused(ctx, K, R, with_delta):
     """gd_q2_0_gemv_norm == add + rmsnorm (f32 out) + f32-x GEMV: against the
     oracle, against the three device calls it replaces, and h' exactly."""
