@@ -68,6 +68,7 @@ _PROTOS = {
     "gd_q2_0_export_rows": (_i, [_vp, _Q2WP, _i64, _i64, _vp]),
     "gd_q2_0_gemv": (_i, [_vp, _Q2WP, _vp, _i, _vp]),
     "gd_q2_0_gemv_split": (_i, [_vp, _Q2WP, _vp, _i, _vp, _i, _vp]),
+    "gd_q2_0_gemv_gated": (_i, [_vp, _Q2WP, _vp, _vp, _vp, _f, _vp, _vp]),
     "gd_q2_0_gemv_norm": (_i, [_vp, _Q2WP, _vp, _vp, _i, _i64, _vp, _f, _vp, _vp, _vp]),
     "gd_q2_0_gemm_swiglu": (_i, [_vp, _Q2WP, _i64, _vp, _vp]),
     "gd_q2_0_gemm_swiglu_plan": (_i, [_vp, _Q2WP, _i64, _vp, _vp, _i]),

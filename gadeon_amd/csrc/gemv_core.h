@@ -126,11 +126,14 @@ __device__ __forceinline__ uint32_t pack_h2(float a, float b) {
 // x values of one staging unit (4 NQ consecutive elements of one block).
 // XT = 0: f16 x; 1: f32 x; 2: f32 residual h (+ delta partials) and the
 // norm weight w, staged as x = (h + delta) * w at f32 precision (the row sums
-// are scaled by 1/rms(h + delta)).
+// are scaled by 1/rms(h + delta)); 3: f32 o, z and the 128-entry norm weight
+// w of a gated head norm, staged as x = f16(o rs w silu(z)) with rs the
+// 1/rms of o over its 128-element block (one head).
 template <int XT, int NQ> struct XChunk;
 template <int NQ> struct XChunk<0, NQ> { u32x4 h[NQ / 2]; };
 template <int NQ> struct XChunk<1, NQ> { f32x4 f[NQ]; };
 template <int NQ> struct XChunk<2, NQ> { f32x4 f[NQ], w[NQ], d[ND_UNROLL][NQ]; };
+template <int NQ> struct XChunk<3, NQ> { f32x4 f[NQ], z[NQ], w[NQ]; };
 
 // SwiGLU output: with pair_sets > 0, W is [gate; up] with pair_sets sets
 // (16 rows) in each half, a workgroup takes gate sets k .. and the matching
@@ -151,6 +154,16 @@ struct NormIn {
     int dstride;             // floats between partials
 };
 
+// XT = 3 side task: advance the conv ring of channels 0 .. n-1, ring rows j
+// at ring + j * stride (j < 3): row 0 <- row 1, row 1 <- row 2, row 2 <-
+// src (the step that read the old rows has run before this launch).  Each
+// workgroup takes a run of channels (ring null: none).
+struct RingAdv {
+    float *ring;
+    const float *src;
+    int n, stride;
+};
+
 // One GEMV: W (codes, scales) [R][K], x, y; the work split (sets per
 // workgroup `per`, K split into nz ranges of ksteps steps, gx workgroups per
 // range: workgroup (bx, bz) takes sets bx * per .. of range bz).  lmag[0] and
@@ -166,6 +179,7 @@ struct Task {
     uint32_t lmag[2];
     NormIn nin;
     GluOut glu;
+    RingAdv ring;
 };
 
 // ceil(2^32 / L) for 1 < L <= 128 (0 otherwise): with it, i / L is
@@ -286,12 +300,13 @@ template <int XT, bool KBP, bool F4, int ND = 0, int SE = 16>
 __device__ void run(const Task &t, int bx, int bz, uint32_t *lds) {
     static_assert(ND >= 0 && ND <= ND_UNROLL && (XT == 2 || ND == 0), "partials: fused input only");
     static_assert(SE == 16 || (SE == 8 && F4), "half-entry staging: fp4 body only");
+    static_assert(XT != 3 || (F4 && SE == 16), "gated head norm: fp4 body, 16 a thread");
     constexpr int NQ = SE / 4;                            // f32x4 of x per staging unit
     constexpr int UPB = 128 / SE;                         // staging units per block
     constexpr int MT = 64 * NW;
     // x at f32 precision: f32 x, and the fused input's h' * w (whose 1/rms
     // scales the row sums instead).
-    constexpr bool XF = XT != 0;
+    constexpr bool XF = XT == 1 || XT == 2;               // (XT = 3 stages f16 values)
     constexpr bool HL = XF && !F4;                        // x carried as f16 hi + lo
     constexpr int NJ = XF ? 4 : 3;                        // F4: e4m3 pieces of x
     __shared__ __align__(16) int next_item;               // next item to take
@@ -335,7 +350,8 @@ __device__ void run(const Task &t, int bx, int bz, uint32_t *lds) {
     const __amdgpu_buffer_rsrc_t xrs = make_rsrc(t.x, (uint32_t)K * (XT ? 4u : 2u));
     const __amdgpu_buffer_rsrc_t drs =
             make_rsrc(nin.delta, nin.nd ? (uint32_t)((nin.nd - 1) * nin.dstride + K) * 4u : 0u);
-    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(nin.w, XT == 2 ? (uint32_t)K * 4u : 0u);
+    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(nin.w, XT == 2 ? (uint32_t)K * 4u : XT == 3 ? 512u : 0u);
+    const __amdgpu_buffer_rsrc_t zrs = make_rsrc(nin.delta, XT == 3 ? (uint32_t)K * 4u : 0u);
     // Element offset of staging unit e (K: a unit past the last x block).
     auto entry_off = [&](int e) { return e < nbx * UPB ? (xb0 + e / UPB) * 128 + SE * (e % UPB) : K; };
     // Dwords 4q .. 4q+3 of partial z of the entry at off; entries past K
@@ -371,6 +387,14 @@ __device__ void run(const Task &t, int bx, int bz, uint32_t *lds) {
 #pragma unroll
                 for (int q = 0; q < NQ; q++)
                     c.w[q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs, off * 4 + 16 * q, 0, 0));
+            }
+            if constexpr (XT == 3) {
+#pragma unroll
+                for (int q = 0; q < NQ; q++) {
+                    c.z[q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(zrs, off * 4 + 16 * q, 0, 0));
+                    c.w[q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                            wrs, (off & 127) * 4 + 16 * q, 0, 0));
+                }
             }
         }
         return c;
@@ -420,6 +444,24 @@ __device__ void run(const Task &t, int bx, int bz, uint32_t *lds) {
         head();
     }
     if (threadIdx.x == 0) next_item = NW * P;
+    // XT = 3: this workgroup's share of the conv ring advance, loaded now
+    // (without a branch: channels outside the share read outside the
+    // resources) and stored at the end.
+    int rch = -1;
+    float rv[3] = {0.f, 0.f, 0.f};
+    if constexpr (XT == 3) {
+        const RingAdv &ra = t.ring;
+        const int nwg = t.gx * t.nz, share = (ra.n + nwg - 1) / nwg;
+        const int c = (bz * t.gx + bx) * share + (int)threadIdx.x;
+        const bool mine = ra.ring && (int)threadIdx.x < share && c < ra.n;
+        const __amdgpu_buffer_rsrc_t rrs = make_rsrc(ra.ring, ra.ring ? (uint32_t)(3 * ra.stride) * 4u : 0u);
+        const __amdgpu_buffer_rsrc_t srs = make_rsrc(ra.src, ra.ring ? (uint32_t)ra.n * 4u : 0u);
+        const uint32_t o = mine ? (uint32_t)c * 4u : 0xfffff000u;
+        rv[0] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rrs, mine ? o + (uint32_t)ra.stride * 4u : o, 0, 0));
+        rv[1] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rrs, mine ? o + (uint32_t)ra.stride * 8u : o, 0, 0));
+        rv[2] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(srs, o, 0, 0));
+        rch = mine ? c : -1;
+    }
 
     // Stage x: pair p = 8i + k of block b holds (x[b,16i+PA[k]], x[b,16i+PA[k]+4]) *
     // XSCALE[k] * 2^-e_b.  Thread (b, i) forms the 8 pairs of x[16i ..
@@ -431,7 +473,23 @@ __device__ void run(const Task &t, int bx, int bz, uint32_t *lds) {
         const int i = SE == 16 ? sub : sub >> 1, hf8 = SE == 16 ? 0 : sub & 1;
         float sum = 0.f, amax = 0.f;
         f32x4 f[NQ];
-        if constexpr (XT == 0) {
+        if constexpr (XT == 3) {
+            // The gated head norm (k_gdn_step's, GDN.swift:113-115): the
+            // block's sum of squares over its lane group, then each value
+            // rounded to f16 as the f16 path stages it.
+            float ssu = 0.f;
+#pragma unroll
+            for (int q = 0; q < NQ; q++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) ssu += xc.f[q][j] * xc.f[q][j];
+            const float ssb = group<UPB>(ssu, [](float a, float b) { return a + b; });
+            const float rsh = 1.0f / sqrtf(ssb / 128.0f + nin.eps);
+#pragma unroll
+            for (int q = 0; q < NQ; q++)
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    f[q][j] = gd_h2f(gd_f2h(xc.f[q][j] * rsh * xc.w[q][j] * gd_silu(xc.z[q][j])));
+        } else if constexpr (XT == 0) {
 #pragma unroll
             for (int q = 0; q < 2 * NQ; q++) {
                 const uint32_t d = xc.h[q >> 2][q & 3];
@@ -798,6 +856,14 @@ __device__ void run(const Task &t, int bx, int bz, uint32_t *lds) {
             if (ok && q == 0 && set_lo * 16 + i < R)
                 __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), yrs,
                                                       (uint32_t)(set_lo * 16 + i) * 4u, 0, 0);
+        }
+    }
+    if constexpr (XT == 3) {
+        if (rch >= 0) {
+            float *rg0 = t.ring.ring;
+            rg0[rch] = rv[0];
+            rg0[t.ring.stride + rch] = rv[1];
+            rg0[2 * t.ring.stride + rch] = rv[2];
         }
     }
 }

@@ -97,6 +97,20 @@ extern "C" int gd_q2_0_gemv_split(gd_ctx *ctx, const gd_q2w *w, const void *x, i
     return gd_gemv_mfma(ctx, w, x, x_dtype, y, ksplit);
 }
 
+extern "C" int gd_q2_0_gemv_gated(gd_ctx *ctx, const gd_q2w *w, const float *o, const float *z,
+                                  const float *w_norm, float eps, const float *bias, float *y) {
+    GD_CHECK_CTX(ctx);
+    int rc = gd_check_q2w(ctx, w, "gd_q2_0_gemv_gated");
+    if (rc) return rc;
+    GD_REQUIRE(ctx, o && z && w_norm && y, "gd_q2_0_gemv_gated: null o, z, w_norm or y");
+    GD_REQUIRE(ctx, (((uintptr_t)o | (uintptr_t)z | (uintptr_t)w_norm) & 15) == 0,
+               "gd_q2_0_gemv_gated: o, z and w_norm must be 16-byte aligned");
+    GD_REQUIRE(ctx, w->K <= 30720 && w->R < (1LL << 30),
+               "gd_q2_0_gemv_gated: K=%lld (at most 30720) or R=%lld too large", (long long)w->K,
+               (long long)w->R);
+    return gd_gemv_mfma_gated(ctx, w, o, z, w_norm, eps, y, bias, nullptr, nullptr, 0, 0);
+}
+
 extern "C" int gd_q2_0_gemv_norm(gd_ctx *ctx, const gd_q2w *w, const float *h,
                                  const float *delta, int nd, int64_t delta_stride,
                                  const float *w_norm, float eps, float *hout, float *y,

@@ -59,7 +59,8 @@ Split plan(int64_t nsets, int steps, int ksplit, int64_t cus, size_t lds_free, i
 // it keeps per-block partials.
 int make_task(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, size_t xlds,
               const NormIn &nin, int ksplit, const GluOut &glu, int cus, const float *bias,
-              gemv::Task *t, size_t *lds_out, bool *kbp) {
+              gemv::Task *t, size_t *lds_out, bool *kbp,
+              const gemv::RingAdv &ring = gemv::RingAdv{nullptr, nullptr, 0, 0}) {
     const int64_t K = w->K, R = w->R;
     const int nblk = (int)(K >> 7), steps = (nblk + 3) / 4;
     // SwiGLU: split over gate sets, each bringing its up set along.
@@ -76,7 +77,7 @@ int make_task(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, size_t xlds
     *t = gemv::Task{(const uint8_t *)w->codes, (const uint16_t *)w->scales, x, y, bias, (int)K, (int)R,
                     (int)nsets, (int)sp.per, sp.ksteps, sp.nz, (int)sp.grid,
                     {gemv::item_magic(sp.ksteps), gemv::item_magic(steps - (sp.nz - 1) * sp.ksteps)},
-                    nin, glu};
+                    nin, glu, ring};
     *lds_out = lds;
     *kbp = sp.kbp;
     return GD_OK;
@@ -85,34 +86,45 @@ int make_task(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, size_t xlds
 template <int XT>
 int launch(gd_ctx *ctx, const gd_q2w *w, const void *x, float *y, XStage xs,
            const NormIn &nin = NormIn{nullptr, nullptr, nullptr, 0.f, 0, 0}, int ksplit = 1,
-           const GluOut &glu = GluOut{nullptr, 0}, const float *bias = nullptr) {
+           const GluOut &glu = GluOut{nullptr, 0}, const float *bias = nullptr,
+           const gemv::RingAdv &ring = gemv::RingAdv{nullptr, nullptr, 0, 0}) {
     const int cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
     gemv::Task t;
     size_t lds;
     bool kbp;
-    int rc = make_task(ctx, w, x, y, xs.bytes, nin, ksplit, glu, cus, bias, &t, &lds, &kbp);
+    int rc = make_task(ctx, w, x, y, xs.bytes, nin, ksplit, glu, cus, bias, &t, &lds, &kbp, ring);
     if (rc) return rc;
-    constexpr int NDM = XT == 2 ? gemv::ND_UNROLL : 0;
-    const int nd = std::min(nin.nd, NDM);
-    // The fp4 kernel with per-block partials and f32 x (four pieces) stages 8
-    // elements a thread where all of x then fits one pass of the workgroup's
-    // threads: the staging VALU work is spread over twice the waves.  (With
-    // f16 x, three pieces, 16 a thread measured faster.)
-    const int nblk = (int)(w->K >> 7);
-    const bool se8 = XT != 0 && xs.f4 && kbp && (nblk + 5) * 16 <= 64 * NW;
-    auto pick = [&](auto ndc) {
-        constexpr int ND = decltype(ndc)::value;
-        if constexpr (XT != 0)
-            if (se8) return q2_0_gemv_mfma_kernel<XT, true, true, ND, 8>;
-        return xs.f4 ? (kbp ? q2_0_gemv_mfma_kernel<XT, true, true, ND> : q2_0_gemv_mfma_kernel<XT, false, true, ND>)
-                     : (kbp ? q2_0_gemv_mfma_kernel<XT, true, false, ND> : q2_0_gemv_mfma_kernel<XT, false, false, ND>);
-    };
-    auto kern = nd == 0 ? pick(std::integral_constant<int, 0>{})
-              : nd == 1 ? pick(std::integral_constant<int, NDM >= 1 ? 1 : 0>{})
-                        : pick(std::integral_constant<int, NDM >= 2 ? 2 : 0>{});
-    hipLaunchKernelGGL(kern, dim3((unsigned)t.gx, t.nz), dim3(64 * NW), lds, ctx->stream, t);
-    GD_LAUNCHED(ctx, "q2_0_gemv_mfma");
-    return GD_OK;
+    if constexpr (XT == 3) {
+        // The gated head norm has the fp4 body with per-block partials only.
+        GD_REQUIRE(ctx, xs.f4 && kbp, "gd_gemv_gated: K=%lld R=%lld does not fit the fp4 body",
+                   (long long)w->K, (long long)w->R);
+        hipLaunchKernelGGL((q2_0_gemv_mfma_kernel<3, true, true, 0>), dim3((unsigned)t.gx, t.nz),
+                           dim3(64 * NW), lds, ctx->stream, t);
+        GD_LAUNCHED(ctx, "q2_0_gemv_mfma");
+        return GD_OK;
+    } else {
+        constexpr int NDM = XT == 2 ? gemv::ND_UNROLL : 0;
+        const int nd = std::min(nin.nd, NDM);
+        // The fp4 kernel with per-block partials and f32 x (four pieces) stages 8
+        // elements a thread where all of x then fits one pass of the workgroup's
+        // threads: the staging VALU work is spread over twice the waves.  (With
+        // f16 x, three pieces, 16 a thread measured faster.)
+        const int nblk = (int)(w->K >> 7);
+        const bool se8 = XT != 0 && xs.f4 && kbp && (nblk + 5) * 16 <= 64 * NW;
+        auto pick = [&](auto ndc) {
+            constexpr int ND = decltype(ndc)::value;
+            if constexpr (XT != 0)
+                if (se8) return q2_0_gemv_mfma_kernel<XT, true, true, ND, 8>;
+            return xs.f4 ? (kbp ? q2_0_gemv_mfma_kernel<XT, true, true, ND> : q2_0_gemv_mfma_kernel<XT, false, true, ND>)
+                         : (kbp ? q2_0_gemv_mfma_kernel<XT, true, false, ND> : q2_0_gemv_mfma_kernel<XT, false, false, ND>);
+        };
+        auto kern = nd == 0 ? pick(std::integral_constant<int, 0>{})
+                  : nd == 1 ? pick(std::integral_constant<int, NDM >= 1 ? 1 : 0>{})
+                            : pick(std::integral_constant<int, NDM >= 2 ? 2 : 0>{});
+        hipLaunchKernelGGL(kern, dim3((unsigned)t.gx, t.nz), dim3(64 * NW), lds, ctx->stream, t);
+        GD_LAUNCHED(ctx, "q2_0_gemv_mfma");
+        return GD_OK;
+    }
 }
 
 }  // namespace
@@ -135,6 +147,21 @@ int gd_gemv_mfma(gd_ctx *ctx, const gd_q2w *w, const void *x, int x_dtype, float
     const GluOut noglu{nullptr, 0};
     return XT ? launch<1>(ctx, w, x, y, xs, none, ksplit, noglu, bias)
               : launch<0>(ctx, w, x, y, xs, none, ksplit, noglu, bias);
+}
+
+// GEMV of x = f16(rmsnorm_128(o) * normw * silu(z)), the norm over each
+// 128-element block of o (one value head), normw [128] (the caller has
+// checked w, K % 128 == 0 and the pointers).  bias (if not null) is added
+// to y.  ring (if not null): the conv ring advance of ring_n channels (rows
+// ring_stride floats apart, the new row from ring_src), a side task of the
+// same launch.
+int gd_gemv_mfma_gated(gd_ctx *ctx, const gd_q2w *w, const float *o, const float *z,
+                       const float *normw, float eps, float *y, const float *bias, float *ring,
+                       const float *ring_src, int ring_n, int ring_stride) {
+    const int nblk = (int)(w->K >> 7);
+    const XStage xs = x_stage(nblk, true);
+    return launch<3>(ctx, w, o, y, xs, NormIn{z, normw, nullptr, eps, 0, 0}, 1, GluOut{nullptr, 0},
+                     bias, gemv::RingAdv{ring, ring_src, ring_n, ring_stride});
 }
 
 // K splits (1..4) for an f16-x GEMV whose partial rows the consumer can sum:

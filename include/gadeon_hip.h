@@ -171,6 +171,16 @@ int gd_q2_0_export_rows(gd_ctx *ctx, const gd_q2w *w, int64_t row0, int64_t nrow
 int gd_q2_0_gemv(gd_ctx *ctx, const gd_q2w *w, const void *x, int x_dtype,
                  float *y);
 
+/* y = W x (+ bias if not null) with x = f16(rmsnorm(o_h) * w_norm * silu(z))
+ * over each 128-element block h of o (one value head): the gated norm of a
+ * GDN layer's output (GDN.swift:113-115; rmsnorm_rows + mul_silu,
+ * Kernels.metal:751-768, 1126-1131) done in the GEMV's x staging, as the
+ * stack's decode feeds its GDN out_proj.  o, z f32 [K], w_norm f32 [128],
+ * bias and y f32 [R]; K a multiple of 128, at most 30720.  No counterpart in
+ * the reference (it runs the norm and the GEMV as separate dispatches). */
+int gd_q2_0_gemv_gated(gd_ctx *ctx, const gd_q2w *w, const float *o, const float *z,
+                       const float *w_norm, float eps, const float *bias, float *y);
+
 /* gd_q2_0_gemv with K cut into `ksplit` (1..4) ranges whose partial rows go
  * to y + z * R (y holds ksplit * R floats); *nsplit receives the number of
  * partials written (it can be lower than ksplit for short K).  Summing them

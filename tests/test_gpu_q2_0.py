@@ -146,6 +146,45 @@ def test_gemv_norm_vs_oracle_and_unfused(ctx, K, R, with_delta):
     free_w(ctx, w)
 
 
+@pytest.mark.parametrize("K,R,with_bias", [(2048, 5120, True), (2048, 300, False), (6144, 777, True),
+                                           (128, 40, False)])
+def test_gemv_gated_head_norm(ctx, K, R, with_bias):
+    """gd_q2_0_gemv_gated == f16(rmsnorm of each 128-block of o * w * silu(z))
+    into the f16-x GEMV: against the oracle's norm and matvec, and against
+    the device chain it replaces (rmsnorm_rows, mul_silu, f16, GEMV).  x is
+    rounded to f16 on both sides, from norm scales formed in another order,
+    so an element may land one f16 step apart: 1e-3."""
+    eps = 1e-6
+    blocks = O.lcg_q2_0(K, R, 3 * K + R)
+    w = upload_w(ctx, blocks, K, R)
+    o = O.lcg_normal(K, 61, 0.0, 0.7)
+    z = O.lcg_normal(K, 62, 0.0, 2.0)
+    wn = O.lcg_normal(128, 63, 1.0, 0.2)
+    bias = O.lcg_normal(R, 64, 0.0, 1.0) if with_bias else None
+    do, dz, dwn, dy = ctx.put(o), ctx.put(z), ctx.put(wn), ctx.alloc(R * 4)
+    db = ctx.put(bias) if with_bias else None
+    ctx.gd_q2_0_gemv_gated(C.byref(w), do, dz, dwn, 1e-6, db, dy)
+    y = ctx.get(dy, R, np.float32)
+    a = O.rmsnorm_rows(o, 128, wn, eps)
+    x16 = (a * (z / (1.0 + np.exp(-z)))).astype(np.float16)
+    want = O.q2_0_matvec(blocks, K, R, x16.astype(np.float32), threads=8)
+    if with_bias:
+        want = want + bias
+    assert rel_diff(y, want) < 1e-3
+    # the device chain: norm rows in place, a * silu(z), f16, f16-x GEMV
+    da = ctx.put(o)
+    ctx.gd_rmsnorm_rows(da, 128, K // 128, dwn, eps)
+    ctx.gd_mul_silu(da, dz, K)
+    dx16 = ctx.put(ctx.get(da, K, np.float32).astype(np.float16).view(np.uint16))
+    dy2 = ctx.alloc(R * 4)
+    ctx.gd_q2_0_gemv(C.byref(w), dx16, ga.F16, dy2)
+    y2 = ctx.get(dy2, R, np.float32) + (bias if with_bias else 0.0)
+    assert rel_diff(y, y2) < 1e-3
+    for p in (do, dz, dwn, dy, da, dx16, dy2) + ((db,) if with_bias else ()):
+        ctx.free(p)
+    free_w(ctx, w)
+
+
 @pytest.mark.parametrize("K,R,ksplit", [(17408, 5120, 4), (2048, 5120, 2), (5120, 777, 3),
                                         (512, 100, 4), (17408, 130, 2)])
 def test_gemv_split_partials_sum_to_gemv(ctx, K, R, ksplit):
