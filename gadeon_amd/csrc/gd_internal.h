@@ -40,13 +40,13 @@ int gd_hip_fail(gd_ctx *ctx, hipError_t e, const char *what);
 // split 0.
 int gd_gemv_mfma(gd_ctx *ctx, const gd_q2w *w, const void *x, int x_dtype, float *y, int ksplit,
                  const float *bias = nullptr);
-// GEMV of x = f16(rmsnorm_128(o) * normw * silu(z)) (each 128-element block
-// of o one head, normw [128]) plus bias; ring (if not null): advance the conv
-// ring of ring_n channels (rows ring_stride apart, new row ring_src) in the
-// same launch.
-int gd_gemv_mfma_gated(gd_ctx *ctx, const gd_q2w *w, const float *o, const float *z,
-                       const float *normw, float eps, float *y, const float *bias, float *ring,
-                       const float *ring_src, int ring_n, int ring_stride);
+// GEMV of x = f16(o * rs * g) (rs the 1/rms of each 128-element block of o,
+// one head; g = norm weight * silu(z), the gate) plus bias; ring (if not
+// null): advance the conv ring of ring_n channels (rows ring_stride apart,
+// new row ring_src) in the same launch.
+int gd_gemv_mfma_gated(gd_ctx *ctx, const gd_q2w *w, const float *o, const float *g, float eps,
+                       float *y, const float *bias, float *ring, const float *ring_src, int ring_n,
+                       int ring_stride);
 // GEMV of x = f16(rmsnorm(h + sum of nd delta partials) * normw); hout <- the
 // sum if not null.
 // glu_out (if not null): w = [gate; up] and glu_out = f16(silu(gate x) * up x)

@@ -126,14 +126,14 @@ __device__ __forceinline__ uint32_t pack_h2(float a, float b) {
 // x values of one staging unit (4 NQ consecutive elements of one block).
 // XT = 0: f16 x; 1: f32 x; 2: f32 residual h (+ delta partials) and the
 // norm weight w, staged as x = (h + delta) * w at f32 precision (the row sums
-// are scaled by 1/rms(h + delta)); 3: f32 o, z and the 128-entry norm weight
-// w of a gated head norm, staged as x = f16(o rs w silu(z)) with rs the
-// 1/rms of o over its 128-element block (one head).
+// are scaled by 1/rms(h + delta)); 3: f32 o and the gate g (= w silu(z)) of
+// a gated head norm, staged as x = f16(o rs g) with rs the 1/rms of o over
+// its 128-element block (one head).
 template <int XT, int NQ> struct XChunk;
 template <int NQ> struct XChunk<0, NQ> { u32x4 h[NQ / 2]; };
 template <int NQ> struct XChunk<1, NQ> { f32x4 f[NQ]; };
 template <int NQ> struct XChunk<2, NQ> { f32x4 f[NQ], w[NQ], d[ND_UNROLL][NQ]; };
-template <int NQ> struct XChunk<3, NQ> { f32x4 f[NQ], z[NQ], w[NQ]; };
+template <int NQ> struct XChunk<3, NQ> { f32x4 f[NQ], g[NQ]; };
 
 // SwiGLU output: with pair_sets > 0, W is [gate; up] with pair_sets sets
 // (16 rows) in each half, a workgroup takes gate sets k .. and the matching
@@ -350,8 +350,8 @@ __device__ void run(const Task &t, int bx, int bz, uint32_t *lds) {
     const __amdgpu_buffer_rsrc_t xrs = make_rsrc(t.x, (uint32_t)K * (XT ? 4u : 2u));
     const __amdgpu_buffer_rsrc_t drs =
             make_rsrc(nin.delta, nin.nd ? (uint32_t)((nin.nd - 1) * nin.dstride + K) * 4u : 0u);
-    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(nin.w, XT == 2 ? (uint32_t)K * 4u : XT == 3 ? 512u : 0u);
-    const __amdgpu_buffer_rsrc_t zrs = make_rsrc(nin.delta, XT == 3 ? (uint32_t)K * 4u : 0u);
+    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(nin.w, XT == 2 ? (uint32_t)K * 4u : 0u);
+    const __amdgpu_buffer_rsrc_t grs = make_rsrc(nin.delta, XT == 3 ? (uint32_t)K * 4u : 0u);
     // Element offset of staging unit e (K: a unit past the last x block).
     auto entry_off = [&](int e) { return e < nbx * UPB ? (xb0 + e / UPB) * 128 + SE * (e % UPB) : K; };
     // Dwords 4q .. 4q+3 of partial z of the entry at off; entries past K
@@ -390,11 +390,8 @@ __device__ void run(const Task &t, int bx, int bz, uint32_t *lds) {
             }
             if constexpr (XT == 3) {
 #pragma unroll
-                for (int q = 0; q < NQ; q++) {
-                    c.z[q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(zrs, off * 4 + 16 * q, 0, 0));
-                    c.w[q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                            wrs, (off & 127) * 4 + 16 * q, 0, 0));
-                }
+                for (int q = 0; q < NQ; q++)
+                    c.g[q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(grs, off * 4 + 16 * q, 0, 0));
             }
         }
         return c;
@@ -474,9 +471,9 @@ __device__ void run(const Task &t, int bx, int bz, uint32_t *lds) {
         float sum = 0.f, amax = 0.f;
         f32x4 f[NQ];
         if constexpr (XT == 3) {
-            // The gated head norm (k_gdn_step's, GDN.swift:113-115): the
-            // block's sum of squares over its lane group, then each value
-            // rounded to f16 as the f16 path stages it.
+            // The gated head norm (GDN.swift:113-115): the block's sum of
+            // squares over its lane group, then each o rs g rounded to f16
+            // as the f16 path stages it.
             float ssu = 0.f;
 #pragma unroll
             for (int q = 0; q < NQ; q++)
@@ -488,7 +485,7 @@ __device__ void run(const Task &t, int bx, int bz, uint32_t *lds) {
             for (int q = 0; q < NQ; q++)
 #pragma unroll
                 for (int j = 0; j < 4; j++)
-                    f[q][j] = gd_h2f(gd_f2h(xc.f[q][j] * rsh * xc.w[q][j] * gd_silu(xc.z[q][j])));
+                    f[q][j] = gd_h2f(gd_f2h(xc.f[q][j] * rsh * xc.g[q][j]));
         } else if constexpr (XT == 0) {
 #pragma unroll
             for (int q = 0; q < 2 * NQ; q++) {

@@ -97,6 +97,12 @@ extern "C" int gd_q2_0_gemv_split(gd_ctx *ctx, const gd_q2w *w, const void *x, i
     return gd_gemv_mfma(ctx, w, x, x_dtype, y, ksplit);
 }
 
+// g[i] = w[i % 128] * silu(z[i]): the gate of the gated head norm.
+__global__ void k_head_gate(const float *z, const float *w, float *g, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) g[i] = w[i & 127] * gd_silu(z[i]);
+}
+
 extern "C" int gd_q2_0_gemv_gated(gd_ctx *ctx, const gd_q2w *w, const float *o, const float *z,
                                   const float *w_norm, float eps, const float *bias, float *y) {
     GD_CHECK_CTX(ctx);
@@ -108,7 +114,12 @@ extern "C" int gd_q2_0_gemv_gated(gd_ctx *ctx, const gd_q2w *w, const float *o, 
     GD_REQUIRE(ctx, w->K <= 30720 && w->R < (1LL << 30),
                "gd_q2_0_gemv_gated: K=%lld (at most 30720) or R=%lld too large", (long long)w->K,
                (long long)w->R);
-    return gd_gemv_mfma_gated(ctx, w, o, z, w_norm, eps, y, bias, nullptr, nullptr, 0, 0);
+    float *g = nullptr;
+    if ((rc = gd_ctx_workspace(ctx, (size_t)w->K * 4, (void **)&g))) return rc;
+    hipLaunchKernelGGL(k_head_gate, dim3(gd_blocks(w->K, 256)), dim3(256), 0, ctx->stream, z,
+                       w_norm, g, (int)w->K);
+    GD_LAUNCHED(ctx, "k_head_gate");
+    return gd_gemv_mfma_gated(ctx, w, o, g, eps, y, bias, nullptr, nullptr, 0, 0);
 }
 
 extern "C" int gd_q2_0_gemv_norm(gd_ctx *ctx, const gd_q2w *w, const float *h,

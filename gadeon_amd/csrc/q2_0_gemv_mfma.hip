@@ -149,18 +149,18 @@ int gd_gemv_mfma(gd_ctx *ctx, const gd_q2w *w, const void *x, int x_dtype, float
               : launch<0>(ctx, w, x, y, xs, none, ksplit, noglu, bias);
 }
 
-// GEMV of x = f16(rmsnorm_128(o) * normw * silu(z)), the norm over each
-// 128-element block of o (one value head), normw [128] (the caller has
-// checked w, K % 128 == 0 and the pointers).  bias (if not null) is added
-// to y.  ring (if not null): the conv ring advance of ring_n channels (rows
-// ring_stride floats apart, the new row from ring_src), a side task of the
-// same launch.
-int gd_gemv_mfma_gated(gd_ctx *ctx, const gd_q2w *w, const float *o, const float *z,
-                       const float *normw, float eps, float *y, const float *bias, float *ring,
-                       const float *ring_src, int ring_n, int ring_stride) {
+// GEMV of x = f16(o * rs * g), rs the 1/rms of o over each 128-element block
+// (one value head) and g the gate (norm weight times silu(z)) (the caller
+// has checked w, K % 128 == 0 and the pointers).  bias (if not null) is
+// added to y.  ring (if not null): the conv ring advance of ring_n channels
+// (rows ring_stride floats apart, the new row from ring_src), a side task of
+// the same launch.
+int gd_gemv_mfma_gated(gd_ctx *ctx, const gd_q2w *w, const float *o, const float *g, float eps,
+                       float *y, const float *bias, float *ring, const float *ring_src, int ring_n,
+                       int ring_stride) {
     const int nblk = (int)(w->K >> 7);
     const XStage xs = x_stage(nblk, true);
-    return launch<3>(ctx, w, o, y, xs, NormIn{z, normw, nullptr, eps, 0, 0}, 1, GluOut{nullptr, 0},
+    return launch<3>(ctx, w, o, y, xs, NormIn{g, nullptr, nullptr, eps, 0, 0}, 1, GluOut{nullptr, 0},
                      bias, gemv::RingAdv{ring, ring_src, ring_n, ring_stride});
 }
 

@@ -200,6 +200,7 @@ __global__ __launch_bounds__(256) void k_gdn_conv_prefill(
 // wave w owns value columns l and l + 64 and key rows 8w .. 8w+7, so each
 // thread streams 16 state values and four waves per SIMD hide the latency.
 constexpr int GS_W = 16, GS_R = HD / GS_W;       // waves, key rows per wave
+constexpr int GS_COLS = 4;                       // k_gdn_step_cols: workgroups per head
 __global__ __launch_bounds__(64 * GS_W) void k_gdn_step(
         const float *proj, float *ring, const float *cw, const float *dt, const float *aNeg,
         float *S, const float *onw, uint16_t *out, int convDim, int keyDim, int off_z, int off_b,
@@ -308,6 +309,103 @@ __global__ __launch_bounds__(64 * GS_W) void k_gdn_step(
         const float sc = 1.0f / sqrtf(ss / (float)HD + eps);
         out[h * HD + lane] = gd_f2h(o0 * sc * nw0 * gd_silu(zv0));
         out[h * HD + lane + 64] = gd_f2h(o1 * sc * nw1 * gd_silu(zv1));
+    }
+}
+
+// k_gdn_step's state update split over NS workgroups per value head, each
+// owning 128/NS value columns of the head's state, so the state streams
+// through NS times as many CUs.  Every workgroup forms the head's q and k
+// (conv + SiLU, the same per-channel arithmetic and the same per-wave norm
+// sums) and its own columns' v, and leaves the rest to its neighbours: the
+// conv ring is read here and advanced by the out_proj launch that follows
+// (gd_gemv_mfma_gated's side task), and the output goes out as f32 o (times
+// 1/|q| and qScale) with the gate g = onw * silu(z) of each column, for that
+// launch's x staging to apply the gated head norm (o * rs * g).
+// Thread (rg, col): rows 8 rg .. 8 rg + 7 of column col, so the S^T k and
+// readout sums run over the same row groups in the same order as
+// k_gdn_step's waves: o is bit-identical to its pre-norm output.
+template <int NS>
+__global__ __launch_bounds__(16 * (HD / NS)) void k_gdn_step_cols(
+        const float *proj, const float *ring, const float *cw, const float *dt, const float *aNeg,
+        float *S, const float *onw, float *o_out, float *g_out, int convDim, int keyDim, int off_z,
+        int off_b, int off_a, float qScale, float eps) {
+    constexpr int NC = HD / NS;                  // value columns of this workgroup
+    static_assert(16 * NC >= 2 * HD + NC + 1, "threads for the q/k/v conv and the gates");
+    __shared__ float kq[2][HD];                  // k, q after conv + SiLU
+    __shared__ float vs[NC];
+    __shared__ float red[16][NC];                // S^T k partials by row group
+    __shared__ float red2[16][NC];               // readout partials
+    __shared__ float gate[2];                    // beta, gamma
+    __shared__ float nsq[4];                     // |q|^2, |k|^2 halves
+    const int h = blockIdx.x, c0 = blockIdx.y * NC, tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int col = tid % NC, rg = tid / NC;
+    float *Sh = S + (int64_t)h * HD * HD;
+    // The gate of this column (row group 0 writes it with o).
+    const float zc = rg == 0 ? proj[off_z + h * HD + c0 + col] : 0.f;
+    const float wc = rg == 0 ? onw[c0 + col] : 0.f;
+    // State loads first: they are the bandwidth.
+    float sv[8];
+#pragma unroll
+    for (int r = 0; r < 8; r++) sv[r] = Sh[(int64_t)(8 * rg + r) * HD + c0 + col];
+    auto conv = [&](int c) {
+        const float w0 = cw[c * 4], w1 = cw[c * 4 + 1], w2 = cw[c * 4 + 2], w3 = cw[c * 4 + 3];
+        const float r0 = ring[c], r1 = ring[convDim + c], r2 = ring[2 * convDim + c];
+        const float cur = proj[c];
+        float acc = 0.0f;
+        acc += r0 * w0;
+        acc += r1 * w1;
+        acc += r2 * w2;
+        acc += cur * w3;
+        return gd_silu(acc);
+    };
+    // Threads 0..127: q channel tid; 128..255: k channel tid - 128; then
+    // this workgroup's NC v channels, then the gates.
+    if (tid < 2 * HD) {
+        const int part = tid / HD, i = tid % HD;
+        const float y = conv(part * keyDim + h * HD + i);
+        kq[1 - part][i] = y;
+        const float ss = gd_wave_sum(y * y);      // waves 0, 1: q; 2, 3: k
+        if (lane == 0) nsq[wave] = ss;
+    } else if (tid < 2 * HD + NC) {
+        vs[tid - 2 * HD] = conv(2 * keyDim + h * HD + c0 + tid - 2 * HD);
+    } else if (tid == 2 * HD + NC) {
+        gate[0] = gd_sigmoid(proj[off_b + h]);
+        gate[1] = expf(gd_softplus(proj[off_a + h] + dt[h]) * aNeg[h]);
+    }
+    __syncthreads();
+    const float rk = 1.0f / sqrtf((nsq[2] + nsq[3]) + eps);
+    const float beta = gate[0], gam = gate[1];
+    float sk = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+        sv[r] *= gam;
+        sk = fmaf(sv[r], kq[0][8 * rg + r], sk);
+    }
+    red[rg][col] = sk;
+    __syncthreads();
+    sk = 0.0f;
+#pragma unroll
+    for (int g = 0; g < 16; g++) sk += red[g][col];
+    sk *= rk;
+    const float d = beta * (vs[col] - sk) * rk;
+    float a = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+        const int i = 8 * rg + r;
+        sv[r] = fmaf(kq[0][i], d, sv[r]);
+        a = fmaf(sv[r], kq[1][i], a);
+        Sh[(int64_t)i * HD + c0 + col] = sv[r];
+    }
+    red2[rg][col] = a;
+    __syncthreads();
+    if (rg == 0) {
+        float o = 0.0f;
+#pragma unroll
+        for (int g = 0; g < 16; g++) o += red2[g][col];
+        const float rq = 1.0f / sqrtf((nsq[0] + nsq[1]) + eps);
+        o_out[h * HD + c0 + col] = o * (rq * qScale);
+        g_out[h * HD + c0 + col] = wc * gd_silu(zc);
     }
 }
 
@@ -617,6 +715,9 @@ int forward(gd_stack *st, int N, bool decode) {
     // GEMV sums the partials, normalizes in its x staging and writes the sum
     // back to x (which no kernel reads by then).
     int nd = 0;
+    // Decode GDN layers whose value heads each have their own q/k head and a
+    // 128-dim state: the state update split over workgroups by columns.
+    const bool gdn_cols = decode && nK == nV && c.d_state == HD && st->valDim == nV * HD;
     auto consume = [&](const gd_q2w *w, const float *normw, float *hout, float *y,
                        uint16_t *glu) {
         return gd_gemv_mfma_norm(ctx, w, st->contrib, nd > 1 ? st->contrib + E : nullptr, nd - 1,
@@ -671,9 +772,18 @@ int forward(gd_stack *st, int N, bool decode) {
         if (ly.rec) {
             const int off_z = st->convDim, off_b = off_z + st->valDim, off_a = off_b + nV;
             if (decode && nK == nV && c.d_state == HD) {
-                K_(k_gdn_step, dim3(nV), dim3(64 * GS_W), 0, s, st->proj, ly.conv_state, ly.conv_w,
-                   ly.dt, ly.a_neg, ly.rec_state, ly.ssm_norm, st->a16, st->convDim, st->keyDim,
-                   off_z, off_b, off_a, qScale, eps);
+                if (gdn_cols) {
+                    // The state over GS_COLS workgroups per head; the gated norm
+                    // and the conv ring advance go with the out_proj below.
+                    K_(k_gdn_step_cols<GS_COLS>, dim3(nV, GS_COLS), dim3(16 * (HD / GS_COLS)), 0, s,
+                       st->proj, ly.conv_state, ly.conv_w, ly.dt, ly.a_neg, ly.rec_state,
+                       ly.ssm_norm, st->o32, st->o32 + st->valDim, st->convDim, st->keyDim, off_z,
+                       off_b, off_a, qScale, eps);
+                } else {
+                    K_(k_gdn_step, dim3(nV), dim3(64 * GS_W), 0, s, st->proj, ly.conv_state,
+                       ly.conv_w, ly.dt, ly.a_neg, ly.rec_state, ly.ssm_norm, st->a16, st->convDim,
+                       st->keyDim, off_z, off_b, off_a, qScale, eps);
+                }
             } else if (decode) {
                 K_(k_conv4, dim3(gd_blocks(st->convDim, 256)), dim3(256), 0, s, st->proj,
                    (int64_t)RP, ly.conv_state, ly.conv_w, st->conv_out, st->convDim, 1);
@@ -748,7 +858,13 @@ int forward(gd_stack *st, int N, bool decode) {
         // Output projections feed only the residual add: a split-K plan
         // leaves its partials in contrib and k_add_rmsnorm sums them.
         int nsplit = 1;
-        if (decode) {
+        if (decode && ly.rec && gdn_cols) {
+            // x = f16(rmsnorm_128(o) * ssm_norm * silu(z)) staged by the GEMV;
+            // its side task advances the conv ring the step read.
+            nd = 1;
+            R_(gd_gemv_mfma_gated(ctx, &ly.out_proj, st->o32, st->o32 + st->valDim, eps, st->contrib,
+                                  st->x, ly.conv_state, st->proj, st->convDim, st->convDim));
+        } else if (decode) {
             nd = gd_gemv_ksplit(ctx, ly.out_proj.K, ly.out_proj.R);
             R_(gd_gemv_mfma(ctx, &ly.out_proj, st->a16, GD_F16, st->contrib, nd, st->x));
         } else {
@@ -963,7 +1079,8 @@ int create(gd_ctx *ctx, const gd_stack_config *cfg, uint64_t seed, bool random, 
     C_(salloc_t(st, (size_t)B * E, &st->x));
     C_(salloc_t(st, (size_t)B * maxproj, &st->proj));
     C_(salloc_t(st, (size_t)B * st->convDim, &st->conv_out));
-    C_(salloc_t(st, (size_t)B * st->valDim, &st->o32));
+    // o32: prefill's GDN output rows; decode's o and gate (two rows).
+    C_(salloc_t(st, (size_t)std::max(B, 2) * st->valDim, &st->o32));
     // Room for the split-K partials of the output projections (at most 8).
     C_(salloc_t(st, (size_t)8 * B * E, &st->contrib));
     C_(salloc_t(st, (size_t)B * c.n_v_head, &st->beta));
